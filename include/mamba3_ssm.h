@@ -1,0 +1,183 @@
+/*
+ * mamba3_ssm.h -- C ABI of the MI355X (gfx950) Mamba-3 SSD scan and decode step.
+ *
+ * This is the boundary a host in any language binds (the reference crate's
+ * Rust host would bind it through a thin `extern "C"` -sys crate; see
+ * INTEGRATION.md).  It replaces the reference's generic Rust API over a
+ * CubeCL runtime (BectorVoom/mamba-trainer):
+ *
+ *   m3_ssm_config / m3_config_*   SsmConfig and its enums   src/ssm/config.rs:19-347
+ *   m3_ssm_state                  SsmState                  src/ssm/scan.rs:293-358
+ *   m3_scan_inputs / m3_scan      ScanInputs, mamba3_scan   src/ssm/scan.rs:360-618
+ *   m3_scan_output                ScanOutput                src/ssm/scan.rs:445-452
+ *   m3_ssd_args / m3_ssd_chunked  ssd_chunked               src/ssm/scan.rs:98-291
+ *   m3_step_inputs / m3_step      mamba3_step               src/ssm/scan.rs:640-712
+ *   m3_status / m3_last_error     Error / Result            src/error.rs:5-61
+ *
+ * Conventions
+ *   - All tensors are caller-allocated, contiguous, row-major device buffers
+ *     with the reference's layouts (rank-last x/b/c, N contiguous in the state).
+ *   - `dtype` selects the storage of x, b, c, theta and y (f32 or bf16, bf16 as
+ *     raw 16-bit words).  dt, lambda, a_log, d_skip and the state are f32.
+ *   - Calls are asynchronous on `stream` (a hipStream_t; NULL = the default
+ *     stream) and never synchronise the host.  No call allocates device memory.
+ *   - Errors return a status; m3_last_error() gives this thread's message.
+ *     Validation mirrors the reference's rules and messages.
+ *   - Deviations from the reference, by design:
+ *       * m3_step updates the state in place (the reference returns a new
+ *         SsmState each step, scan.rs:704-711);
+ *       * seq == 0 returns an empty y and passes the state through (the
+ *         reference's mamba3_scan would underflow `seq - 1` there).
+ */
+#ifndef MAMBA3_SSM_H
+#define MAMBA3_SSM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define M3_ABI_VERSION 1
+
+/* Error taxonomy of src/error.rs:9-49; M3_ERR_HIP / M3_ERR_ARGUMENT have no
+ * reference counterpart (device failures and NULL/invalid pointers). */
+typedef enum m3_status {
+    M3_OK = 0,
+    M3_ERR_CONFIG = 1,       /* Error::Config      */
+    M3_ERR_SHAPE = 2,        /* Error::Shape       */
+    M3_ERR_RANK = 3,         /* Error::Rank        */
+    M3_ERR_UNSUPPORTED = 4,  /* Error::Unsupported */
+    M3_ERR_HIP = 5,
+    M3_ERR_ARGUMENT = 6
+} m3_status;
+
+typedef enum m3_dtype { M3_F32 = 0, M3_BF16 = 1 } m3_dtype;
+
+/* src/ssm/config.rs:19-26 */
+typedef enum m3_discretization {
+    M3_EULER = 0,
+    M3_TRAPEZOID = 1,
+    M3_LEARNED_TRAPEZOID = 2
+} m3_discretization;
+
+/* src/ssm/config.rs:46-55 */
+typedef enum m3_dynamics { M3_REAL = 0, M3_ROTATIONAL = 1 } m3_dynamics;
+
+/* SsmConfig, src/ssm/config.rs:84-128.  `rank` is SsmMode (1 = Siso,
+ * R > 1 = Mimo{rank: R}; 0 is invalid); `conv_kernel` 0 means None. */
+typedef struct m3_ssm_config {
+    size_t d_model, n_heads, head_dim, d_state, n_groups;
+    int32_t discretization;   /* m3_discretization */
+    int32_t dynamics;         /* m3_dynamics */
+    size_t rank;
+    size_t chunk_size;
+    size_t conv_kernel;
+    int32_t bc_norm, bc_bias, post_gate_norm, skip_connection;
+    float dt_min, dt_max, dt_init_floor, a_init_min, a_init_max;
+    int32_t bias;
+} m3_ssm_config;
+
+/* Default::default() (config.rs:130-156). */
+m3_status m3_config_default(m3_ssm_config *out);
+/* SsmConfig::validate (config.rs:203-245). */
+m3_status m3_config_validate(const m3_ssm_config *cfg);
+/* Widths, config.rs:164-200. */
+size_t m3_config_d_inner(const m3_ssm_config *cfg);
+size_t m3_config_bc_width(const m3_ssm_config *cfg);
+size_t m3_config_theta_width(const m3_ssm_config *cfg);
+size_t m3_config_lambda_width(const m3_ssm_config *cfg);
+size_t m3_config_in_proj_width(const m3_ssm_config *cfg);
+/* Discretization::fixed_lambda (config.rs:29-36): 1, 0.5, or NaN if learned. */
+float m3_discretization_fixed_lambda(int32_t discretization);
+
+/* SsmState, src/ssm/scan.rs:294-302. */
+typedef struct m3_ssm_state {
+    float *h;       /* [B, H, P, N] */
+    float *last_u;  /* [B, H, P, N] */
+    float *angle;   /* [B, H, N/2], NULL for real dynamics */
+} m3_ssm_state;
+
+/* ScanInputs, src/ssm/scan.rs:361-385. */
+typedef struct m3_scan_inputs {
+    size_t batch, seq, heads, head_dim, d_state, rank;
+    int32_t dtype;            /* m3_dtype of x, b, c, theta, y */
+    const void *x;            /* [B, T, H, P, R] */
+    const void *b;            /* [B, T, H, N, R] */
+    const void *c;            /* [B, T, H, N, R] */
+    const float *dt;          /* [B, T, H], positive */
+    const float *a_log;       /* [H], A = -exp(a_log) */
+    const float *lambda;      /* [B, T, H], in [0, 1] */
+    const void *theta;        /* [B, T, H, N/2] or NULL (real dynamics) */
+    const float *d_skip;      /* [H] or NULL */
+    const m3_ssm_state *state;/* carried-in state or NULL */
+    size_t chunk_size;        /* > 0; the kernel tiles time itself (a hint) */
+    int32_t want_state;       /* ScanInputs::want_state */
+} m3_scan_inputs;
+
+/* ScanOutput, src/ssm/scan.rs:446-452.  `state` is written when want_state
+ * (angle when theta is given).  Outputs must not alias inputs. */
+typedef struct m3_scan_output {
+    void *y;                  /* [B, T, H, P, R] */
+    m3_ssm_state state;
+} m3_scan_output;
+
+/* mamba3_scan (scan.rs:458-618): trapezoid weights, rotating frame, MIMO
+ * fold, carried state, skip path and boundary state in one launch. */
+m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *stream);
+
+/* ssd_chunked arguments (scan.rs:100-126): one input/output channel. */
+typedef struct m3_ssd_args {
+    size_t batch, seq, heads, head_dim, d_state;
+    int32_t dtype;            /* m3_dtype of x, b, c, y */
+    const void *x;            /* [B, T, H, P] */
+    const void *b;            /* [B, T, H, N] */
+    const void *c;            /* [B, T, H, N] */
+    const float *a;           /* [B, T, H], log decay dt*A (non-positive) */
+    const float *g;           /* [B, T, H], diagonal weight */
+    const float *w;           /* [B, T, H], off-diagonal weight */
+    const float *initial_state; /* [B, H, P, N] or NULL */
+    size_t chunk_size;
+    int32_t want_state;
+} m3_ssd_args;
+
+/* ssd_chunked (scan.rs:116-291).  final_state [B,H,P,N] is written when
+ * want_state (it may be NULL otherwise). */
+m3_status m3_ssd_chunked(const m3_ssd_args *args, void *y, float *final_state, void *stream);
+
+/* mamba3_step arguments (scan.rs:646-659): one token per sequence. */
+typedef struct m3_step_inputs {
+    size_t batch, heads, head_dim, d_state, rank;
+    int32_t dtype;            /* m3_dtype of x, b, c, theta, y */
+    const void *x;            /* [B, H, P, R] */
+    const void *b;            /* [B, H, N, R] */
+    const void *c;            /* [B, H, N, R] */
+    const float *dt;          /* [B, H] */
+    const float *lambda;      /* [B, H] */
+    const float *a_log;       /* [H] */
+    const void *theta;        /* [B, H, N/2] or NULL */
+    const float *d_skip;      /* [H] or NULL */
+} m3_step_inputs;
+
+/* mamba3_step (scan.rs:649-712), in place: `state` (h, last_u and, with
+ * theta, angle) is read and overwritten; y [B, H, P, R] is written. */
+m3_status m3_step(const m3_step_inputs *in, m3_ssm_state *state, void *y, void *stream);
+
+/* Status name and this thread's last error message ("" after success). */
+const char *m3_status_string(m3_status status);
+const char *m3_last_error(void);
+
+/* Kernel launches issued by this library since load (the reference's
+ * launch counter, src/backend.rs:231-281). */
+uint64_t m3_launch_count(void);
+
+/* Runs the MFMA lane-layout self test on the current device: *result is 0
+ * when the layouts the kernels assume hold.  Synchronous; allocates 4 bytes. */
+m3_status m3_selftest_mfma(int32_t *result);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA3_SSM_H */

@@ -1,0 +1,241 @@
+// Recurrent decode step of the Mamba-3 SSM for gfx950, in place on the f32
+// state cache.  Restates src/ssm/scan.rs:649-712 (mamba3_step) and the fused
+// kernels it calls:
+//   ssm_coefficients  src/tensor/ops/fused.rs:1679-1697
+//   ssm_angle         src/tensor/ops/fused.rs:1534-1555
+//   rotate_halves     src/tensor/ops/fused.rs:588-619 (from_angle)
+//   ssm_state_update  src/tensor/ops/fused.rs:1348-1364
+// plus the u = x B^T and y = C^T h products (scan.rs:683-698) and the skip.
+//
+// One workgroup per (batch, head).  Its prologue advances the angle, rotates B
+// and C into LDS and forms alpha, beta, gamma; the body then streams the
+// [P, N] f32 state once: read h and last_u, write h' and last_u' = u, with
+// y = C~^T h' reduced across the lanes that hold one row.  That is the
+// minimum traffic of 16 bytes per state element -- the reference's step
+// reads and writes the state about twice that (new u tensor, a separate
+// update pass, and a materialised transpose of h for the readout).
+#include "m3_device.hpp"
+#include "m3_internal.hpp"
+
+namespace m3 {
+
+namespace {
+
+constexpr int kStepThreads = 256;
+constexpr int kMaxRank = 8;        // register-resident y partials per row
+
+template <typename T>
+__device__ __forceinline__ float ld(const void *p, size_t i) {
+    return to_f32(static_cast<const T *>(p)[i]);
+}
+
+// Prologue shared by both bodies: angle advance, rotation of B and C into
+// LDS (rank-last [N][R] layout kept), x into LDS, and the coefficients.
+template <typename T>
+__device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, float *bt,
+                                              float *ct, float *xs, float &alpha,
+                                              float &beta, float &gamma) {
+    const int tid = threadIdx.x;
+    const size_t N = a.d_state, P = a.head_dim, R = a.rank;
+    const size_t half = N / 2;
+    const size_t hh = bh % a.heads;
+    const float step = a.dt[bh];
+    const float lam = a.lambda[bh];
+    const size_t bc_base = bh * N * R;
+    if (a.theta != nullptr) {
+        for (size_t i = tid; i < half; i += kStepThreads) {
+            // phi = wrap(prev + dt * theta)   (fused.rs:1549-1553)
+            float raw = ld<T>(a.theta, bh * half + i) * step + a.angle[bh * half + i];
+            float phi = wrap_angle(raw);
+            a.angle[bh * half + i] = phi;
+            float sn, cs;
+            sincosf(phi, &sn, &cs);
+            for (size_t r = 0; r < R; ++r) {
+                float b1 = ld<T>(a.b, bc_base + i * R + r);
+                float b2 = ld<T>(a.b, bc_base + (i + half) * R + r);
+                float c1 = ld<T>(a.c, bc_base + i * R + r);
+                float c2 = ld<T>(a.c, bc_base + (i + half) * R + r);
+                // rotation by -phi: (x1 cos + x2 sin, -x1 sin + x2 cos)
+                bt[i * R + r] = b1 * cs + b2 * sn;
+                bt[(i + half) * R + r] = -b1 * sn + b2 * cs;
+                ct[i * R + r] = c1 * cs + c2 * sn;
+                ct[(i + half) * R + r] = -c1 * sn + c2 * cs;
+            }
+        }
+        // odd N: the unpaired last component is not rotated (N is even whenever
+        // theta is given; validation enforces it)
+    } else {
+        for (size_t i = tid; i < N * R; i += kStepThreads) {
+            bt[i] = ld<T>(a.b, bc_base + i);
+            ct[i] = ld<T>(a.c, bc_base + i);
+        }
+    }
+    for (size_t i = tid; i < P * R; i += kStepThreads) xs[i] = ld<T>(a.x, bh * P * R + i);
+    // alpha = exp(dt * -exp(a_log)), beta = (1 - lambda) dt alpha, gamma = lambda dt
+    const float A = 0.0f - expf(a.a_log[hh]);
+    alpha = expf(step * A);
+    beta = (1.0f - lam) * step * alpha;
+    gamma = lam * step;
+}
+
+// Vector body: N % 4 == 0 and G = N / 4 lanes per row with G a power of two
+// that divides 64.  Each lane owns four consecutive state columns of a row.
+template <typename T, int RK>
+__global__ void __launch_bounds__(kStepThreads)
+step_kernel_vec(StepLaunch a) {
+    extern __shared__ float smem[];
+    const size_t N = a.d_state, P = a.head_dim;
+    constexpr int R = RK;
+    float *bt = smem;
+    float *ct = bt + N * R;
+    float *xs = ct + N * R;
+    const size_t bh = blockIdx.x;
+    float alpha, beta, gamma;
+    step_prologue<T>(a, bh, bt, ct, xs, alpha, beta, gamma);
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int G = static_cast<int>(N / 4);          // lanes per row
+    const int rows_per_wave = 64 / G;
+    const int rows_per_pass = rows_per_wave * (kStepThreads / 64);
+    const int col4 = (lane % G) * 4;
+    const float dskip = a.d_skip ? a.d_skip[bh % a.heads] : 0.0f;
+    f32x4 *h4 = reinterpret_cast<f32x4 *>(a.h + bh * P * N);
+    f32x4 *u4 = reinterpret_cast<f32x4 *>(a.last_u + bh * P * N);
+
+    // B~ columns this lane touches, hoisted out of the row loop.
+    float bcol[4][R], ccol[4][R];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            bcol[j][r] = bt[(col4 + j) * R + r];
+            ccol[j][r] = ct[(col4 + j) * R + r];
+        }
+
+    constexpr int kBatch = 4;   // rows in flight per lane
+    for (int base = wave * rows_per_wave + lane / G; base < static_cast<int>(P);
+         base += rows_per_pass * kBatch) {
+        f32x4 hv[kBatch], lv[kBatch];
+        int rows[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            rows[k] = base + k * rows_per_pass;
+            if (rows[k] < static_cast<int>(P)) {
+                size_t idx = (static_cast<size_t>(rows[k]) * N + col4) / 4;
+                hv[k] = __builtin_nontemporal_load(&h4[idx]);
+                lv[k] = __builtin_nontemporal_load(&u4[idx]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int p = rows[k];
+            // every lane of a row group shares `p`, so the guard is uniform per group
+            const bool live = p < static_cast<int>(P);
+            float ypart[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) ypart[r] = 0.0f;
+            if (live) {
+                float xr[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) xr[r] = xs[p * R + r];
+                f32x4 hn, un;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float u = 0.0f;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) u += xr[r] * bcol[j][r];
+                    // h' = h*alpha + last_u*beta + u*gamma   (fused.rs:1360-1362)
+                    float hnew = hv[k][j] * alpha + lv[k][j] * beta + u * gamma;
+                    hn[j] = hnew;
+                    un[j] = u;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) ypart[r] += ccol[j][r] * hnew;
+                }
+                size_t idx = (static_cast<size_t>(p) * N + col4) / 4;
+                __builtin_nontemporal_store(hn, &h4[idx]);
+                __builtin_nontemporal_store(un, &u4[idx]);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) ypart[r] = group_sum(ypart[r], G);
+            if (live && (lane % G) == 0) {
+                T *y = static_cast<T *>(a.y);
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    y[(bh * P + p) * R + r] = from_f32<T>(ypart[r] + xs[p * R + r] * dskip);
+            }
+        }
+    }
+}
+
+// Generic body for shapes the vector body does not cover (odd N, N > 256,
+// rank above kMaxRank): one thread per state row.
+template <typename T>
+__global__ void __launch_bounds__(kStepThreads)
+step_kernel_generic(StepLaunch a) {
+    extern __shared__ float smem[];
+    const size_t N = a.d_state, P = a.head_dim, R = a.rank;
+    float *bt = smem;
+    float *ct = bt + N * R;
+    float *xs = ct + N * R;
+    const size_t bh = blockIdx.x;
+    float alpha, beta, gamma;
+    step_prologue<T>(a, bh, bt, ct, xs, alpha, beta, gamma);
+    __syncthreads();
+    const float dskip = a.d_skip ? a.d_skip[bh % a.heads] : 0.0f;
+    float *h = a.h + bh * P * N;
+    float *lu = a.last_u + bh * P * N;
+    T *y = static_cast<T *>(a.y);
+    for (size_t p = threadIdx.x; p < P; p += kStepThreads) {
+        for (size_t n = 0; n < N; ++n) {
+            float u = 0.0f;
+            for (size_t r = 0; r < R; ++r) u += xs[p * R + r] * bt[n * R + r];
+            float hnew = h[p * N + n] * alpha + lu[p * N + n] * beta + u * gamma;
+            h[p * N + n] = hnew;
+            lu[p * N + n] = u;
+        }
+        for (size_t r = 0; r < R; ++r) {
+            float acc = 0.0f;
+            for (size_t n = 0; n < N; ++n) acc += ct[n * R + r] * h[p * N + n];
+            y[(bh * P + p) * R + r] = from_f32<T>(acc + xs[p * R + r] * dskip);
+        }
+    }
+}
+
+template <typename T, int RK>
+hipError_t launch_vec(const StepLaunch &a, size_t smem, hipStream_t s) {
+    hipLaunchKernelGGL((step_kernel_vec<T, RK>), dim3(a.batch * a.heads), dim3(kStepThreads),
+                       smem, s, a);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t dispatch(const StepLaunch &a, hipStream_t s) {
+    const size_t N = a.d_state, R = a.rank;
+    const size_t smem = (2 * N * R + a.head_dim * R) * sizeof(float);
+    const size_t G = N / 4;
+    const bool vec = (N % 4 == 0) && G >= 1 && G <= 64 && (G & (G - 1)) == 0;
+    if (vec) {
+        switch (R) {
+            case 1: return launch_vec<T, 1>(a, smem, s);
+            case 2: return launch_vec<T, 2>(a, smem, s);
+            case 3: return launch_vec<T, 3>(a, smem, s);
+            case 4: return launch_vec<T, 4>(a, smem, s);
+            case 8: return launch_vec<T, 8>(a, smem, s);
+            default: break;
+        }
+    }
+    hipLaunchKernelGGL((step_kernel_generic<T>), dim3(a.batch * a.heads), dim3(kStepThreads),
+                       smem, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_step(const StepLaunch &a, hipStream_t stream) {
+    if (a.batch * a.heads == 0) return hipSuccess;
+    return a.bf16 ? dispatch<bf16_t>(a, stream) : dispatch<float>(a, stream);
+}
+
+}  // namespace m3

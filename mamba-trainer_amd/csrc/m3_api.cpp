@@ -1,0 +1,351 @@
+// C ABI of the gfx950 Mamba-3 path: argument validation (mirroring the
+// reference's rules and messages), dispatch to the HIP kernels, and the error
+// channel.  See include/mamba3_ssm.h for the contract.
+#include "mamba3_ssm.h"
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "m3_internal.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+std::atomic<uint64_t> g_launches{0};
+
+m3_status fail(m3_status st, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    const char *prefix = "";
+    switch (st) {
+        case M3_ERR_CONFIG: prefix = "invalid configuration: "; break;   // error.rs:12
+        case M3_ERR_SHAPE: prefix = "shape error: "; break;              // error.rs:16
+        case M3_ERR_UNSUPPORTED: prefix = "unsupported: "; break;        // error.rs:47
+        default: break;
+    }
+    g_last_error = std::string(prefix) + buf;
+    return st;
+}
+
+m3_status ok() {
+    g_last_error.clear();
+    return M3_OK;
+}
+
+m3_status hip_fail(hipError_t e, const char *what) {
+    return fail(M3_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Largest rows-per-chunk the scan instantiations use for this dtype / d_state
+// (a row is one (token, rank) pair, so rank may not exceed it).
+size_t scan_rows(int dtype, size_t d_state) {
+    if (dtype == M3_BF16) return d_state <= 128 ? 64 : 32;
+    return d_state <= 128 ? 32 : 16;
+}
+
+bool dtype_ok(int32_t d) { return d == M3_F32 || d == M3_BF16; }
+
+}  // namespace
+
+extern "C" {
+
+m3_status m3_config_default(m3_ssm_config *out) {
+    if (out == nullptr) return fail(M3_ERR_ARGUMENT, "config pointer is NULL");
+    // config.rs:130-156
+    out->d_model = 768;
+    out->n_heads = 24;
+    out->head_dim = 64;
+    out->d_state = 64;
+    out->n_groups = 24;
+    out->discretization = M3_LEARNED_TRAPEZOID;
+    out->dynamics = M3_ROTATIONAL;
+    out->rank = 1;
+    out->chunk_size = 64;
+    out->conv_kernel = 4;
+    out->bc_norm = 1;
+    out->bc_bias = 1;
+    out->post_gate_norm = 0;
+    out->skip_connection = 1;
+    out->dt_min = 0.001f;
+    out->dt_max = 0.1f;
+    out->dt_init_floor = 1e-4f;
+    out->a_init_min = 1.0f;
+    out->a_init_max = 16.0f;
+    out->bias = 0;
+    return ok();
+}
+
+m3_status m3_config_validate(const m3_ssm_config *c) {
+    if (c == nullptr) return fail(M3_ERR_ARGUMENT, "config pointer is NULL");
+    // config.rs:203-245, rule for rule
+    if (c->d_model == 0 || c->n_heads == 0 || c->head_dim == 0 || c->d_state == 0)
+        return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
+    if (c->n_groups == 0 || c->n_heads % c->n_groups != 0)
+        return fail(M3_ERR_CONFIG, "n_heads (%zu) must be a multiple of n_groups (%zu)",
+                    c->n_heads, c->n_groups);
+    if (c->dynamics == M3_ROTATIONAL && c->d_state % 2 != 0)
+        return fail(M3_ERR_CONFIG,
+                    "rotational dynamics pair up state dimensions, so d_state must be even, "
+                    "got %zu",
+                    c->d_state);
+    if (c->chunk_size == 0) return fail(M3_ERR_CONFIG, "chunk_size must be positive");
+    if (c->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
+    if (!(c->dt_min > 0.0f) || !(c->dt_max > c->dt_min))
+        return fail(M3_ERR_CONFIG, "expected 0 < dt_min < dt_max, got %g and %g",
+                    static_cast<double>(c->dt_min), static_cast<double>(c->dt_max));
+    if (!(c->a_init_min > 0.0f) || c->a_init_max < c->a_init_min)
+        return fail(M3_ERR_CONFIG, "expected 0 < a_init_min <= a_init_max");
+    if (c->conv_kernel != 0 && c->conv_kernel < 2)
+        return fail(M3_ERR_CONFIG, "conv_kernel must be at least 2; use None to disable");
+    if (c->discretization < M3_EULER || c->discretization > M3_LEARNED_TRAPEZOID)
+        return fail(M3_ERR_CONFIG, "unknown discretization %d", c->discretization);
+    if (c->dynamics != M3_REAL && c->dynamics != M3_ROTATIONAL)
+        return fail(M3_ERR_CONFIG, "unknown dynamics %d", c->dynamics);
+    return ok();
+}
+
+size_t m3_config_d_inner(const m3_ssm_config *c) { return c->n_heads * c->head_dim * c->rank; }
+size_t m3_config_bc_width(const m3_ssm_config *c) { return c->n_groups * c->d_state * c->rank; }
+size_t m3_config_theta_width(const m3_ssm_config *c) {
+    return c->dynamics == M3_ROTATIONAL ? c->n_heads * c->d_state / 2 : 0;
+}
+size_t m3_config_lambda_width(const m3_ssm_config *c) {
+    return c->discretization == M3_LEARNED_TRAPEZOID ? c->n_heads : 0;
+}
+size_t m3_config_in_proj_width(const m3_ssm_config *c) {
+    // z gate, x, B, C, dt, lambda, theta  (config.rs:191-200)
+    return 2 * m3_config_d_inner(c) + 2 * m3_config_bc_width(c) + c->n_heads +
+           m3_config_lambda_width(c) + m3_config_theta_width(c);
+}
+
+float m3_discretization_fixed_lambda(int32_t d) {
+    if (d == M3_EULER) return 1.0f;
+    if (d == M3_TRAPEZOID) return 0.5f;
+    return std::nanf("");
+}
+
+m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *stream) {
+    if (in == nullptr || out == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/outputs are NULL");
+    if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
+    if (in->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
+    if (in->head_dim == 0 || in->d_state == 0)
+        return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
+    if (in->theta != nullptr && in->d_state % 2 != 0)   // scan.rs:485-489
+        return fail(M3_ERR_CONFIG, "rotational dynamics require an even d_state");
+    if (in->head_dim > m3::kScanMaxHeadDim)
+        return fail(M3_ERR_UNSUPPORTED, "head_dim %zu exceeds the scan kernel's %zu",
+                    in->head_dim, m3::kScanMaxHeadDim);
+    if (in->d_state > m3::kScanMaxState)
+        return fail(M3_ERR_UNSUPPORTED, "d_state %zu exceeds the scan kernel's %zu",
+                    in->d_state, m3::kScanMaxState);
+    const size_t rows = scan_rows(in->dtype, in->d_state);
+    if (in->rank > rows)
+        return fail(M3_ERR_UNSUPPORTED, "MIMO rank %zu exceeds %zu rows per chunk", in->rank,
+                    rows);
+    const m3_ssm_state *st = in->state;
+    if (st != nullptr && (st->h == nullptr || st->last_u == nullptr))
+        return fail(M3_ERR_ARGUMENT, "state needs both h and last_u");
+    if (in->want_state) {
+        if (out->state.h == nullptr || out->state.last_u == nullptr)
+            return fail(M3_ERR_ARGUMENT, "want_state needs output h and last_u buffers");
+        if (in->theta != nullptr && out->state.angle == nullptr)
+            return fail(M3_ERR_ARGUMENT, "want_state with theta needs an output angle buffer");
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t B = in->batch, H = in->heads, P = in->head_dim, N = in->d_state;
+    const size_t sbytes = B * H * P * N * sizeof(float);
+    if (B * H == 0) return ok();
+    if (in->seq == 0) {
+        // empty window: nothing to mix, the state passes through
+        if (in->want_state) {
+            hipError_t e;
+            if (st != nullptr) {
+                e = hipMemcpyAsync(out->state.h, st->h, sbytes, hipMemcpyDeviceToDevice, s);
+                if (e == hipSuccess)
+                    e = hipMemcpyAsync(out->state.last_u, st->last_u, sbytes,
+                                       hipMemcpyDeviceToDevice, s);
+            } else {
+                e = hipMemsetAsync(out->state.h, 0, sbytes, s);
+                if (e == hipSuccess) e = hipMemsetAsync(out->state.last_u, 0, sbytes, s);
+            }
+            if (e == hipSuccess && in->theta != nullptr) {
+                const size_t abytes = B * H * (N / 2) * sizeof(float);
+                if (st != nullptr && st->angle != nullptr)
+                    e = hipMemcpyAsync(out->state.angle, st->angle, abytes,
+                                       hipMemcpyDeviceToDevice, s);
+                else
+                    e = hipMemsetAsync(out->state.angle, 0, abytes, s);
+            }
+            if (e != hipSuccess) return hip_fail(e, "state pass-through");
+        }
+        return ok();
+    }
+    if (in->x == nullptr || in->b == nullptr || in->c == nullptr || in->dt == nullptr ||
+        in->a_log == nullptr || in->lambda == nullptr || out->y == nullptr)
+        return fail(M3_ERR_ARGUMENT, "x, b, c, dt, a_log, lambda and y are required");
+
+    m3::ScanLaunch a{};
+    a.batch = B;
+    a.seq = in->seq;
+    a.heads = H;
+    a.head_dim = P;
+    a.d_state = N;
+    a.rank = in->rank;
+    a.bf16 = in->dtype == M3_BF16;
+    a.mode_raw = 1;
+    a.x = in->x;
+    a.b = in->b;
+    a.c = in->c;
+    a.dt = in->dt;
+    a.lambda = in->lambda;
+    a.a_log = in->a_log;
+    a.theta = in->theta;
+    a.d_skip = in->d_skip;
+    a.h0 = st ? st->h : nullptr;
+    a.last_u0 = st ? st->last_u : nullptr;
+    a.angle0 = (st && in->theta) ? st->angle : nullptr;
+    a.y = out->y;
+    if (in->want_state) {
+        a.h_out = out->state.h;
+        a.last_u_out = out->state.last_u;
+        a.angle_out = in->theta ? out->state.angle : nullptr;
+    }
+    hipError_t e = m3::launch_scan(a, s);
+    if (e != hipSuccess) return hip_fail(e, "scan launch");
+    g_launches.fetch_add(1, std::memory_order_relaxed);
+    return ok();
+}
+
+m3_status m3_ssd_chunked(const m3_ssd_args *in, void *y, float *final_state, void *stream) {
+    if (in == nullptr) return fail(M3_ERR_ARGUMENT, "arguments are NULL");
+    if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
+    if (in->head_dim == 0 || in->d_state == 0)
+        return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
+    if (in->head_dim > m3::kScanMaxHeadDim || in->d_state > m3::kScanMaxState)
+        return fail(M3_ERR_UNSUPPORTED, "head_dim %zu / d_state %zu exceed the scan kernel's",
+                    in->head_dim, in->d_state);
+    if (in->want_state && final_state == nullptr)
+        return fail(M3_ERR_ARGUMENT, "want_state needs a final_state buffer");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t B = in->batch, H = in->heads, P = in->head_dim, N = in->d_state;
+    if (B * H == 0) return ok();
+    if (in->seq == 0) {   // scan.rs:134-144
+        if (in->want_state) {
+            const size_t sbytes = B * H * P * N * sizeof(float);
+            hipError_t e = in->initial_state
+                               ? hipMemcpyAsync(final_state, in->initial_state, sbytes,
+                                                hipMemcpyDeviceToDevice, s)
+                               : hipMemsetAsync(final_state, 0, sbytes, s);
+            if (e != hipSuccess) return hip_fail(e, "state pass-through");
+        }
+        return ok();
+    }
+    if (in->x == nullptr || in->b == nullptr || in->c == nullptr || in->a == nullptr ||
+        in->g == nullptr || in->w == nullptr || y == nullptr)
+        return fail(M3_ERR_ARGUMENT, "x, b, c, a, g, w and y are required");
+    m3::ScanLaunch a{};
+    a.batch = B;
+    a.seq = in->seq;
+    a.heads = H;
+    a.head_dim = P;
+    a.d_state = N;
+    a.rank = 1;
+    a.bf16 = in->dtype == M3_BF16;
+    a.mode_raw = 0;
+    a.x = in->x;
+    a.b = in->b;
+    a.c = in->c;
+    a.a = in->a;
+    a.g = in->g;
+    a.w = in->w;
+    a.init_state = in->initial_state;
+    a.y = y;
+    a.h_out = in->want_state ? final_state : nullptr;
+    hipError_t e = m3::launch_scan(a, s);
+    if (e != hipSuccess) return hip_fail(e, "ssd_chunked launch");
+    g_launches.fetch_add(1, std::memory_order_relaxed);
+    return ok();
+}
+
+m3_status m3_step(const m3_step_inputs *in, m3_ssm_state *state, void *y, void *stream) {
+    if (in == nullptr || state == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/state are NULL");
+    if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
+    if (in->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
+    if (in->head_dim == 0 || in->d_state == 0)
+        return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
+    if (in->theta != nullptr && in->d_state % 2 != 0)
+        return fail(M3_ERR_CONFIG, "rotational dynamics require an even d_state");
+    if (state->h == nullptr || state->last_u == nullptr)
+        return fail(M3_ERR_ARGUMENT, "state needs both h and last_u");
+    if (in->theta != nullptr && state->angle == nullptr)
+        return fail(M3_ERR_ARGUMENT, "theta needs the state's angle buffer (updated in place)");
+    if (in->batch * in->heads == 0) return ok();
+    if (in->x == nullptr || in->b == nullptr || in->c == nullptr || in->dt == nullptr ||
+        in->lambda == nullptr || in->a_log == nullptr || y == nullptr)
+        return fail(M3_ERR_ARGUMENT, "x, b, c, dt, lambda, a_log and y are required");
+    if (in->d_state * in->rank * 2 + in->head_dim * in->rank > 16384)
+        return fail(M3_ERR_UNSUPPORTED, "d_state/head_dim/rank too large for the step kernel");
+    m3::StepLaunch a{};
+    a.batch = in->batch;
+    a.heads = in->heads;
+    a.head_dim = in->head_dim;
+    a.d_state = in->d_state;
+    a.rank = in->rank;
+    a.bf16 = in->dtype == M3_BF16;
+    a.x = in->x;
+    a.b = in->b;
+    a.c = in->c;
+    a.dt = in->dt;
+    a.lambda = in->lambda;
+    a.a_log = in->a_log;
+    a.theta = in->theta;
+    a.d_skip = in->d_skip;
+    a.h = state->h;
+    a.last_u = state->last_u;
+    a.angle = in->theta ? state->angle : nullptr;
+    a.y = y;
+    // the vector body issues 16-byte state accesses
+    const bool aligned = (reinterpret_cast<uintptr_t>(a.h) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(a.last_u) % 16 == 0);
+    if (!aligned) return fail(M3_ERR_ARGUMENT, "state buffers must be 16-byte aligned");
+    hipError_t e = m3::launch_step(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "step launch");
+    g_launches.fetch_add(1, std::memory_order_relaxed);
+    return ok();
+}
+
+const char *m3_status_string(m3_status s) {
+    switch (s) {
+        case M3_OK: return "M3_OK";
+        case M3_ERR_CONFIG: return "M3_ERR_CONFIG";
+        case M3_ERR_SHAPE: return "M3_ERR_SHAPE";
+        case M3_ERR_RANK: return "M3_ERR_RANK";
+        case M3_ERR_UNSUPPORTED: return "M3_ERR_UNSUPPORTED";
+        case M3_ERR_HIP: return "M3_ERR_HIP";
+        case M3_ERR_ARGUMENT: return "M3_ERR_ARGUMENT";
+    }
+    return "M3_UNKNOWN";
+}
+
+const char *m3_last_error(void) { return g_last_error.c_str(); }
+
+uint64_t m3_launch_count(void) { return g_launches.load(std::memory_order_relaxed); }
+
+m3_status m3_selftest_mfma(int32_t *result) {
+    if (result == nullptr) return fail(M3_ERR_ARGUMENT, "result pointer is NULL");
+    int r = -1;
+    hipError_t e = m3::launch_mfma_selftest(&r);
+    if (e != hipSuccess) return hip_fail(e, "mfma self test");
+    *result = r;
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,89 @@
+// Device-side helpers shared by the gfx950 kernels: storage conversions,
+// MFMA wrappers with their lane layouts, and wave-level collectives.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace m3 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// bf16 storage is raw 16-bit words; widening is a shift, narrowing rounds to
+// nearest-even (v_cvt_pk_bf16_f32 on gfx950).
+struct bf16_t {
+    uint16_t bits;
+};
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
+    __bf16 h = static_cast<__bf16>(v);
+    bf16_t r;
+    r.bits = __builtin_bit_cast(uint16_t, h);
+    return r;
+}
+
+__device__ __forceinline__ __bf16 to_bf16(float v) { return static_cast<__bf16>(v); }
+
+// ---------------------------------------------------------------------------
+// MFMA.  Both variants compute a 16x16 f32 tile D += A(16xK) * B(Kx16).
+// Lane l of the wave, g = l / 16, c = l % 16:
+//   A operand: row c, k-slots owned by lane group g
+//   B operand: column c, the same k-slots
+//   D: column c, rows 4g + r for r = 0..3 (element r of the f32x4)
+// bf16 16x16x32: lane group g owns k = 8g .. 8g+7 (eight bf16 per lane).
+// f32  16x16x4 : lane group g owns k = g (one f32 per lane).
+// Any permutation of k is valid as long as A and B use the same one; the
+// kernels exploit this to feed accumulators straight back in as operands.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level (64-lane) collectives.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_inclusive_scan(float v, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        float o = __shfl_up(v, off, 64);
+        if (lane >= off) v += o;
+    }
+    return v;
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+__device__ __forceinline__ float group_sum(float v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Wrap an angle into [-pi, pi] by subtracting whole turns, as
+// x - round(x / 2pi) * 2pi (the reference's wrap, elemwise.rs:349).
+__device__ __forceinline__ float wrap_angle(float x) {
+    const float two_pi = 6.28318530717958647692f;
+    return x - rintf(x * 0.15915494309189533577f) * two_pi;
+}
+
+// exp(clamp(d, -60, 0)): the scan's decay factor with its log floor.
+__device__ __forceinline__ float decay_exp(float d) {
+    d = fminf(fmaxf(d, -60.0f), 0.0f);
+    return expf(d);
+}
+
+}  // namespace m3

@@ -1,0 +1,127 @@
+"""ctypes binding of libmamba3_hip.so (include/mamba3_ssm.h).
+
+Loading fails loudly when the library is missing: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+from .error import (ArgumentError, ConfigError, DeviceError, Mamba3Error, RankError,
+                    ShapeError, UnsupportedError)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmamba3_hip.so")
+
+M3_OK, M3_ERR_CONFIG, M3_ERR_SHAPE, M3_ERR_RANK = 0, 1, 2, 3
+M3_ERR_UNSUPPORTED, M3_ERR_HIP, M3_ERR_ARGUMENT = 4, 5, 6
+M3_F32, M3_BF16 = 0, 1
+
+_Z = C.c_size_t
+_P = C.c_void_p
+_FP = C.POINTER(C.c_float)
+
+
+class SsmConfigC(C.Structure):
+    _fields_ = [
+        ("d_model", _Z), ("n_heads", _Z), ("head_dim", _Z), ("d_state", _Z), ("n_groups", _Z),
+        ("discretization", C.c_int32), ("dynamics", C.c_int32),
+        ("rank", _Z), ("chunk_size", _Z), ("conv_kernel", _Z),
+        ("bc_norm", C.c_int32), ("bc_bias", C.c_int32), ("post_gate_norm", C.c_int32),
+        ("skip_connection", C.c_int32),
+        ("dt_min", C.c_float), ("dt_max", C.c_float), ("dt_init_floor", C.c_float),
+        ("a_init_min", C.c_float), ("a_init_max", C.c_float),
+        ("bias", C.c_int32),
+    ]
+
+
+class SsmStateC(C.Structure):
+    _fields_ = [("h", _P), ("last_u", _P), ("angle", _P)]
+
+
+class ScanInputsC(C.Structure):
+    _fields_ = [
+        ("batch", _Z), ("seq", _Z), ("heads", _Z), ("head_dim", _Z), ("d_state", _Z),
+        ("rank", _Z), ("dtype", C.c_int32),
+        ("x", _P), ("b", _P), ("c", _P), ("dt", _P), ("a_log", _P), ("lambda_", _P),
+        ("theta", _P), ("d_skip", _P), ("state", C.POINTER(SsmStateC)),
+        ("chunk_size", _Z), ("want_state", C.c_int32),
+    ]
+
+
+class ScanOutputC(C.Structure):
+    _fields_ = [("y", _P), ("state", SsmStateC)]
+
+
+class SsdArgsC(C.Structure):
+    _fields_ = [
+        ("batch", _Z), ("seq", _Z), ("heads", _Z), ("head_dim", _Z), ("d_state", _Z),
+        ("dtype", C.c_int32),
+        ("x", _P), ("b", _P), ("c", _P), ("a", _P), ("g", _P), ("w", _P),
+        ("initial_state", _P), ("chunk_size", _Z), ("want_state", C.c_int32),
+    ]
+
+
+class StepInputsC(C.Structure):
+    _fields_ = [
+        ("batch", _Z), ("heads", _Z), ("head_dim", _Z), ("d_state", _Z), ("rank", _Z),
+        ("dtype", C.c_int32),
+        ("x", _P), ("b", _P), ("c", _P), ("dt", _P), ("lambda_", _P), ("a_log", _P),
+        ("theta", _P), ("d_skip", _P),
+    ]
+
+
+# Every exported symbol of include/mamba3_ssm.h with its ctypes signature.
+SIGNATURES = {
+    "m3_config_default": (C.c_int, [C.POINTER(SsmConfigC)]),
+    "m3_config_validate": (C.c_int, [C.POINTER(SsmConfigC)]),
+    "m3_config_d_inner": (_Z, [C.POINTER(SsmConfigC)]),
+    "m3_config_bc_width": (_Z, [C.POINTER(SsmConfigC)]),
+    "m3_config_theta_width": (_Z, [C.POINTER(SsmConfigC)]),
+    "m3_config_lambda_width": (_Z, [C.POINTER(SsmConfigC)]),
+    "m3_config_in_proj_width": (_Z, [C.POINTER(SsmConfigC)]),
+    "m3_discretization_fixed_lambda": (C.c_float, [C.c_int32]),
+    "m3_scan": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanOutputC), _P]),
+    "m3_ssd_chunked": (C.c_int, [C.POINTER(SsdArgsC), _P, _P, _P]),
+    "m3_step": (C.c_int, [C.POINTER(StepInputsC), C.POINTER(SsmStateC), _P, _P]),
+    "m3_status_string": (C.c_char_p, [C.c_int]),
+    "m3_last_error": (C.c_char_p, []),
+    "m3_launch_count": (C.c_uint64, []),
+    "m3_selftest_mfma": (C.c_int, [C.POINTER(C.c_int32)]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libmamba3_hip.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python mamba-trainer_amd/build_lib.py` "
+                "(or __graft_entry__.build()); there is no fallback implementation")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+_ERRORS = {
+    M3_ERR_CONFIG: ConfigError,
+    M3_ERR_SHAPE: ShapeError,
+    M3_ERR_RANK: ShapeError,
+    M3_ERR_UNSUPPORTED: UnsupportedError,
+    M3_ERR_HIP: DeviceError,
+    M3_ERR_ARGUMENT: ArgumentError,
+}
+
+
+def check(status: int):
+    if status == M3_OK:
+        return
+    msg = lib().m3_last_error().decode(errors="replace")
+    raise _ERRORS.get(status, Mamba3Error)(msg)

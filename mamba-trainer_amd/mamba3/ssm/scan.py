@@ -1,0 +1,292 @@
+"""The chunked scan and the decode step (src/ssm/scan.rs), on the gfx950 kernels.
+
+Same names, argument meanings and errors as the reference's `ssm::scan`
+module; every call goes through the C ABI of libmamba3_hip.so
+(include/mamba3_ssm.h).  torch tensors are used only as device buffers: the
+arithmetic is in the HIP kernels, and there is no CPU or torch fallback --
+tensors that are not on a ROCm device are rejected.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from .. import _lib
+from ..error import ArgumentError, RankError, ShapeError, UnsupportedError
+
+_DTYPES = {torch.float32: _lib.M3_F32, torch.bfloat16: _lib.M3_BF16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise UnsupportedError(f"unsupported: storage dtype {t.dtype}; use float32 or bfloat16")
+
+
+def _dev(t: torch.Tensor, what: str) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ArgumentError(f"{what} must be a ROCm device tensor (got {t.device}); "
+                            "the scan has no CPU path")
+    return t.contiguous()
+
+
+def _f32(t: Optional[torch.Tensor], what: str) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    t = _dev(t, what)
+    return t if t.dtype == torch.float32 else t.float()
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _expect_shape(t: torch.Tensor, shape, what: str):
+    if tuple(t.shape) != tuple(shape):
+        raise ShapeError(f"shape error: {what} has shape {list(t.shape)}, expected {list(shape)}")
+
+
+@dataclass
+class SsmState:
+    """scan.rs:293-358: h and last_u [B, H, P, N] (f32), angle [B, H, N/2] or None."""
+    h: torch.Tensor
+    last_u: torch.Tensor
+    angle: Optional[torch.Tensor] = None
+
+    def num_elements(self) -> int:
+        return self.h.numel() + self.last_u.numel() + (
+            self.angle.numel() if self.angle is not None else 0)
+
+    @staticmethod
+    def zeros(batch, heads, head_dim, d_state, rotational, device) -> "SsmState":
+        shape = (batch, heads, head_dim, d_state)
+        return SsmState(
+            torch.zeros(shape, dtype=torch.float32, device=device),
+            torch.zeros(shape, dtype=torch.float32, device=device),
+            torch.zeros((batch, heads, d_state // 2), dtype=torch.float32, device=device)
+            if rotational else None)
+
+    def clone(self) -> "SsmState":
+        return SsmState(self.h.clone(), self.last_u.clone(),
+                        None if self.angle is None else self.angle.clone())
+
+    def detach(self) -> "SsmState":
+        return SsmState(self.h.detach(), self.last_u.detach(),
+                        None if self.angle is None else self.angle.detach())
+
+    def _c(self) -> _lib.SsmStateC:
+        return _lib.SsmStateC(self.h.data_ptr(), self.last_u.data_ptr(),
+                              None if self.angle is None else self.angle.data_ptr())
+
+
+class ScanInputs:
+    """scan.rs:360-443, with the same builder methods and defaults."""
+
+    def __init__(self, x, b, c, dt, a_log, lam):
+        self.x, self.b, self.c = x, b, c
+        self.dt, self.a_log, self.lam = dt, a_log, lam
+        self.theta = None
+        self.d_skip = None
+        self.state: Optional[SsmState] = None
+        self.chunk_size = 64
+        self.want_state = True
+
+    def with_theta(self, theta):
+        self.theta = theta
+        return self
+
+    def with_skip(self, d_skip):
+        self.d_skip = d_skip
+        return self
+
+    def with_state(self, state: SsmState):
+        self.state = state
+        return self
+
+    def with_chunk_size(self, chunk_size: int):
+        self.chunk_size = chunk_size
+        return self
+
+    def with_state_output(self, want_state: bool):
+        self.want_state = want_state
+        return self
+
+
+@dataclass
+class ScanOutput:
+    """scan.rs:445-452."""
+    y: torch.Tensor
+    state: Optional[SsmState]
+
+
+def mamba3_scan(inputs: ScanInputs) -> ScanOutput:
+    """scan.rs:454-618: the Mamba-3 selective scan, one kernel launch."""
+    x = inputs.x
+    if x.dim() != 5:
+        raise RankError(5, x.dim(), x.shape)
+    B, T, H, P, R = x.shape
+    if inputs.b.dim() != 5:
+        raise RankError(5, inputs.b.dim(), inputs.b.shape)
+    N = inputs.b.shape[3]
+    code = _dtype_code(x)
+    x = _dev(x, "x")
+    b = _dev(inputs.b, "b")
+    c = _dev(inputs.c, "c")
+    for t, what in ((b, "b"), (c, "c")):
+        if t.dtype != x.dtype:
+            raise ShapeError(f"shape error: {what} is {t.dtype} but x is {x.dtype}")
+    _expect_shape(b, (B, T, H, N, R), "b")
+    _expect_shape(c, (B, T, H, N, R), "c")
+    dt = _f32(inputs.dt, "dt")
+    lam = _f32(inputs.lam, "lambda")
+    a_log = _f32(inputs.a_log, "a_log")
+    _expect_shape(dt, (B, T, H), "dt")
+    _expect_shape(lam, (B, T, H), "lambda")
+    _expect_shape(a_log, (H,), "a_log")
+    theta = None
+    if inputs.theta is not None:
+        theta = _dev(inputs.theta, "theta")
+        if theta.dtype != x.dtype:
+            theta = theta.to(x.dtype)
+        if N % 2 == 0:
+            _expect_shape(theta, (B, T, H, N // 2), "theta")
+    d_skip = _f32(inputs.d_skip, "d_skip")
+    if d_skip is not None:
+        _expect_shape(d_skip, (H,), "d_skip")
+    st = inputs.state
+    st_c = None
+    keep = []
+    if st is not None:
+        h0, l0 = _f32(st.h, "state.h"), _f32(st.last_u, "state.last_u")
+        _expect_shape(h0, (B, H, P, N), "state.h")
+        _expect_shape(l0, (B, H, P, N), "state.last_u")
+        a0 = _f32(st.angle, "state.angle") if (st.angle is not None and theta is not None) else None
+        keep += [h0, l0, a0]
+        st_c = _lib.SsmStateC(h0.data_ptr(), l0.data_ptr(),
+                              None if a0 is None else a0.data_ptr())
+
+    y = torch.empty_like(x)
+    out_state = None
+    if inputs.want_state:
+        out_state = SsmState(
+            torch.empty((B, H, P, N), dtype=torch.float32, device=x.device),
+            torch.empty((B, H, P, N), dtype=torch.float32, device=x.device),
+            torch.empty((B, H, N // 2), dtype=torch.float32, device=x.device)
+            if theta is not None else None)
+    cin = _lib.ScanInputsC(
+        B, T, H, P, N, R, code, x.data_ptr(), b.data_ptr(), c.data_ptr(), dt.data_ptr(),
+        a_log.data_ptr(), lam.data_ptr(), None if theta is None else theta.data_ptr(),
+        None if d_skip is None else d_skip.data_ptr(),
+        C.pointer(st_c) if st_c is not None else None,
+        int(inputs.chunk_size), int(bool(inputs.want_state)))
+    cout = _lib.ScanOutputC(y.data_ptr(), out_state._c() if out_state else _lib.SsmStateC())
+    _lib.check(_lib.lib().m3_scan(C.byref(cin), C.byref(cout), _stream(x)))
+    return ScanOutput(y, out_state)
+
+
+def ssd_chunked(x, b, c, a, g, w, initial_state=None, chunk_size=64,
+                want_state=True) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """scan.rs:98-291: x [B,T,H,P]; b, c [B,T,H,N]; a, g, w [B,T,H]."""
+    if x.dim() != 4:
+        raise RankError(4, x.dim(), x.shape)
+    if b.dim() != 4:
+        raise RankError(4, b.dim(), b.shape)
+    B, T, H, P = x.shape
+    N = b.shape[3]
+    code = _dtype_code(x)
+    x, b, c = _dev(x, "x"), _dev(b, "b"), _dev(c, "c")
+    _expect_shape(b, (B, T, H, N), "b")
+    _expect_shape(c, (B, T, H, N), "c")
+    a, g, w = _f32(a, "a"), _f32(g, "g"), _f32(w, "w")
+    for t, what in ((a, "a"), (g, "g"), (w, "w")):
+        _expect_shape(t, (B, T, H), what)
+    init = _f32(initial_state, "initial_state")
+    if init is not None:
+        _expect_shape(init, (B, H, P, N), "initial_state")
+    y = torch.empty_like(x)
+    fs = torch.empty((B, H, P, N), dtype=torch.float32, device=x.device) if want_state else None
+    args = _lib.SsdArgsC(B, T, H, P, N, code, x.data_ptr(), b.data_ptr(), c.data_ptr(),
+                         a.data_ptr(), g.data_ptr(), w.data_ptr(),
+                         None if init is None else init.data_ptr(), int(chunk_size),
+                         int(bool(want_state)))
+    _lib.check(_lib.lib().m3_ssd_chunked(C.byref(args), C.c_void_p(y.data_ptr()),
+                                         _ptr(fs), _stream(x)))
+    return y, fs
+
+
+def _step_args(x, b, c, dt, lam, a_log, theta, d_skip):
+    if x.dim() != 4:
+        raise RankError(4, x.dim(), x.shape)
+    B, H, P, R = x.shape
+    N = b.shape[2]
+    code = _dtype_code(x)
+    x, b, c = _dev(x, "x"), _dev(b, "b"), _dev(c, "c")
+    _expect_shape(b, (B, H, N, R), "b")
+    _expect_shape(c, (B, H, N, R), "c")
+    dt, lam, a_log = _f32(dt, "dt"), _f32(lam, "lambda"), _f32(a_log, "a_log")
+    _expect_shape(dt.reshape(-1), (B * H,), "dt")
+    _expect_shape(lam.reshape(-1), (B * H,), "lambda")
+    _expect_shape(a_log, (H,), "a_log")
+    if theta is not None:
+        theta = _dev(theta, "theta")
+        if theta.dtype != x.dtype:
+            theta = theta.to(x.dtype)
+    d_skip = _f32(d_skip, "d_skip")
+    keep = (x, b, c, dt, lam, a_log, theta, d_skip)
+    args = _lib.StepInputsC(B, H, P, N, R, code, x.data_ptr(), b.data_ptr(), c.data_ptr(),
+                            dt.data_ptr(), lam.data_ptr(), a_log.data_ptr(),
+                            None if theta is None else theta.data_ptr(),
+                            None if d_skip is None else d_skip.data_ptr())
+    return args, keep
+
+
+def mamba3_step_(x, b, c, dt, lam, a_log, theta, d_skip, state: SsmState) -> torch.Tensor:
+    """mamba3_step with the state updated IN PLACE (the C ABI's semantics); returns y."""
+    args, keep = _step_args(x, b, c, dt, lam, a_log, theta, d_skip)
+    B, H, P, R = keep[0].shape
+    N = keep[1].shape[2]
+    for t, what in ((state.h, "state.h"), (state.last_u, "state.last_u")):
+        if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+            raise ArgumentError(f"{what} must be a contiguous float32 device tensor")
+        _expect_shape(t, (B, H, P, N), what)
+    if theta is not None:
+        if state.angle is None:
+            raise ArgumentError("theta needs the state's angle tensor (updated in place)")
+        _expect_shape(state.angle, (B, H, N // 2), "state.angle")
+    y = torch.empty_like(keep[0])
+    st_c = state._c()
+    _lib.check(_lib.lib().m3_step(C.byref(args), C.byref(st_c), C.c_void_p(y.data_ptr()),
+                                  _stream(keep[0])))
+    return y
+
+
+def mamba3_step(x, b, c, dt, lam, a_log, theta, d_skip,
+                state: SsmState) -> Tuple[torch.Tensor, SsmState]:
+    """scan.rs:640-712: one decoding step; returns (y, new SsmState) like the reference."""
+    new = state.clone()
+    if theta is not None and new.angle is None:
+        B, H = x.shape[0], x.shape[1]
+        new.angle = torch.zeros((B, H, b.shape[2] // 2), dtype=torch.float32, device=x.device)
+    y = mamba3_step_(x, b, c, dt, lam, a_log, theta, d_skip, new)
+    if theta is None:
+        new.angle = None
+    return y, new
+
+
+def shift_left(x: torch.Tensor, axis: int) -> torch.Tensor:
+    """scan.rs:59-75: shift towards smaller indices along `axis`, zero-filling the end."""
+    n = x.shape[axis]
+    if n == 0:
+        return x.clone()
+    out = torch.zeros_like(x)
+    if n > 1:
+        out.narrow(axis, 0, n - 1).copy_(x.narrow(axis, 1, n - 1))
+    return out

@@ -1,0 +1,146 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol,
+and its host-only entry points (config validation, widths, argument checks
+that fail before any device work) behave like the reference.  No GPU needed.
+"""
+import ctypes as C
+import math
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "mamba3_ssm.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(m3_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from mamba3 import _lib
+    L = _lib.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 15
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, f"declared but not exported: {missing}"
+    # and the Python binding declares a signature for each of them
+    assert set(syms) == set(_lib.SIGNATURES), set(syms) ^ set(_lib.SIGNATURES)
+
+
+def test_status_strings():
+    from mamba3 import _lib
+    L = _lib.lib()
+    assert L.m3_status_string(0) == b"M3_OK"
+    assert L.m3_status_string(4) == b"M3_ERR_UNSUPPORTED"
+
+
+def test_config_defaults_match_reference():
+    """config.rs:130-156."""
+    from mamba3.ssm import Discretization, SsmConfig, StateDynamics
+    c = SsmConfig.default_from_abi()
+    assert (c.d_model, c.n_heads, c.head_dim, c.d_state, c.n_groups) == (768, 24, 64, 64, 24)
+    assert c.discretization == Discretization.LearnedTrapezoid
+    assert c.dynamics == StateDynamics.Rotational
+    assert c.mode.rank() == 1 and c.chunk_size == 64 and c.conv_kernel == 4
+    assert c.bc_norm and c.bc_bias and not c.post_gate_norm and c.skip_connection
+    assert math.isclose(c.dt_min, 0.001, rel_tol=1e-6) and math.isclose(c.dt_max, 0.1, rel_tol=1e-6)
+    assert (c.a_init_min, c.a_init_max) == (1.0, 16.0)
+
+
+def test_config_widths():
+    """config.rs:164-200."""
+    from mamba3.ssm import Discretization, SsmConfig, SsmMode, StateDynamics
+    c = SsmConfig(n_heads=12, n_groups=12, head_dim=64, d_state=128, mode=SsmMode.mimo(4))
+    assert c.d_inner() == 12 * 64 * 4
+    assert c.bc_width() == 12 * 128 * 4
+    assert c.theta_width() == 12 * 64
+    assert c.lambda_width() == 12
+    assert c.in_proj_width() == 2 * c.d_inner() + 2 * c.bc_width() + 12 + 12 + 12 * 64
+    c.dynamics = StateDynamics.Real
+    c.discretization = Discretization.Euler
+    assert c.theta_width() == 0 and c.lambda_width() == 0
+    assert Discretization.Euler.fixed_lambda() == 1.0
+    assert Discretization.Trapezoid.fixed_lambda() == 0.5
+    assert Discretization.LearnedTrapezoid.fixed_lambda() is None
+
+
+@pytest.mark.parametrize("change,message", [
+    (dict(d_state=0), "SSM dimensions must all be positive"),
+    (dict(n_heads=6, n_groups=4), "n_heads (6) must be a multiple of n_groups (4)"),
+    (dict(d_state=7), "d_state must be even, got 7"),
+    (dict(chunk_size=0), "chunk_size must be positive"),
+    (dict(mode="rank0"), "MIMO rank must be positive"),
+    (dict(dt_min=0.2, dt_max=0.1), "expected 0 < dt_min < dt_max"),
+    (dict(a_init_min=0.0), "expected 0 < a_init_min <= a_init_max"),
+    (dict(conv_kernel=1), "conv_kernel must be at least 2"),
+])
+def test_config_validation_rules(change, message):
+    """config.rs:203-245, rule by rule, with the reference's messages."""
+    from mamba3 import ConfigError
+    from mamba3.ssm import SsmConfig, SsmMode
+    c = SsmConfig()
+    for k, v in change.items():
+        if v == "rank0":
+            c.mode = SsmMode(0)
+        else:
+            setattr(c, k, v)
+    with pytest.raises(ConfigError) as e:
+        c.validate()
+    assert message in str(e.value)
+    assert str(e.value).startswith("invalid configuration: ")
+
+
+def test_builder_expand_and_build():
+    """config.rs:331-347."""
+    from mamba3.ssm import SsmConfig
+    c = SsmConfig.builder().d_model(256).head_dim(32).expand(2.0).build()
+    assert c.n_heads == 16 and c.n_groups == 16
+
+
+def _scan_inputs(**kw):
+    from mamba3 import _lib
+    base = dict(batch=1, seq=4, heads=1, head_dim=4, d_state=4, rank=1, dtype=0, x=None,
+                b=None, c=None, dt=None, a_log=None, lambda_=None, theta=None, d_skip=None,
+                state=None, chunk_size=4, want_state=0)
+    base.update(kw)
+    return _lib.ScanInputsC(**base)
+
+
+@pytest.mark.parametrize("kw,status,message", [
+    (dict(rank=0), 1, "MIMO rank must be positive"),
+    (dict(d_state=5, theta=1), 1, "rotational dynamics require an even d_state"),
+    (dict(head_dim=0), 1, "SSM dimensions must all be positive"),
+    (dict(head_dim=256), 4, "head_dim 256 exceeds"),
+    (dict(d_state=512), 4, "d_state 512 exceeds"),
+    (dict(rank=65, dtype=1), 4, "MIMO rank 65 exceeds"),
+    (dict(dtype=7), 6, "unknown dtype"),
+    (dict(want_state=1), 6, "want_state needs output h and last_u"),
+])
+def test_scan_argument_validation_before_device_work(kw, status, message):
+    """Reference rules (scan.rs:462, 485-489; config.rs:203-245) rejected on the host."""
+    from mamba3 import _lib
+    L = _lib.lib()
+    cin = _scan_inputs(**kw)
+    cout = _lib.ScanOutputC()
+    st = L.m3_scan(C.byref(cin), C.byref(cout), None)
+    assert st == status, L.m3_last_error()
+    assert message in L.m3_last_error().decode()
+
+
+def test_python_api_rejects_host_tensors():
+    """The product path has no CPU fallback: host tensors fail loudly."""
+    import torch
+    from mamba3 import ArgumentError, RankError
+    from mamba3.ssm import ScanInputs, mamba3_scan
+    x = torch.zeros(1, 4, 1, 4, 1)
+    b = torch.zeros(1, 4, 1, 4, 1)
+    dt = torch.zeros(1, 4, 1)
+    a_log = torch.zeros(1)
+    with pytest.raises(ArgumentError, match="no CPU path"):
+        mamba3_scan(ScanInputs(x, b, b, dt, a_log, dt))
+    with pytest.raises(RankError):
+        mamba3_scan(ScanInputs(x[..., 0], b, b, dt, a_log, dt))

@@ -1,0 +1,239 @@
+"""GPU parity of the chunked scan (m3_scan / m3_ssd_chunked through the C ABI)
+against the CPU oracle on the same seeded inputs.
+
+Bars: f32 rel-L2 <= 1e-5 against the f64 recurrence (and the reference test
+metric, worst |a-e|/(1+|e|), at the reference's own tolerances against its
+own oracle); bf16 storage rel-L2 <= 1e-2 against the f64 recurrence evaluated
+on the same bf16-rounded inputs.
+"""
+import math
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from cases import Case, assert_close, baseline_inputs, rel_l2
+from gpu_util import dev, host, oracle_scan, run_scan
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_TOL = 1e-2
+
+
+def angle_err(a, b):
+    d = np.asarray(a, np.float64) - np.asarray(b, np.float64)
+    d = (d + math.pi) % (2 * math.pi) - math.pi
+    return float(np.max(np.abs(d))) if d.size else 0.0
+
+
+def test_mfma_lane_layouts():
+    import mamba3
+    assert mamba3.selftest_mfma() == 0
+
+
+# ---------------------------------------------------------------- the reference's own cases
+
+@pytest.mark.parametrize("chunk", [1, 2, 3, 4, 8, 16])
+def test_chunked_scan_matches_the_recurrence(chunk):
+    """tests/ssm.rs:187-205 through m3_ssd_chunked."""
+    from mamba3.ssm import ssd_chunked
+    case = Case(2, 12, 3, 4, 6)
+    a, g, w = case.weights()
+    y, st = ssd_chunked(dev(case.x), dev(case.b), dev(case.c), dev(a), dev(g), dev(w), None,
+                        chunk, True)
+    want_y, want_h = case.reference()
+    assert_close(host(y), want_y, 2e-4, f"y (chunk={chunk})")
+    assert_close(host(st), want_h, 2e-4, f"final state (chunk={chunk})")
+    y64, h64, _, _ = oracle.scan_recurrence_f64(*[v[..., None] for v in (case.x, case.b, case.c)],
+                                                case.dt, case.a_log, case.lam)
+    assert rel_l2(host(y), y64[..., 0]) <= F32_TOL
+    assert rel_l2(host(st), h64) <= F32_TOL
+
+
+@pytest.mark.parametrize("seq", [1, 5, 7, 13])
+def test_chunked_scan_handles_ragged_lengths(seq):
+    """tests/ssm.rs:207-220."""
+    from mamba3.ssm import ssd_chunked
+    case = Case(1, seq, 2, 3, 4)
+    a, g, w = case.weights()
+    y, st = ssd_chunked(dev(case.x), dev(case.b), dev(case.c), dev(a), dev(g), dev(w), None, 4,
+                        True)
+    want_y, want_h = case.reference()
+    assert_close(host(y), want_y, 2e-4, f"y (seq={seq})")
+    assert_close(host(st), want_h, 2e-4, f"state (seq={seq})")
+
+
+def test_euler_mode_reproduces_mamba2():
+    """tests/ssm.rs:222-236: want_state=false returns no state."""
+    from mamba3.ssm import ssd_chunked
+    case = Case(1, 8, 2, 3, 4)
+    case.lam = np.ones_like(case.lam)
+    a, g, w = case.weights()
+    assert np.abs(w - g).max() <= 1e-6
+    y, st = ssd_chunked(dev(case.x), dev(case.b), dev(case.c), dev(a), dev(g), dev(w), None, 4,
+                        False)
+    assert st is None
+    want_y, _ = case.reference()
+    assert_close(host(y), want_y, 2e-4, "euler y")
+
+
+def test_split_windows_match_a_single_pass():
+    """tests/ssm.rs:238-310: rotation plus state carried across a cut at t=5."""
+    case = Case(2, 12, 2, 3, 4)
+    theta = case.theta()
+    x, b, c = case.rank1()
+    full = dict(x=x, b=b, c=c, dt=case.dt, a_log=case.a_log, lam=case.lam, theta=theta)
+
+    def part(sl):
+        return {k: (v[:, sl] if k not in ("a_log",) else v) for k, v in full.items()}
+
+    y_full, h_full, _, _ = run_scan(full, chunk=4)
+    y1, h1, l1, a1 = run_scan(part(slice(0, 5)), chunk=4)
+    y2, h2, _, _ = run_scan(part(slice(5, 12)), chunk=4, state=(h1, l1, a1))
+    assert_close(np.concatenate([y1, y2], axis=1), y_full, 3e-4, "split vs full")
+    assert_close(h2, h_full, 3e-4, "split final state")
+    y64, h64, _, _ = oracle_scan(full)
+    assert rel_l2(y_full, y64) <= F32_TOL and rel_l2(h_full, h64) <= F32_TOL
+
+
+# ---------------------------------------------------------------- every ScanInputs feature
+
+FEATURE_CASES = [
+    # B, T, H, P, N, R, theta, skip, state, dtype
+    (2, 37, 3, 16, 32, 1, True, True, True, "f32"),
+    (1, 100, 2, 64, 64, 1, False, False, False, "f32"),
+    (1, 129, 2, 64, 128, 1, True, True, True, "f32"),
+    (2, 70, 2, 24, 16, 2, True, True, True, "f32"),
+    (1, 50, 2, 32, 32, 3, True, False, True, "f32"),
+    (1, 40, 1, 16, 32, 4, True, True, False, "f32"),
+    (2, 37, 3, 16, 32, 1, True, True, True, "bf16"),
+    (1, 200, 2, 64, 128, 1, True, True, True, "bf16"),
+    (1, 130, 2, 64, 128, 4, True, True, True, "bf16"),
+    (1, 65, 1, 128, 256, 1, True, False, True, "bf16"),
+    (1, 33, 1, 48, 256, 2, True, True, True, "f32"),
+    (1, 9, 2, 3, 6, 1, True, True, True, "f32"),
+    (1, 1, 2, 5, 4, 2, True, True, True, "f32"),
+]
+
+
+@pytest.mark.parametrize("B,T,H,P,N,R,theta,skip,state,dtype", FEATURE_CASES)
+def test_scan_features_against_f64(B, T, H, P, N, R, theta, skip, state, dtype):
+    rng = np.random.default_rng(zlib.crc32(repr((B, T, H, P, N, R, theta, skip, state,
+                                                  dtype)).encode()))
+    inp = baseline_inputs(rng, B, T, H, P, N, R, theta=theta, dtype=dtype,
+                          theta_per_head=False, state=state)
+    d_skip = rng.uniform(-1, 1, H).astype(np.float32) if skip else None
+    st = (inp["h0"], inp["last_u0"], inp.get("angle0")) if state else None
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    y, h, lu, ang = run_scan(inp, dtype=tdt, theta=theta, skip=d_skip, state=st)
+    y64, h64, lu64, ang64 = oracle_scan(inp, theta=theta, skip=d_skip, state=st)
+    tol = BF16_TOL if dtype == "bf16" else F32_TOL
+    assert rel_l2(y, y64) <= tol, ("y", rel_l2(y, y64))
+    assert rel_l2(h, h64) <= tol, ("h", rel_l2(h, h64))
+    assert rel_l2(lu, lu64) <= tol, ("last_u", rel_l2(lu, lu64))
+    if theta:
+        assert angle_err(ang, ang64) <= (1e-4 if dtype == "f32" else 1e-3)
+
+
+def test_want_state_false_writes_no_state():
+    rng = np.random.default_rng(5)
+    inp = baseline_inputs(rng, 1, 20, 1, 16, 32, 1, theta=True)
+    y, h, lu, ang = run_scan(inp, want_state=False)
+    assert h is None and lu is None
+    y64, _, _, _ = oracle_scan(inp)
+    assert rel_l2(y, y64) <= F32_TOL
+
+
+def test_empty_window_passes_the_state_through():
+    """seq = 0: empty y; the carried state comes back unchanged."""
+    rng = np.random.default_rng(6)
+    inp = baseline_inputs(rng, 2, 0, 2, 16, 32, 1, theta=True, state=True)
+    st = (inp["h0"], inp["last_u0"], inp["angle0"])
+    y, h, lu, ang = run_scan(inp, state=st)
+    assert y.shape == (2, 0, 2, 16, 1)
+    assert np.array_equal(h, inp["h0"]) and np.array_equal(lu, inp["last_u0"])
+    assert np.array_equal(ang, inp["angle0"])
+
+
+def test_errors_surface_as_reference_errors():
+    from mamba3 import ConfigError, UnsupportedError
+    rng = np.random.default_rng(8)
+    inp = baseline_inputs(rng, 1, 8, 1, 16, 6, 1, theta=True)
+    inp["b"] = inp["b"][:, :, :, :5]
+    inp["c"] = inp["c"][:, :, :, :5]
+    inp["theta"] = inp["theta"][..., :2]
+    with pytest.raises(ConfigError, match="even d_state"):
+        run_scan(inp)
+    inp = baseline_inputs(rng, 1, 8, 1, 16, 32, 40, theta=False)
+    with pytest.raises(UnsupportedError, match="rank"):
+        run_scan(inp, dtype=torch.float32, theta=False)
+
+
+# ---------------------------------------------------------------- BASELINE configs
+
+def test_config0_f32_full_size():
+    """B2 L512 H4 P64 N64, f32, Real, LearnedTrapezoid."""
+    rng = np.random.default_rng(0x4D414D42)
+    inp = baseline_inputs(rng, 2, 512, 4, 64, 64, 1, theta=False)
+    y, h, lu, _ = run_scan(inp, theta=False)
+    y64, h64, lu64, _ = oracle_scan(inp, theta=False)
+    assert rel_l2(y, y64) <= F32_TOL
+    assert rel_l2(h, h64) <= F32_TOL
+    assert rel_l2(lu, lu64) <= F32_TOL
+    # and the composed f32 restatement of the reference algorithm agrees as well
+    yc, hc, _, _ = oracle.scan_composed_f32(inp["x"], inp["b"], inp["c"], inp["dt"],
+                                            inp["a_log"], inp["lam"], chunk=64)
+    assert rel_l2(y, yc) <= 1e-5
+
+
+def test_config1_bf16_two_heads_full_length():
+    """BASELINE config 1 shapes (L2048, P64, N128, bf16, Rotational) on 2 heads."""
+    rng = np.random.default_rng(0x4D414D43)
+    inp = baseline_inputs(rng, 1, 2048, 2, 64, 128, 1, theta=True, dtype="bf16")
+    y, h, lu, ang = run_scan(inp, dtype=torch.bfloat16)
+    y64, h64, lu64, ang64 = oracle_scan(inp)
+    assert rel_l2(y, y64) <= BF16_TOL
+    assert rel_l2(h, h64) <= BF16_TOL
+    assert angle_err(ang, ang64) <= 1e-3
+
+
+def test_config2_mimo_bf16_one_head():
+    """BASELINE config 2 shapes (MIMO R=4, L4096, P64, N128, bf16) on one head."""
+    rng = np.random.default_rng(0x4D414D44)
+    inp = baseline_inputs(rng, 1, 4096, 1, 64, 128, 4, theta=True, dtype="bf16")
+    y, h, lu, ang = run_scan(inp, dtype=torch.bfloat16)
+    y64, h64, lu64, ang64 = oracle_scan(inp)
+    assert rel_l2(y, y64) <= BF16_TOL
+    assert rel_l2(h, h64) <= BF16_TOL
+
+
+def test_config1_full_size_split_window_property():
+    """Full config 1 (B8 L2048 H12): scan(x) == scan(x[:1024]) then scan(x[1024:])
+    carrying the state -- a size-independent check at the benchmark shape."""
+    g = torch.Generator(device="cuda").manual_seed(1)
+    B, T, H, P, N = 8, 2048, 12, 64, 128
+    from mamba3.ssm import ScanInputs, mamba3_scan
+    x = torch.randn(B, T, H, P, 1, device="cuda", generator=g).to(torch.bfloat16)
+    b = (torch.randn(B, T, H, N, 1, device="cuda", generator=g) / math.sqrt(N)).to(torch.bfloat16)
+    c = (torch.randn(B, T, H, N, 1, device="cuda", generator=g) / math.sqrt(N)).to(torch.bfloat16)
+    dt = torch.nn.functional.softplus(torch.randn(B, T, H, device="cuda", generator=g) - 3
+                                      ).clamp(1e-3, 0.1)
+    lam = torch.sigmoid(torch.randn(B, T, H, device="cuda", generator=g))
+    a_log = torch.rand(H, device="cuda", generator=g) * math.log(16)
+    th = (torch.rand(1, 1, H, N // 2, device="cuda", generator=g) * math.pi).expand(
+        B, T, H, N // 2).contiguous().to(torch.bfloat16)
+    full = mamba3_scan(ScanInputs(x, b, c, dt, a_log, lam).with_theta(th))
+    cut = 1000
+    s = slice(0, cut)
+    first = mamba3_scan(ScanInputs(x[:, s], b[:, s], c[:, s], dt[:, s], a_log, lam[:, s])
+                        .with_theta(th[:, s]))
+    s = slice(cut, T)
+    second = mamba3_scan(ScanInputs(x[:, s], b[:, s], c[:, s], dt[:, s], a_log, lam[:, s])
+                         .with_theta(th[:, s]).with_state(first.state))
+    joined = torch.cat([first.y, second.y], dim=1).float()
+    assert rel_l2(host(joined), host(full.y)) <= BF16_TOL
+    assert rel_l2(host(second.state.h), host(full.state.h)) <= BF16_TOL
+    assert torch.isfinite(full.y.float()).all()

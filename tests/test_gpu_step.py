@@ -1,0 +1,147 @@
+"""GPU parity of the decode step (m3_step through the C ABI) against the oracle:
+the reference's step-vs-scan test, the f64 recurrence, the f32 restatement of
+mamba3_step, in-place semantics, and BASELINE config 3's shape (f32 state,
+rel-L2 <= 1e-5)."""
+import math
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from cases import Case, assert_close, rel_l2
+from gpu_util import dev, host
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+
+
+def test_step_matches_the_chunked_scan():
+    """tests/ssm.rs:312-380: stepwise mamba3_step (theta, D) vs the scan."""
+    from mamba3.ssm import ScanInputs, SsmState, mamba3_scan, mamba3_step
+    case = Case(2, 9, 2, 3, 4)
+    theta = case.theta()
+    d_skip = np.array([0.3, -0.2], np.float32)
+    x, b, c = case.rank1()
+    par = mamba3_scan(ScanInputs(dev(x), dev(b), dev(c), dev(case.dt), dev(case.a_log),
+                                 dev(case.lam)).with_theta(dev(theta)).with_skip(dev(d_skip))
+                      .with_chunk_size(4))
+    state = SsmState.zeros(case.batch, case.heads, case.head_dim, case.state, True, "cuda")
+    steps = []
+    for t in range(case.seq):
+        y, state = mamba3_step(dev(x[:, t]), dev(b[:, t]), dev(c[:, t]), dev(case.dt[:, t]),
+                               dev(case.lam[:, t]), dev(case.a_log), dev(theta[:, t]),
+                               dev(d_skip), state)
+        steps.append(host(y))
+    stepwise = np.stack(steps, axis=1)
+    assert_close(stepwise, host(par.y), 3e-4, "step vs chunked")
+    y64, h64, lu64, a64 = oracle.scan_recurrence_f64(x, b, c, case.dt, case.a_log, case.lam,
+                                                     theta, d_skip)
+    assert rel_l2(stepwise, y64) <= F32_TOL
+    assert rel_l2(host(state.h), h64) <= F32_TOL
+    assert rel_l2(host(state.last_u), lu64) <= F32_TOL
+
+
+STEP_CASES = [
+    # B, H, P, N, R, theta, skip, dtype
+    (3, 4, 64, 128, 1, True, True, "f32"),
+    (2, 3, 64, 64, 1, False, True, "f32"),
+    (2, 2, 32, 32, 2, True, False, "f32"),
+    (2, 2, 16, 128, 4, True, True, "f32"),
+    (1, 2, 8, 6, 1, True, True, "f32"),
+    (1, 2, 5, 256, 3, True, True, "f32"),
+    (2, 2, 64, 128, 1, True, True, "bf16"),
+    (1, 1, 4, 512, 1, True, False, "f32"),
+]
+
+
+@pytest.mark.parametrize("B,H,P,N,R,theta,skip,dtype", STEP_CASES)
+def test_step_in_place_against_oracle(B, H, P, N, R, theta, skip, dtype):
+    from cases import bf16_round
+    from mamba3.ssm import SsmState, mamba3_step_
+    rng = np.random.default_rng(zlib.crc32(repr((B, H, P, N, R, theta, skip, dtype)).encode()))
+    f = np.float32
+    x = rng.standard_normal((B, H, P, R), dtype=f)
+    b = (rng.standard_normal((B, H, N, R), dtype=f) / f(math.sqrt(N))).astype(f)
+    c = (rng.standard_normal((B, H, N, R), dtype=f) / f(math.sqrt(N))).astype(f)
+    th = rng.uniform(0, math.pi, (B, H, N // 2)).astype(f) if theta else None
+    if dtype == "bf16":
+        x, b, c = bf16_round(x), bf16_round(b), bf16_round(c)
+        th = bf16_round(th) if theta else None
+    dt = np.clip(np.log1p(np.exp(rng.standard_normal((B, H)) - 3)), 1e-3, 0.1).astype(f)
+    lam = (1 / (1 + np.exp(-rng.standard_normal((B, H))))).astype(f)
+    a_log = rng.uniform(0, math.log(16), H).astype(f)
+    d_skip = rng.uniform(-1, 1, H).astype(f) if skip else None
+    h = (rng.standard_normal((B, H, P, N), dtype=f) * f(0.1)).astype(f)
+    lu = (rng.standard_normal((B, H, P, N), dtype=f) * f(0.1)).astype(f)
+    ang = rng.uniform(-math.pi, math.pi, (B, H, N // 2)).astype(f) if theta else None
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    state = SsmState(dev(h), dev(lu), dev(ang) if theta else None)
+    y = mamba3_step_(dev(x, tdt), dev(b, tdt), dev(c, tdt), dev(dt), dev(lam), dev(a_log),
+                     dev(th, tdt) if theta else None, dev(d_skip), state)
+    torch.cuda.synchronize()
+    # the f32 restatement of mamba3_step and the f64 recurrence (one token, carried state)
+    yo, ho, luo, ango = oracle.step_f32(x, b, c, dt, lam, a_log, th, d_skip, h, lu, ang)
+    y64, h64, lu64, a64 = oracle.scan_recurrence_f64(
+        x[:, None], b[:, None], c[:, None], dt[:, None], a_log, lam[:, None],
+        th[:, None] if theta else None, d_skip, h, lu, ang)
+    tol = 1e-2 if dtype == "bf16" else F32_TOL
+    assert rel_l2(host(y), y64[:, 0]) <= tol
+    assert rel_l2(host(state.h), h64) <= tol
+    assert rel_l2(host(state.last_u), lu64) <= tol
+    assert rel_l2(host(y), yo) <= tol
+    if theta:
+        d = host(state.angle) - a64
+        d = (d + math.pi) % (2 * math.pi) - math.pi
+        assert np.abs(d).max() <= 1e-5
+
+
+def test_config3_shape_one_layer_many_steps():
+    """BASELINE config 3 per-layer shape (batch 256, 24 heads, P64, N128, f32 cache):
+    8 consecutive in-place steps on the GPU against 8 oracle steps."""
+    from mamba3.ssm import SsmState, mamba3_step_
+    B, H, P, N = 256, 24, 64, 128
+    rng = np.random.default_rng(3)
+    f = np.float32
+    h = (rng.standard_normal((B, H, P, N), dtype=f) * f(0.1)).astype(f)
+    lu = (rng.standard_normal((B, H, P, N), dtype=f) * f(0.1)).astype(f)
+    ang = rng.uniform(-math.pi, math.pi, (B, H, N // 2)).astype(f)
+    a_log = rng.uniform(0, math.log(16), H).astype(f)
+    d_skip = np.ones(H, f)
+    state = SsmState(dev(h), dev(lu), dev(ang))
+    ho, luo, ango = h.copy(), lu.copy(), ang.copy()
+    for step in range(8):
+        x = rng.standard_normal((B, H, P, 1), dtype=f)
+        b = (rng.standard_normal((B, H, N, 1), dtype=f) / f(math.sqrt(N))).astype(f)
+        c = (rng.standard_normal((B, H, N, 1), dtype=f) / f(math.sqrt(N))).astype(f)
+        th = rng.uniform(0, math.pi, (B, H, N // 2)).astype(f)
+        dt = np.clip(np.log1p(np.exp(rng.standard_normal((B, H)) - 3)), 1e-3, 0.1).astype(f)
+        lam = (1 / (1 + np.exp(-rng.standard_normal((B, H))))).astype(f)
+        y = mamba3_step_(dev(x), dev(b), dev(c), dev(dt), dev(lam), dev(a_log), dev(th),
+                         dev(d_skip), state)
+        yo, ho, luo, ango = oracle.step_f32(x, b, c, dt, lam, a_log, th, d_skip, ho, luo, ango)
+        assert rel_l2(host(y), yo) <= F32_TOL, step
+    assert rel_l2(host(state.h), ho) <= F32_TOL
+    assert rel_l2(host(state.last_u), luo) <= F32_TOL
+
+
+def test_state_cache_layers_are_independent():
+    """infer::StateCache: stepping one layer leaves the others untouched."""
+    from mamba3 import StateCache
+    cache = StateCache(3, 2, 2, 16, 32, True, "cuda", init_std=0.1,
+                       generator=torch.Generator(device="cuda").manual_seed(0))
+    before = cache.h.clone()
+    x = torch.randn(2, 2, 16, 1, device="cuda")
+    b = torch.randn(2, 2, 32, 1, device="cuda")
+    dt = torch.full((2, 2), 0.05, device="cuda")
+    lam = torch.full((2, 2), 0.5, device="cuda")
+    a_log = torch.zeros(2, device="cuda")
+    th = torch.rand(2, 2, 16, device="cuda")
+    cache.step_layer(1, x, b, b, dt, lam, a_log, th)
+    cache.advance(1)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.h[0], before[0]) and torch.equal(cache.h[2], before[2])
+    assert not torch.equal(cache.h[1], before[1])
+    assert cache.position() == 1
