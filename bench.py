@@ -1,0 +1,287 @@
+"""Benchmark of the MI355X Mamba-3 hot path (one JSON line on stdout).
+
+Headline (`value`): the SSD scan forward at BASELINE config 1 -- B=8, L=2048,
+H=12, P=64, N=128, chunk 64, bf16 storage with f32 accumulation, Rotational
+dynamics with a learned trapezoid -- as whole-job tokens/s on one GPU.  A step
+is one m3_scan call over the batch with every input already resident in HBM.
+
+Also reported on the same line:
+  roofline       the scan kernel's algorithmic bytes per launch over its
+                 average launch time (HIP events on the launch stream), against
+                 the 8 TB/s HBM peak, plus its MFMA fraction;
+  decode         BASELINE config 3: one token for 256 sequences through
+                 24 layers x 24 heads (P=64, N=128) of f32 state cache, in place,
+                 timed over consecutive steps: us per step, GB/s, fraction of HBM peak;
+  cpu_baseline   the CPU restatement of the reference's composed algorithm
+                 (oracle/, OpenMP) on the same config-1 workload, on the host.
+
+Inputs are synthetic (seeded torch RNG on the device, the distributions of
+BASELINE.json).  `--gpus N` with N > 1 exits: this build measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mamba-trainer_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+
+# BASELINE config 1 (the headline) and config 3 (decode)
+SCAN = dict(B=8, L=2048, H=12, P=64, N=128, R=1, Q=64)
+DECODE = dict(B=256, layers=24, H=24, P=64, N=128, R=1, sets=4)
+
+
+def scan_algorithmic(B, L, H, P, N, R, Q, s_io=2, theta_per_token=True, want_state=True):
+    """Algorithmic HBM bytes and MFMA-contractible FLOPs of one scan launch.
+
+    Per (token, head): x, b, c (and theta, materialised per token) read at s_io
+    bytes, dt and lambda read as f32, y written at s_io bytes; plus the outgoing
+    state h, last_u [B,H,P,N] f32 and angle [B,H,N/2] f32 when wanted.
+    FLOPs per (token, head): 2*Q*R^2*(N+P) (the masked C B^T and its product
+    with X) + 4*R*P*N (chunk state and carry-in output).
+    """
+    per_tok = (P * R + 2 * N * R + (N // 2 if theta_per_token else 0)) * s_io + 8 + P * R * s_io
+    nbytes = B * L * H * per_tok
+    if want_state:
+        nbytes += B * H * (2 * P * N + N // 2) * 4
+    flops = B * L * H * (2 * Q * R * R * (N + P) + 4 * R * P * N)
+    return nbytes, flops
+
+
+def decode_algorithmic(B, H, P, N, R):
+    """Bytes per layer step: h and last_u read + written (16 B per state element)
+    plus x, b, c, theta, dt, lambda read, angle read + written, y written (f32)."""
+    state = 16 * B * H * P * N
+    io = B * H * (P * R + 2 * N * R + N // 2 + 2 + 2 * (N // 2) + P * R) * 4
+    return state + io
+
+
+def make_scan_inputs(torch, dev, B, L, H, P, N, R, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    bf = torch.bfloat16
+    x = torch.randn(B, L, H, P, R, device=dev, generator=g).to(bf)
+    b = (torch.randn(B, L, H, N, R, device=dev, generator=g) / math.sqrt(N)).to(bf)
+    c = (torch.randn(B, L, H, N, R, device=dev, generator=g) / math.sqrt(N)).to(bf)
+    dt = torch.nn.functional.softplus(torch.randn(B, L, H, device=dev, generator=g) - 3.0
+                                      ).clamp(1e-3, 0.1)
+    lam = torch.sigmoid(torch.randn(B, L, H, device=dev, generator=g))
+    a_log = torch.rand(H, device=dev, generator=g) * math.log(16.0)
+    # theta ~ U(0, pi) per head per state pair, materialised per token
+    theta = (torch.rand(1, 1, H, N // 2, device=dev, generator=g) * math.pi).expand(
+        B, L, H, N // 2).contiguous().to(bf)
+    return dict(x=x, b=b, c=c, dt=dt, lam=lam, a_log=a_log, theta=theta)
+
+
+def bench_scan(torch, lib, L_, args):
+    dev = "cuda:0"
+    s = SCAN
+    B, L, H, P, N, R, Q = s["B"], s["L"], s["H"], s["P"], s["N"], s["R"], s["Q"]
+    inp = make_scan_inputs(torch, dev, B, L, H, P, N, R, 0x4D414D43)
+    y = torch.empty_like(inp["x"])
+    h = torch.empty(B, H, P, N, device=dev)
+    lu = torch.empty(B, H, P, N, device=dev)
+    ang = torch.empty(B, H, N // 2, device=dev)
+    cin = L_.ScanInputsC(B, L, H, P, N, R, L_.M3_BF16, inp["x"].data_ptr(), inp["b"].data_ptr(),
+                         inp["c"].data_ptr(), inp["dt"].data_ptr(), inp["a_log"].data_ptr(),
+                         inp["lam"].data_ptr(), inp["theta"].data_ptr(), None, None, Q, 1)
+    cout = L_.ScanOutputC(y.data_ptr(), L_.SsmStateC(h.data_ptr(), lu.data_ptr(), ang.data_ptr()))
+    stream = torch.cuda.current_stream()
+    sp = C.c_void_p(stream.cuda_stream)
+    fn = lib.m3_scan
+    pin, pout = C.byref(cin), C.byref(cout)
+
+    def step():
+        st = fn(pin, pout, sp)
+        if st != 0:
+            L_.check(st)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = e0.elapsed_time(e1) / args.steps
+    assert torch.isfinite(y.float()).all(), "non-finite scan output"
+    return dict(wall_ms=wall * 1e3 / args.steps, kernel_ms=ev_ms, tokens=B * L)
+
+
+def bench_decode(torch, lib, L_, args):
+    dev = "cuda:0"
+    d = DECODE
+    B, NL, H, P, N, R, K = d["B"], d["layers"], d["H"], d["P"], d["N"], d["R"], d["sets"]
+    g = torch.Generator(device=dev).manual_seed(0x4D414D45)
+    h = torch.randn(NL, B, H, P, N, device=dev, generator=g) * 0.1
+    lu = torch.randn(NL, B, H, P, N, device=dev, generator=g) * 0.1
+    ang = (torch.rand(NL, B, H, N // 2, device=dev, generator=g) * 2 - 1) * math.pi
+    a_log = torch.rand(NL, H, device=dev, generator=g) * math.log(16.0)
+    d_skip = torch.ones(H, device=dev)
+    sets = []
+    for _ in range(K):
+        x = torch.randn(B, H, P, R, device=dev, generator=g)
+        b = torch.randn(B, H, N, R, device=dev, generator=g) / math.sqrt(N)
+        c = torch.randn(B, H, N, R, device=dev, generator=g) / math.sqrt(N)
+        th = torch.rand(B, H, N // 2, device=dev, generator=g) * math.pi
+        dt = torch.nn.functional.softplus(torch.randn(B, H, device=dev, generator=g) - 3.0
+                                          ).clamp(1e-3, 0.1)
+        lam = torch.sigmoid(torch.randn(B, H, device=dev, generator=g))
+        sets.append((x, b, c, th, dt, lam))
+    y = torch.empty(B, H, P, R, device=dev)
+    calls = []
+    for k in range(K):
+        x, b, c, th, dt, lam = sets[k]
+        per_layer = []
+        for l in range(NL):
+            args_c = L_.StepInputsC(B, H, P, N, R, L_.M3_F32, x.data_ptr(), b.data_ptr(),
+                                    c.data_ptr(), dt.data_ptr(), lam.data_ptr(),
+                                    a_log[l].data_ptr(), th.data_ptr(), d_skip.data_ptr())
+            st = L_.SsmStateC(h[l].data_ptr(), lu[l].data_ptr(), ang[l].data_ptr())
+            per_layer.append((args_c, st))
+        calls.append(per_layer)
+    stream = torch.cuda.current_stream()
+    sp = C.c_void_p(stream.cuda_stream)
+    fn = lib.m3_step
+    yp = C.c_void_p(y.data_ptr())
+    refs = [[(C.byref(a), C.byref(s)) for a, s in per] for per in calls]
+
+    def step(i):
+        for pa, ps in refs[i % K]:
+            st = fn(pa, ps, yp, sp)
+            if st != 0:
+                L_.check(st)
+
+    for i in range(args.decode_warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.decode_steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.decode_steps
+    assert torch.isfinite(h).all(), "non-finite decode state"
+    nbytes = NL * decode_algorithmic(B, H, P, N, R)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(us_per_step=round(ms * 1e3, 2), steps=args.decode_steps, layers=NL,
+                bytes_per_step=nbytes, achieved_GBps=round(gbs, 1),
+                frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4),
+                us_per_layer=round(ms * 1e3 / NL, 2))
+
+
+def cpu_baseline(args):
+    """The oracle's f32 restatement of the reference's composed scan on the host
+    (OpenMP over batch x head), on config 1's full workload, bf16-rounded inputs."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle
+    from cases import baseline_inputs
+    s = SCAN
+    B = args.cpu_batch
+    rng = np.random.default_rng(0x4D414D43)
+    inp = baseline_inputs(rng, B, s["L"], s["H"], s["P"], s["N"], 1, theta=True, dtype="bf16")
+    run = lambda: oracle.scan_composed_f32(inp["x"], inp["b"], inp["c"], inp["dt"],
+                                           inp["a_log"], inp["lam"], inp["theta"],
+                                           chunk=s["Q"], want_state=True)
+    run()   # warmup
+    times = []
+    for _ in range(args.cpu_reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    tokens = B * s["L"]
+    return {"value": round(tokens / med, 1), "unit": "tokens/s",
+            "cores": oracle.num_threads(), "kind": "port",
+            "sample": (f"config 1 at batch {B} (L=2048, H=12, P=64, N=128, Q=64, Rotational, "
+                       f"bf16-rounded inputs, f32 math), composed reference algorithm "
+                       f"(oracle/mamba3_oracle.c m3o_scan_composed_f32), 1 warmup + median "
+                       f"of {args.cpu_reps}: {med:.3f} s per pass")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--decode-warmup", type=int, default=8)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-batch", type=int, default=8)
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: every GPU box in this build has one, and the path "
+              "has no multi-GPU leg (sharding is designed, not built). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs the MI355X (no ROCm device visible)", file=sys.stderr)
+        sys.exit(1)
+    from mamba3 import _lib as L_
+    lib = L_.lib()
+
+    torch.cuda.synchronize()
+    sc = bench_scan(torch, lib, L_, args)
+    s = SCAN
+    nbytes, flops = scan_algorithmic(s["B"], s["L"], s["H"], s["P"], s["N"], s["R"], s["Q"])
+    k_s = sc["kernel_ms"] * 1e-3
+    achieved = nbytes / k_s / 1e9
+    tflops = flops / k_s / 1e12
+    ms_step = sc["wall_ms"]
+    value = sc["tokens"] / (ms_step * 1e-3)
+
+    dec = None if args.no_decode else bench_decode(torch, lib, L_, args)
+    cpu = None if args.no_cpu else cpu_baseline(args)
+
+    line = {
+        "metric": "SSD scan fwd tokens/s (config 1) + % roofline; decode-step us & HBM GB/s "
+                  "at batch 256",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded device RNG, BASELINE.json distributions)",
+        "config": {"workload": "mamba3_scan config 1: B=8 L=2048 H=12 P=64 N=128 chunk=64, "
+                               "bf16 storage f32 accumulate, Rotational, LearnedTrapezoid, "
+                               "SISO, want_state",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "ssd_scan_kernel", "kernel_us": round(sc["kernel_ms"] * 1e3, 2),
+                     "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
+                     "mfma_tflops": round(tflops, 2),
+                     "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)},
+        "decode": dec,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -176,7 +176,9 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
                 e = hipMemsetAsync(out->state.h, 0, sbytes, s);
                 if (e == hipSuccess) e = hipMemsetAsync(out->state.last_u, 0, sbytes, s);
             }
-            if (e == hipSuccess && in->theta != nullptr) {
+            // An empty theta tensor may arrive as a NULL pointer, so the angle
+            // passes through whenever the caller gave an output angle buffer.
+            if (e == hipSuccess && out->state.angle != nullptr) {
                 const size_t abytes = B * H * (N / 2) * sizeof(float);
                 if (st != nullptr && st->angle != nullptr)
                     e = hipMemcpyAsync(out->state.angle, st->angle, abytes,

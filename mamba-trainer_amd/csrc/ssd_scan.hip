@@ -316,13 +316,18 @@ ssd_scan_kernel(ScanLaunch a, int qtok, int nchunks) {
         // ================= S3: band -> Ms, carry-in output, state advance
         f32x4 yacc[NT];
         {
-            // (a) G^T tiles (s-tile si <= t-tile tj), masked, into Ms[t][s]
+            // (a) G^T tiles, masked, into Ms[t][s].  An s-tile is needed when its
+            // first row's token is not after the last token of the t-tile; for a
+            // rank that does not divide 16 a token's rows straddle two tiles, so
+            // that includes the tile just above the diagonal.
             int idx = 0;
 #pragma unroll
             for (int tj = 0; tj < NT; ++tj) {
+                const int tlast = (16 * tj + 15) / static_cast<int>(R);
 #pragma unroll
-                for (int si = 0; si <= tj; ++si, ++idx) {
-                    if (idx % PT != wave) continue;
+                for (int si = 0; si < NT; ++si) {
+                    if ((16 * si) / static_cast<int>(R) > tlast) continue;
+                    if ((idx++) % PT != wave) continue;
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
                     const op_t *ar = &sm.Bs[(16 * si + c) * LDN];
                     const op_t *br = &sm.Cs[(16 * tj + c) * LDN];
@@ -427,7 +432,10 @@ ssd_scan_kernel(ScanLaunch a, int qtok, int nchunks) {
 #pragma unroll
             for (int tj = 0; tj < NT; ++tj) {
                 const op_t *mr = &sm.Ms[(16 * tj + c) * LDR];
-                const int nkb = (16 * (tj + 1) + KB - 1) / KB;
+                // s-rows past the last token of this t-tile are masked to zero
+                const int tlast = (16 * tj + 15) / static_cast<int>(R);
+                const int send = min(ROWS, (tlast + 1) * static_cast<int>(R));
+                const int nkb = (send + KB - 1) / KB;
 #pragma unroll
                 for (int kb = 0; kb < (ROWS / KB); ++kb)
                     if (kb < nkb) yacc[tj] = mma_kblock(xr + kb * KB, mr + kb * KB, yacc[tj], g);
