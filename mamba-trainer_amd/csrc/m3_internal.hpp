@@ -39,6 +39,10 @@ struct ScanLaunch {
     float *h_out, *last_u_out, *angle_out;  // null when not wanted
 };
 hipError_t launch_scan(const ScanLaunch &a, hipStream_t stream);
+// The specialised kernel (head_dim 64, d_state 64/128, rank 1/2/4, 16-byte
+// aligned x/b/c/theta/y); hipErrorNotSupported for anything else.
+bool scan_fast_supported(const ScanLaunch &a);
+hipError_t launch_scan_fast(const ScanLaunch &a, hipStream_t stream);
 
 // Largest head_dim / d_state the scan kernels are instantiated for.
 constexpr size_t kScanMaxHeadDim = 128;
