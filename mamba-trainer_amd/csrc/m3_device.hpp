@@ -67,6 +67,26 @@ __device__ __forceinline__ float wave_inclusive_scan(float v, int lane) {
     return v;
 }
 
+// Inclusive scan over each aligned segment of SW lanes (SW = 16, 32 or 64):
+// DPP row_shr steps within 16-lane rows, then row_bcast:15 / row_bcast:31
+// carries across rows.  Lanes whose shifted source falls outside the row
+// read zero (bound_ctrl), rows masked out of a broadcast add zero.
+template <int CTRL, int ROWM, bool BC>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWM, 0xf, BC));
+}
+template <int SW>
+__device__ __forceinline__ float seg_scan(float v) {
+    static_assert(SW == 16 || SW == 32 || SW == 64, "segments of 16, 32 or 64 lanes");
+    v += dpp_f<0x111, 0xf, true>(v);   // row_shr:1
+    v += dpp_f<0x112, 0xf, true>(v);   // row_shr:2
+    v += dpp_f<0x114, 0xf, true>(v);   // row_shr:4
+    v += dpp_f<0x118, 0xf, true>(v);   // row_shr:8
+    if constexpr (SW >= 32) v += dpp_f<0x142, 0xa, false>(v);   // row_bcast:15 -> rows 1, 3
+    if constexpr (SW >= 64) v += dpp_f<0x143, 0xc, false>(v);   // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
 __device__ __forceinline__ float group_sum(float v, int width) {
     for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -1,5 +1,6 @@
-// On-device check of the MFMA lane layouts the scan kernels are written
-// against (see m3_device.hpp): integer-valued operands, exact in bf16 and f32.
+// On-device check of the MFMA lane layouts and the DPP segmented scans the
+// scan kernels are written against (see m3_device.hpp): integer-valued
+// operands, exact in bf16 and f32.
 #include "m3_device.hpp"
 #include "m3_internal.hpp"
 
@@ -34,6 +35,18 @@ __global__ void mfma_layout_kernel(int *fail) {
         for (int k = 0; k < 4; ++k) want += a_val(m, k) * b_val(k, n);
         if (e[r] != want) atomicOr(fail, 2);
     }
+    // segmented inclusive scans (lane + 1 summed within 16/32/64-lane segments)
+    const float v = static_cast<float>(lane + 1);
+    const float s16 = seg_scan<16>(v), s32 = seg_scan<32>(v), s64 = seg_scan<64>(v);
+    auto tri = [&](int seg) {
+        const int first = lane - lane % seg;
+        float want = 0.f;
+        for (int j = first; j <= lane; ++j) want += static_cast<float>(j + 1);
+        return want;
+    };
+    if (s16 != tri(16)) atomicOr(fail, 4);
+    if (s32 != tri(32)) atomicOr(fail, 8);
+    if (s64 != tri(64)) atomicOr(fail, 16);
 }
 
 }  // namespace
