@@ -220,10 +220,34 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
         a.last_u_out = out->state.last_u;
         a.angle_out = in->theta ? out->state.angle : nullptr;
     }
-    hipError_t e = m3::launch_scan(a, s);
+    hipError_t e;
+    const size_t need = m3::scan_split_workspace(a);
+    if (need > 0 && in->workspace != nullptr && in->workspace_bytes >= need) {
+        e = m3::launch_scan_split(a, in->workspace, s);
+        if (e == hipSuccess) g_launches.fetch_add(2, std::memory_order_relaxed);
+    } else {
+        e = m3::launch_scan(a, s);
+        if (e == hipSuccess) g_launches.fetch_add(1, std::memory_order_relaxed);
+    }
     if (e != hipSuccess) return hip_fail(e, "scan launch");
-    g_launches.fetch_add(1, std::memory_order_relaxed);
     return ok();
+}
+
+size_t m3_scan_workspace_bytes(const m3_scan_inputs *in) {
+    if (in == nullptr || !dtype_ok(in->dtype) || in->seq == 0) return 0;
+    m3::ScanLaunch a{};
+    a.batch = in->batch;
+    a.seq = in->seq;
+    a.heads = in->heads;
+    a.head_dim = in->head_dim;
+    a.d_state = in->d_state;
+    a.rank = in->rank;
+    a.bf16 = in->dtype == M3_BF16;
+    // alignment is checked at launch; size the shape as if aligned
+    alignas(16) static float dummy[4] = {0, 0, 0, 0};
+    a.x = a.b = a.c = dummy;
+    a.y = dummy;
+    return m3::scan_split_workspace(a);
 }
 
 m3_status m3_ssd_chunked(const m3_ssd_args *in, void *y, float *final_state, void *stream) {

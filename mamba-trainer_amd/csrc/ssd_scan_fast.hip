@@ -30,57 +30,13 @@
 //
 // The LDS operand set is double-buffered, so the stage of chunk k+1 runs in
 // the same phase as P5 of chunk k: two workgroup barriers per chunk.
-#include "m3_device.hpp"
-#include "m3_internal.hpp"
+#include "scan_common.hpp"
 
 namespace m3 {
 
 namespace {
 
-constexpr int kThreads = 256;
-
-__device__ __forceinline__ void lds_barrier() {
-    // waits for LDS traffic only: prefetched buffer loads stay in flight
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt untouched
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-template <typename T> struct Op;
-template <> struct Op<bf16_t> {
-    using t = __bf16;
-    static constexpr int KB = 32;
-};
-template <> struct Op<float> {
-    using t = float;
-    static constexpr int KB = 16;
-};
-
-// Geometry of one instantiation.  A chunk holds ROWS rows; a row is a
-// (token, rank) pair rho = t*R + r (the MIMO fold of scan.rs:537-589).
-template <typename T, int N, int P, int R, int ROWS>
-struct Geo {
-    static constexpr int SZ = static_cast<int>(sizeof(T));
-    static constexpr int E = 16 / SZ;              // elements per 16 bytes
-    static constexpr int QT = ROWS / R;            // tokens per chunk
-    static constexpr int NH = N / 2;               // rotation pairs
-    static constexpr int SW = QT > 16 ? QT : 16;   // lanes of one token segment
-    static constexpr int SUBS = 64 / SW;           // segments per wave
-    static constexpr int PW = NH / 4;              // pairs per wave
-    static constexpr int PPL = PW / SUBS;          // pairs per lane
-    static constexpr int HE = PPL * R;             // elements of a lane's half-row slice
-    static constexpr int HV = HE / E;              // ... in 16-byte vectors
-    static constexpr int THB = PPL * SZ;           // theta bytes per lane
-    static constexpr int TW = THB / 4;
-    static constexpr int XE = 16 * R / SUBS;       // x elements per lane
-    static constexpr int XV = XE * SZ / 16;
-    static_assert(SUBS * SW == 64 && PPL * SUBS == PW && PPL >= 1, "pair slices");
-    static_assert(HV * E == HE && HV >= 1, "half-row slices are whole vectors");
-    static_assert(TW * 4 == THB && TW >= 1, "theta slices are whole words");
-    static_assert(XV * 16 == XE * SZ && XV >= 1, "x slices are whole vectors");
-    static_assert(P == 64, "four waves own sixteen head_dim columns each");
-};
+using namespace scan;
 
 template <typename T, int N, int P, int R, int ROWS>
 struct Smem {
@@ -109,86 +65,6 @@ struct Raw {
     unsigned int th[G::TW];
     u32x4 x[G::XV];
     float s0, s1, s2, s3;   // dt, lambda, dt_next, lambda_next (or a, g, w)
-};
-
-template <typename T> __device__ __forceinline__ float elem(const u32x4 *v, int i);
-template <> __device__ __forceinline__ float elem<bf16_t>(const u32x4 *v, int i) {
-    const unsigned int w = v[i >> 3][(i >> 1) & 3];
-    return __uint_as_float((i & 1) ? (w & 0xFFFF0000u) : (w << 16));
-}
-template <> __device__ __forceinline__ float elem<float>(const u32x4 *v, int i) {
-    return __uint_as_float(v[i >> 2][i & 3]);
-}
-template <typename T> __device__ __forceinline__ float welem(const unsigned int *w, int i);
-template <> __device__ __forceinline__ float welem<bf16_t>(const unsigned int *w, int i) {
-    const unsigned int u = w[i >> 1];
-    return __uint_as_float((i & 1) ? (u & 0xFFFF0000u) : (u << 16));
-}
-template <> __device__ __forceinline__ float welem<float>(const unsigned int *w, int i) {
-    return __uint_as_float(w[i]);
-}
-
-template <typename O> __device__ __forceinline__ O to_op(float v);
-template <> __device__ __forceinline__ float to_op<float>(float v) { return v; }
-template <> __device__ __forceinline__ __bf16 to_op<__bf16>(float v) {
-    return static_cast<__bf16>(v);
-}
-__device__ __forceinline__ float op_f32(float v) { return v; }
-__device__ __forceinline__ float op_f32(__bf16 v) { return static_cast<float>(v); }
-
-// Column order of a B~ / C~ row.  For bf16 the columns of each 32-block are
-// stored as [g][h][r] instead of [h][g][r] (n = 32kb + 16h + 4g + r): one
-// 16-byte read then yields the k-slots an MFMA lane needs both for the band
-// (any k order works when both operands share it) and for the carry-in
-// product, whose A operand comes straight from the state accumulators.
-template <bool BF>
-__device__ __forceinline__ int npos(int n) {
-    if constexpr (!BF) return n;
-    return (n & ~31) | ((n & 12) << 1) | ((n & 16) >> 2) | (n & 3);
-}
-
-// exp(clamp(d, -60, 0)), the scan's decay with its log floor (scan.rs:57,
-// fused.rs:2064).  bf16 storage takes the hardware exp2; f32 keeps expf.
-template <bool FAST>
-__device__ __forceinline__ float dexp(float d) {
-    d = fminf(fmaxf(d, -60.0f), 0.0f);
-    if constexpr (FAST) return __builtin_amdgcn_exp2f(d * 1.44269504088896341f);
-    return expf(d);
-}
-
-// Store four consecutive operand values.
-__device__ __forceinline__ void st4(__bf16 *dst, const float *v) {
-    typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
-    bf16x4v p;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = static_cast<__bf16>(v[i]);
-    *reinterpret_cast<bf16x4v *>(dst) = p;
-}
-__device__ __forceinline__ void st4(float *dst, const float *v) {
-    *reinterpret_cast<f32x4 *>(dst) = f32x4{v[0], v[1], v[2], v[3]};
-}
-
-__device__ __forceinline__ f32x4 mma_kb(const __bf16 *ar, const __bf16 *br, f32x4 acc, int g) {
-    const bf16x8 av = *reinterpret_cast<const bf16x8 *>(ar + 8 * g);
-    const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(br + 8 * g);
-    return mfma_bf16(av, bv, acc);
-}
-__device__ __forceinline__ f32x4 mma_kb(const float *ar, const float *br, f32x4 acc, int g) {
-    const f32x4 av = *reinterpret_cast<const f32x4 *>(ar + 4 * g);
-    const f32x4 bv = *reinterpret_cast<const f32x4 *>(br + 4 * g);
-    acc = mfma_f32(av[0], bv[0], acc);
-    acc = mfma_f32(av[1], bv[1], acc);
-    acc = mfma_f32(av[2], bv[2], acc);
-    acc = mfma_f32(av[3], bv[3], acc);
-    return acc;
-}
-
-// Buffer resources of one (batch, head) sequence; offsets are bytes from that
-// sequence's token 0, so a token at or past the sequence end reads as zero.
-struct SeqBufs {
-    rsrc_t b, c, x, th, y, s0, s1, s2, s3;
-    uint32_t tok_bc, tok_x, tok_th, tok_s;   // bytes between consecutive tokens
-    uint32_t nxt_s;                          // token offset of s2/s3 (1 raw, 0 ssd)
 };
 
 template <typename T, int N, int P, int R, int ROWS>

@@ -46,6 +46,7 @@ class ScanInputsC(C.Structure):
         ("x", _P), ("b", _P), ("c", _P), ("dt", _P), ("a_log", _P), ("lambda_", _P),
         ("theta", _P), ("d_skip", _P), ("state", C.POINTER(SsmStateC)),
         ("chunk_size", _Z), ("want_state", C.c_int32),
+        ("workspace", _P), ("workspace_bytes", _Z),
     ]
 
 
@@ -82,6 +83,7 @@ SIGNATURES = {
     "m3_config_in_proj_width": (_Z, [C.POINTER(SsmConfigC)]),
     "m3_discretization_fixed_lambda": (C.c_float, [C.c_int32]),
     "m3_scan": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanOutputC), _P]),
+    "m3_scan_workspace_bytes": (_Z, [C.POINTER(ScanInputsC)]),
     "m3_ssd_chunked": (C.c_int, [C.POINTER(SsdArgsC), _P, _P, _P]),
     "m3_step": (C.c_int, [C.POINTER(StepInputsC), C.POINTER(SsmStateC), _P, _P]),
     "m3_status_string": (C.c_char_p, [C.c_int]),

@@ -144,3 +144,25 @@ def test_python_api_rejects_host_tensors():
         mamba3_scan(ScanInputs(x, b, b, dt, a_log, dt))
     with pytest.raises(RankError):
         mamba3_scan(ScanInputs(x[..., 0], b, b, dt, a_log, dt))
+
+
+def test_scan_workspace_query():
+    """m3_scan_workspace_bytes: the two-pass kernels cover head_dim 64, d_state
+    64/128, rank 1/2/4; other shapes run single-pass and need none."""
+    import ctypes as C
+    from mamba3 import _lib
+    L = _lib.lib()
+
+    def need(B, T, H, P, N, R, dtype):
+        cin = _lib.ScanInputsC(B, T, H, P, N, R, dtype, None, None, None, None, None, None,
+                               None, None, None, 64, 1, None, 0)
+        return int(L.m3_scan_workspace_bytes(C.byref(cin)))
+
+    w1 = need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16)
+    # per chunk: band 64x64, C~ 64x128 and (B~w)^T 128x64 in bf16, plus scalars
+    assert 96 * 32 * (64 * 64 + 2 * 64 * 128) * 2 <= w1 <= 96 * 32 * 44 * 1024
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) > w1
+    assert need(1, 100, 2, 48, 128, 1, _lib.M3_BF16) == 0      # head_dim 48
+    assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) == 0       # d_state 96
+    assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) == 0      # rank 3
+    assert need(1, 0, 2, 64, 128, 1, _lib.M3_BF16) == 0        # empty window

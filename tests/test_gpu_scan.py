@@ -116,11 +116,18 @@ FEATURE_CASES = [
     (1, 33, 1, 48, 256, 2, True, True, True, "f32"),
     (1, 9, 2, 3, 6, 1, True, True, True, "f32"),
     (1, 1, 2, 5, 4, 2, True, True, True, "f32"),
+    (2, 150, 3, 64, 64, 1, True, True, True, "f32"),
+    (1, 77, 2, 64, 128, 2, True, True, True, "f32"),
+    (1, 70, 2, 64, 64, 4, True, True, True, "f32"),
+    (1, 90, 2, 64, 64, 2, True, True, True, "bf16"),
+    (2, 129, 2, 64, 64, 4, False, True, False, "bf16"),
+    (1, 64, 3, 64, 128, 1, True, False, True, "bf16"),
 ]
 
 
+@pytest.mark.parametrize("two_pass", [True, False], ids=["two_pass", "single_pass"])
 @pytest.mark.parametrize("B,T,H,P,N,R,theta,skip,state,dtype", FEATURE_CASES)
-def test_scan_features_against_f64(B, T, H, P, N, R, theta, skip, state, dtype):
+def test_scan_features_against_f64(B, T, H, P, N, R, theta, skip, state, dtype, two_pass):
     rng = np.random.default_rng(zlib.crc32(repr((B, T, H, P, N, R, theta, skip, state,
                                                   dtype)).encode()))
     inp = baseline_inputs(rng, B, T, H, P, N, R, theta=theta, dtype=dtype,
@@ -128,7 +135,8 @@ def test_scan_features_against_f64(B, T, H, P, N, R, theta, skip, state, dtype):
     d_skip = rng.uniform(-1, 1, H).astype(np.float32) if skip else None
     st = (inp["h0"], inp["last_u0"], inp.get("angle0")) if state else None
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
-    y, h, lu, ang = run_scan(inp, dtype=tdt, theta=theta, skip=d_skip, state=st)
+    y, h, lu, ang = run_scan(inp, dtype=tdt, theta=theta, skip=d_skip, state=st,
+                             two_pass=two_pass)
     y64, h64, lu64, ang64 = oracle_scan(inp, theta=theta, skip=d_skip, state=st)
     tol = BF16_TOL if dtype == "bf16" else F32_TOL
     assert rel_l2(y, y64) <= tol, ("y", rel_l2(y, y64))
@@ -208,6 +216,37 @@ def test_config2_mimo_bf16_one_head():
     y64, h64, lu64, ang64 = oracle_scan(inp)
     assert rel_l2(y, y64) <= BF16_TOL
     assert rel_l2(h, h64) <= BF16_TOL
+
+
+@pytest.mark.parametrize("R", [1, 4])
+def test_two_pass_matches_single_pass_at_benchmark_shapes(R):
+    """Configs 1 and 2 at full batch and head count (shorter sequence): the
+    two-pass kernels and the single-pass kernel agree, and both match the
+    f64 recurrence on two of the sequences."""
+    from mamba3.ssm import ScanInputs, mamba3_scan
+    g = torch.Generator(device="cuda").manual_seed(7 + R)
+    B, T, H, P, N = (8, 512, 12, 64, 128) if R == 1 else (4, 256, 24, 64, 128)
+    x = torch.randn(B, T, H, P, R, device="cuda", generator=g).to(torch.bfloat16)
+    b = (torch.randn(B, T, H, N, R, device="cuda", generator=g) / math.sqrt(N)).to(torch.bfloat16)
+    c = (torch.randn(B, T, H, N, R, device="cuda", generator=g) / math.sqrt(N)).to(torch.bfloat16)
+    dt = torch.nn.functional.softplus(torch.randn(B, T, H, device="cuda", generator=g) - 3
+                                      ).clamp(1e-3, 0.1)
+    lam = torch.sigmoid(torch.randn(B, T, H, device="cuda", generator=g))
+    a_log = torch.rand(H, device="cuda", generator=g) * math.log(16)
+    th = (torch.rand(B, T, H, N // 2, device="cuda", generator=g) * math.pi).to(torch.bfloat16)
+    mk = lambda two: mamba3_scan(ScanInputs(x, b, c, dt, a_log, lam).with_theta(th)
+                                 .with_two_pass(two))
+    two, one = mk(True), mk(False)
+    assert rel_l2(host(two.y), host(one.y)) <= BF16_TOL
+    assert rel_l2(host(two.state.h), host(one.state.h)) <= BF16_TOL
+    assert rel_l2(host(two.state.last_u), host(one.state.last_u)) <= BF16_TOL
+    assert angle_err(host(two.state.angle), host(one.state.angle)) <= 1e-3
+    for bb, hh in ((0, 0), (B - 1, H - 1)):
+        sl = lambda t: host(t[bb:bb + 1, :, hh:hh + 1])
+        y64, h64, _, _ = oracle.scan_recurrence_f64(
+            sl(x), sl(b), sl(c), sl(dt), host(a_log[hh:hh + 1]), sl(lam), sl(th))
+        assert rel_l2(host(two.y[bb:bb + 1, :, hh:hh + 1]), y64) <= BF16_TOL
+        assert rel_l2(host(two.state.h[bb:bb + 1, hh:hh + 1]), h64) <= BF16_TOL
 
 
 def test_config1_full_size_split_window_property():
