@@ -30,9 +30,11 @@ template <> struct Op<float> {
     static constexpr int KB = 16;
 };
 
-// Geometry of one instantiation.  A chunk holds ROWS rows; a row is a
-// (token, rank) pair rho = t*R + r (the MIMO fold of scan.rs:537-589).
-template <typename T, int N, int P, int R, int ROWS>
+// Geometry of one instantiation with NW waves.  A chunk holds ROWS rows; a
+// row is a (token, rank) pair rho = t*R + r (the MIMO fold of
+// scan.rs:537-589).  In the staging mapping lane = token: wave w owns the
+// rotation pairs [w*PW, (w+1)*PW) and head_dim columns [w*P/NW, (w+1)*P/NW).
+template <typename T, int N, int P, int R, int ROWS, int NW = 4>
 struct Geo {
     static constexpr int SZ = static_cast<int>(sizeof(T));
     static constexpr int E = 16 / SZ;              // elements per 16 bytes
@@ -40,19 +42,19 @@ struct Geo {
     static constexpr int NH = N / 2;               // rotation pairs
     static constexpr int SW = QT > 16 ? QT : 16;   // lanes of one token segment
     static constexpr int SUBS = 64 / SW;           // segments per wave
-    static constexpr int PW = NH / 4;              // pairs per wave
+    static constexpr int PW = NH / NW;             // pairs per wave
     static constexpr int PPL = PW / SUBS;          // pairs per lane
     static constexpr int HE = PPL * R;             // elements of a lane's half-row slice
     static constexpr int HV = HE / E;              // ... in 16-byte vectors
     static constexpr int THB = PPL * SZ;           // theta bytes per lane
     static constexpr int TW = THB / 4;
-    static constexpr int XE = 16 * R / SUBS;       // x elements per lane
+    static constexpr int XE = (P / NW) * R / SUBS; // x elements per lane
     static constexpr int XV = XE * SZ / 16;
     static_assert(SUBS * SW == 64 && PPL * SUBS == PW && PPL >= 1, "pair slices");
     static_assert(HV * E == HE && HV >= 1, "half-row slices are whole vectors");
     static_assert(TW * 4 == THB && TW >= 1, "theta slices are whole words");
     static_assert(XV * 16 == XE * SZ && XV >= 1, "x slices are whole vectors");
-    static_assert(P == 64, "four waves own sixteen head_dim columns each");
+    static_assert(P == 64, "head_dim 64: sixteen-column MFMA tiles, one or two waves each");
 };
 
 template <typename T> __device__ __forceinline__ float elem(const u32x4 *v, int i);

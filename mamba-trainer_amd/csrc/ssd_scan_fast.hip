@@ -4,29 +4,34 @@
 // ssd_scan.hip.  Both restate src/ssm/scan.rs:116-291 (ssd_chunked) and
 // 458-638 (mamba3_scan) and are checked against the same oracle.
 //
-// One workgroup of four waves per (batch, head) walks the sequence chunk by
-// chunk; the state S (f32) never leaves registers (wave w owns head_dim
-// columns [16w, 16w+16)).  Per chunk:
+// One workgroup per (batch, head) walks the sequence chunk by chunk; the f32
+// state S never leaves registers.  Per chunk:
 //
-//   stage  Lane = token.  Wave w loads, for its token, the rotation pairs
-//          [w*NH/4, (w+1)*NH/4) of B and C, the matching theta slice, its
-//          head_dim slice of x, and dt/lambda of the token and the next one
-//          (raw buffer loads: past the sequence end they read as zeros).  The
-//          in-chunk prefixes -- the log-decay cumsum (ops/scan.rs:18-51) and
-//          the frame angle cumsum of dt*theta -- are DPP scans across the
-//          wave's lanes, so each lane ends up with its own token's decay
-//          weights, trapezoid weights (fused.rs:2483-2503) and wrapped angle
-//          (elemwise.rs:349).  B and C are rotated by -phi in registers
-//          (fused.rs:588-619) and written to LDS as MFMA operands; so are
-//          (B~ * w * decay-to-end)^T and X^T.  The inputs of the chunk after
-//          next are requested before the stage starts.
-//   P4     MFMA: the masked C B^T band (ssd_band, fused.rs:2044-2070) into LDS;
-//          the carry-in output (C~ exp(acum)) S^T (scan.rs:253-263) straight
-//          from the state registers; the state advance
-//          S = exp(dA) S + (w-decayed B~)^T X (scan.rs:207-251, an O(C) walk in
-//          place of the O(C^2) transfer matrix).
-//   P5     MFMA: y += (band o C B^T) X (with the skip D on the band's
-//          diagonal), then the store.
+//   stage  Lane = token.  Wave w loads, for its token, its rotation pairs of
+//          B and C, the matching theta slice, its head_dim slice of x, and
+//          dt/lambda of the token and the next one (raw buffer loads: past the
+//          sequence end they read as zeros).  The in-chunk prefixes -- the
+//          log-decay cumsum (ops/scan.rs:18-51) and the frame angle cumsum of
+//          dt*theta -- are DPP scans across the wave's lanes, so each lane ends
+//          up with its own token's decay weights, trapezoid weights
+//          (fused.rs:2483-2503) and wrapped angle (elemwise.rs:349).  B and C
+//          are rotated by -phi in registers (fused.rs:588-619) and written to
+//          LDS as MFMA operands; so are (B~ * w * decay-to-end)^T and X^T.  The
+//          inputs of the chunk after next are requested before the stage.
+//   P4     MFMA: the masked C B^T band (ssd_band, fused.rs:2044-2070) into LDS,
+//          and the state advance S = exp(dA) S + (w-decayed B~)^T X
+//          (scan.rs:207-251, an O(C) walk in place of the O(C^2) transfer).
+//   P5     MFMA: y = exp(acum) (C~ S) + (band o C B^T) X (scan.rs:253-263;
+//          the skip D rides on the band's diagonal), then the store.
+//
+// Two shapes of workgroup:
+//   NW = 4  wave w owns head_dim columns [16w, 16w+16) and the whole state of
+//           those columns.
+//   NW = 8  (bf16, d_state 128) wave w = (p-tile w%4, half w/4) owns n-tiles
+//           [4*half, 4*half+4) of the state of its sixteen columns, produces y
+//           for t-tiles {2*half, 2*half+1}, and gets the other half of the
+//           state it needs for the carry-in product as bf16 through LDS.  Two
+//           waves per SIMD hide each other's LDS and MFMA latency.
 //
 // The LDS operand set is double-buffered, so the stage of chunk k+1 runs in
 // the same phase as P5 of chunk k: two workgroup barriers per chunk.
@@ -38,9 +43,9 @@ namespace {
 
 using namespace scan;
 
-template <typename T, int N, int P, int R, int ROWS>
+template <typename T, int N, int P, int R, int ROWS, int NW>
 struct Smem {
-    using G = Geo<T, N, P, R, ROWS>;
+    using G = Geo<T, N, P, R, ROWS, NW>;
     using op_t = typename Op<T>::t;
     static constexpr int PAD = 16 / static_cast<int>(sizeof(op_t));
     static constexpr int LDN = N + PAD;    // pitch of [row][n] operands
@@ -54,12 +59,15 @@ struct Smem {
     };
     Set set[2];
     op_t Ms[ROWS * LDR];        // masked band (C~ B~^T o L)[rho_t][rho_s]
+    // NW = 8: each wave's half of S_k as bf16 MFMA A-operand slices,
+    // [p-tile][half][k-block within the half][lane]
+    bf16x8 xchg[NW == 8 ? 4 * 2 * (N / 64) * 64 : 1];
 };
 
 // Raw inputs of one chunk as this lane loads them.
-template <typename T, int N, int P, int R, int ROWS>
+template <typename T, int N, int P, int R, int ROWS, int NW>
 struct Raw {
-    using G = Geo<T, N, P, R, ROWS>;
+    using G = Geo<T, N, P, R, ROWS, NW>;
     u32x4 b[2][G::HV];
     u32x4 c[2][G::HV];
     unsigned int th[G::TW];
@@ -67,10 +75,10 @@ struct Raw {
     float s0, s1, s2, s3;   // dt, lambda, dt_next, lambda_next (or a, g, w)
 };
 
-template <typename T, int N, int P, int R, int ROWS>
+template <typename T, int N, int P, int R, int ROWS, int NW>
 __device__ __forceinline__ void load_chunk(const SeqBufs &rs, int ck, int wave, int lane,
-                                           Raw<T, N, P, R, ROWS> &raw) {
-    using G = Geo<T, N, P, R, ROWS>;
+                                           Raw<T, N, P, R, ROWS, NW> &raw) {
+    using G = Geo<T, N, P, R, ROWS, NW>;
     constexpr uint32_t SZ = sizeof(T);
     const uint32_t sub = lane / G::SW;
     const uint32_t tok = static_cast<uint32_t>(ck) * G::QT + lane % G::SW;
@@ -99,7 +107,7 @@ __device__ __forceinline__ void load_chunk(const SeqBufs &rs, int ck, int wave, 
     } else {
         raw.th[0] = bld4(rs.th, ot);
     }
-    const uint32_t ox = tok * rs.tok_x + (wave * 16 * R + sub * G::XE) * SZ;
+    const uint32_t ox = tok * rs.tok_x + (wave * (P / NW) * R + sub * G::XE) * SZ;
 #pragma unroll
     for (int v = 0; v < G::XV; ++v) raw.x[v] = bld16(rs.x, ox + 16 * v);
     raw.s0 = bldf(rs.s0, tok * rs.tok_s);
@@ -108,13 +116,14 @@ __device__ __forceinline__ void load_chunk(const SeqBufs &rs, int ck, int wave, 
     raw.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
 }
 
-template <typename T, int N, int P, int R, int ROWS>
-__global__ void __launch_bounds__(kThreads, 1)
+template <typename T, int N, int P, int R, int ROWS, int NW>
+__global__ void __launch_bounds__(64 * NW, 1)
 ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
-    using G = Geo<T, N, P, R, ROWS>;
-    using S = Smem<T, N, P, R, ROWS>;
-    using RawT = Raw<T, N, P, R, ROWS>;
+    using G = Geo<T, N, P, R, ROWS, NW>;
+    using S = Smem<T, N, P, R, ROWS, NW>;
+    using RawT = Raw<T, N, P, R, ROWS, NW>;
     using op_t = typename S::op_t;
+    constexpr int THREADS = 64 * NW;
     constexpr int KB = Op<T>::KB;
     constexpr int LDN = S::LDN, LDR = S::LDR;
     constexpr int QT = G::QT, NH = G::NH, PPL = G::PPL;
@@ -122,6 +131,10 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
     constexpr int NTN = N / 16;      // state-column tiles
     constexpr bool kBf16 = sizeof(op_t) == 2;
     constexpr uint32_t SZ = sizeof(T);
+    static_assert(NW == 4 || (NW == 8 && kBf16), "eight waves split the bf16 state in halves");
+    // state n-tiles held by a wave, and the t-tiles of y it produces
+    constexpr int SNT = NW == 8 ? NTN / 2 : NTN;
+    constexpr int YT = NW == 8 ? NT / 2 : NT;
 
     extern __shared__ __align__(16) unsigned char smem_raw[];
     S &sm = *reinterpret_cast<S *>(smem_raw);
@@ -131,6 +144,10 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
     const int wave = tid >> 6;
     const int g = lane >> 4;
     const int c = lane & 15;
+    const int pt = wave & 3;                       // my p-tile (columns [16pt, 16pt+16))
+    const int hf = NW == 8 ? (wave >> 2) : 0;      // my state half / y half
+    const int n0 = hf * SNT;                       // my first state n-tile
+    const int t0 = hf * YT;                        // my first y t-tile
 
     const size_t H = a.heads, L = a.seq;
     const size_t bb = blockIdx.x / H, hh = blockIdx.x % H;
@@ -174,21 +191,22 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
     }
 
     RawT raw0, raw1;
-    load_chunk<T, N, P, R, ROWS>(rs, 0, wave, lane, raw0);
-    load_chunk<T, N, P, R, ROWS>(rs, 1, wave, lane, raw1);
+    load_chunk<T, N, P, R, ROWS, NW>(rs, 0, wave, lane, raw0);
+    load_chunk<T, N, P, R, ROWS, NW>(rs, 1, wave, lane, raw1);
 
     // zero the operand buffers once: pads and the never-written upper band tiles
     {
         uint32_t *z = reinterpret_cast<uint32_t *>(smem_raw);
         const int words = static_cast<int>(sizeof(S) / 4);
-        for (int i = tid; i < words; i += kThreads) z[i] = 0u;
+        for (int i = tid; i < words; i += THREADS) z[i] = 0u;
     }
 
-    // state registers: S^T[n][p] tiles, lane holds n = 16i + 4g + r, p = 16w + c
-    f32x4 st[NTN];
+    // state registers: S^T[n][p] tiles n-tile n0 + i, lane holds
+    // n = 16(n0 + i) + 4g + r, p = 16pt + c
+    f32x4 st[SNT];
 #pragma unroll
-    for (int i = 0; i < NTN; ++i) st[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int pcol = 16 * wave + c;
+    for (int i = 0; i < SNT; ++i) st[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int pcol = 16 * pt + c;
     const size_t sbase = (bb * H + hh) * P * N;
     {
         const float *h0 = a.mode_raw ? a.h0 : a.init_state;
@@ -201,8 +219,8 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
                 first = (1.0f - a.lambda[i0s]) * a.dt[i0s];
             }
 #pragma unroll
-            for (int i = 0; i < NTN; ++i) {
-                const size_t o = sbase + pcol * N + 16 * i + 4 * g;
+            for (int i = 0; i < SNT; ++i) {
+                const size_t o = sbase + pcol * N + 16 * (n0 + i) + 4 * g;
                 f32x4 v = *reinterpret_cast<const f32x4 *>(h0 + o);
                 if (l0 != nullptr) v += *reinterpret_cast<const f32x4 *>(l0 + o) * first;
                 st[i] = v;
@@ -280,7 +298,7 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
             // X^T from my head_dim slice of x
 #pragma unroll
             for (int e = 0; e < G::XE; ++e) {
-                const int o = wave * 16 * R + sub * G::XE + e;
+                const int o = wave * (P / NW) * R + sub * G::XE + e;
                 const int p = o / R, r = o % R;
                 ss.Xt[p * LDR + my_t * R + r] = to_op<op_t>(elem<T>(cur.x, e));
             }
@@ -327,7 +345,9 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
     };
 
     // ---------------------------------------------------------------- P4
-    auto p4 = [&](const typename S::Set &ss, f32x4 *yacc) {
+    // the band into Ms; my half of S_k to the exchange (NW = 8) or as the
+    // carry-in A operand (kept in registers); the state advance
+    auto p4 = [&](const typename S::Set &ss, bf16x8 *sa, f32x4 *ycar) {
         int idx = 0;
 #pragma unroll
         for (int tj = 0; tj < NT; ++tj) {
@@ -335,7 +355,7 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
 #pragma unroll
             for (int si = 0; si < NT; ++si) {
                 if ((16 * si) / R > tlast) continue;
-                if ((idx++) % 4 != wave) continue;
+                if ((idx++) % NW != wave) continue;
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
                 const op_t *ar = &ss.Bs[(16 * si + c) * LDN];
                 const op_t *br = &ss.Cs[(16 * tj + c) * LDN];
@@ -363,48 +383,41 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
             }
         }
 
-        // carry-in output: y^T[p][t] = exp(acum_t) * sum_n S[p][n] C~[t][n]
+        // S_k for the carry-in product.  bf16: as MFMA A-operand slices (k = n
+        // in the npos column order), for eight waves also to the exchange;
+        // f32: the product itself, before the advance overwrites S_k.
         if constexpr (kBf16) {
-            bf16x8 sa[N / 32];
 #pragma unroll
-            for (int kb = 0; kb < N / 32; ++kb)
+            for (int kb = 0; kb < SNT / 2; ++kb) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     sa[kb][j] = to_bf16(st[2 * kb][j]);
                     sa[kb][4 + j] = to_bf16(st[2 * kb + 1][j]);
                 }
-#pragma unroll
-            for (int tj = 0; tj < NT; ++tj) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                const op_t *cr = &ss.Cs[(16 * tj + c) * LDN];
-#pragma unroll
-                for (int kb = 0; kb < N / 32; ++kb)
-                    acc = mfma_bf16(sa[kb], *reinterpret_cast<const bf16x8 *>(cr + 32 * kb + 8 * g),
-                                    acc);
-                yacc[tj] = acc * ss.eac[(16 * tj + c) / R];
+                if constexpr (NW == 8) sm.xchg[((pt * 2 + hf) * (SNT / 2) + kb) * 64 + lane] = sa[kb];
             }
         } else {
 #pragma unroll
-            for (int tj = 0; tj < NT; ++tj) {
+            for (int q = 0; q < YT; ++q) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                const op_t *cr = &ss.Cs[(16 * tj + c) * LDN];
+                const op_t *cr = &ss.Cs[(16 * (t0 + q) + c) * LDN];
 #pragma unroll
                 for (int i = 0; i < NTN; ++i) {
                     const f32x4 bv = *reinterpret_cast<const f32x4 *>(cr + 16 * i + 4 * g);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc = mfma_f32(st[i][r], bv[r], acc);
                 }
-                yacc[tj] = acc * ss.eac[(16 * tj + c) / R];
+                ycar[q] = acc;
             }
         }
 
         // state advance: S^T = exp(dA) S^T + (B~ w decay)^T X
         const float edA = dexp<kBf16>(ss.acum[QT - 1]);
-        const op_t *xr = &ss.Xt[(16 * wave + c) * LDR];
+        const op_t *xr = &ss.Xt[pcol * LDR];
 #pragma unroll
-        for (int i = 0; i < NTN; ++i) {
+        for (int i = 0; i < SNT; ++i) {
             f32x4 acc = st[i] * edA;
-            const op_t *ar = &ss.Bwt[(16 * i + c) * LDR];
+            const op_t *ar = &ss.Bwt[(16 * (n0 + i) + c) * LDR];
 #pragma unroll
             for (int kb = 0; kb < ROWS / KB; ++kb)
                 acc = mma_kb(ar + kb * KB, xr + kb * KB, acc, g);
@@ -413,27 +426,51 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
     };
 
     // ---------------------------------------------------------------- P5
-    auto p5 = [&](int ck, const typename S::Set &ss, f32x4 *yacc) {
-        const op_t *xr = &ss.Xt[(16 * wave + c) * LDR];
+    // y^T[p][t] = exp(acum_t) sum_n S_k[p][n] C~[t][n] + sum_s X^T[p][s] M[t][s]
+    auto p5 = [&](int ck, const typename S::Set &ss, const bf16x8 *sa, const f32x4 *ycar) {
+        constexpr int KH = kBf16 ? SNT / 2 : 1;   // 32-wide k-blocks of one state half
+        f32x4 yacc[YT];
 #pragma unroll
-        for (int tj = 0; tj < NT; ++tj) {
+        for (int q = 0; q < YT; ++q) {
+            const int tj = t0 + q;
+            f32x4 acc;
+            if constexpr (kBf16) {
+                acc = f32x4{0.f, 0.f, 0.f, 0.f};
+                const op_t *cr = &ss.Cs[(16 * tj + c) * LDN + 8 * g];
+#pragma unroll
+                for (int kb = 0; kb < KH; ++kb)
+                    acc = mfma_bf16(sa[kb], *reinterpret_cast<const bf16x8 *>(cr + 32 * (hf * KH + kb)),
+                                    acc);
+                if constexpr (NW == 8) {
+                    const int oh = 1 - hf;   // the partner wave's half
+#pragma unroll
+                    for (int kb = 0; kb < KH; ++kb)
+                        acc = mfma_bf16(sm.xchg[((pt * 2 + oh) * KH + kb) * 64 + lane],
+                                        *reinterpret_cast<const bf16x8 *>(cr + 32 * (oh * KH + kb)), acc);
+                }
+            } else {
+                acc = ycar[q];
+            }
+            acc = acc * ss.eac[(16 * tj + c) / R];
             const op_t *mr = &sm.Ms[(16 * tj + c) * LDR];
+            const op_t *xr = &ss.Xt[pcol * LDR];
             const int tlast = (16 * tj + 15) / R;
             const int send = (tlast + 1) * R < ROWS ? (tlast + 1) * R : ROWS;
             const int nkb = (send + KB - 1) / KB;
 #pragma unroll
             for (int kb = 0; kb < ROWS / KB; ++kb)
-                if (kb < nkb) yacc[tj] = mma_kb(xr + kb * KB, mr + kb * KB, yacc[tj], g);
+                if (kb < nkb) acc = mma_kb(xr + kb * KB, mr + kb * KB, acc, g);
+            yacc[q] = acc;
         }
         const uint32_t tau0 = static_cast<uint32_t>(ck) * QT;
 #pragma unroll
-        for (int tj = 0; tj < NT; ++tj) {
-            const int rho = 16 * tj + c;
+        for (int q = 0; q < YT; ++q) {
+            const int rho = 16 * (t0 + q) + c;
             const int rr = rho % R;
             const uint32_t tau = tau0 + rho / R;
-            const f32x4 v = yacc[tj];
+            const f32x4 v = yacc[q];
             // rows past the sequence end fall outside the buffer: dropped
-            const uint32_t oy = tau * rs.tok_x + ((16 * wave + 4 * g) * R + rr) * SZ;
+            const uint32_t oy = tau * rs.tok_x + ((16 * pt + 4 * g) * R + rr) * SZ;
             if constexpr (R == 1) {
                 if constexpr (kBf16) {
                     u32x2 pk;
@@ -465,14 +502,13 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
     lds_barrier();
     auto step = [&](int ck, typename S::Set &cur, typename S::Set &nxt, RawT &mine,
                     const RawT &next_raw) {
-        f32x4 yacc[NT];
-        p4(cur, yacc);
+        bf16x8 sa[kBf16 ? SNT / 2 : 1];
+        f32x4 ycar[kBf16 ? 1 : YT];
+        p4(cur, sa, ycar);
         lds_barrier();
-        p5(ck, cur, yacc);
-        if (ck + 1 < nchunks) {
-            load_chunk<T, N, P, R, ROWS>(rs, ck + 2, wave, lane, mine);
-            stage(ck + 1, next_raw, nxt);
-        }
+        p5(ck, cur, sa, ycar);
+        load_chunk<T, N, P, R, ROWS, NW>(rs, ck + 2, wave, lane, mine);   // zeros past the end
+        if (ck + 1 < nchunks) stage(ck + 1, next_raw, nxt);
         lds_barrier();
     };
     for (int ck = 0; ck < nchunks; ck += 2) {
@@ -483,14 +519,14 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
     // ---- boundary state (scan.rs:270-288, 599-638)
     if (a.h_out != nullptr) {
 #pragma unroll
-        for (int i = 0; i < NTN; ++i)
-            *reinterpret_cast<f32x4 *>(a.h_out + sbase + pcol * N + 16 * i + 4 * g) = st[i];
+        for (int i = 0; i < SNT; ++i)
+            *reinterpret_cast<f32x4 *>(a.h_out + sbase + pcol * N + 16 * (n0 + i) + 4 * g) = st[i];
     }
     if (a.last_u_out != nullptr) {
         // last_u = sum_r x_{L-1,r} B~_{L-1,r}^T, from the final chunk's LDS tiles
         const typename S::Set &ls = sm.set[(nchunks - 1) & 1];
         const int tl = static_cast<int>((L - 1) - static_cast<size_t>(nchunks - 1) * QT);
-        for (int it = tid; it < P * N; it += kThreads) {
+        for (int it = tid; it < P * N; it += THREADS) {
             const int p = it / N;
             const int n = it - p * N;
             float acc = 0.0f;
@@ -504,33 +540,33 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
     }
 }
 
-template <typename T, int N, int R, int ROWS>
+template <typename T, int N, int R, int ROWS, int NW>
 hipError_t launch_one(const ScanLaunch &a, hipStream_t s) {
     constexpr int P = 64;
-    using Sm = Smem<T, N, P, R, ROWS>;
-    using G = Geo<T, N, P, R, ROWS>;
+    using Sm = Smem<T, N, P, R, ROWS, NW>;
+    using G = Geo<T, N, P, R, ROWS, NW>;
     const int nchunks = static_cast<int>((a.seq + G::QT - 1) / G::QT);
     const size_t smem = sizeof(Sm);
-    auto kern = ssd_scan_fast_kernel<T, N, P, R, ROWS>;
+    auto kern = ssd_scan_fast_kernel<T, N, P, R, ROWS, NW>;
     static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  static_cast<int>(smem));
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(kern, dim3(a.batch * a.heads), dim3(kThreads), smem, s, a, nchunks);
+    hipLaunchKernelGGL(kern, dim3(a.batch * a.heads), dim3(64 * NW), smem, s, a, nchunks);
     return hipGetLastError();
 }
 
-template <typename T, int ROWS>
+template <typename T, int ROWS, int NW128>
 hipError_t launch_t(const ScanLaunch &a, hipStream_t s) {
     const size_t n = a.d_state, r = a.rank;
     if (n == 128) {
-        if (r == 1) return launch_one<T, 128, 1, ROWS>(a, s);
-        if (r == 2) return launch_one<T, 128, 2, ROWS>(a, s);
-        if (r == 4) return launch_one<T, 128, 4, ROWS>(a, s);
+        if (r == 1) return launch_one<T, 128, 1, ROWS, NW128>(a, s);
+        if (r == 2) return launch_one<T, 128, 2, ROWS, NW128>(a, s);
+        if (r == 4) return launch_one<T, 128, 4, ROWS, NW128>(a, s);
     } else if (n == 64) {
-        if (r == 1) return launch_one<T, 64, 1, ROWS>(a, s);
-        if (r == 2) return launch_one<T, 64, 2, ROWS>(a, s);
-        if (r == 4) return launch_one<T, 64, 4, ROWS>(a, s);
+        if (r == 1) return launch_one<T, 64, 1, ROWS, 4>(a, s);
+        if (r == 2) return launch_one<T, 64, 2, ROWS, 4>(a, s);
+        if (r == 4) return launch_one<T, 64, 4, ROWS, 4>(a, s);
     }
     return hipErrorNotSupported;
 }
@@ -558,8 +594,8 @@ bool scan_fast_supported(const ScanLaunch &a) {
 
 hipError_t launch_scan_fast(const ScanLaunch &a, hipStream_t stream) {
     if (!scan_fast_supported(a)) return hipErrorNotSupported;
-    if (a.bf16) return launch_t<bf16_t, 64>(a, stream);
-    return launch_t<float, 32>(a, stream);
+    if (a.bf16) return launch_t<bf16_t, 64, 8>(a, stream);
+    return launch_t<float, 32, 4>(a, stream);
 }
 
 }  // namespace m3
