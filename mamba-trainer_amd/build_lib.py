@@ -19,7 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "mamba3", "libmamba3_hip.so")
 
-SOURCES = ["m3_api.cpp", "ssd_scan.hip", "ssd_scan_fast.hip", "ssd_scan_split.hip", "decode_step.hip", "mfma_selftest.hip"]
+SOURCES = ["m3_api.cpp", "ssd_scan.hip", "ssd_scan_fast.hip", "ssd_scan_chunked.hip", "decode_step.hip", "mfma_selftest.hip"]
 ARCH = "gfx950"
 # Packed-FP32 instructions stay off: hipcc derives them from plain float code
 # and some forms have been unreliable; scalar FP32 is used instead.

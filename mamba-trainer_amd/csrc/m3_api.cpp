@@ -221,10 +221,11 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
         a.angle_out = in->theta ? out->state.angle : nullptr;
     }
     hipError_t e;
-    const size_t need = m3::scan_split_workspace(a);
-    if (need > 0 && in->workspace != nullptr && in->workspace_bytes >= need) {
-        e = m3::launch_scan_split(a, in->workspace, s);
-        if (e == hipSuccess) g_launches.fetch_add(2, std::memory_order_relaxed);
+    const size_t need = m3::scan_chunked_workspace(a);
+    const bool ws_aligned = (reinterpret_cast<uintptr_t>(in->workspace) & 255u) == 0;
+    if (need > 0 && in->workspace != nullptr && in->workspace_bytes >= need && ws_aligned) {
+        e = m3::launch_scan_chunked(a, in->workspace, s);
+        if (e == hipSuccess) g_launches.fetch_add(3, std::memory_order_relaxed);
     } else {
         e = m3::launch_scan(a, s);
         if (e == hipSuccess) g_launches.fetch_add(1, std::memory_order_relaxed);
@@ -247,7 +248,7 @@ size_t m3_scan_workspace_bytes(const m3_scan_inputs *in) {
     alignas(16) static float dummy[4] = {0, 0, 0, 0};
     a.x = a.b = a.c = dummy;
     a.y = dummy;
-    return m3::scan_split_workspace(a);
+    return m3::scan_chunked_workspace(a);
 }
 
 m3_status m3_ssd_chunked(const m3_ssd_args *in, void *y, float *final_state, void *stream) {

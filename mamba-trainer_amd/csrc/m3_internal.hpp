@@ -43,10 +43,12 @@ hipError_t launch_scan(const ScanLaunch &a, hipStream_t stream);
 // aligned x/b/c/theta/y); hipErrorNotSupported for anything else.
 bool scan_fast_supported(const ScanLaunch &a);
 hipError_t launch_scan_fast(const ScanLaunch &a, hipStream_t stream);
-// The two-pass form of the same shapes (chunk-parallel pass + state walk):
-// workspace bytes it needs (0 when the shape is not covered), and the launch.
-size_t scan_split_workspace(const ScanLaunch &a);
-hipError_t launch_scan_split(const ScanLaunch &a, void *workspace, hipStream_t stream);
+// The chunk-parallel form of the same shapes (chunk states, an elementwise
+// state pass, chunk outputs: three launches over a 256-byte aligned caller
+// workspace): the workspace bytes it needs (0 when the shape is not covered),
+// and the launch.
+size_t scan_chunked_workspace(const ScanLaunch &a);
+hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream);
 
 // Largest head_dim / d_state the scan kernels are instantiated for.
 constexpr size_t kScanMaxHeadDim = 128;

@@ -64,58 +64,6 @@ struct Smem {
     bf16x8 xchg[NW == 8 ? 4 * 2 * (N / 64) * 64 : 1];
 };
 
-// Raw inputs of one chunk as this lane loads them.
-template <typename T, int N, int P, int R, int ROWS, int NW>
-struct Raw {
-    using G = Geo<T, N, P, R, ROWS, NW>;
-    u32x4 b[2][G::HV];
-    u32x4 c[2][G::HV];
-    unsigned int th[G::TW];
-    u32x4 x[G::XV];
-    float s0, s1, s2, s3;   // dt, lambda, dt_next, lambda_next (or a, g, w)
-};
-
-template <typename T, int N, int P, int R, int ROWS, int NW>
-__device__ __forceinline__ void load_chunk(const SeqBufs &rs, int ck, int wave, int lane,
-                                           Raw<T, N, P, R, ROWS, NW> &raw) {
-    using G = Geo<T, N, P, R, ROWS, NW>;
-    constexpr uint32_t SZ = sizeof(T);
-    const uint32_t sub = lane / G::SW;
-    const uint32_t tok = static_cast<uint32_t>(ck) * G::QT + lane % G::SW;
-    const uint32_t i0 = wave * G::PW + sub * G::PPL;
-    const uint32_t ob = tok * rs.tok_bc;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int v = 0; v < G::HV; ++v) {
-            const uint32_t off = ob + ((i0 + h * G::NH) * R + v * G::E) * SZ;
-            raw.b[h][v] = bld16(rs.b, off);
-            raw.c[h][v] = bld16(rs.c, off);
-        }
-    const uint32_t ot = tok * rs.tok_th + i0 * SZ;
-    if constexpr (G::THB >= 16) {
-#pragma unroll
-        for (int v = 0; v < G::THB / 16; ++v) {
-            const u32x4 q = bld16(rs.th, ot + 16 * v);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) raw.th[4 * v + j] = q[j];
-        }
-    } else if constexpr (G::THB == 8) {
-        const u32x2 q = bld8(rs.th, ot);
-        raw.th[0] = q[0];
-        raw.th[1] = q[1];
-    } else {
-        raw.th[0] = bld4(rs.th, ot);
-    }
-    const uint32_t ox = tok * rs.tok_x + (wave * (P / NW) * R + sub * G::XE) * SZ;
-#pragma unroll
-    for (int v = 0; v < G::XV; ++v) raw.x[v] = bld16(rs.x, ox + 16 * v);
-    raw.s0 = bldf(rs.s0, tok * rs.tok_s);
-    raw.s1 = bldf(rs.s1, tok * rs.tok_s);
-    raw.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
-    raw.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
-}
-
 template <typename T, int N, int P, int R, int ROWS, int NW>
 __global__ void __launch_bounds__(64 * NW, 1)
 ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
@@ -159,36 +107,7 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
     const bool tok_lane = my_t < QT;
     const int i0 = wave * G::PW + sub * PPL;
 
-    // per-sequence buffer resources (token tau of this head at tau * tok bytes)
-    SeqBufs rs;
-    {
-        const size_t row0 = bb * L * H + hh;
-        const size_t rows = L * H - hh;
-        auto mk = [&](const void *base, size_t row_bytes) {
-            return make_rsrc(static_cast<const char *>(base) + row0 * row_bytes,
-                             static_cast<uint32_t>(rows * row_bytes));
-        };
-        rs.b = mk(a.b, N * R * SZ);
-        rs.c = mk(a.c, N * R * SZ);
-        rs.x = mk(a.x, P * R * SZ);
-        rs.y = mk(a.y, P * R * SZ);
-        rs.th = rot ? mk(a.theta, NH * SZ) : make_rsrc(a.x, 0u);   // no records: zeros
-        if (a.mode_raw) {
-            rs.s0 = rs.s2 = mk(a.dt, 4);
-            rs.s1 = rs.s3 = mk(a.lambda, 4);
-            rs.nxt_s = 1;
-        } else {
-            rs.s0 = mk(a.a, 4);
-            rs.s1 = mk(a.g, 4);
-            rs.s2 = mk(a.w, 4);
-            rs.s3 = make_rsrc(a.a, 0u);
-            rs.nxt_s = 0;
-        }
-        rs.tok_bc = static_cast<uint32_t>(H * N * R * SZ);
-        rs.tok_x = static_cast<uint32_t>(H * P * R * SZ);
-        rs.tok_th = static_cast<uint32_t>(H * NH * SZ);
-        rs.tok_s = static_cast<uint32_t>(H * 4);
-    }
+    const SeqBufs rs = seq_bufs<T, N, P, R>(a, bb, hh);
 
     RawT raw0, raw1;
     load_chunk<T, N, P, R, ROWS, NW>(rs, 0, wave, lane, raw0);

@@ -147,8 +147,8 @@ def test_python_api_rejects_host_tensors():
 
 
 def test_scan_workspace_query():
-    """m3_scan_workspace_bytes: the two-pass kernels cover head_dim 64, d_state
-    64/128, rank 1/2/4; other shapes run single-pass and need none."""
+    """m3_scan_workspace_bytes: the chunk-parallel kernels cover head_dim 64,
+    d_state 64/128, rank 1/2/4; other shapes run single-pass and need none."""
     import ctypes as C
     from mamba3 import _lib
     L = _lib.lib()
@@ -159,9 +159,12 @@ def test_scan_workspace_query():
         return int(L.m3_scan_workspace_bytes(C.byref(cin)))
 
     w1 = need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16)
-    # per chunk: band 64x64, C~ 64x128 and (B~w)^T 128x64 in bf16, plus scalars
-    assert 96 * 32 * (64 * 64 + 2 * 64 * 128) * 2 <= w1 <= 96 * 32 * 44 * 1024
-    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) > w1
+    # per chunk of 64 tokens: U_k and S_k (bf16 64x128 each), the chunk
+    # decay, and angle total / cosine / sine per pair (3 x 64 f32)
+    bhk = 8 * 12 * 32
+    assert w1 == bhk * (2 * 64 * 128 * 2 + 4 + 3 * 64 * 4)
+    # f32 storage: 32-token chunks at rank 1 and an f32 S_k
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) == 2 * bhk * (64 * 128 * 8 + 4 + 3 * 64 * 4)
     assert need(1, 100, 2, 48, 128, 1, _lib.M3_BF16) == 0      # head_dim 48
     assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) == 0       # d_state 96
     assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) == 0      # rank 3
