@@ -114,11 +114,12 @@ typedef struct m3_scan_inputs {
     const m3_ssm_state *state;/* carried-in state or NULL */
     size_t chunk_size;        /* > 0; the kernel tiles time itself (a hint) */
     int32_t want_state;       /* ScanInputs::want_state */
-    /* Device scratch for the two-pass scan (no reference counterpart: the
-     * reference allocates its intermediates per call).  NULL, or fewer than
-     * m3_scan_workspace_bytes() bytes, selects the single-pass kernels, which
-     * give the same results.  The contents need no initialisation; calls that
-     * share a workspace must be ordered on one stream. */
+    /* Device scratch for the chunk-parallel scan (no reference counterpart:
+     * the reference allocates its intermediates per call): 256-byte aligned,
+     * at least m3_scan_workspace_bytes() bytes.  NULL, a smaller or unaligned
+     * buffer selects the single-pass kernel, which gives the same results to
+     * rounding and needs no scratch.  The contents need no initialisation;
+     * calls that share a workspace must be ordered on one stream. */
     void *workspace;
     size_t workspace_bytes;
 } m3_scan_inputs;
@@ -134,7 +135,7 @@ typedef struct m3_scan_output {
  * fold, carried state, skip path and boundary state in one launch. */
 m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *stream);
 
-/* Workspace bytes the two-pass scan needs for these inputs (shapes and
+/* Workspace bytes the chunk-parallel scan needs for these inputs (shapes and
  * dtype are read; pointers are not); 0 when the shape runs single-pass only.
  * No reference counterpart (see m3_scan_inputs.workspace). */
 size_t m3_scan_workspace_bytes(const m3_scan_inputs *in);

@@ -98,7 +98,7 @@ class ScanInputs:
         self.state: Optional[SsmState] = None
         self.chunk_size = 64
         self.want_state = True
-        self.two_pass = False    # the chunk-parallel + state-walk kernels, when they apply
+        self.chunk_parallel = True   # the three chunk-parallel kernels, where they apply
 
     def with_theta(self, theta):
         self.theta = theta
@@ -120,10 +120,11 @@ class ScanInputs:
         self.want_state = want_state
         return self
 
-    def with_two_pass(self, two_pass: bool):
-        """Select the two-pass kernels or the single-pass kernels (default); the
-        results agree to rounding.  No reference counterpart."""
-        self.two_pass = two_pass
+    def with_chunk_parallel(self, chunk_parallel: bool):
+        """Select the chunk-parallel kernels (default; they take a workspace from
+        torch's allocator) or the single-pass kernel, which allocates nothing;
+        the results agree to rounding.  No reference counterpart."""
+        self.chunk_parallel = chunk_parallel
         return self
 
 
@@ -195,29 +196,17 @@ def mamba3_scan(inputs: ScanInputs) -> ScanOutput:
         C.pointer(st_c) if st_c is not None else None,
         int(inputs.chunk_size), int(bool(inputs.want_state)), None, 0)
     ws = None
-    if inputs.two_pass:
+    if inputs.chunk_parallel:
         need = int(_lib.lib().m3_scan_workspace_bytes(C.byref(cin)))
         if need > 0:
-            ws = _workspace(x.device, need)
+            # stream-ordered by torch's caching allocator: freed after this
+            # call's kernels, reused by later work on the same stream
+            ws = torch.empty(need, dtype=torch.uint8, device=x.device)
             cin.workspace = ws.data_ptr()
             cin.workspace_bytes = need
     cout = _lib.ScanOutputC(y.data_ptr(), out_state._c() if out_state else _lib.SsmStateC())
     _lib.check(_lib.lib().m3_scan(C.byref(cin), C.byref(cout), _stream(x)))
     return ScanOutput(y, out_state)
-
-
-_WORKSPACES = {}
-
-
-def _workspace(device, nbytes: int) -> torch.Tensor:
-    """Per-device scratch for the two-pass scan, grown on demand and reused by
-    calls on the current stream (the library never allocates)."""
-    key = (device.type, device.index)
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
-        _WORKSPACES[key] = ws
-    return ws
 
 
 def ssd_chunked(x, b, c, a, g, w, initial_state=None, chunk_size=64,

@@ -24,7 +24,7 @@ def host(t):
 
 
 def run_scan(inp, dtype=torch.float32, chunk=64, want_state=True, theta=True, skip=None,
-             state=None, two_pass=True):
+             state=None, chunk_parallel=True):
     """inp: dict from cases.baseline_inputs (x, b, c, dt, a_log, lam, theta, h0, ...)."""
     from mamba3.ssm import ScanInputs, SsmState, mamba3_scan
     si = ScanInputs(dev(inp["x"], dtype), dev(inp["b"], dtype), dev(inp["c"], dtype),
@@ -36,7 +36,7 @@ def run_scan(inp, dtype=torch.float32, chunk=64, want_state=True, theta=True, sk
     if state is not None:
         si = si.with_state(SsmState(dev(state[0]), dev(state[1]),
                                     dev(state[2]) if state[2] is not None else None))
-    si = si.with_chunk_size(chunk).with_state_output(want_state).with_two_pass(two_pass)
+    si = si.with_chunk_size(chunk).with_state_output(want_state).with_chunk_parallel(chunk_parallel)
     out = mamba3_scan(si)
     torch.cuda.synchronize()
     st = out.state

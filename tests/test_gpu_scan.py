@@ -125,9 +125,9 @@ FEATURE_CASES = [
 ]
 
 
-@pytest.mark.parametrize("two_pass", [True, False], ids=["two_pass", "single_pass"])
+@pytest.mark.parametrize("chunk_parallel", [True, False], ids=["chunk_parallel", "single_pass"])
 @pytest.mark.parametrize("B,T,H,P,N,R,theta,skip,state,dtype", FEATURE_CASES)
-def test_scan_features_against_f64(B, T, H, P, N, R, theta, skip, state, dtype, two_pass):
+def test_scan_features_against_f64(B, T, H, P, N, R, theta, skip, state, dtype, chunk_parallel):
     rng = np.random.default_rng(zlib.crc32(repr((B, T, H, P, N, R, theta, skip, state,
                                                   dtype)).encode()))
     inp = baseline_inputs(rng, B, T, H, P, N, R, theta=theta, dtype=dtype,
@@ -136,7 +136,7 @@ def test_scan_features_against_f64(B, T, H, P, N, R, theta, skip, state, dtype, 
     st = (inp["h0"], inp["last_u0"], inp.get("angle0")) if state else None
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     y, h, lu, ang = run_scan(inp, dtype=tdt, theta=theta, skip=d_skip, state=st,
-                             two_pass=two_pass)
+                             chunk_parallel=chunk_parallel)
     y64, h64, lu64, ang64 = oracle_scan(inp, theta=theta, skip=d_skip, state=st)
     tol = BF16_TOL if dtype == "bf16" else F32_TOL
     assert rel_l2(y, y64) <= tol, ("y", rel_l2(y, y64))
@@ -219,9 +219,9 @@ def test_config2_mimo_bf16_one_head():
 
 
 @pytest.mark.parametrize("R", [1, 4])
-def test_two_pass_matches_single_pass_at_benchmark_shapes(R):
+def test_chunk_parallel_matches_single_pass_at_benchmark_shapes(R):
     """Configs 1 and 2 at full batch and head count (shorter sequence): the
-    two-pass kernels and the single-pass kernel agree, and both match the
+    chunk-parallel kernels and the single-pass kernel agree, and both match the
     f64 recurrence on two of the sequences."""
     from mamba3.ssm import ScanInputs, mamba3_scan
     g = torch.Generator(device="cuda").manual_seed(7 + R)
@@ -235,7 +235,7 @@ def test_two_pass_matches_single_pass_at_benchmark_shapes(R):
     a_log = torch.rand(H, device="cuda", generator=g) * math.log(16)
     th = (torch.rand(B, T, H, N // 2, device="cuda", generator=g) * math.pi).to(torch.bfloat16)
     mk = lambda two: mamba3_scan(ScanInputs(x, b, c, dt, a_log, lam).with_theta(th)
-                                 .with_two_pass(two))
+                                 .with_chunk_parallel(two))
     two, one = mk(True), mk(False)
     assert rel_l2(host(two.y), host(one.y)) <= BF16_TOL
     assert rel_l2(host(two.state.h), host(one.state.h)) <= BF16_TOL
