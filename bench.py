@@ -39,6 +39,12 @@ sys.path.insert(0, os.path.join(ROOT, "mamba-trainer_amd"))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 
+# HBM-side bytes of one headline scan call (chunk_state + state_pass +
+# chunk_scan), from rocprofv3 FETCH_SIZE / WRITE_SIZE per dispatch scaled by a
+# 256 MiB copy (FETCH x 2 KiB, WRITE x 1 KiB): 361.5 MB read + 134.6 MB written.
+# Counters cannot be read inside this process; re-measured when the kernels change.
+SCAN_TRAFFIC_BYTES = 496_145_013
+
 # BASELINE config 1 (the headline) and config 3 (decode)
 SCAN = dict(B=8, L=2048, H=12, P=64, N=128, R=1, Q=64)
 DECODE = dict(B=256, layers=24, H=24, P=64, N=128, R=1, sets=4)
@@ -237,6 +243,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--scan-only", action="store_true",
+                    help="run only the headline scan --steps times (for counter runs)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="copy MIB MiB device to device --steps times and exit (the known-size "
+                         "kernel that scales FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: every GPU box in this build has one, and the path "
@@ -248,10 +259,23 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs the MI355X (no ROCm device visible)", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n * 4, "copies": args.steps}), flush=True)
+        return
     from mamba3 import _lib as L_
     lib = L_.lib()
 
     torch.cuda.synchronize()
+    if args.scan_only:
+        sc = bench_scan(torch, lib, L_, args, chunk_parallel=True)
+        print(json.dumps({"scan_us": round(sc["kernel_ms"] * 1e3, 2)}), flush=True)
+        return
     sc = bench_scan(torch, lib, L_, args, chunk_parallel=True)
     sc1 = bench_scan(torch, lib, L_, args, chunk_parallel=False, inp=sc["inp"])
     s = SCAN
@@ -285,7 +309,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": SCAN_TRAFFIC_BYTES,
                      "kernel": "m3_scan: chunk_state_kernel + state_pass_kernel + "
                                "chunk_scan_kernel (one scan call)",
                      "kernel_us": round(sc["kernel_ms"] * 1e3, 2),
