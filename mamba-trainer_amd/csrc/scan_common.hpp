@@ -140,15 +140,18 @@ struct SeqBufs {
 // Buffer resources of sequence (bb, hh): token tau of this head at tau * tok
 // bytes from the resource base; s0..s3 are dt, lambda and the next token's dt,
 // lambda (mamba3_scan) or a, g, w (ssd_chunked).
+// With `live` false every resource has no records: loads through it return
+// zeros without touching memory (a prefetch past the last chunk).
 template <typename T, int N, int P, int R>
-__device__ __forceinline__ SeqBufs seq_bufs(const ScanLaunch &a, size_t bb, size_t hh) {
+__device__ __forceinline__ SeqBufs seq_bufs(const ScanLaunch &a, size_t bb, size_t hh,
+                                            bool live = true) {
     constexpr uint32_t SZ = sizeof(T);
     constexpr int NH = N / 2;
     const size_t H = a.heads, L = a.seq;
     const bool rot = a.theta != nullptr;
     SeqBufs rs;
     const size_t row0 = bb * L * H + hh;
-    const size_t rows = L * H - hh;
+    const size_t rows = live ? L * H - hh : 0;
     auto mk = [&](const void *base, size_t row_bytes) {
         return make_rsrc(static_cast<const char *>(base) + row0 * row_bytes,
                          static_cast<uint32_t>(rows * row_bytes));
@@ -193,20 +196,21 @@ struct Raw {
 template <typename T, int N, int P, int R, int ROWS, int NW, bool WC>
 __device__ __forceinline__ void load_chunk(const SeqBufs &rs, int ck, int wave, int lane,
                                            Raw<T, N, P, R, ROWS, NW, WC> &raw) {
+    // issued in the order the stage consumes them (vmcnt counts in order):
+    // the per-token scalars and theta feed the prefix scans and the sines
+    // while B, C and x are still in flight
     using G = Geo<T, N, P, R, ROWS, NW>;
     constexpr uint32_t SZ = sizeof(T);
     const uint32_t sub = lane / G::SW;
     const uint32_t tok = static_cast<uint32_t>(ck) * G::QT + lane % G::SW;
     const uint32_t i0 = wave * G::PW + sub * G::PPL;
-    const uint32_t ob = tok * rs.tok_bc;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int v = 0; v < G::HV; ++v) {
-            const uint32_t off = ob + ((i0 + h * G::NH) * R + v * G::E) * SZ;
-            raw.b[h][v] = bld16(rs.b, off);
-            if constexpr (WC) raw.c[h][v] = bld16(rs.c, off);
-        }
+    raw.s0 = bldf(rs.s0, tok * rs.tok_s);
+    raw.s1 = bldf(rs.s1, tok * rs.tok_s);
+    raw.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
+    raw.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
+    // the scheduler keeps the groups in this order wherever the function is
+    // inlined, so every call site leaves the same vmcnt pattern behind
+    __builtin_amdgcn_sched_barrier(0);
     const uint32_t ot = tok * rs.tok_th + i0 * SZ;
     if constexpr (G::THB >= 16) {
 #pragma unroll
@@ -222,13 +226,21 @@ __device__ __forceinline__ void load_chunk(const SeqBufs &rs, int ck, int wave, 
     } else {
         raw.th[0] = bld4(rs.th, ot);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t ob = tok * rs.tok_bc;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int v = 0; v < G::HV; ++v) {
+            const uint32_t off = ob + ((i0 + h * G::NH) * R + v * G::E) * SZ;
+            raw.b[h][v] = bld16(rs.b, off);
+            if constexpr (WC) raw.c[h][v] = bld16(rs.c, off);
+        }
+    __builtin_amdgcn_sched_barrier(0);
     const uint32_t ox = tok * rs.tok_x + (wave * (P / NW) * R + sub * G::XE) * SZ;
 #pragma unroll
     for (int v = 0; v < G::XV; ++v) raw.x[v] = bld16(rs.x, ox + 16 * v);
-    raw.s0 = bldf(rs.s0, tok * rs.tok_s);
-    raw.s1 = bldf(rs.s1, tok * rs.tok_s);
-    raw.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
-    raw.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 }  // namespace scan
