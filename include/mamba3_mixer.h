@@ -1,0 +1,101 @@
+/*
+ * mamba3_mixer.h -- C ABI of the token-parallel operations of the Mamba-3
+ * mixer and language model around the scan (gfx950, bf16 activations).
+ *
+ * With m3_scan / m3_step (mamba3_ssm.h) these compose Mamba3Mixer::apply,
+ * ::apply_with_state and ::step and the Mamba3Lm forward:
+ *
+ *   m3_rms_norm                 RmsNorm::apply            src/nn/norm.rs:95-105
+ *                               (fused rms_norm_kernel    src/tensor/ops/fused.rs:140-185)
+ *   m3_quantize_int8_columns    Quantizer::quantize, QuantConfig::int8_weights
+ *                                                         src/nn/quant.rs:95-103, 231-245, 282-330
+ *   m3_linear                   Linear::apply (+ the stack's residual add)
+ *                                                         src/nn/linear.rs:155-185,
+ *                                                         src/models/hybrid.rs:446-456
+ *   m3_mixer_prologue           Mamba3Mixer::project after in_proj
+ *                                                         src/models/mamba3.rs:376-466
+ *   m3_mixer_gate               Mamba3Mixer::finish before out_proj
+ *                                                         src/models/mamba3.rs:468-477
+ *   m3_embedding_lookup         Embedding::lookup         src/nn/embedding.rs
+ *
+ * Conventions are those of mamba3_ssm.h: caller-allocated contiguous device
+ * buffers, asynchronous on `stream`, status codes with m3_last_error().
+ * Activations are bf16 (raw 16-bit words); weights of norms and biases, and
+ * dt / lambda, are f32.
+ */
+#ifndef MAMBA3_MIXER_H
+#define MAMBA3_MIXER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mamba3_ssm.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * weight, rows of `dim` bf16
+ * elements at strides x_stride / y_stride (elements); weight [dim] f32 or
+ * NULL (no gain). */
+m3_status m3_rms_norm(size_t rows, size_t dim, const void *x, size_t x_stride, const float *weight,
+                      float eps, void *y, size_t y_stride, void *stream);
+
+/* Symmetric per-output-channel int8 fake quantization of a Linear weight
+ * w [in_features, out_features] (f32, row-major as the reference stores it):
+ * scale_j = max(max_i |w_ij|, 1e-12) / 127, code_ij = clamp(round(w_ij /
+ * scale_j), -127, 127).  codes [in, out] are written as bf16 (whole numbers,
+ * exact), scales [out] as f32; w' = code * scale is the fake-quantized
+ * weight. */
+m3_status m3_quantize_int8_columns(size_t in_features, size_t out_features, const float *w,
+                                   void *codes, float *scales, void *stream);
+
+/* y[m, n] = (x[m, k] @ w[k, n]) * col_scale[n] + residual[m, n], bf16 with f32
+ * accumulation (hipBLASLt).  col_scale and residual may be NULL; residual may
+ * alias y.  The workspace (up to m3_linear_workspace_bytes(), 256-byte
+ * aligned, or NULL) widens the kernels hipBLASLt may pick. */
+size_t m3_linear_workspace_bytes(void);
+m3_status m3_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
+                    const float *col_scale, const void *residual, void *y, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+/* Shapes of one mixer (SsmConfig fields, config.rs:84-128). */
+typedef struct m3_mixer_dims {
+    size_t tokens;            /* batch * seq */
+    size_t heads, head_dim, d_state, rank, groups;
+    int32_t discretization;   /* m3_discretization: learned -> lambda piece present */
+    int32_t dynamics;         /* m3_dynamics: rotational -> theta piece present */
+    float norm_eps;           /* RmsNorm eps of bc_norm (1e-5) */
+} m3_mixer_dims;
+
+/* Width of the in_proj output row (SsmConfig::in_proj_width). */
+size_t m3_mixer_in_proj_width(const m3_mixer_dims *d);
+
+/* From the in_proj output `projected` [tokens, in_proj_width] (bf16) to the
+ * scan inputs: x [tokens, H, P, R], b and c [tokens, H, N, R] (bf16), dt and
+ * lambda [tokens, H] (f32), theta [tokens, H, N/2] (bf16, rotational only).
+ * b_bias / c_bias [H, N] and bc_norm [N] (RMSNorm gain) are f32 or NULL when
+ * the config has no bias / no norm.  No convolution (conv_kernel None). */
+m3_status m3_mixer_prologue(const m3_mixer_dims *d, const void *projected, const float *dt_bias,
+                            const float *b_bias, const float *c_bias, const float *bc_norm,
+                            void *x, void *b, void *c, float *dt, float *lambda, void *theta,
+                            void *stream);
+
+/* out[t] = [RMSNorm(y[t]) * norm_weight] * silu(z[t]) over rows of d_inner;
+ * z rows are z_stride elements apart (the z piece of the projection);
+ * norm_weight NULL skips the post-gate norm. */
+m3_status m3_mixer_gate(size_t tokens, size_t d_inner, const void *y, const void *z,
+                        size_t z_stride, const float *norm_weight, float eps, void *out,
+                        void *stream);
+
+/* out[i] = table[ids[i]] for bf16 rows of dim (table [vocab, dim]).  The
+ * ids live on the device, so they are not checked on the host: an id outside
+ * [0, vocab) reads nothing and yields a zero row. */
+m3_status m3_embedding_lookup(size_t n, size_t dim, const int32_t *ids, size_t vocab,
+                              const void *table, void *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA3_MIXER_H */

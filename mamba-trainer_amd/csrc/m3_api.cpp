@@ -18,12 +18,9 @@ namespace {
 thread_local std::string g_last_error;
 std::atomic<uint64_t> g_launches{0};
 
-m3_status fail(m3_status st, const char *fmt, ...) {
+m3_status vfail(m3_status st, const char *fmt, va_list ap) {
     char buf[512];
-    va_list ap;
-    va_start(ap, fmt);
     vsnprintf(buf, sizeof(buf), fmt, ap);
-    va_end(ap);
     const char *prefix = "";
     switch (st) {
         case M3_ERR_CONFIG: prefix = "invalid configuration: "; break;   // error.rs:12
@@ -33,6 +30,14 @@ m3_status fail(m3_status st, const char *fmt, ...) {
     }
     g_last_error = std::string(prefix) + buf;
     return st;
+}
+
+m3_status fail(m3_status st, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    const m3_status r = vfail(st, fmt, ap);
+    va_end(ap);
+    return r;
 }
 
 m3_status ok() {
@@ -54,6 +59,19 @@ size_t scan_rows(int dtype, size_t d_state) {
 bool dtype_ok(int32_t d) { return d == M3_F32 || d == M3_BF16; }
 
 }  // namespace
+
+namespace m3 {
+m3_status api_fail(m3_status st, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    const m3_status r = vfail(st, fmt, ap);
+    va_end(ap);
+    return r;
+}
+m3_status api_ok() { return ok(); }
+m3_status api_hip_fail(hipError_t e, const char *what) { return hip_fail(e, what); }
+void count_launches(uint64_t n) { g_launches.fetch_add(n, std::memory_order_relaxed); }
+}  // namespace m3
 
 extern "C" {
 

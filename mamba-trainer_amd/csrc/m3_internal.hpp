@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+#include <stdint.h>
 
 namespace m3 {
 
@@ -57,5 +58,43 @@ constexpr size_t kScanMaxRank = 64;
 
 // MFMA lane-layout self test (writes 0 on success, else a failure code).
 hipError_t launch_mfma_selftest(int *result_host);
+
+// ---------------------------------------------------------------- mixer ops
+// Row-wise RMSNorm over bf16 rows (y = x * rsqrt(mean(x^2) + eps) * w).
+hipError_t launch_rms_norm(size_t rows, size_t dim, const void *x, size_t x_stride,
+                           const float *w, float eps, void *y, size_t y_stride, hipStream_t s);
+// Symmetric per-output-channel int8 codes (as exact bf16) and f32 scales of
+// a [k, n] f32 weight.
+hipError_t launch_quantize_columns(size_t k, size_t n, const float *w, void *codes, float *scales,
+                                   hipStream_t s);
+// Mamba3Mixer::project after the input projection.
+struct PrologueLaunch {
+    size_t tokens, heads, head_dim, d_state, rank, groups;
+    size_t width;                   // row width of `projected`
+    int learned_lambda;             // lambda piece present (else fixed_lambda)
+    float fixed_lambda;
+    int has_theta;
+    float norm_eps;
+    const void *projected;          // bf16 [tokens, width]
+    const float *dt_bias;           // [H]
+    const float *b_bias, *c_bias;   // [H, N] or null
+    const float *bc_norm;           // [N] RMSNorm gain or null (no norm)
+    void *x, *b, *c;                // bf16 [tokens, H, P, R], [tokens, H, N, R] x2
+    float *dt, *lambda;             // [tokens, H]
+    void *theta;                    // bf16 [tokens, H, N/2] (has_theta)
+};
+hipError_t launch_mixer_prologue(const PrologueLaunch &a, hipStream_t s);
+// out = [RMSNorm(y)] * silu(z), rows of d_inner.
+hipError_t launch_mixer_gate(size_t tokens, size_t d_inner, const void *y, const void *z,
+                             size_t z_stride, const float *norm_w, float eps, void *out,
+                             hipStream_t s);
+// out[i] = table[ids[i]], bf16 rows of dim (zero rows for ids outside vocab).
+hipError_t launch_embedding(size_t n, size_t dim, const int32_t *ids, size_t vocab, const void *table,
+                            void *out, hipStream_t s);
+// y = (x @ w) * col_scale + residual through hipBLASLt (bf16, f32 accumulate).
+hipError_t launch_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
+                         const float *col_scale, const void *residual, void *y, void *workspace,
+                         size_t workspace_bytes, hipStream_t s);
+constexpr size_t kLinearWorkspace = size_t(32) << 20;
 
 }  // namespace m3

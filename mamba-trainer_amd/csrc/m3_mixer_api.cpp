@@ -1,0 +1,160 @@
+// C ABI of the mixer and language-model operations (include/mamba3_mixer.h):
+// argument checks and dispatch.  Errors go through the library's error
+// channel (m3_last_error).
+#include "mamba3_mixer.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+
+#include "m3_internal.hpp"
+
+namespace m3 {
+m3_status api_fail(m3_status st, const char *fmt, ...);
+m3_status api_ok();
+m3_status api_hip_fail(hipError_t e, const char *what);
+void count_launches(uint64_t n);
+}  // namespace m3
+
+namespace {
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+bool lambda_learned(int32_t d) { return d == M3_LEARNED_TRAPEZOID; }
+
+m3_status launched(hipError_t e, const char *what, uint64_t n = 1) {
+    if (e != hipSuccess) return m3::api_hip_fail(e, what);
+    m3::count_launches(n);
+    return m3::api_ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+m3_status m3_rms_norm(size_t rows, size_t dim, const void *x, size_t x_stride, const float *weight,
+                      float eps, void *y, size_t y_stride, void *stream) {
+    if (rows > 0 && (x == nullptr || y == nullptr))
+        return m3::api_fail(M3_ERR_ARGUMENT, "rms_norm buffers are NULL");
+    if (dim == 0) return m3::api_fail(M3_ERR_SHAPE, "RmsNorm over an empty axis");
+    if (x_stride < dim || y_stride < dim)
+        return m3::api_fail(M3_ERR_SHAPE, "row strides (%zu, %zu) are shorter than the row (%zu)",
+                            x_stride, y_stride, dim);
+    if (!(eps >= 0.0f)) return m3::api_fail(M3_ERR_CONFIG, "RmsNorm eps must be non-negative");
+    return launched(m3::launch_rms_norm(rows, dim, x, x_stride, weight, eps, y, y_stride,
+                                        as_stream(stream)),
+                    "rms_norm launch");
+}
+
+m3_status m3_quantize_int8_columns(size_t in_features, size_t out_features, const float *w,
+                                   void *codes, float *scales, void *stream) {
+    if (in_features == 0 || out_features == 0)
+        return m3::api_fail(M3_ERR_SHAPE, "quantizing an empty weight [%zu, %zu]", in_features,
+                            out_features);
+    if (w == nullptr || codes == nullptr || scales == nullptr)
+        return m3::api_fail(M3_ERR_ARGUMENT, "quantization buffers are NULL");
+    return launched(m3::launch_quantize_columns(in_features, out_features, w, codes, scales,
+                                                as_stream(stream)),
+                    "quantize launch");
+}
+
+size_t m3_linear_workspace_bytes(void) { return m3::kLinearWorkspace; }
+
+m3_status m3_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
+                    const float *col_scale, const void *residual, void *y, void *workspace,
+                    size_t workspace_bytes, void *stream) {
+    if (k == 0) return m3::api_fail(M3_ERR_SHAPE, "Linear with zero input features");
+    if (m > 0 && n > 0 && (x == nullptr || w == nullptr || y == nullptr))
+        return m3::api_fail(M3_ERR_ARGUMENT, "linear buffers are NULL");
+    if (workspace != nullptr && (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+        return m3::api_fail(M3_ERR_ARGUMENT, "linear workspace must be 256-byte aligned");
+    const size_t ws = workspace ? (workspace_bytes < m3::kLinearWorkspace ? workspace_bytes
+                                                                           : m3::kLinearWorkspace)
+                                : 0;
+    const hipError_t e = m3::launch_linear(m, k, n, x, w, col_scale, residual, y, workspace, ws,
+                                           as_stream(stream));
+    if (e == hipErrorNotSupported)
+        return m3::api_fail(M3_ERR_UNSUPPORTED, "no hipBLASLt kernel for a [%zu x %zu] @ [%zu x %zu] "
+                            "bf16 product", m, k, k, n);
+    return launched(e, "linear launch");
+}
+
+size_t m3_mixer_in_proj_width(const m3_mixer_dims *d) {
+    if (d == nullptr) return 0;
+    const size_t din = d->heads * d->head_dim * d->rank;
+    const size_t bc = d->groups * d->d_state * d->rank;
+    return 2 * din + 2 * bc + d->heads + (lambda_learned(d->discretization) ? d->heads : 0) +
+           (d->dynamics == M3_ROTATIONAL ? d->heads * d->d_state / 2 : 0);
+}
+
+m3_status m3_mixer_prologue(const m3_mixer_dims *d, const void *projected, const float *dt_bias,
+                            const float *b_bias, const float *c_bias, const float *bc_norm,
+                            void *x, void *b, void *c, float *dt, float *lambda, void *theta,
+                            void *stream) {
+    if (d == nullptr) return m3::api_fail(M3_ERR_ARGUMENT, "mixer dims are NULL");
+    if (d->heads == 0 || d->head_dim == 0 || d->d_state == 0 || d->rank == 0 || d->groups == 0)
+        return m3::api_fail(M3_ERR_CONFIG, "heads, head_dim, d_state, rank and groups must be positive");
+    if (d->heads % d->groups != 0)   // config.rs:207-212
+        return m3::api_fail(M3_ERR_CONFIG, "n_heads (%zu) must be a multiple of n_groups (%zu)",
+                            d->heads, d->groups);
+    const bool rot = d->dynamics == M3_ROTATIONAL;
+    if (rot && d->d_state % 2 != 0)
+        return m3::api_fail(M3_ERR_CONFIG, "rotational dynamics need an even d_state, got %zu",
+                            d->d_state);
+    if (d->tokens == 0) return m3::api_ok();
+    if (projected == nullptr || dt_bias == nullptr || x == nullptr || b == nullptr || c == nullptr ||
+        dt == nullptr || lambda == nullptr || (rot && theta == nullptr))
+        return m3::api_fail(M3_ERR_ARGUMENT, "prologue buffers are NULL");
+    const bool learned = lambda_learned(d->discretization);
+    const float fixed = m3_discretization_fixed_lambda(d->discretization);
+    if (!learned && !(fixed == fixed))
+        return m3::api_fail(M3_ERR_CONFIG, "unknown discretization %d", d->discretization);
+    m3::PrologueLaunch a{};
+    a.tokens = d->tokens;
+    a.heads = d->heads;
+    a.head_dim = d->head_dim;
+    a.d_state = d->d_state;
+    a.rank = d->rank;
+    a.groups = d->groups;
+    a.width = m3_mixer_in_proj_width(d);
+    a.learned_lambda = learned ? 1 : 0;
+    a.fixed_lambda = learned ? 0.0f : fixed;
+    a.has_theta = rot ? 1 : 0;
+    a.norm_eps = d->norm_eps;
+    a.projected = projected;
+    a.dt_bias = dt_bias;
+    a.b_bias = b_bias;
+    a.c_bias = c_bias;
+    a.bc_norm = bc_norm;
+    a.x = x;
+    a.b = b;
+    a.c = c;
+    a.dt = dt;
+    a.lambda = lambda;
+    a.theta = theta;
+    return launched(m3::launch_mixer_prologue(a, as_stream(stream)), "prologue launch");
+}
+
+m3_status m3_mixer_gate(size_t tokens, size_t d_inner, const void *y, const void *z,
+                        size_t z_stride, const float *norm_weight, float eps, void *out,
+                        void *stream) {
+    if (d_inner == 0) return m3::api_fail(M3_ERR_SHAPE, "gate over an empty row");
+    if (z_stride < d_inner)
+        return m3::api_fail(M3_ERR_SHAPE, "z stride %zu is shorter than d_inner %zu", z_stride, d_inner);
+    if (tokens > 0 && (y == nullptr || z == nullptr || out == nullptr))
+        return m3::api_fail(M3_ERR_ARGUMENT, "gate buffers are NULL");
+    return launched(m3::launch_mixer_gate(tokens, d_inner, y, z, z_stride, norm_weight, eps, out,
+                                          as_stream(stream)),
+                    "gate launch");
+}
+
+m3_status m3_embedding_lookup(size_t n, size_t dim, const int32_t *ids, size_t vocab,
+                              const void *table, void *out, void *stream) {
+    if (dim == 0 || vocab == 0) return m3::api_fail(M3_ERR_SHAPE, "empty embedding table");
+    if (n > 0 && (ids == nullptr || table == nullptr || out == nullptr))
+        return m3::api_fail(M3_ERR_ARGUMENT, "embedding buffers are NULL");
+    return launched(m3::launch_embedding(n, dim, ids, vocab, table, out, as_stream(stream)),
+                    "embedding launch");
+}
+
+}  // extern "C"

@@ -73,6 +73,13 @@ class StepInputsC(C.Structure):
 
 
 # Every exported symbol of include/mamba3_ssm.h with its ctypes signature.
+class MixerDimsC(C.Structure):
+    """m3_mixer_dims (mamba3_mixer.h)."""
+    _fields_ = [("tokens", _Z), ("heads", _Z), ("head_dim", _Z), ("d_state", _Z), ("rank", _Z),
+                ("groups", _Z), ("discretization", C.c_int32), ("dynamics", C.c_int32),
+                ("norm_eps", C.c_float)]
+
+
 SIGNATURES = {
     "m3_config_default": (C.c_int, [C.POINTER(SsmConfigC)]),
     "m3_config_validate": (C.c_int, [C.POINTER(SsmConfigC)]),
@@ -90,6 +97,15 @@ SIGNATURES = {
     "m3_last_error": (C.c_char_p, []),
     "m3_launch_count": (C.c_uint64, []),
     "m3_selftest_mfma": (C.c_int, [C.POINTER(C.c_int32)]),
+    # mamba3_mixer.h
+    "m3_rms_norm": (C.c_int, [_Z, _Z, _P, _Z, _P, C.c_float, _P, _Z, _P]),
+    "m3_quantize_int8_columns": (C.c_int, [_Z, _Z, _P, _P, _P, _P]),
+    "m3_linear_workspace_bytes": (_Z, []),
+    "m3_linear": (C.c_int, [_Z, _Z, _Z, _P, _P, _P, _P, _P, _P, _Z, _P]),
+    "m3_mixer_in_proj_width": (_Z, [C.POINTER(MixerDimsC)]),
+    "m3_mixer_prologue": (C.c_int, [C.POINTER(MixerDimsC)] + [_P] * 12),
+    "m3_mixer_gate": (C.c_int, [_Z, _Z, _P, _P, _Z, _P, C.c_float, _P, _P]),
+    "m3_embedding_lookup": (C.c_int, [_Z, _Z, _P, _Z, _P, _P, _P]),
 }
 
 _lib = None

@@ -1,0 +1,182 @@
+"""The Mamba-3 token mixer, bf16 activations, over libmamba3_hip.so.
+
+Mirrors `Mamba3Mixer` (BectorVoom/mamba-trainer src/models/mamba3.rs):
+init (168-266), project (350-466), finish (468-477), apply / apply_with_state
+(479-567) and step (569-630).  The projections are hipBLASLt GEMMs with the
+int8 per-output-channel weight grid applied in their epilogue; the prologue
+(split, silu, B/C bias + RMSNorm, softplus, sigmoid), the scan or the decode
+step, and the gate are the library's own gfx950 kernels.
+
+Not covered (raise UnsupportedError): the causal convolution (conv_kernel),
+the bidirectional form and LoRA adapters.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .error import ShapeError, UnsupportedError
+from .nn import Linear, RmsNorm, _bf16_dev, _stream, normal, residual_scaled
+from .ssm import ScanInputs, SsmConfig, SsmState, StateDynamics, mamba3_scan, mamba3_step_
+
+
+@dataclasses.dataclass
+class MixerCache:
+    """mamba3.rs:35-70 (no convolution history: conv_kernel is None)."""
+    ssm: SsmState
+
+
+@dataclasses.dataclass
+class Projected:
+    """mamba3.rs:278-287, shaped for the scan."""
+    z: torch.Tensor          # [B, T, d_inner] view into the projection (row stride width)
+    projected: torch.Tensor  # [B, T, width] (keeps z's storage)
+    x: torch.Tensor          # [B, T, H, P, R] bf16
+    b: torch.Tensor          # [B, T, H, N, R] bf16
+    c: torch.Tensor
+    dt: torch.Tensor         # [B, T, H] f32
+    lam: torch.Tensor
+    theta: Optional[torch.Tensor]   # [B, T, H, N/2] bf16
+
+
+class Mamba3Mixer:
+    """A Mamba-3 mixer for `[batch, seq, d_model]` bf16 activations."""
+
+    def __init__(self, cfg: SsmConfig, *, device, gen: torch.Generator, n_layers: int = 1,
+                 int8_weights: bool = False):
+        """Mamba3MixerConfig::init (mamba3.rs:168-266), parameters drawn as there
+        from a torch generator (the reference's ChaCha stream is not reproduced)."""
+        cfg.validate()
+        if cfg.conv_kernel is not None:
+            raise UnsupportedError("unsupported: the causal convolution (conv_kernel) is not on "
+                                   "the gfx950 path; use conv_kernel=None")
+        if cfg.bias:
+            raise UnsupportedError("unsupported: projection biases are not on the gfx950 path")
+        self.cfg = cfg
+        H, N = cfg.n_heads, cfg.d_state
+        self.in_proj = Linear(normal((cfg.d_model, cfg.in_proj_width()), 0.02, device, gen),
+                              int8_weights=int8_weights)
+        self.out_proj = Linear(residual_scaled((cfg.d_inner(), cfg.d_model), 0.02, n_layers,
+                                               device, gen), int8_weights=int8_weights)
+        # dt_bias: softplus(dt_bias) log-uniform over [dt_min, dt_max] (mamba3.rs:198-209)
+        u = torch.rand(H, generator=gen, device=device)
+        dt = torch.exp(math.log(cfg.dt_min) + u * (math.log(cfg.dt_max) - math.log(cfg.dt_min)))
+        dt = dt.clamp_min(cfg.dt_init_floor)
+        self.dt_bias = (dt + torch.log(-torch.expm1(-dt))).float()
+        # a_log = ln(U(a_init_min, a_init_max)) (mamba3.rs:211-216)
+        u = torch.rand(H, generator=gen, device=device)
+        a = cfg.a_init_min + u * (cfg.a_init_max - cfg.a_init_min)
+        self.a_log = torch.log(a.clamp_min(1e-4)).float()
+        self.d_skip = torch.ones(H, device=device) if cfg.skip_connection else None
+        self.b_bias = torch.zeros((H, N), device=device) if cfg.bc_bias else None
+        self.c_bias = torch.zeros((H, N), device=device) if cfg.bc_bias else None
+        self.bc_norm = RmsNorm(N, device) if cfg.bc_norm else None
+        self.post_gate_norm = RmsNorm(cfg.d_inner(), device) if cfg.post_gate_norm else None
+
+    # ------------------------------------------------------------ pieces
+    def _dims(self, tokens: int) -> _lib.MixerDimsC:
+        c = self.cfg
+        return _lib.MixerDimsC(tokens, c.n_heads, c.head_dim, c.d_state, c.mode.rank(),
+                               c.n_groups, int(c.discretization), int(c.dynamics),
+                               1e-5 if self.bc_norm is None else self.bc_norm.eps)
+
+    def project(self, input: torch.Tensor) -> Projected:
+        """mamba3.rs:350-466 without the convolution."""
+        c = self.cfg
+        input = _bf16_dev(input, "mixer input")
+        if input.dim() != 3 or input.shape[2] != c.d_model:
+            raise ShapeError(f"shape error: Mamba3Mixer expects d_model={c.d_model}, "
+                             f"got {tuple(input.shape)}")
+        B, T, _ = input.shape
+        H, P, N, R = c.n_heads, c.head_dim, c.d_state, c.mode.rank()
+        projected = self.in_proj.apply(input)
+        dev = input.device
+        x = torch.empty((B, T, H, P, R), dtype=torch.bfloat16, device=dev)
+        b = torch.empty((B, T, H, N, R), dtype=torch.bfloat16, device=dev)
+        cc = torch.empty_like(b)
+        dt = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+        lam = torch.empty_like(dt)
+        rot = c.dynamics == StateDynamics.Rotational
+        theta = torch.empty((B, T, H, N // 2), dtype=torch.bfloat16, device=dev) if rot else None
+        dims = self._dims(B * T)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        _lib.check(_lib.lib().m3_mixer_prologue(
+            C.byref(dims), projected.data_ptr(), self.dt_bias.data_ptr(), ptr(self.b_bias),
+            ptr(self.c_bias), None if self.bc_norm is None else self.bc_norm.weight.data_ptr(),
+            x.data_ptr(), b.data_ptr(), cc.data_ptr(), dt.data_ptr(), lam.data_ptr(), ptr(theta),
+            _stream(input)))
+        return Projected(projected[..., :c.d_inner()], projected, x, b, cc, dt, lam, theta)
+
+    def finish(self, y: torch.Tensor, proj: Projected, residual: Optional[torch.Tensor] = None,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """mamba3.rs:468-477: [post-gate norm] * silu(z), then out_proj; the
+        stack's residual add rides on the projection's epilogue."""
+        c = self.cfg
+        d = c.d_inner()
+        B, T = proj.x.shape[0], proj.x.shape[1]
+        gated = torch.empty((B, T, d), dtype=torch.bfloat16, device=y.device)
+        nw = None if self.post_gate_norm is None else self.post_gate_norm.weight.data_ptr()
+        eps = 1e-5 if self.post_gate_norm is None else self.post_gate_norm.eps
+        _lib.check(_lib.lib().m3_mixer_gate(B * T, d, y.data_ptr(), proj.projected.data_ptr(),
+                                            proj.projected.shape[-1], nw, C.c_float(eps),
+                                            gated.data_ptr(), _stream(y)))
+        return self.out_proj.apply(gated, residual=residual, out=out)
+
+    # ------------------------------------------------------------ entry points
+    def empty_cache(self, batch: int, device) -> MixerCache:
+        c = self.cfg
+        return MixerCache(SsmState.zeros(batch, c.n_heads, c.head_dim, c.d_state,
+                                         c.dynamics == StateDynamics.Rotational, device))
+
+    def apply(self, input: torch.Tensor, residual: Optional[torch.Tensor] = None,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return self.apply_with_state(input, None, residual=residual, out=out)[0]
+
+    def apply_with_state(self, input: torch.Tensor, cache: Optional[MixerCache],
+                         residual: Optional[torch.Tensor] = None,
+                         out: Optional[torch.Tensor] = None):
+        """mamba3.rs:498-567: the mixer over a window; with a cache the scan
+        starts from its state and the boundary state is returned."""
+        proj = self.project(input)
+        si = ScanInputs(proj.x, proj.b, proj.c, proj.dt, self.a_log, proj.lam)
+        si = si.with_chunk_size(self.cfg.chunk_size).with_state_output(cache is not None)
+        if proj.theta is not None:
+            si = si.with_theta(proj.theta)
+        if self.d_skip is not None:
+            si = si.with_skip(self.d_skip)
+        if cache is not None:
+            si = si.with_state(cache.ssm)
+        scan = mamba3_scan(si)
+        y = self.finish(scan.y, proj, residual=residual, out=out)
+        new = MixerCache(scan.state) if cache is not None else None
+        return y, new
+
+    def step_(self, input: torch.Tensor, cache: MixerCache,
+              residual: Optional[torch.Tensor] = None,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """mamba3.rs:569-630 for [batch, 1, d_model], the cache's state updated
+        in place (the reference returns a new cache)."""
+        if input.dim() != 3 or input.shape[1] != 1:
+            raise ShapeError("shape error: step() expects a single position; use "
+                             "apply_with_state for a window")
+        c = self.cfg
+        proj = self.project(input)
+        B = input.shape[0]
+        sq = lambda t: None if t is None else t.reshape((B,) + tuple(t.shape[2:]))
+        y = mamba3_step_(sq(proj.x), sq(proj.b), sq(proj.c), sq(proj.dt), sq(proj.lam),
+                         self.a_log, sq(proj.theta), self.d_skip, cache.ssm)
+        return self.finish(y.reshape(proj.x.shape), proj, residual=residual, out=out)
+
+    def step(self, input: torch.Tensor, cache: MixerCache):
+        """mamba3.rs:569-630: returns (output, new cache) like the reference."""
+        new = MixerCache(cache.ssm.clone())
+        if new.ssm.angle is None and self.cfg.dynamics == StateDynamics.Rotational:
+            B = input.shape[0]
+            new.ssm.angle = torch.zeros((B, self.cfg.n_heads, self.cfg.d_state // 2),
+                                        dtype=torch.float32, device=input.device)
+        return self.step_(input, new), new

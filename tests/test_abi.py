@@ -11,20 +11,23 @@ import pytest
 
 from conftest import ROOT
 
-HEADER = os.path.join(ROOT, "include", "mamba3_ssm.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
 
 
 def declared_symbols():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(m3_[a-z0-9_]+)\s*\(", text)))
+    syms = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        syms.update(re.findall(r"\b(m3_[a-z0-9_]+)\s*\(", text))
+    return sorted(syms)
 
 
 def test_library_exports_every_declared_symbol():
     from mamba3 import _lib
     L = _lib.lib()
     syms = declared_symbols()
-    assert len(syms) >= 15
+    assert len(syms) >= 24
     missing = [s for s in syms if not hasattr(L, s)]
     assert not missing, f"declared but not exported: {missing}"
     # and the Python binding declares a signature for each of them
