@@ -13,6 +13,8 @@ Also reported on the same line:
   roofline       the scan call's algorithmic bytes (its inputs and outputs)
                  over the average duration of one call (HIP events on the launch
                  stream), against the 8 TB/s HBM peak, plus its MFMA fraction;
+  prefill        BASELINE config 4: the whole Mamba3Lm prefill (B=16, L=2048,
+                 24 layers, int8 projections): tokens/s and matrix TFLOP/s;
   decode         BASELINE config 3: one token for 256 sequences through
                  24 layers x 24 heads (P=64, N=128) of f32 state cache, in place,
                  timed over consecutive steps: us per step, GB/s, fraction of HBM peak;
@@ -138,6 +140,59 @@ def bench_scan(torch, lib, L_, args, chunk_parallel=True, inp=None):
                 workspace_bytes=0 if ws is None else ws.numel())
 
 
+# Mamba3Lm prefill (next-row workload, reported beside the headline)
+PREFILL = dict(B=16, L=2048, vocab=32000, d_model=768, layers=24, H=12, P=64, N=128, G=12)
+
+
+def prefill_flops(p):
+    """Matrix FLOPs of one prefill: per layer in_proj and out_proj, then the head
+    (the scan's own MFMA work is counted in scan_algorithmic)."""
+    d, H, P, N, G = p["d_model"], p["H"], p["P"], p["N"], p["G"]
+    din = H * P
+    width = 2 * din + 2 * G * N + H + H + H * N // 2
+    m = p["B"] * p["L"]
+    per_layer = 2 * m * d * width + 2 * m * din * d
+    return per_layer * p["layers"] + 2 * m * d * p["vocab"]
+
+
+def bench_prefill(torch, args):
+    """Config 4 end to end: embedding, 24 x (RMSNorm, int8 in_proj, prologue,
+    scan, gate, int8 out_proj + residual), final norm, head; random init."""
+    from mamba3 import Discretization, SsmConfig, SsmMode, StateDynamics
+    from mamba3.lm import Mamba3Lm, Mamba3LmConfig
+    p = PREFILL
+    dev = "cuda:0"
+    ssm = SsmConfig(d_model=p["d_model"], n_heads=p["H"], head_dim=p["P"], d_state=p["N"],
+                    n_groups=p["G"], discretization=Discretization.LearnedTrapezoid,
+                    dynamics=StateDynamics.Rotational, mode=SsmMode(1), chunk_size=64,
+                    conv_kernel=None, bc_norm=True)
+    lm = Mamba3Lm(Mamba3LmConfig(vocab_size=p["vocab"], d_model=p["d_model"],
+                                 n_layers=p["layers"], ssm=ssm, int8_weights=True, seed=4), dev)
+    g = torch.Generator(device=dev).manual_seed(0x4D414D46)
+    ids = torch.randint(0, p["vocab"], (p["B"], p["L"]), device=dev, generator=g)
+    for _ in range(2):
+        logits = lm.forward(ids)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.prefill_steps):
+        logits = lm.forward(ids)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.prefill_steps
+    assert torch.isfinite(logits[0, :4].float()).all(), "non-finite logits"
+    flops = prefill_flops(p)
+    toks = p["B"] * p["L"]
+    return {"workload": "config 4: Mamba3Lm prefill B=16 L=2048, vocab 32000, d_model 768, "
+                        "24 layers x 12 heads x 64, N 128, groups 12, bc_norm, no conv, int8 "
+                        "per-output-channel fake-quant projections, bf16 activations",
+            "tokens_per_s": round(toks / (ms * 1e-3), 1), "ms_per_prefill": round(ms, 3),
+            "matrix_tflop": round(flops / 1e12, 3),
+            "matrix_tflops_achieved": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_bf16_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+
+
 def bench_decode(torch, lib, L_, args):
     dev = "cuda:0"
     d = DECODE
@@ -240,6 +295,8 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--decode-warmup", type=int, default=8)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill leg")
+    ap.add_argument("--prefill-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -287,6 +344,7 @@ def main():
     value = sc["tokens"] / (ms_step * 1e-3)
 
     dec = None if args.no_decode else bench_decode(torch, lib, L_, args)
+    pre = None if args.no_prefill else bench_prefill(torch, args)
     cpu = None if args.no_cpu else cpu_baseline(args)
 
     line = {
@@ -319,6 +377,7 @@ def main():
                      "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)},
         "scan_single_pass_us": round(sc1["kernel_ms"] * 1e3, 2),
         "decode": dec,
+        "prefill": pre,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
