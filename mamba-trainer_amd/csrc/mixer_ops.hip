@@ -159,6 +159,129 @@ mixer_prologue_kernel(PrologueLaunch a) {
     }
 }
 
+// ---------------------------------------------------------------- prologue, 16-byte path
+// The same prologue with every piece moved as 16-byte vectors of eight bf16.
+// Needs d_state a multiple of 8 with d_state / 8 dividing 64, d_inner and the
+// row width multiples of 8 and 16-byte aligned buffers (the host checks).
+// Then theta's offset in the row, 2*d_inner + 2*G*R*N + H or 2H, is a multiple
+// of 8 as well: the width is that offset plus H*N/2, which is 0 or 4 mod 8
+// (4 only for odd H), and H or 2H is never 4 mod 8 for odd H.
+// One workgroup per token walks a flat list of vector items:
+//   [0, 2*H*lq)        B then C: head h, state lanes q = 0..lq-1 (lq = N/8),
+//                      each lane holding eight states of every rank;
+//   [.., + din/8)      x;
+//   [.., + H*N/16)     theta, copied.
+// A (B|C, head) row's lq lanes are consecutive and lq-aligned, so the RMSNorm
+// sum over the state axis is a reduction over those lanes.  The rank-last
+// output of a lane is the 8 x R block of states q*8.. of all ranks: R whole
+// vectors.  silu uses exp(-v) = 2^(-v log2 e) on v_exp_f32 and v_rcp_f32,
+// within a few f32 ulps of the exact value, below bf16 rounding.
+__device__ __forceinline__ float silu_fast(float v) {
+    const float e = __builtin_amdgcn_exp2f(-v * 1.4426950408889634f);
+    return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+__device__ __forceinline__ void unpack8(const uint4 q, float *f) {
+    const unsigned int u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = __uint_as_float(u[j] << 16);
+        f[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
+    }
+}
+
+__device__ __forceinline__ unsigned int pack2(float a, float b) {
+    return static_cast<unsigned int>(to_bits(a)) | (static_cast<unsigned int>(to_bits(b)) << 16);
+}
+
+template <int R>
+__global__ void __launch_bounds__(256)
+mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
+    const size_t t = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int H = static_cast<int>(a.heads), N = static_cast<int>(a.d_state);
+    const int din = static_cast<int>(a.heads * a.head_dim) * R;
+    const int bcw = static_cast<int>(a.groups) * R * N;
+    const int per_group = H / static_cast<int>(a.groups);
+    const uint16_t *__restrict__ row = static_cast<const uint16_t *>(a.projected) + t * a.width;
+    const uint16_t *px = row + din;
+    const uint16_t *pb = px + din;
+    const uint16_t *pc = pb + bcw;
+    const uint16_t *pdt = pc + bcw;
+    const uint16_t *plam = pdt + H;
+    const uint16_t *pth = plam + (a.learned_lambda ? H : 0);
+    const int nbc = 2 * H * lq;
+    const int nx = din / 8;
+    const int thw = a.has_theta ? H * (N / 2) : 0;
+    const int total = nbc + nx + thw / 8;
+
+    for (int i = tid; i < total; i += 256) {
+        if (i < nbc) {
+            const int u = i / lq, q = i - u * lq;
+            const int which = u >= H ? 1 : 0;
+            const int h = u - which * H;
+            const uint16_t *s = (which ? pc : pb) + (h / per_group) * R * N + q * 8;
+            const float *bias = which ? a.c_bias : a.b_bias;
+            float v[R][8];
+#pragma unroll
+            for (int r = 0; r < R; ++r) unpack8(*reinterpret_cast<const uint4 *>(s + r * N), v[r]);
+            float bb[8];
+            if (bias) {
+                const float4 b0 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8);
+                const float4 b1 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8 + 4);
+                bb[0] = b0.x; bb[1] = b0.y; bb[2] = b0.z; bb[3] = b0.w;
+                bb[4] = b1.x; bb[5] = b1.y; bb[6] = b1.z; bb[7] = b1.w;
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[r][j] = silu_fast(v[r][j]) + (bias ? bb[j] : 0.0f);
+            if (a.bc_norm) {
+                const float4 w0 = *reinterpret_cast<const float4 *>(a.bc_norm + q * 8);
+                const float4 w1 = *reinterpret_cast<const float4 *>(a.bc_norm + q * 8 + 4);
+                const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) ss += v[r][j] * v[r][j];
+                    ss = group_sum(ss, lq);
+                    const float scale = 1.0f / sqrtf(ss / static_cast<float>(N) + a.norm_eps);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[r][j] = v[r][j] * scale * w[j];
+                }
+            }
+            uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(which ? a.c : a.b) +
+                                                   ((t * H + h) * N + q * 8) * R);
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                unsigned int o[4];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int e0 = 8 * k + 2 * m, e1 = e0 + 1;     // element e = j * R + r
+                    o[m] = pack2(v[e0 % R][e0 / R], v[e1 % R][e1 / R]);
+                }
+                dst[k] = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        } else if (i < nbc + nx) {
+            const int k = i - nbc;
+            float f[8];
+            unpack8(*reinterpret_cast<const uint4 *>(px + k * 8), f);
+            uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.x) + t * din) + k;
+            *dst = make_uint4(pack2(silu_fast(f[0]), silu_fast(f[1])), pack2(silu_fast(f[2]), silu_fast(f[3])),
+                              pack2(silu_fast(f[4]), silu_fast(f[5])), pack2(silu_fast(f[6]), silu_fast(f[7])));
+        } else {
+            const int k = (i - nbc - nx) * 8;
+            uint16_t *to = static_cast<uint16_t *>(a.theta) + t * thw;
+            *reinterpret_cast<uint4 *>(to + k) = *reinterpret_cast<const uint4 *>(pth + k);
+        }
+    }
+    for (int h = tid; h < H; h += 256) {
+        a.dt[t * H + h] = softplusf_(bf(pdt, h) + a.dt_bias[h]);
+        a.lambda[t * H + h] = a.learned_lambda ? sigmoidf_(bf(plam, h)) : a.fixed_lambda;
+    }
+}
+
 // ---------------------------------------------------------------- gate
 // out = [RMSNorm(y)] * silu(z) over rows of d_inner (mamba3.rs:468-477); one
 // wave per token.
@@ -185,6 +308,44 @@ mixer_gate_kernel(size_t tokens, size_t d, const uint16_t *y, const uint16_t *z,
         float v = bf(yr, i);
         if (nw) v = v * scale * nw[i];
         orow[i] = to_bits(v * siluf_(bf(zr, i)));
+    }
+}
+
+// The gate with 16-byte vectors: d_inner and the z stride multiples of 8,
+// 16-byte aligned buffers (the host checks).  One wave per token.
+__global__ void __launch_bounds__(256)
+mixer_gate_vec_kernel(size_t tokens, size_t d, const uint16_t *y, const uint16_t *z, size_t zs,
+                      const float *nw, float eps, uint16_t *out) {
+    const size_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= tokens) return;
+    const uint16_t *yr = y + t * d;
+    const uint16_t *zr = z + t * zs;
+    uint16_t *orow = out + t * d;
+    float scale = 1.0f;
+    if (nw) {
+        float ss = 0.0f;
+        for (size_t i = lane * 8; i < d; i += 512) {
+            float f[8];
+            unpack8(*reinterpret_cast<const uint4 *>(yr + i), f);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+        }
+        ss = group_sum(ss, 64);
+        scale = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+    }
+    for (size_t i = lane * 8; i < d; i += 512) {
+        float f[8], g[8];
+        unpack8(*reinterpret_cast<const uint4 *>(yr + i), f);
+        unpack8(*reinterpret_cast<const uint4 *>(zr + i), g);
+        if (nw) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = f[j] * scale * nw[i + j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] *= silu_fast(g[j]);
+        *reinterpret_cast<uint4 *>(orow + i) =
+            make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
     }
 }
 
@@ -232,10 +393,28 @@ hipError_t launch_quantize_columns(size_t k, size_t n, const float *w, void *cod
     return hipGetLastError();
 }
 
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 hipError_t launch_mixer_prologue(const PrologueLaunch &a, hipStream_t s) {
     if (a.tokens == 0) return hipSuccess;
-    hipLaunchKernelGGL(mixer_prologue_kernel, dim3(static_cast<unsigned int>(a.tokens)), dim3(256), 0, s,
-                       a);
+    const dim3 grid(static_cast<unsigned int>(a.tokens));
+    const size_t N = a.d_state, din = a.heads * a.head_dim * a.rank;
+    const size_t lq = N / 8;
+    const bool vec = N % 8 == 0 && lq >= 1 && lq <= 64 && (lq & (lq - 1)) == 0 && din % 8 == 0 &&
+                     a.width % 8 == 0 && (a.rank == 1 || a.rank == 2 || a.rank == 4) &&
+                     aligned16(a.projected) && aligned16(a.x) && aligned16(a.b) && aligned16(a.c) &&
+                     aligned16(a.b_bias) && aligned16(a.c_bias) && aligned16(a.bc_norm) &&
+                     aligned16(a.theta) && a.width < (1u << 30);
+    if (!vec) {
+        hipLaunchKernelGGL(mixer_prologue_kernel, grid, dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
+    const int l = static_cast<int>(lq);
+    switch (a.rank) {
+    case 1: hipLaunchKernelGGL(mixer_prologue_vec_kernel<1>, grid, dim3(256), 0, s, a, l); break;
+    case 2: hipLaunchKernelGGL(mixer_prologue_vec_kernel<2>, grid, dim3(256), 0, s, a, l); break;
+    default: hipLaunchKernelGGL(mixer_prologue_vec_kernel<4>, grid, dim3(256), 0, s, a, l); break;
+    }
     return hipGetLastError();
 }
 
@@ -243,6 +422,13 @@ hipError_t launch_mixer_gate(size_t tokens, size_t d_inner, const void *y, const
                              size_t z_stride, const float *norm_w, float eps, void *out,
                              hipStream_t s) {
     if (tokens == 0) return hipSuccess;
+    if (d_inner % 8 == 0 && z_stride % 8 == 0 && aligned16(y) && aligned16(z) && aligned16(out) &&
+        aligned16(norm_w)) {
+        hipLaunchKernelGGL(mixer_gate_vec_kernel, dim3(blocks(tokens, 4)), dim3(256), 0, s, tokens,
+                           d_inner, static_cast<const uint16_t *>(y), static_cast<const uint16_t *>(z),
+                           z_stride, norm_w, eps, static_cast<uint16_t *>(out));
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(mixer_gate_kernel, dim3(blocks(tokens, 4)), dim3(256), 0, s, tokens, d_inner,
                        static_cast<const uint16_t *>(y), static_cast<const uint16_t *>(z), z_stride,
                        norm_w, eps, static_cast<uint16_t *>(out));

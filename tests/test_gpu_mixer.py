@@ -92,11 +92,16 @@ def test_linear_against_f64(m, k, n, int8, resid):
     assert rel_l2(host(y), ref) <= 1e-2
 
 
-@pytest.mark.parametrize("H,G,P,N,R,learned,rot", [(4, 2, 4, 8, 1, True, True),
-                                                   (12, 12, 64, 128, 1, True, True),
-                                                   (2, 1, 4, 4, 2, False, False),
-                                                   (4, 4, 16, 32, 4, True, True)])
-def test_prologue_against_oracle(H, G, P, N, R, learned, rot):
+# The first, second, fourth and fifth shapes take the 16-byte path (ranks 1, 4
+# and 2); the third (d_state 4) and the last (width 2*8*3 + 2*3*8 + 3 + 12, not
+# a multiple of 8) take the element-wise one.  `plain` drops biases and norm.
+@pytest.mark.parametrize("H,G,P,N,R,learned,rot,plain", [(4, 2, 4, 8, 1, True, True, False),
+                                                         (12, 12, 64, 128, 1, True, True, False),
+                                                         (2, 1, 4, 4, 2, False, False, False),
+                                                         (4, 4, 16, 32, 4, True, True, False),
+                                                         (8, 4, 8, 64, 2, False, False, True),
+                                                         (3, 3, 8, 8, 1, False, True, True)])
+def test_prologue_against_oracle(H, G, P, N, R, learned, rot, plain):
     import ctypes as C
     from mamba3 import Discretization, StateDynamics
     rng = np.random.default_rng(H * N + R)
@@ -110,6 +115,8 @@ def test_prologue_against_oracle(H, G, P, N, R, learned, rot):
              b_bias=rng.normal(0, 0.3, (H, N)).astype(np.float32),
              c_bias=rng.normal(0, 0.3, (H, N)).astype(np.float32),
              bc_norm=rng.uniform(0.5, 1.5, N).astype(np.float32))
+    if plain:
+        p.update(b_bias=None, c_bias=None, bc_norm=None)
     ref = mo.mixer_project(proj, cfg, p, rnd=True)
     L = lib()
     disc = Discretization.LearnedTrapezoid if learned else Discretization.Trapezoid
@@ -125,7 +132,8 @@ def test_prologue_against_oracle(H, G, P, N, R, learned, rot):
     keep = [t_f32(p[k]) for k in ("dt_bias", "b_bias", "c_bias", "bc_norm")]
     projd = t_bf16(proj)                              # held until the launch has run
     L.check(L.lib().m3_mixer_prologue(C.byref(dims), projd.data_ptr(),
-                                      *[k.data_ptr() for k in keep], x.data_ptr(), b.data_ptr(),
+                                      *[None if k is None else k.data_ptr() for k in keep],
+                                      x.data_ptr(), b.data_ptr(),
                                       c.data_ptr(), dt.data_ptr(), lam.data_ptr(),
                                       None if th is None else th.data_ptr(), None))
     torch.cuda.synchronize()
@@ -138,11 +146,13 @@ def test_prologue_against_oracle(H, G, P, N, R, learned, rot):
         assert np.array_equal(host(th), ref["theta"])
 
 
+# z stride 200 takes the 16-byte path, 201 the element-wise one.
+@pytest.mark.parametrize("zs", [200, 201])
 @pytest.mark.parametrize("norm", [False, True])
-def test_gate_against_oracle(norm):
+def test_gate_against_oracle(norm, zs):
     import ctypes as C
     rng = np.random.default_rng(11 + norm)
-    T, d, zs = 29, 96, 200
+    T, d = 29, 96
     y = mo.bf16(rng.normal(0, 1, (T, d)))
     z = mo.bf16(rng.normal(0, 2, (T, zs)))
     w = rng.uniform(0.5, 1.5, d) if norm else None
