@@ -18,6 +18,9 @@ Also reported on the same line:
   decode         BASELINE config 3: one token for 256 sequences through
                  24 layers x 24 heads (P=64, N=128) of f32 state cache, in place,
                  timed over consecutive steps: us per step, GB/s, fraction of HBM peak;
+  decode_lm      the whole Mamba3Lm decode step around it (d_model 1536, int8
+                 projections, head): us per step, tokens/s, GB/s over the state,
+                 weight and logit bytes;
   cpu_baseline   the CPU restatement of the reference's composed algorithm
                  (oracle/, OpenMP) on the same config-1 workload, on the host.
 
@@ -140,6 +143,14 @@ def bench_scan(torch, lib, L_, args, chunk_parallel=True, inp=None):
                 workspace_bytes=0 if ws is None else ws.numel())
 
 
+def _pause_for_trace(args):
+    """With --only, a 0.5 s idle gap separates a leg's warm-up (weight
+    quantisation, GEMM plan probes) from its timed passes, so a kernel trace
+    can tell them apart."""
+    if args.only:
+        time.sleep(0.5)
+
+
 # BASELINE config 4: Mamba3Lm prefill (next-row workload, reported beside the headline)
 PREFILL = dict(B=16, L=2048, vocab=32000, d_model=768, layers=24, H=12, P=64, N=128, G=12)
 
@@ -173,6 +184,7 @@ def bench_prefill(torch, args):
     for _ in range(2):
         logits = lm.forward(ids)
     torch.cuda.synchronize()
+    _pause_for_trace(args)
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
@@ -191,6 +203,59 @@ def bench_prefill(torch, args):
             "matrix_tflop": round(flops / 1e12, 3),
             "matrix_tflops_achieved": round(flops / (ms * 1e-3) / 1e12, 1),
             "frac_bf16_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+
+
+# Row (f2): the whole Mamba3Lm decode step at config 3's mixer shapes
+DECODE_LM = dict(B=256, vocab=32000, d_model=1536, layers=24, H=24, P=64, N=128, G=24)
+
+
+def bench_decode_lm(torch, args):
+    """One token per sequence through the 24-layer stack with the state cache
+    updated in place: embedding, 24 x (RMSNorm, int8 in_proj, prologue, decode
+    step, gate, int8 out_proj + residual), final norm, head (lm.rs:337-353)."""
+    from mamba3 import Discretization, SsmConfig, SsmMode, StateDynamics
+    from mamba3.lm import Mamba3Lm, Mamba3LmConfig
+    p = DECODE_LM
+    dev = "cuda:0"
+    B, H, P, N = p["B"], p["H"], p["P"], p["N"]
+    ssm = SsmConfig(d_model=p["d_model"], n_heads=H, head_dim=P, d_state=N, n_groups=p["G"],
+                    discretization=Discretization.LearnedTrapezoid,
+                    dynamics=StateDynamics.Rotational, mode=SsmMode(1), chunk_size=64,
+                    conv_kernel=None, bc_norm=True)
+    lm = Mamba3Lm(Mamba3LmConfig(vocab_size=p["vocab"], d_model=p["d_model"],
+                                 n_layers=p["layers"], ssm=ssm, int8_weights=True, seed=5), dev)
+    g = torch.Generator(device=dev).manual_seed(0x4D414D47)
+    cache = lm.empty_cache(B, dev)
+    for c in cache:                        # config 3's state: N(0, 0.1), angles U(-pi, pi)
+        c.ssm.h.normal_(0.0, 0.1, generator=g)
+        c.ssm.last_u.normal_(0.0, 0.1, generator=g)
+        c.ssm.angle.uniform_(-math.pi, math.pi, generator=g)
+    ids = torch.randint(0, p["vocab"], (16, B, 1), device=dev, generator=g)
+    for i in range(4):
+        logits = lm.forward_cached(ids[i], cache)
+    torch.cuda.synchronize()
+    _pause_for_trace(args)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    steps = args.decode_lm_steps
+    e0.record(stream)
+    for i in range(steps):
+        logits = lm.forward_cached(ids[i % 16], cache)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    assert torch.isfinite(logits.float()).all(), "non-finite logits"
+    d, NL = p["d_model"], p["layers"]
+    width = ssm.in_proj_width()
+    weights = NL * (d * width * 2 + width * 4 + d * d * 2 + d * 4) + d * p["vocab"] * 2
+    nbytes = NL * decode_algorithmic(B, H, P, N, 1) + weights + B * p["vocab"] * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": "Mamba3Lm decode step, batch 256 x 1 token, vocab 32000, d_model 1536, "
+                        "24 layers x 24 heads x 64, N 128, groups 24, bc_norm, no conv, int8 "
+                        "per-output-channel fake-quant projections, f32 state cache in place",
+            "us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(B / (ms * 1e-3), 1),
+            "bytes_per_step": nbytes, "achieved_GBps": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "steps": steps}
 
 
 def bench_decode(torch, lib, L_, args):
@@ -297,9 +362,13 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill leg")
     ap.add_argument("--prefill-steps", type=int, default=5)
+    ap.add_argument("--no-decode-lm", action="store_true", help="skip the LM decode-step leg")
+    ap.add_argument("--decode-lm-steps", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--only", choices=("prefill", "decode_lm"), default=None,
+                    help="run one model leg alone and print its object (for kernel traces)")
     ap.add_argument("--scan-only", action="store_true",
                     help="run only the headline scan --steps times (for counter runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -329,6 +398,10 @@ def main():
     lib = L_.lib()
 
     torch.cuda.synchronize()
+    if args.only:
+        leg = bench_prefill(torch, args) if args.only == "prefill" else bench_decode_lm(torch, args)
+        print(json.dumps({args.only: leg}), flush=True)
+        return
     if args.scan_only:
         sc = bench_scan(torch, lib, L_, args, chunk_parallel=True)
         print(json.dumps({"scan_us": round(sc["kernel_ms"] * 1e3, 2)}), flush=True)
@@ -345,6 +418,7 @@ def main():
 
     dec = None if args.no_decode else bench_decode(torch, lib, L_, args)
     pre = None if args.no_prefill else bench_prefill(torch, args)
+    dlm = None if args.no_decode_lm else bench_decode_lm(torch, args)
     cpu = None if args.no_cpu else cpu_baseline(args)
 
     line = {
@@ -378,6 +452,7 @@ def main():
         "scan_single_pass_us": round(sc1["kernel_ms"] * 1e3, 2),
         "decode": dec,
         "prefill": pre,
+        "decode_lm": dlm,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -53,7 +53,13 @@ m3_status m3_quantize_int8_columns(size_t in_features, size_t out_features, cons
 /* y[m, n] = (x[m, k] @ w[k, n]) * col_scale[n] + residual[m, n], bf16 with f32
  * accumulation (hipBLASLt).  col_scale and residual may be NULL; residual may
  * alias y.  The workspace (up to m3_linear_workspace_bytes(), 256-byte
- * aligned, or NULL) widens the kernels hipBLASLt may pick. */
+ * aligned, or NULL) widens the kernels hipBLASLt may pick.  The first call
+ * for a (m, k, n, scaled, workspace) shape times hipBLASLt's candidate
+ * algorithms on the caller's inputs into a scratch output it allocates and
+ * frees, and blocks on `stream` once; later calls are asynchronous.  The
+ * reference tunes its matmul plans once per shape the same way
+ * (src/tensor/matmul.rs:1636-1943).  M3_LINEAR_TUNE=0 in the environment
+ * keeps hipBLASLt's first choice instead. */
 size_t m3_linear_workspace_bytes(void);
 m3_status m3_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
                     const float *col_scale, const void *residual, void *y, void *workspace,

@@ -8,12 +8,25 @@
 // Row-major y = x w is column-major D = W X with D (N x M), W (N x K) and
 // X (K x M), so the output channels are D's rows and the scale vector is
 // hipBLASLt's per-row alpha vector.
+//
+// Plan choice follows the reference's tuned plans (tensor/matmul.rs:1636-1943:
+// timing probes once per shape): the first call for a shape asks hipBLASLt's
+// heuristic for up to kCandidates algorithms, runs each a few times on the
+// caller's data into a scratch output (the caller's buffers, including an
+// in-place residual, are left untouched), keeps the fastest and blocks on the
+// stream once to read the timings.  Later calls with the shape launch the kept
+// plan asynchronously.  M3_LINEAR_TUNE=0 keeps the heuristic's first choice
+// (no probe, no blocking), for runs that must pick the same algorithm in
+// every process.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <vector>
 
 #include "m3_internal.hpp"
 
@@ -21,10 +34,14 @@ namespace m3 {
 
 namespace {
 
+constexpr int kCandidates = 8;
+constexpr int kProbeRuns = 3;
+
 struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
     hipblasLtMatmulAlgo_t algo{};
+    std::vector<hipblasLtMatmulAlgo_t> candidates;
     bool ok = false;
 };
 
@@ -59,20 +76,67 @@ bool build_plan(hipblasLtHandle_t h, size_t m, size_t k, size_t n, bool scaled, 
     uint64_t wsb = ws;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
                                           sizeof(wsb));
-    hipblasLtMatmulHeuristicResult_t res[4];
+    hipblasLtMatmulHeuristicResult_t res[kCandidates];
     int count = 0;
     const hipblasStatus_t st =
-        hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.c, p.c, pref, 4, res, &count);
+        hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.c, p.c, pref, kCandidates, res, &count);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (st != HIPBLAS_STATUS_SUCCESS || count == 0) return false;
-    for (int i = 0; i < count; ++i) {
-        if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws) {
-            p.algo = res[i].algo;
-            p.ok = true;
-            return true;
-        }
+    for (int i = 0; i < count; ++i)
+        if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws)
+            p.candidates.push_back(res[i].algo);
+    if (p.candidates.empty()) return false;
+    p.algo = p.candidates.front();
+    p.ok = true;
+    return true;
+}
+
+bool tuning_enabled() {
+    const char *v = std::getenv("M3_LINEAR_TUNE");
+    return v == nullptr || std::strcmp(v, "0") != 0;
+}
+
+// Times every candidate of `p` (kProbeRuns runs after one warm-up each) with
+// beta = 0 into a scratch [m, n] output and keeps the fastest.  Any failure
+// leaves the heuristic's first choice in place.
+void tune_plan(hipblasLtHandle_t h, size_t m, size_t n, Plan &p, const void *alpha, const void *w,
+               const void *x, void *workspace, size_t ws, hipStream_t s) {
+    if (p.candidates.size() < 2) return;
+    void *scratch = nullptr;
+    if (hipMalloc(&scratch, m * n * 2) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
     }
-    return false;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+        const float zero = 0.0f;
+        float best = 0.0f;
+        size_t pick = 0;
+        bool any = false;
+        for (size_t i = 0; i < p.candidates.size(); ++i) {
+            auto run = [&]() {
+                return hipblasLtMatmul(h, p.desc, alpha, w, p.a, x, p.b, &zero, scratch, p.c, scratch,
+                                       p.c, &p.candidates[i], workspace, ws, s);
+            };
+            if (run() != HIPBLAS_STATUS_SUCCESS) continue;
+            bool ok = hipEventRecord(e0, s) == hipSuccess;
+            for (int r = 0; ok && r < kProbeRuns; ++r) ok = run() == HIPBLAS_STATUS_SUCCESS;
+            ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+            float ms = 0.0f;
+            if (!ok || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) continue;
+            if (!any || ms < best) {
+                best = ms;
+                pick = i;
+                any = true;
+            }
+        }
+        if (any) p.algo = p.candidates[pick];
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(scratch);
+    (void)hipGetLastError();
 }
 
 }  // namespace
@@ -98,9 +162,12 @@ hipError_t launch_linear(size_t m, size_t k, size_t n, const void *x, const void
         handle = d.handle;
         auto key = std::make_tuple(m, k, n, scaled, ws);
         auto it = d.plans.find(key);
+        const float one = 1.0f;
+        const void *alpha = scaled ? static_cast<const void *>(col_scale) : static_cast<const void *>(&one);
         if (it == d.plans.end()) {
             Plan p;
             if (!build_plan(handle, m, k, n, scaled, ws, p)) return hipErrorNotSupported;
+            if (tuning_enabled()) tune_plan(handle, m, n, p, alpha, w, x, workspace, ws, s);
             it = d.plans.emplace(key, p).first;
         }
         plan = &it->second;
