@@ -30,6 +30,7 @@ BASELINE.json).  `--gpus N` with N > 1 exits: this build measures one GPU.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import ctypes as C
 import json
 import math
@@ -205,6 +206,59 @@ def bench_prefill(torch, args):
             "frac_bf16_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
 
 
+def bench_ingest(torch, args):
+    """Row (f4): a checkpoint of config 4's model in the reference's JSON format
+    written, parsed and restored (checkpoint.rs:54-83, module.rs:249-285); the
+    parse is timed beside Python's json module on one layer's in_proj."""
+    import json as _json
+    import tempfile
+    from mamba3 import Discretization, SsmConfig, SsmMode, StateDynamics
+    from mamba3.checkpoint import Checkpoint
+    from mamba3.lm import Mamba3Lm, Mamba3LmConfig
+    p = PREFILL
+    dev = "cuda:0"
+    ssm = SsmConfig(d_model=p["d_model"], n_heads=p["H"], head_dim=p["P"], d_state=p["N"],
+                    n_groups=p["G"], discretization=Discretization.LearnedTrapezoid,
+                    dynamics=StateDynamics.Rotational, mode=SsmMode(1), chunk_size=64,
+                    conv_kernel=None, bc_norm=True)
+    cfg = Mamba3LmConfig(vocab_size=p["vocab"], d_model=p["d_model"], n_layers=p["layers"],
+                         ssm=ssm, int8_weights=True, seed=6)
+    src = Mamba3Lm(cfg, dev)
+    ck = Checkpoint.capture(src, 1).with_metadata({"d_model": p["d_model"]})
+    values = ck.num_values()
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "config4.json")
+        t0 = time.perf_counter()
+        ck.save(path)
+        t_save = time.perf_counter() - t0
+        nbytes = os.path.getsize(path)
+        t0 = time.perf_counter()
+        loaded = Checkpoint.load(path)
+        t_load = time.perf_counter() - t0
+        dst = Mamba3Lm(dataclasses.replace(cfg, seed=7), dev)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loaded.restore(dst, strict=True)
+        torch.cuda.synchronize()
+        t_restore = time.perf_counter() - t0
+        ids = torch.randint(0, p["vocab"], (1, 64), device=dev)
+        same = bool(torch.equal(src.forward(ids), dst.forward(ids)))
+        # Python's json on one layer's in_proj (a bounded sample of the same text)
+        e = loaded.state.entries["stack.layers.0.mixer.in_proj.weight"]
+        sample = _json.dumps({"entries": {"w": {"shape": e.shape, "data": e.data.tolist()}}})
+        t0 = time.perf_counter()
+        _json.loads(sample)
+        t_py = time.perf_counter() - t0
+    return {"workload": "config-4 Mamba3Lm checkpoint (24 layers, vocab 32000, d_model 768) in "
+                        "the reference's JSON format",
+            "values": values, "file_MB": round(nbytes / 1e6, 1),
+            "save_s": round(t_save, 3), "load_s": round(t_load, 3),
+            "load_MBps": round(nbytes / 1e6 / t_load, 1), "restore_s": round(t_restore, 3),
+            "restored_logits_identical": same, "threads": min(os.cpu_count() or 1, 16),
+            "python_json_MBps": round(len(sample) / 1e6 / t_py, 1),
+            "python_json_sample": "one layer's in_proj (4.1 M values) through json.loads"}
+
+
 # Row (f2): the whole Mamba3Lm decode step at config 3's mixer shapes
 DECODE_LM = dict(B=256, vocab=32000, d_model=1536, layers=24, H=24, P=64, N=128, G=24)
 
@@ -367,7 +421,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-reps", type=int, default=3)
-    ap.add_argument("--only", choices=("prefill", "decode_lm"), default=None,
+    ap.add_argument("--only", choices=("prefill", "decode_lm", "ingest"), default=None,
                     help="run one model leg alone and print its object (for kernel traces)")
     ap.add_argument("--scan-only", action="store_true",
                     help="run only the headline scan --steps times (for counter runs)")
@@ -399,7 +453,8 @@ def main():
 
     torch.cuda.synchronize()
     if args.only:
-        leg = bench_prefill(torch, args) if args.only == "prefill" else bench_decode_lm(torch, args)
+        leg = {"prefill": bench_prefill, "decode_lm": bench_decode_lm,
+               "ingest": bench_ingest}[args.only](torch, args)
         print(json.dumps({args.only: leg}), flush=True)
         return
     if args.scan_only:

@@ -50,7 +50,10 @@ typedef enum m3_status {
     M3_ERR_RANK = 3,         /* Error::Rank        */
     M3_ERR_UNSUPPORTED = 4,  /* Error::Unsupported */
     M3_ERR_HIP = 5,
-    M3_ERR_ARGUMENT = 6
+    M3_ERR_ARGUMENT = 6,
+    M3_ERR_STATE_DICT = 7,   /* Error::StateDict   */
+    M3_ERR_IO = 8,           /* Error::Io          */
+    M3_ERR_JSON = 9          /* Error::Json        */
 } m3_status;
 
 typedef enum m3_dtype { M3_F32 = 0, M3_BF16 = 1 } m3_dtype;

@@ -19,8 +19,9 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "mamba3", "libmamba3_hip.so")
 
-SOURCES = ["m3_api.cpp", "m3_mixer_api.cpp", "linear.cpp", "ssd_scan.hip", "ssd_scan_fast.hip",
-           "ssd_scan_chunked.hip", "decode_step.hip", "mfma_selftest.hip", "mixer_ops.hip"]
+SOURCES = ["m3_api.cpp", "m3_mixer_api.cpp", "linear.cpp", "checkpoint.cpp", "ssd_scan.hip",
+           "ssd_scan_fast.hip", "ssd_scan_chunked.hip", "decode_step.hip", "mfma_selftest.hip",
+           "mixer_ops.hip"]
 ARCH = "gfx950"
 # Packed-FP32 instructions stay off: hipcc derives them from plain float code
 # and some forms have been unreliable; scalar FP32 is used instead.
@@ -52,7 +53,7 @@ def build(verbose: bool = True) -> str:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", tmp] + objs + [
-        "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
+        "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib", "-pthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

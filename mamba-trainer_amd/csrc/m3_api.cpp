@@ -26,6 +26,9 @@ m3_status vfail(m3_status st, const char *fmt, va_list ap) {
         case M3_ERR_CONFIG: prefix = "invalid configuration: "; break;   // error.rs:12
         case M3_ERR_SHAPE: prefix = "shape error: "; break;              // error.rs:16
         case M3_ERR_UNSUPPORTED: prefix = "unsupported: "; break;        // error.rs:47
+        case M3_ERR_STATE_DICT: prefix = "state dict error: "; break;    // error.rs:35
+        case M3_ERR_IO: prefix = "io error: "; break;                    // error.rs:39
+        case M3_ERR_JSON: prefix = "json error: "; break;                // error.rs:43
         default: break;
     }
     g_last_error = std::string(prefix) + buf;
@@ -376,6 +379,9 @@ const char *m3_status_string(m3_status s) {
         case M3_ERR_UNSUPPORTED: return "M3_ERR_UNSUPPORTED";
         case M3_ERR_HIP: return "M3_ERR_HIP";
         case M3_ERR_ARGUMENT: return "M3_ERR_ARGUMENT";
+        case M3_ERR_STATE_DICT: return "M3_ERR_STATE_DICT";
+        case M3_ERR_IO: return "M3_ERR_IO";
+        case M3_ERR_JSON: return "M3_ERR_JSON";
     }
     return "M3_UNKNOWN";
 }

@@ -7,14 +7,15 @@ from __future__ import annotations
 import ctypes as C
 import os
 
-from .error import (ArgumentError, ConfigError, DeviceError, Mamba3Error, RankError,
-                    ShapeError, UnsupportedError)
+from .error import (ArgumentError, ConfigError, DeviceError, IoError, JsonError, Mamba3Error,
+                    RankError, ShapeError, StateDictError, UnsupportedError)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmamba3_hip.so")
 
 M3_OK, M3_ERR_CONFIG, M3_ERR_SHAPE, M3_ERR_RANK = 0, 1, 2, 3
 M3_ERR_UNSUPPORTED, M3_ERR_HIP, M3_ERR_ARGUMENT = 4, 5, 6
+M3_ERR_STATE_DICT, M3_ERR_IO, M3_ERR_JSON = 7, 8, 9
 M3_F32, M3_BF16 = 0, 1
 
 _Z = C.c_size_t
@@ -106,6 +107,19 @@ SIGNATURES = {
     "m3_mixer_prologue": (C.c_int, [C.POINTER(MixerDimsC)] + [_P] * 12),
     "m3_mixer_gate": (C.c_int, [_Z, _Z, _P, _P, _Z, _P, C.c_float, _P, _P]),
     "m3_embedding_lookup": (C.c_int, [_Z, _Z, _P, _Z, _P, _P, _P]),
+    # mamba3_checkpoint.h
+    "m3_checkpoint_load": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
+    "m3_state_dict_load": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
+    "m3_state_dict_free": (None, [_P]),
+    "m3_state_dict_len": (_Z, [_P]),
+    "m3_state_dict_entry": (C.c_int, [_P, _Z, C.POINTER(C.c_char_p), C.POINTER(_Z),
+                                      C.POINTER(C.POINTER(_Z)), C.POINTER(_FP), C.POINTER(_Z)]),
+    "m3_state_dict_find": (C.c_int64, [_P, C.c_char_p]),
+    "m3_checkpoint_step": (C.c_uint64, [_P]),
+    "m3_checkpoint_metadata": (C.c_char_p, [_P]),
+    "m3_state_dict_save": (C.c_int, [C.c_char_p, C.c_int32, C.c_uint64, C.c_char_p, _Z,
+                                     C.POINTER(C.c_char_p), C.POINTER(_Z),
+                                     C.POINTER(C.POINTER(_Z)), C.POINTER(_FP), C.POINTER(_Z)]),
 }
 
 _lib = None
@@ -135,6 +149,9 @@ _ERRORS = {
     M3_ERR_UNSUPPORTED: UnsupportedError,
     M3_ERR_HIP: DeviceError,
     M3_ERR_ARGUMENT: ArgumentError,
+    M3_ERR_STATE_DICT: StateDictError,
+    M3_ERR_IO: IoError,
+    M3_ERR_JSON: JsonError,
 }
 
 

@@ -31,3 +31,15 @@ class DeviceError(Mamba3Error):
 
 class ArgumentError(Mamba3Error, ValueError):
     """A required buffer is missing or malformed (no reference counterpart)."""
+
+
+class StateDictError(Mamba3Error):
+    """Error::StateDict -- a checkpoint / state dict does not fit the model."""
+
+
+class IoError(Mamba3Error, OSError):
+    """Error::Io -- a checkpoint file could not be read or written."""
+
+
+class JsonError(Mamba3Error, ValueError):
+    """Error::Json -- a checkpoint file is not the expected JSON."""

@@ -18,7 +18,7 @@ import torch
 
 from .error import ShapeError, UnsupportedError
 from .mixer import Mamba3Mixer, MixerCache
-from .nn import Embedding, Linear, RmsNorm, normal
+from .nn import Embedding, Linear, RmsNorm, normal, tensor_param
 from .ssm import SsmConfig
 
 
@@ -63,6 +63,33 @@ class Mamba3Lm:
         self.norm_f = RmsNorm(cfg.d_model, device, eps=cfg.norm_eps)
         self.head = Linear(normal((cfg.d_model, cfg.vocab_size), 0.02, device, gen))
 
+    # ------------------------------------------------------------ parameters
+    def named_parameters(self):
+        """lm.rs:355-362 over hybrid.rs:497-516: embed, stack.layers.{i}.{norm,
+        mixer}, norm_f, head -- the paths of the reference's state dicts."""
+        out = [("embed.weight", self.embed.param())]
+        for i, (norm, mixer) in enumerate(self.layers):
+            pre = f"stack.layers.{i}."
+            if norm.weight is not None:
+                out.append((pre + "norm.weight", tensor_param(norm, "weight")))
+            out += [(pre + "mixer." + n, p) for n, p in mixer.named_parameters()]
+        if self.norm_f.weight is not None:
+            out.append(("norm_f.weight", tensor_param(self.norm_f, "weight")))
+        out.append(("head.weight", self.head.param()))
+        return out
+
+    def num_parameters(self) -> int:
+        return sum(p.numel() for _, p in self.named_parameters())
+
+    def state_dict(self):
+        from .checkpoint import state_dict
+        return state_dict(self)
+
+    def load_state_dict(self, state, strict: bool = True) -> None:
+        from .checkpoint import load_state_dict
+        load_state_dict(self, state, strict)
+
+    # ------------------------------------------------------------ forward
     def hidden(self, ids: torch.Tensor) -> torch.Tensor:
         """lm.rs:295-303: the residual stream after the stack and the final norm."""
         if ids.dim() != 2:

@@ -21,7 +21,7 @@ import torch
 
 from . import _lib
 from .error import ShapeError, UnsupportedError
-from .nn import Linear, RmsNorm, _bf16_dev, _stream, normal, residual_scaled
+from .nn import Linear, RmsNorm, _bf16_dev, _stream, normal, residual_scaled, tensor_param
 from .ssm import ScanInputs, SsmConfig, SsmState, StateDynamics, mamba3_scan, mamba3_step_
 
 
@@ -77,6 +77,21 @@ class Mamba3Mixer:
         self.c_bias = torch.zeros((H, N), device=device) if cfg.bc_bias else None
         self.bc_norm = RmsNorm(N, device) if cfg.bc_norm else None
         self.post_gate_norm = RmsNorm(cfg.d_inner(), device) if cfg.post_gate_norm else None
+
+    def named_parameters(self):
+        """mamba3.rs:634-656: the reference's visit order and paths."""
+        out = [("in_proj.weight", self.in_proj.param()), ("out_proj.weight", self.out_proj.param()),
+               ("dt_bias", tensor_param(self, "dt_bias")), ("a_log", tensor_param(self, "a_log"))]
+        if self.d_skip is not None:
+            out.append(("d", tensor_param(self, "d_skip")))
+        if self.b_bias is not None:
+            out.append(("b_bias", tensor_param(self, "b_bias")))
+        if self.c_bias is not None:
+            out.append(("c_bias", tensor_param(self, "c_bias")))
+        for name, norm in (("bc_norm", self.bc_norm), ("post_gate_norm", self.post_gate_norm)):
+            if norm is not None and norm.weight is not None:
+                out.append((f"{name}.weight", tensor_param(norm, "weight")))
+        return out
 
     # ------------------------------------------------------------ pieces
     def _dims(self, tokens: int) -> _lib.MixerDimsC:

@@ -40,6 +40,14 @@ def residual_scaled(shape, std: float, n_layers: int, device, gen: torch.Generat
     return normal(shape, std / math.sqrt(2.0 * max(n_layers, 1)), device, gen)
 
 
+def tensor_param(owner, attr: str):
+    """A checkpoint Param over an f32 device tensor held as `owner.<attr>`."""
+    from .checkpoint import Param
+    t = getattr(owner, attr)
+    return Param(tuple(t.shape), lambda: getattr(owner, attr),
+                 lambda v: getattr(owner, attr).copy_(v.to(torch.float32)))
+
+
 _WS = {}
 
 
@@ -119,6 +127,16 @@ class Linear:
             self.codes = self.weight.to(torch.bfloat16)
             self.scales = None
 
+    def param(self):
+        """The master weight [in, out] as a checkpoint Param; setting it
+        re-derives the GEMM operands (codes and scales)."""
+        from .checkpoint import Param
+
+        def put(v):
+            self.weight.copy_(v.to(torch.float32))
+            self.prepare()
+        return Param(tuple(self.weight.shape), lambda: self.weight, put)
+
     def effective_weight(self) -> torch.Tensor:
         """The weight the product uses, in f32 (w' for the quantized form)."""
         if self.scales is None:
@@ -159,6 +177,13 @@ class Embedding:
     @property
     def dim(self) -> int:
         return self.table.shape[1]
+
+    def param(self):
+        """The table as a checkpoint Param: read as f32, stored back as bf16
+        (round to nearest even, as the reference's from_f32 for bf16)."""
+        from .checkpoint import Param
+        return Param(tuple(self.table.shape), lambda: self.table.float(),
+                     lambda v: self.table.copy_(v.to(torch.float32).to(torch.bfloat16)))
 
     def lookup(self, ids: torch.Tensor) -> torch.Tensor:
         if not ids.is_cuda:
