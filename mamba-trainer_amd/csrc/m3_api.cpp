@@ -265,6 +265,7 @@ size_t m3_scan_workspace_bytes(const m3_scan_inputs *in) {
     a.d_state = in->d_state;
     a.rank = in->rank;
     a.bf16 = in->dtype == M3_BF16;
+    a.mode_raw = 1;   // m3_scan's prologue, as the launch sets it
     // alignment is checked at launch; size the shape as if aligned
     alignas(16) static float dummy[4] = {0, 0, 0, 0};
     a.x = a.b = a.c = dummy;

@@ -50,6 +50,11 @@ hipError_t launch_scan_fast(const ScanLaunch &a, hipStream_t stream);
 // and the launch.
 size_t scan_chunked_workspace(const ScanLaunch &a);
 hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream);
+// The single-launch form with a decoupled look-back (bf16 storage, the shapes
+// above, mamba3_scan mode): workspace bytes (0 when not covered) and launch.
+bool scan_lookback_supported(const ScanLaunch &a);
+size_t scan_lookback_workspace(const ScanLaunch &a);
+hipError_t launch_scan_lookback(const ScanLaunch &a, void *workspace, hipStream_t stream);
 
 // Largest head_dim / d_state the scan kernels are instantiated for.
 constexpr size_t kScanMaxHeadDim = 128;

@@ -243,5 +243,22 @@ __device__ __forceinline__ void load_chunk(const SeqBufs &rs, int ck, int wave, 
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// Per-token scalars of this lane's token: log decay a, diagonal weight g,
+// off-diagonal weight w (fused.rs:2483-2503), zero for tokens past the end.
+template <typename RawT>
+__device__ __forceinline__ void token_scalars(const ScanLaunch &a, const RawT &cur, float A,
+                                              bool live, float &av, float &gv, float &wv) {
+    if (a.mode_raw) {
+        av = cur.s0 * A;
+        gv = cur.s1 * cur.s0;                        // fused.rs:2494
+        wv = gv + (1.0f - cur.s3) * cur.s2;          // fused.rs:2496-2498
+    } else {
+        av = cur.s0;
+        gv = cur.s1;
+        wv = cur.s2;
+    }
+    if (!live) av = gv = wv = 0.f;
+}
+
 }  // namespace scan
 }  // namespace m3

@@ -31,6 +31,8 @@
 // and band are latency-bound there.  Here both heavy passes spread over every
 // chunk of every sequence; the sequential pass is a few FMAs per element and
 // streams U_k from HBM.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "scan_common.hpp"
@@ -112,23 +114,6 @@ __device__ __forceinline__ f32x4 load_u(const void *u, size_t e) {
     } else {
         return *reinterpret_cast<const f32x4 *>(static_cast<const float *>(u) + e);
     }
-}
-
-// Per-token scalars of this lane's token: log decay a, diagonal weight g,
-// off-diagonal weight w (fused.rs:2483-2503), zero for tokens past the end.
-template <typename RawT>
-__device__ __forceinline__ void token_scalars(const ScanLaunch &a, const RawT &cur, float A,
-                                              bool live, float &av, float &gv, float &wv) {
-    if (a.mode_raw) {
-        av = cur.s0 * A;
-        gv = cur.s1 * cur.s0;                        // fused.rs:2494
-        wv = gv + (1.0f - cur.s3) * cur.s2;          // fused.rs:2496-2498
-    } else {
-        av = cur.s0;
-        gv = cur.s1;
-        wv = cur.s2;
-    }
-    if (!live) av = gv = wv = 0.f;
 }
 
 // ================================================================ chunk state
@@ -723,9 +708,20 @@ static size_t device_cus() {
     return static_cast<size_t>(cus);
 }
 
+// M3_SCAN_CHUNKED=lookback routes bf16 scans in mamba3_scan mode to the
+// single-launch look-back kernel (ssd_scan_lookback.hip) instead of these
+// three launches.  It is parity-tested but slower at the benchmark shapes
+// (141 vs 110 us at config 1 on MI355X), so it is opt-in.
+static bool use_lookback(const ScanLaunch &a) {
+    const char *e = std::getenv("M3_SCAN_CHUNKED");
+    const bool look = e != nullptr && std::strcmp(e, "lookback") == 0;
+    return look && scan_lookback_supported(a);
+}
+
 size_t scan_chunked_workspace(const ScanLaunch &a) {
     if (!scan_fast_supported(a) || a.seq == 0) return 0;
     if (a.batch * a.heads * 10 >= device_cus() * 7) return 0;
+    if (use_lookback(a)) return scan_lookback_workspace(a);
     const size_t qt = static_cast<size_t>(rows_for(a)) / a.rank;
     const size_t nck = (a.seq + qt - 1) / qt;
     return chunked_layout(a.batch * a.heads * nck, a.d_state, a.bf16 != 0).total;
@@ -733,6 +729,7 @@ size_t scan_chunked_workspace(const ScanLaunch &a) {
 
 hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream) {
     if (!scan_fast_supported(a) || a.seq == 0) return hipErrorNotSupported;
+    if (use_lookback(a)) return launch_scan_lookback(a, workspace, stream);
     char *ws = static_cast<char *>(workspace);
     if (a.bf16) return launch_t<bf16_t, 64>(a, ws, stream);
     return launch_t<float, 32>(a, ws, stream);
