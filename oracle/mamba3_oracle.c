@@ -13,7 +13,7 @@
  *        the reference test-suite's own input generator and its own direct
  *        recurrence oracle (tests/ssm.rs:26-34, 58-106), restated verbatim in
  *        f32 with the same loop order.
- *   2. m3o_scan_recurrence_f64
+ *   2. m3o_scan_recurrence_f64 (and its reverse mode, m3o_scan_backward_f64)
  *        the exponential-trapezoidal recurrence (src/ssm/scan.rs:5-45) evaluated
  *        token by token in double precision, extended with everything the scan
  *        API carries: MIMO rank (scan.rs:538-589), the rotating frame
@@ -40,6 +40,11 @@
  *     against closed forms (one token, pure rotation e^{i*theta*t}, pure decay),
  *     and against the invariants split-window == single pass, stepwise ==
  *     parallel, MIMO == sum of SISO systems, Euler == Mamba-2.
+ *   - m3o_scan_backward_f64: against central finite differences of
+ *     m3o_scan_recurrence_f64 on every input (x, b, c, dt, lambda, a_log,
+ *     theta, d_skip, h0, last_u0, angle0) through random directional
+ *     derivatives, with and without upstream state gradients; and against the
+ *     reference's scan_is_differentiable case (tests/ssm.rs:382-426).
  *   - m3o_ssd_chunked_f32 / m3o_scan_composed_f32 / m3o_step_f32: against the
  *     f64 recurrence at the reference's own tolerances (2e-4 / 3e-4).
  *   - fault injection (m3o_set_fault) plants a mistake in this file on the
@@ -73,6 +78,7 @@ enum {
     M3O_FAULT_SKIP_SIGN = 7,        /* y -= D*x */
     M3O_FAULT_CARRY_BETA = 8,       /* incoming last_u ignored */
     M3O_FAULT_CHUNK_STATE_W = 9,    /* chunk summary weighted by g instead of w */
+    M3O_FAULT_BWD_ROT_SIGN = 10,    /* backward: dB, dC rotated by -phi instead of +phi */
 };
 static int g_fault = 0;
 void m3o_set_fault(int code) { g_fault = code; }
@@ -258,6 +264,236 @@ void m3o_scan_recurrence_f64(size_t B, size_t T, size_t H, size_t P, size_t N, s
                     angle_out[(bb * H + hh) * half + i] = T ? wrap_pi_f64(phi[i]) : phi[i];
             free(h); free(lu); free(u); free(phi); free(bt); free(ct);
         }
+}
+
+/*
+ * Reverse mode of m3o_scan_recurrence_f64 (the gradient the reference gets by
+ * autodiff through mamba3_scan, src/ssm/scan.rs:458-638, whose hand-written
+ * pieces are ssd_band_backward fused.rs:2080-2138, exp_decay_backward
+ * 2326-2382 and trapezoid_weights_backward 2513-2549), evaluated token by
+ * token in double precision.
+ *
+ * Forward, per (batch, head):  h_t = alpha_t h_{t-1} + beta_t u_{t-1} + gamma_t u_t,
+ * u_t = sum_r x_t[:, r] B~_t[:, r]^T, y_t = C~_t^T h_t + D x_t, with
+ * phi_t = angle0 + sum_{s<=t} dt_s theta_s (the angle is wrapped only where it
+ * is output, so its derivative is 1).  Backward walks t = T-1 .. 0 carrying
+ * dh = dL/dh_t, dlu = dL/du_t (through beta_{t+1}) and the running sum of
+ * dL/dphi over t' >= t; states are recomputed from checkpoints every
+ * M3O_BWD_SEG tokens.
+ *
+ * Inputs as m3o_scan_recurrence_f64, plus dy [B,T,H,P,R] and the optional
+ * upstream gradients of the outgoing state dh_out, dlast_u_out [B,H,P,N],
+ * dangle_out [B,H,N/2] (NULL = zero).  Outputs (any may be NULL): dx, db, dc,
+ * ddt, dlambda, dtheta (theta's layout), da_log [H], dd_skip [H] (summed over
+ * the batch), dh0, dlast_u0 [B,H,P,N], dangle0 [B,H,N/2].
+ */
+#define M3O_BWD_SEG 32
+
+void m3o_scan_backward_f64(size_t B, size_t T, size_t H, size_t P, size_t N, size_t R,
+                           const float *x, const float *b, const float *c, const float *dt,
+                           const float *a_log, const float *lambda, const float *theta,
+                           const float *d_skip, const float *h0, const float *last_u0,
+                           const float *angle0, const double *dy, const double *dh_out,
+                           const double *dlast_u_out, const double *dangle_out, double *dx,
+                           double *db, double *dc, double *ddt, double *dlambda,
+                           double *dtheta, double *da_log, double *dd_skip, double *dh0,
+                           double *dlast_u0, double *dangle0) {
+    const size_t half = N / 2, PN = P * N, NR = N * R;
+    double *part_a = (double *)calloc(B * H + 1, sizeof(double));
+    double *part_d = (double *)calloc(B * H + 1, sizeof(double));
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (size_t bb = 0; bb < B; ++bb)
+        for (size_t hh = 0; hh < H; ++hh) {
+            const size_t nseg = (T + M3O_BWD_SEG - 1) / M3O_BWD_SEG;
+            double *alpha = (double *)calloc(T + 1, sizeof(double));
+            double *beta = (double *)calloc(T + 1, sizeof(double));
+            double *gamma = (double *)calloc(T + 1, sizeof(double));
+            double *phi = (double *)calloc(T * half + 1, sizeof(double));
+            double *bt = (double *)calloc(T * NR + 1, sizeof(double));
+            double *ct = (double *)calloc(T * NR + 1, sizeof(double));
+            double *hck = (double *)calloc((nseg + 1) * PN + 1, sizeof(double));
+            double *luck = (double *)calloc((nseg + 1) * PN + 1, sizeof(double));
+            double *hs = (double *)calloc(M3O_BWD_SEG * PN + 1, sizeof(double));
+            double *us = (double *)calloc(M3O_BWD_SEG * PN + 1, sizeof(double));
+            double *h = (double *)calloc(PN + 1, sizeof(double));
+            double *lu = (double *)calloc(PN + 1, sizeof(double));
+            double *dh = (double *)calloc(PN + 1, sizeof(double));
+            double *dlu = (double *)calloc(PN + 1, sizeof(double));
+            double *du = (double *)calloc(PN + 1, sizeof(double));
+            double *dbt = (double *)calloc(NR + 1, sizeof(double));
+            double *dct = (double *)calloc(NR + 1, sizeof(double));
+            double *dphi = (double *)calloc(half + 1, sizeof(double));
+            const size_t so = (bb * H + hh) * PN;
+            const double A = -exp((double)a_log[hh]);
+            const double D = d_skip ? (double)d_skip[hh] : 0.0;
+            double dA = 0.0, dD = 0.0;
+
+            /* per-token coefficients and rotated B, C (as the forward) */
+            for (size_t i = 0; i < half; ++i) dphi[i] = angle0 ? angle0[(bb * H + hh) * half + i] : 0.0;
+            for (size_t t = 0; t < T; ++t) {
+                const size_t idx = (bb * T + t) * H + hh;
+                const double step = dt[idx], lam = lambda[idx];
+                alpha[t] = exp(step * A);
+                beta[t] = (1.0 - lam) * step * alpha[t];
+                gamma[t] = lam * step;
+                if (g_fault == M3O_FAULT_DROP_BETA) beta[t] = 0.0;
+                const float *bs = b + idx * NR, *cs = c + idx * NR;
+                for (size_t i = 0; i < NR; ++i) { bt[t * NR + i] = bs[i]; ct[t * NR + i] = cs[i]; }
+                if (theta)
+                    for (size_t i = 0; i < half; ++i) {
+                        dphi[i] += step * (double)theta[idx * half + i];
+                        phi[t * half + i] = dphi[i];
+                        for (size_t r = 0; r < R; ++r) {
+                            double o1, o2;
+                            rot_neg_f64(dphi[i], bs[i * R + r], bs[(i + half) * R + r], &o1, &o2);
+                            bt[t * NR + i * R + r] = o1; bt[t * NR + (i + half) * R + r] = o2;
+                            rot_neg_f64(dphi[i], cs[i * R + r], cs[(i + half) * R + r], &o1, &o2);
+                            ct[t * NR + i * R + r] = o1; ct[t * NR + (i + half) * R + r] = o2;
+                        }
+                    }
+            }
+            /* forward with a checkpoint of (h, last_u) at every segment start */
+            if (h0) for (size_t i = 0; i < PN; ++i) h[i] = h0[so + i];
+            if (last_u0) for (size_t i = 0; i < PN; ++i) lu[i] = last_u0[so + i];
+            for (size_t t = 0; t < T; ++t) {
+                if (t % M3O_BWD_SEG == 0) {
+                    memcpy(hck + (t / M3O_BWD_SEG) * PN, h, PN * sizeof(double));
+                    memcpy(luck + (t / M3O_BWD_SEG) * PN, lu, PN * sizeof(double));
+                }
+                const float *xs = x + ((bb * T + t) * H + hh) * P * R;
+                for (size_t p = 0; p < P; ++p)
+                    for (size_t n = 0; n < N; ++n) {
+                        double acc = 0.0;
+                        for (size_t r = 0; r < R; ++r) acc += (double)xs[p * R + r] * bt[t * NR + n * R + r];
+                        h[p * N + n] = alpha[t] * h[p * N + n] + beta[t] * lu[p * N + n] + gamma[t] * acc;
+                        lu[p * N + n] = acc;
+                    }
+            }
+
+            /* backward */
+            for (size_t i = 0; i < PN; ++i) {
+                dh[i] = dh_out ? dh_out[so + i] : 0.0;
+                dlu[i] = dlast_u_out ? dlast_u_out[so + i] : 0.0;
+            }
+            for (size_t i = 0; i < half; ++i)
+                dphi[i] = dangle_out ? dangle_out[(bb * H + hh) * half + i] : 0.0;
+            for (size_t sg = nseg; sg-- > 0;) {
+                const size_t t0 = sg * M3O_BWD_SEG;
+                const size_t t1 = (t0 + M3O_BWD_SEG < T) ? t0 + M3O_BWD_SEG : T;
+                memcpy(h, hck + sg * PN, PN * sizeof(double));
+                memcpy(lu, luck + sg * PN, PN * sizeof(double));
+                for (size_t t = t0; t < t1; ++t) {
+                    const float *xs = x + ((bb * T + t) * H + hh) * P * R;
+                    double *hv = hs + (t - t0) * PN, *uv = us + (t - t0) * PN;
+                    for (size_t p = 0; p < P; ++p)
+                        for (size_t n = 0; n < N; ++n) {
+                            double acc = 0.0;
+                            for (size_t r = 0; r < R; ++r) acc += (double)xs[p * R + r] * bt[t * NR + n * R + r];
+                            h[p * N + n] = alpha[t] * h[p * N + n] + beta[t] * lu[p * N + n] + gamma[t] * acc;
+                            lu[p * N + n] = acc;
+                            hv[p * N + n] = h[p * N + n];
+                            uv[p * N + n] = acc;
+                        }
+                }
+                for (size_t t = t1; t-- > t0;) {
+                    const size_t idx = (bb * T + t) * H + hh;
+                    const float *xs = x + idx * P * R;
+                    const double *hv = hs + (t - t0) * PN, *uv = us + (t - t0) * PN;
+                    const double *hp = (t > t0) ? hs + (t - 1 - t0) * PN : hck + sg * PN;
+                    const double *up = (t > t0) ? us + (t - 1 - t0) * PN : luck + sg * PN;
+                    double ddt_t = 0.0, dlam_t = 0.0;
+                    for (size_t i = 0; i < NR; ++i) { dbt[i] = 0.0; dct[i] = 0.0; }
+                    /* y_t = C~_t^T h_t + D x_t */
+                    for (size_t p = 0; p < P; ++p)
+                        for (size_t r = 0; r < R; ++r) {
+                            const double g = dy[idx * P * R + p * R + r];
+                            dD += g * (double)xs[p * R + r];
+                            if (dx) dx[idx * P * R + p * R + r] = D * g;
+                            for (size_t n = 0; n < N; ++n) {
+                                dh[p * N + n] += g * ct[t * NR + n * R + r];
+                                dct[n * R + r] += g * hv[p * N + n];
+                            }
+                        }
+                    /* h_t = alpha h_{t-1} + beta u_{t-1} + gamma u_t */
+                    double dal = 0.0, dbe = 0.0, dga = 0.0;
+                    for (size_t i = 0; i < PN; ++i) {
+                        dal += dh[i] * hp[i];
+                        dbe += dh[i] * up[i];
+                        dga += dh[i] * uv[i];
+                        du[i] = gamma[t] * dh[i] + dlu[i];
+                        dlu[i] = beta[t] * dh[i];
+                        dh[i] = alpha[t] * dh[i];
+                    }
+                    /* u_t = sum_r x_t[:, r] B~_t[:, r]^T */
+                    for (size_t p = 0; p < P; ++p)
+                        for (size_t r = 0; r < R; ++r) {
+                            double acc = 0.0;
+                            for (size_t n = 0; n < N; ++n) acc += du[p * N + n] * bt[t * NR + n * R + r];
+                            if (dx) dx[idx * P * R + p * R + r] += acc;
+                        }
+                    for (size_t n = 0; n < N; ++n)
+                        for (size_t r = 0; r < R; ++r) {
+                            double acc = 0.0;
+                            for (size_t p = 0; p < P; ++p) acc += du[p * N + n] * (double)xs[p * R + r];
+                            dbt[n * R + r] = acc;
+                        }
+                    /* alpha = exp(dt A), beta = (1 - lambda) dt alpha, gamma = lambda dt */
+                    const double step = dt[idx], lam = lambda[idx], al = alpha[t];
+                    ddt_t += dal * al * A;
+                    dA += dal * al * step;
+                    if (g_fault != M3O_FAULT_DROP_BETA) {
+                        dlam_t -= dbe * step * al;
+                        ddt_t += dbe * (1.0 - lam) * (al + step * al * A);
+                        dA += dbe * (1.0 - lam) * step * al * step;
+                    }
+                    dlam_t += dga * step;
+                    ddt_t += dga * lam;
+                    /* rotation by -phi: dB = R(phi) dB~, dphi = dB~1 B~2 - dB~2 B~1 (and C) */
+                    if (theta) {
+                        for (size_t i = 0; i < half; ++i) {
+                            const double ph = phi[t * half + i], cs = cos(ph);
+                            const double sn = (g_fault == M3O_FAULT_BWD_ROT_SIGN) ? -sin(ph) : sin(ph);
+                            double dp = 0.0;
+                            for (size_t r = 0; r < R; ++r) {
+                                const size_t i1 = i * R + r, i2 = (i + half) * R + r;
+                                const double b1 = bt[t * NR + i1], b2 = bt[t * NR + i2];
+                                const double c1 = ct[t * NR + i1], c2 = ct[t * NR + i2];
+                                dp += dbt[i1] * b2 - dbt[i2] * b1 + dct[i1] * c2 - dct[i2] * c1;
+                                const double db1 = dbt[i1] * cs - dbt[i2] * sn;
+                                const double db2 = dbt[i1] * sn + dbt[i2] * cs;
+                                const double dc1 = dct[i1] * cs - dct[i2] * sn;
+                                const double dc2 = dct[i1] * sn + dct[i2] * cs;
+                                dbt[i1] = db1; dbt[i2] = db2; dct[i1] = dc1; dct[i2] = dc2;
+                            }
+                            dphi[i] += dp;
+                            if (dtheta) dtheta[idx * half + i] = step * dphi[i];
+                            ddt_t += (double)theta[idx * half + i] * dphi[i];
+                        }
+                    }
+                    if (db) for (size_t i = 0; i < NR; ++i) db[idx * NR + i] = dbt[i];
+                    if (dc) for (size_t i = 0; i < NR; ++i) dc[idx * NR + i] = dct[i];
+                    if (ddt) ddt[idx] = ddt_t;
+                    if (dlambda) dlambda[idx] = dlam_t;
+                }
+            }
+            if (dh0) for (size_t i = 0; i < PN; ++i) dh0[so + i] = dh[i];
+            if (dlast_u0) for (size_t i = 0; i < PN; ++i) dlast_u0[so + i] = dlu[i];
+            if (dangle0)
+                for (size_t i = 0; i < half; ++i) dangle0[(bb * H + hh) * half + i] = theta ? dphi[i] : 0.0;
+            part_a[bb * H + hh] = dA * A;
+            part_d[bb * H + hh] = dD;
+            free(alpha); free(beta); free(gamma); free(phi); free(bt); free(ct); free(hck);
+            free(luck); free(hs); free(us); free(h); free(lu); free(dh); free(dlu); free(du);
+            free(dbt); free(dct); free(dphi);
+        }
+    for (size_t hh = 0; hh < H; ++hh) {
+        double sa = 0.0, sd = 0.0;
+        for (size_t bb = 0; bb < B; ++bb) { sa += part_a[bb * H + hh]; sd += part_d[bb * H + hh]; }
+        if (da_log) da_log[hh] = sa;
+        if (dd_skip) dd_skip[hh] = sd;
+    }
+    free(part_a);
+    free(part_d);
 }
 
 /* ---------------------------------------------------------------------------

@@ -31,6 +31,7 @@ FAULTS = {
     "skip_sign": 7,
     "carry_beta": 8,
     "chunk_state_w": 9,
+    "bwd_rot_sign": 10,
 }
 
 
@@ -64,6 +65,7 @@ def _declare(L):
     L.m3o_noise.argtypes = [_Z, C.c_uint64, _F]
     L.m3o_test_reference_f32.argtypes = [_Z] * 5 + [_F] * 8
     L.m3o_scan_recurrence_f64.argtypes = [_Z] * 6 + [_F] * 11 + [_D] * 4
+    L.m3o_scan_backward_f64.argtypes = [_Z] * 6 + [_F] * 11 + [_D] * 15
     L.m3o_cumsum.argtypes = [_F, _F, _Z, _Z, _Z, C.c_int, C.c_int]
     L.m3o_wrap_to.argtypes = [C.c_float, C.c_float]
     L.m3o_wrap_to.restype = C.c_float
@@ -149,6 +151,33 @@ def scan_recurrence_f64(x, b, c, dt, a_log, lam, theta=None, d_skip=None,
                                   _pf(last_u0), _pf(angle0), _pd(y), _pd(h), _pd(lu),
                                   _pd(ang))
     return y, h, lu, ang
+
+
+def scan_backward_f64(x, b, c, dt, a_log, lam, dy, theta=None, d_skip=None, h0=None,
+                      last_u0=None, angle0=None, dh_out=None, dlast_u_out=None,
+                      dangle_out=None):
+    """Reverse mode of scan_recurrence_f64 for the loss sum(dy * y) (+ the
+    upstream state gradients).  Returns a dict of f64 gradients: x, b, c, dt,
+    lam, a_log, theta, d_skip, h0, last_u0, angle0 (None where the input is
+    absent)."""
+    x, b, c, dt, a_log, lam = map(_f32, (x, b, c, dt, a_log, lam))
+    theta, d_skip, h0, last_u0, angle0 = map(_f32, (theta, d_skip, h0, last_u0, angle0))
+    d64 = lambda a: None if a is None else np.ascontiguousarray(a, np.float64)
+    dy, dh_out, dlast_u_out, dangle_out = map(d64, (dy, dh_out, dlast_u_out, dangle_out))
+    B, T, H, P, R = x.shape
+    N = b.shape[3]
+    z = lambda *shape: np.zeros(shape, np.float64)
+    g = dict(x=z(B, T, H, P, R), b=z(B, T, H, N, R), c=z(B, T, H, N, R), dt=z(B, T, H),
+             lam=z(B, T, H), a_log=z(H), theta=z(B, T, H, N // 2) if theta is not None else None,
+             d_skip=z(H), h0=z(B, H, P, N), last_u0=z(B, H, P, N), angle0=z(B, H, N // 2))
+    lib().m3o_scan_backward_f64(B, T, H, P, N, R, _pf(x), _pf(b), _pf(c), _pf(dt), _pf(a_log),
+                                _pf(lam), _pf(theta), _pf(d_skip), _pf(h0), _pf(last_u0),
+                                _pf(angle0), _pd(dy), _pd(dh_out), _pd(dlast_u_out),
+                                _pd(dangle_out), _pd(g["x"]), _pd(g["b"]), _pd(g["c"]),
+                                _pd(g["dt"]), _pd(g["lam"]), _pd(g["theta"]), _pd(g["a_log"]),
+                                _pd(g["d_skip"]), _pd(g["h0"]), _pd(g["last_u0"]),
+                                _pd(g["angle0"]))
+    return g
 
 
 def cumsum(x, axis, reverse=False, exclusive=False):

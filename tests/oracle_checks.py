@@ -451,6 +451,129 @@ def outer_product_orientation():
     return max(float(np.max(np.abs(lu[0, 0] - want))), float(np.max(np.abs(h[0, 0] - 0.25 * want))))
 
 
+# --------------------------------------------------------------------------- backward
+
+def _loss_f64(inp, seeds):
+    """L = <dy, y> + <dh, h> + <dlu, last_u> + <dang, angle> on the f64 recurrence."""
+    y, h, lu, ang = oracle.scan_recurrence_f64(
+        inp["x"], inp["b"], inp["c"], inp["dt"], inp["a_log"], inp["lam"], inp.get("theta"),
+        inp.get("d_skip"), inp.get("h0"), inp.get("last_u0"), inp.get("angle0"))
+    L = float(np.sum(seeds["dy"] * y))
+    if seeds.get("dh") is not None:
+        L += float(np.sum(seeds["dh"] * h)) + float(np.sum(seeds["dlu"] * lu))
+    if seeds.get("dang") is not None and ang is not None:
+        L += float(np.sum(seeds["dang"] * ang))
+    return L
+
+
+def _directional_errors(inp, seeds, eps=2e-5, seed=0):
+    """For every input, |<grad, d> - (L(+) - L(-))/2| / scale, where d is half
+    the f32 difference of the two perturbed inputs (central differences).  The
+    error of a correct gradient is the O(eps^2) truncation term: about 4e-9
+    at eps = 2e-5 (it falls 100x per 10x smaller eps)."""
+    g = oracle.scan_backward_f64(
+        inp["x"], inp["b"], inp["c"], inp["dt"], inp["a_log"], inp["lam"], seeds["dy"],
+        inp.get("theta"), inp.get("d_skip"), inp.get("h0"), inp.get("last_u0"),
+        inp.get("angle0"), seeds.get("dh"), seeds.get("dlu"), seeds.get("dang"))
+    rng = np.random.default_rng(seed)
+    errs = []
+    for k in ("x", "b", "c", "dt", "lam", "a_log", "theta", "d_skip", "h0", "last_u0", "angle0"):
+        if inp.get(k) is None:
+            continue
+        v = inp[k].astype(np.float64)
+        direction = rng.standard_normal(v.shape)
+        step = eps * (np.abs(v) + 0.1)
+        plus = dict(inp)
+        minus = dict(inp)
+        plus[k] = (v + step * direction).astype(np.float32)
+        minus[k] = (v - step * direction).astype(np.float32)
+        d = (plus[k].astype(np.float64) - minus[k].astype(np.float64)) / 2.0
+        numeric = (_loss_f64(plus, seeds) - _loss_f64(minus, seeds)) / 2.0
+        analytic = float(np.sum(g[k] * d))
+        errs.append(abs(analytic - numeric) / (abs(numeric) + 1e-3 * np.linalg.norm(d) + 1e-30))
+    return max(errs)
+
+
+def _bwd_case(B, T, H, P, N, R, theta, skip, state, seed):
+    rng = np.random.default_rng(seed)
+    inp = dict(baseline_like(rng, B, T, H, P, N, R, theta, state))
+    if skip:
+        inp["d_skip"] = rng.uniform(-1, 1, H).astype(np.float32)
+    seeds = dict(dy=rng.standard_normal((B, T, H, P, R)))
+    if state:
+        seeds["dh"] = rng.standard_normal((B, H, P, N))
+        seeds["dlu"] = rng.standard_normal((B, H, P, N))
+        if theta:
+            seeds["dang"] = rng.standard_normal((B, H, N // 2))
+    return inp, seeds
+
+
+def baseline_like(rng, B, T, H, P, N, R, theta, state):
+    f = np.float32
+    out = dict(
+        x=rng.standard_normal((B, T, H, P, R)).astype(f),
+        b=(rng.standard_normal((B, T, H, N, R)) / math.sqrt(N)).astype(f),
+        c=(rng.standard_normal((B, T, H, N, R)) / math.sqrt(N)).astype(f),
+        dt=rng.uniform(0.02, 0.3, (B, T, H)).astype(f),
+        a_log=rng.uniform(-0.5, 1.5, H).astype(f),
+        lam=rng.uniform(0.1, 0.9, (B, T, H)).astype(f))
+    if theta:
+        out["theta"] = rng.uniform(0.0, math.pi, (B, T, H, N // 2)).astype(f)
+    if state:
+        out["h0"] = (0.3 * rng.standard_normal((B, H, P, N))).astype(f)
+        out["last_u0"] = (0.3 * rng.standard_normal((B, H, P, N))).astype(f)
+        if theta:
+            out["angle0"] = rng.uniform(-3.0, 3.0, (B, H, N // 2)).astype(f)
+    return out
+
+
+@check(1e-7)
+def backward_directional_derivatives_rotational_state_skip():
+    """Every gradient against central differences of the f64 recurrence:
+    rotating frame, skip, carried-in state and upstream state gradients,
+    two checkpoint segments (T = 37)."""
+    inp, seeds = _bwd_case(1, 37, 2, 3, 4, 1, True, True, True, 1)
+    return _directional_errors(inp, seeds, seed=1)
+
+
+@check(1e-7)
+def backward_directional_derivatives_mimo():
+    """MIMO rank 2 (the R^2 cross terms, scan.rs:538-589), rotating frame."""
+    inp, seeds = _bwd_case(2, 20, 1, 2, 6, 2, True, False, False, 2)
+    return _directional_errors(inp, seeds, seed=2)
+
+
+@check(1e-7)
+def backward_directional_derivatives_real_long():
+    """Real dynamics over three checkpoint segments (T = 70), no state."""
+    inp, seeds = _bwd_case(1, 70, 2, 4, 2, 1, False, True, False, 3)
+    return _directional_errors(inp, seeds, seed=3)
+
+
+@check(2e-2)
+def backward_reference_differentiable_case():
+    """tests/ssm.rs:382-426: Case::new(1, 6, 2, 3, 4), loss = sum(y^2), dx at
+    coordinates 0, 5, 17, 30 against central differences (eps 1e-3) at the
+    reference's own tolerance 2e-2 * (1 + |numeric|)."""
+    case = Case(1, 6, 2, 3, 4)
+    x, b, c = case.rank1()
+    args = (b, c, case.dt, case.a_log, case.lam)
+    y, _, _, _ = oracle.scan_recurrence_f64(x, *args)
+    g = oracle.scan_backward_f64(x, b, c, case.dt, case.a_log, case.lam, 2.0 * y)
+    worst = 0.0
+    for i in (0, 5, 17, 30):
+        def run(data):
+            yy, _, _, _ = oracle.scan_recurrence_f64(data.reshape(x.shape), *args)
+            return float(np.sum(yy.astype(np.float32) ** 2))
+        plus = x.ravel().copy()
+        minus = x.ravel().copy()
+        plus[i] += np.float32(1e-3)
+        minus[i] -= np.float32(1e-3)
+        numeric = (run(plus) - run(minus)) / (2e-3)
+        worst = max(worst, abs(g["x"].ravel()[i] - numeric) / (1.0 + abs(numeric)))
+    return worst
+
+
 def run_all():
     """Run every check; returns {name: (passed, worst_error)}."""
     out = {}
