@@ -18,6 +18,8 @@ Also reported on the same line:
   decode         BASELINE config 3: one token for 256 sequences through
                  24 layers x 24 heads (P=64, N=128) of f32 state cache, in place,
                  timed over consecutive steps: us per step, GB/s, fraction of HBM peak;
+  backward       config 1's scan backward (every input gradient from dL/dy):
+                 us per call, fwd+bwd tokens/s, HBM fraction of its minimum bytes;
   decode_lm      the whole Mamba3Lm decode step around it (d_model 1536, int8
                  projections, head): us per step, tokens/s, GB/s over the state,
                  weight and logit bytes;
@@ -263,6 +265,62 @@ def bench_ingest(torch, args):
 DECODE_LM = dict(B=256, vocab=32000, d_model=1536, layers=24, H=24, P=64, N=128, G=24)
 
 
+def scan_backward_algorithmic(B, L, H, P, N, R, s_io=2):
+    """HBM bytes of one backward call at the algorithm's minimum: x, b, c,
+    theta (per token), dy read at s_io bytes and dt, lambda as f32; dx, db, dc,
+    dtheta written at s_io bytes and ddt, dlambda as f32."""
+    per_tok = (2 * P * R + 2 * N * R + N // 2) * s_io + 8 + (P * R + 2 * N * R + N // 2) * s_io + 8
+    return B * L * H * per_tok
+
+
+def bench_backward(torch, lib, L_, args, inp, fwd_ms):
+    """Config 1's scan backward (m3_scan_backward): dL/dy -> every input
+    gradient, the forward chunk states recomputed inside the call."""
+    import ctypes as C
+    dev = "cuda:0"
+    s = SCAN
+    B, L, H, P, N, R = s["B"], s["L"], s["H"], s["P"], s["N"], s["R"]
+    g = torch.Generator(device=dev).manual_seed(0x4D414D45)
+    dy = torch.randn(B, L, H, P, R, device=dev, generator=g).to(torch.bfloat16)
+    cin = L_.ScanInputsC(B, L, H, P, N, R, L_.M3_BF16, inp["x"].data_ptr(), inp["b"].data_ptr(),
+                         inp["c"].data_ptr(), inp["dt"].data_ptr(), inp["a_log"].data_ptr(),
+                         inp["lam"].data_ptr(), inp["theta"].data_ptr(), None, None, s["Q"], 0,
+                         None, 0)
+    need = int(lib.m3_scan_backward_workspace_bytes(C.byref(cin)))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    cin.workspace, cin.workspace_bytes = ws.data_ptr(), need
+    gx, gb, gc, gth = (torch.empty_like(inp[k]) for k in ("x", "b", "c", "theta"))
+    gdt, glam = torch.empty_like(inp["dt"]), torch.empty_like(inp["lam"])
+    ga = torch.empty(H, device=dev)
+    gr = L_.ScanGradsC(dy.data_ptr(), None, None, gx.data_ptr(), gb.data_ptr(), gc.data_ptr(),
+                       gdt.data_ptr(), glam.data_ptr(), ga.data_ptr(), gth.data_ptr(), None, None,
+                       None, None)
+    stream = torch.cuda.current_stream()
+    call = lambda: L_.check(lib.m3_scan_backward(C.byref(cin), C.byref(gr),
+                                                 C.c_void_p(stream.cuda_stream)))
+    for _ in range(max(2, args.warmup // 4)):
+        call()
+    torch.cuda.synchronize()
+    steps = max(5, args.steps // 4)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / steps * 1e3
+    assert bool(torch.isfinite(gx.float()).all()) and bool(torch.isfinite(ga).all())
+    nbytes = scan_backward_algorithmic(B, L, H, P, N, R)
+    tokens = B * L
+    return {"us_per_call": round(us, 2), "calls": steps,
+            "tokens_per_s_fwd_bwd": round(tokens / ((us * 1e-3 + fwd_ms) * 1e-3), 1),
+            "algorithmic_bytes": nbytes, "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "workspace_MB": round(need / 1e6, 1),
+            "note": "bf16 storage, f32 arithmetic (MFMA f32 16x16x4); includes the recompute "
+                    "of the forward chunk states"}
+
+
 def bench_decode_lm(torch, args):
     """One token per sequence through the 24-layer stack with the state cache
     updated in place: embedding, 24 x (RMSNorm, int8 in_proj, prologue, decode
@@ -419,6 +477,7 @@ def main():
     ap.add_argument("--no-decode-lm", action="store_true", help="skip the LM decode-step leg")
     ap.add_argument("--decode-lm-steps", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-backward", action="store_true", help="skip the scan backward leg")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--only", choices=("prefill", "decode_lm", "ingest"), default=None,
@@ -471,6 +530,8 @@ def main():
     ms_step = sc["wall_ms"]
     value = sc["tokens"] / (ms_step * 1e-3)
 
+    bwd = None if args.no_backward else bench_backward(torch, lib, L_, args, sc["inp"],
+                                                       sc["kernel_ms"])
     dec = None if args.no_decode else bench_decode(torch, lib, L_, args)
     pre = None if args.no_prefill else bench_prefill(torch, args)
     dlm = None if args.no_decode_lm else bench_decode_lm(torch, args)
@@ -505,6 +566,7 @@ def main():
                      "mfma_tflops": round(tflops, 2),
                      "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)},
         "scan_single_pass_us": round(sc1["kernel_ms"] * 1e3, 2),
+        "backward": bwd,
         "decode": dec,
         "prefill": pre,
         "decode_lm": dlm,

@@ -10,6 +10,10 @@
  *   m3_ssm_state                  SsmState                  src/ssm/scan.rs:293-358
  *   m3_scan_inputs / m3_scan      ScanInputs, mamba3_scan   src/ssm/scan.rs:360-618
  *   m3_scan_output                ScanOutput                src/ssm/scan.rs:445-452
+ *   m3_scan_grads / m3_scan_backward
+ *                                 gradient of mamba3_scan   src/ssm/scan.rs:458-638 under
+ *                                 autodiff (src/autodiff/), with the hand-written adjoints
+ *                                 src/tensor/ops/fused.rs:2080-2138, 2326-2382, 2513-2549
  *   m3_ssd_args / m3_ssd_chunked  ssd_chunked               src/ssm/scan.rs:98-291
  *   m3_step_inputs / m3_step      mamba3_step               src/ssm/scan.rs:640-712
  *   m3_status / m3_last_error     Error / Result            src/error.rs:5-61
@@ -142,6 +146,42 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
  * dtype are read; pointers are not); 0 when the shape runs single-pass only.
  * No reference counterpart (see m3_scan_inputs.workspace). */
 size_t m3_scan_workspace_bytes(const m3_scan_inputs *in);
+
+/* Gradients of mamba3_scan for the loss L, given dL/dy.  The reference gets
+ * them by reverse-mode autodiff through the composed scan (Var::backward over
+ * scan.rs:458-638; its own adjoint kernels are ssd_band_backward fused.rs:
+ * 2080-2138, exp_decay_backward 2326-2382 and trapezoid_weights_backward
+ * 2513-2549).  Layouts as m3_scan_inputs; dx, db, dc and dtheta are in the
+ * inputs' dtype, the rest f32.  The upstream gradient of the outgoing last_u
+ * is not accepted (training runs with want_state false, mamba3.rs:518). */
+typedef struct m3_scan_grads {
+    const void *dy;           /* [B, T, H, P, R]: dL/dy (required) */
+    const float *dh;          /* [B, H, P, N]: dL/d(output state h), or NULL */
+    const float *dangle;      /* [B, H, N/2]: dL/d(output state angle), or NULL */
+    void *dx;                 /* [B, T, H, P, R] (required) */
+    void *db;                 /* [B, T, H, N, R] (required) */
+    void *dc;                 /* [B, T, H, N, R] (required) */
+    float *ddt;               /* [B, T, H] (required) */
+    float *dlambda;           /* [B, T, H] (required) */
+    float *da_log;            /* [H] (required), summed over the batch */
+    void *dtheta;             /* [B, T, H, N/2], required when theta is given */
+    float *dd_skip;           /* [H] or NULL (written when d_skip is given) */
+    float *dh0;               /* [B, H, P, N] or NULL (carried-in state only) */
+    float *dlast_u0;          /* [B, H, P, N] or NULL (carried-in state only) */
+    float *dangle0;           /* [B, H, N/2] or NULL (carried-in angle only) */
+} m3_scan_grads;
+
+/* Backward of m3_scan on the same inputs (`in`, whose workspace must hold
+ * m3_scan_backward_workspace_bytes(in) bytes, 256-byte aligned).  The forward
+ * chunk states are recomputed; the forward outputs are not needed.  Covers
+ * head_dim 64, d_state 64/128, rank 1/2/4 with aligned buffers (else
+ * M3_ERR_UNSUPPORTED).  Partial sums inside a workgroup are accumulated with
+ * LDS atomics, so repeated calls agree to f32 rounding, not bit for bit. */
+m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *grads, void *stream);
+
+/* Workspace bytes m3_scan_backward needs for these inputs (0 when the shape
+ * is not covered).  No reference counterpart. */
+size_t m3_scan_backward_workspace_bytes(const m3_scan_inputs *in);
 
 /* ssd_chunked arguments (scan.rs:100-126): one input/output channel. */
 typedef struct m3_ssd_args {

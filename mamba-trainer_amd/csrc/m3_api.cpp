@@ -273,6 +273,116 @@ size_t m3_scan_workspace_bytes(const m3_scan_inputs *in) {
     return m3::scan_chunked_workspace(a);
 }
 
+static m3::ScanLaunch scan_launch_of(const m3_scan_inputs *in) {
+    m3::ScanLaunch a{};
+    a.batch = in->batch;
+    a.seq = in->seq;
+    a.heads = in->heads;
+    a.head_dim = in->head_dim;
+    a.d_state = in->d_state;
+    a.rank = in->rank;
+    a.bf16 = in->dtype == M3_BF16;
+    a.mode_raw = 1;
+    a.x = in->x;
+    a.b = in->b;
+    a.c = in->c;
+    a.dt = in->dt;
+    a.lambda = in->lambda;
+    a.a_log = in->a_log;
+    a.theta = in->theta;
+    a.d_skip = in->d_skip;
+    const m3_ssm_state *st = in->state;
+    a.h0 = st ? st->h : nullptr;
+    a.last_u0 = st ? st->last_u : nullptr;
+    a.angle0 = (st && in->theta) ? st->angle : nullptr;
+    return a;
+}
+
+m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, void *stream) {
+    if (in == nullptr || g == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/grads are NULL");
+    if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
+    if (in->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
+    if (in->head_dim == 0 || in->d_state == 0)
+        return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
+    if (in->theta != nullptr && in->d_state % 2 != 0)   // scan.rs:485-489
+        return fail(M3_ERR_CONFIG, "rotational dynamics require an even d_state");
+    const m3_ssm_state *st = in->state;
+    if (st != nullptr && (st->h == nullptr || st->last_u == nullptr))
+        return fail(M3_ERR_ARGUMENT, "state needs both h and last_u");
+    const size_t B = in->batch, H = in->heads, P = in->head_dim, N = in->d_state;
+    if (B * H == 0) return ok();
+    if (in->x == nullptr || in->b == nullptr || in->c == nullptr || in->dt == nullptr ||
+        in->a_log == nullptr || in->lambda == nullptr)
+        return fail(M3_ERR_ARGUMENT, "x, b, c, dt, a_log and lambda are required");
+    if (g->dy == nullptr || g->dx == nullptr || g->db == nullptr || g->dc == nullptr ||
+        g->ddt == nullptr || g->dlambda == nullptr || g->da_log == nullptr)
+        return fail(M3_ERR_ARGUMENT, "dy, dx, db, dc, ddt, dlambda and da_log are required");
+    if (in->theta != nullptr && g->dtheta == nullptr)
+        return fail(M3_ERR_ARGUMENT, "theta is given: dtheta is required");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipSuccess;
+    if (in->seq == 0) {
+        // empty window: the state passed through, nothing else was read
+        const size_t sbytes = B * H * P * N * sizeof(float);
+        e = hipMemsetAsync(g->da_log, 0, H * sizeof(float), s);
+        if (e == hipSuccess && g->dd_skip) e = hipMemsetAsync(g->dd_skip, 0, H * sizeof(float), s);
+        if (e == hipSuccess && g->dh0)
+            e = g->dh ? hipMemcpyAsync(g->dh0, g->dh, sbytes, hipMemcpyDeviceToDevice, s)
+                      : hipMemsetAsync(g->dh0, 0, sbytes, s);
+        if (e == hipSuccess && g->dlast_u0) e = hipMemsetAsync(g->dlast_u0, 0, sbytes, s);
+        if (e == hipSuccess && g->dangle0) {
+            const size_t abytes = B * H * (N / 2) * sizeof(float);
+            e = g->dangle ? hipMemcpyAsync(g->dangle0, g->dangle, abytes, hipMemcpyDeviceToDevice, s)
+                          : hipMemsetAsync(g->dangle0, 0, abytes, s);
+        }
+        if (e != hipSuccess) return hip_fail(e, "empty-window backward");
+        return ok();
+    }
+    const m3::ScanLaunch a = scan_launch_of(in);
+    if (!m3::scan_backward_supported(a))
+        return fail(M3_ERR_UNSUPPORTED,
+                    "the scan backward covers head_dim 64, d_state 64/128, rank 1/2/4 with "
+                    "16-byte aligned buffers");
+    const size_t need = m3::scan_backward_workspace(a);
+    if (in->workspace == nullptr || in->workspace_bytes < need ||
+        (reinterpret_cast<uintptr_t>(in->workspace) & 255u) != 0)
+        return fail(M3_ERR_ARGUMENT, "the backward needs a 256-byte aligned workspace of %zu bytes",
+                    need);
+    m3::ScanGrads gr{};
+    gr.dy = g->dy;
+    gr.dh_out = g->dh;
+    gr.dangle_out = in->theta ? g->dangle : nullptr;
+    gr.dx = g->dx;
+    gr.db = g->db;
+    gr.dc = g->dc;
+    gr.ddt = g->ddt;
+    gr.dlambda = g->dlambda;
+    gr.da_log = g->da_log;
+    gr.dtheta = in->theta ? g->dtheta : nullptr;
+    gr.dd_skip = in->d_skip ? g->dd_skip : nullptr;
+    gr.dh0 = st ? g->dh0 : nullptr;
+    gr.dlast_u0 = st ? g->dlast_u0 : nullptr;
+    gr.dangle0 = (st && st->angle && in->theta) ? g->dangle0 : nullptr;
+    e = m3::launch_scan_backward(a, gr, in->workspace, s);
+    if (e != hipSuccess) return hip_fail(e, "scan backward launch");
+    g_launches.fetch_add(in->theta ? 7 : 6, std::memory_order_relaxed);
+    if (g->dd_skip != nullptr && in->d_skip == nullptr) {
+        e = hipMemsetAsync(g->dd_skip, 0, H * sizeof(float), s);
+        if (e != hipSuccess) return hip_fail(e, "dd_skip");
+    }
+    return ok();
+}
+
+size_t m3_scan_backward_workspace_bytes(const m3_scan_inputs *in) {
+    if (in == nullptr || !dtype_ok(in->dtype) || in->seq == 0) return 0;
+    m3::ScanLaunch a = scan_launch_of(in);
+    alignas(16) static float dummy[4] = {0, 0, 0, 0};
+    a.x = a.b = a.c = dummy;   // alignment is checked at launch
+    a.theta = in->theta ? dummy : nullptr;
+    a.h0 = a.last_u0 = nullptr;
+    return m3::scan_backward_workspace(a);
+}
+
 m3_status m3_ssd_chunked(const m3_ssd_args *in, void *y, float *final_state, void *stream) {
     if (in == nullptr) return fail(M3_ERR_ARGUMENT, "arguments are NULL");
     if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);

@@ -50,6 +50,43 @@ hipError_t launch_scan_fast(const ScanLaunch &a, hipStream_t stream);
 // and the launch.
 size_t scan_chunked_workspace(const ScanLaunch &a);
 hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream);
+// The backward's recompute of the forward chunk states: chunk_state +
+// state_pass at scan_backward_rows() rows per chunk (the outputs of `a` are not written).  The view
+// gives the per-chunk sections inside the workspace: the state entering each
+// chunk (f32, MFMA D layout [chunk][p-tile][n-tile][lane][4]), the chunk
+// decay, and per rotation pair the
+// chunk angle total with its cosine and sine.
+struct ChunkStatesView {
+    const void *s;
+    const float *eda, *phi, *cph, *sph;
+    size_t nck, bytes;
+};
+// Rows (token, rank) per chunk of the backward: 32, or 64 for bf16 storage
+// with d_state 64 (whose 16-byte staging needs the longer chunk).
+inline int scan_backward_rows(const ScanLaunch &a) { return (a.bf16 && a.d_state == 64) ? 64 : 32; }
+ChunkStatesView scan_states_view(const ScanLaunch &a, void *workspace);
+hipError_t launch_scan_states(const ScanLaunch &a, void *workspace, hipStream_t stream);
+
+// Backward of the scan (mamba3_scan mode, the chunk-parallel shapes): the
+// gradients of the loss given dL/dy (and optionally dL/dh, dL/dangle of the
+// outgoing state).  Outputs in the storage type where the input has it.
+struct ScanGrads {
+    const void *dy;                 // [B,T,H,P,R]
+    const float *dh_out;            // [B,H,P,N] or null
+    const float *dangle_out;        // [B,H,N/2] or null
+    void *dx, *db, *dc;             // like x, b, c
+    float *ddt, *dlambda;           // [B,T,H]
+    float *da_log;                  // [H]
+    void *dtheta;                   // like theta, or null
+    float *dd_skip;                 // [H] or null
+    float *dh0, *dlast_u0;          // [B,H,P,N] or null
+    float *dangle0;                 // [B,H,N/2] or null
+};
+bool scan_backward_supported(const ScanLaunch &a);
+size_t scan_backward_workspace(const ScanLaunch &a);
+hipError_t launch_scan_backward(const ScanLaunch &a, const ScanGrads &g, void *workspace,
+                                hipStream_t stream);
+
 // The single-launch form with a decoupled look-back (bf16 storage, the shapes
 // above, mamba3_scan mode): workspace bytes (0 when not covered) and launch.
 bool scan_lookback_supported(const ScanLaunch &a);

@@ -1,0 +1,798 @@
+// Backward of the chunked SSD scan (mamba3_scan, src/ssm/scan.rs:458-638) for
+// gfx950: the gradient the reference obtains by autodiff through the composed
+// scan, whose hand-written adjoints are ssd_band_backward
+// (src/tensor/ops/fused.rs:2080-2138), exp_decay_backward (2326-2382) and
+// trapezoid_weights_backward (2513-2549).  Shapes as the chunk-parallel
+// forward: head_dim 64, d_state 64/128, rank 1/2/4; f32 or bf16 storage,
+// f32 arithmetic (MFMA f32 16x16x4 over f32 operands in LDS).
+//
+// Chunks of 32 rows (token, rank); 64 for bf16 storage with d_state 64.  In chunk k's own rotating frame, with
+// alpha the in-chunk inclusive cumsum of a = dt A, K_ts = W_ts e^{alpha_t -
+// alpha_s} (W = g on the token diagonal, w below it), CB = C~ B~^T, M = CB o K,
+// wbar_s = e^{alpha_E - alpha_s} w_s, S_k the state entering the chunk and
+// Gh_k = dL/d(e_k S_k + U_k) = R(-Phi_k) G_{k+1}:
+//
+//   dX       = M^T dY + D dY + diag(wbar) B~ Gh^T
+//   dC~      = (dY X^T o K) B~ + diag(e^alpha) dY S
+//   dB~      = (dY X^T o K)^T C~ + diag(wbar) X Gh
+//   G_k      = e_k Gh_k + (diag(e^alpha) dY)^T C~            (reverse state pass)
+//   dalpha_t = sum_{s<t} L_ts - sum_{t'>t} L_t't + e^{alpha_t} dy_t . (S C~_t)
+//              - wbar_t x_t . (Gh B~_t)   (+ the alpha_E terms on the last row),
+//              L = dM o M;  da = in-chunk reverse cumsum of dalpha
+//   dphi_t   = sum_pairs dB~1 B~2 - dB~2 B~1 + dC~1 C~2 - dC~2 C~1, invariant
+//              under the frame rotation, so the global angle gradient is its
+//              reverse cumsum over the whole sequence.
+//
+// Launches: the forward recompute of S_k (chunk_state + state_pass at 32 rows),
+// bwd_v_kernel (the chunk's direct share of G), bwd_state_pass_kernel (G and
+// Gh per chunk, and dh0 / dlast_u0), bwd_chunk_kernel (dx, db, dc and the
+// per-token da, dg, dw and angle sums), bwd_angle_kernel (the angle sums of
+// later chunks), bwd_token_kernel (dtheta, ddt, dlambda: trapezoid_weights
+// backward, the decay and angle chains) and bwd_head_kernel (da_log, dD).
+#include <algorithm>
+
+#include "scan_common.hpp"
+
+namespace m3 {
+
+namespace {
+
+constexpr int kP = 64;
+constexpr int kWaves = 8;
+constexpr int kBT = 64 * kWaves;
+
+struct BwdArgs {
+    const void *dy;           // [B,T,H,P,R]
+    const float *dh_out;      // [B,H,P,N] or null
+    const float *dangle_out;  // [B,H,N/2] or null
+    void *dx, *db, *dc;       // storage type
+    float *ddt, *dlambda;     // [B,T,H]
+    float *da_log;            // [H]
+    void *dtheta;             // [B,T,H,N/2] or null
+    float *dd_skip;           // [H] or null
+    float *dh0, *dlast_u0;    // [B,H,P,N] or null
+    float *dangle0;           // [B,H,N/2] or null
+};
+
+// Backward workspace, after the forward chunk states (ChunkStatesView.bytes).
+struct BwdLayout {
+    size_t v, gh, cin, ctot, off, da, dg, dw, pd, pa, pfirst, total;
+};
+
+size_t balign(size_t v) { return (v + 255) & ~size_t(255); }
+
+BwdLayout bwd_layout(size_t states_bytes, size_t bh, size_t nck, size_t seq, size_t n) {
+    const size_t bhk = bh * nck;
+    BwdLayout l;
+    size_t o = balign(states_bytes);
+    l.v = o;      o = balign(o + bhk * kP * n * 4);
+    l.gh = o;     o = balign(o + bhk * kP * n * 4);
+    l.cin = o;    o = balign(o + bh * seq * (n / 2) * 4);
+    l.ctot = o;   o = balign(o + bhk * (n / 2) * 4);
+    l.off = o;    o = balign(o + bhk * (n / 2) * 4);
+    l.da = o;     o = balign(o + bh * seq * 4);
+    l.dg = o;     o = balign(o + bh * seq * 4);
+    l.dw = o;     o = balign(o + bh * seq * 4);
+    l.pd = o;     o = balign(o + bhk * 4);
+    l.pa = o;     o = balign(o + bhk * 4);
+    l.pfirst = o; o = balign(o + bh * (n / 32) * 4);
+    l.total = o;
+    return l;
+}
+
+struct BwdWs {
+    ChunkStatesView fw;
+    float *v, *gh, *cin, *ctot, *off, *da, *dg, *dw, *pd, *pa, *pfirst;
+};
+
+// element access in the storage type
+template <typename T> __device__ __forceinline__ float ldv(const void *p, size_t i);
+template <> __device__ __forceinline__ float ldv<float>(const void *p, size_t i) {
+    return static_cast<const float *>(p)[i];
+}
+template <> __device__ __forceinline__ float ldv<bf16_t>(const void *p, size_t i) {
+    return to_f32(static_cast<const bf16_t *>(p)[i]);
+}
+template <typename T> __device__ __forceinline__ void stv(void *p, size_t i, float v);
+template <> __device__ __forceinline__ void stv<float>(void *p, size_t i, float v) {
+    static_cast<float *>(p)[i] = v;
+}
+template <> __device__ __forceinline__ void stv<bf16_t>(void *p, size_t i, float v) {
+    static_cast<bf16_t *>(p)[i] = from_f32<bf16_t>(v);
+}
+
+// (p, n) of element e of a [p-tile][n-tile][lane][4] MFMA D-layout record
+__device__ __forceinline__ void dl_pn(int e, int ntn, int &p, int &n) {
+    const int r = e & 3, lane = (e >> 2) & 63, tile = e >> 8;
+    const int i = tile % ntn, pt = tile / ntn;
+    p = 16 * pt + (lane & 15);
+    n = 16 * i + 4 * (lane >> 4) + r;
+}
+
+__device__ __forceinline__ float clamp_exp(float d) {
+    return expf(fminf(fmaxf(d, -60.0f), 0.0f));
+}
+
+template <bool PRECISE>
+__device__ __forceinline__ void sincos_any(float x, float &s, float &c) {
+    if constexpr (PRECISE) {
+        sincosf(x, &s, &c);
+    } else {
+        const float rev = wrap_angle(x) * 0.15915494309189533577f;
+        s = __builtin_amdgcn_sinf(rev);
+        c = __builtin_amdgcn_cosf(rev);
+    }
+}
+
+// D(16x16) += A(16 x K) B(K x 16) in f32: A(m, k) = a[m * am + k * ak],
+// B(k, n) = b[k * bk + n * bn]; lane (c, g) supplies A(c, k0+g), B(k0+g, c).
+__device__ __forceinline__ f32x4 mma_f32(const float *a, int am, int ak, const float *b, int bk,
+                                         int bn, int K, f32x4 acc, int c, int g) {
+    for (int k0 = 0; k0 < K; k0 += 4)
+        acc = mfma_f32(a[c * am + (k0 + g) * ak], b[(k0 + g) * bk + c * bn], acc);
+    return acc;
+}
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) s += red[w];
+    return s;
+}
+
+// ---------------------------------------------------------------- staging
+template <int N, int R, int kRows>
+struct Smem {
+    static constexpr int QT = kRows / R, NH = N / 2, NTN = N / 16;
+    static constexpr int LB = N + 1;     // B~, C~ rows; odd pitch: rows and columns both
+    static constexpr int LX = kP + 1;    // X, dY rows   read with at most 4-way conflicts
+    static constexpr int LM = kRows + 1; // M, dCB rows
+    static constexpr int LS = N + 1;     // S, Gh rows
+    float Bs[kRows * LB], Cs[kRows * LB];
+    float Xs[kRows * LX], Ys[kRows * LX];
+    float Ms[kRows * LM], Ds[kRows * LM];
+    float Ss[kP * LS], Gs[kP * LS];
+    float psi[QT * NH];     // in-chunk angle per token and pair
+    float cang[QT * NH];    // angle sums per token and pair
+    float dtv[QT], lamv[QT], acum[QT], gw[QT], ww[QT], eac[QT], ebar[QT], wbar[QT];
+    float rin[kRows], cinx[kRows], dwi[kRows], qv[kRows], rcr[kRows];
+    float dgv[QT], dal[QT];
+    float red[16];
+    float gs, pdsum;
+};
+
+// Per-token scalars, the in-chunk angles, and (X, dY) / (B~, C~) as asked.
+template <typename T, int N, int R, int kRows, bool WANT_B, bool WANT_X>
+__device__ void stage(const ScanLaunch &a, const BwdArgs &g, Smem<N, R, kRows> &sm, size_t bh,
+                      int ck) {
+    using S = Smem<N, R, kRows>;
+    constexpr int QT = S::QT, NH = S::NH;
+    constexpr bool kPrecise = true;   // precise sines whatever the storage
+    const int tid = threadIdx.x;
+    const size_t H = a.heads, L = a.seq;
+    const size_t bb = bh / H, hh = bh % H;
+    const bool rot = a.theta != nullptr;
+    const float A = 0.0f - expf(a.a_log[hh]);
+    if (tid < QT) {
+        const size_t t = static_cast<size_t>(ck) * QT + tid;
+        const bool live = t < L;
+        const size_t ix = (bb * L + t) * H + hh;
+        const float dt = live ? a.dt[ix] : 0.0f, lam = live ? a.lambda[ix] : 0.0f;
+        const bool nlive = t + 1 < L;
+        const float dtn = nlive ? a.dt[ix + H] : 0.0f, lamn = nlive ? a.lambda[ix + H] : 0.0f;
+        sm.dtv[tid] = dt;
+        sm.lamv[tid] = lam;
+        sm.acum[tid] = dt * A;
+        sm.gw[tid] = lam * dt;                          // fused.rs:2494
+        sm.ww[tid] = lam * dt + (1.0f - lamn) * dtn;    // fused.rs:2496-2498
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float run = 0.0f;
+        for (int t = 0; t < QT; ++t) {
+            run += sm.acum[t];
+            sm.acum[t] = run;
+        }
+    }
+    if (rot && tid >= 64 && tid < 64 + NH) {
+        const int i = tid - 64;
+        float run = 0.0f;
+        for (int t = 0; t < QT; ++t) {
+            const size_t tg = static_cast<size_t>(ck) * QT + t;
+            if (tg < L) run += sm.dtv[t] * ldv<T>(a.theta, ((bb * L + tg) * H + hh) * NH + i);
+            sm.psi[t * NH + i] = run;
+        }
+    }
+    __syncthreads();
+    if (tid < QT) {
+        const float e = sm.acum[QT - 1];
+        sm.eac[tid] = clamp_exp(sm.acum[tid]);
+        sm.ebar[tid] = clamp_exp(e - sm.acum[tid]);
+        sm.wbar[tid] = sm.ebar[tid] * sm.ww[tid];
+    }
+    if constexpr (WANT_B) {
+        for (int e = tid; e < QT * NH; e += blockDim.x) {
+            const int t = e / NH, i = e % NH;
+            const size_t tg = static_cast<size_t>(ck) * QT + t;
+            float sn = 0.0f, cs = 1.0f;
+            if (rot) sincos_any<kPrecise>(sm.psi[t * NH + i], sn, cs);
+            const bool live = tg < L;
+            const size_t base = ((bb * L + (live ? tg : 0)) * H + hh) * N * R;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int rho = t * R + r;
+                float b1 = 0.f, b2 = 0.f, c1 = 0.f, c2 = 0.f;
+                if (live) {
+                    b1 = ldv<T>(a.b, base + i * R + r);
+                    b2 = ldv<T>(a.b, base + (i + NH) * R + r);
+                    c1 = ldv<T>(a.c, base + i * R + r);
+                    c2 = ldv<T>(a.c, base + (i + NH) * R + r);
+                }
+                // rotation by -psi (fused.rs:610-617)
+                sm.Bs[rho * S::LB + i] = b1 * cs + b2 * sn;
+                sm.Bs[rho * S::LB + i + NH] = -b1 * sn + b2 * cs;
+                sm.Cs[rho * S::LB + i] = c1 * cs + c2 * sn;
+                sm.Cs[rho * S::LB + i + NH] = -c1 * sn + c2 * cs;
+            }
+        }
+    } else {
+        // C~ only
+        for (int e = tid; e < QT * NH; e += blockDim.x) {
+            const int t = e / NH, i = e % NH;
+            const size_t tg = static_cast<size_t>(ck) * QT + t;
+            float sn = 0.0f, cs = 1.0f;
+            if (rot) sincos_any<kPrecise>(sm.psi[t * NH + i], sn, cs);
+            const bool live = tg < L;
+            const size_t base = ((bb * L + (live ? tg : 0)) * H + hh) * N * R;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int rho = t * R + r;
+                float c1 = 0.f, c2 = 0.f;
+                if (live) {
+                    c1 = ldv<T>(a.c, base + i * R + r);
+                    c2 = ldv<T>(a.c, base + (i + NH) * R + r);
+                }
+                sm.Cs[rho * S::LB + i] = c1 * cs + c2 * sn;
+                sm.Cs[rho * S::LB + i + NH] = -c1 * sn + c2 * cs;
+            }
+        }
+    }
+    for (int e = tid; e < kRows * kP; e += blockDim.x) {
+        const int rho = e / kP, p = e % kP;
+        const int t = rho / R, r = rho % R;
+        const size_t tg = static_cast<size_t>(ck) * QT + t;
+        const bool live = tg < L;
+        const size_t ix = (((bb * L + (live ? tg : 0)) * H + hh) * kP + p) * R + r;
+        sm.Ys[rho * S::LX + p] = live ? ldv<T>(g.dy, ix) : 0.0f;
+        if constexpr (WANT_X) sm.Xs[rho * S::LX + p] = live ? ldv<T>(a.x, ix) : 0.0f;
+    }
+}
+
+// ---------------------------------------------------------------- V_k
+// V_k^T[n][p] = sum_rho C~[rho][n] e^{alpha} dY[rho][p]: the chunk's direct
+// share of dL/dS_k (the carry-in product y += e^alpha C~ S, scan.rs:253-263).
+template <typename T, int N, int R, int kRows>
+__global__ void __launch_bounds__(kBT, 1) bwd_v_kernel(ScanLaunch a, BwdArgs g, BwdWs w, int nck) {
+    using S = Smem<N, R, kRows>;
+    constexpr int NTN = N / 16;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    S &sm = *reinterpret_cast<S *>(smem_raw);
+    const size_t bhk = blockIdx.x;
+    const int ck = static_cast<int>(bhk % nck);
+    const size_t bh = bhk / nck;
+    stage<T, N, R, kRows, false, false>(a, g, sm, bh, ck);
+    __syncthreads();
+    // scale dY rows by e^{alpha}
+    for (int e = threadIdx.x; e < kRows * kP; e += blockDim.x) {
+        const int rho = e / kP;
+        sm.Ys[rho * S::LX + e % kP] *= sm.eac[rho / R];
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, gq = lane >> 4;
+    float *v = w.v + bhk * kP * N;
+    for (int tile = wave; tile < 4 * NTN; tile += kWaves) {
+        const int pt = tile / NTN, i = tile % NTN;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        // A(m = n, k = rho) = C~[rho][n]; B(k = rho, col = p) = dY'[rho][p]
+        acc = mma_f32(sm.Cs + 16 * i, 1, S::LB, sm.Ys + 16 * pt, S::LX, 1, kRows, acc, c, gq);
+        *reinterpret_cast<f32x4 *>(v + ((pt * NTN + i) * 64 + lane) * 4) = acc;
+    }
+}
+
+// ---------------------------------------------------------------- reverse state pass
+// G_C = R(phi_end) dh_out (or 0); for k = C-1 .. 0: Gh_k = R(-Phi_k) G_{k+1},
+// G_k = e_k Gh_k + V_k.  Then S_0 = R(angle0)(h0 + (1 - lambda_0) dt_0 last_u0)
+// gives dh0, dlast_u0 and the gradient of (1 - lambda_0) dt_0 (scan.rs:521-535).
+template <int N>
+__global__ void __launch_bounds__(256) bwd_state_pass_kernel(ScanLaunch a, BwdArgs g, BwdWs w,
+                                                             int nck) {
+    constexpr int NTN = N / 16, HT = NTN / 2, NH = N / 2;
+    const int tid = threadIdx.x, lane = tid & 63, pt = tid >> 6;
+    const int c = lane & 15, gq = lane >> 4;
+    const int i1 = static_cast<int>(blockIdx.x % HT);
+    const size_t bh = blockIdx.x / HT;
+    const size_t H = a.heads, L = a.seq;
+    const size_t bb = bh / H, hh = bh % H;
+    const bool rot = a.theta != nullptr;
+    const int p = 16 * pt + c, nlo = 16 * i1 + 4 * gq;
+    const size_t sbase = bh * kP * N + static_cast<size_t>(p) * N;
+    auto rot4 = [](f32x4 &lo, f32x4 &hi, f32x4 cs, f32x4 sn) {
+        const f32x4 l = lo;
+        lo = l * cs - hi * sn;
+        hi = l * sn + hi * cs;
+    };
+    auto sincos4 = [](f32x4 t, f32x4 &sn, f32x4 &cs) {
+        for (int r = 0; r < 4; ++r) {
+            float s, cc;
+            sincosf(t[r], &s, &cc);
+            sn[r] = s;
+            cs[r] = cc;
+        }
+    };
+    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+    if (g.dh_out != nullptr) {
+        lo = *reinterpret_cast<const f32x4 *>(g.dh_out + sbase + nlo);
+        hi = *reinterpret_cast<const f32x4 *>(g.dh_out + sbase + nlo + NH);
+        if (rot) {
+            // phi_end = angle0 + sum_k Phi_k: the final frame, S_C = R(phi_end) h_out
+            f32x4 ph = {0.f, 0.f, 0.f, 0.f};
+            if (a.angle0 != nullptr) ph = *reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo);
+            for (int k = 0; k < nck; ++k)
+                ph += *reinterpret_cast<const f32x4 *>(w.fw.phi + (bh * nck + k) * NH + nlo);
+            f32x4 sn, cs;
+            sincos4(ph, sn, cs);
+            rot4(lo, hi, cs, sn);
+        }
+    }
+    for (int k = nck - 1; k >= 0; --k) {
+        const size_t bhk = bh * nck + k;
+        if (rot) {
+            const f32x4 cs = *reinterpret_cast<const f32x4 *>(w.fw.cph + bhk * NH + nlo);
+            const f32x4 sn = *reinterpret_cast<const f32x4 *>(w.fw.sph + bhk * NH + nlo);
+            rot4(lo, hi, cs, -sn);   // R(-Phi_k)
+        }
+        const size_t o = bhk * kP * N + ((pt * NTN + i1) * 64 + lane) * 4;
+        const size_t oh = bhk * kP * N + ((pt * NTN + i1 + HT) * 64 + lane) * 4;
+        *reinterpret_cast<f32x4 *>(w.gh + o) = lo;
+        *reinterpret_cast<f32x4 *>(w.gh + oh) = hi;
+        const float e = w.fw.eda[bhk];
+        lo = lo * e + *reinterpret_cast<const f32x4 *>(w.v + o);
+        hi = hi * e + *reinterpret_cast<const f32x4 *>(w.v + oh);
+    }
+    // into the global frame: dZ0 = R(-angle0) G_0
+    if (rot && a.angle0 != nullptr) {
+        f32x4 sn, cs;
+        sincos4(*reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo), sn, cs);
+        rot4(lo, hi, cs, -sn);
+    }
+    float dfirst = 0.0f;
+    if (a.h0 != nullptr) {
+        if (g.dh0 != nullptr) {
+            *reinterpret_cast<f32x4 *>(g.dh0 + sbase + nlo) = lo;
+            *reinterpret_cast<f32x4 *>(g.dh0 + sbase + nlo + NH) = hi;
+        }
+        if (a.last_u0 != nullptr) {
+            const size_t i0 = (bb * L) * H + hh;
+            const float first = (1.0f - a.lambda[i0]) * a.dt[i0];
+            const f32x4 ul = *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo);
+            const f32x4 uh = *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo + NH);
+            for (int r = 0; r < 4; ++r) dfirst += lo[r] * ul[r] + hi[r] * uh[r];
+            if (g.dlast_u0 != nullptr) {
+                *reinterpret_cast<f32x4 *>(g.dlast_u0 + sbase + nlo) = lo * first;
+                *reinterpret_cast<f32x4 *>(g.dlast_u0 + sbase + nlo + NH) = hi * first;
+            }
+        }
+    }
+    __shared__ float red[16];
+    dfirst = block_sum(dfirst, red);
+    if (tid == 0) w.pfirst[blockIdx.x] = dfirst;
+}
+
+// ---------------------------------------------------------------- chunk gradients
+template <typename T, int N, int R, int kRows>
+__global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs g, BwdWs w,
+                                                           int nck) {
+    using S = Smem<N, R, kRows>;
+    constexpr int NT = kRows / 16;
+    constexpr int QT = S::QT, NH = S::NH, NTN = N / 16;
+    constexpr int LB = S::LB, LX = S::LX, LM = S::LM, LS = S::LS;
+    constexpr bool kPrecise = true;   // precise sines whatever the storage
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    S &sm = *reinterpret_cast<S *>(smem_raw);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 15, gq = lane >> 4;
+    const size_t bhk = blockIdx.x;
+    const int ck = static_cast<int>(bhk % nck);
+    const size_t bh = bhk / nck;
+    const size_t H = a.heads, L = a.seq;
+    const size_t bb = bh / H, hh = bh % H;
+    const float D = a.d_skip ? a.d_skip[hh] : 0.0f;
+
+    stage<T, N, R, kRows, true, true>(a, g, sm, bh, ck);
+    // the state entering the chunk and Gh, [p][n]
+    for (int e = tid; e < kP * N; e += blockDim.x) {
+        int p, n;
+        dl_pn(e, NTN, p, n);
+        sm.Ss[p * LS + n] = static_cast<const float *>(w.fw.s)[bhk * kP * N + e];
+        sm.Gs[p * LS + n] = w.gh[bhk * kP * N + e];
+    }
+    for (int e = tid; e < kRows * LM; e += blockDim.x) {
+        sm.Ms[e] = 0.0f;
+        sm.Ds[e] = 0.0f;
+    }
+    for (int e = tid; e < QT * NH; e += blockDim.x) sm.cang[e] = 0.0f;
+    if (tid < kRows) {
+        sm.rin[tid] = sm.cinx[tid] = sm.dwi[tid] = sm.qv[tid] = sm.rcr[tid] = 0.0f;
+    }
+    if (tid < QT) sm.dgv[tid] = 0.0f;
+    __syncthreads();
+
+    // ---- band tiles (t-tile tj, s-tile si <= tj); tiles above lie above the token diagonal
+    for (int tile = wave; tile < NT * NT; tile += kWaves) {
+        const int tj = tile / NT, si = tile % NT;
+        if (si > tj) continue;
+        f32x4 cb = {0.f, 0.f, 0.f, 0.f}, dm = cb;
+        // CB[t][s] = sum_n C~[t][n] B~[s][n]; dM[t][s] = sum_p dY[t][p] X[s][p]
+        cb = mma_f32(sm.Cs + 16 * tj * LB, LB, 1, sm.Bs + 16 * si * LB, 1, LB, N, cb, c, gq);
+        dm = mma_f32(sm.Ys + 16 * tj * LX, LX, 1, sm.Xs + 16 * si * LX, 1, LX, kP, dm, c, gq);
+        const int s = 16 * si + c, ts = s / R;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tj + 4 * gq + r, tt = t / R;
+            if (tt < ts) continue;
+            const float E = clamp_exp(sm.acum[tt] - sm.acum[ts]);
+            const float W = tt == ts ? sm.gw[ts] : sm.ww[ts];
+            const float K = W * E;
+            const float m = cb[r] * K;
+            sm.Ms[t * LM + s] = m;
+            sm.Ds[t * LM + s] = dm[r] * K;
+            if (tt == ts) {
+                atomicAdd(&sm.dgv[ts], dm[r] * cb[r]);
+            } else {
+                const float lam = dm[r] * m;
+                atomicAdd(&sm.rin[t], lam);
+                atomicAdd(&sm.cinx[s], lam);
+                atomicAdd(&sm.dwi[s], dm[r] * cb[r] * E);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- dX^T[p][s] = wbar_s sum_n Gh[p][n] B~[s][n] + sum_t dY[t][p] M[t][s] + D dY[s][p]
+    for (int tile = wave; tile < 4 * NT; tile += kWaves) {
+        const int pt = tile & 3, st = tile >> 2;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = mma_f32(sm.Gs + 16 * pt * LS, LS, 1, sm.Bs + 16 * st * LB, 1, LB, N, acc, c, gq);
+        const int s = 16 * st + c, ts = s / R, rs = s % R;
+        acc = acc * sm.wbar[ts];
+        acc = mma_f32(sm.Ys + 16 * pt, 1, LX, sm.Ms + 16 * st, LM, 1, kRows, acc, c, gq);
+        const size_t tg = static_cast<size_t>(ck) * QT + ts;
+        if (tg < L) {
+            const size_t base = ((bb * L + tg) * H + hh) * kP * R;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int p = 16 * pt + 4 * gq + r;
+                stv<T>(g.dx, base + p * R + rs, acc[r] + D * sm.Ys[s * LX + p]);
+            }
+        }
+    }
+
+    // ---- dC~ and dB~ as [n][row] tiles; job = (pair tile i, row tile), one per wave in turn
+    constexpr int PT = NTN / 2;
+    for (int job = wave; job < NT * PT; job += kWaves) {
+        const int i = job % PT, rt = job / PT;
+        const int row = 16 * rt + c, tr = row / R, rr = row % R;
+        const size_t tg = static_cast<size_t>(ck) * QT + tr;
+        const bool live = tg < L;
+        float sn[4], cs[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sn[r] = 0.0f;
+            cs[r] = 1.0f;
+            if (a.theta != nullptr) sincos_any<kPrecise>(sm.psi[tr * NH + 16 * i + 4 * gq + r], sn[r], cs[r]);
+        }
+        // dC~^T[n][t] = e^{alpha_t} sum_p S[p][n] dY[t][p] + sum_s B~[s][n] dCB[t][s]
+        f32x4 dcl = {0.f, 0.f, 0.f, 0.f}, dch = dcl;
+        dcl = mma_f32(sm.Ss + 16 * i, 1, LS, sm.Ys + 16 * rt * LX, 1, LX, kP, dcl, c, gq);
+        dch = mma_f32(sm.Ss + 16 * (i + PT), 1, LS, sm.Ys + 16 * rt * LX, 1, LX, kP, dch, c, gq);
+        const float ea = sm.eac[tr];
+        dcl = dcl * ea;
+        dch = dch * ea;
+        {
+            float rc = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int n = 16 * i + 4 * gq + r;
+                rc += dcl[r] * sm.Cs[row * LB + n] + dch[r] * sm.Cs[row * LB + n + NH];
+            }
+            atomicAdd(&sm.rcr[row], rc);
+        }
+        dcl = mma_f32(sm.Bs + 16 * i, 1, LB, sm.Ds + 16 * rt * LM, 1, LM, kRows, dcl, c, gq);
+        dch = mma_f32(sm.Bs + 16 * (i + PT), 1, LB, sm.Ds + 16 * rt * LM, 1, LM, kRows, dch, c, gq);
+        // dB~^T[n][s] = wbar_s sum_p Gh[p][n] X[s][p] + sum_t C~[t][n] dCB[t][s]
+        f32x4 dbl = {0.f, 0.f, 0.f, 0.f}, dbh = dbl;
+        dbl = mma_f32(sm.Gs + 16 * i, 1, LS, sm.Xs + 16 * rt * LX, 1, LX, kP, dbl, c, gq);
+        dbh = mma_f32(sm.Gs + 16 * (i + PT), 1, LS, sm.Xs + 16 * rt * LX, 1, LX, kP, dbh, c, gq);
+        {
+            float q = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int n = 16 * i + 4 * gq + r;
+                q += dbl[r] * sm.Bs[row * LB + n] + dbh[r] * sm.Bs[row * LB + n + NH];
+            }
+            atomicAdd(&sm.qv[row], q);
+        }
+        const float wb = sm.wbar[tr];
+        dbl = dbl * wb;
+        dbh = dbh * wb;
+        dbl = mma_f32(sm.Cs + 16 * i, 1, LB, sm.Ds + 16 * rt, LM, 1, kRows, dbl, c, gq);
+        dbh = mma_f32(sm.Cs + 16 * (i + PT), 1, LB, sm.Ds + 16 * rt, LM, 1, kRows, dbh, c, gq);
+        // angle sums and the rotation back, dB = R(psi) dB~ (the transpose of fused.rs:610-617)
+        const size_t base = ((bb * L + (live ? tg : 0)) * H + hh) * N * R;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int n = 16 * i + 4 * gq + r;
+            const float b1 = sm.Bs[row * LB + n], b2 = sm.Bs[row * LB + n + NH];
+            const float c1 = sm.Cs[row * LB + n], c2 = sm.Cs[row * LB + n + NH];
+            const float cross = dbl[r] * b2 - dbh[r] * b1 + dcl[r] * c2 - dch[r] * c1;
+            if (a.theta != nullptr) atomicAdd(&sm.cang[tr * NH + n], cross);
+            if (live) {
+                stv<T>(g.db, base + n * R + rr, dbl[r] * cs[r] - dbh[r] * sn[r]);
+                stv<T>(g.db, base + (n + NH) * R + rr, dbl[r] * sn[r] + dbh[r] * cs[r]);
+                stv<T>(g.dc, base + n * R + rr, dcl[r] * cs[r] - dch[r] * sn[r]);
+                stv<T>(g.dc, base + (n + NH) * R + rr, dcl[r] * sn[r] + dch[r] * cs[r]);
+            }
+        }
+    }
+
+    // ---- <Gh, S> and the skip's sum dY . X
+    {
+        float gsum = 0.0f, dsum = 0.0f;
+        for (int e = tid; e < kP * N; e += blockDim.x) {
+            const int p = e / N, n = e % N;
+            gsum += sm.Gs[p * LS + n] * sm.Ss[p * LS + n];
+        }
+        for (int e = tid; e < kRows * kP; e += blockDim.x) {
+            const int rho = e / kP, p = e % kP;
+            dsum += sm.Ys[rho * LX + p] * sm.Xs[rho * LX + p];
+        }
+        gsum = block_sum(gsum, sm.red);
+        dsum = block_sum(dsum, sm.red + 8);
+        if (tid == 0) {
+            sm.gs = gsum;
+            w.pd[bhk] = dsum;
+        }
+    }
+    __syncthreads();
+
+    // ---- per-token scalars: dalpha, then da = in-chunk reverse cumsum
+    if (tid < QT) {
+        float d = 0.0f, dw = 0.0f;
+        for (int r = 0; r < R; ++r) {
+            const int row = tid * R + r;
+            d += sm.rin[row] - sm.cinx[row] + sm.rcr[row] - sm.qv[row] * sm.wbar[tid];
+            dw += sm.dwi[row] + sm.qv[row] * sm.ebar[tid];
+        }
+        if (tid == QT - 1) {
+            float e = 0.0f;
+            for (int row = 0; row < kRows; ++row) e += sm.qv[row] * sm.wbar[row / R];
+            d += e + w.fw.eda[bhk] * sm.gs;
+        }
+        sm.dal[tid] = d;
+        const size_t tg = static_cast<size_t>(ck) * QT + tid;
+        if (tg < L) {
+            w.dg[bh * L + tg] = sm.dgv[tid];
+            w.dw[bh * L + tg] = dw;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float run = 0.0f;
+        for (int t = QT - 1; t >= 0; --t) {
+            run += sm.dal[t];
+            const size_t tg = static_cast<size_t>(ck) * QT + t;
+            if (tg < L) w.da[bh * L + tg] = run;
+        }
+    }
+    if (a.theta != nullptr && tid >= 64 && tid < 64 + NH) {
+        const int i = tid - 64;
+        float run = 0.0f;
+        for (int t = QT - 1; t >= 0; --t) {
+            run += sm.cang[t * NH + i];
+            const size_t tg = static_cast<size_t>(ck) * QT + t;
+            if (tg < L) w.cin[(bh * L + tg) * NH + i] = run;
+        }
+        w.ctot[bhk * NH + i] = run;
+    }
+}
+
+// ---------------------------------------------------------------- angle sums of later chunks
+template <int N>
+__global__ void bwd_angle_kernel(ScanLaunch a, BwdArgs g, BwdWs w, int nck) {
+    constexpr int NH = N / 2;
+    const size_t bh = blockIdx.x;
+    const int i = threadIdx.x;
+    if (i >= NH) return;
+    float run = g.dangle_out ? g.dangle_out[bh * NH + i] : 0.0f;
+    for (int k = nck - 1; k >= 0; --k) {
+        w.off[(bh * nck + k) * NH + i] = run;
+        run += w.ctot[(bh * nck + k) * NH + i];
+    }
+    if (g.dangle0 != nullptr) g.dangle0[bh * NH + i] = run;
+}
+
+// ---------------------------------------------------------------- per token
+// dtheta_t = dt_t dphi_t, ddt_t = theta_t . dphi_t + A da_t
+//   + lambda_t (dg_t + dw_t) + (1 - lambda_t) dw_{t-1},
+// dlambda_t = dt_t (dg_t + dw_t) - dt_t dw_{t-1}    (trapezoid_weights_backward,
+// fused.rs:2513-2549), plus the carried-in boundary term at t = 0.
+// One workgroup per chunk, one wave per token, lane = rotation pair.
+template <typename T, int N, int R, int kRows>
+__global__ void __launch_bounds__(256) bwd_token_kernel(ScanLaunch a, BwdArgs g, BwdWs w, int nck) {
+    constexpr int NH = N / 2, QT = kRows / R;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t bhk = blockIdx.x;
+    const int ck = static_cast<int>(bhk % nck);
+    const size_t bh = bhk / nck;
+    const size_t H = a.heads, L = a.seq;
+    const size_t bb = bh / H, hh = bh % H;
+    const float A = 0.0f - expf(a.a_log[hh]);
+    const bool rot = a.theta != nullptr;
+    float asum = 0.0f;
+    for (int t = wave; t < QT; t += 4) {
+        const size_t tg = static_cast<size_t>(ck) * QT + t;
+        if (tg >= L) break;
+        const size_t ix = (bb * L + tg) * H + hh;
+        const float dt = a.dt[ix], lam = a.lambda[ix];
+        float part = 0.0f;
+        if (rot && lane < NH) {
+            const float dphi = w.cin[(bh * L + tg) * NH + lane] + w.off[bhk * NH + lane];
+            if (g.dtheta != nullptr) stv<T>(g.dtheta, ix * NH + lane, dt * dphi);
+            part = ldv<T>(a.theta, ix * NH + lane) * dphi;
+        }
+        part = group_sum(part, 64);
+        if (lane == 0) {
+            const float da = w.da[bh * L + tg];
+            const float dgw = w.dg[bh * L + tg] + w.dw[bh * L + tg];
+            const float dwp = tg > 0 ? w.dw[bh * L + tg - 1] : 0.0f;
+            float ddt = part + A * da + lam * dgw + (1.0f - lam) * dwp;
+            float dlam = dt * dgw - dt * dwp;
+            if (tg == 0 && a.h0 != nullptr && a.last_u0 != nullptr) {
+                float dfirst = 0.0f;
+                for (int j = 0; j < N / 32; ++j) dfirst += w.pfirst[bh * (N / 32) + j];
+                ddt += (1.0f - lam) * dfirst;
+                dlam -= dt * dfirst;
+            }
+            g.ddt[ix] = ddt;
+            g.dlambda[ix] = dlam;
+            asum += dt * da;
+        }
+    }
+    __shared__ float red[16];
+    asum = block_sum(asum, red);
+    if (threadIdx.x == 0) w.pa[bhk] = asum;
+}
+
+// ---------------------------------------------------------------- per head
+__global__ void bwd_head_kernel(ScanLaunch a, BwdArgs g, BwdWs w, int nck) {
+    const size_t hh = blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t H = a.heads;
+    if (hh >= H) return;
+    const float A = 0.0f - expf(a.a_log[hh]);
+    float sa = 0.0f, sd = 0.0f;
+    for (size_t bb = 0; bb < a.batch; ++bb)
+        for (int k = 0; k < nck; ++k) {
+            const size_t bhk = (bb * H + hh) * nck + k;
+            sa += w.pa[bhk];
+            sd += w.pd[bhk];
+        }
+    g.da_log[hh] = A * sa;     // A = -exp(a_log): dA/da_log = A
+    if (g.dd_skip != nullptr) g.dd_skip[hh] = sd;
+}
+
+template <typename K>
+hipError_t set_lds(K kern, size_t bytes) {
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+}
+
+template <typename T, int N, int R, int RW>
+hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStream_t s) {
+    hipError_t e = launch_scan_states(a, base, s);
+    if (e != hipSuccess) return e;
+    const ChunkStatesView fw = scan_states_view(a, base);
+    const int nck = static_cast<int>(fw.nck);
+    const size_t bh = a.batch * a.heads, bhk = bh * nck;
+    const BwdLayout l = bwd_layout(fw.bytes, bh, nck, a.seq, N);
+    BwdWs w;
+    w.fw = fw;
+    w.v = reinterpret_cast<float *>(base + l.v);
+    w.gh = reinterpret_cast<float *>(base + l.gh);
+    w.cin = reinterpret_cast<float *>(base + l.cin);
+    w.ctot = reinterpret_cast<float *>(base + l.ctot);
+    w.off = reinterpret_cast<float *>(base + l.off);
+    w.da = reinterpret_cast<float *>(base + l.da);
+    w.dg = reinterpret_cast<float *>(base + l.dg);
+    w.dw = reinterpret_cast<float *>(base + l.dw);
+    w.pd = reinterpret_cast<float *>(base + l.pd);
+    w.pa = reinterpret_cast<float *>(base + l.pa);
+    w.pfirst = reinterpret_cast<float *>(base + l.pfirst);
+
+    const size_t lds = sizeof(Smem<N, R, RW>);
+    static const hipError_t a1 = set_lds(bwd_v_kernel<T, N, R, RW>, lds);
+    static const hipError_t a2 = set_lds(bwd_chunk_kernel<T, N, R, RW>, lds);
+    if (a1 != hipSuccess) return a1;
+    if (a2 != hipSuccess) return a2;
+    hipLaunchKernelGGL((bwd_v_kernel<T, N, R, RW>), dim3(bhk), dim3(kBT), lds, s, a, g, w, nck);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL((bwd_state_pass_kernel<N>), dim3(bh * (N / 32)), dim3(256), 0, s, a, g, w,
+                       nck);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL((bwd_chunk_kernel<T, N, R, RW>), dim3(bhk), dim3(kBT), lds, s, a, g, w, nck);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (a.theta != nullptr) {
+        hipLaunchKernelGGL((bwd_angle_kernel<N>), dim3(bh), dim3(64), 0, s, a, g, w, nck);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((bwd_token_kernel<T, N, R, RW>), dim3(bhk), dim3(256), 0, s, a, g, w, nck);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(bwd_head_kernel, dim3((a.heads + 63) / 64), dim3(64), 0, s, a, g, w, nck);
+    return hipGetLastError();
+}
+
+template <typename T, int N64ROWS>
+hipError_t launch_bwd_t(const ScanLaunch &a, const BwdArgs &g, char *ws, hipStream_t s) {
+    const size_t n = a.d_state, r = a.rank;
+    if (n == 128) {
+        if (r == 1) return launch_bwd<T, 128, 1, 32>(a, g, ws, s);
+        if (r == 2) return launch_bwd<T, 128, 2, 32>(a, g, ws, s);
+        if (r == 4) return launch_bwd<T, 128, 4, 32>(a, g, ws, s);
+    } else if (n == 64) {
+        if (r == 1) return launch_bwd<T, 64, 1, N64ROWS>(a, g, ws, s);
+        if (r == 2) return launch_bwd<T, 64, 2, N64ROWS>(a, g, ws, s);
+        if (r == 4) return launch_bwd<T, 64, 4, N64ROWS>(a, g, ws, s);
+    }
+    return hipErrorNotSupported;
+}
+
+}  // namespace
+
+bool scan_backward_supported(const ScanLaunch &a) {
+    return a.mode_raw && a.seq > 0 && scan_fast_supported(a);
+}
+
+size_t scan_backward_workspace(const ScanLaunch &a) {
+    if (!scan_backward_supported(a)) return 0;
+    const ChunkStatesView fw = scan_states_view(a, nullptr);
+    return bwd_layout(fw.bytes, a.batch * a.heads, fw.nck, a.seq, a.d_state).total;
+}
+
+hipError_t launch_scan_backward(const ScanLaunch &a, const ScanGrads &gr, void *workspace,
+                                hipStream_t stream) {
+    if (!scan_backward_supported(a)) return hipErrorNotSupported;
+    BwdArgs g;
+    g.dy = gr.dy;
+    g.dh_out = gr.dh_out;
+    g.dangle_out = gr.dangle_out;
+    g.dx = gr.dx;
+    g.db = gr.db;
+    g.dc = gr.dc;
+    g.ddt = gr.ddt;
+    g.dlambda = gr.dlambda;
+    g.da_log = gr.da_log;
+    g.dtheta = gr.dtheta;
+    g.dd_skip = gr.dd_skip;
+    g.dh0 = gr.dh0;
+    g.dlast_u0 = gr.dlast_u0;
+    g.dangle0 = gr.dangle0;
+    char *ws = static_cast<char *>(workspace);
+    if (a.bf16) return launch_bwd_t<bf16_t, 64>(a, g, ws, stream);
+    return launch_bwd_t<float, 32>(a, g, ws, stream);
+}
+
+}  // namespace m3

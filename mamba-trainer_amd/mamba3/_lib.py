@@ -51,6 +51,12 @@ class ScanInputsC(C.Structure):
     ]
 
 
+class ScanGradsC(C.Structure):
+    """m3_scan_grads (include/mamba3_ssm.h)."""
+    _fields_ = [(n, _P) for n in ("dy", "dh", "dangle", "dx", "db", "dc", "ddt", "dlambda",
+                                  "da_log", "dtheta", "dd_skip", "dh0", "dlast_u0", "dangle0")]
+
+
 class ScanOutputC(C.Structure):
     _fields_ = [("y", _P), ("state", SsmStateC)]
 
@@ -92,6 +98,8 @@ SIGNATURES = {
     "m3_discretization_fixed_lambda": (C.c_float, [C.c_int32]),
     "m3_scan": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanOutputC), _P]),
     "m3_scan_workspace_bytes": (_Z, [C.POINTER(ScanInputsC)]),
+    "m3_scan_backward": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanGradsC), _P]),
+    "m3_scan_backward_workspace_bytes": (_Z, [C.POINTER(ScanInputsC)]),
     "m3_ssd_chunked": (C.c_int, [C.POINTER(SsdArgsC), _P, _P, _P]),
     "m3_step": (C.c_int, [C.POINTER(StepInputsC), C.POINTER(SsmStateC), _P, _P]),
     "m3_status_string": (C.c_char_p, [C.c_int]),

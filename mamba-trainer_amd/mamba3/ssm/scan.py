@@ -136,7 +136,129 @@ class ScanOutput:
 
 
 def mamba3_scan(inputs: ScanInputs) -> ScanOutput:
-    """scan.rs:454-618: the Mamba-3 selective scan, one kernel launch."""
+    """scan.rs:454-618: the Mamba-3 selective scan.
+
+    Differentiable like the reference's Var-based scan: when autograd is on and
+    an input requires grad, the backward is m3_scan_backward (the gradient the
+    reference gets by autodiff through the composed scan)."""
+    tensors = _scan_tensors(inputs)
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        cfg = (inputs.chunk_size, inputs.want_state, inputs.chunk_parallel)
+        y, h, lu, ang = _ScanFn.apply(cfg, *tensors)
+        return ScanOutput(y, SsmState(h, lu, ang) if inputs.want_state else None)
+    return _scan_forward(inputs)
+
+
+def _scan_tensors(inputs: ScanInputs):
+    st = inputs.state
+    return (inputs.x, inputs.b, inputs.c, inputs.dt, inputs.a_log, inputs.lam, inputs.theta,
+            inputs.d_skip, st.h if st else None, st.last_u if st else None,
+            st.angle if st else None)
+
+
+def _inputs_of(cfg, x, b, c, dt, a_log, lam, theta, d_skip, h0, last_u0, angle0) -> ScanInputs:
+    si = ScanInputs(x, b, c, dt, a_log, lam)
+    si.theta, si.d_skip = theta, d_skip
+    si.state = SsmState(h0, last_u0, angle0) if h0 is not None else None
+    si.chunk_size, si.want_state, si.chunk_parallel = cfg
+    return si
+
+
+class _ScanFn(torch.autograd.Function):
+    """mamba3_scan as one differentiable node: forward m3_scan, backward
+    m3_scan_backward (which recomputes the chunk states it needs)."""
+
+    @staticmethod
+    def forward(ctx, cfg, *tensors):
+        with torch.no_grad():
+            out = _scan_forward(_inputs_of(cfg, *tensors))
+        ctx.cfg = cfg
+        ctx.save_for_backward(*tensors)
+        ctx.set_materialize_grads(False)
+        st = out.state
+        return (out.y, st.h if st else None, st.last_u if st else None,
+                st.angle if st else None)
+
+    @staticmethod
+    def backward(ctx, dy, dh, dlu, dang):
+        tensors = ctx.saved_tensors
+        if dlu is not None and bool(torch.any(dlu != 0)):
+            raise UnsupportedError("unsupported: a gradient through the output state's last_u")
+        x = tensors[0]
+        if dy is None:
+            dy = torch.zeros_like(x)
+        g = mamba3_scan_backward(_inputs_of(ctx.cfg, *tensors), dy, dh, dang)
+        order = (g.x, g.b, g.c, g.dt, g.a_log, g.lam, g.theta, g.d_skip, g.h0, g.last_u0,
+                 g.angle0)
+        grads = [None if (t is None or gt is None) else gt.to(t.dtype).view_as(t)
+                 for t, gt in zip(tensors, order)]
+        return (None, *grads)
+
+
+@dataclass
+class ScanGrads:
+    """Gradients of mamba3_scan's inputs (None where the input is absent)."""
+    x: torch.Tensor
+    b: torch.Tensor
+    c: torch.Tensor
+    dt: torch.Tensor
+    a_log: torch.Tensor
+    lam: torch.Tensor
+    theta: Optional[torch.Tensor]
+    d_skip: Optional[torch.Tensor]
+    h0: Optional[torch.Tensor]
+    last_u0: Optional[torch.Tensor]
+    angle0: Optional[torch.Tensor]
+
+
+def mamba3_scan_backward(inputs: ScanInputs, dy: torch.Tensor, dh: Optional[torch.Tensor] = None,
+                         dangle: Optional[torch.Tensor] = None) -> ScanGrads:
+    """Gradients of the scan's inputs for dL/dy = dy (and dL/d state.h, dL/d
+    state.angle of the output state), through m3_scan_backward."""
+    x = _dev(inputs.x, "x")
+    if x.dim() != 5:
+        raise RankError(5, x.dim(), x.shape)
+    B, T, H, P, R = x.shape
+    N = inputs.b.shape[3]
+    code = _dtype_code(x)
+    b, c = _dev(inputs.b, "b"), _dev(inputs.c, "c")
+    _expect_shape(b, (B, T, H, N, R), "b")
+    _expect_shape(c, (B, T, H, N, R), "c")
+    dt, lam, a_log = _f32(inputs.dt, "dt"), _f32(inputs.lam, "lambda"), _f32(inputs.a_log, "a_log")
+    theta = None if inputs.theta is None else _dev(inputs.theta, "theta").to(x.dtype)
+    d_skip = _f32(inputs.d_skip, "d_skip")
+    dy = _dev(dy, "dy").to(x.dtype)
+    _expect_shape(dy, (B, T, H, P, R), "dy")
+    dh = _f32(dh, "dh")
+    dangle = _f32(dangle, "dangle") if theta is not None else None
+    st = inputs.state
+    st_c, h0, l0, a0 = None, None, None, None
+    if st is not None:
+        h0, l0 = _f32(st.h, "state.h"), _f32(st.last_u, "state.last_u")
+        a0 = _f32(st.angle, "state.angle") if (st.angle is not None and theta is not None) else None
+        st_c = _lib.SsmStateC(h0.data_ptr(), l0.data_ptr(), None if a0 is None else a0.data_ptr())
+    cin = _lib.ScanInputsC(
+        B, T, H, P, N, R, code, x.data_ptr(), b.data_ptr(), c.data_ptr(), dt.data_ptr(),
+        a_log.data_ptr(), lam.data_ptr(), None if theta is None else theta.data_ptr(),
+        None if d_skip is None else d_skip.data_ptr(),
+        C.pointer(st_c) if st_c is not None else None, int(inputs.chunk_size), 0, None, 0)
+    need = int(_lib.lib().m3_scan_backward_workspace_bytes(C.byref(cin)))
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    cin.workspace, cin.workspace_bytes = ws.data_ptr(), ws.numel()
+    f32 = lambda *shape: torch.empty(shape, dtype=torch.float32, device=x.device)
+    g = ScanGrads(torch.empty_like(x), torch.empty_like(b), torch.empty_like(c), f32(B, T, H),
+                  f32(H), f32(B, T, H), None if theta is None else torch.empty_like(theta),
+                  None if d_skip is None else f32(H), None if st is None else f32(B, H, P, N),
+                  None if st is None else f32(B, H, P, N), None if a0 is None else f32(B, H, N // 2))
+    gc = _lib.ScanGradsC(dy.data_ptr(), _ptr(dh), _ptr(dangle), g.x.data_ptr(), g.b.data_ptr(),
+                         g.c.data_ptr(), g.dt.data_ptr(), g.lam.data_ptr(), g.a_log.data_ptr(),
+                         _ptr(g.theta), _ptr(g.d_skip), _ptr(g.h0), _ptr(g.last_u0),
+                         _ptr(g.angle0))
+    _lib.check(_lib.lib().m3_scan_backward(C.byref(cin), C.byref(gc), _stream(x)))
+    return g
+
+
+def _scan_forward(inputs: ScanInputs) -> ScanOutput:
     x = inputs.x
     if x.dim() != 5:
         raise RankError(5, x.dim(), x.shape)
