@@ -165,11 +165,20 @@ struct Smem {
     float gs, pdsum;
 };
 
+// What bwd_v_kernel stages: C~, dY, the angles and the per-token scalars.
+template <int N, int R, int kRows>
+struct VSmem {
+    static constexpr int QT = kRows / R, NH = N / 2, NTN = N / 16;
+    static constexpr int LB = N + 1, LX = kP + 1;
+    float Cs[kRows * LB];
+    float Ys[kRows * LX];
+    float psi[QT * NH];
+    float dtv[QT], lamv[QT], acum[QT], gw[QT], ww[QT], eac[QT], ebar[QT], wbar[QT];
+};
+
 // Per-token scalars, the in-chunk angles, and (X, dY) / (B~, C~) as asked.
-template <typename T, int N, int R, int kRows, bool WANT_B, bool WANT_X>
-__device__ void stage(const ScanLaunch &a, const BwdArgs &g, Smem<N, R, kRows> &sm, size_t bh,
-                      int ck) {
-    using S = Smem<N, R, kRows>;
+template <typename T, int N, int R, int kRows, bool WANT_B, bool WANT_X, typename S>
+__device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, int ck) {
     constexpr int QT = S::QT, NH = S::NH;
     constexpr bool kPrecise = true;   // precise sines whatever the storage
     const int tid = threadIdx.x;
@@ -191,20 +200,23 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, Smem<N, R, kRows> &
         sm.ww[tid] = lam * dt + (1.0f - lamn) * dtn;    // fused.rs:2496-2498
     }
     __syncthreads();
-    if (tid == 0) {
-        float run = 0.0f;
-        for (int t = 0; t < QT; ++t) {
-            run += sm.acum[t];
-            sm.acum[t] = run;
+    // in-chunk prefixes as wave scans, lane = token: the log decay (wave 0)
+    // and the angle of every pair (pairs spread over the waves)
+    {
+        const int lane = tid & 63, wave = tid >> 6;
+        const size_t tg = static_cast<size_t>(ck) * QT + lane;
+        const bool live = lane < QT && tg < L;
+        if (wave == 0) {
+            const float v = seg_scan<64>(lane < QT ? sm.acum[lane] : 0.0f);
+            if (lane < QT) sm.acum[lane] = v;
         }
-    }
-    if (rot && tid >= 64 && tid < 64 + NH) {
-        const int i = tid - 64;
-        float run = 0.0f;
-        for (int t = 0; t < QT; ++t) {
-            const size_t tg = static_cast<size_t>(ck) * QT + t;
-            if (tg < L) run += sm.dtv[t] * ldv<T>(a.theta, ((bb * L + tg) * H + hh) * NH + i);
-            sm.psi[t * NH + i] = run;
+        if (rot) {
+            const float dtl = live ? sm.dtv[lane] : 0.0f;
+            const size_t th0 = ((bb * L + (live ? tg : 0)) * H + hh) * NH;
+            for (int i = wave; i < NH; i += static_cast<int>(blockDim.x >> 6)) {
+                const float v = seg_scan<64>(live ? dtl * ldv<T>(a.theta, th0 + i) : 0.0f);
+                if (lane < QT) sm.psi[lane * NH + i] = v;
+            }
         }
     }
     __syncthreads();
@@ -275,9 +287,10 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, Smem<N, R, kRows> &
 // ---------------------------------------------------------------- V_k
 // V_k^T[n][p] = sum_rho C~[rho][n] e^{alpha} dY[rho][p]: the chunk's direct
 // share of dL/dS_k (the carry-in product y += e^alpha C~ S, scan.rs:253-263).
+constexpr int kVThreads = 256;
 template <typename T, int N, int R, int kRows>
-__global__ void __launch_bounds__(kBT, 1) bwd_v_kernel(ScanLaunch a, BwdArgs g, BwdWs w, int nck) {
-    using S = Smem<N, R, kRows>;
+__global__ void __launch_bounds__(kVThreads) bwd_v_kernel(ScanLaunch a, BwdArgs g, BwdWs w, int nck) {
+    using S = VSmem<N, R, kRows>;
     constexpr int NTN = N / 16;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     S &sm = *reinterpret_cast<S *>(smem_raw);
@@ -295,7 +308,7 @@ __global__ void __launch_bounds__(kBT, 1) bwd_v_kernel(ScanLaunch a, BwdArgs g, 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, gq = lane >> 4;
     float *v = w.v + bhk * kP * N;
-    for (int tile = wave; tile < 4 * NTN; tile += kWaves) {
+    for (int tile = wave; tile < 4 * NTN; tile += kVThreads / 64) {
         const int pt = tile / NTN, i = tile % NTN;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         // A(m = n, k = rho) = C~[rho][n]; B(k = rho, col = p) = dY'[rho][p]
@@ -349,20 +362,48 @@ __global__ void __launch_bounds__(256) bwd_state_pass_kernel(ScanLaunch a, BwdAr
             rot4(lo, hi, cs, sn);
         }
     }
-    for (int k = nck - 1; k >= 0; --k) {
+    struct In {
+        f32x4 vlo, vhi, cs, sn;
+        float e;
+    };
+    auto offs = [&](int k, size_t &o, size_t &oh) {
         const size_t bhk = bh * nck + k;
+        o = bhk * kP * N + ((pt * NTN + i1) * 64 + lane) * 4;
+        oh = bhk * kP * N + ((pt * NTN + i1 + HT) * 64 + lane) * 4;
+    };
+    auto load = [&](int k, In &d) {
+        const int kk = k >= 0 ? k : 0;   // past the start: re-read chunk 0, unused
+        const size_t bhk = bh * nck + kk;
+        size_t o, oh;
+        offs(kk, o, oh);
+        d.vlo = *reinterpret_cast<const f32x4 *>(w.v + o);
+        d.vhi = *reinterpret_cast<const f32x4 *>(w.v + oh);
+        d.e = w.fw.eda[bhk];
         if (rot) {
-            const f32x4 cs = *reinterpret_cast<const f32x4 *>(w.fw.cph + bhk * NH + nlo);
-            const f32x4 sn = *reinterpret_cast<const f32x4 *>(w.fw.sph + bhk * NH + nlo);
-            rot4(lo, hi, cs, -sn);   // R(-Phi_k)
+            d.cs = *reinterpret_cast<const f32x4 *>(w.fw.cph + bhk * NH + nlo);
+            d.sn = *reinterpret_cast<const f32x4 *>(w.fw.sph + bhk * NH + nlo);
         }
-        const size_t o = bhk * kP * N + ((pt * NTN + i1) * 64 + lane) * 4;
-        const size_t oh = bhk * kP * N + ((pt * NTN + i1 + HT) * 64 + lane) * 4;
+    };
+    auto step = [&](int k, const In &d) {
+        if (rot) rot4(lo, hi, d.cs, -d.sn);   // R(-Phi_k)
+        size_t o, oh;
+        offs(k, o, oh);
         *reinterpret_cast<f32x4 *>(w.gh + o) = lo;
         *reinterpret_cast<f32x4 *>(w.gh + oh) = hi;
-        const float e = w.fw.eda[bhk];
-        lo = lo * e + *reinterpret_cast<const f32x4 *>(w.v + o);
-        hi = hi * e + *reinterpret_cast<const f32x4 *>(w.v + oh);
+        lo = lo * d.e + d.vlo;
+        hi = hi * d.e + d.vhi;
+    };
+    // eight chunks in flight ahead of the one being applied
+    constexpr int D = 8;
+    In d[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) load(nck - 1 - j, d[j]);
+    for (int k = nck - 1; k >= 0; k -= D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            if (k - j >= 0) step(k - j, d[j]);
+            load(k - D - j, d[j]);
+        }
     }
     // into the global frame: dZ0 = R(-angle0) G_0
     if (rot && a.angle0 != nullptr) {
@@ -441,8 +482,10 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
         cb = mma_f32(sm.Cs + 16 * tj * LB, LB, 1, sm.Bs + 16 * si * LB, 1, LB, N, cb, c, gq);
         dm = mma_f32(sm.Ys + 16 * tj * LX, LX, 1, sm.Xs + 16 * si * LX, 1, LX, kP, dm, c, gq);
         const int s = 16 * si + c, ts = s / R;
+        float rsum[4], csum = 0.0f, wsum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+            rsum[r] = 0.0f;
             const int t = 16 * tj + 4 * gq + r, tt = t / R;
             if (tt < ts) continue;
             const float E = clamp_exp(sm.acum[tt] - sm.acum[ts]);
@@ -455,10 +498,29 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
                 atomicAdd(&sm.dgv[ts], dm[r] * cb[r]);
             } else {
                 const float lam = dm[r] * m;
-                atomicAdd(&sm.rin[t], lam);
-                atomicAdd(&sm.cinx[s], lam);
-                atomicAdd(&sm.dwi[s], dm[r] * cb[r] * E);
+                rsum[r] = lam;
+                csum += lam;
+                wsum += dm[r] * cb[r] * E;
             }
+        }
+        // row sums over the sixteen columns of the lane group, column sums
+        // over the four lane groups: one LDS atomic per row and per column
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float v = rsum[r];
+            v += __shfl_xor(v, 1, 64);
+            v += __shfl_xor(v, 2, 64);
+            v += __shfl_xor(v, 4, 64);
+            v += __shfl_xor(v, 8, 64);
+            if (c == 0) atomicAdd(&sm.rin[16 * tj + 4 * gq + r], v);
+        }
+        csum += __shfl_xor(csum, 16, 64);
+        csum += __shfl_xor(csum, 32, 64);
+        wsum += __shfl_xor(wsum, 16, 64);
+        wsum += __shfl_xor(wsum, 32, 64);
+        if (gq == 0) {
+            atomicAdd(&sm.cinx[s], csum);
+            atomicAdd(&sm.dwi[s], wsum);
         }
     }
     __syncthreads();
@@ -510,7 +572,9 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
                 const int n = 16 * i + 4 * gq + r;
                 rc += dcl[r] * sm.Cs[row * LB + n] + dch[r] * sm.Cs[row * LB + n + NH];
             }
-            atomicAdd(&sm.rcr[row], rc);
+            rc += __shfl_xor(rc, 16, 64);
+            rc += __shfl_xor(rc, 32, 64);
+            if (gq == 0) atomicAdd(&sm.rcr[row], rc);
         }
         dcl = mma_f32(sm.Bs + 16 * i, 1, LB, sm.Ds + 16 * rt * LM, 1, LM, kRows, dcl, c, gq);
         dch = mma_f32(sm.Bs + 16 * (i + PT), 1, LB, sm.Ds + 16 * rt * LM, 1, LM, kRows, dch, c, gq);
@@ -525,7 +589,9 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
                 const int n = 16 * i + 4 * gq + r;
                 q += dbl[r] * sm.Bs[row * LB + n] + dbh[r] * sm.Bs[row * LB + n + NH];
             }
-            atomicAdd(&sm.qv[row], q);
+            q += __shfl_xor(q, 16, 64);
+            q += __shfl_xor(q, 32, 64);
+            if (gq == 0) atomicAdd(&sm.qv[row], q);
         }
         const float wb = sm.wbar[tr];
         dbl = dbl * wb;
@@ -614,14 +680,22 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
 // ---------------------------------------------------------------- angle sums of later chunks
 template <int N>
 __global__ void bwd_angle_kernel(ScanLaunch a, BwdArgs g, BwdWs w, int nck) {
-    constexpr int NH = N / 2;
+    constexpr int NH = N / 2, D = 8;
     const size_t bh = blockIdx.x;
     const int i = threadIdx.x;
     if (i >= NH) return;
     float run = g.dangle_out ? g.dangle_out[bh * NH + i] : 0.0f;
-    for (int k = nck - 1; k >= 0; --k) {
-        w.off[(bh * nck + k) * NH + i] = run;
-        run += w.ctot[(bh * nck + k) * NH + i];
+    // eight chunk totals in flight ahead of the running sum
+    for (int k0 = nck - 1; k0 >= 0; k0 -= D) {
+        float v[D];
+#pragma unroll
+        for (int j = 0; j < D; ++j) v[j] = k0 - j >= 0 ? w.ctot[(bh * nck + k0 - j) * NH + i] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            if (k0 - j < 0) break;
+            w.off[(bh * nck + k0 - j) * NH + i] = run;
+            run += v[j];
+        }
     }
     if (g.dangle0 != nullptr) g.dangle0[bh * NH + i] = run;
 }
@@ -644,16 +718,31 @@ __global__ void __launch_bounds__(256) bwd_token_kernel(ScanLaunch a, BwdArgs g,
     const float A = 0.0f - expf(a.a_log[hh]);
     const bool rot = a.theta != nullptr;
     float asum = 0.0f;
-    for (int t = wave; t < QT; t += 4) {
+    constexpr int TW = (QT + 3) / 4;   // tokens per wave
+    float cin[TW], th[TW];
+    // every load of this wave's tokens first, then the arithmetic
+#pragma unroll
+    for (int j = 0; j < TW; ++j) {
+        const int t = wave + 4 * j;
         const size_t tg = static_cast<size_t>(ck) * QT + t;
-        if (tg >= L) break;
+        const bool live = t < QT && tg < L && rot && lane < NH;
+        const size_t ix = (bb * L + (live ? tg : 0)) * H + hh;
+        cin[j] = live ? w.cin[(bh * L + tg) * NH + lane] : 0.0f;
+        th[j] = live ? ldv<T>(a.theta, ix * NH + lane) : 0.0f;
+    }
+    const float off = (rot && lane < NH) ? w.off[bhk * NH + lane] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < TW; ++j) {
+        const int t = wave + 4 * j;
+        const size_t tg = static_cast<size_t>(ck) * QT + t;
+        if (t >= QT || tg >= L) break;
         const size_t ix = (bb * L + tg) * H + hh;
         const float dt = a.dt[ix], lam = a.lambda[ix];
         float part = 0.0f;
         if (rot && lane < NH) {
-            const float dphi = w.cin[(bh * L + tg) * NH + lane] + w.off[bhk * NH + lane];
+            const float dphi = cin[j] + off;
             if (g.dtheta != nullptr) stv<T>(g.dtheta, ix * NH + lane, dt * dphi);
-            part = ldv<T>(a.theta, ix * NH + lane) * dphi;
+            part = th[j] * dphi;
         }
         part = group_sum(part, 64);
         if (lane == 0) {
@@ -664,7 +753,7 @@ __global__ void __launch_bounds__(256) bwd_token_kernel(ScanLaunch a, BwdArgs g,
             float dlam = dt * dgw - dt * dwp;
             if (tg == 0 && a.h0 != nullptr && a.last_u0 != nullptr) {
                 float dfirst = 0.0f;
-                for (int j = 0; j < N / 32; ++j) dfirst += w.pfirst[bh * (N / 32) + j];
+                for (int q = 0; q < N / 32; ++q) dfirst += w.pfirst[bh * (N / 32) + q];
                 ddt += (1.0f - lam) * dfirst;
                 dlam -= dt * dfirst;
             }
@@ -679,20 +768,25 @@ __global__ void __launch_bounds__(256) bwd_token_kernel(ScanLaunch a, BwdArgs g,
 }
 
 // ---------------------------------------------------------------- per head
-__global__ void bwd_head_kernel(ScanLaunch a, BwdArgs g, BwdWs w, int nck) {
-    const size_t hh = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ void __launch_bounds__(256) bwd_head_kernel(ScanLaunch a, BwdArgs g, BwdWs w, int nck) {
+    __shared__ float red[16];
+    const size_t hh = blockIdx.x;
     const size_t H = a.heads;
-    if (hh >= H) return;
     const float A = 0.0f - expf(a.a_log[hh]);
     float sa = 0.0f, sd = 0.0f;
-    for (size_t bb = 0; bb < a.batch; ++bb)
-        for (int k = 0; k < nck; ++k) {
-            const size_t bhk = (bb * H + hh) * nck + k;
-            sa += w.pa[bhk];
-            sd += w.pd[bhk];
-        }
-    g.da_log[hh] = A * sa;     // A = -exp(a_log): dA/da_log = A
-    if (g.dd_skip != nullptr) g.dd_skip[hh] = sd;
+    const size_t n = a.batch * static_cast<size_t>(nck);
+    for (size_t j = threadIdx.x; j < n; j += blockDim.x) {
+        const size_t bb = j / nck, k = j % nck;
+        const size_t bhk = (bb * H + hh) * nck + k;
+        sa += w.pa[bhk];
+        sd += w.pd[bhk];
+    }
+    sa = block_sum(sa, red);
+    sd = block_sum(sd, red + 8);
+    if (threadIdx.x == 0) {
+        g.da_log[hh] = A * sa;     // A = -exp(a_log): dA/da_log = A
+        if (g.dd_skip != nullptr) g.dd_skip[hh] = sd;
+    }
 }
 
 template <typename K>
@@ -723,12 +817,13 @@ hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStre
     w.pa = reinterpret_cast<float *>(base + l.pa);
     w.pfirst = reinterpret_cast<float *>(base + l.pfirst);
 
-    const size_t lds = sizeof(Smem<N, R, RW>);
-    static const hipError_t a1 = set_lds(bwd_v_kernel<T, N, R, RW>, lds);
+    const size_t lds = sizeof(Smem<N, R, RW>), vlds = sizeof(VSmem<N, R, RW>);
+    static const hipError_t a1 = set_lds(bwd_v_kernel<T, N, R, RW>, vlds);
     static const hipError_t a2 = set_lds(bwd_chunk_kernel<T, N, R, RW>, lds);
     if (a1 != hipSuccess) return a1;
     if (a2 != hipSuccess) return a2;
-    hipLaunchKernelGGL((bwd_v_kernel<T, N, R, RW>), dim3(bhk), dim3(kBT), lds, s, a, g, w, nck);
+    hipLaunchKernelGGL((bwd_v_kernel<T, N, R, RW>), dim3(bhk), dim3(kVThreads), vlds, s, a, g, w,
+                       nck);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_state_pass_kernel<N>), dim3(bh * (N / 32)), dim3(256), 0, s, a, g, w,
                        nck);
@@ -741,7 +836,7 @@ hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStre
     }
     hipLaunchKernelGGL((bwd_token_kernel<T, N, R, RW>), dim3(bhk), dim3(256), 0, s, a, g, w, nck);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(bwd_head_kernel, dim3((a.heads + 63) / 64), dim3(64), 0, s, a, g, w, nck);
+    hipLaunchKernelGGL(bwd_head_kernel, dim3(a.heads), dim3(256), 0, s, a, g, w, nck);
     return hipGetLastError();
 }
 
