@@ -46,6 +46,7 @@ sys.path.insert(0, os.path.join(ROOT, "mamba-trainer_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA, TFLOP/s
 
 # HBM-side bytes of one headline scan call (chunk_state + state_pass +
 # chunk_scan), from rocprofv3 FETCH_SIZE / WRITE_SIZE per dispatch scaled by a
@@ -273,6 +274,15 @@ def scan_backward_algorithmic(B, L, H, P, N, R, s_io=2):
     return B * L * H * per_tok
 
 
+def scan_backward_flops(B, L, H, P, N, R, Q=32):
+    """MFMA-contractible FLOPs of one backward call, counted like the forward
+    (full Q x Q band products): per row (token, rank), the band products C~B~^T,
+    dY X^T, M^T dY, (dM o K) B~ and (dM o K)^T C~ (2 Q (3N + 2P)), and the five
+    P x N products B~ Gh^T, dY S, X Gh, the V-state and the recompute of U
+    (10 P N).  Q is the backward's chunk length in rows."""
+    return B * L * H * R * (2 * Q * (3 * N + 2 * P) + 10 * P * N)
+
+
 def bench_backward(torch, lib, L_, args, inp, fwd_ms):
     """Config 1's scan backward (m3_scan_backward): dL/dy -> every input
     gradient, the forward chunk states recomputed inside the call."""
@@ -311,14 +321,21 @@ def bench_backward(torch, lib, L_, args, inp, fwd_ms):
     us = e0.elapsed_time(e1) / steps * 1e3
     assert bool(torch.isfinite(gx.float()).all()) and bool(torch.isfinite(ga).all())
     nbytes = scan_backward_algorithmic(B, L, H, P, N, R)
+    flops = scan_backward_flops(B, L, H, P, N, R)
     tokens = B * L
-    return {"us_per_call": round(us, 2), "calls": steps,
-            "tokens_per_s_fwd_bwd": round(tokens / ((us * 1e-3 + fwd_ms) * 1e-3), 1),
-            "algorithmic_bytes": nbytes, "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "workspace_MB": round(need / 1e6, 1),
-            "note": "bf16 storage, f32 arithmetic (MFMA f32 16x16x4); includes the recompute "
-                    "of the forward chunk states"}
+    tflops = flops / (us * 1e-6) / 1e12
+    out = {"us_per_call": round(us, 2), "calls": steps,
+           "tokens_per_s_bwd": round(tokens / (us * 1e-6), 1),
+           "algorithmic_bytes": nbytes, "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+           "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+           "algorithmic_flops": flops, "mfma_f32_tflops": round(tflops, 2),
+           "frac_mfma_f32_peak": round(tflops / MFMA_F32_PEAK_TFLOPS, 4),
+           "bound": "mfma_f32", "workspace_MB": round(need / 1e6, 1),
+           "note": "bf16 storage, f32 arithmetic (MFMA f32 16x16x4); includes the recompute "
+                   "of the forward chunk states"}
+    if fwd_ms is not None:
+        out["tokens_per_s_fwd_bwd"] = round(tokens / ((us * 1e-3 + fwd_ms) * 1e-3), 1)
+    return out
 
 
 def bench_decode_lm(torch, args):
@@ -480,7 +497,7 @@ def main():
     ap.add_argument("--no-backward", action="store_true", help="skip the scan backward leg")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-reps", type=int, default=3)
-    ap.add_argument("--only", choices=("prefill", "decode_lm", "ingest"), default=None,
+    ap.add_argument("--only", choices=("prefill", "decode_lm", "ingest", "backward"), default=None,
                     help="run one model leg alone and print its object (for kernel traces)")
     ap.add_argument("--scan-only", action="store_true",
                     help="run only the headline scan --steps times (for counter runs)")
@@ -511,6 +528,15 @@ def main():
     lib = L_.lib()
 
     torch.cuda.synchronize()
+    if args.only == "backward":
+        s = SCAN
+        inp = make_scan_inputs(torch, "cuda:0", s["B"], s["L"], s["H"], s["P"], s["N"], s["R"],
+                               0x4D414D43)
+        torch.cuda.synchronize()
+        _pause_for_trace(args)
+        print(json.dumps({"backward": bench_backward(torch, lib, L_, args, inp, None)}),
+              flush=True)
+        return
     if args.only:
         leg = {"prefill": bench_prefill, "decode_lm": bench_decode_lm,
                "ingest": bench_ingest}[args.only](torch, args)

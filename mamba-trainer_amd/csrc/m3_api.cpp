@@ -343,6 +343,14 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
         return fail(M3_ERR_UNSUPPORTED,
                     "the scan backward covers head_dim 64, d_state 64/128, rank 1/2/4 with "
                     "16-byte aligned buffers");
+    {
+        // gradient buffers are written (and dh read) in 8- and 16-byte pieces
+        const void *ptrs[] = {g->dx, g->db, g->dc, g->dtheta, g->dh, g->dh0, g->dlast_u0};
+        for (const void *q : ptrs)
+            if ((reinterpret_cast<uintptr_t>(q) & 15u) != 0)
+                return fail(M3_ERR_UNSUPPORTED,
+                            "the scan backward needs 16-byte aligned gradient buffers");
+    }
     const size_t need = m3::scan_backward_workspace(a);
     if (in->workspace == nullptr || in->workspace_bytes < need ||
         (reinterpret_cast<uintptr_t>(in->workspace) & 255u) != 0)

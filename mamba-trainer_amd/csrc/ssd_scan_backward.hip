@@ -38,7 +38,7 @@ namespace m3 {
 namespace {
 
 constexpr int kP = 64;
-constexpr int kWaves = 8;
+constexpr int kWaves = 16;
 constexpr int kBT = 64 * kWaves;
 
 struct BwdArgs {
@@ -101,6 +101,26 @@ template <> __device__ __forceinline__ void stv<bf16_t>(void *p, size_t i, float
     static_cast<bf16_t *>(p)[i] = from_f32<bf16_t>(v);
 }
 
+// Four elements i, i + R, i + 2R, i + 3R in the storage type: one 16-byte
+// (f32) or 8-byte (bf16) store when they are adjacent (rank 1; i is then a
+// multiple of 4 in a 16-byte aligned buffer), else four scalar stores.
+template <typename T, int R>
+__device__ __forceinline__ void st4(void *p, size_t i, f32x4 v) {
+    if constexpr (R == 1) {
+        if constexpr (sizeof(T) == 4) {
+            *reinterpret_cast<f32x4 *>(static_cast<float *>(p) + i) = v;
+        } else {
+            bf16x4 h;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) h[r] = to_bf16(v[r]);
+            *reinterpret_cast<bf16x4 *>(static_cast<bf16_t *>(p) + i) = h;
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) stv<T>(p, i + r * R, v[r]);
+    }
+}
+
 // (p, n) of element e of a [p-tile][n-tile][lane][4] MFMA D-layout record
 __device__ __forceinline__ void dl_pn(int e, int ntn, int &p, int &n) {
     const int r = e & 3, lane = (e >> 2) & 63, tile = e >> 8;
@@ -126,11 +146,51 @@ __device__ __forceinline__ void sincos_any(float x, float &s, float &c) {
 
 // D(16x16) += A(16 x K) B(K x 16) in f32: A(m, k) = a[m * am + k * ak],
 // B(k, n) = b[k * bk + n * bn]; lane (c, g) supplies A(c, k0+g), B(k0+g, c).
+// The operands of up to sixteen MFMAs are read from LDS together and the
+// MFMAs then issue back to back (one LDS wait per batch, not per MFMA).
+template <int K>
 __device__ __forceinline__ f32x4 mma_f32(const float *a, int am, int ak, const float *b, int bk,
-                                         int bn, int K, f32x4 acc, int c, int g) {
-    for (int k0 = 0; k0 < K; k0 += 4)
-        acc = mfma_f32(a[c * am + (k0 + g) * ak], b[(k0 + g) * bk + c * bn], acc);
+                                         int bn, f32x4 acc, int c, int g) {
+    static_assert(K % 4 == 0, "K");
+    constexpr int KB = K / 4 < 16 ? K / 4 : 16;
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 4 * KB) {
+        float av[KB], bv[KB];
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            const int k = k0 + 4 * j + g;
+            av[j] = a[c * am + k * ak];
+            bv[j] = b[k * bk + c * bn];
+        }
+#pragma unroll
+        for (int j = 0; j < KB; ++j) acc = mfma_f32(av[j], bv[j], acc);
+    }
     return acc;
+}
+
+// Two products sharing the B operand: D0 += A0 B, D1 += A1 B.
+template <int K>
+__device__ __forceinline__ void mma2_f32(const float *a0, const float *a1, int am, int ak,
+                                         const float *b, int bk, int bn, f32x4 &d0, f32x4 &d1,
+                                         int c, int g) {
+    static_assert(K % 4 == 0, "K");
+    constexpr int KB = K / 4 < 16 ? K / 4 : 16;
+#pragma unroll
+    for (int k0 = 0; k0 < K; k0 += 4 * KB) {
+        float av[KB], aw[KB], bv[KB];
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            const int k = k0 + 4 * j + g;
+            av[j] = a0[c * am + k * ak];
+            aw[j] = a1[c * am + k * ak];
+            bv[j] = b[k * bk + c * bn];
+        }
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            d0 = mfma_f32(av[j], bv[j], d0);
+            d1 = mfma_f32(aw[j], bv[j], d1);
+        }
+    }
 }
 
 __device__ __forceinline__ float block_sum(float v, float *red) {
@@ -148,20 +208,28 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 template <int N, int R, int kRows>
 struct Smem {
     static constexpr int QT = kRows / R, NH = N / 2, NTN = N / 16;
-    static constexpr int LB = N + 1;     // B~, C~ rows; odd pitch: rows and columns both
-    static constexpr int LX = kP + 1;    // X, dY rows   read with at most 4-way conflicts
-    static constexpr int LM = kRows + 1; // M, dCB rows
-    static constexpr int LS = N + 1;     // S, Gh rows
+    // Row pitches = 12 (mod 64 words) where LDS allows: an MFMA operand read
+    // as A(c, k0 + g) = m[c * pitch + k] then touches each bank at most once
+    // (64 banks) or twice (32), and read transposed, m[c + k * pitch], at most
+    // twice (three times).  The 64-row chunk keeps 4 (mod 64) to fit.
+    static constexpr int kPad = kRows == 64 ? 4 : 12;
+    static constexpr int LB = N + kPad;     // B~, C~ rows
+    static constexpr int LX = kP + kPad;    // X, dY rows
+    static constexpr int LM = kRows + kPad; // M, dCB rows
+    static constexpr int LS = N + kPad;     // S, Gh rows
     float Bs[kRows * LB], Cs[kRows * LB];
     float Xs[kRows * LX], Ys[kRows * LX];
     float Ms[kRows * LM], Ds[kRows * LM];
     float Ss[kP * LS], Gs[kP * LS];
-    float psi[QT * NH];     // in-chunk angle per token and pair
-    float cang[QT * NH];    // angle sums per token and pair
+    // per token and pair, rows of AP = NH + 3 words: a row-strided access by
+    // sixteen lanes then spreads over the banks instead of landing on one
+    static constexpr int AP = NH + 3;
+    float psi[QT * AP];     // in-chunk angle
+    float cang[QT * AP];    // angle sums
     float dtv[QT], lamv[QT], acum[QT], gw[QT], ww[QT], eac[QT], ebar[QT], wbar[QT];
     float rin[kRows], cinx[kRows], dwi[kRows], qv[kRows], rcr[kRows];
     float dgv[QT], dal[QT];
-    float red[16];
+    float red[32];
     float gs, pdsum;
 };
 
@@ -169,55 +237,113 @@ struct Smem {
 template <int N, int R, int kRows>
 struct VSmem {
     static constexpr int QT = kRows / R, NH = N / 2, NTN = N / 16;
-    static constexpr int LB = N + 1, LX = kP + 1;
+    static constexpr int LB = N + 12, LX = kP + 12;
     float Cs[kRows * LB];
     float Ys[kRows * LX];
-    float psi[QT * NH];
+    static constexpr int AP = NH + 3;
+    float psi[QT * AP];
     float dtv[QT], lamv[QT], acum[QT], gw[QT], ww[QT], eac[QT], ebar[QT], wbar[QT];
 };
 
 // Per-token scalars, the in-chunk angles, and (X, dY) / (B~, C~) as asked.
-template <typename T, int N, int R, int kRows, bool WANT_B, bool WANT_X, typename S>
+// Every global load of the chunk is issued before the first use of any of
+// them (NTH threads, the workgroup size): a wave then waits once for its
+// whole share instead of once per staged element.
+template <typename T, int N, int R, int kRows, bool WANT_B, bool WANT_X, int NTH, typename S>
 __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, int ck) {
-    constexpr int QT = S::QT, NH = S::NH;
+    constexpr int QT = S::QT, NH = S::NH, NW = NTH / 64;
+    constexpr int TI = NH / NW;                 // angle pairs per wave
+    constexpr int JB = (QT * NH + NTH - 1) / NTH;   // (token, pair) items per thread
+    constexpr int JX = kRows * kP / NTH;        // (row, p) items per thread
+    static_assert(NH % NW == 0 && (kRows * kP) % NTH == 0, "stage split");
     constexpr bool kPrecise = true;   // precise sines whatever the storage
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t H = a.heads, L = a.seq;
     const size_t bb = bh / H, hh = bh % H;
     const bool rot = a.theta != nullptr;
     const float A = 0.0f - expf(a.a_log[hh]);
+    const size_t t0 = static_cast<size_t>(ck) * QT;
+
+    // ---- loads
+    float dt = 0.0f, lam = 0.0f, dtn = 0.0f, lamn = 0.0f;
     if (tid < QT) {
-        const size_t t = static_cast<size_t>(ck) * QT + tid;
-        const bool live = t < L;
+        const size_t t = t0 + tid;
         const size_t ix = (bb * L + t) * H + hh;
-        const float dt = live ? a.dt[ix] : 0.0f, lam = live ? a.lambda[ix] : 0.0f;
-        const bool nlive = t + 1 < L;
-        const float dtn = nlive ? a.dt[ix + H] : 0.0f, lamn = nlive ? a.lambda[ix + H] : 0.0f;
+        if (t < L) {
+            dt = a.dt[ix];
+            lam = a.lambda[ix];
+        }
+        if (t + 1 < L) {
+            dtn = a.dt[ix + H];
+            lamn = a.lambda[ix + H];
+        }
+    }
+    const size_t tgl = t0 + lane;
+    const bool tlive = lane < QT && tgl < L;
+    float th[TI];
+    {
+        const size_t th0 = ((bb * L + (tlive ? tgl : 0)) * H + hh) * NH;
+#pragma unroll
+        for (int j = 0; j < TI; ++j)
+            th[j] = (rot && tlive) ? ldv<T>(a.theta, th0 + wave + j * NW) : 0.0f;
+    }
+    float b1[JB][R], b2[JB][R], c1[JB][R], c2[JB][R];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+        const int e = tid + j * NTH, t = e / NH, i = e % NH;
+        const size_t tg = t0 + t;
+        const bool live = e < QT * NH && tg < L;
+        const size_t base = ((bb * L + (live ? tg : 0)) * H + hh) * N * R;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            b1[j][r] = b2[j][r] = c1[j][r] = c2[j][r] = 0.0f;
+            if (live) {
+                if constexpr (WANT_B) {
+                    b1[j][r] = ldv<T>(a.b, base + i * R + r);
+                    b2[j][r] = ldv<T>(a.b, base + (i + NH) * R + r);
+                }
+                c1[j][r] = ldv<T>(a.c, base + i * R + r);
+                c2[j][r] = ldv<T>(a.c, base + (i + NH) * R + r);
+            }
+        }
+    }
+    float yv[JX], xv[JX];
+#pragma unroll
+    for (int j = 0; j < JX; ++j) {
+        const int e = tid + j * NTH, rho = e / kP, p = e % kP;
+        const int t = rho / R, r = rho % R;
+        const size_t tg = t0 + t;
+        const bool live = tg < L;
+        const size_t ix = (((bb * L + (live ? tg : 0)) * H + hh) * kP + p) * R + r;
+        yv[j] = live ? ldv<T>(g.dy, ix) : 0.0f;
+        xv[j] = (WANT_X && live) ? ldv<T>(a.x, ix) : 0.0f;
+    }
+
+    // ---- per-token scalars and the in-chunk prefixes (wave scans, lane = token)
+    if (tid < QT) {
         sm.dtv[tid] = dt;
         sm.lamv[tid] = lam;
-        sm.acum[tid] = dt * A;
         sm.gw[tid] = lam * dt;                          // fused.rs:2494
         sm.ww[tid] = lam * dt + (1.0f - lamn) * dtn;    // fused.rs:2496-2498
     }
+    if (wave == 0) {
+        const float v = seg_scan<64>(tid < QT ? dt * A : 0.0f);
+        if (lane < QT) sm.acum[lane] = v;
+    }
     __syncthreads();
-    // in-chunk prefixes as wave scans, lane = token: the log decay (wave 0)
-    // and the angle of every pair (pairs spread over the waves)
-    {
-        const int lane = tid & 63, wave = tid >> 6;
-        const size_t tg = static_cast<size_t>(ck) * QT + lane;
-        const bool live = lane < QT && tg < L;
-        if (wave == 0) {
-            const float v = seg_scan<64>(lane < QT ? sm.acum[lane] : 0.0f);
-            if (lane < QT) sm.acum[lane] = v;
+    if (rot) {
+        const float dtl = tlive ? sm.dtv[lane] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < TI; ++j) {
+            const float v = seg_scan<64>(dtl * th[j]);
+            if (lane < QT) sm.psi[lane * S::AP + wave + j * NW] = v;
         }
-        if (rot) {
-            const float dtl = live ? sm.dtv[lane] : 0.0f;
-            const size_t th0 = ((bb * L + (live ? tg : 0)) * H + hh) * NH;
-            for (int i = wave; i < NH; i += static_cast<int>(blockDim.x >> 6)) {
-                const float v = seg_scan<64>(live ? dtl * ldv<T>(a.theta, th0 + i) : 0.0f);
-                if (lane < QT) sm.psi[lane * NH + i] = v;
-            }
-        }
+    }
+#pragma unroll
+    for (int j = 0; j < JX; ++j) {
+        const int e = tid + j * NTH, rho = e / kP, p = e % kP;
+        sm.Ys[rho * S::LX + p] = yv[j];
+        if constexpr (WANT_X) sm.Xs[rho * S::LX + p] = xv[j];
     }
     __syncthreads();
     if (tid < QT) {
@@ -226,61 +352,23 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, i
         sm.ebar[tid] = clamp_exp(e - sm.acum[tid]);
         sm.wbar[tid] = sm.ebar[tid] * sm.ww[tid];
     }
-    if constexpr (WANT_B) {
-        for (int e = tid; e < QT * NH; e += blockDim.x) {
-            const int t = e / NH, i = e % NH;
-            const size_t tg = static_cast<size_t>(ck) * QT + t;
-            float sn = 0.0f, cs = 1.0f;
-            if (rot) sincos_any<kPrecise>(sm.psi[t * NH + i], sn, cs);
-            const bool live = tg < L;
-            const size_t base = ((bb * L + (live ? tg : 0)) * H + hh) * N * R;
+    // ---- rotation by -psi (fused.rs:610-617) into LDS
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int rho = t * R + r;
-                float b1 = 0.f, b2 = 0.f, c1 = 0.f, c2 = 0.f;
-                if (live) {
-                    b1 = ldv<T>(a.b, base + i * R + r);
-                    b2 = ldv<T>(a.b, base + (i + NH) * R + r);
-                    c1 = ldv<T>(a.c, base + i * R + r);
-                    c2 = ldv<T>(a.c, base + (i + NH) * R + r);
-                }
-                // rotation by -psi (fused.rs:610-617)
-                sm.Bs[rho * S::LB + i] = b1 * cs + b2 * sn;
-                sm.Bs[rho * S::LB + i + NH] = -b1 * sn + b2 * cs;
-                sm.Cs[rho * S::LB + i] = c1 * cs + c2 * sn;
-                sm.Cs[rho * S::LB + i + NH] = -c1 * sn + c2 * cs;
-            }
-        }
-    } else {
-        // C~ only
-        for (int e = tid; e < QT * NH; e += blockDim.x) {
-            const int t = e / NH, i = e % NH;
-            const size_t tg = static_cast<size_t>(ck) * QT + t;
-            float sn = 0.0f, cs = 1.0f;
-            if (rot) sincos_any<kPrecise>(sm.psi[t * NH + i], sn, cs);
-            const bool live = tg < L;
-            const size_t base = ((bb * L + (live ? tg : 0)) * H + hh) * N * R;
+    for (int j = 0; j < JB; ++j) {
+        const int e = tid + j * NTH, t = e / NH, i = e % NH;
+        if (e >= QT * NH) break;
+        float sn = 0.0f, cs = 1.0f;
+        if (rot) sincos_any<kPrecise>(sm.psi[t * S::AP + i], sn, cs);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int rho = t * R + r;
-                float c1 = 0.f, c2 = 0.f;
-                if (live) {
-                    c1 = ldv<T>(a.c, base + i * R + r);
-                    c2 = ldv<T>(a.c, base + (i + NH) * R + r);
-                }
-                sm.Cs[rho * S::LB + i] = c1 * cs + c2 * sn;
-                sm.Cs[rho * S::LB + i + NH] = -c1 * sn + c2 * cs;
+        for (int r = 0; r < R; ++r) {
+            const int rho = t * R + r;
+            if constexpr (WANT_B) {
+                sm.Bs[rho * S::LB + i] = b1[j][r] * cs + b2[j][r] * sn;
+                sm.Bs[rho * S::LB + i + NH] = -b1[j][r] * sn + b2[j][r] * cs;
             }
+            sm.Cs[rho * S::LB + i] = c1[j][r] * cs + c2[j][r] * sn;
+            sm.Cs[rho * S::LB + i + NH] = -c1[j][r] * sn + c2[j][r] * cs;
         }
-    }
-    for (int e = tid; e < kRows * kP; e += blockDim.x) {
-        const int rho = e / kP, p = e % kP;
-        const int t = rho / R, r = rho % R;
-        const size_t tg = static_cast<size_t>(ck) * QT + t;
-        const bool live = tg < L;
-        const size_t ix = (((bb * L + (live ? tg : 0)) * H + hh) * kP + p) * R + r;
-        sm.Ys[rho * S::LX + p] = live ? ldv<T>(g.dy, ix) : 0.0f;
-        if constexpr (WANT_X) sm.Xs[rho * S::LX + p] = live ? ldv<T>(a.x, ix) : 0.0f;
     }
 }
 
@@ -297,7 +385,7 @@ __global__ void __launch_bounds__(kVThreads) bwd_v_kernel(ScanLaunch a, BwdArgs 
     const size_t bhk = blockIdx.x;
     const int ck = static_cast<int>(bhk % nck);
     const size_t bh = bhk / nck;
-    stage<T, N, R, kRows, false, false>(a, g, sm, bh, ck);
+    stage<T, N, R, kRows, false, false, kVThreads>(a, g, sm, bh, ck);
     __syncthreads();
     // scale dY rows by e^{alpha}
     for (int e = threadIdx.x; e < kRows * kP; e += blockDim.x) {
@@ -312,7 +400,7 @@ __global__ void __launch_bounds__(kVThreads) bwd_v_kernel(ScanLaunch a, BwdArgs 
         const int pt = tile / NTN, i = tile % NTN;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         // A(m = n, k = rho) = C~[rho][n]; B(k = rho, col = p) = dY'[rho][p]
-        acc = mma_f32(sm.Cs + 16 * i, 1, S::LB, sm.Ys + 16 * pt, S::LX, 1, kRows, acc, c, gq);
+        acc = mma_f32<kRows>(sm.Cs + 16 * i, 1, S::LB, sm.Ys + 16 * pt, S::LX, 1, acc, c, gq);
         *reinterpret_cast<f32x4 *>(v + ((pt * NTN + i) * 64 + lane) * 4) = acc;
     }
 }
@@ -454,19 +542,36 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
     const size_t bb = bh / H, hh = bh % H;
     const float D = a.d_skip ? a.d_skip[hh] : 0.0f;
 
-    stage<T, N, R, kRows, true, true>(a, g, sm, bh, ck);
-    // the state entering the chunk and Gh, [p][n]
-    for (int e = tid; e < kP * N; e += blockDim.x) {
-        int p, n;
-        dl_pn(e, NTN, p, n);
-        sm.Ss[p * LS + n] = static_cast<const float *>(w.fw.s)[bhk * kP * N + e];
-        sm.Gs[p * LS + n] = w.gh[bhk * kP * N + e];
+    stage<T, N, R, kRows, true, true, kBT>(a, g, sm, bh, ck);
+    // the state entering the chunk and Gh, [p][n]: four consecutive n per
+    // 16-byte record piece, all loads in flight together
+    {
+        constexpr int JS = kP * N / 4 / kBT;
+        static_assert(JS * 4 * kBT == kP * N, "state copy split");
+        f32x4 sv[JS], gv[JS];
+        const f32x4 *s4 = reinterpret_cast<const f32x4 *>(static_cast<const float *>(w.fw.s) +
+                                                          bhk * kP * N);
+        const f32x4 *g4 = reinterpret_cast<const f32x4 *>(w.gh + bhk * kP * N);
+#pragma unroll
+        for (int j = 0; j < JS; ++j) {
+            sv[j] = s4[tid + j * kBT];
+            gv[j] = g4[tid + j * kBT];
+        }
+#pragma unroll
+        for (int j = 0; j < JS; ++j) {
+            int p, n;
+            dl_pn(4 * (tid + j * kBT), NTN, p, n);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sm.Ss[p * LS + n + r] = sv[j][r];
+                sm.Gs[p * LS + n + r] = gv[j][r];
+            }
+        }
     }
     for (int e = tid; e < kRows * LM; e += blockDim.x) {
         sm.Ms[e] = 0.0f;
         sm.Ds[e] = 0.0f;
     }
-    for (int e = tid; e < QT * NH; e += blockDim.x) sm.cang[e] = 0.0f;
     if (tid < kRows) {
         sm.rin[tid] = sm.cinx[tid] = sm.dwi[tid] = sm.qv[tid] = sm.rcr[tid] = 0.0f;
     }
@@ -479,8 +584,8 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
         if (si > tj) continue;
         f32x4 cb = {0.f, 0.f, 0.f, 0.f}, dm = cb;
         // CB[t][s] = sum_n C~[t][n] B~[s][n]; dM[t][s] = sum_p dY[t][p] X[s][p]
-        cb = mma_f32(sm.Cs + 16 * tj * LB, LB, 1, sm.Bs + 16 * si * LB, 1, LB, N, cb, c, gq);
-        dm = mma_f32(sm.Ys + 16 * tj * LX, LX, 1, sm.Xs + 16 * si * LX, 1, LX, kP, dm, c, gq);
+        cb = mma_f32<N>(sm.Cs + 16 * tj * LB, LB, 1, sm.Bs + 16 * si * LB, 1, LB, cb, c, gq);
+        dm = mma_f32<kP>(sm.Ys + 16 * tj * LX, LX, 1, sm.Xs + 16 * si * LX, 1, LX, dm, c, gq);
         const int s = 16 * si + c, ts = s / R;
         float rsum[4], csum = 0.0f, wsum = 0.0f;
 #pragma unroll
@@ -529,90 +634,106 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
     for (int tile = wave; tile < 4 * NT; tile += kWaves) {
         const int pt = tile & 3, st = tile >> 2;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = mma_f32(sm.Gs + 16 * pt * LS, LS, 1, sm.Bs + 16 * st * LB, 1, LB, N, acc, c, gq);
+        acc = mma_f32<N>(sm.Gs + 16 * pt * LS, LS, 1, sm.Bs + 16 * st * LB, 1, LB, acc, c, gq);
         const int s = 16 * st + c, ts = s / R, rs = s % R;
         acc = acc * sm.wbar[ts];
-        acc = mma_f32(sm.Ys + 16 * pt, 1, LX, sm.Ms + 16 * st, LM, 1, kRows, acc, c, gq);
+        acc = mma_f32<kRows>(sm.Ys + 16 * pt, 1, LX, sm.Ms + 16 * st, LM, 1, acc, c, gq);
         const size_t tg = static_cast<size_t>(ck) * QT + ts;
         if (tg < L) {
             const size_t base = ((bb * L + tg) * H + hh) * kP * R;
+            const int p0 = 16 * pt + 4 * gq;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int p = 16 * pt + 4 * gq + r;
-                stv<T>(g.dx, base + p * R + rs, acc[r] + D * sm.Ys[s * LX + p]);
-            }
+            for (int r = 0; r < 4; ++r) acc[r] += D * sm.Ys[s * LX + p0 + r];
+            st4<T, R>(g.dx, base + p0 * R + rs, acc);
         }
     }
 
-    // ---- dC~ and dB~ as [n][row] tiles; job = (pair tile i, row tile), one per wave in turn
-    constexpr int PT = NTN / 2;
-    for (int job = wave; job < NT * PT; job += kWaves) {
-        const int i = job % PT, rt = job / PT;
-        const int row = 16 * rt + c, tr = row / R, rr = row % R;
+    // ---- dC~ and dB~ as [n][row] tiles; job = (which, pair tile i, row tile),
+    // at most one per wave; a job writes the gradient of C (which = 0) or B
+    constexpr int PT = NTN / 2, NJ = NT * PT;
+    static_assert(2 * NJ <= kWaves, "one dC~ / dB~ job per wave");
+    const bool has_job = wave < 2 * NJ, isb = wave >= NJ;
+    const int jj = isb ? wave - NJ : wave;
+    const int ji = jj % PT, rt = jj / PT;
+    const int row = 16 * rt + c, tr = row / R, rr = row % R;
+    const int n0 = 16 * ji + 4 * gq;
+    const bool rot = a.theta != nullptr;
+    float sn[4], cs[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        sn[r] = 0.0f;
+        cs[r] = 1.0f;
+        if (has_job && rot) sincos_any<kPrecise>(sm.psi[tr * S::AP + n0 + r], sn[r], cs[r]);
+    }
+    // psi is free from here on: it receives the dB~ half of the angle sums,
+    // cang the dC~ half (each (token, pair) written by one lane, no atomics)
+    __syncthreads();
+    if (has_job) {
         const size_t tg = static_cast<size_t>(ck) * QT + tr;
         const bool live = tg < L;
-        float sn[4], cs[4];
+        // the job's own rotated operand (C~ for dC~, B~ for dB~) at its elements
+        const float *own = isb ? sm.Bs : sm.Cs;
+        float o1[4], o2[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            sn[r] = 0.0f;
-            cs[r] = 1.0f;
-            if (a.theta != nullptr) sincos_any<kPrecise>(sm.psi[tr * NH + 16 * i + 4 * gq + r], sn[r], cs[r]);
+            o1[r] = own[row * LB + n0 + r];
+            o2[r] = own[row * LB + n0 + r + NH];
         }
-        // dC~^T[n][t] = e^{alpha_t} sum_p S[p][n] dY[t][p] + sum_s B~[s][n] dCB[t][s]
-        f32x4 dcl = {0.f, 0.f, 0.f, 0.f}, dch = dcl;
-        dcl = mma_f32(sm.Ss + 16 * i, 1, LS, sm.Ys + 16 * rt * LX, 1, LX, kP, dcl, c, gq);
-        dch = mma_f32(sm.Ss + 16 * (i + PT), 1, LS, sm.Ys + 16 * rt * LX, 1, LX, kP, dch, c, gq);
-        const float ea = sm.eac[tr];
-        dcl = dcl * ea;
-        dch = dch * ea;
-        {
-            float rc = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int n = 16 * i + 4 * gq + r;
-                rc += dcl[r] * sm.Cs[row * LB + n] + dch[r] * sm.Cs[row * LB + n + NH];
-            }
-            rc += __shfl_xor(rc, 16, 64);
-            rc += __shfl_xor(rc, 32, 64);
-            if (gq == 0) atomicAdd(&sm.rcr[row], rc);
+        f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+        if (!isb) {
+            // dC~^T[n][t] = e^{alpha_t} sum_p S[p][n] dY[t][p] + sum_s B~[s][n] dCB[t][s]
+            mma2_f32<kP>(sm.Ss + 16 * ji, sm.Ss + 16 * (ji + PT), 1, LS, sm.Ys + 16 * rt * LX, 1,
+                         LX, lo, hi, c, gq);
+            const float ea = sm.eac[tr];
+            lo = lo * ea;
+            hi = hi * ea;
+        } else {
+            // dB~^T[n][s] = wbar_s sum_p Gh[p][n] X[s][p] + sum_t C~[t][n] dCB[t][s]
+            mma2_f32<kP>(sm.Gs + 16 * ji, sm.Gs + 16 * (ji + PT), 1, LS, sm.Xs + 16 * rt * LX, 1,
+                         LX, lo, hi, c, gq);
         }
-        dcl = mma_f32(sm.Bs + 16 * i, 1, LB, sm.Ds + 16 * rt * LM, 1, LM, kRows, dcl, c, gq);
-        dch = mma_f32(sm.Bs + 16 * (i + PT), 1, LB, sm.Ds + 16 * rt * LM, 1, LM, kRows, dch, c, gq);
-        // dB~^T[n][s] = wbar_s sum_p Gh[p][n] X[s][p] + sum_t C~[t][n] dCB[t][s]
-        f32x4 dbl = {0.f, 0.f, 0.f, 0.f}, dbh = dbl;
-        dbl = mma_f32(sm.Gs + 16 * i, 1, LS, sm.Xs + 16 * rt * LX, 1, LX, kP, dbl, c, gq);
-        dbh = mma_f32(sm.Gs + 16 * (i + PT), 1, LS, sm.Xs + 16 * rt * LX, 1, LX, kP, dbh, c, gq);
         {
+            // row . (S or Gh part): the e^alpha dy.(S C~) and wbar x.(Gh B~) terms
             float q = 0.0f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int n = 16 * i + 4 * gq + r;
-                q += dbl[r] * sm.Bs[row * LB + n] + dbh[r] * sm.Bs[row * LB + n + NH];
-            }
+            for (int r = 0; r < 4; ++r) q += lo[r] * o1[r] + hi[r] * o2[r];
             q += __shfl_xor(q, 16, 64);
             q += __shfl_xor(q, 32, 64);
-            if (gq == 0) atomicAdd(&sm.qv[row], q);
+            if (gq == 0) atomicAdd(isb ? &sm.qv[row] : &sm.rcr[row], q);
         }
-        const float wb = sm.wbar[tr];
-        dbl = dbl * wb;
-        dbh = dbh * wb;
-        dbl = mma_f32(sm.Cs + 16 * i, 1, LB, sm.Ds + 16 * rt, LM, 1, kRows, dbl, c, gq);
-        dbh = mma_f32(sm.Cs + 16 * (i + PT), 1, LB, sm.Ds + 16 * rt, LM, 1, kRows, dbh, c, gq);
-        // angle sums and the rotation back, dB = R(psi) dB~ (the transpose of fused.rs:610-617)
-        const size_t base = ((bb * L + (live ? tg : 0)) * H + hh) * N * R;
+        if (!isb) {
+            mma2_f32<kRows>(sm.Bs + 16 * ji, sm.Bs + 16 * (ji + PT), 1, LB, sm.Ds + 16 * rt * LM,
+                            1, LM, lo, hi, c, gq);
+        } else {
+            const float wb = sm.wbar[tr];
+            lo = lo * wb;
+            hi = hi * wb;
+            mma2_f32<kRows>(sm.Cs + 16 * ji, sm.Cs + 16 * (ji + PT), 1, LB, sm.Ds + 16 * rt, LM, 1,
+                            lo, hi, c, gq);
+        }
+        // angle sums and the rotation back, d = R(psi) d~ (the transpose of fused.rs:610-617)
+        if (rot) {
+            float *half = isb ? sm.psi : sm.cang;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float cr = lo[r] * o2[r] - hi[r] * o1[r];
+                // the R rows of a token sit in adjacent lanes
+                if constexpr (R >= 2) cr += __shfl_xor(cr, 1, 64);
+                if constexpr (R >= 4) cr += __shfl_xor(cr, 2, 64);
+                if (rr == 0) half[tr * S::AP + n0 + r] = cr;
+            }
+        }
+        f32x4 v1, v2;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int n = 16 * i + 4 * gq + r;
-            const float b1 = sm.Bs[row * LB + n], b2 = sm.Bs[row * LB + n + NH];
-            const float c1 = sm.Cs[row * LB + n], c2 = sm.Cs[row * LB + n + NH];
-            const float cross = dbl[r] * b2 - dbh[r] * b1 + dcl[r] * c2 - dch[r] * c1;
-            if (a.theta != nullptr) atomicAdd(&sm.cang[tr * NH + n], cross);
-            if (live) {
-                stv<T>(g.db, base + n * R + rr, dbl[r] * cs[r] - dbh[r] * sn[r]);
-                stv<T>(g.db, base + (n + NH) * R + rr, dbl[r] * sn[r] + dbh[r] * cs[r]);
-                stv<T>(g.dc, base + n * R + rr, dcl[r] * cs[r] - dch[r] * sn[r]);
-                stv<T>(g.dc, base + (n + NH) * R + rr, dcl[r] * sn[r] + dch[r] * cs[r]);
-            }
+            v1[r] = lo[r] * cs[r] - hi[r] * sn[r];
+            v2[r] = lo[r] * sn[r] + hi[r] * cs[r];
+        }
+        if (live) {
+            void *dst = isb ? g.db : g.dc;
+            const size_t base = ((bb * L + tg) * H + hh) * N * R;
+            st4<T, R>(dst, base + n0 * R + rr, v1);
+            st4<T, R>(dst, base + (n0 + NH) * R + rr, v2);
         }
     }
 
@@ -628,7 +749,7 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
             dsum += sm.Ys[rho * LX + p] * sm.Xs[rho * LX + p];
         }
         gsum = block_sum(gsum, sm.red);
-        dsum = block_sum(dsum, sm.red + 8);
+        dsum = block_sum(dsum, sm.red + 16);
         if (tid == 0) {
             sm.gs = gsum;
             w.pd[bhk] = dsum;
@@ -637,43 +758,45 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
     __syncthreads();
 
     // ---- per-token scalars: dalpha, then da = in-chunk reverse cumsum
-    if (tid < QT) {
+    if (wave == 0) {
+        // the alpha_E terms of the last row: sum over rows of wbar q
+        const float e = group_sum(lane < kRows ? sm.qv[lane] * sm.wbar[lane / R] : 0.0f, 64);
         float d = 0.0f, dw = 0.0f;
-        for (int r = 0; r < R; ++r) {
-            const int row = tid * R + r;
-            d += sm.rin[row] - sm.cinx[row] + sm.rcr[row] - sm.qv[row] * sm.wbar[tid];
-            dw += sm.dwi[row] + sm.qv[row] * sm.ebar[tid];
+        if (tid < QT) {
+            for (int r = 0; r < R; ++r) {
+                const int row = tid * R + r;
+                d += sm.rin[row] - sm.cinx[row] + sm.rcr[row] - sm.qv[row] * sm.wbar[tid];
+                dw += sm.dwi[row] + sm.qv[row] * sm.ebar[tid];
+            }
         }
-        if (tid == QT - 1) {
-            float e = 0.0f;
-            for (int row = 0; row < kRows; ++row) e += sm.qv[row] * sm.wbar[row / R];
-            d += e + w.fw.eda[bhk] * sm.gs;
-        }
-        sm.dal[tid] = d;
+        if (tid == QT - 1) d += e + w.fw.eda[bhk] * sm.gs;
+        if (tid < QT) sm.dal[tid] = d;
         const size_t tg = static_cast<size_t>(ck) * QT + tid;
-        if (tg < L) {
+        if (tid < QT && tg < L) {
             w.dg[bh * L + tg] = sm.dgv[tid];
             w.dw[bh * L + tg] = dw;
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        float run = 0.0f;
-        for (int t = QT - 1; t >= 0; --t) {
-            run += sm.dal[t];
-            const size_t tg = static_cast<size_t>(ck) * QT + t;
-            if (tg < L) w.da[bh * L + tg] = run;
+    // in-chunk reverse cumsums as wave scans over lanes in reverse token order
+    // (lane l holds token QT-1-l): da from dalpha (wave 0), and per rotation
+    // pair the angle sums (pairs spread over the waves)
+    {
+        const int t = QT - 1 - lane;
+        const size_t tg = static_cast<size_t>(ck) * QT + t;
+        const bool live = lane < QT && tg < L;
+        if (wave == 0) {
+            const float v = seg_scan<64>(lane < QT ? sm.dal[t] : 0.0f);
+            if (live) w.da[bh * L + tg] = v;
         }
-    }
-    if (a.theta != nullptr && tid >= 64 && tid < 64 + NH) {
-        const int i = tid - 64;
-        float run = 0.0f;
-        for (int t = QT - 1; t >= 0; --t) {
-            run += sm.cang[t * NH + i];
-            const size_t tg = static_cast<size_t>(ck) * QT + t;
-            if (tg < L) w.cin[(bh * L + tg) * NH + i] = run;
+        if (a.theta != nullptr) {
+            for (int i = wave; i < NH; i += kWaves) {
+                const float v = seg_scan<64>(
+                    lane < QT ? sm.cang[t * S::AP + i] + sm.psi[t * S::AP + i] : 0.0f);
+                if (live) w.cin[(bh * L + tg) * NH + i] = v;
+                if (lane == QT - 1) w.ctot[bhk * NH + i] = v;
+            }
         }
-        w.ctot[bhk * NH + i] = run;
     }
 }
 
@@ -817,6 +940,7 @@ hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStre
     w.pa = reinterpret_cast<float *>(base + l.pa);
     w.pfirst = reinterpret_cast<float *>(base + l.pfirst);
 
+    static_assert(sizeof(Smem<N, R, RW>) <= 160 * 1024, "chunk kernel LDS over 160 KB");
     const size_t lds = sizeof(Smem<N, R, RW>), vlds = sizeof(VSmem<N, R, RW>);
     static const hipError_t a1 = set_lds(bwd_v_kernel<T, N, R, RW>, vlds);
     static const hipError_t a2 = set_lds(bwd_chunk_kernel<T, N, R, RW>, lds);

@@ -154,6 +154,28 @@ def test_backward_errors_surface_as_reference_errors():
                      dev(inp["a_log"]), dev(inp["lam"])).with_theta(dev(inp["theta"])))
     with pytest.raises(UnsupportedError):
         mamba3_scan_backward(si, dev(np.zeros((1, 10, 1, 32, 1), np.float32)))
+    # a gradient buffer off the 16-byte grid
+    from mamba3 import _lib
+    import ctypes as C
+    inp2 = baseline_inputs(rng, 1, 40, 1, 64, 64, 1, theta=False)
+    xs = dev(inp2["x"])
+    cin = _lib.ScanInputsC(1, 40, 1, 64, 64, 1, _lib.M3_F32, xs.data_ptr(),
+                           dev(inp2["b"]).data_ptr(), dev(inp2["c"]).data_ptr(),
+                           dev(inp2["dt"]).data_ptr(), dev(inp2["a_log"]).data_ptr(),
+                           dev(inp2["lam"]).data_ptr(), None, None, None, 64, 0, None, 0)
+    ws = torch.zeros(int(_lib.lib().m3_scan_backward_workspace_bytes(C.byref(cin))),
+                     dtype=torch.uint8, device="cuda")
+    cin.workspace, cin.workspace_bytes = ws.data_ptr(), ws.numel()
+    big = torch.zeros(xs.numel() + 4, device="cuda")
+    gb, gc = torch.zeros(2, 40 * 64, device="cuda")
+    gdt, glam, ga = torch.zeros(40, device="cuda"), torch.zeros(40, device="cuda"), \
+        torch.zeros(1, device="cuda")
+    gr = _lib.ScanGradsC(xs.data_ptr(), None, None, big.data_ptr() + 4, gb.data_ptr(),
+                         gc.data_ptr(), gdt.data_ptr(), glam.data_ptr(), ga.data_ptr(), None,
+                         None, None, None, None)
+    st = _lib.lib().m3_scan_backward(C.byref(cin), C.byref(gr),
+                                     C.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == _lib.M3_ERR_UNSUPPORTED
     x = torch.zeros(1, 10, 1, 64, 1, device="cuda")
     with pytest.raises(ArgumentError):
         mamba3_scan_backward(ScanInputs(x, dev(inp["b"]), dev(inp["c"]), dev(inp["dt"]),
