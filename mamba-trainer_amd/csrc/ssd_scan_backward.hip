@@ -280,31 +280,42 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, i
     }
     const size_t tgl = t0 + lane;
     const bool tlive = lane < QT && tgl < L;
+    // Loads are unconditional at clamped (in-bounds) indices and the dead
+    // lanes zeroed afterwards, so no load sits behind a branch (which would
+    // make each one wait for its data before the next is issued).
     float th[TI];
-    {
+    if (rot) {
         const size_t th0 = ((bb * L + (tlive ? tgl : 0)) * H + hh) * NH;
 #pragma unroll
-        for (int j = 0; j < TI; ++j)
-            th[j] = (rot && tlive) ? ldv<T>(a.theta, th0 + wave + j * NW) : 0.0f;
+        for (int j = 0; j < TI; ++j) {
+            const float v = ldv<T>(a.theta, th0 + wave + j * NW);
+            th[j] = tlive ? v : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < TI; ++j) th[j] = 0.0f;
     }
     float b1[JB][R], b2[JB][R], c1[JB][R], c2[JB][R];
 #pragma unroll
     for (int j = 0; j < JB; ++j) {
-        const int e = tid + j * NTH, t = e / NH, i = e % NH;
+        const int e = tid + j * NTH, t = e / NH;
+        const int i = e < QT * NH ? e % NH : 0;
         const size_t tg = t0 + t;
         const bool live = e < QT * NH && tg < L;
         const size_t base = ((bb * L + (live ? tg : 0)) * H + hh) * N * R;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            b1[j][r] = b2[j][r] = c1[j][r] = c2[j][r] = 0.0f;
-            if (live) {
-                if constexpr (WANT_B) {
-                    b1[j][r] = ldv<T>(a.b, base + i * R + r);
-                    b2[j][r] = ldv<T>(a.b, base + (i + NH) * R + r);
-                }
-                c1[j][r] = ldv<T>(a.c, base + i * R + r);
-                c2[j][r] = ldv<T>(a.c, base + (i + NH) * R + r);
+            b1[j][r] = b2[j][r] = 0.0f;
+            if constexpr (WANT_B) {
+                const float u1 = ldv<T>(a.b, base + i * R + r);
+                const float u2 = ldv<T>(a.b, base + (i + NH) * R + r);
+                b1[j][r] = live ? u1 : 0.0f;
+                b2[j][r] = live ? u2 : 0.0f;
             }
+            const float v1 = ldv<T>(a.c, base + i * R + r);
+            const float v2 = ldv<T>(a.c, base + (i + NH) * R + r);
+            c1[j][r] = live ? v1 : 0.0f;
+            c2[j][r] = live ? v2 : 0.0f;
         }
     }
     float yv[JX], xv[JX];
@@ -315,8 +326,13 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, i
         const size_t tg = t0 + t;
         const bool live = tg < L;
         const size_t ix = (((bb * L + (live ? tg : 0)) * H + hh) * kP + p) * R + r;
-        yv[j] = live ? ldv<T>(g.dy, ix) : 0.0f;
-        xv[j] = (WANT_X && live) ? ldv<T>(a.x, ix) : 0.0f;
+        const float vy = ldv<T>(g.dy, ix);
+        yv[j] = live ? vy : 0.0f;
+        xv[j] = 0.0f;
+        if constexpr (WANT_X) {
+            const float vx = ldv<T>(a.x, ix);
+            xv[j] = live ? vx : 0.0f;
+        }
     }
 
     // ---- per-token scalars and the in-chunk prefixes (wave scans, lane = token)
@@ -840,51 +856,67 @@ __global__ void __launch_bounds__(256) bwd_token_kernel(ScanLaunch a, BwdArgs g,
     const size_t bb = bh / H, hh = bh % H;
     const float A = 0.0f - expf(a.a_log[hh]);
     const bool rot = a.theta != nullptr;
-    float asum = 0.0f;
-    constexpr int TW = (QT + 3) / 4;   // tokens per wave
+    constexpr int TW = (QT + 3) / 4;   // tokens per wave: wave + 4 j
+    static_assert(TW <= 64, "tokens per wave");
+    // per pair (lane = pair): dtheta and the angle part of ddt, with every
+    // load issued first (unconditional at clamped indices)
     float cin[TW], th[TW];
-    // every load of this wave's tokens first, then the arithmetic
+    const int pl = lane < NH ? lane : 0;
 #pragma unroll
     for (int j = 0; j < TW; ++j) {
         const int t = wave + 4 * j;
         const size_t tg = static_cast<size_t>(ck) * QT + t;
-        const bool live = t < QT && tg < L && rot && lane < NH;
-        const size_t ix = (bb * L + (live ? tg : 0)) * H + hh;
-        cin[j] = live ? w.cin[(bh * L + tg) * NH + lane] : 0.0f;
-        th[j] = live ? ldv<T>(a.theta, ix * NH + lane) : 0.0f;
+        const bool live = t < QT && tg < L && lane < NH;
+        const size_t tc = live ? tg : 0;
+        const size_t ix = (bb * L + tc) * H + hh;
+        float u = 0.0f, v = 0.0f;
+        if (rot) {
+            u = w.cin[(bh * L + tc) * NH + pl];
+            v = ldv<T>(a.theta, ix * NH + pl);
+        }
+        cin[j] = live ? u : 0.0f;
+        th[j] = live ? v : 0.0f;
     }
-    const float off = (rot && lane < NH) ? w.off[bhk * NH + lane] : 0.0f;
+    const float off = rot ? w.off[bhk * NH + pl] : 0.0f;
+    float mine = 0.0f;   // lane j keeps token wave + 4 j's angle part
 #pragma unroll
     for (int j = 0; j < TW; ++j) {
         const int t = wave + 4 * j;
         const size_t tg = static_cast<size_t>(ck) * QT + t;
-        if (t >= QT || tg >= L) break;
-        const size_t ix = (bb * L + tg) * H + hh;
-        const float dt = a.dt[ix], lam = a.lambda[ix];
         float part = 0.0f;
-        if (rot && lane < NH) {
+        if (rot && t < QT && tg < L && lane < NH) {
+            const size_t ix = (bb * L + tg) * H + hh;
             const float dphi = cin[j] + off;
-            if (g.dtheta != nullptr) stv<T>(g.dtheta, ix * NH + lane, dt * dphi);
+            if (g.dtheta != nullptr) stv<T>(g.dtheta, ix * NH + lane, a.dt[ix] * dphi);
             part = th[j] * dphi;
         }
         part = group_sum(part, 64);
-        if (lane == 0) {
-            const float da = w.da[bh * L + tg];
-            const float dgw = w.dg[bh * L + tg] + w.dw[bh * L + tg];
-            const float dwp = tg > 0 ? w.dw[bh * L + tg - 1] : 0.0f;
-            float ddt = part + A * da + lam * dgw + (1.0f - lam) * dwp;
-            float dlam = dt * dgw - dt * dwp;
-            if (tg == 0 && a.h0 != nullptr && a.last_u0 != nullptr) {
-                float dfirst = 0.0f;
-                for (int q = 0; q < N / 32; ++q) dfirst += w.pfirst[bh * (N / 32) + q];
-                ddt += (1.0f - lam) * dfirst;
-                dlam -= dt * dfirst;
-            }
-            g.ddt[ix] = ddt;
-            g.dlambda[ix] = dlam;
-            asum += dt * da;
-        }
+        if (lane == j) mine = part;
     }
+    // per token (lane j = token wave + 4 j): trapezoid and decay chains
+    const int t = wave + 4 * lane;
+    const size_t tg = static_cast<size_t>(ck) * QT + t;
+    const bool live = lane < TW && t < QT && tg < L;
+    const size_t tc = live ? tg : 0;
+    const size_t ix = (bb * L + tc) * H + hh;
+    const float dt = a.dt[ix], lam = a.lambda[ix];
+    const float da = w.da[bh * L + tc];
+    const float dgw = w.dg[bh * L + tc] + w.dw[bh * L + tc];
+    const float dwv = w.dw[bh * L + (tc > 0 ? tc - 1 : 0)];
+    const float dwp = tc > 0 ? dwv : 0.0f;
+    float ddt = mine + A * da + lam * dgw + (1.0f - lam) * dwp;
+    float dlam = dt * dgw - dt * dwp;
+    if (live && tg == 0 && a.h0 != nullptr && a.last_u0 != nullptr) {
+        float dfirst = 0.0f;
+        for (int q = 0; q < N / 32; ++q) dfirst += w.pfirst[bh * (N / 32) + q];
+        ddt += (1.0f - lam) * dfirst;
+        dlam -= dt * dfirst;
+    }
+    if (live) {
+        g.ddt[ix] = ddt;
+        g.dlambda[ix] = dlam;
+    }
+    float asum = live ? dt * da : 0.0f;
     __shared__ float red[16];
     asum = block_sum(asum, red);
     if (threadIdx.x == 0) w.pa[bhk] = asum;
