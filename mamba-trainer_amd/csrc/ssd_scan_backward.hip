@@ -584,64 +584,76 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
             }
         }
     }
-    for (int e = tid; e < kRows * LM; e += blockDim.x) {
-        sm.Ms[e] = 0.0f;
-        sm.Ds[e] = 0.0f;
-    }
     if (tid < kRows) {
         sm.rin[tid] = sm.cinx[tid] = sm.dwi[tid] = sm.qv[tid] = sm.rcr[tid] = 0.0f;
     }
     if (tid < QT) sm.dgv[tid] = 0.0f;
     __syncthreads();
 
-    // ---- band tiles (t-tile tj, s-tile si <= tj); tiles above lie above the token diagonal
-    for (int tile = wave; tile < NT * NT; tile += kWaves) {
-        const int tj = tile / NT, si = tile % NT;
-        if (si > tj) continue;
-        f32x4 cb = {0.f, 0.f, 0.f, 0.f}, dm = cb;
-        // CB[t][s] = sum_n C~[t][n] B~[s][n]; dM[t][s] = sum_p dY[t][p] X[s][p]
-        cb = mma_f32<N>(sm.Cs + 16 * tj * LB, LB, 1, sm.Bs + 16 * si * LB, 1, LB, cb, c, gq);
-        dm = mma_f32<kP>(sm.Ys + 16 * tj * LX, LX, 1, sm.Xs + 16 * si * LX, 1, LX, dm, c, gq);
-        const int s = 16 * si + c, ts = s / R;
-        float rsum[4], csum = 0.0f, wsum = 0.0f;
+    // ---- band products, raw: CB[t][s] = sum_n C~[t][n] B~[s][n] into Ms and
+    // dM[t][s] = sum_p dY[t][p] X[s][p] into Ds, for the tiles on and below
+    // the diagonal (the tiles above lie above the token diagonal); one
+    // product per wave in turn
+    constexpr int NB = NT * (NT + 1) / 2;
+    for (int job = wave; job < 2 * NB; job += kWaves) {
+        int q = job >> 1, tj = 0;
+        while (q > tj) {
+            q -= tj + 1;
+            ++tj;
+        }
+        const int si = q;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        float *dst;
+        if ((job & 1) == 0) {
+            acc = mma_f32<N>(sm.Cs + 16 * tj * LB, LB, 1, sm.Bs + 16 * si * LB, 1, LB, acc, c, gq);
+            dst = sm.Ms;
+        } else {
+            acc = mma_f32<kP>(sm.Ys + 16 * tj * LX, LX, 1, sm.Xs + 16 * si * LX, 1, LX, acc, c, gq);
+            dst = sm.Ds;
+        }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            rsum[r] = 0.0f;
-            const int t = 16 * tj + 4 * gq + r, tt = t / R;
-            if (tt < ts) continue;
-            const float E = clamp_exp(sm.acum[tt] - sm.acum[ts]);
-            const float W = tt == ts ? sm.gw[ts] : sm.ww[ts];
-            const float K = W * E;
-            const float m = cb[r] * K;
-            sm.Ms[t * LM + s] = m;
-            sm.Ds[t * LM + s] = dm[r] * K;
-            if (tt == ts) {
-                atomicAdd(&sm.dgv[ts], dm[r] * cb[r]);
-            } else {
-                const float lam = dm[r] * m;
-                rsum[r] = lam;
-                csum += lam;
-                wsum += dm[r] * cb[r] * E;
+        for (int r = 0; r < 4; ++r) dst[(16 * tj + 4 * gq + r) * LM + 16 * si + c] = acc[r];
+    }
+    __syncthreads();
+    // ---- the band, elementwise (one (t, s) per thread in turn, s fastest):
+    // K = W e^{alpha_t - alpha_s}, M = CB o K, dCB = dM o K; the diagonal's dg
+    // sums, and off it L = dM o M (row sums, column sums) and the dw sums
+    static_assert(kRows == 32 || kRows == 64, "band rows");
+    for (int e0 = 0; e0 < kRows * kRows; e0 += kBT) {
+        const int e = e0 + tid, t = e / kRows, s = e % kRows;
+        const int tt = t / R, ts = s / R;
+        float lam = 0.0f, dwe = 0.0f;
+        if (e < kRows * kRows) {
+            float m = 0.0f, d = 0.0f;
+            if (tt >= ts) {
+                const float cb = sm.Ms[t * LM + s], dm = sm.Ds[t * LM + s];
+                const float E = clamp_exp(sm.acum[tt] - sm.acum[ts]);
+                const float K = (tt == ts ? sm.gw[ts] : sm.ww[ts]) * E;
+                m = cb * K;
+                d = dm * K;
+                if (tt == ts) {
+                    atomicAdd(&sm.dgv[ts], dm * cb);
+                } else {
+                    lam = dm * m;
+                    dwe = dm * cb * E;
+                }
             }
+            sm.Ms[t * LM + s] = m;
+            sm.Ds[t * LM + s] = d;
         }
-        // row sums over the sixteen columns of the lane group, column sums
-        // over the four lane groups: one LDS atomic per row and per column
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float v = rsum[r];
-            v += __shfl_xor(v, 1, 64);
-            v += __shfl_xor(v, 2, 64);
-            v += __shfl_xor(v, 4, 64);
-            v += __shfl_xor(v, 8, 64);
-            if (c == 0) atomicAdd(&sm.rin[16 * tj + 4 * gq + r], v);
+        // row sums: a row is kRows consecutive lanes of one wave
+        float rs = lam;
+        for (int off = 1; off < kRows; off <<= 1) rs += __shfl_xor(rs, off, 64);
+        if (s == 0 && e < kRows * kRows) sm.rin[t] = rs;
+        // column sums: add the wave's rows first, then one atomic per column
+        float cl = lam, cw = dwe;
+        if constexpr (kRows == 32) {
+            cl += __shfl_xor(cl, 32, 64);
+            cw += __shfl_xor(cw, 32, 64);
         }
-        csum += __shfl_xor(csum, 16, 64);
-        csum += __shfl_xor(csum, 32, 64);
-        wsum += __shfl_xor(wsum, 16, 64);
-        wsum += __shfl_xor(wsum, 32, 64);
-        if (gq == 0) {
-            atomicAdd(&sm.cinx[s], csum);
-            atomicAdd(&sm.dwi[s], wsum);
+        if (lane < kRows && e < kRows * kRows) {
+            atomicAdd(&sm.cinx[s], cl);
+            atomicAdd(&sm.dwi[s], cw);
         }
     }
     __syncthreads();
@@ -753,28 +765,32 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
         }
     }
 
-    // ---- <Gh, S> and the skip's sum dY . X
+    // ---- <Gh, S> and the skip's sum dY . X, one block reduction for both
     {
         float gsum = 0.0f, dsum = 0.0f;
-        for (int e = tid; e < kP * N; e += blockDim.x) {
+        for (int e = tid; e < kP * N; e += kBT) {
             const int p = e / N, n = e % N;
             gsum += sm.Gs[p * LS + n] * sm.Ss[p * LS + n];
         }
-        for (int e = tid; e < kRows * kP; e += blockDim.x) {
+        for (int e = tid; e < kRows * kP; e += kBT) {
             const int rho = e / kP, p = e % kP;
             dsum += sm.Ys[rho * LX + p] * sm.Xs[rho * LX + p];
         }
-        gsum = block_sum(gsum, sm.red);
-        dsum = block_sum(dsum, sm.red + 16);
-        if (tid == 0) {
-            sm.gs = gsum;
-            w.pd[bhk] = dsum;
+        gsum = group_sum(gsum, 64);
+        dsum = group_sum(dsum, 64);
+        if (lane == 0) {
+            sm.red[wave] = gsum;
+            sm.red[16 + wave] = dsum;
         }
     }
+    static_assert(kWaves <= 16, "block reduction slots");
     __syncthreads();
 
     // ---- per-token scalars: dalpha, then da = in-chunk reverse cumsum
     if (wave == 0) {
+        const float gs = group_sum(lane < kWaves ? sm.red[lane] : 0.0f, 64);
+        const float ds = group_sum(lane < kWaves ? sm.red[16 + lane] : 0.0f, 64);
+        if (lane == 0) w.pd[bhk] = ds;
         // the alpha_E terms of the last row: sum over rows of wbar q
         const float e = group_sum(lane < kRows ? sm.qv[lane] * sm.wbar[lane / R] : 0.0f, 64);
         float d = 0.0f, dw = 0.0f;
@@ -785,7 +801,7 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
                 dw += sm.dwi[row] + sm.qv[row] * sm.ebar[tid];
             }
         }
-        if (tid == QT - 1) d += e + w.fw.eda[bhk] * sm.gs;
+        if (tid == QT - 1) d += e + w.fw.eda[bhk] * gs;
         if (tid < QT) sm.dal[tid] = d;
         const size_t tg = static_cast<size_t>(ck) * QT + tid;
         if (tid < QT && tg < L) {
@@ -796,7 +812,7 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
     __syncthreads();
     // in-chunk reverse cumsums as wave scans over lanes in reverse token order
     // (lane l holds token QT-1-l): da from dalpha (wave 0), and per rotation
-    // pair the angle sums (pairs spread over the waves)
+    // pair the angle sums (pairs spread over the waves, written back to cang)
     {
         const int t = QT - 1 - lane;
         const size_t tg = static_cast<size_t>(ck) * QT + t;
@@ -809,9 +825,18 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
             for (int i = wave; i < NH; i += kWaves) {
                 const float v = seg_scan<64>(
                     lane < QT ? sm.cang[t * S::AP + i] + sm.psi[t * S::AP + i] : 0.0f);
-                if (live) w.cin[(bh * L + tg) * NH + i] = v;
+                if (lane < QT) sm.cang[t * S::AP + i] = v;
                 if (lane == QT - 1) w.ctot[bhk * NH + i] = v;
             }
+        }
+    }
+    if (a.theta != nullptr) {
+        __syncthreads();
+        // token-major rows of pairs, stored whole
+        for (int e = tid; e < QT * NH; e += kBT) {
+            const int t = e / NH, i = e % NH;
+            const size_t tg = static_cast<size_t>(ck) * QT + t;
+            if (tg < L) w.cin[(bh * L + tg) * NH + i] = sm.cang[t * S::AP + i];
         }
     }
 }
