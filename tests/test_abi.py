@@ -175,3 +175,51 @@ def test_scan_workspace_query():
     assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) == 0       # d_state 96
     assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) == 0      # rank 3
     assert need(1, 0, 2, 64, 128, 1, _lib.M3_BF16) == 0        # empty window
+
+
+@pytest.mark.parametrize("kw,grads,status,message", [
+    (dict(rank=0), {}, 1, "MIMO rank must be positive"),
+    (dict(d_state=5, theta=1), {}, 1, "rotational dynamics require an even d_state"),
+    (dict(dtype=7), {}, 6, "unknown dtype"),
+    (dict(x=16, b=16, c=16, dt=16, a_log=16, lambda_=16), dict(dx=None), 6,
+     "dy, dx, db, dc, ddt, dlambda and da_log are required"),
+    (dict(x=16, b=16, c=16, dt=16, a_log=16, lambda_=16, theta=16, d_state=4), {}, 6,
+     "dtheta is required"),
+    (dict(x=16, b=16, c=16, dt=16, a_log=16, lambda_=16), {}, 4,
+     "the scan backward covers head_dim 64"),
+])
+def test_scan_backward_argument_validation_before_device_work(kw, grads, status, message):
+    """m3_scan_backward rejects bad arguments with the reference's rules and
+    messages before any device work (the pointers here are never read)."""
+    from mamba3 import _lib
+    fields = dict(dy=16, dh=None, dangle=None, dx=16, db=16, dc=16, ddt=16, dlambda=16, da_log=16,
+                  dtheta=None, dd_skip=None, dh0=None, dlast_u0=None, dangle0=None)
+    fields.update(grads)
+    g = _lib.ScanGradsC(**fields)
+    st = _lib.lib().m3_scan_backward(C.byref(_scan_inputs(**kw)), C.byref(g), None)
+    assert st == status
+    assert message in _lib.lib().m3_last_error().decode()
+
+
+def test_scan_backward_workspace_query():
+    """m3_scan_backward_workspace_bytes: the forward's chunk states at the
+    backward's chunk length plus its own per-chunk sections; 0 for shapes the
+    backward does not cover."""
+    from mamba3 import _lib
+    L = _lib.lib()
+
+    def need(B, T, H, P, N, R, dtype):
+        cin = _lib.ScanInputsC(B, T, H, P, N, R, dtype, None, None, None, None, None, None,
+                               None, None, None, 64, 0, None, 0)
+        return int(L.m3_scan_backward_workspace_bytes(C.byref(cin)))
+
+    w1 = need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16)
+    bhk = 8 * 12 * (2048 // 32)
+    # at least U, S (f32 records for the recompute) and V, Gh (f32) per chunk
+    assert w1 >= bhk * 4 * (64 * 128 * 4)
+    assert w1 % 256 == 0
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) == w1
+    assert need(2, 100, 3, 64, 64, 2, _lib.M3_BF16) > 0
+    assert need(1, 100, 2, 48, 128, 1, _lib.M3_BF16) == 0      # head_dim 48
+    assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) == 0       # d_state 96
+    assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) == 0      # rank 3
