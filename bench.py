@@ -335,7 +335,39 @@ def bench_backward(torch, lib, L_, args, inp, fwd_ms):
                    "of the forward chunk states"}
     if fwd_ms is not None:
         out["tokens_per_s_fwd_bwd"] = round(tokens / ((us * 1e-3 + fwd_ms) * 1e-3), 1)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_backward_baseline(args)
     return out
+
+
+def cpu_backward_baseline(args):
+    """The oracle's f64 reverse mode of the scan recurrence on the host (OpenMP
+    over batch x head), on a sample of config 1: batch 1, every head, full
+    length, bf16-rounded inputs."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle
+    from cases import baseline_inputs
+    s = SCAN
+    rng = np.random.default_rng(0x4D414D45)
+    inp = baseline_inputs(rng, 1, s["L"], s["H"], s["P"], s["N"], 1, theta=True, dtype="bf16")
+    dy = rng.standard_normal((1, s["L"], s["H"], s["P"], 1)).astype(np.float32)
+    run = lambda: oracle.scan_backward_f64(inp["x"], inp["b"], inp["c"], inp["dt"], inp["a_log"],
+                                           inp["lam"], dy, inp["theta"])
+    run()   # warmup
+    times = []
+    for _ in range(args.cpu_reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(s["L"] / med, 1), "unit": "tokens/s", "cores": oracle.num_threads(),
+            "kind": "port",
+            "sample": (f"config 1 at batch 1 (L=2048, H=12, P=64, N=128, Rotational, bf16-rounded "
+                       f"inputs), f64 reverse mode of the recurrence (oracle/mamba3_oracle.c "
+                       f"m3o_scan_backward_f64), 1 warmup + median of {args.cpu_reps}: "
+                       f"{med:.3f} s per pass")}
 
 
 def bench_decode_lm(torch, args):

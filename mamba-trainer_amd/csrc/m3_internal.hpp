@@ -50,22 +50,9 @@ hipError_t launch_scan_fast(const ScanLaunch &a, hipStream_t stream);
 // and the launch.
 size_t scan_chunked_workspace(const ScanLaunch &a);
 hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream);
-// The backward's recompute of the forward chunk states: chunk_state +
-// state_pass at scan_backward_rows() rows per chunk (the outputs of `a` are not written).  The view
-// gives the per-chunk sections inside the workspace: the state entering each
-// chunk (f32, MFMA D layout [chunk][p-tile][n-tile][lane][4]), the chunk
-// decay, and per rotation pair the
-// chunk angle total with its cosine and sine.
-struct ChunkStatesView {
-    const void *s;
-    const float *eda, *phi, *cph, *sph;
-    size_t nck, bytes;
-};
 // Rows (token, rank) per chunk of the backward: 32, or 64 for bf16 storage
 // with d_state 64 (whose 16-byte staging needs the longer chunk).
 inline int scan_backward_rows(const ScanLaunch &a) { return (a.bf16 && a.d_state == 64) ? 64 : 32; }
-ChunkStatesView scan_states_view(const ScanLaunch &a, void *workspace);
-hipError_t launch_scan_states(const ScanLaunch &a, void *workspace, hipStream_t stream);
 
 // Backward of the scan (mamba3_scan mode, the chunk-parallel shapes): the
 // gradients of the loss given dL/dy (and optionally dL/dh, dL/dangle of the

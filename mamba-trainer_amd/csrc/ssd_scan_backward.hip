@@ -6,8 +6,8 @@
 // forward: head_dim 64, d_state 64/128, rank 1/2/4; f32 or bf16 storage,
 // f32 arithmetic (MFMA f32 16x16x4 over f32 operands in LDS).
 //
-// Chunks of 32 rows (token, rank); 64 for bf16 storage with d_state 64.  In chunk k's own rotating frame, with
-// alpha the in-chunk inclusive cumsum of a = dt A, K_ts = W_ts e^{alpha_t -
+// Chunks of 32 rows (token, rank); 64 for bf16 storage with d_state 64.  In
+// chunk k's own rotating frame, with alpha the in-chunk inclusive cumsum of a = dt A, K_ts = W_ts e^{alpha_t -
 // alpha_s} (W = g on the token diagonal, w below it), CB = C~ B~^T, M = CB o K,
 // wbar_s = e^{alpha_E - alpha_s} w_s, S_k the state entering the chunk and
 // Gh_k = dL/d(e_k S_k + U_k) = R(-Phi_k) G_{k+1}:
@@ -23,11 +23,12 @@
 //              under the frame rotation, so the global angle gradient is its
 //              reverse cumsum over the whole sequence.
 //
-// Launches: the forward recompute of S_k (chunk_state + state_pass at 32 rows),
-// bwd_v_kernel (the chunk's direct share of G), bwd_state_pass_kernel (G and
-// Gh per chunk, and dh0 / dlast_u0), bwd_chunk_kernel (dx, db, dc and the
-// per-token da, dg, dw and angle sums), bwd_angle_kernel (the angle sums of
-// later chunks), bwd_token_kernel (dtheta, ddt, dlambda: trapezoid_weights
+// Launches: bwd_uv_kernel (per chunk U_k, the forward's chunk state, and
+// V_k, the chunk's direct share of G, with f32 operands), bwd_passes_kernel
+// (the forward recurrence giving S_k and the reverse one giving G and Gh per
+// chunk with dh0 / dlast_u0, side by side), bwd_chunk_kernel (dx, db, dc and
+// the per-token da, dg, dw and angle sums), bwd_angle_kernel (the angle sums
+// of later chunks), bwd_token_kernel (dtheta, ddt, dlambda: trapezoid_weights
 // backward, the decay and angle chains) and bwd_head_kernel (da_log, dD).
 #include <algorithm>
 
@@ -54,22 +55,31 @@ struct BwdArgs {
     float *dangle0;           // [B,H,N/2] or null
 };
 
-// Backward workspace, after the forward chunk states (ChunkStatesView.bytes).
+// Backward workspace, 256-byte aligned sections.  Per (batch, head, chunk):
+// U_k, S_k, V_k and Gh_k as f32 [p-tile][n-tile][lane][4] MFMA D-layout
+// records of the [P][N] state, the chunk decay e_k, and per rotation pair the
+// chunk's angle total Phi_k with its cosine and sine.
 struct BwdLayout {
-    size_t v, gh, cin, ctot, off, da, dg, dw, pd, pa, pfirst, total;
+    size_t u, s, v, gh, eda, phi, cph, sph, cin, ctot, off, da, dg, dw, pd, pa, pfirst, total;
 };
 
 size_t balign(size_t v) { return (v + 255) & ~size_t(255); }
 
-BwdLayout bwd_layout(size_t states_bytes, size_t bh, size_t nck, size_t seq, size_t n) {
-    const size_t bhk = bh * nck;
+BwdLayout bwd_layout(size_t bh, size_t nck, size_t seq, size_t n) {
+    const size_t bhk = bh * nck, rec = bhk * kP * n * 4, pairs = bhk * (n / 2) * 4;
     BwdLayout l;
-    size_t o = balign(states_bytes);
-    l.v = o;      o = balign(o + bhk * kP * n * 4);
-    l.gh = o;     o = balign(o + bhk * kP * n * 4);
+    size_t o = 0;
+    l.u = o;      o = balign(o + rec);
+    l.s = o;      o = balign(o + rec);
+    l.v = o;      o = balign(o + rec);
+    l.gh = o;     o = balign(o + rec);
+    l.eda = o;    o = balign(o + bhk * 4);
+    l.phi = o;    o = balign(o + pairs);
+    l.cph = o;    o = balign(o + pairs);
+    l.sph = o;    o = balign(o + pairs);
     l.cin = o;    o = balign(o + bh * seq * (n / 2) * 4);
-    l.ctot = o;   o = balign(o + bhk * (n / 2) * 4);
-    l.off = o;    o = balign(o + bhk * (n / 2) * 4);
+    l.ctot = o;   o = balign(o + pairs);
+    l.off = o;    o = balign(o + pairs);
     l.da = o;     o = balign(o + bh * seq * 4);
     l.dg = o;     o = balign(o + bh * seq * 4);
     l.dw = o;     o = balign(o + bh * seq * 4);
@@ -81,8 +91,8 @@ BwdLayout bwd_layout(size_t states_bytes, size_t bh, size_t nck, size_t seq, siz
 }
 
 struct BwdWs {
-    ChunkStatesView fw;
-    float *v, *gh, *cin, *ctot, *off, *da, *dg, *dw, *pd, *pa, *pfirst;
+    float *u, *s, *v, *gh, *eda, *phi, *cph, *sph;
+    float *cin, *ctot, *off, *da, *dg, *dw, *pd, *pa, *pfirst;
 };
 
 // element access in the storage type
@@ -217,6 +227,9 @@ struct Smem {
     static constexpr int LX = kP + kPad;    // X, dY rows
     static constexpr int LM = kRows + kPad; // M, dCB rows
     static constexpr int LS = N + kPad;     // S, Gh rows
+    // staged element (row rho, column n / p)
+    __device__ static int bi(int rho, int n) { return rho * LB + n; }
+    __device__ static int xi(int rho, int p) { return rho * LX + p; }
     float Bs[kRows * LB], Cs[kRows * LB];
     float Xs[kRows * LX], Ys[kRows * LX];
     float Ms[kRows * LM], Ds[kRows * LM];
@@ -233,16 +246,20 @@ struct Smem {
     float gs, pdsum;
 };
 
-// What bwd_v_kernel stages: C~, dY, the angles and the per-token scalars.
+// What bwd_uv_kernel stages: B~, C~, X, dY transposed ([n][rho], [p][rho],
+// rows of LDR = rows + 4 words: an MFMA lane reads four consecutive rho in one
+// 16-byte access), the angles and the per-token scalars.
 template <int N, int R, int kRows>
-struct VSmem {
+struct UVSmem {
     static constexpr int QT = kRows / R, NH = N / 2, NTN = N / 16;
-    static constexpr int LB = N + 12, LX = kP + 12;
-    float Cs[kRows * LB];
-    float Ys[kRows * LX];
+    static constexpr int LDR = kRows + 4;
+    float Bs[N * LDR], Cs[N * LDR];
+    float Xs[kP * LDR], Ys[kP * LDR];
     static constexpr int AP = NH + 3;
     float psi[QT * AP];
     float dtv[QT], lamv[QT], acum[QT], gw[QT], ww[QT], eac[QT], ebar[QT], wbar[QT];
+    __device__ static int bi(int rho, int n) { return n * LDR + rho; }
+    __device__ static int xi(int rho, int p) { return p * LDR + rho; }
 };
 
 // Per-token scalars, the in-chunk angles, and (X, dY) / (B~, C~) as asked.
@@ -358,8 +375,8 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, i
 #pragma unroll
     for (int j = 0; j < JX; ++j) {
         const int e = tid + j * NTH, rho = e / kP, p = e % kP;
-        sm.Ys[rho * S::LX + p] = yv[j];
-        if constexpr (WANT_X) sm.Xs[rho * S::LX + p] = xv[j];
+        sm.Ys[S::xi(rho, p)] = yv[j];
+        if constexpr (WANT_X) sm.Xs[S::xi(rho, p)] = xv[j];
     }
     __syncthreads();
     if (tid < QT) {
@@ -379,45 +396,158 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, i
         for (int r = 0; r < R; ++r) {
             const int rho = t * R + r;
             if constexpr (WANT_B) {
-                sm.Bs[rho * S::LB + i] = b1[j][r] * cs + b2[j][r] * sn;
-                sm.Bs[rho * S::LB + i + NH] = -b1[j][r] * sn + b2[j][r] * cs;
+                sm.Bs[S::bi(rho, i)] = b1[j][r] * cs + b2[j][r] * sn;
+                sm.Bs[S::bi(rho, i + NH)] = -b1[j][r] * sn + b2[j][r] * cs;
             }
-            sm.Cs[rho * S::LB + i] = c1[j][r] * cs + c2[j][r] * sn;
-            sm.Cs[rho * S::LB + i + NH] = -c1[j][r] * sn + c2[j][r] * cs;
+            sm.Cs[S::bi(rho, i)] = c1[j][r] * cs + c2[j][r] * sn;
+            sm.Cs[S::bi(rho, i + NH)] = -c1[j][r] * sn + c2[j][r] * cs;
         }
     }
 }
 
-// ---------------------------------------------------------------- V_k
-// V_k^T[n][p] = sum_rho C~[rho][n] e^{alpha} dY[rho][p]: the chunk's direct
-// share of dL/dS_k (the carry-in product y += e^alpha C~ S, scan.rs:253-263).
-constexpr int kVThreads = 256;
+// ---------------------------------------------------------------- U_k, V_k
+// Per chunk, in its own frame:
+//   U_k^T[n][p] = sum_rho wbar B~[rho][n] X[rho][p], the chunk's contribution to
+//     the state (the forward's chunk state, scan.rs:207-251), with f32 operands;
+//   V_k^T[n][p] = sum_rho C~[rho][n] e^{alpha} dY[rho][p], the chunk's direct
+//     share of dL/dS_k (the carry-in product y += e^alpha C~ S, scan.rs:253-263);
+// and the chunk decay e_k and per pair the angle total Phi_k, cos Phi_k, sin Phi_k.
+constexpr int kUVThreads = 512;
 template <typename T, int N, int R, int kRows>
-__global__ void __launch_bounds__(kVThreads) bwd_v_kernel(ScanLaunch a, BwdArgs g, BwdWs w, int nck) {
-    using S = VSmem<N, R, kRows>;
-    constexpr int NTN = N / 16;
+__global__ void __launch_bounds__(kUVThreads) bwd_uv_kernel(ScanLaunch a, BwdArgs g, BwdWs w,
+                                                            int nck) {
+    using S = UVSmem<N, R, kRows>;
+    constexpr int NTN = N / 16, QT = S::QT, NH = S::NH;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     S &sm = *reinterpret_cast<S *>(smem_raw);
+    const int tid = threadIdx.x;
     const size_t bhk = blockIdx.x;
     const int ck = static_cast<int>(bhk % nck);
     const size_t bh = bhk / nck;
-    stage<T, N, R, kRows, false, false, kVThreads>(a, g, sm, bh, ck);
+    stage<T, N, R, kRows, true, true, kUVThreads>(a, g, sm, bh, ck);
     __syncthreads();
-    // scale dY rows by e^{alpha}
-    for (int e = threadIdx.x; e < kRows * kP; e += blockDim.x) {
-        const int rho = e / kP;
-        sm.Ys[rho * S::LX + e % kP] *= sm.eac[rho / R];
+    // the chunk's scalars; B~ rows scaled by wbar, dY rows by e^{alpha}
+    if (tid == 0) w.eda[bhk] = clamp_exp(sm.acum[QT - 1]);
+    if (tid < NH) {
+        const float tot = a.theta != nullptr ? sm.psi[(QT - 1) * S::AP + tid] : 0.0f;
+        float ts = 0.0f, tc = 1.0f;
+        if (a.theta != nullptr) sincosf(tot, &ts, &tc);
+        w.phi[bhk * NH + tid] = tot;
+        w.cph[bhk * NH + tid] = tc;
+        w.sph[bhk * NH + tid] = ts;
+    }
+    for (int e = tid; e < kRows * N; e += kUVThreads) {
+        const int n = e / kRows, rho = e % kRows;
+        sm.Bs[S::bi(rho, n)] *= sm.wbar[rho / R];
+    }
+    for (int e = tid; e < kRows * kP; e += kUVThreads) {
+        const int p = e / kRows, rho = e % kRows;
+        sm.Ys[S::xi(rho, p)] *= sm.eac[rho / R];
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = tid & 63, wave = tid >> 6;
     const int c = lane & 15, gq = lane >> 4;
-    float *v = w.v + bhk * kP * N;
-    for (int tile = wave; tile < 4 * NTN; tile += kVThreads / 64) {
-        const int pt = tile / NTN, i = tile % NTN;
+    float *u = w.u + bhk * kP * N, *v = w.v + bhk * kP * N;
+    for (int tile = wave; tile < 8 * NTN; tile += kUVThreads / 64) {
+        const bool isv = tile >= 4 * NTN;
+        const int tt = isv ? tile - 4 * NTN : tile;
+        const int pt = tt / NTN, i = tt % NTN;
+        // A(m = n, k = rho) = B~' or C~ [n][rho]; B(k = rho, col = p) = X or dY' [p][rho]
+        const float *ar = (isv ? sm.Cs : sm.Bs) + (16 * i + c) * S::LDR;
+        const float *br = (isv ? sm.Ys : sm.Xs) + (16 * pt + c) * S::LDR;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        // A(m = n, k = rho) = C~[rho][n]; B(k = rho, col = p) = dY'[rho][p]
-        acc = mma_f32<kRows>(sm.Cs + 16 * i, 1, S::LB, sm.Ys + 16 * pt, S::LX, 1, acc, c, gq);
-        *reinterpret_cast<f32x4 *>(v + ((pt * NTN + i) * 64 + lane) * 4) = acc;
+#pragma unroll
+        for (int kb = 0; kb < kRows / 16; ++kb) acc = scan::mma_kb(ar + 16 * kb, br + 16 * kb, acc, gq);
+        *reinterpret_cast<f32x4 *>((isv ? v : u) + ((pt * NTN + i) * 64 + lane) * 4) = acc;
+    }
+}
+
+// ---------------------------------------------------------------- forward state pass
+// The recompute's sequential part: S_0 = R(angle0)(h0 + (1 - lambda_0) dt_0
+// last_u0) (scan.rs:521-535), S_{k+1} = R(Phi_k)(e_k S_k + U_k), S_k written
+// for every chunk (scan.rs:244-251 in chunk frames).  One workgroup per
+// (batch, head, n-tile pair); thread = (p, four state pairs).
+template <int N>
+__device__ void forward_pass(const ScanLaunch &a, const BwdWs &w, int nck, size_t blk) {
+    constexpr int NTN = N / 16, HT = NTN / 2, NH = N / 2;
+    const int tid = threadIdx.x, lane = tid & 63, pt = tid >> 6;
+    const int c = lane & 15, gq = lane >> 4;
+    const int i1 = static_cast<int>(blk % HT);
+    const size_t bh = blk / HT;
+    const size_t H = a.heads, L = a.seq;
+    const size_t bb = bh / H, hh = bh % H;
+    const bool rot = a.theta != nullptr;
+    const int p = 16 * pt + c, nlo = 16 * i1 + 4 * gq;
+    const size_t sbase = bh * kP * N + static_cast<size_t>(p) * N;
+    auto rot4 = [](f32x4 &lo, f32x4 &hi, f32x4 cs, f32x4 sn) {
+        const f32x4 l = lo;
+        lo = l * cs - hi * sn;
+        hi = l * sn + hi * cs;
+    };
+    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+    if (a.h0 != nullptr) {
+        lo = *reinterpret_cast<const f32x4 *>(a.h0 + sbase + nlo);
+        hi = *reinterpret_cast<const f32x4 *>(a.h0 + sbase + nlo + NH);
+        if (a.last_u0 != nullptr) {
+            const size_t i0 = (bb * L) * H + hh;
+            const float first = (1.0f - a.lambda[i0]) * a.dt[i0];
+            lo += *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo) * first;
+            hi += *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo + NH) * first;
+        }
+    }
+    if (rot && a.angle0 != nullptr) {
+        const f32x4 ph = *reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo);
+        f32x4 sn, cs;
+        for (int r = 0; r < 4; ++r) {
+            float sv, cv;
+            sincosf(ph[r], &sv, &cv);
+            sn[r] = sv;
+            cs[r] = cv;
+        }
+        rot4(lo, hi, cs, sn);
+    }
+    struct In {
+        f32x4 ulo, uhi, cs, sn;
+        float e;
+    };
+    auto offs = [&](int k, size_t &o, size_t &oh) {
+        const size_t bhk = bh * nck + k;
+        o = bhk * kP * N + ((pt * NTN + i1) * 64 + lane) * 4;
+        oh = bhk * kP * N + ((pt * NTN + i1 + HT) * 64 + lane) * 4;
+    };
+    auto load = [&](int k, In &d) {
+        const int kk = k < nck ? k : nck - 1;   // past the end: re-read the last chunk, unused
+        const size_t bhk = bh * nck + kk;
+        size_t o, oh;
+        offs(kk, o, oh);
+        d.ulo = *reinterpret_cast<const f32x4 *>(w.u + o);
+        d.uhi = *reinterpret_cast<const f32x4 *>(w.u + oh);
+        d.e = w.eda[bhk];
+        if (rot) {
+            d.cs = *reinterpret_cast<const f32x4 *>(w.cph + bhk * NH + nlo);
+            d.sn = *reinterpret_cast<const f32x4 *>(w.sph + bhk * NH + nlo);
+        }
+    };
+    auto step = [&](int k, const In &d) {
+        size_t o, oh;
+        offs(k, o, oh);
+        *reinterpret_cast<f32x4 *>(w.s + o) = lo;
+        *reinterpret_cast<f32x4 *>(w.s + oh) = hi;
+        lo = lo * d.e + d.ulo;
+        hi = hi * d.e + d.uhi;
+        if (rot) rot4(lo, hi, d.cs, d.sn);   // R(Phi_k)
+    };
+    // eight chunks in flight ahead of the one being applied
+    constexpr int D = 8;
+    In d[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) load(j, d[j]);
+    for (int k = 0; k < nck; k += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            if (k + j < nck) step(k + j, d[j]);
+            load(k + D + j, d[j]);
+        }
     }
 }
 
@@ -426,13 +556,13 @@ __global__ void __launch_bounds__(kVThreads) bwd_v_kernel(ScanLaunch a, BwdArgs 
 // G_k = e_k Gh_k + V_k.  Then S_0 = R(angle0)(h0 + (1 - lambda_0) dt_0 last_u0)
 // gives dh0, dlast_u0 and the gradient of (1 - lambda_0) dt_0 (scan.rs:521-535).
 template <int N>
-__global__ void __launch_bounds__(256) bwd_state_pass_kernel(ScanLaunch a, BwdArgs g, BwdWs w,
-                                                             int nck) {
+__device__ void reverse_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs &w, int nck,
+                             size_t blk) {
     constexpr int NTN = N / 16, HT = NTN / 2, NH = N / 2;
     const int tid = threadIdx.x, lane = tid & 63, pt = tid >> 6;
     const int c = lane & 15, gq = lane >> 4;
-    const int i1 = static_cast<int>(blockIdx.x % HT);
-    const size_t bh = blockIdx.x / HT;
+    const int i1 = static_cast<int>(blk % HT);
+    const size_t bh = blk / HT;
     const size_t H = a.heads, L = a.seq;
     const size_t bb = bh / H, hh = bh % H;
     const bool rot = a.theta != nullptr;
@@ -460,7 +590,7 @@ __global__ void __launch_bounds__(256) bwd_state_pass_kernel(ScanLaunch a, BwdAr
             f32x4 ph = {0.f, 0.f, 0.f, 0.f};
             if (a.angle0 != nullptr) ph = *reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo);
             for (int k = 0; k < nck; ++k)
-                ph += *reinterpret_cast<const f32x4 *>(w.fw.phi + (bh * nck + k) * NH + nlo);
+                ph += *reinterpret_cast<const f32x4 *>(w.phi + (bh * nck + k) * NH + nlo);
             f32x4 sn, cs;
             sincos4(ph, sn, cs);
             rot4(lo, hi, cs, sn);
@@ -482,10 +612,10 @@ __global__ void __launch_bounds__(256) bwd_state_pass_kernel(ScanLaunch a, BwdAr
         offs(kk, o, oh);
         d.vlo = *reinterpret_cast<const f32x4 *>(w.v + o);
         d.vhi = *reinterpret_cast<const f32x4 *>(w.v + oh);
-        d.e = w.fw.eda[bhk];
+        d.e = w.eda[bhk];
         if (rot) {
-            d.cs = *reinterpret_cast<const f32x4 *>(w.fw.cph + bhk * NH + nlo);
-            d.sn = *reinterpret_cast<const f32x4 *>(w.fw.sph + bhk * NH + nlo);
+            d.cs = *reinterpret_cast<const f32x4 *>(w.cph + bhk * NH + nlo);
+            d.sn = *reinterpret_cast<const f32x4 *>(w.sph + bhk * NH + nlo);
         }
     };
     auto step = [&](int k, const In &d) {
@@ -535,7 +665,19 @@ __global__ void __launch_bounds__(256) bwd_state_pass_kernel(ScanLaunch a, BwdAr
     }
     __shared__ float red[16];
     dfirst = block_sum(dfirst, red);
-    if (tid == 0) w.pfirst[blockIdx.x] = dfirst;
+    if (tid == 0) w.pfirst[blk] = dfirst;
+}
+
+// Both sequential passes in one launch (they are independent): workgroups
+// [0, nb) run the forward recurrence, [nb, 2 nb) the reverse one.
+template <int N>
+__global__ void __launch_bounds__(256) bwd_passes_kernel(ScanLaunch a, BwdArgs g, BwdWs w,
+                                                         int nck) {
+    const size_t nb = a.batch * a.heads * (N / 32);
+    if (blockIdx.x < nb)
+        forward_pass<N>(a, w, nck, blockIdx.x);
+    else
+        reverse_pass<N>(a, g, w, nck, blockIdx.x - nb);
 }
 
 // ---------------------------------------------------------------- chunk gradients
@@ -565,7 +707,7 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
         constexpr int JS = kP * N / 4 / kBT;
         static_assert(JS * 4 * kBT == kP * N, "state copy split");
         f32x4 sv[JS], gv[JS];
-        const f32x4 *s4 = reinterpret_cast<const f32x4 *>(static_cast<const float *>(w.fw.s) +
+        const f32x4 *s4 = reinterpret_cast<const f32x4 *>(w.s +
                                                           bhk * kP * N);
         const f32x4 *g4 = reinterpret_cast<const f32x4 *>(w.gh + bhk * kP * N);
 #pragma unroll
@@ -801,7 +943,7 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
                 dw += sm.dwi[row] + sm.qv[row] * sm.ebar[tid];
             }
         }
-        if (tid == QT - 1) d += e + w.fw.eda[bhk] * gs;
+        if (tid == QT - 1) d += e + w.eda[bhk] * gs;
         if (tid < QT) sm.dal[tid] = d;
         const size_t tg = static_cast<size_t>(ck) * QT + tid;
         if (tid < QT && tg < L) {
@@ -977,36 +1119,40 @@ hipError_t set_lds(K kern, size_t bytes) {
 
 template <typename T, int N, int R, int RW>
 hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStream_t s) {
-    hipError_t e = launch_scan_states(a, base, s);
-    if (e != hipSuccess) return e;
-    const ChunkStatesView fw = scan_states_view(a, base);
-    const int nck = static_cast<int>(fw.nck);
+    const int nck = static_cast<int>((a.seq + RW / R - 1) / (RW / R));
     const size_t bh = a.batch * a.heads, bhk = bh * nck;
-    const BwdLayout l = bwd_layout(fw.bytes, bh, nck, a.seq, N);
+    const BwdLayout l = bwd_layout(bh, nck, a.seq, N);
     BwdWs w;
-    w.fw = fw;
-    w.v = reinterpret_cast<float *>(base + l.v);
-    w.gh = reinterpret_cast<float *>(base + l.gh);
-    w.cin = reinterpret_cast<float *>(base + l.cin);
-    w.ctot = reinterpret_cast<float *>(base + l.ctot);
-    w.off = reinterpret_cast<float *>(base + l.off);
-    w.da = reinterpret_cast<float *>(base + l.da);
-    w.dg = reinterpret_cast<float *>(base + l.dg);
-    w.dw = reinterpret_cast<float *>(base + l.dw);
-    w.pd = reinterpret_cast<float *>(base + l.pd);
-    w.pa = reinterpret_cast<float *>(base + l.pa);
-    w.pfirst = reinterpret_cast<float *>(base + l.pfirst);
+    auto f = [base](size_t off) { return reinterpret_cast<float *>(base + off); };
+    w.u = f(l.u);
+    w.s = f(l.s);
+    w.v = f(l.v);
+    w.gh = f(l.gh);
+    w.eda = f(l.eda);
+    w.phi = f(l.phi);
+    w.cph = f(l.cph);
+    w.sph = f(l.sph);
+    w.cin = f(l.cin);
+    w.ctot = f(l.ctot);
+    w.off = f(l.off);
+    w.da = f(l.da);
+    w.dg = f(l.dg);
+    w.dw = f(l.dw);
+    w.pd = f(l.pd);
+    w.pa = f(l.pa);
+    w.pfirst = f(l.pfirst);
 
     static_assert(sizeof(Smem<N, R, RW>) <= 160 * 1024, "chunk kernel LDS over 160 KB");
-    const size_t lds = sizeof(Smem<N, R, RW>), vlds = sizeof(VSmem<N, R, RW>);
-    static const hipError_t a1 = set_lds(bwd_v_kernel<T, N, R, RW>, vlds);
+    const size_t lds = sizeof(Smem<N, R, RW>), uvlds = sizeof(UVSmem<N, R, RW>);
+    static const hipError_t a1 = set_lds(bwd_uv_kernel<T, N, R, RW>, uvlds);
     static const hipError_t a2 = set_lds(bwd_chunk_kernel<T, N, R, RW>, lds);
     if (a1 != hipSuccess) return a1;
     if (a2 != hipSuccess) return a2;
-    hipLaunchKernelGGL((bwd_v_kernel<T, N, R, RW>), dim3(bhk), dim3(kVThreads), vlds, s, a, g, w,
-                       nck);
+    hipError_t e;
+    hipLaunchKernelGGL((bwd_uv_kernel<T, N, R, RW>), dim3(bhk), dim3(kUVThreads), uvlds, s, a, g,
+                       w, nck);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_state_pass_kernel<N>), dim3(bh * (N / 32)), dim3(256), 0, s, a, g, w,
+    hipLaunchKernelGGL((bwd_passes_kernel<N>), dim3(2 * bh * (N / 32)), dim3(256), 0, s, a, g, w,
                        nck);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_chunk_kernel<T, N, R, RW>), dim3(bhk), dim3(kBT), lds, s, a, g, w, nck);
@@ -1044,8 +1190,9 @@ bool scan_backward_supported(const ScanLaunch &a) {
 
 size_t scan_backward_workspace(const ScanLaunch &a) {
     if (!scan_backward_supported(a)) return 0;
-    const ChunkStatesView fw = scan_states_view(a, nullptr);
-    return bwd_layout(fw.bytes, a.batch * a.heads, fw.nck, a.seq, a.d_state).total;
+    const size_t qt = static_cast<size_t>(scan_backward_rows(a)) / a.rank;
+    const size_t nck = (a.seq + qt - 1) / qt;
+    return bwd_layout(a.batch * a.heads, nck, a.seq, a.d_state).total;
 }
 
 hipError_t launch_scan_backward(const ScanLaunch &a, const ScanGrads &gr, void *workspace,

@@ -117,9 +117,9 @@ __device__ __forceinline__ f32x4 load_u(const void *u, size_t e) {
 }
 
 // ================================================================ chunk state
-template <typename T, int N, int R, int ROWS, typename OT = typename Op<T>::t>
+template <typename T, int N, int R, int ROWS>
 struct StateSmem {
-    using op_t = OT;
+    using op_t = typename Op<T>::t;
     static constexpr int PAD = 16 / static_cast<int>(sizeof(op_t));
     static constexpr int LDR = ROWS + PAD;
     op_t Bwt[N * LDR];      // (B^(k) * w * decay-to-end)^T [n][rho]
@@ -127,17 +127,15 @@ struct StateSmem {
     float phi_tot[N / 2];
 };
 
-// OT: the operand type of the U product (the storage's by default; f32 for
-// the backward's recompute, which keeps U and every decay and sine precise).
-template <typename T, int N, int R, int ROWS, typename OT = typename Op<T>::t>
+template <typename T, int N, int R, int ROWS>
 __global__ void __launch_bounds__(kThreads, 2)
 chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     constexpr int P = kP;
     using G = Geo<T, N, P, R, ROWS, 4>;
-    using S = StateSmem<T, N, R, ROWS, OT>;
+    using S = StateSmem<T, N, R, ROWS>;
     using RawT = Raw<T, N, P, R, ROWS, 4, false>;
     using op_t = typename S::op_t;
-    constexpr int KB = sizeof(OT) == 2 ? 32 : 16;
+    constexpr int KB = sizeof(typename S::op_t) == 2 ? 32 : 16;
     constexpr int LDR = S::LDR;
     constexpr int QT = G::QT, NH = G::NH, PPL = G::PPL;
     constexpr int NTN = N / 16;
@@ -689,43 +687,6 @@ hipError_t launch_t(const ScanLaunch &a, char *ws, hipStream_t s) {
 
 int rows_for(const ScanLaunch &a) { return a.bf16 ? 64 : 32; }
 
-// chunk_state + state_pass only (the backward's recompute of the state
-// entering every chunk).  The outputs of `a` are not written.
-template <typename T, int N, int R, int ROWS>
-hipError_t launch_states(const ScanLaunch &a0, char *base, hipStream_t s) {
-    constexpr int QT = ROWS / R;
-    ScanLaunch a = a0;
-    a.y = nullptr;
-    a.h_out = a.last_u_out = a.angle_out = nullptr;
-    const int nck = static_cast<int>((a.seq + QT - 1) / QT);
-    const size_t bh = a.batch * a.heads;
-    // f32 operands, U and S whatever the storage: the state pass then runs its
-    // f32 form (it reads no storage-typed input when no output is written)
-    const ChunkWs ws = chunk_ws(base, chunked_layout(bh * nck, N, false));
-    hipLaunchKernelGGL((chunk_state_kernel<T, N, R, ROWS, float>), dim3(bh * nck), dim3(kThreads),
-                       0, s, a, ws, nck);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((state_pass_kernel<float, N>), dim3(bh * (N / 32)), dim3(kThreads), 0, s,
-                       a, ws, nck);
-    return hipGetLastError();
-}
-
-template <typename T, int N64ROWS>
-hipError_t launch_states_t(const ScanLaunch &a, char *ws, hipStream_t s) {
-    const size_t n = a.d_state, r = a.rank;
-    if (n == 128) {
-        if (r == 1) return launch_states<T, 128, 1, 32>(a, ws, s);
-        if (r == 2) return launch_states<T, 128, 2, 32>(a, ws, s);
-        if (r == 4) return launch_states<T, 128, 4, 32>(a, ws, s);
-    } else if (n == 64) {
-        if (r == 1) return launch_states<T, 64, 1, N64ROWS>(a, ws, s);
-        if (r == 2) return launch_states<T, 64, 2, N64ROWS>(a, ws, s);
-        if (r == 4) return launch_states<T, 64, 4, N64ROWS>(a, ws, s);
-    }
-    return hipErrorNotSupported;
-}
-
 }  // namespace
 
 // The single pass walks each (batch, head) sequence with one workgroup per CU;
@@ -764,32 +725,6 @@ size_t scan_chunked_workspace(const ScanLaunch &a) {
     const size_t qt = static_cast<size_t>(rows_for(a)) / a.rank;
     const size_t nck = (a.seq + qt - 1) / qt;
     return chunked_layout(a.batch * a.heads * nck, a.d_state, a.bf16 != 0).total;
-}
-
-ChunkStatesView scan_states_view(const ScanLaunch &a, void *workspace) {
-    const size_t qt = static_cast<size_t>(scan_backward_rows(a)) / a.rank;
-    const size_t nck = (a.seq + qt - 1) / qt;
-    const size_t bhk = a.batch * a.heads * nck;
-    const ChunkedLayout l = chunked_layout(bhk, a.d_state, false);
-    char *base = static_cast<char *>(workspace);
-    ChunkStatesView v{};
-    if (base != nullptr) {   // a null workspace asks for the sizes only
-        v.s = base + l.s;
-        v.eda = reinterpret_cast<const float *>(base + l.eda);
-        v.phi = reinterpret_cast<const float *>(base + l.phi);
-        v.cph = reinterpret_cast<const float *>(base + l.cph);
-        v.sph = reinterpret_cast<const float *>(base + l.sph);
-    }
-    v.nck = nck;
-    v.bytes = l.total;
-    return v;
-}
-
-hipError_t launch_scan_states(const ScanLaunch &a, void *workspace, hipStream_t stream) {
-    if (!scan_fast_supported(a) || a.seq == 0) return hipErrorNotSupported;
-    char *ws = static_cast<char *>(workspace);
-    if (a.bf16) return launch_states_t<bf16_t, 64>(a, ws, stream);
-    return launch_states_t<float, 32>(a, ws, stream);
 }
 
 hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream) {
