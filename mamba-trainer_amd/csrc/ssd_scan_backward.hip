@@ -732,12 +732,22 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
     if (tid < QT) sm.dgv[tid] = 0.0f;
     __syncthreads();
 
-    // ---- band products, raw: CB[t][s] = sum_n C~[t][n] B~[s][n] into Ms and
-    // dM[t][s] = sum_p dY[t][p] X[s][p] into Ds, for the tiles on and below
-    // the diagonal (the tiles above lie above the token diagonal); one
-    // product per wave in turn
+    // Three phases.  Phase 1 is everything that does not need the band: the
+    // band products themselves, the Gh B~^T half of dX, the S dY / Gh X half of
+    // each dC~ / dB~ job with its row sums, and the jobs' sines.  Phase 2 is
+    // the band, elementwise.  Phase 3 finishes dX and the jobs with M and dCB.
+    // Work per wave: at most one dX tile and one job (accumulators stay in
+    // registers across the barriers); band products go to the waves from
+    // kWaves / 2 on first, which carry no dX tile.
     constexpr int NB = NT * (NT + 1) / 2;
-    for (int job = wave; job < 2 * NB; job += kWaves) {
+    constexpr int PT = NTN / 2, NJ = NT * PT;
+    static_assert(2 * NJ <= kWaves && 4 * NT <= kWaves, "one job and one dX tile per wave");
+    const bool rot = a.theta != nullptr;
+
+    // ---- phase 1a: band products, raw: CB[t][s] = sum_n C~[t][n] B~[s][n]
+    // into Ms and dM[t][s] = sum_p dY[t][p] X[s][p] into Ds, for the tiles on
+    // and below the diagonal (the tiles above lie above the token diagonal)
+    for (int job = (wave + kWaves / 2) % kWaves; job < 2 * NB; job += kWaves) {
         int q = job >> 1, tj = 0;
         while (q > tj) {
             q -= tj + 1;
@@ -756,10 +766,65 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
 #pragma unroll
         for (int r = 0; r < 4; ++r) dst[(16 * tj + 4 * gq + r) * LM + 16 * si + c] = acc[r];
     }
+
+    // ---- phase 1b: dX^T[p][s] = wbar_s sum_n Gh[p][n] B~[s][n] (+ phase 3)
+    const bool has_dx = wave < 4 * NT;
+    const int xpt = wave & 3, xst = wave >> 2;
+    f32x4 xacc = {0.f, 0.f, 0.f, 0.f};
+    if (has_dx)
+        xacc = mma_f32<N>(sm.Gs + 16 * xpt * LS, LS, 1, sm.Bs + 16 * xst * LB, 1, LB, xacc, c, gq);
+
+    // ---- phase 1c: dC~ and dB~ as [n][row] tiles; job = (which, pair tile i,
+    // row tile); a job writes the gradient of C (which = 0) or B
+    const bool has_job = wave < 2 * NJ, isb = wave >= NJ;
+    const int jj = isb ? wave - NJ : wave;
+    const int ji = jj % PT, rt = jj / PT;
+    const int row = 16 * rt + c, tr = row / R, rr = row % R;
+    const int n0 = 16 * ji + 4 * gq;
+    // the job's own rotated operand (C~ for dC~, B~ for dB~) at its elements
+    const float *own = isb ? sm.Bs : sm.Cs;
+    float sn[4], cs[4], o1[4], o2[4];
+    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+    if (has_job) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sn[r] = 0.0f;
+            cs[r] = 1.0f;
+            if (rot) sincos_any<kPrecise>(sm.psi[tr * S::AP + n0 + r], sn[r], cs[r]);
+            o1[r] = own[row * LB + n0 + r];
+            o2[r] = own[row * LB + n0 + r + NH];
+        }
+        if (!isb) {
+            // dC~^T[n][t] = e^{alpha_t} sum_p S[p][n] dY[t][p] + (phase 3)
+            mma2_f32<kP>(sm.Ss + 16 * ji, sm.Ss + 16 * (ji + PT), 1, LS, sm.Ys + 16 * rt * LX, 1,
+                         LX, lo, hi, c, gq);
+            const float ea = sm.eac[tr];
+            lo = lo * ea;
+            hi = hi * ea;
+        } else {
+            // dB~^T[n][s] = wbar_s sum_p Gh[p][n] X[s][p] + (phase 3)
+            mma2_f32<kP>(sm.Gs + 16 * ji, sm.Gs + 16 * (ji + PT), 1, LS, sm.Xs + 16 * rt * LX, 1,
+                         LX, lo, hi, c, gq);
+        }
+        // row . (S or Gh part): the e^alpha dy.(S C~) and wbar x.(Gh B~) terms
+        float q = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) q += lo[r] * o1[r] + hi[r] * o2[r];
+        q += __shfl_xor(q, 16, 64);
+        q += __shfl_xor(q, 32, 64);
+        if (gq == 0) atomicAdd(isb ? &sm.qv[row] : &sm.rcr[row], q);
+        if (isb) {
+            const float wb = sm.wbar[tr];
+            lo = lo * wb;
+            hi = hi * wb;
+        }
+    }
     __syncthreads();
-    // ---- the band, elementwise (one (t, s) per thread in turn, s fastest):
-    // K = W e^{alpha_t - alpha_s}, M = CB o K, dCB = dM o K; the diagonal's dg
-    // sums, and off it L = dM o M (row sums, column sums) and the dw sums
+
+    // ---- phase 2: the band, elementwise (one (t, s) per thread in turn, s
+    // fastest): K = W e^{alpha_t - alpha_s}, M = CB o K, dCB = dM o K; the
+    // diagonal's dg sums, and off it L = dM o M (row sums, column sums) and
+    // the dw sums
     static_assert(kRows == 32 || kRows == 64, "band rows");
     for (int e0 = 0; e0 < kRows * kRows; e0 += kBT) {
         const int e = e0 + tid, t = e / kRows, s = e % kRows;
@@ -800,88 +865,32 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
     }
     __syncthreads();
 
-    // ---- dX^T[p][s] = wbar_s sum_n Gh[p][n] B~[s][n] + sum_t dY[t][p] M[t][s] + D dY[s][p]
-    for (int tile = wave; tile < 4 * NT; tile += kWaves) {
-        const int pt = tile & 3, st = tile >> 2;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = mma_f32<N>(sm.Gs + 16 * pt * LS, LS, 1, sm.Bs + 16 * st * LB, 1, LB, acc, c, gq);
-        const int s = 16 * st + c, ts = s / R, rs = s % R;
-        acc = acc * sm.wbar[ts];
-        acc = mma_f32<kRows>(sm.Ys + 16 * pt, 1, LX, sm.Ms + 16 * st, LM, 1, acc, c, gq);
+    // ---- phase 3a: dX^T[p][s] += sum_t dY[t][p] M[t][s] + D dY[s][p]
+    if (has_dx) {
+        const int s = 16 * xst + c, ts = s / R, rs = s % R;
+        f32x4 acc = xacc * sm.wbar[ts];
+        acc = mma_f32<kRows>(sm.Ys + 16 * xpt, 1, LX, sm.Ms + 16 * xst, LM, 1, acc, c, gq);
         const size_t tg = static_cast<size_t>(ck) * QT + ts;
         if (tg < L) {
             const size_t base = ((bb * L + tg) * H + hh) * kP * R;
-            const int p0 = 16 * pt + 4 * gq;
+            const int p0 = 16 * xpt + 4 * gq;
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[r] += D * sm.Ys[s * LX + p0 + r];
             st4<T, R>(g.dx, base + p0 * R + rs, acc);
         }
     }
-
-    // ---- dC~ and dB~ as [n][row] tiles; job = (which, pair tile i, row tile),
-    // at most one per wave; a job writes the gradient of C (which = 0) or B
-    constexpr int PT = NTN / 2, NJ = NT * PT;
-    static_assert(2 * NJ <= kWaves, "one dC~ / dB~ job per wave");
-    const bool has_job = wave < 2 * NJ, isb = wave >= NJ;
-    const int jj = isb ? wave - NJ : wave;
-    const int ji = jj % PT, rt = jj / PT;
-    const int row = 16 * rt + c, tr = row / R, rr = row % R;
-    const int n0 = 16 * ji + 4 * gq;
-    const bool rot = a.theta != nullptr;
-    float sn[4], cs[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        sn[r] = 0.0f;
-        cs[r] = 1.0f;
-        if (has_job && rot) sincos_any<kPrecise>(sm.psi[tr * S::AP + n0 + r], sn[r], cs[r]);
-    }
-    // psi is free from here on: it receives the dB~ half of the angle sums,
-    // cang the dC~ half (each (token, pair) written by one lane, no atomics)
-    __syncthreads();
+    // ---- phase 3b: the band halves of dC~ and dB~
+    //   dC~^T[n][t] += sum_s B~[s][n] dCB[t][s],  dB~^T[n][s] += sum_t C~[t][n] dCB[t][s]
+    // then the angle sums (psi is free: every sine was taken in phase 1; psi
+    // receives the dB~ half, cang the dC~ half, one lane per (token, pair))
+    // and the rotation back, d = R(psi) d~ (the transpose of fused.rs:610-617)
     if (has_job) {
-        const size_t tg = static_cast<size_t>(ck) * QT + tr;
-        const bool live = tg < L;
-        // the job's own rotated operand (C~ for dC~, B~ for dB~) at its elements
-        const float *own = isb ? sm.Bs : sm.Cs;
-        float o1[4], o2[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            o1[r] = own[row * LB + n0 + r];
-            o2[r] = own[row * LB + n0 + r + NH];
-        }
-        f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
-        if (!isb) {
-            // dC~^T[n][t] = e^{alpha_t} sum_p S[p][n] dY[t][p] + sum_s B~[s][n] dCB[t][s]
-            mma2_f32<kP>(sm.Ss + 16 * ji, sm.Ss + 16 * (ji + PT), 1, LS, sm.Ys + 16 * rt * LX, 1,
-                         LX, lo, hi, c, gq);
-            const float ea = sm.eac[tr];
-            lo = lo * ea;
-            hi = hi * ea;
-        } else {
-            // dB~^T[n][s] = wbar_s sum_p Gh[p][n] X[s][p] + sum_t C~[t][n] dCB[t][s]
-            mma2_f32<kP>(sm.Gs + 16 * ji, sm.Gs + 16 * (ji + PT), 1, LS, sm.Xs + 16 * rt * LX, 1,
-                         LX, lo, hi, c, gq);
-        }
-        {
-            // row . (S or Gh part): the e^alpha dy.(S C~) and wbar x.(Gh B~) terms
-            float q = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) q += lo[r] * o1[r] + hi[r] * o2[r];
-            q += __shfl_xor(q, 16, 64);
-            q += __shfl_xor(q, 32, 64);
-            if (gq == 0) atomicAdd(isb ? &sm.qv[row] : &sm.rcr[row], q);
-        }
-        if (!isb) {
+        if (!isb)
             mma2_f32<kRows>(sm.Bs + 16 * ji, sm.Bs + 16 * (ji + PT), 1, LB, sm.Ds + 16 * rt * LM,
                             1, LM, lo, hi, c, gq);
-        } else {
-            const float wb = sm.wbar[tr];
-            lo = lo * wb;
-            hi = hi * wb;
+        else
             mma2_f32<kRows>(sm.Cs + 16 * ji, sm.Cs + 16 * (ji + PT), 1, LB, sm.Ds + 16 * rt, LM, 1,
                             lo, hi, c, gq);
-        }
-        // angle sums and the rotation back, d = R(psi) d~ (the transpose of fused.rs:610-617)
         if (rot) {
             float *half = isb ? sm.psi : sm.cang;
 #pragma unroll
@@ -899,7 +908,8 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
             v1[r] = lo[r] * cs[r] - hi[r] * sn[r];
             v2[r] = lo[r] * sn[r] + hi[r] * cs[r];
         }
-        if (live) {
+        const size_t tg = static_cast<size_t>(ck) * QT + tr;
+        if (tg < L) {
             void *dst = isb ? g.db : g.dc;
             const size_t base = ((bb * L + tg) * H + hh) * N * R;
             st4<T, R>(dst, base + n0 * R + rr, v1);
