@@ -235,10 +235,12 @@ struct Smem {
     float Ms[kRows * LM], Ds[kRows * LM];
     float Ss[kP * LS], Gs[kP * LS];
     // per token and pair, rows of AP = NH + 3 words: a row-strided access by
-    // sixteen lanes then spreads over the banks instead of landing on one
+    // sixteen lanes then spreads over the banks instead of landing on one.
+    // cos and sin of the in-chunk angle; once every reader holds its values
+    // they take the two halves of the angle sums
     static constexpr int AP = NH + 3;
-    float psi[QT * AP];     // in-chunk angle
-    float cang[QT * AP];    // angle sums
+    float acs[QT * AP], asn[QT * AP];
+    float phi_end[NH];      // the chunk's angle total per pair
     float dtv[QT], lamv[QT], acum[QT], gw[QT], ww[QT], eac[QT], ebar[QT], wbar[QT];
     float rin[kRows], cinx[kRows], dwi[kRows], qv[kRows], rcr[kRows];
     float dgv[QT], dal[QT];
@@ -256,7 +258,8 @@ struct UVSmem {
     float Bs[N * LDR], Cs[N * LDR];
     float Xs[kP * LDR], Ys[kP * LDR];
     static constexpr int AP = NH + 3;
-    float psi[QT * AP];
+    float acs[QT * AP], asn[QT * AP];
+    float phi_end[NH];
     float dtv[QT], lamv[QT], acum[QT], gw[QT], ww[QT], eac[QT], ebar[QT], wbar[QT];
     __device__ static int bi(int rho, int n) { return n * LDR + rho; }
     __device__ static int xi(int rho, int p) { return p * LDR + rho; }
@@ -270,6 +273,11 @@ template <typename T, int N, int R, int kRows, bool WANT_B, bool WANT_X, int NTH
 __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, int ck) {
     constexpr int QT = S::QT, NH = S::NH, NW = NTH / 64;
     constexpr int TI = NH / NW;                 // angle pairs per wave
+    // chunks of at most 32 tokens scan two pairs per wave scan (lanes [0, 32)
+    // and [32, 64)); lane -> token tl of pair wave + (PK j + hl) NW
+    constexpr bool PACK = QT <= 32;
+    constexpr int PK = PACK ? 2 : 1, TS = TI / PK;
+    static_assert(TI % PK == 0, "paired angle scans");
     constexpr int JB = (QT * NH + NTH - 1) / NTH;   // (token, pair) items per thread
     constexpr int JX = kRows * kP / NTH;        // (row, p) items per thread
     static_assert(NH % NW == 0 && (kRows * kP) % NTH == 0, "stage split");
@@ -295,22 +303,23 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, i
             lamn = a.lambda[ix + H];
         }
     }
-    const size_t tgl = t0 + lane;
-    const bool tlive = lane < QT && tgl < L;
+    const int tl = PACK ? (lane & 31) : lane, hl = PACK ? (lane >> 5) : 0;
+    const size_t tgl = t0 + tl;
+    const bool tlive = tl < QT && tgl < L;
     // Loads are unconditional at clamped (in-bounds) indices and the dead
     // lanes zeroed afterwards, so no load sits behind a branch (which would
     // make each one wait for its data before the next is issued).
-    float th[TI];
+    float th[TS];
     if (rot) {
         const size_t th0 = ((bb * L + (tlive ? tgl : 0)) * H + hh) * NH;
 #pragma unroll
-        for (int j = 0; j < TI; ++j) {
-            const float v = ldv<T>(a.theta, th0 + wave + j * NW);
+        for (int j = 0; j < TS; ++j) {
+            const float v = ldv<T>(a.theta, th0 + wave + (PK * j + hl) * NW);
             th[j] = tlive ? v : 0.0f;
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < TI; ++j) th[j] = 0.0f;
+        for (int j = 0; j < TS; ++j) th[j] = 0.0f;
     }
     float b1[JB][R], b2[JB][R], c1[JB][R], c2[JB][R];
 #pragma unroll
@@ -365,11 +374,19 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, i
     }
     __syncthreads();
     if (rot) {
-        const float dtl = tlive ? sm.dtv[lane] : 0.0f;
+        // the in-chunk angle (inclusive cumsum of dt theta) and its cos / sin
+        const float dtl = tlive ? sm.dtv[tl] : 0.0f;
 #pragma unroll
-        for (int j = 0; j < TI; ++j) {
-            const float v = seg_scan<64>(dtl * th[j]);
-            if (lane < QT) sm.psi[lane * S::AP + wave + j * NW] = v;
+        for (int j = 0; j < TS; ++j) {
+            const int i = wave + (PK * j + hl) * NW;
+            const float v = PACK ? seg_scan<32>(dtl * th[j]) : seg_scan<64>(dtl * th[j]);
+            if (tl < QT) {
+                float sv, cv;
+                sincos_any<kPrecise>(v, sv, cv);
+                sm.acs[tl * S::AP + i] = cv;
+                sm.asn[tl * S::AP + i] = sv;
+            }
+            if (tl == QT - 1) sm.phi_end[i] = v;
         }
     }
 #pragma unroll
@@ -385,13 +402,16 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, i
         sm.ebar[tid] = clamp_exp(e - sm.acum[tid]);
         sm.wbar[tid] = sm.ebar[tid] * sm.ww[tid];
     }
-    // ---- rotation by -psi (fused.rs:610-617) into LDS
+    // ---- rotation by the negative in-chunk angle (fused.rs:610-617) into LDS
 #pragma unroll
     for (int j = 0; j < JB; ++j) {
         const int e = tid + j * NTH, t = e / NH, i = e % NH;
         if (e >= QT * NH) break;
         float sn = 0.0f, cs = 1.0f;
-        if (rot) sincos_any<kPrecise>(sm.psi[t * S::AP + i], sn, cs);
+        if (rot) {
+            cs = sm.acs[t * S::AP + i];
+            sn = sm.asn[t * S::AP + i];
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int rho = t * R + r;
@@ -429,7 +449,7 @@ __global__ void __launch_bounds__(kUVThreads) bwd_uv_kernel(ScanLaunch a, BwdArg
     // the chunk's scalars; B~ rows scaled by wbar, dY rows by e^{alpha}
     if (tid == 0) w.eda[bhk] = clamp_exp(sm.acum[QT - 1]);
     if (tid < NH) {
-        const float tot = a.theta != nullptr ? sm.psi[(QT - 1) * S::AP + tid] : 0.0f;
+        const float tot = a.theta != nullptr ? sm.phi_end[tid] : 0.0f;
         float ts = 0.0f, tc = 1.0f;
         if (a.theta != nullptr) sincosf(tot, &ts, &tc);
         w.phi[bhk * NH + tid] = tot;
@@ -688,7 +708,6 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
     constexpr int NT = kRows / 16;
     constexpr int QT = S::QT, NH = S::NH, NTN = N / 16;
     constexpr int LB = S::LB, LX = S::LX, LM = S::LM, LS = S::LS;
-    constexpr bool kPrecise = true;   // precise sines whatever the storage
     extern __shared__ __align__(16) unsigned char smem_raw[];
     S &sm = *reinterpret_cast<S *>(smem_raw);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -790,7 +809,10 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
         for (int r = 0; r < 4; ++r) {
             sn[r] = 0.0f;
             cs[r] = 1.0f;
-            if (rot) sincos_any<kPrecise>(sm.psi[tr * S::AP + n0 + r], sn[r], cs[r]);
+            if (rot) {
+                cs[r] = sm.acs[tr * S::AP + n0 + r];
+                sn[r] = sm.asn[tr * S::AP + n0 + r];
+            }
             o1[r] = own[row * LB + n0 + r];
             o2[r] = own[row * LB + n0 + r + NH];
         }
@@ -881,9 +903,9 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
     }
     // ---- phase 3b: the band halves of dC~ and dB~
     //   dC~^T[n][t] += sum_s B~[s][n] dCB[t][s],  dB~^T[n][s] += sum_t C~[t][n] dCB[t][s]
-    // then the angle sums (psi is free: every sine was taken in phase 1; psi
-    // receives the dB~ half, cang the dC~ half, one lane per (token, pair))
-    // and the rotation back, d = R(psi) d~ (the transpose of fused.rs:610-617)
+    // then the angle sums (every cos / sin was read in phase 1: asn receives
+    // the dB~ half, acs the dC~ half, one lane per (token, pair)) and the
+    // rotation back, d = R(psi) d~ (the transpose of fused.rs:610-617)
     if (has_job) {
         if (!isb)
             mma2_f32<kRows>(sm.Bs + 16 * ji, sm.Bs + 16 * (ji + PT), 1, LB, sm.Ds + 16 * rt * LM,
@@ -892,7 +914,7 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
             mma2_f32<kRows>(sm.Cs + 16 * ji, sm.Cs + 16 * (ji + PT), 1, LB, sm.Ds + 16 * rt, LM, 1,
                             lo, hi, c, gq);
         if (rot) {
-            float *half = isb ? sm.psi : sm.cang;
+            float *half = isb ? sm.asn : sm.acs;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 float cr = lo[r] * o2[r] - hi[r] * o1[r];
@@ -964,7 +986,7 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
     __syncthreads();
     // in-chunk reverse cumsums as wave scans over lanes in reverse token order
     // (lane l holds token QT-1-l): da from dalpha (wave 0), and per rotation
-    // pair the angle sums (pairs spread over the waves, written back to cang)
+    // pair the angle sums (pairs spread over the waves, written back to acs)
     {
         const int t = QT - 1 - lane;
         const size_t tg = static_cast<size_t>(ck) * QT + t;
@@ -976,8 +998,8 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
         if (a.theta != nullptr) {
             for (int i = wave; i < NH; i += kWaves) {
                 const float v = seg_scan<64>(
-                    lane < QT ? sm.cang[t * S::AP + i] + sm.psi[t * S::AP + i] : 0.0f);
-                if (lane < QT) sm.cang[t * S::AP + i] = v;
+                    lane < QT ? sm.acs[t * S::AP + i] + sm.asn[t * S::AP + i] : 0.0f);
+                if (lane < QT) sm.acs[t * S::AP + i] = v;
                 if (lane == QT - 1) w.ctot[bhk * NH + i] = v;
             }
         }
@@ -988,7 +1010,7 @@ __global__ void __launch_bounds__(kBT, 1) bwd_chunk_kernel(ScanLaunch a, BwdArgs
         for (int e = tid; e < QT * NH; e += kBT) {
             const int t = e / NH, i = e % NH;
             const size_t tg = static_cast<size_t>(ck) * QT + t;
-            if (tg < L) w.cin[(bh * L + tg) * NH + i] = sm.cang[t * S::AP + i];
+            if (tg < L) w.cin[(bh * L + tg) * NH + i] = sm.acs[t * S::AP + i];
         }
     }
 }
