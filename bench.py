@@ -419,6 +419,70 @@ def bench_decode_lm(torch, args):
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "steps": steps}
 
 
+# BASELINE configs 0 and 2 (parity cases; their forward scans are reported beside
+# the headline): name -> (B, L, H, P, N, R, bf16, rotational)
+OTHER_SCANS = {"config0": (2, 512, 4, 64, 64, 1, False, False),
+               "config2": (4, 4096, 24, 64, 128, 4, True, True)}
+
+
+def bench_other_scans(torch, lib, L_, args):
+    """Forward scans of configs 0 (f32, Real, SISO) and 2 (bf16, Rotational,
+    MIMO rank 4) through m3_scan with the workspace the library asks for."""
+    dev = "cuda:0"
+    out = {}
+    for name, (B, L, H, P, N, R, bf16, rot) in OTHER_SCANS.items():
+        g = torch.Generator(device=dev).manual_seed(0x4D414D43)
+        st = torch.bfloat16 if bf16 else torch.float32
+        x = torch.randn(B, L, H, P, R, device=dev, generator=g).to(st)
+        b = (torch.randn(B, L, H, N, R, device=dev, generator=g) / math.sqrt(N)).to(st)
+        c = (torch.randn(B, L, H, N, R, device=dev, generator=g) / math.sqrt(N)).to(st)
+        dt = torch.nn.functional.softplus(torch.randn(B, L, H, device=dev, generator=g) - 3.0
+                                          ).clamp(1e-3, 0.1)
+        lam = torch.sigmoid(torch.randn(B, L, H, device=dev, generator=g))
+        a_log = torch.rand(H, device=dev, generator=g) * math.log(16.0)
+        th = ((torch.rand(1, 1, H, N // 2, device=dev, generator=g) * math.pi)
+              .expand(B, L, H, N // 2).contiguous().to(st)) if rot else None
+        y = torch.empty_like(x)
+        h = torch.empty(B, H, P, N, device=dev)
+        lu = torch.empty_like(h)
+        ang = torch.empty(B, H, N // 2, device=dev) if rot else None
+        cin = L_.ScanInputsC(B, L, H, P, N, R, L_.M3_BF16 if bf16 else L_.M3_F32, x.data_ptr(),
+                             b.data_ptr(), c.data_ptr(), dt.data_ptr(), a_log.data_ptr(),
+                             lam.data_ptr(), th.data_ptr() if rot else None, None, None, 64, 1,
+                             None, 0)
+        need = int(lib.m3_scan_workspace_bytes(C.byref(cin)))
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        if need:
+            cin.workspace, cin.workspace_bytes = ws.data_ptr(), need
+        cout = L_.ScanOutputC(y.data_ptr(), L_.SsmStateC(h.data_ptr(), lu.data_ptr(),
+                                                         ang.data_ptr() if rot else None))
+        stream = torch.cuda.current_stream()
+        call = lambda: L_.check(lib.m3_scan(C.byref(cin), C.byref(cout),
+                                            C.c_void_p(stream.cuda_stream)))
+        for _ in range(5):
+            call()
+        torch.cuda.synchronize()
+        steps = max(10, args.steps // 4)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / steps * 1e3
+        assert bool(torch.isfinite(y.float()).all())
+        nbytes, flops = scan_algorithmic(B, L, H, P, N, R, 64, s_io=2 if bf16 else 4,
+                                         theta_per_token=rot)
+        out[name] = {"workload": f"B={B} L={L} H={H} P={P} N={N} R={R} "
+                                 f"{'bf16' if bf16 else 'f32'} {'Rotational' if rot else 'Real'}",
+                     "us_per_call": round(us, 2), "tokens_per_s": round(B * L / (us * 1e-6), 1),
+                     "path": "chunk-parallel" if need else "single pass",
+                     "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "mfma_tflops": round(flops / (us * 1e-6) / 1e12, 2)}
+    return out
+
+
 def bench_decode(torch, lib, L_, args):
     dev = "cuda:0"
     d = DECODE
@@ -476,10 +540,25 @@ def bench_decode(torch, lib, L_, args):
     assert torch.isfinite(h).all(), "non-finite decode state"
     nbytes = NL * decode_algorithmic(B, H, P, N, R)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    # a practical stream ceiling beside it: torch's device copy of one layer's
+    # h and last_u (the same bytes read and written as one layer's update)
+    src = torch.cat([h[0].reshape(-1), lu[0].reshape(-1)])
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    reps = 20
+    e0.record(stream)
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    copy_gbs = 2 * src.numel() * 4 / (e0.elapsed_time(e1) / reps * 1e-3) / 1e9
     return dict(us_per_step=round(ms * 1e3, 2), steps=args.decode_steps, layers=NL,
                 bytes_per_step=nbytes, achieved_GBps=round(gbs, 1),
                 frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4),
-                us_per_layer=round(ms * 1e3 / NL, 2))
+                us_per_layer=round(ms * 1e3 / NL, 2),
+                device_copy_GBps=round(copy_gbs, 1))
 
 
 def cpu_baseline(args):
@@ -590,6 +669,7 @@ def main():
 
     bwd = None if args.no_backward else bench_backward(torch, lib, L_, args, sc["inp"],
                                                        sc["kernel_ms"])
+    other = bench_other_scans(torch, lib, L_, args)
     dec = None if args.no_decode else bench_decode(torch, lib, L_, args)
     pre = None if args.no_prefill else bench_prefill(torch, args)
     dlm = None if args.no_decode_lm else bench_decode_lm(torch, args)
@@ -624,6 +704,7 @@ def main():
                      "mfma_tflops": round(tflops, 2),
                      "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)},
         "scan_single_pass_us": round(sc1["kernel_ms"] * 1e3, 2),
+        "other_scans": other,
         "backward": bwd,
         "decode": dec,
         "prefill": pre,
