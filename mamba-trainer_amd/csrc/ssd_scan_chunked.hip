@@ -124,10 +124,17 @@ struct StateSmem {
     static constexpr int LDR = ROWS + PAD;
     op_t Bwt[N * LDR];      // (B^(k) * w * decay-to-end)^T [n][rho]
     op_t Xt[kP * LDR];      // X^T [p][rho]
-    float phi_tot[N / 2];
+    float phi_tot[N / 2];   // the sub-chunk's angle total per pair
+    float phi_acc[N / 2];   // the chunk's so far
 };
 
-template <typename T, int N, int R, int ROWS>
+// A chunk here is HALF sub-chunks of ROWS rows (the MIMO ranks take HALF = R,
+// so that a chunk spans ROWS tokens whatever the rank), staged one after the
+// other.  With U_h, e_h, Phi_h those of sub-chunk h in its own frame, the
+// chunk's are accumulated as U = e_h U + R(-Phi) U_h, e = e e_h,
+// Phi = Phi + Phi_h: the state recurrence S' = R(Phi)(e S + U) composed over
+// the sub-chunks (the per-pair rotations commute).
+template <typename T, int N, int R, int ROWS, int HALF>
 __global__ void __launch_bounds__(kThreads, 2)
 chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     constexpr int P = kP;
@@ -162,88 +169,140 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     const int i0 = wave * G::PW + sub * PPL;
 
     const SeqBufs rs = seq_bufs<T, N, P, R>(a, bb, hh);
-    RawT cur;
-    load_chunk<T, N, P, R, ROWS, 4, false>(rs, ck, wave, lane, cur);
 
     float A = 0.0f;
     if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);   // a_log.exp().neg() (scan.rs:470-474)
 
-    const size_t tau = static_cast<size_t>(ck) * QT + my_t;
-    const bool live = tok_lane && tau < L;
-    float av, gv, wv;
-    token_scalars(a, cur, A, live, av, gv, wv);
-    const float acum = seg_scan<G::SW>(av);
-    const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
-    const float wd = dexp<kBf16>(last - acum) * wv;   // exp_decay(last, acum, w)
-    if (tid == 0) ws.eda[bhk] = dexp<kBf16>(last);
+    // U^T[n][p] of this wave's p-tile, accumulated over the sub-chunks
+    f32x4 uacc[NTN];
+    float eacc = 1.0f;
+#pragma unroll 1
+    for (int h = 0; h < HALF; ++h) {
+        const int sck = ck * HALF + h;
+        RawT cur;
+        load_chunk<T, N, P, R, ROWS, 4, false>(rs, sck, wave, lane, cur);
 
-    // in-chunk angle (inclusive cumsum of dt * theta), rotation by its negative
-    float cs[PPL], sn[PPL];
-#pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-        cs[j] = 1.0f;
-        sn[j] = 0.0f;
-    }
-    if (rot) {
-        const float dtt = live ? cur.s0 : 0.0f;
+        const size_t tau = static_cast<size_t>(sck) * QT + my_t;
+        const bool live = tok_lane && tau < L;
+        float av, gv, wv;
+        token_scalars(a, cur, A, live, av, gv, wv);
+        const float acum = seg_scan<G::SW>(av);
+        const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
+        const float wd = dexp<kBf16>(last - acum) * wv;   // exp_decay(last, acum, w)
+        const float eh = dexp<kBf16>(last);
+
+        // in-chunk angle (inclusive cumsum of dt * theta), rotation by its negative
+        float cs[PPL], sn[PPL];
 #pragma unroll
         for (int j = 0; j < PPL; ++j) {
-            const float pre = seg_scan<G::SW>(dtt * welem<T>(cur.th, j));
-            if (my_t == QT - 1) sm.phi_tot[i0 + j] = pre;
-            const float psi = wrap_angle(pre);
-            if constexpr (kBf16) {
-                // the hardware sine takes revolutions; |psi| <= pi
-                const float rev = psi * 0.15915494309189533577f;
-                sn[j] = __builtin_amdgcn_sinf(rev);
-                cs[j] = __builtin_amdgcn_cosf(rev);
-            } else {
-                sincosf(psi, &sn[j], &cs[j]);
-            }
+            cs[j] = 1.0f;
+            sn[j] = 0.0f;
         }
-    }
-    if (tok_lane) {
-#pragma unroll
-        for (int e = 0; e < G::XE; ++e) {
-            const int o = wave * (P / 4) * R + sub * G::XE + e;
-            const int p = o / R, r = o % R;
-            sm.Xt[p * LDR + my_t * R + r] = to_op<op_t>(elem<T>(cur.x, e));
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int rho = my_t * R + r;
+        if (rot) {
+            const float dtt = live ? cur.s0 : 0.0f;
 #pragma unroll
             for (int j = 0; j < PPL; ++j) {
-                const float b1 = elem<T>(cur.b[0], j * R + r);
-                const float b2 = elem<T>(cur.b[1], j * R + r);
-                const float w1 = (b1 * cs[j] + b2 * sn[j]) * wd;    // fused.rs:610-617
-                const float w2 = (-b1 * sn[j] + b2 * cs[j]) * wd;
-                sm.Bwt[(i0 + j) * LDR + rho] = to_op<op_t>(w1);
-                sm.Bwt[(i0 + NH + j) * LDR + rho] = to_op<op_t>(w2);
+                const float pre = seg_scan<G::SW>(dtt * welem<T>(cur.th, j));
+                if (my_t == QT - 1) sm.phi_tot[i0 + j] = pre;
+                const float psi = wrap_angle(pre);
+                if constexpr (kBf16) {
+                    // the hardware sine takes revolutions; |psi| <= pi
+                    const float rev = psi * 0.15915494309189533577f;
+                    sn[j] = __builtin_amdgcn_sinf(rev);
+                    cs[j] = __builtin_amdgcn_cosf(rev);
+                } else {
+                    sincosf(psi, &sn[j], &cs[j]);
+                }
             }
         }
-    }
-    __syncthreads();
-
-    // the chunk's angle total per pair, with its cosine and sine
-    if (tid < NH) {
-        const float tot = rot ? sm.phi_tot[tid] : 0.0f;
-        float ts = 0.0f, tc = 1.0f;
-        if (rot) sincosf(tot, &ts, &tc);
-        ws.phi[bhk * NH + tid] = tot;
-        ws.cph[bhk * NH + tid] = tc;
-        ws.sph[bhk * NH + tid] = ts;
-    }
-
-    // U^T[n][p] = sum_rho Bwt[n][rho] X^T[p][rho]; wave w takes p-tile w
-    const op_t *xr = &sm.Xt[(16 * wave + c) * LDR];
-    const size_t uo = (bhk * 4 + wave) * NTN * 256 + lane * 4;
+        if (tok_lane) {
 #pragma unroll
-    for (int i = 0; i < NTN; ++i) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const op_t *ar = &sm.Bwt[(16 * i + c) * LDR];
+            for (int e = 0; e < G::XE; ++e) {
+                const int o = wave * (P / 4) * R + sub * G::XE + e;
+                const int p = o / R, r = o % R;
+                sm.Xt[p * LDR + my_t * R + r] = to_op<op_t>(elem<T>(cur.x, e));
+            }
 #pragma unroll
-        for (int kb = 0; kb < ROWS / KB; ++kb) acc = mma_kb(ar + kb * KB, xr + kb * KB, acc, g);
-        store_u<kBf16>(ws.u, uo + i * 256, acc);
+            for (int r = 0; r < R; ++r) {
+                const int rho = my_t * R + r;
+#pragma unroll
+                for (int j = 0; j < PPL; ++j) {
+                    const float b1 = elem<T>(cur.b[0], j * R + r);
+                    const float b2 = elem<T>(cur.b[1], j * R + r);
+                    const float w1 = (b1 * cs[j] + b2 * sn[j]) * wd;    // fused.rs:610-617
+                    const float w2 = (-b1 * sn[j] + b2 * cs[j]) * wd;
+                    sm.Bwt[(i0 + j) * LDR + rho] = to_op<op_t>(w1);
+                    sm.Bwt[(i0 + NH + j) * LDR + rho] = to_op<op_t>(w2);
+                }
+            }
+        }
+        __syncthreads();
+
+        if constexpr (HALF == 1) {
+            // the chunk's angle total per pair, with its cosine and sine
+            if (tid < NH) {
+                const float tot = rot ? sm.phi_tot[tid] : 0.0f;
+                float ts = 0.0f, tc = 1.0f;
+                if (rot) sincosf(tot, &ts, &tc);
+                ws.phi[bhk * NH + tid] = tot;
+                ws.cph[bhk * NH + tid] = tc;
+                ws.sph[bhk * NH + tid] = ts;
+            }
+            if (tid == 0) ws.eda[bhk] = eh;
+        }
+        // U_h^T[n][p] = sum_rho Bwt[n][rho] X^T[p][rho]; wave w takes p-tile w
+        const op_t *xr = &sm.Xt[(16 * wave + c) * LDR];
+        const size_t uo = (bhk * 4 + wave) * NTN * 256 + lane * 4;
+        f32x4 uh[NTN];
+#pragma unroll
+        for (int i = 0; i < NTN; ++i) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const op_t *ar = &sm.Bwt[(16 * i + c) * LDR];
+#pragma unroll
+            for (int kb = 0; kb < ROWS / KB; ++kb) acc = mma_kb(ar + kb * KB, xr + kb * KB, acc, g);
+            if constexpr (HALF == 1) store_u<kBf16>(ws.u, uo + i * 256, acc);
+            uh[i] = acc;
+        }
+        if constexpr (HALF > 1) {
+            if (h == 0) {
+#pragma unroll
+                for (int i = 0; i < NTN; ++i) uacc[i] = uh[i];
+            } else {
+                // U = e_h U + R(-Phi) U_h over the pairs (n, n + N/2): tiles i, i + NTN/2
+#pragma unroll
+                for (int i = 0; i < NTN / 2; ++i) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float ps = 0.0f, pc = 1.0f;
+                        if (rot) sincosf(sm.phi_acc[16 * i + 4 * g + r], &ps, &pc);
+                        const float lo = uh[i][r], hi = uh[i + NTN / 2][r];
+                        uacc[i][r] = eh * uacc[i][r] + lo * pc + hi * ps;
+                        uacc[i + NTN / 2][r] = eh * uacc[i + NTN / 2][r] - lo * ps + hi * pc;
+                    }
+                }
+            }
+            eacc *= eh;
+            __syncthreads();   // every read of this sub-chunk's LDS is done
+            if (tid < NH)
+                sm.phi_acc[tid] = (h == 0 ? 0.0f : sm.phi_acc[tid]) + (rot ? sm.phi_tot[tid] : 0.0f);
+            __syncthreads();
+        }
+    }
+
+    if constexpr (HALF > 1) {
+        const size_t uo = (bhk * 4 + wave) * NTN * 256 + lane * 4;
+#pragma unroll
+        for (int i = 0; i < NTN; ++i) store_u<kBf16>(ws.u, uo + i * 256, uacc[i]);
+        if (tid == 0) ws.eda[bhk] = eacc;
+        // the chunk's angle total per pair, with its cosine and sine
+        if (tid < NH) {
+            const float tot = sm.phi_acc[tid];
+            float ts = 0.0f, tc = 1.0f;
+            if (rot) sincosf(tot, &ts, &tc);
+            ws.phi[bhk * NH + tid] = tot;
+            ws.cph[bhk * NH + tid] = tc;
+            ws.sph[bhk * NH + tid] = ts;
+        }
     }
 }
 
@@ -393,7 +452,7 @@ state_pass_kernel(ScanLaunch a, ChunkWs ws, int nck) {
 }
 
 // ================================================================ chunk scan
-template <typename T, int N, int R, int ROWS>
+template <typename T, int N, int R, int ROWS, int HALF>
 struct ScanSmem {
     using G = Geo<T, N, kP, R, ROWS, 4>;
     using op_t = typename Op<T>::t;
@@ -405,14 +464,20 @@ struct ScanSmem {
     op_t Xt[kP * LDR];      // X^T [p][rho]
     op_t Ms[ROWS * LDR];    // masked band (C B^T o L)[rho_t][rho_s]
     float acum[G::QT], gw[G::QT], ww[G::QT], eac[G::QT];
+    // with sub-chunks: the sub-chunk's angle total per pair, w x decay to its end per token
+    float phi_tot[HALF > 1 ? N / 2 : 1];
+    float wdv[HALF > 1 ? G::QT : 1];
 };
 
-template <typename T, int N, int R, int ROWS>
-__global__ void __launch_bounds__(kThreads, 3)
+// HALF sub-chunks of ROWS rows per chunk, one after the other: between them
+// the state advances in registers, S' = R(Phi_h)(e_h S + U_h), with U_h formed
+// from the sub-chunk's staged B~ and X^T.
+template <typename T, int N, int R, int ROWS, int HALF>
+__global__ void __launch_bounds__(kThreads, HALF > 1 ? 2 : 3)
 chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     constexpr int P = kP;
     using G = Geo<T, N, P, R, ROWS, 4>;
-    using S = ScanSmem<T, N, R, ROWS>;
+    using S = ScanSmem<T, N, R, ROWS, HALF>;
     using RawT = Raw<T, N, P, R, ROWS, 4, true>;
     using op_t = typename S::op_t;
     constexpr int KB = Op<T>::KB;
@@ -445,8 +510,10 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     const int pcol = 16 * wave + c;
 
     const SeqBufs rs = seq_bufs<T, N, P, R>(a, bb, hh);
+    // without sub-chunks the chunk's inputs go first: the stage waits for them
+    // while the state fragments below are still in flight
     RawT cur;
-    load_chunk<T, N, P, R, ROWS, 4, true>(rs, ck, wave, lane, cur);
+    if constexpr (HALF == 1) load_chunk<T, N, P, R, ROWS, 4, true>(rs, ck, wave, lane, cur);
 
     // the state entering this chunk, in its frame, as carry-in A operands
     // (bf16: n-tiles 2kb and 2kb + 1 form k-block kb, matching npos)
@@ -471,9 +538,13 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     const float dskip = a.d_skip ? a.d_skip[hh] : 0.0f;
     const bool skip = a.d_skip != nullptr;
 
+#pragma unroll 1
+    for (int h = 0; h < HALF; ++h) {
+    const int sck = ck * HALF + h;
+    if constexpr (HALF > 1) load_chunk<T, N, P, R, ROWS, 4, true>(rs, sck, wave, lane, cur);
     // ---- stage: per-token scalars, in-chunk angles, rotated B and C, X^T
     {
-        const size_t tau = static_cast<size_t>(ck) * QT + my_t;
+        const size_t tau = static_cast<size_t>(sck) * QT + my_t;
         const bool live = tok_lane && tau < L;
         float av, gv, wv;
         token_scalars(a, cur, A, live, av, gv, wv);
@@ -483,6 +554,11 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
             sm.gw[my_t] = gv;
             sm.ww[my_t] = wv;
             sm.eac[my_t] = dexp<kBf16>(acum);             // exp_decay(acum)
+            if (HALF > 1) {
+                const float last = __int_as_float(
+                    __builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
+                sm.wdv[my_t] = dexp<kBf16>(last - acum) * wv;   // w x decay to the end
+            }
         }
         float cs[PPL], sn[PPL];
 #pragma unroll
@@ -494,7 +570,9 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
             const float dtt = live ? cur.s0 : 0.0f;
 #pragma unroll
             for (int j = 0; j < PPL; ++j) {
-                const float psi = wrap_angle(seg_scan<G::SW>(dtt * welem<T>(cur.th, j)));
+                const float pre = seg_scan<G::SW>(dtt * welem<T>(cur.th, j));
+                if (HALF > 1 && my_t == QT - 1) sm.phi_tot[i0 + j] = pre;
+                const float psi = wrap_angle(pre);
                 if constexpr (kBf16) {
                     const float rev = psi * 0.15915494309189533577f;
                     sn[j] = __builtin_amdgcn_sinf(rev);
@@ -594,7 +672,7 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
 
     // ---- y^T[p][t] = exp(acum_t) sum_n S[p][n] C[t][n] + sum_s X^T[p][s] M[t][s]
     const op_t *xr = &sm.Xt[pcol * LDR];
-    const uint32_t tau0 = static_cast<uint32_t>(ck) * QT;
+    const uint32_t tau0 = static_cast<uint32_t>(sck) * QT;
 #pragma unroll
     for (int tj = 0; tj < NT; ++tj) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -648,25 +726,109 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
             }
         }
     }
+
+    if (h + 1 < HALF) {
+        // ---- the state entering the next sub-chunk: S' = R(Phi_h)(e_h S + U_h),
+        // U_h^T[n][p] = sum_rho (B~ w decay-to-end)[rho][n] X^T[p][rho] over
+        // this wave's p-tile; the D tiles of U line up with the S fragments
+        const float eh = dexp<kBf16>(sm.acum[QT - 1]);
+        f32x4 uh[NTN];
+#pragma unroll
+        for (int i = 0; i < NTN; ++i) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const int n = 16 * i + c;
+#pragma unroll
+            for (int kb = 0; kb < ROWS / KB; ++kb) {
+                if constexpr (kBf16) {
+                    bf16x8 av;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int rho = 32 * kb + 8 * g + j;
+                        av[j] = static_cast<__bf16>(
+                            static_cast<float>(sm.Bs[rho * LDN + npos<kBf16>(n)]) * sm.wdv[rho / R]);
+                    }
+                    acc = mfma_bf16(av, *reinterpret_cast<const bf16x8 *>(xr + 32 * kb + 8 * g), acc);
+                } else {
+                    const f32x4 bv = *reinterpret_cast<const f32x4 *>(xr + 16 * kb + 4 * g);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int rho = 16 * kb + 4 * g + j;
+                        acc = mfma_f32(static_cast<float>(sm.Bs[rho * LDN + n]) * sm.wdv[rho / R],
+                                       bv[j], acc);
+                    }
+                }
+            }
+            uh[i] = acc;
+        }
+        // S (this lane: p = 16 wave + c, n = 16 i + 4 g + r) in f32, advanced and rotated
+        f32x4 st[NTN];
+#pragma unroll
+        for (int i = 0; i < NTN; ++i) {
+            if constexpr (kBf16) {
+                const bf16x8 f = sf[i / 2];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) st[i][r] = static_cast<float>(f[(i & 1) * 4 + r]);
+            } else {
+                st[i] = sf[i];
+            }
+            st[i] = st[i] * eh + uh[i];
+        }
+        if (rot) {
+#pragma unroll
+            for (int i = 0; i < NTN / 2; ++i) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float ps, pc;
+                    sincosf(sm.phi_tot[16 * i + 4 * g + r], &ps, &pc);
+                    const float lo = st[i][r], hi = st[i + NTN / 2][r];
+                    st[i][r] = lo * pc - hi * ps;                  // R(Phi_h)
+                    st[i + NTN / 2][r] = lo * ps + hi * pc;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NTN; ++i) {
+            if constexpr (kBf16) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sf[i / 2][(i & 1) * 4 + r] = static_cast<__bf16>(st[i][r]);
+            } else {
+                sf[i] = st[i];
+            }
+        }
+        lds_barrier();   // the next sub-chunk's staging reuses the LDS
+    }
+    }   // sub-chunks
+}
+
+// Sub-chunks per chunk of the three launches: one per rank, so that a chunk
+// spans ROWS tokens whatever the rank and the U / S records and the state
+// pass stay per ROWS tokens (the MIMO ranks would otherwise multiply them).
+constexpr int half_for(int r) { return r; }
+
+size_t chunk_count(const ScanLaunch &a, int rows) {
+    const size_t qt = static_cast<size_t>(rows) / a.rank;
+    const size_t nsub = (a.seq + qt - 1) / qt;
+    const size_t half = static_cast<size_t>(half_for(static_cast<int>(a.rank)));
+    return (nsub + half - 1) / half;
 }
 
 template <typename T, int N, int R, int ROWS>
 hipError_t launch_three(const ScanLaunch &a, char *base, hipStream_t s) {
-    constexpr int QT = ROWS / R;
-    const int nck = static_cast<int>((a.seq + QT - 1) / QT);
+    constexpr int HALF = half_for(R);
+    const int nck = static_cast<int>(chunk_count(a, ROWS));
     const size_t bh = a.batch * a.heads;
     const size_t bhk = bh * nck;
     const ChunkWs ws = chunk_ws(base, chunked_layout(bhk, N, sizeof(T) == 2));
-    hipLaunchKernelGGL((chunk_state_kernel<T, N, R, ROWS>), dim3(bhk), dim3(kThreads), 0, s, a, ws,
-                       nck);
+    hipLaunchKernelGGL((chunk_state_kernel<T, N, R, ROWS, HALF>), dim3(bhk), dim3(kThreads), 0, s,
+                       a, ws, nck);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((state_pass_kernel<T, N>), dim3(bh * (N / 32)), dim3(kThreads), 0, s, a, ws,
                        nck);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((chunk_scan_kernel<T, N, R, ROWS>), dim3(bhk), dim3(kThreads), 0, s, a, ws,
-                       nck);
+    hipLaunchKernelGGL((chunk_scan_kernel<T, N, R, ROWS, HALF>), dim3(bhk), dim3(kThreads), 0, s,
+                       a, ws, nck);
     return hipGetLastError();
 }
 
@@ -722,9 +884,8 @@ size_t scan_chunked_workspace(const ScanLaunch &a) {
     if (!scan_fast_supported(a) || a.seq == 0) return 0;
     if (a.batch * a.heads * 10 >= device_cus() * 7) return 0;
     if (use_lookback(a)) return scan_lookback_workspace(a);
-    const size_t qt = static_cast<size_t>(rows_for(a)) / a.rank;
-    const size_t nck = (a.seq + qt - 1) / qt;
-    return chunked_layout(a.batch * a.heads * nck, a.d_state, a.bf16 != 0).total;
+    return chunked_layout(a.batch * a.heads * chunk_count(a, rows_for(a)), a.d_state, a.bf16 != 0)
+        .total;
 }
 
 hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream) {
