@@ -510,10 +510,14 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     const int pcol = 16 * wave + c;
 
     const SeqBufs rs = seq_bufs<T, N, P, R>(a, bb, hh);
-    // without sub-chunks the chunk's inputs go first: the stage waits for them
-    // while the state fragments below are still in flight
-    RawT cur;
-    if constexpr (HALF == 1) load_chunk<T, N, P, R, ROWS, 4, true>(rs, ck, wave, lane, cur);
+    // The (first sub-)chunk's inputs go first: the stage waits for them while
+    // the state fragments below are still in flight.  bf16 sub-chunks then load
+    // the next sub-chunk's inputs behind the current one's work (f32 lacks the
+    // registers for it).
+    constexpr bool kPrefetch = HALF > 1 && sizeof(T) == 2;
+    RawT cur, nxt;
+    if constexpr (HALF == 1 || kPrefetch)
+        load_chunk<T, N, P, R, ROWS, 4, true>(rs, ck * HALF, wave, lane, HALF == 1 ? cur : nxt);
 
     // the state entering this chunk, in its frame, as carry-in A operands
     // (bf16: n-tiles 2kb and 2kb + 1 form k-block kb, matching npos)
@@ -541,7 +545,12 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
 #pragma unroll 1
     for (int h = 0; h < HALF; ++h) {
     const int sck = ck * HALF + h;
-    if constexpr (HALF > 1) load_chunk<T, N, P, R, ROWS, 4, true>(rs, sck, wave, lane, cur);
+    if constexpr (kPrefetch) {
+        cur = nxt;
+        if (h + 1 < HALF) load_chunk<T, N, P, R, ROWS, 4, true>(rs, sck + 1, wave, lane, nxt);
+    } else if constexpr (HALF > 1) {
+        load_chunk<T, N, P, R, ROWS, 4, true>(rs, sck, wave, lane, cur);
+    }
     // ---- stage: per-token scalars, in-chunk angles, rotated B and C, X^T
     {
         const size_t tau = static_cast<size_t>(sck) * QT + my_t;
