@@ -860,12 +860,14 @@ int rows_for(const ScanLaunch &a) { return a.bf16 ? 64 : 32; }
 
 }  // namespace
 
-// The single pass walks each (batch, head) sequence with one workgroup per CU;
-// once the sequences fill most of the chip it moves less data than the three
-// chunk-parallel launches and is the faster form (measured on MI355X: 96
-// sequences of config 1 take 113 us chunked vs 191 us single pass; 192
-// sequences take 250 us vs 227 us).  The workspace is asked for only below
-// that point.
+// The single pass walks each (batch, head) sequence with one workgroup per CU,
+// so its time goes in whole rounds of one sequence per CU; the three
+// chunk-parallel launches cost about the same per sequence at any count.  The
+// single pass is the faster form once the last round fills ~70 % of the chip
+// (measured on MI355X at L = 2048, H = 12, N = 128, bf16, in us chunked vs
+// single pass: 96 sequences 107 vs 191, 192: 239 vs 222, 240: 299 vs 227,
+// 288: 367 vs 434, 384: 482 vs 442).  The workspace is asked for only where
+// the chunked form wins.
 static size_t device_cus() {
     static int cus = 0;
     if (cus == 0) {
@@ -891,7 +893,9 @@ static bool use_lookback(const ScanLaunch &a) {
 
 size_t scan_chunked_workspace(const ScanLaunch &a) {
     if (!scan_fast_supported(a) || a.seq == 0) return 0;
-    if (a.batch * a.heads * 10 >= device_cus() * 7) return 0;
+    const size_t seqs = a.batch * a.heads, cus = device_cus();
+    const size_t rounds = (seqs + cus - 1) / cus;
+    if (seqs * 10 >= rounds * cus * 7) return 0;
     if (use_lookback(a)) return scan_lookback_workspace(a);
     return chunked_layout(a.batch * a.heads * chunk_count(a, rows_for(a)), a.d_state, a.bf16 != 0)
         .total;

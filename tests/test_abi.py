@@ -168,9 +168,13 @@ def test_scan_workspace_query():
     assert w1 == bhk * (2 * 64 * 128 * 2 + 4 + 3 * 64 * 4)
     # f32 storage: 32-token chunks at rank 1 and an f32 S_k
     assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) == 2 * bhk * (64 * 128 * 8 + 4 + 3 * 64 * 4)
-    # 192 sequences fill most of the 256 CUs: the single pass is the faster form
-    assert need(16, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 0
-    assert need(14, 2048, 12, 64, 128, 1, _lib.M3_BF16) > 0   # 168 sequences
+    # the single pass runs one sequence per CU (256 CUs here, the CPU
+    # fallback of the query): it is the faster form once its last round of
+    # sequences fills 70 % of the CUs
+    assert need(16, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 0   # 192 sequences
+    assert need(14, 2048, 12, 64, 128, 1, _lib.M3_BF16) > 0    # 168
+    assert need(24, 2048, 12, 64, 128, 1, _lib.M3_BF16) > 0    # 288: 1.13 rounds
+    assert need(32, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 0   # 384: 1.5 rounds
     assert need(1, 100, 2, 48, 128, 1, _lib.M3_BF16) == 0      # head_dim 48
     assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) == 0       # d_state 96
     assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) == 0      # rank 3
