@@ -218,14 +218,22 @@ def test_config2_mimo_bf16_one_head():
     assert rel_l2(h, h64) <= BF16_TOL
 
 
-@pytest.mark.parametrize("R", [1, 4])
-def test_chunk_parallel_matches_single_pass_at_benchmark_shapes(R):
-    """Configs 1 and 2 at full batch and head count (shorter sequence): the
-    chunk-parallel kernels and the single-pass kernel agree, and both match the
-    f64 recurrence on two of the sequences."""
+@pytest.mark.parametrize("B,T,H,R", [(8, 512, 12, 1), (4, 256, 24, 4), (24, 200, 12, 1)],
+                         ids=["config1", "config2", "288_sequences"])
+def test_chunk_parallel_matches_single_pass_at_benchmark_shapes(B, T, H, R):
+    """Configs 1 and 2 at full batch and head count (shorter sequence), and 288
+    sequences (past one round of the single pass's one sequence per CU, where
+    the chunked launches are chosen again): the chunk-parallel kernels and the
+    single-pass kernel agree, and both match the f64 recurrence on two of the
+    sequences."""
+    import ctypes as C
+    from mamba3 import _lib
     from mamba3.ssm import ScanInputs, mamba3_scan
-    g = torch.Generator(device="cuda").manual_seed(7 + R)
-    B, T, H, P, N = (8, 512, 12, 64, 128) if R == 1 else (4, 256, 24, 64, 128)
+    g = torch.Generator(device="cuda").manual_seed(7 + R + B)
+    P, N = 64, 128
+    cin = _lib.ScanInputsC(B, T, H, P, N, R, _lib.M3_BF16, 16, 16, 16, 16, 16, 16, 16, None,
+                           None, 64, 1, None, 0)
+    assert _lib.lib().m3_scan_workspace_bytes(C.byref(cin)) > 0   # the chunked form runs
     x = torch.randn(B, T, H, P, R, device="cuda", generator=g).to(torch.bfloat16)
     b = (torch.randn(B, T, H, N, R, device="cuda", generator=g) / math.sqrt(N)).to(torch.bfloat16)
     c = (torch.randn(B, T, H, N, R, device="cuda", generator=g) / math.sqrt(N)).to(torch.bfloat16)
