@@ -404,8 +404,44 @@ def bench_decode_lm(torch, args):
         logits = lm.forward_cached(ids[i % 16], cache)
     e1.record(stream)
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    ms_eager = e0.elapsed_time(e1) / steps
     assert torch.isfinite(logits.float()).all(), "non-finite logits"
+    # the same step captured once as a HIP graph and replayed (the serving form)
+    graph = lm.capture_decode(cache, B)
+    for i in range(2):
+        graph.step(ids[i])
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(steps):
+        logits = graph.step(ids[i % 16])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    assert torch.isfinite(logits.float()).all(), "non-finite logits (graph)"
+    # at batch 1 the eager step is bound by the host issuing its launches; the
+    # graph replay is not
+    small = {}
+    cache1 = lm.empty_cache(1, dev)
+    ids1 = ids[:, :1]
+    for i in range(4):
+        lm.forward_cached(ids1[i], cache1)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(steps):
+        lm.forward_cached(ids1[i % 16], cache1)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    small["us_per_step_eager"] = round(e0.elapsed_time(e1) / steps * 1e3, 1)
+    graph1 = lm.capture_decode(cache1, 1)
+    for i in range(2):
+        graph1.step(ids1[i])
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(steps):
+        graph1.step(ids1[i % 16])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    small["us_per_step_graph"] = round(e0.elapsed_time(e1) / steps * 1e3, 1)
     d, NL = p["d_model"], p["layers"]
     width = ssm.in_proj_width()
     weights = NL * (d * width * 2 + width * 4 + d * d * 2 + d * 4) + d * p["vocab"] * 2
@@ -416,7 +452,9 @@ def bench_decode_lm(torch, args):
                         "per-output-channel fake-quant projections, f32 state cache in place",
             "us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(B / (ms * 1e-3), 1),
             "bytes_per_step": nbytes, "achieved_GBps": round(gbs, 1),
-            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "steps": steps}
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "steps": steps,
+            "launch": "one HIP graph replay per step (Mamba3Lm.capture_decode)",
+            "us_per_step_eager": round(ms_eager * 1e3, 1), "batch1": small}
 
 
 # BASELINE configs 0 and 2 (parity cases; their forward scans are reported beside

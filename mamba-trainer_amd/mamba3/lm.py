@@ -130,3 +130,47 @@ class Mamba3Lm:
             else:
                 _, cache[i] = mixer.apply_with_state(normed, cache[i], residual=x, out=x)
         return self.logits_from(self.norm_f.apply(x))
+
+    def capture_decode(self, cache: List[MixerCache], batch: int) -> "DecodeGraph":
+        """forward_cached for one token per sequence, captured once as a HIP
+        graph over `cache` (whose states each replay updates in place).  No
+        reference counterpart: the reference issues every op from the host."""
+        return DecodeGraph(self, cache, batch)
+
+
+class DecodeGraph:
+    """One decode step of a Mamba3Lm (`forward_cached` over [batch, 1] ids,
+    the cache's states updated in place) as a captured HIP graph: a replay
+    sends the step's ~150 kernels to the GPU as one graph launch, with none of
+    the host work of issuing them one by one.
+
+    Capture records the cache's buffers: replays read and update those same
+    tensors, so the cache must stay alive and keep its storage.  The warm-up
+    before capture runs on copies of the states (it settles the GEMM plans,
+    whose first call times candidates and blocks, which capture forbids), so
+    capturing does not advance the caller's states."""
+
+    def __init__(self, lm: Mamba3Lm, cache: List[MixerCache], batch: int):
+        dev = cache[0].ssm.h.device
+        self.ids = torch.zeros((batch, 1), dtype=torch.int64, device=dev)
+        scratch = [MixerCache(c.ssm.clone()) for c in cache]
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            lm.forward_cached(self.ids, scratch)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = lm.forward_cached(self.ids, cache)
+        self._captured = (lm, cache)
+
+    def step(self, ids: torch.Tensor) -> torch.Tensor:
+        """Replays the step for `ids` [batch, 1]; returns the logits buffer,
+        which the next replay overwrites."""
+        if tuple(ids.shape) != tuple(self.ids.shape):
+            raise ShapeError(f"shape error: the captured step takes ids of shape "
+                             f"{tuple(self.ids.shape)}, got {tuple(ids.shape)}")
+        self.ids.copy_(ids)
+        self.graph.replay()
+        return self.logits

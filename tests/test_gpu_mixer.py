@@ -262,3 +262,39 @@ def test_config4_layer_shapes_against_oracle():
     got = host(lm.forward(torch.from_numpy(ids).to(DEV)))
     ref = mo.lm_forward(ids, model, rnd=True)
     assert rel_l2(got, ref) <= 1e-2, rel_l2(got, ref)
+
+
+def test_decode_graph_replays_match_eager_steps():
+    """Mamba3Lm.capture_decode: a captured decode step replayed six times, with
+    eager steps and host synchronisation between the replays; every replay's
+    logits and states equal the eager step's bit for bit (the same kernels on
+    the same inputs), and capturing leaves the states where they were."""
+    from mamba3.mixer import MixerCache
+    rng = np.random.default_rng(61)
+    model = mo.random_model(rng, vocab=64, d_model=64, n_layers=2, heads=4, head_dim=16,
+                            d_state=16, int8=True, bias_scale=0.3)
+    lm = gpu_lm_from_oracle(model, True)
+    B = 8
+    gen = torch.Generator(device=DEV).manual_seed(62)
+    cache_e = lm.empty_cache(B, DEV)
+    for c in cache_e:
+        c.ssm.h.normal_(0.0, 0.1, generator=gen)
+        c.ssm.last_u.normal_(0.0, 0.1, generator=gen)
+        c.ssm.angle.uniform_(-3.0, 3.0, generator=gen)
+    cache_g = [MixerCache(c.ssm.clone()) for c in cache_e]
+    graph = lm.capture_decode(cache_g, B)
+    torch.cuda.synchronize()
+    for ce, cg in zip(cache_e, cache_g):
+        assert torch.equal(ce.ssm.h, cg.ssm.h) and torch.equal(ce.ssm.angle, cg.ssm.angle)
+    for step in range(6):
+        ids = torch.randint(0, 64, (B, 1), device=DEV, generator=gen)
+        want = lm.forward_cached(ids, cache_e).clone()
+        torch.cuda.synchronize()
+        got = graph.step(ids).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), step
+        for ce, cg in zip(cache_e, cache_g):
+            assert torch.equal(ce.ssm.h, cg.ssm.h), step
+            assert torch.equal(ce.ssm.last_u, cg.ssm.last_u), step
+            assert torch.equal(ce.ssm.angle, cg.ssm.angle), step
+    assert torch.isfinite(got.float()).all()
