@@ -2,9 +2,9 @@
  * mamba3_ssm.h -- C ABI of the MI355X (gfx950) Mamba-3 SSD scan and decode step.
  *
  * This is the boundary a host in any language binds (the reference crate's
- * Rust host would bind it through a thin `extern "C"` -sys crate; see
- * INTEGRATION.md).  It replaces the reference's generic Rust API over a
- * CubeCL runtime (BectorVoom/mamba-trainer):
+ * Rust host would bind it through a thin `extern "C"` -sys crate that
+ * declares these functions and structs 1:1).  It replaces the reference's
+ * generic Rust API over a CubeCL runtime (BectorVoom/mamba-trainer):
  *
  *   m3_ssm_config / m3_config_*   SsmConfig and its enums   src/ssm/config.rs:19-347
  *   m3_ssm_state                  SsmState                  src/ssm/scan.rs:293-358
