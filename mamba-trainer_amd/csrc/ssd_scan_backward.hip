@@ -1057,6 +1057,17 @@ __global__ void __launch_bounds__(256) bwd_token_kernel(ScanLaunch a, BwdArgs g,
     const bool rot = a.theta != nullptr;
     constexpr int TW = (QT + 3) / 4;   // tokens per wave: wave + 4 j
     static_assert(TW <= 64, "tokens per wave");
+    // the per-token scalars of the second part (lane j = token wave + 4 j)
+    // go out first: they depend on nothing below
+    const int tk = wave + 4 * lane;
+    const size_t tkg = static_cast<size_t>(ck) * QT + tk;
+    const bool tk_live = lane < TW && tk < QT && tkg < L;
+    const size_t tkc = tk_live ? tkg : 0;
+    const size_t tkx = (bb * L + tkc) * H + hh;
+    const float dt = a.dt[tkx], lam = a.lambda[tkx];
+    const float da = w.da[bh * L + tkc];
+    const float dgw = w.dg[bh * L + tkc] + w.dw[bh * L + tkc];
+    const float dwv = w.dw[bh * L + (tkc > 0 ? tkc - 1 : 0)];
     // per pair (lane = pair): dtheta and the angle part of ddt, with every
     // load issued first (unconditional at clamped indices)
     float cin[TW], th[TW];
@@ -1093,29 +1104,20 @@ __global__ void __launch_bounds__(256) bwd_token_kernel(ScanLaunch a, BwdArgs g,
         if (lane == j) mine = part;
     }
     // per token (lane j = token wave + 4 j): trapezoid and decay chains
-    const int t = wave + 4 * lane;
-    const size_t tg = static_cast<size_t>(ck) * QT + t;
-    const bool live = lane < TW && t < QT && tg < L;
-    const size_t tc = live ? tg : 0;
-    const size_t ix = (bb * L + tc) * H + hh;
-    const float dt = a.dt[ix], lam = a.lambda[ix];
-    const float da = w.da[bh * L + tc];
-    const float dgw = w.dg[bh * L + tc] + w.dw[bh * L + tc];
-    const float dwv = w.dw[bh * L + (tc > 0 ? tc - 1 : 0)];
-    const float dwp = tc > 0 ? dwv : 0.0f;
+    const float dwp = tkc > 0 ? dwv : 0.0f;
     float ddt = mine + A * da + lam * dgw + (1.0f - lam) * dwp;
     float dlam = dt * dgw - dt * dwp;
-    if (live && tg == 0 && a.h0 != nullptr && a.last_u0 != nullptr) {
+    if (tk_live && tkg == 0 && a.h0 != nullptr && a.last_u0 != nullptr) {
         float dfirst = 0.0f;
         for (int q = 0; q < N / 32; ++q) dfirst += w.pfirst[bh * (N / 32) + q];
         ddt += (1.0f - lam) * dfirst;
         dlam -= dt * dfirst;
     }
-    if (live) {
-        g.ddt[ix] = ddt;
-        g.dlambda[ix] = dlam;
+    if (tk_live) {
+        g.ddt[tkx] = ddt;
+        g.dlambda[tkx] = dlam;
     }
-    float asum = live ? dt * da : 0.0f;
+    float asum = tk_live ? dt * da : 0.0f;
     __shared__ float red[16];
     asum = block_sum(asum, red);
     if (threadIdx.x == 0) w.pa[bhk] = asum;
