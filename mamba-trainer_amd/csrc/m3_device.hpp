@@ -146,23 +146,4 @@ __device__ __forceinline__ void bst2(uint16_t v, rsrc_t r, uint32_t off) {
     __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, 0);
 }
 
-// Device-coherent forms (cache policy sc1, device scope): the access goes to
-// the point of coherence shared by every XCD, so a record one workgroup
-// stores is seen by a workgroup on another XCD once the store has completed
-// (s_waitcnt vmcnt(0)) and a flag published after it has been read.  Plain
-// loads and stores may be served by the XCD's own L2.
-constexpr int kCohPolicy = 16;   // sc1
-__device__ __forceinline__ u32x4 bld16_coh(rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCohPolicy);
-}
-__device__ __forceinline__ float bldf_coh(rsrc_t r, uint32_t off) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCohPolicy));
-}
-__device__ __forceinline__ void bst16_coh(u32x4 v, rsrc_t r, uint32_t off) {
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCohPolicy);
-}
-__device__ __forceinline__ void bstf_coh(float v, rsrc_t r, uint32_t off) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kCohPolicy);
-}
-
 }  // namespace m3

@@ -74,12 +74,6 @@ size_t scan_backward_workspace(const ScanLaunch &a);
 hipError_t launch_scan_backward(const ScanLaunch &a, const ScanGrads &g, void *workspace,
                                 hipStream_t stream);
 
-// The single-launch form with a decoupled look-back (bf16 storage, the shapes
-// above, mamba3_scan mode): workspace bytes (0 when not covered) and launch.
-bool scan_lookback_supported(const ScanLaunch &a);
-size_t scan_lookback_workspace(const ScanLaunch &a);
-hipError_t launch_scan_lookback(const ScanLaunch &a, void *workspace, hipStream_t stream);
-
 // Largest head_dim / d_state the scan kernels are instantiated for.
 constexpr size_t kScanMaxHeadDim = 128;
 constexpr size_t kScanMaxState = 256;

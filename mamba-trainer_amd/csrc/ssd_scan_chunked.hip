@@ -31,8 +31,6 @@
 // and band are latency-bound there.  Here both heavy passes spread over every
 // chunk of every sequence; the sequential pass is a few FMAs per element and
 // streams U_k from HBM.
-#include <cstdlib>
-#include <cstring>
 #include <type_traits>
 
 #include "scan_common.hpp"
@@ -881,29 +879,17 @@ static size_t device_cus() {
     return static_cast<size_t>(cus);
 }
 
-// M3_SCAN_CHUNKED=lookback routes bf16 scans in mamba3_scan mode to the
-// single-launch look-back kernel (ssd_scan_lookback.hip) instead of these
-// three launches.  It is parity-tested but slower at the benchmark shapes
-// (141 vs 110 us at config 1 on MI355X), so it is opt-in.
-static bool use_lookback(const ScanLaunch &a) {
-    const char *e = std::getenv("M3_SCAN_CHUNKED");
-    const bool look = e != nullptr && std::strcmp(e, "lookback") == 0;
-    return look && scan_lookback_supported(a);
-}
-
 size_t scan_chunked_workspace(const ScanLaunch &a) {
     if (!scan_fast_supported(a) || a.seq == 0) return 0;
     const size_t seqs = a.batch * a.heads, cus = device_cus();
     const size_t rounds = (seqs + cus - 1) / cus;
     if (seqs * 10 >= rounds * cus * 7) return 0;
-    if (use_lookback(a)) return scan_lookback_workspace(a);
     return chunked_layout(a.batch * a.heads * chunk_count(a, rows_for(a)), a.d_state, a.bf16 != 0)
         .total;
 }
 
 hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream) {
     if (!scan_fast_supported(a) || a.seq == 0) return hipErrorNotSupported;
-    if (use_lookback(a)) return launch_scan_lookback(a, workspace, stream);
     char *ws = static_cast<char *>(workspace);
     if (a.bf16) return launch_t<bf16_t, 64>(a, ws, stream);
     return launch_t<float, 32>(a, ws, stream);
