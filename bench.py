@@ -100,51 +100,82 @@ def make_scan_inputs(torch, dev, B, L, H, P, N, R, seed):
     return dict(x=x, b=b, c=c, dt=dt, lam=lam, a_log=a_log, theta=theta)
 
 
-def bench_scan(torch, lib, L_, args, chunk_parallel=True, inp=None):
+def bench_scan(torch, lib, L_, args, chunk_parallel=True, inp=None, sets=None):
+    """Config 1's scan through m3_scan.  Step i runs on input/output set
+    i % sets: with several sets (their inputs total well over the 256 MB
+    Infinity Cache) no call finds the previous call's inputs cached, so the
+    figure is HBM-bound as a fresh batch would be; sets=1 re-reads one resident
+    set (the cache-assisted figure, reported beside it)."""
     dev = "cuda:0"
     s = SCAN
     B, L, H, P, N, R, Q = s["B"], s["L"], s["H"], s["P"], s["N"], s["R"], s["Q"]
+    K = args.scan_sets if sets is None else sets
     if inp is None:
-        inp = make_scan_inputs(torch, dev, B, L, H, P, N, R, 0x4D414D43)
-    y = torch.empty_like(inp["x"])
-    h = torch.empty(B, H, P, N, device=dev)
-    lu = torch.empty(B, H, P, N, device=dev)
-    ang = torch.empty(B, H, N // 2, device=dev)
-    cin = L_.ScanInputsC(B, L, H, P, N, R, L_.M3_BF16, inp["x"].data_ptr(), inp["b"].data_ptr(),
-                         inp["c"].data_ptr(), inp["dt"].data_ptr(), inp["a_log"].data_ptr(),
-                         inp["lam"].data_ptr(), inp["theta"].data_ptr(), None, None, Q, 1,
-                         None, 0)
+        inp = [make_scan_inputs(torch, dev, B, L, H, P, N, R, 0x4D414D43 + k) for k in range(K)]
+    calls, keep = [], []
     ws = None
-    if chunk_parallel:
-        need = int(lib.m3_scan_workspace_bytes(C.byref(cin)))
-        ws = torch.empty(need, dtype=torch.uint8, device=dev)
-        cin.workspace, cin.workspace_bytes = ws.data_ptr(), need
-    cout = L_.ScanOutputC(y.data_ptr(), L_.SsmStateC(h.data_ptr(), lu.data_ptr(), ang.data_ptr()))
+    for k in range(K):
+        d = inp[k]
+        y = torch.empty_like(d["x"])
+        h = torch.empty(B, H, P, N, device=dev)
+        lu = torch.empty(B, H, P, N, device=dev)
+        ang = torch.empty(B, H, N // 2, device=dev)
+        cin = L_.ScanInputsC(B, L, H, P, N, R, L_.M3_BF16, d["x"].data_ptr(), d["b"].data_ptr(),
+                             d["c"].data_ptr(), d["dt"].data_ptr(), d["a_log"].data_ptr(),
+                             d["lam"].data_ptr(), d["theta"].data_ptr(), None, None, Q, 1,
+                             None, 0)
+        if chunk_parallel:
+            need = int(lib.m3_scan_workspace_bytes(C.byref(cin)))
+            if ws is None:
+                ws = torch.empty(need, dtype=torch.uint8, device=dev)
+            cin.workspace, cin.workspace_bytes = ws.data_ptr(), need
+        cout = L_.ScanOutputC(y.data_ptr(), L_.SsmStateC(h.data_ptr(), lu.data_ptr(),
+                                                         ang.data_ptr()))
+        keep.append((cin, cout, y, h, lu, ang))
+        calls.append((C.byref(cin), C.byref(cout)))
     stream = torch.cuda.current_stream()
     sp = C.c_void_p(stream.cuda_stream)
     fn = lib.m3_scan
-    pin, pout = C.byref(cin), C.byref(cout)
 
-    def step():
+    def step(i):
+        pin, pout = calls[i % K]
         st = fn(pin, pout, sp)
         if st != 0:
             L_.check(st)
 
-    for _ in range(args.warmup):
-        step()
+    for i in range(args.warmup):
+        step(i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
-    for _ in range(args.steps):
-        step()
+    for i in range(args.steps):
+        step(i)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ev_ms = e0.elapsed_time(e1) / args.steps
-    assert torch.isfinite(y.float()).all(), "non-finite scan output"
+    for kp in keep:
+        assert torch.isfinite(kp[2].float()).all(), "non-finite scan output"
+    in_bytes = sum(t.numel() * t.element_size() for d in inp[:K] for t in d.values())
     return dict(wall_ms=wall * 1e3 / args.steps, kernel_ms=ev_ms, tokens=B * L, inp=inp,
+                sets=K, input_MB=round(in_bytes / 1e6, 1),
                 workspace_bytes=0 if ws is None else ws.numel())
+
+
+def cpu_model():
+    """The host CPU's model name and logical core count (lscpu's fields, read
+    from /proc/cpuinfo)."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": name, "host_logical_cpus": os.cpu_count()}
 
 
 def _pause_for_trace(args):
@@ -363,7 +394,7 @@ def cpu_backward_baseline(args):
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     return {"value": round(s["L"] / med, 1), "unit": "tokens/s", "cores": oracle.num_threads(),
-            "kind": "port",
+            "kind": "port", **cpu_model(),
             "sample": (f"config 1 at batch 1 (L=2048, H=12, P=64, N=128, Rotational, bf16-rounded "
                        f"inputs), f64 reverse mode of the recurrence (oracle/mamba3_oracle.c "
                        f"m3o_scan_backward_f64), 1 warmup + median of {args.cpu_reps}: "
@@ -465,59 +496,72 @@ OTHER_SCANS = {"config0": (2, 512, 4, 64, 64, 1, False, False),
 
 def bench_other_scans(torch, lib, L_, args):
     """Forward scans of configs 0 (f32, Real, SISO) and 2 (bf16, Rotational,
-    MIMO rank 4) through m3_scan with the workspace the library asks for."""
+    MIMO rank 4) through m3_scan with the workspace the library asks for,
+    rotating over --scan-sets input/output sets as the headline does (config 2
+    takes three: one set is 1.26 GB already)."""
     dev = "cuda:0"
     out = {}
     for name, (B, L, H, P, N, R, bf16, rot) in OTHER_SCANS.items():
-        g = torch.Generator(device=dev).manual_seed(0x4D414D43)
+        K = min(args.scan_sets, 3) if name == "config2" else args.scan_sets
         st = torch.bfloat16 if bf16 else torch.float32
-        x = torch.randn(B, L, H, P, R, device=dev, generator=g).to(st)
-        b = (torch.randn(B, L, H, N, R, device=dev, generator=g) / math.sqrt(N)).to(st)
-        c = (torch.randn(B, L, H, N, R, device=dev, generator=g) / math.sqrt(N)).to(st)
-        dt = torch.nn.functional.softplus(torch.randn(B, L, H, device=dev, generator=g) - 3.0
-                                          ).clamp(1e-3, 0.1)
-        lam = torch.sigmoid(torch.randn(B, L, H, device=dev, generator=g))
-        a_log = torch.rand(H, device=dev, generator=g) * math.log(16.0)
-        th = ((torch.rand(1, 1, H, N // 2, device=dev, generator=g) * math.pi)
-              .expand(B, L, H, N // 2).contiguous().to(st)) if rot else None
-        y = torch.empty_like(x)
-        h = torch.empty(B, H, P, N, device=dev)
-        lu = torch.empty_like(h)
-        ang = torch.empty(B, H, N // 2, device=dev) if rot else None
-        cin = L_.ScanInputsC(B, L, H, P, N, R, L_.M3_BF16 if bf16 else L_.M3_F32, x.data_ptr(),
-                             b.data_ptr(), c.data_ptr(), dt.data_ptr(), a_log.data_ptr(),
-                             lam.data_ptr(), th.data_ptr() if rot else None, None, None, 64, 1,
-                             None, 0)
-        need = int(lib.m3_scan_workspace_bytes(C.byref(cin)))
-        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
-        if need:
-            cin.workspace, cin.workspace_bytes = ws.data_ptr(), need
-        cout = L_.ScanOutputC(y.data_ptr(), L_.SsmStateC(h.data_ptr(), lu.data_ptr(),
-                                                         ang.data_ptr() if rot else None))
+        calls, keep = [], []
+        ws = None
+        for k in range(K):
+            g = torch.Generator(device=dev).manual_seed(0x4D414D43 + k)
+            x = torch.randn(B, L, H, P, R, device=dev, generator=g).to(st)
+            b = (torch.randn(B, L, H, N, R, device=dev, generator=g) / math.sqrt(N)).to(st)
+            c = (torch.randn(B, L, H, N, R, device=dev, generator=g) / math.sqrt(N)).to(st)
+            dt = torch.nn.functional.softplus(torch.randn(B, L, H, device=dev, generator=g) - 3.0
+                                              ).clamp(1e-3, 0.1)
+            lam = torch.sigmoid(torch.randn(B, L, H, device=dev, generator=g))
+            a_log = torch.rand(H, device=dev, generator=g) * math.log(16.0)
+            th = ((torch.rand(1, 1, H, N // 2, device=dev, generator=g) * math.pi)
+                  .expand(B, L, H, N // 2).contiguous().to(st)) if rot else None
+            y = torch.empty_like(x)
+            h = torch.empty(B, H, P, N, device=dev)
+            lu = torch.empty_like(h)
+            ang = torch.empty(B, H, N // 2, device=dev) if rot else None
+            cin = L_.ScanInputsC(B, L, H, P, N, R, L_.M3_BF16 if bf16 else L_.M3_F32,
+                                 x.data_ptr(), b.data_ptr(), c.data_ptr(), dt.data_ptr(),
+                                 a_log.data_ptr(), lam.data_ptr(), th.data_ptr() if rot else None,
+                                 None, None, 64, 1, None, 0)
+            need = int(lib.m3_scan_workspace_bytes(C.byref(cin)))
+            if ws is None:
+                ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+            if need:
+                cin.workspace, cin.workspace_bytes = ws.data_ptr(), need
+            cout = L_.ScanOutputC(y.data_ptr(), L_.SsmStateC(h.data_ptr(), lu.data_ptr(),
+                                                             ang.data_ptr() if rot else None))
+            keep.append((cin, cout, x, b, c, dt, lam, a_log, th, y, h, lu, ang))
+            calls.append((C.byref(cin), C.byref(cout)))
         stream = torch.cuda.current_stream()
-        call = lambda: L_.check(lib.m3_scan(C.byref(cin), C.byref(cout),
-                                            C.c_void_p(stream.cuda_stream)))
-        for _ in range(5):
-            call()
+        sp = C.c_void_p(stream.cuda_stream)
+        call = lambda i: L_.check(lib.m3_scan(calls[i % K][0], calls[i % K][1], sp))
+        for i in range(5):
+            call(i)
         torch.cuda.synchronize()
-        steps = max(10, args.steps // 4)
+        steps = max(12, args.steps // 4)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for _ in range(steps):
-            call()
+        for i in range(steps):
+            call(i)
         e1.record(stream)
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) / steps * 1e3
-        assert bool(torch.isfinite(y.float()).all())
+        for kp in keep:
+            assert bool(torch.isfinite(kp[9].float()).all())
         nbytes, flops = scan_algorithmic(B, L, H, P, N, R, 64, s_io=2 if bf16 else 4,
                                          theta_per_token=rot)
         out[name] = {"workload": f"B={B} L={L} H={H} P={P} N={N} R={R} "
                                  f"{'bf16' if bf16 else 'f32'} {'Rotational' if rot else 'Real'}",
                      "us_per_call": round(us, 2), "tokens_per_s": round(B * L / (us * 1e-6), 1),
-                     "path": "chunk-parallel" if need else "single pass",
+                     "path": "chunk-parallel" if need else "single pass", "input_sets": K,
                      "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
                      "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "mfma_tflops": round(flops / (us * 1e-6) / 1e12, 2)}
+                     "mfma_tflops": round(flops / (us * 1e-6) / 1e12, 2),
+                     "frac_bf16_mfma_peak": round(flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+        del keep, calls, ws
+        torch.cuda.empty_cache()
     return out
 
 
@@ -623,7 +667,7 @@ def cpu_baseline(args):
     med = statistics.median(times)
     tokens = B * s["L"]
     return {"value": round(tokens / med, 1), "unit": "tokens/s",
-            "cores": oracle.num_threads(), "kind": "port",
+            "cores": oracle.num_threads(), "kind": "port", **cpu_model(),
             "sample": (f"config 1 at batch {B} (L=2048, H=12, P=64, N=128, Q=64, Rotational, "
                        f"bf16-rounded inputs, f32 math), composed reference algorithm "
                        f"(oracle/mamba3_oracle.c m3o_scan_composed_f32), 1 warmup + median "
@@ -644,9 +688,12 @@ def main():
     ap.add_argument("--decode-lm-steps", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-backward", action="store_true", help="skip the scan backward leg")
+    ap.add_argument("--scan-sets", type=int, default=4,
+                    help="input/output sets the scan legs rotate over (4 x 152 MB at config 1)")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-reps", type=int, default=3)
-    ap.add_argument("--only", choices=("prefill", "decode_lm", "ingest", "backward"), default=None,
+    ap.add_argument("--only", choices=("prefill", "decode_lm", "ingest", "backward", "other_scans",
+                                       "decode"), default=None,
                     help="run one model leg alone and print its object (for kernel traces)")
     ap.add_argument("--scan-only", action="store_true",
                     help="run only the headline scan --steps times (for counter runs)")
@@ -686,6 +733,10 @@ def main():
         print(json.dumps({"backward": bench_backward(torch, lib, L_, args, inp, None)}),
               flush=True)
         return
+    if args.only in ("other_scans", "decode"):
+        fn = bench_other_scans if args.only == "other_scans" else bench_decode
+        print(json.dumps({args.only: fn(torch, lib, L_, args)}), flush=True)
+        return
     if args.only:
         leg = {"prefill": bench_prefill, "decode_lm": bench_decode_lm,
                "ingest": bench_ingest}[args.only](torch, args)
@@ -693,9 +744,11 @@ def main():
         return
     if args.scan_only:
         sc = bench_scan(torch, lib, L_, args, chunk_parallel=True)
-        print(json.dumps({"scan_us": round(sc["kernel_ms"] * 1e3, 2)}), flush=True)
+        print(json.dumps({"scan_us": round(sc["kernel_ms"] * 1e3, 2), "sets": sc["sets"]}),
+              flush=True)
         return
     sc = bench_scan(torch, lib, L_, args, chunk_parallel=True)
+    sc_res = bench_scan(torch, lib, L_, args, chunk_parallel=True, inp=sc["inp"], sets=1)
     sc1 = bench_scan(torch, lib, L_, args, chunk_parallel=False, inp=sc["inp"])
     s = SCAN
     nbytes, flops = scan_algorithmic(s["B"], s["L"], s["H"], s["P"], s["N"], s["R"], s["Q"])
@@ -705,7 +758,7 @@ def main():
     ms_step = sc["wall_ms"]
     value = sc["tokens"] / (ms_step * 1e-3)
 
-    bwd = None if args.no_backward else bench_backward(torch, lib, L_, args, sc["inp"],
+    bwd = None if args.no_backward else bench_backward(torch, lib, L_, args, sc["inp"][0],
                                                        sc["kernel_ms"])
     other = bench_other_scans(torch, lib, L_, args)
     dec = None if args.no_decode else bench_decode(torch, lib, L_, args)
@@ -737,11 +790,14 @@ def main():
                      "kernel": "m3_scan: chunk_state_kernel + state_pass_kernel + "
                                "chunk_scan_kernel (one scan call)",
                      "kernel_us": round(sc["kernel_ms"] * 1e3, 2),
+                     "input_sets": sc["sets"], "input_MB_total": sc["input_MB"],
+                     "kernel_us_resident_inputs": round(sc_res["kernel_ms"] * 1e3, 2),
                      "workspace_MB": round(sc["workspace_bytes"] / 1e6, 1),
                      "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
                      "mfma_tflops": round(tflops, 2),
                      "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)},
         "scan_single_pass_us": round(sc1["kernel_ms"] * 1e3, 2),
+        "scan_rotated_sets": sc["sets"],
         "other_scans": other,
         "backward": bwd,
         "decode": dec,
