@@ -147,6 +147,25 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
  * No reference counterpart (see m3_scan_inputs.workspace). */
 size_t m3_scan_workspace_bytes(const m3_scan_inputs *in);
 
+/* Size of the static device scratch m3_scan_no_alloc uses, in MiB. */
+#define M3_NO_ALLOC_SCRATCH_MIB 32
+
+/* m3_scan without any allocation.  No reference counterpart: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  The chunk-parallel path's workspace
+ * is a file-scope device array of M3_NO_ALLOC_SCRATCH_MIB MiB instead of the
+ * caller's buffer (in->workspace and in->workspace_bytes are ignored).  Each GPU
+ * holds its own copy of that array from the first call on that device until the
+ * process ends.  Shapes whose workspace (m3_scan_workspace_bytes) exceeds it
+ * return M3_ERR_UNSUPPORTED before any device work.  Results are those of
+ * m3_scan with a caller workspace, bit for bit.  Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams, or
+ * different host threads without ordering) race and give wrong results.  The
+ * scratch needs no clearing: the chunk-parallel kernels write every byte they
+ * later read within one call.  It calls no hipMalloc, hipFree or allocating
+ * library routine. */
+m3_status m3_scan_no_alloc(const m3_scan_inputs *in, const m3_scan_output *out, void *stream);
+
 /* Gradients of mamba3_scan for the loss L, given dL/dy.  The reference gets
  * them by reverse-mode autodiff through the composed scan (Var::backward over
  * scan.rs:458-638; its own adjoint kernels are ssd_band_backward fused.rs:

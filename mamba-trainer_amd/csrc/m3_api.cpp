@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "m3_internal.hpp"
@@ -60,6 +61,23 @@ size_t scan_rows(int dtype, size_t d_state) {
 }
 
 bool dtype_ok(int32_t d) { return d == M3_F32 || d == M3_BF16; }
+
+// Zero `n` floats on `s` with a kernel rather than hipMemsetAsync, so that a
+// caller who captures the call into a HIP graph records a kernel node only.
+__global__ void zero_fill_kernel(float *p, size_t n) {
+    for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n;
+         i += size_t(gridDim.x) * blockDim.x)
+        p[i] = 0.0f;
+}
+
+hipError_t zero_async(float *p, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)),
+                       dim3(256), 0, s, p, n);
+    g_launches.fetch_add(1, std::memory_order_relaxed);
+    return hipGetLastError();
+}
 
 }  // namespace
 
@@ -194,8 +212,8 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
                     e = hipMemcpyAsync(out->state.last_u, st->last_u, sbytes,
                                        hipMemcpyDeviceToDevice, s);
             } else {
-                e = hipMemsetAsync(out->state.h, 0, sbytes, s);
-                if (e == hipSuccess) e = hipMemsetAsync(out->state.last_u, 0, sbytes, s);
+                e = zero_async(out->state.h, sbytes / sizeof(float), s);
+                if (e == hipSuccess) e = zero_async(out->state.last_u, sbytes / sizeof(float), s);
             }
             // An empty theta tensor may arrive as a NULL pointer, so the angle
             // passes through whenever the caller gave an output angle buffer.
@@ -205,7 +223,7 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
                     e = hipMemcpyAsync(out->state.angle, st->angle, abytes,
                                        hipMemcpyDeviceToDevice, s);
                 else
-                    e = hipMemsetAsync(out->state.angle, 0, abytes, s);
+                    e = zero_async(out->state.angle, abytes / sizeof(float), s);
             }
             if (e != hipSuccess) return hip_fail(e, "state pass-through");
         }
@@ -271,6 +289,72 @@ size_t m3_scan_workspace_bytes(const m3_scan_inputs *in) {
     a.x = a.b = a.c = dummy;
     a.y = dummy;
     return m3::scan_chunked_workspace(a);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The chunk-parallel scan's workspace for m3_scan_no_alloc: one file-scope
+// device array, so each GPU the library runs on holds its own copy until the
+// process ends.  In host code `scratch` names a host-side stand-in, never the
+// device memory: kernels get the address hipGetSymbolAddress returns for the
+// current device, looked up once per device and kept in g_scratch.
+constexpr size_t kNoAllocScratchBytes = size_t(M3_NO_ALLOC_SCRATCH_MIB) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (nullptr and a message on failure).
+void *scratch_for_current_device() {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipGetDevice");
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        fail(M3_ERR_UNSUPPORTED, "device %d is beyond the %d devices the static scratch covers", dev,
+             kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+            return nullptr;
+        }
+        g_scratch[dev] = p;
+    }
+    return g_scratch[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+m3_status m3_scan_no_alloc(const m3_scan_inputs *in, const m3_scan_output *out, void *stream) {
+    if (in == nullptr || out == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/outputs are NULL");
+    m3_scan_inputs local = *in;
+    local.workspace = nullptr;
+    local.workspace_bytes = 0;
+    const size_t need = m3_scan_workspace_bytes(&local);
+    if (need > kNoAllocScratchBytes)
+        return fail(M3_ERR_UNSUPPORTED,
+                    "this scan needs %zu bytes of scratch; m3_scan_no_alloc's static scratch holds "
+                    "%zu (%d MiB): call m3_scan with a caller workspace instead",
+                    need, kNoAllocScratchBytes, M3_NO_ALLOC_SCRATCH_MIB);
+    if (need > 0) {
+        void *p = scratch_for_current_device();
+        if (p == nullptr) return M3_ERR_HIP;
+        local.workspace = p;
+        local.workspace_bytes = kNoAllocScratchBytes;
+    }
+    return m3_scan(&local, out, stream);
 }
 
 static m3::ScanLaunch scan_launch_of(const m3_scan_inputs *in) {

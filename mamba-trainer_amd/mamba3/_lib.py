@@ -98,6 +98,7 @@ SIGNATURES = {
     "m3_discretization_fixed_lambda": (C.c_float, [C.c_int32]),
     "m3_scan": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanOutputC), _P]),
     "m3_scan_workspace_bytes": (_Z, [C.POINTER(ScanInputsC)]),
+    "m3_scan_no_alloc": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanOutputC), _P]),
     "m3_scan_backward": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanGradsC), _P]),
     "m3_scan_backward_workspace_bytes": (_Z, [C.POINTER(ScanInputsC)]),
     "m3_ssd_chunked": (C.c_int, [C.POINTER(SsdArgsC), _P, _P, _P]),

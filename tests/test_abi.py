@@ -227,3 +227,22 @@ def test_scan_backward_workspace_query():
     assert need(1, 100, 2, 48, 128, 1, _lib.M3_BF16) == 0      # head_dim 48
     assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) == 0       # d_state 96
     assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) == 0      # rank 3
+
+
+def test_no_alloc_scan_rejects_beyond_its_scratch():
+    """m3_scan_no_alloc: a shape whose chunk-parallel workspace exceeds the
+    static scratch fails with M3_ERR_UNSUPPORTED before any device work (the
+    pointers below are stand-ins that are never dereferenced)."""
+    from mamba3 import _lib
+    L = _lib.lib()
+    fake = 1 << 20
+    cin = _lib.ScanInputsC(1, 65536, 12, 64, 128, 1, _lib.M3_BF16, fake, fake, fake, fake, fake,
+                           fake, fake, None, None, 64, 0, None, 0)
+    need = int(L.m3_scan_workspace_bytes(C.byref(cin)))
+    assert need > 32 << 20
+    cout = _lib.ScanOutputC(fake, _lib.SsmStateC())
+    st = L.m3_scan_no_alloc(C.byref(cin), C.byref(cout), None)
+    assert st == _lib.M3_ERR_UNSUPPORTED
+    msg = L.m3_last_error().decode()
+    assert "static scratch holds 33554432 (32 MiB)" in msg and str(need) in msg
+    assert L.m3_scan_no_alloc(None, C.byref(cout), None) == _lib.M3_ERR_ARGUMENT
