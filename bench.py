@@ -49,10 +49,13 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA, TFLOP/s
 
 # HBM-side bytes of one headline scan call (chunk_state + state_pass +
-# chunk_scan), from rocprofv3 FETCH_SIZE / WRITE_SIZE per dispatch scaled by a
-# 256 MiB copy (FETCH x 2 KiB, WRITE x 1 KiB): 361.5 MB read + 134.6 MB written.
-# Counters cannot be read inside this process; re-measured when the kernels change.
-SCAN_TRAFFIC_BYTES = 496_145_013
+# chunk_scan) and the MFMA-busy fraction of its two MFMA kernels, from
+# profiles/scan_config1_kernels.txt (rocprofv3 FETCH_SIZE / WRITE_SIZE per
+# dispatch scaled by a 256 MiB copy, SQ_VALU_MFMA_BUSY_CYCLES over
+# GRBM_GUI_ACTIVE): 310.2 MB read + 83.0 MB written.  Counters cannot be read
+# inside this process; re-measured when the kernels change.
+SCAN_TRAFFIC_BYTES = 393_200_000
+SCAN_MFMA_BUSY = {"chunk_scan_kernel": 0.048, "chunk_state_kernel": 0.028}
 
 # BASELINE config 1 (the headline) and config 3 (decode)
 SCAN = dict(B=8, L=2048, H=12, P=64, N=128, R=1, Q=64)
@@ -794,6 +797,7 @@ def main():
                      "kernel_us_resident_inputs": round(sc_res["kernel_ms"] * 1e3, 2),
                      "workspace_MB": round(sc["workspace_bytes"] / 1e6, 1),
                      "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
+                     "mfma_busy": SCAN_MFMA_BUSY,
                      "mfma_tflops": round(tflops, 2),
                      "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)},
         "scan_single_pass_us": round(sc1["kernel_ms"] * 1e3, 2),

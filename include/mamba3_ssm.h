@@ -119,7 +119,9 @@ typedef struct m3_scan_inputs {
     const void *theta;        /* [B, T, H, N/2] or NULL (real dynamics) */
     const float *d_skip;      /* [H] or NULL */
     const m3_ssm_state *state;/* carried-in state or NULL */
-    size_t chunk_size;        /* > 0; the kernel tiles time itself (a hint) */
+    size_t chunk_size;        /* > 0; the chunk-parallel kernels pass the state
+                               * between segments of at least this many tokens
+                               * (tiles inside a segment are the kernel's own) */
     int32_t want_state;       /* ScanInputs::want_state */
     /* Device scratch for the chunk-parallel scan (no reference counterpart:
      * the reference allocates its intermediates per call): 256-byte aligned,

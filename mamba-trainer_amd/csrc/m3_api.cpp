@@ -242,6 +242,7 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
     a.rank = in->rank;
     a.bf16 = in->dtype == M3_BF16;
     a.mode_raw = 1;
+    a.chunk_size = in->chunk_size;
     a.x = in->x;
     a.b = in->b;
     a.c = in->c;
@@ -284,6 +285,7 @@ size_t m3_scan_workspace_bytes(const m3_scan_inputs *in) {
     a.rank = in->rank;
     a.bf16 = in->dtype == M3_BF16;
     a.mode_raw = 1;   // m3_scan's prologue, as the launch sets it
+    a.chunk_size = in->chunk_size;
     // alignment is checked at launch; size the shape as if aligned
     alignas(16) static float dummy[4] = {0, 0, 0, 0};
     a.x = a.b = a.c = dummy;

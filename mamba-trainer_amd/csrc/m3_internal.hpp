@@ -38,6 +38,9 @@ struct ScanLaunch {
     const float *init_state;        // ssd_chunked's initial_state or null
     void *y;                        // [B,T,H,P,R]
     float *h_out, *last_u_out, *angle_out;  // null when not wanted
+    // the caller's chunk_size (tokens; 0 = 64): the chunk-parallel path passes
+    // the state between segments of at least this many tokens
+    size_t chunk_size;
 };
 hipError_t launch_scan(const ScanLaunch &a, hipStream_t stream);
 // The specialised kernel (head_dim 64, d_state 64/128, rank 1/2/4, 16-byte

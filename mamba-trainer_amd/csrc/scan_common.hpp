@@ -102,6 +102,18 @@ __device__ __forceinline__ float dexp(float d) {
     return expf(d);
 }
 
+// Transposed LDS read (ds_read_b64_tr_b16, gfx950).  Within each group of 16
+// lanes, lane l supplies the address of four consecutive 16-bit values W[l];
+// lane j receives {W[j/4][j%4], W[4 + j/4][j%4], W[8 + j/4][j%4],
+// W[12 + j/4][j%4]}: column j of the 4 x 16 block whose row r is
+// W[4r] .. W[4r + 3].  So with lane 4r + q pointing at row r, columns
+// 4q .. 4q + 3 of a row-major [k][col] array, lane j gets k = 0..3 of column j:
+// an MFMA operand whose k runs down the rows.
+__device__ __forceinline__ bf16x4 lds_read_tr16(const __bf16 *p) {
+    typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(p));
+}
+
 // Store four consecutive operand values.
 __device__ __forceinline__ void st4(__bf16 *dst, const float *v) {
     typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));

@@ -2,35 +2,41 @@
 // workspace.  Same shapes as ssd_scan_fast.hip (head_dim 64, d_state 64/128,
 // rank 1/2/4, aligned operands) and the same algorithm, src/ssm/scan.rs:116-291
 // (ssd_chunked) and 458-638 (mamba3_scan), regrouped so that only an
-// elementwise recurrence runs in sequence:
+// elementwise recurrence runs in sequence.  A sequence is cut into segments of
+// kseg sub-chunks (64 rows of (token, rank) for bf16, 32 for f32):
 //
-//   chunk_state_kernel  one workgroup per (batch, head, chunk).  In the chunk's
-//       own rotating frame (angles relative to the chunk start, so nothing from
-//       earlier chunks is needed) it forms U_k = sum_s (B_s w_s decay_s)^T x_s,
-//       the chunk's contribution to the state (scan.rs:207-251), together with
-//       the chunk decay exp(sum dt A) and, per rotation pair, the chunk's angle
-//       total Phi_k with its cosine and sine.
+//   chunk_state_kernel  one workgroup per (batch, head, segment).  In the
+//       segment's own rotating frame (angles relative to the segment start, so
+//       nothing from earlier segments is needed) it forms
+//       U = sum_s (B_s w_s decay_s)^T x_s, the segment's contribution to the
+//       state (scan.rs:207-251), sub-chunk by sub-chunk, with the segment's
+//       decay exp(sum dt A) and, per rotation pair, its angle total Phi with
+//       its cosine and sine.
 //   state_pass_kernel   one thread per (batch, head, p, four state pairs):
-//       S_0 = R(angle0) h0 and S_{k+1} = R(Phi_k) (decay_k S_k + U_k), the state
-//       entering each chunk expressed in that chunk's frame, written as MFMA
-//       operand fragments; at the end the boundary state in the global frame
-//       (scan.rs:270-288, 599-638).
-//   chunk_scan_kernel   one workgroup per (batch, head, chunk):
-//       y = (C~ B~^T o L) X + exp(acum) C~ S_k  (ssd_band fused.rs:2044-2070,
-//       scan.rs:253-263), the skip D on the band's diagonal (scan.rs:593-597).
+//       S_0 = R(angle0) h0 and S_{j+1} = R(Phi_j) (decay_j S_j + U_j), the
+//       state entering each segment expressed in that segment's frame, written
+//       as MFMA operand fragments; at the end the boundary state in the global
+//       frame (scan.rs:270-288, 599-638).
+//   chunk_scan_kernel   one workgroup per (batch, head, segment), its
+//       sub-chunks in turn from the segment's S:
+//       y = (C~ B~^T o L) X + exp(acum) C~ S  (ssd_band fused.rs:2044-2070,
+//       scan.rs:253-263), the skip D on the band's diagonal (scan.rs:593-597),
+//       then S advanced in registers to the next sub-chunk.
 //
-// Frames.  With phi_t the running angle and phi^s_k its value entering chunk k,
-// B~_t = R(-phi_t) B_t = R(-phi^s_k) B^(k)_t where B^(k)_t is B_t rotated by the
-// in-chunk angle only.  The state in chunk k's frame is S = R(phi^s_k) h, so
-// C~_t . h = C^(k)_t . S, and moving to the next frame is a rotation of every
-// (n, n + N/2) pair by the chunk total Phi_k.
+// Frames.  With phi_t the running angle and phi^s its value entering a
+// segment, B~_t = R(-phi_t) B_t = R(-phi^s) B^(s)_t where B^(s)_t is B_t rotated
+// by its angle relative to the segment start.  The state in the segment's
+// frame is S = R(phi^s) h, so C~_t . h = C^(s)_t . S; within the segment the
+// state advances without rotation, and moving to the next segment's frame is a
+// rotation of every (n, n + N/2) pair by the segment total Phi.
 //
 // Why three launches: a batch x head count of ~100 sequences fills under half
 // of the chip's 256 CUs when each sequence is walked by one workgroup, and
-// every chunk's rotation (a sine and cosine per token and pair), decay weights
-// and band are latency-bound there.  Here both heavy passes spread over every
-// chunk of every sequence; the sequential pass is a few FMAs per element and
-// streams U_k from HBM.
+// every sub-chunk's rotation (a sine and cosine per token and pair), decay
+// weights and band are latency-bound there.  Here both heavy passes spread
+// over every segment of every sequence; the sequential pass is a few FMAs per
+// element and streams U from HBM.  Segments of several sub-chunks keep the U
+// and S records (and the state pass) small while still filling the chip.
 #include <type_traits>
 
 #include "scan_common.hpp"
@@ -72,12 +78,12 @@ ChunkedLayout chunked_layout(size_t bhk, size_t n, bool bf16) {
 }
 
 struct ChunkWs {
-    void *u;        // [bhk][p-tile][n-tile][lane][4]: U^T tiles in MFMA D layout
-    void *s;        // as u: S^T tiles of the state entering each chunk
-    float *eda;     // [bhk] exp(clamp(sum of dt A over the chunk))
-    float *phi;     // [bhk][N/2] angle total of the chunk per pair
-    float *cph;     // [bhk][N/2] cos Phi
-    float *sph;     // [bhk][N/2] sin Phi
+    void *u;        // [bhs][p-tile][n-tile][lane][4]: U^T tiles in MFMA D layout
+    void *s;        // as u: S^T tiles of the state entering each segment
+    float *eda;     // [bhs] exp(sum of the clamped dt A of each sub-chunk)
+    float *phi;     // [bhs][N/2] angle total of the segment per pair (wrapped)
+    float *cph;     // [bhs][N/2] cos Phi
+    float *sph;     // [bhs][N/2] sin Phi
 };
 
 ChunkWs chunk_ws(char *base, const ChunkedLayout &l) {
@@ -120,21 +126,28 @@ struct StateSmem {
     using op_t = typename Op<T>::t;
     static constexpr int PAD = 16 / static_cast<int>(sizeof(op_t));
     static constexpr int LDR = ROWS + PAD;
-    op_t Bwt[N * LDR];      // (B^(k) * w * decay-to-end)^T [n][rho]
+    op_t Bwt[N * LDR];      // (B~ * w * decay-to-end)^T [n][rho], segment frame
     op_t Xt[kP * LDR];      // X^T [p][rho]
-    float phi_tot[N / 2];   // the sub-chunk's angle total per pair
-    float phi_acc[N / 2];   // the chunk's so far
+    // wrapped angle per pair entering the sub-chunk, relative to the segment
+    // start; each pair is read and rewritten by the one wave whose lanes own
+    // it, so one copy serves every sub-chunk (a wave's LDS accesses execute
+    // in order)
+    float psi[N / 2];
 };
 
-// A chunk here is HALF sub-chunks of ROWS rows (the MIMO ranks take HALF = R,
-// so that a chunk spans ROWS tokens whatever the rank), staged one after the
-// other.  With U_h, e_h, Phi_h those of sub-chunk h in its own frame, the
-// chunk's are accumulated as U = e_h U + R(-Phi) U_h, e = e e_h,
-// Phi = Phi + Phi_h: the state recurrence S' = R(Phi)(e S + U) composed over
-// the sub-chunks (the per-pair rotations commute).
-template <typename T, int N, int R, int ROWS, int HALF>
+// One workgroup per (batch, head, segment).  A segment is `kseg` sub-chunks
+// of ROWS rows (ROWS / R tokens each), staged one after the other.  B is
+// rotated by its angle relative to the segment start (a running wrapped
+// angle per pair, as the single pass carries it), so every sub-chunk's
+// contribution U_h is already in the segment's frame and the segment's U is
+// U = e_h U + U_h over the sub-chunks: the state recurrence of
+// scan.rs:207-251 composed over the segment.  The segment's decay and angle
+// total (with its cosine and sine) go to the workspace beside U.  PF: the
+// next sub-chunk's inputs are loaded into registers behind the current one's
+// work.
+template <typename T, int N, int R, int ROWS, bool PF>
 __global__ void __launch_bounds__(kThreads, 2)
-chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nck) {
+chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     constexpr int P = kP;
     using G = Geo<T, N, P, R, ROWS, 4>;
     using S = StateSmem<T, N, R, ROWS>;
@@ -155,9 +168,9 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     const int c = lane & 15;
 
     const size_t H = a.heads, L = a.seq;
-    const size_t bhk = blockIdx.x;
-    const int ck = static_cast<int>(bhk % nck);
-    const size_t bh = bhk / nck;
+    const size_t bhs = blockIdx.x;
+    const int seg = static_cast<int>(bhs % nseg);
+    const size_t bh = bhs / nseg;
     const size_t bb = bh / H, hh = bh % H;
     const bool rot = a.theta != nullptr;
 
@@ -171,14 +184,38 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     float A = 0.0f;
     if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);   // a_log.exp().neg() (scan.rs:470-474)
 
-    // U^T[n][p] of this wave's p-tile, accumulated over the sub-chunks
+    // U^T[n][p] of this wave's p-tile, the segment's decay, and the wrapped
+    // angle of my pairs relative to the segment start
     f32x4 uacc[NTN];
+#pragma unroll
+    for (int i = 0; i < NTN; ++i) uacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float eacc = 1.0f;
+    if (tid < NH) sm.psi[tid] = 0.0f;
+    __syncthreads();
+
+    const int h_end = min(kseg, nsub - seg * kseg);
+    RawT cur, nxt;
+    if constexpr (PF) load_chunk<T, N, P, R, ROWS, 4, false>(rs, seg * kseg, wave, lane, nxt);
 #pragma unroll 1
-    for (int h = 0; h < HALF; ++h) {
-        const int sck = ck * HALF + h;
-        RawT cur;
-        load_chunk<T, N, P, R, ROWS, 4, false>(rs, sck, wave, lane, cur);
+    for (int h = 0; h < h_end; ++h) {
+        // lane-derived indices from an opaque copy of the lane number, so the
+        // LDS addresses they feed are formed in the loop, not held across it
+        int lane_v = lane;
+        asm volatile("" : "+v"(lane_v));
+        const int lane = lane_v;
+        const int g = lane >> 4;
+        const int c = lane & 15;
+        const int sub = lane / G::SW;
+        const int my_t = lane % G::SW;
+        const bool tok_lane = my_t < QT;
+        const int i0 = wave * G::PW + sub * PPL;
+        const int sck = seg * kseg + h;
+        if constexpr (PF) {
+            cur = nxt;
+            if (h + 1 < h_end) load_chunk<T, N, P, R, ROWS, 4, false>(rs, sck + 1, wave, lane, nxt);
+        } else {
+            load_chunk<T, N, P, R, ROWS, 4, false>(rs, sck, wave, lane, cur);
+        }
 
         const size_t tau = static_cast<size_t>(sck) * QT + my_t;
         const bool live = tok_lane && tau < L;
@@ -189,30 +226,6 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nck) {
         const float wd = dexp<kBf16>(last - acum) * wv;   // exp_decay(last, acum, w)
         const float eh = dexp<kBf16>(last);
 
-        // in-chunk angle (inclusive cumsum of dt * theta), rotation by its negative
-        float cs[PPL], sn[PPL];
-#pragma unroll
-        for (int j = 0; j < PPL; ++j) {
-            cs[j] = 1.0f;
-            sn[j] = 0.0f;
-        }
-        if (rot) {
-            const float dtt = live ? cur.s0 : 0.0f;
-#pragma unroll
-            for (int j = 0; j < PPL; ++j) {
-                const float pre = seg_scan<G::SW>(dtt * welem<T>(cur.th, j));
-                if (my_t == QT - 1) sm.phi_tot[i0 + j] = pre;
-                const float psi = wrap_angle(pre);
-                if constexpr (kBf16) {
-                    // the hardware sine takes revolutions; |psi| <= pi
-                    const float rev = psi * 0.15915494309189533577f;
-                    sn[j] = __builtin_amdgcn_sinf(rev);
-                    cs[j] = __builtin_amdgcn_cosf(rev);
-                } else {
-                    sincosf(psi, &sn[j], &cs[j]);
-                }
-            }
-        }
         if (tok_lane) {
 #pragma unroll
             for (int e = 0; e < G::XE; ++e) {
@@ -220,87 +233,70 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nck) {
                 const int p = o / R, r = o % R;
                 sm.Xt[p * LDR + my_t * R + r] = to_op<op_t>(elem<T>(cur.x, e));
             }
+        }
+        // per pair: the angle within the segment (the running angle plus the
+        // in-sub-chunk inclusive cumsum of dt * theta), its sine and cosine,
+        // and B rotated by its negative (fused.rs:610-617), weighted and
+        // stored -- one pair's values live at a time
+        const float dtt = live ? cur.s0 : 0.0f;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int rho = my_t * R + r;
+        for (int j = 0; j < PPL; ++j) {
+            float cs = 1.0f, sn = 0.0f;
+            if (rot) {
+                const float pre = seg_scan<G::SW>(dtt * welem<T>(cur.th, j));
+                const float phi = wrap_angle(sm.psi[i0 + j] + pre);
+                // the sub-chunk's last token carries the angle to the next one
+                if (my_t == QT - 1) sm.psi[i0 + j] = phi;
+                if constexpr (kBf16) {
+                    // the hardware sine takes revolutions; |phi| <= pi
+                    const float rev = phi * 0.15915494309189533577f;
+                    sn = __builtin_amdgcn_sinf(rev);
+                    cs = __builtin_amdgcn_cosf(rev);
+                } else {
+                    sincosf(phi, &sn, &cs);
+                }
+            }
+            if (tok_lane) {
 #pragma unroll
-                for (int j = 0; j < PPL; ++j) {
+                for (int r = 0; r < R; ++r) {
+                    const int rho = my_t * R + r;
                     const float b1 = elem<T>(cur.b[0], j * R + r);
                     const float b2 = elem<T>(cur.b[1], j * R + r);
-                    const float w1 = (b1 * cs[j] + b2 * sn[j]) * wd;    // fused.rs:610-617
-                    const float w2 = (-b1 * sn[j] + b2 * cs[j]) * wd;
-                    sm.Bwt[(i0 + j) * LDR + rho] = to_op<op_t>(w1);
-                    sm.Bwt[(i0 + NH + j) * LDR + rho] = to_op<op_t>(w2);
+                    sm.Bwt[(i0 + j) * LDR + rho] = to_op<op_t>((b1 * cs + b2 * sn) * wd);
+                    sm.Bwt[(i0 + NH + j) * LDR + rho] = to_op<op_t>((-b1 * sn + b2 * cs) * wd);
                 }
             }
         }
         __syncthreads();
 
-        if constexpr (HALF == 1) {
-            // the chunk's angle total per pair, with its cosine and sine
-            if (tid < NH) {
-                const float tot = rot ? sm.phi_tot[tid] : 0.0f;
-                float ts = 0.0f, tc = 1.0f;
-                if (rot) sincosf(tot, &ts, &tc);
-                ws.phi[bhk * NH + tid] = tot;
-                ws.cph[bhk * NH + tid] = tc;
-                ws.sph[bhk * NH + tid] = ts;
-            }
-            if (tid == 0) ws.eda[bhk] = eh;
-        }
-        // U_h^T[n][p] = sum_rho Bwt[n][rho] X^T[p][rho]; wave w takes p-tile w
+        // U = e_h U + U_h, U_h^T[n][p] = sum_rho Bwt[n][rho] X^T[p][rho]; wave w
+        // takes p-tile w
         const op_t *xr = &sm.Xt[(16 * wave + c) * LDR];
-        const size_t uo = (bhk * 4 + wave) * NTN * 256 + lane * 4;
-        f32x4 uh[NTN];
 #pragma unroll
         for (int i = 0; i < NTN; ++i) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            f32x4 acc = uacc[i] * eh;
             const op_t *ar = &sm.Bwt[(16 * i + c) * LDR];
 #pragma unroll
             for (int kb = 0; kb < ROWS / KB; ++kb) acc = mma_kb(ar + kb * KB, xr + kb * KB, acc, g);
-            if constexpr (HALF == 1) store_u<kBf16>(ws.u, uo + i * 256, acc);
-            uh[i] = acc;
+            uacc[i] = acc;
         }
-        if constexpr (HALF > 1) {
-            if (h == 0) {
-#pragma unroll
-                for (int i = 0; i < NTN; ++i) uacc[i] = uh[i];
-            } else {
-                // U = e_h U + R(-Phi) U_h over the pairs (n, n + N/2): tiles i, i + NTN/2
-#pragma unroll
-                for (int i = 0; i < NTN / 2; ++i) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        float ps = 0.0f, pc = 1.0f;
-                        if (rot) sincosf(sm.phi_acc[16 * i + 4 * g + r], &ps, &pc);
-                        const float lo = uh[i][r], hi = uh[i + NTN / 2][r];
-                        uacc[i][r] = eh * uacc[i][r] + lo * pc + hi * ps;
-                        uacc[i + NTN / 2][r] = eh * uacc[i + NTN / 2][r] - lo * ps + hi * pc;
-                    }
-                }
-            }
-            eacc *= eh;
-            __syncthreads();   // every read of this sub-chunk's LDS is done
-            if (tid < NH)
-                sm.phi_acc[tid] = (h == 0 ? 0.0f : sm.phi_acc[tid]) + (rot ? sm.phi_tot[tid] : 0.0f);
-            __syncthreads();
-        }
+        eacc *= eh;
+        __syncthreads();   // every read of this sub-chunk's LDS is done
     }
 
-    if constexpr (HALF > 1) {
-        const size_t uo = (bhk * 4 + wave) * NTN * 256 + lane * 4;
+    const size_t uo = (bhs * 4 + wave) * NTN * 256 + lane * 4;
 #pragma unroll
-        for (int i = 0; i < NTN; ++i) store_u<kBf16>(ws.u, uo + i * 256, uacc[i]);
-        if (tid == 0) ws.eda[bhk] = eacc;
-        // the chunk's angle total per pair, with its cosine and sine
-        if (tid < NH) {
-            const float tot = sm.phi_acc[tid];
-            float ts = 0.0f, tc = 1.0f;
-            if (rot) sincosf(tot, &ts, &tc);
-            ws.phi[bhk * NH + tid] = tot;
-            ws.cph[bhk * NH + tid] = tc;
-            ws.sph[bhk * NH + tid] = ts;
-        }
+    for (int i = 0; i < NTN; ++i) store_u<kBf16>(ws.u, uo + i * 256, uacc[i]);
+    if (tid == 0) ws.eda[bhs] = eacc;
+    // the segment's angle total per pair (wrapped), with its cosine and sine:
+    // one thread per pair (the loop's last barrier ordered the angle writes)
+    if (tid < NH) {
+        const float tot = rot ? sm.psi[tid] : 0.0f;
+        float ts = 0.0f, tc = 1.0f;
+        if (rot) sincosf(tot, &ts, &tc);
+        ws.phi[bhs * NH + tid] = tot;
+        ws.cph[bhs * NH + tid] = tc;
+        ws.sph[bhs * NH + tid] = ts;
     }
 }
 
@@ -325,7 +321,7 @@ __device__ __forceinline__ void rotate_pairs(f32x4 &lo, f32x4 &hi, const f32x4 c
 
 template <typename T, int N>
 __global__ void __launch_bounds__(kThreads)
-state_pass_kernel(ScanLaunch a, ChunkWs ws, int nck) {
+state_pass_kernel(ScanLaunch a, ChunkWs ws, int nck) {   // nck: segments per sequence
     constexpr int P = kP;
     constexpr int NTN = N / 16;
     constexpr int HT = NTN / 2;   // n-tiles per half
@@ -450,32 +446,41 @@ state_pass_kernel(ScanLaunch a, ChunkWs ws, int nck) {
 }
 
 // ================================================================ chunk scan
-template <typename T, int N, int R, int ROWS, int HALF>
+template <typename T, int N, int R, int ROWS>
 struct ScanSmem {
     using G = Geo<T, N, kP, R, ROWS, 4>;
     using op_t = typename Op<T>::t;
     static constexpr int PAD = 16 / static_cast<int>(sizeof(op_t));
     static constexpr int LDN = N + PAD;
     static constexpr int LDR = ROWS + PAD;
-    op_t Bs[ROWS * LDN];    // B^(k)[rho][npos(n)]
-    op_t Cs[ROWS * LDN];    // C^(k)[rho][npos(n)]
+    op_t Bs[ROWS * LDN];    // B~[rho][npos(n)], segment frame
+    op_t Cs[ROWS * LDN];    // C~[rho][npos(n)], segment frame
     op_t Xt[kP * LDR];      // X^T [p][rho]
     op_t Ms[ROWS * LDR];    // masked band (C B^T o L)[rho_t][rho_s]
-    float acum[G::QT], gw[G::QT], ww[G::QT], eac[G::QT];
-    // with sub-chunks: the sub-chunk's angle total per pair, w x decay to its end per token
-    float phi_tot[HALF > 1 ? N / 2 : 1];
-    float wdv[HALF > 1 ? G::QT : 1];
+    float acum[G::QT], gw[G::QT], ww[G::QT];
+    float wdv[G::QT];       // w x decay to the sub-chunk's end, per token
+    // wrapped angle per pair entering the sub-chunk, relative to the segment
+    // start.  Each pair is read and rewritten by the one wave whose lanes own
+    // it (the write depends on the read, and a wave's LDS accesses execute in
+    // order), so one copy serves every sub-chunk.
+    float psi[N / 2];
 };
 
-// HALF sub-chunks of ROWS rows per chunk, one after the other: between them
-// the state advances in registers, S' = R(Phi_h)(e_h S + U_h), with U_h formed
-// from the sub-chunk's staged B~ and X^T.
-template <typename T, int N, int R, int ROWS, int HALF>
-__global__ void __launch_bounds__(kThreads, HALF > 1 ? 2 : 3)
-chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
+// One workgroup per (batch, head, segment): the segment's kseg sub-chunks of
+// ROWS rows one after the other, starting from the state S the state pass
+// left for the segment (in its frame).  Per sub-chunk:
+//   y = (C~ B~^T o L) X + exp(acum) C~ S    (ssd_band fused.rs:2044-2070,
+//       scan.rs:253-263; the skip D on the band's diagonal, scan.rs:593-597)
+//   S <- e_h S + (B~ w decay-to-end)^T X    (scan.rs:207-251)
+// with B~ and C~ rotated by their angle relative to the segment start, so the
+// state needs no rotation between sub-chunks.  PF: the next sub-chunk's
+// inputs are loaded into registers behind the current one's work.
+template <typename T, int N, int R, int ROWS, bool PF>
+__global__ void __launch_bounds__(kThreads, (R > 1 || PF) ? 2 : 3)
+chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     constexpr int P = kP;
     using G = Geo<T, N, P, R, ROWS, 4>;
-    using S = ScanSmem<T, N, R, ROWS, HALF>;
+    using S = ScanSmem<T, N, R, ROWS>;
     using RawT = Raw<T, N, P, R, ROWS, 4, true>;
     using op_t = typename S::op_t;
     constexpr int KB = Op<T>::KB;
@@ -495,9 +500,9 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     const int c = lane & 15;
 
     const size_t H = a.heads, L = a.seq;
-    const size_t bhk = blockIdx.x;
-    const int ck = static_cast<int>(bhk % nck);
-    const size_t bh = bhk / nck;
+    const size_t bhs = blockIdx.x;
+    const int seg = static_cast<int>(bhs % nseg);
+    const size_t bh = bhs / nseg;
     const size_t bb = bh / H, hh = bh % H;
     const bool rot = a.theta != nullptr;
 
@@ -508,29 +513,26 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     const int pcol = 16 * wave + c;
 
     const SeqBufs rs = seq_bufs<T, N, P, R>(a, bb, hh);
-    // The (first sub-)chunk's inputs go first: the stage waits for them while
-    // the state fragments below are still in flight.  bf16 sub-chunks then load
-    // the next sub-chunk's inputs behind the current one's work (f32 lacks the
-    // registers for it).
-    constexpr bool kPrefetch = HALF > 1 && sizeof(T) == 2;
+    const int h_end = min(kseg, nsub - seg * kseg);
+    // The first sub-chunk's inputs go first: its stage waits for them while
+    // the state fragments below are still in flight.
     RawT cur, nxt;
-    if constexpr (HALF == 1 || kPrefetch)
-        load_chunk<T, N, P, R, ROWS, 4, true>(rs, ck * HALF, wave, lane, HALF == 1 ? cur : nxt);
+    load_chunk<T, N, P, R, ROWS, 4, true>(rs, seg * kseg, wave, lane, PF ? nxt : cur);
 
-    // the state entering this chunk, in its frame, as carry-in A operands
+    // the state entering this segment, in its frame, as carry-in A operands
     // (bf16: n-tiles 2kb and 2kb + 1 form k-block kb, matching npos)
     using frag_t = typename std::conditional<kBf16, bf16x8, f32x4>::type;
     constexpr int NF = kBf16 ? N / 32 : NTN;
     frag_t sf[NF];
     if constexpr (kBf16) {
-        const bf16x4 *src = static_cast<const bf16x4 *>(ws.s) + (bhk * 4 + wave) * NTN * 64 + lane;
+        const bf16x4 *src = static_cast<const bf16x4 *>(ws.s) + (bhs * 4 + wave) * NTN * 64 + lane;
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
             const bf16x4 lo = src[(2 * f) * 64], hi = src[(2 * f + 1) * 64];
             sf[f] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
     } else {
-        const f32x4 *src = static_cast<const f32x4 *>(ws.s) + (bhk * 4 + wave) * NTN * 64 + lane;
+        const f32x4 *src = static_cast<const f32x4 *>(ws.s) + (bhs * 4 + wave) * NTN * 64 + lane;
 #pragma unroll
         for (int f = 0; f < NF; ++f) sf[f] = src[f * 64];
     }
@@ -539,17 +541,40 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
     if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);
     const float dskip = a.d_skip ? a.d_skip[hh] : 0.0f;
     const bool skip = a.d_skip != nullptr;
+    // the angle of every pair relative to the segment start is zero on entry
+    if (tid < NH) sm.psi[tid] = 0.0f;
+    // With the prefetch, the state fragments and the first sub-chunk's inputs
+    // land before the loop: a wait for them inside it would also cover the
+    // next sub-chunk's prefetch on every pass (vmcnt counts in issue order).
+    // Without it, the first stage starts while the fragments are in flight.
+    if constexpr (PF) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
 
 #pragma unroll 1
-    for (int h = 0; h < HALF; ++h) {
-    const int sck = ck * HALF + h;
-    if constexpr (kPrefetch) {
+    for (int h = 0; h < h_end; ++h) {
+    // The lane-derived indices are re-derived from an opaque copy of the lane
+    // number in every sub-chunk: otherwise the compiler hoists every LDS
+    // address they feed out of the loop and keeps them live across it, which
+    // costs ~60 VGPRs and spills at three workgroups per CU.
+    int lane_v = lane;
+    asm volatile("" : "+v"(lane_v));
+    const int lane = lane_v;
+    const int g = lane >> 4;
+    const int c = lane & 15;
+    const int sub = lane / G::SW;
+    const int my_t = lane % G::SW;
+    const bool tok_lane = my_t < QT;
+    const int i0 = wave * G::PW + sub * PPL;
+    const int pcol = 16 * wave + c;
+    const int sck = seg * kseg + h;
+    const bool advance = h + 1 < h_end;
+    if constexpr (PF) {
         cur = nxt;
-        if (h + 1 < HALF) load_chunk<T, N, P, R, ROWS, 4, true>(rs, sck + 1, wave, lane, nxt);
-    } else if constexpr (HALF > 1) {
+        if (advance) load_chunk<T, N, P, R, ROWS, 4, true>(rs, sck + 1, wave, lane, nxt);
+    } else if (h > 0) {
         load_chunk<T, N, P, R, ROWS, 4, true>(rs, sck, wave, lane, cur);
     }
-    // ---- stage: per-token scalars, in-chunk angles, rotated B and C, X^T
+    // ---- stage: per-token scalars, angles, rotated B and C, X^T
     {
         const size_t tau = static_cast<size_t>(sck) * QT + my_t;
         const bool live = tok_lane && tau < L;
@@ -560,34 +585,9 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
             sm.acum[my_t] = acum;
             sm.gw[my_t] = gv;
             sm.ww[my_t] = wv;
-            sm.eac[my_t] = dexp<kBf16>(acum);             // exp_decay(acum)
-            if (HALF > 1) {
-                const float last = __int_as_float(
-                    __builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
-                sm.wdv[my_t] = dexp<kBf16>(last - acum) * wv;   // w x decay to the end
-            }
-        }
-        float cs[PPL], sn[PPL];
-#pragma unroll
-        for (int j = 0; j < PPL; ++j) {
-            cs[j] = 1.0f;
-            sn[j] = 0.0f;
-        }
-        if (rot) {
-            const float dtt = live ? cur.s0 : 0.0f;
-#pragma unroll
-            for (int j = 0; j < PPL; ++j) {
-                const float pre = seg_scan<G::SW>(dtt * welem<T>(cur.th, j));
-                if (HALF > 1 && my_t == QT - 1) sm.phi_tot[i0 + j] = pre;
-                const float psi = wrap_angle(pre);
-                if constexpr (kBf16) {
-                    const float rev = psi * 0.15915494309189533577f;
-                    sn[j] = __builtin_amdgcn_sinf(rev);
-                    cs[j] = __builtin_amdgcn_cosf(rev);
-                } else {
-                    sincosf(psi, &sn[j], &cs[j]);
-                }
-            }
+            const float last = __int_as_float(
+                __builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
+            sm.wdv[my_t] = dexp<kBf16>(last - acum) * wv;   // w x decay to the end
         }
         if (tok_lane) {
 #pragma unroll
@@ -596,36 +596,57 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
                 const int p = o / R, r = o % R;
                 sm.Xt[p * LDR + my_t * R + r] = to_op<op_t>(elem<T>(cur.x, e));
             }
+        }
+        // per group of (up to) four pairs: the angle within the segment (the
+        // running angle plus the in-sub-chunk inclusive cumsum of dt * theta),
+        // its sine and cosine, and B and C rotated by its negative
+        // (fused.rs:610-617) and stored -- one group's values live at a time
+        const float dtt = live ? cur.s0 : 0.0f;
+        constexpr int GP = PPL % 4 == 0 ? 4 : 1;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int rho = my_t * R + r;
-                float rb[2][PPL], rc[2][PPL];
+        for (int q = 0; q < PPL; q += GP) {
+            float cs[GP], sn[GP];
 #pragma unroll
-                for (int j = 0; j < PPL; ++j) {
-                    const float b1 = elem<T>(cur.b[0], j * R + r);
-                    const float b2 = elem<T>(cur.b[1], j * R + r);
-                    const float c1 = elem<T>(cur.c[0], j * R + r);
-                    const float c2 = elem<T>(cur.c[1], j * R + r);
-                    rb[0][j] = b1 * cs[j] + b2 * sn[j];
-                    rb[1][j] = -b1 * sn[j] + b2 * cs[j];
-                    rc[0][j] = c1 * cs[j] + c2 * sn[j];
-                    rc[1][j] = -c1 * sn[j] + c2 * cs[j];
-                }
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    if constexpr (PPL % 4 == 0) {
-#pragma unroll
-                        for (int q = 0; q < PPL; q += 4) {
-                            const int n = i0 + h * NH + q;
-                            st4(&sm.Bs[rho * LDN + npos<kBf16>(n)], &rb[h][q]);
-                            st4(&sm.Cs[rho * LDN + npos<kBf16>(n)], &rc[h][q]);
-                        }
+            for (int jj = 0; jj < GP; ++jj) {
+                const int j = q + jj;
+                cs[jj] = 1.0f;
+                sn[jj] = 0.0f;
+                if (rot) {
+                    const float pre = seg_scan<G::SW>(dtt * welem<T>(cur.th, j));
+                    const float phi = wrap_angle(sm.psi[i0 + j] + pre);
+                    // the sub-chunk's last token carries the angle to the next one
+                    if (my_t == QT - 1) sm.psi[i0 + j] = phi;
+                    if constexpr (kBf16) {
+                        const float rev = phi * 0.15915494309189533577f;
+                        sn[jj] = __builtin_amdgcn_sinf(rev);
+                        cs[jj] = __builtin_amdgcn_cosf(rev);
                     } else {
+                        sincosf(phi, &sn[jj], &cs[jj]);
+                    }
+                }
+            }
+            if (tok_lane) {
 #pragma unroll
-                        for (int j = 0; j < PPL; ++j) {
-                            const int n = i0 + h * NH + j;
-                            sm.Bs[rho * LDN + npos<kBf16>(n)] = to_op<op_t>(rb[h][j]);
-                            sm.Cs[rho * LDN + npos<kBf16>(n)] = to_op<op_t>(rc[h][j]);
+                for (int which = 0; which < 2; ++which) {
+                    const u32x4(&src)[2][G::HV] = which == 0 ? cur.b : cur.c;
+                    op_t *dst = which == 0 ? sm.Bs : sm.Cs;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const int rho = my_t * R + r;
+                        float rv[2][GP];
+#pragma unroll
+                        for (int jj = 0; jj < GP; ++jj) {
+                            const float v1 = elem<T>(src[0], (q + jj) * R + r);
+                            const float v2 = elem<T>(src[1], (q + jj) * R + r);
+                            rv[0][jj] = v1 * cs[jj] + v2 * sn[jj];
+                            rv[1][jj] = -v1 * sn[jj] + v2 * cs[jj];
+                        }
+#pragma unroll
+                        for (int hf = 0; hf < 2; ++hf) {
+                            if constexpr (GP == 4)
+                                st4(&dst[rho * LDN + npos<kBf16>(i0 + hf * NH + q)], rv[hf]);
+                            else
+                                dst[rho * LDN + npos<kBf16>(i0 + hf * NH + q)] = to_op<op_t>(rv[hf][0]);
                         }
                     }
                 }
@@ -696,7 +717,7 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
                 for (int r = 0; r < 4; ++r) acc = mfma_f32(sf[i][r], bv[r], acc);
             }
         }
-        acc = acc * sm.eac[(16 * tj + c) / R];
+        acc = acc * dexp<kBf16>(sm.acum[(16 * tj + c) / R]);   // exp_decay(acum)
         const op_t *mr = &sm.Ms[(16 * tj + c) * LDR];
         const int tlast = (16 * tj + 15) / R;
         const int send = (tlast + 1) * R < ROWS ? (tlast + 1) * R : ROWS;
@@ -734,129 +755,72 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nck) {
         }
     }
 
-    if (h + 1 < HALF) {
-        // ---- the state entering the next sub-chunk: S' = R(Phi_h)(e_h S + U_h),
+    if (advance) {
+        // ---- the state entering the next sub-chunk: S' = e_h S + U_h with
         // U_h^T[n][p] = sum_rho (B~ w decay-to-end)[rho][n] X^T[p][rho] over
-        // this wave's p-tile; the D tiles of U line up with the S fragments
+        // this wave's p-tile.  This lane holds S at p = 16 wave + c,
+        // n = 16 i + 4 g + r: the D layout of the U_h tiles.
         const float eh = dexp<kBf16>(sm.acum[QT - 1]);
-        f32x4 uh[NTN];
+        if constexpr (kBf16) {
+            // A operand B~^T (rows n = 16 i + c, k-slot j <-> rho = 32 kb + 8 g + j)
+            // by two transposed reads of the row-major B~; B operand the
+            // weighted X^T slice (w decay per row, rounded to bf16 once).  One
+            // fragment (two n-tiles) at a time, so few f32 tiles are live.
+            constexpr int NKB = ROWS / 32;
+            bf16x8 xw[NKB];
 #pragma unroll
-        for (int i = 0; i < NTN; ++i) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            const int n = 16 * i + c;
+            for (int kb = 0; kb < NKB; ++kb) {
+                const bf16x8 xv = *reinterpret_cast<const bf16x8 *>(xr + 32 * kb + 8 * g);
 #pragma unroll
-            for (int kb = 0; kb < ROWS / KB; ++kb) {
-                if constexpr (kBf16) {
-                    bf16x8 av;
+                for (int j = 0; j < 8; ++j)
+                    xw[kb][j] = static_cast<__bf16>(static_cast<float>(xv[j]) *
+                                                    sm.wdv[(32 * kb + 8 * g + j) / R]);
+            }
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int rho = 32 * kb + 8 * g + j;
-                        av[j] = static_cast<__bf16>(
-                            static_cast<float>(sm.Bs[rho * LDN + npos<kBf16>(n)]) * sm.wdv[rho / R]);
+            for (int f = 0; f < NF; ++f) {
+                f32x4 st[2];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) st[q][r] = static_cast<float>(sf[f][q * 4 + r]) * eh;
+#pragma unroll
+                    for (int kb = 0; kb < NKB; ++kb) {
+                        const int row0 = 32 * kb + 8 * g + (c >> 2);
+                        const __bf16 *p0 =
+                            &sm.Bs[row0 * LDN + npos<true>(16 * (2 * f + q) + 4 * (c & 3))];
+                        const bf16x4 lo = lds_read_tr16(p0);
+                        const bf16x4 hi = lds_read_tr16(p0 + 4 * LDN);
+                        const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                        st[q] = mfma_bf16(av, xw[kb], st[q]);
                     }
-                    acc = mfma_bf16(av, *reinterpret_cast<const bf16x8 *>(xr + 32 * kb + 8 * g), acc);
-                } else {
+                }
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sf[f][q * 4 + r] = static_cast<__bf16>(st[q][r]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NTN; ++i) {
+                f32x4 st = sf[i] * eh;
+                const int n = 16 * i + c;
+#pragma unroll
+                for (int kb = 0; kb < ROWS / KB; ++kb) {
                     const f32x4 bv = *reinterpret_cast<const f32x4 *>(xr + 16 * kb + 4 * g);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int rho = 16 * kb + 4 * g + j;
-                        acc = mfma_f32(static_cast<float>(sm.Bs[rho * LDN + n]) * sm.wdv[rho / R],
-                                       bv[j], acc);
+                        st = mfma_f32(static_cast<float>(sm.Bs[rho * LDN + n]) * sm.wdv[rho / R],
+                                      bv[j], st);
                     }
                 }
-            }
-            uh[i] = acc;
-        }
-        // S (this lane: p = 16 wave + c, n = 16 i + 4 g + r) in f32, advanced and rotated
-        f32x4 st[NTN];
-#pragma unroll
-        for (int i = 0; i < NTN; ++i) {
-            if constexpr (kBf16) {
-                const bf16x8 f = sf[i / 2];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) st[i][r] = static_cast<float>(f[(i & 1) * 4 + r]);
-            } else {
-                st[i] = sf[i];
-            }
-            st[i] = st[i] * eh + uh[i];
-        }
-        if (rot) {
-#pragma unroll
-            for (int i = 0; i < NTN / 2; ++i) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float ps, pc;
-                    sincosf(sm.phi_tot[16 * i + 4 * g + r], &ps, &pc);
-                    const float lo = st[i][r], hi = st[i + NTN / 2][r];
-                    st[i][r] = lo * pc - hi * ps;                  // R(Phi_h)
-                    st[i + NTN / 2][r] = lo * ps + hi * pc;
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < NTN; ++i) {
-            if constexpr (kBf16) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) sf[i / 2][(i & 1) * 4 + r] = static_cast<__bf16>(st[i][r]);
-            } else {
-                sf[i] = st[i];
+                sf[i] = st;
             }
         }
         lds_barrier();   // the next sub-chunk's staging reuses the LDS
     }
     }   // sub-chunks
 }
-
-// Sub-chunks per chunk of the three launches: one per rank, so that a chunk
-// spans ROWS tokens whatever the rank and the U / S records and the state
-// pass stay per ROWS tokens (the MIMO ranks would otherwise multiply them).
-constexpr int half_for(int r) { return r; }
-
-size_t chunk_count(const ScanLaunch &a, int rows) {
-    const size_t qt = static_cast<size_t>(rows) / a.rank;
-    const size_t nsub = (a.seq + qt - 1) / qt;
-    const size_t half = static_cast<size_t>(half_for(static_cast<int>(a.rank)));
-    return (nsub + half - 1) / half;
-}
-
-template <typename T, int N, int R, int ROWS>
-hipError_t launch_three(const ScanLaunch &a, char *base, hipStream_t s) {
-    constexpr int HALF = half_for(R);
-    const int nck = static_cast<int>(chunk_count(a, ROWS));
-    const size_t bh = a.batch * a.heads;
-    const size_t bhk = bh * nck;
-    const ChunkWs ws = chunk_ws(base, chunked_layout(bhk, N, sizeof(T) == 2));
-    hipLaunchKernelGGL((chunk_state_kernel<T, N, R, ROWS, HALF>), dim3(bhk), dim3(kThreads), 0, s,
-                       a, ws, nck);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((state_pass_kernel<T, N>), dim3(bh * (N / 32)), dim3(kThreads), 0, s, a, ws,
-                       nck);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((chunk_scan_kernel<T, N, R, ROWS, HALF>), dim3(bhk), dim3(kThreads), 0, s,
-                       a, ws, nck);
-    return hipGetLastError();
-}
-
-template <typename T, int ROWS>
-hipError_t launch_t(const ScanLaunch &a, char *ws, hipStream_t s) {
-    const size_t n = a.d_state, r = a.rank;
-    if (n == 128) {
-        if (r == 1) return launch_three<T, 128, 1, ROWS>(a, ws, s);
-        if (r == 2) return launch_three<T, 128, 2, ROWS>(a, ws, s);
-        if (r == 4) return launch_three<T, 128, 4, ROWS>(a, ws, s);
-    } else if (n == 64) {
-        if (r == 1) return launch_three<T, 64, 1, ROWS>(a, ws, s);
-        if (r == 2) return launch_three<T, 64, 2, ROWS>(a, ws, s);
-        if (r == 4) return launch_three<T, 64, 4, ROWS>(a, ws, s);
-    }
-    return hipErrorNotSupported;
-}
-
-int rows_for(const ScanLaunch &a) { return a.bf16 ? 64 : 32; }
-
-}  // namespace
 
 // The single pass walks each (batch, head) sequence with one workgroup per CU,
 // so its time goes in whole rounds of one sequence per CU; the three
@@ -879,13 +843,87 @@ static size_t device_cus() {
     return static_cast<size_t>(cus);
 }
 
+int rows_for(const ScanLaunch &a) { return a.bf16 ? 64 : 32; }
+
+// How a sequence is cut: nsub sub-chunks of ROWS rows (ROWS / R tokens), kseg
+// of them per segment, nseg segments.  The state passes between segments
+// only, so U and S records and the state pass shrink with kseg, while the
+// chunk_scan workgroups (one per segment) should still fill the chip once: a
+// segment takes at least the caller's chunk_size tokens, and more where
+// there are sub-chunks to spare beyond one resident workgroup per slot.
+struct SegPlan {
+    int nsub, kseg, nseg;
+};
+
+SegPlan seg_plan(const ScanLaunch &a) {
+    const size_t qt = static_cast<size_t>(rows_for(a)) / a.rank;
+    const size_t nsub = (a.seq + qt - 1) / qt;
+    const size_t q = a.chunk_size ? a.chunk_size : 64;
+    const size_t kmin = (q + qt - 1) / qt;
+    // rounds of resident chunk_scan workgroups: two at rank 1, eight for MIMO
+    // (measured on MI355X, rotated inputs, us per call: config 1 at 1 / 2 / 4
+    // rounds 123.1 / 120.0 / 132.0; config 2 at 2 / 4 / 8 / 16 rounds
+    // 624 / 592 / 580 / 591, against 125.0 and 724.6 for one 64-token chunk
+    // per workgroup)
+    const size_t slots = device_cus() * (a.rank > 1 ? 2 : 3);
+    const size_t rounds = a.rank > 1 ? 8 : 2;
+    const size_t kfill = a.batch * a.heads * nsub / (rounds * slots);
+    size_t k = kmin > kfill ? kmin : kfill;
+    if (k < 1) k = 1;
+    if (k > nsub) k = nsub;
+    SegPlan p;
+    p.nsub = static_cast<int>(nsub);
+    p.kseg = static_cast<int>(k);
+    p.nseg = static_cast<int>((nsub + k - 1) / k);
+    return p;
+}
+
+template <typename T, int N, int R, int ROWS>
+hipError_t launch_three(const ScanLaunch &a, char *base, hipStream_t s) {
+    // MIMO sub-chunks hold few tokens: their inputs are loaded behind the
+    // previous one's work (bf16; f32 lacks the registers).  At rank 1 the
+    // prefetch measured slower (its 52 VGPRs cost more than the loads it hides).
+    constexpr bool kPf = R > 1 && sizeof(T) == 2;
+    const SegPlan sp = seg_plan(a);
+    const size_t bh = a.batch * a.heads;
+    const size_t bhs = bh * sp.nseg;
+    const ChunkWs ws = chunk_ws(base, chunked_layout(bhs, N, sizeof(T) == 2));
+    hipLaunchKernelGGL((chunk_state_kernel<T, N, R, ROWS, kPf>), dim3(bhs),
+                       dim3(kThreads), 0, s, a, ws, sp.nsub, sp.kseg, sp.nseg);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((state_pass_kernel<T, N>), dim3(bh * (N / 32)), dim3(kThreads), 0, s, a, ws,
+                       sp.nseg);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((chunk_scan_kernel<T, N, R, ROWS, kPf>), dim3(bhs), dim3(kThreads), 0, s, a,
+                       ws, sp.nsub, sp.kseg, sp.nseg);
+    return hipGetLastError();
+}
+
+template <typename T, int ROWS>
+hipError_t launch_t(const ScanLaunch &a, char *ws, hipStream_t s) {
+    const size_t n = a.d_state, r = a.rank;
+    if (n == 128) {
+        if (r == 1) return launch_three<T, 128, 1, ROWS>(a, ws, s);
+        if (r == 2) return launch_three<T, 128, 2, ROWS>(a, ws, s);
+        if (r == 4) return launch_three<T, 128, 4, ROWS>(a, ws, s);
+    } else if (n == 64) {
+        if (r == 1) return launch_three<T, 64, 1, ROWS>(a, ws, s);
+        if (r == 2) return launch_three<T, 64, 2, ROWS>(a, ws, s);
+        if (r == 4) return launch_three<T, 64, 4, ROWS>(a, ws, s);
+    }
+    return hipErrorNotSupported;
+}
+
+}  // namespace
+
 size_t scan_chunked_workspace(const ScanLaunch &a) {
     if (!scan_fast_supported(a) || a.seq == 0) return 0;
     const size_t seqs = a.batch * a.heads, cus = device_cus();
     const size_t rounds = (seqs + cus - 1) / cus;
     if (seqs * 10 >= rounds * cus * 7) return 0;
-    return chunked_layout(a.batch * a.heads * chunk_count(a, rows_for(a)), a.d_state, a.bf16 != 0)
-        .total;
+    return chunked_layout(seqs * seg_plan(a).nseg, a.d_state, a.bf16 != 0).total;
 }
 
 hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream) {

@@ -156,18 +156,23 @@ def test_scan_workspace_query():
     from mamba3 import _lib
     L = _lib.lib()
 
-    def need(B, T, H, P, N, R, dtype):
+    def need(B, T, H, P, N, R, dtype, chunk=64):
         cin = _lib.ScanInputsC(B, T, H, P, N, R, dtype, None, None, None, None, None, None,
-                               None, None, None, 64, 1, None, 0)
+                               None, None, None, chunk, 1, None, 0)
         return int(L.m3_scan_workspace_bytes(C.byref(cin)))
 
-    w1 = need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16)
-    # per chunk of 64 tokens: U_k and S_k (bf16 64x128 each), the chunk
-    # decay, and angle total / cosine / sine per pair (3 x 64 f32)
-    bhk = 8 * 12 * 32
-    assert w1 == bhk * (2 * 64 * 128 * 2 + 4 + 3 * 64 * 4)
-    # f32 storage: 32-token chunks at rank 1 and an f32 S_k
-    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) == 2 * bhk * (64 * 128 * 8 + 4 + 3 * 64 * 4)
+    # per segment: U and S (bf16 64x128 each), the segment decay, and angle
+    # total / cosine / sine per pair (3 x 64 f32).  At config 1 (96 sequences
+    # of 32 sub-chunks of 64 tokens) segments of 2 sub-chunks give 1536
+    # chunk_scan workgroups: two rounds of three per CU on the 256 CUs the
+    # query assumes without a device
+    record = 2 * 64 * 128 * 2 + 4 + 3 * 64 * 4
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 8 * 12 * 16 * record
+    # chunk_size is the shortest segment: 512 tokens -> 4 segments per sequence
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16, chunk=512) == 8 * 12 * 4 * record
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16, chunk=1) == 8 * 12 * 16 * record
+    # f32 storage: 32-token sub-chunks, 4 per segment, and f32 U and S
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) == 8 * 12 * 16 * (64 * 128 * 8 + 4 + 3 * 64 * 4)
     # the single pass runs one sequence per CU (256 CUs here, the CPU
     # fallback of the query): it is the faster form once its last round of
     # sequences fills 70 % of the CUs
@@ -236,7 +241,8 @@ def test_no_alloc_scan_rejects_beyond_its_scratch():
     from mamba3 import _lib
     L = _lib.lib()
     fake = 1 << 20
-    cin = _lib.ScanInputsC(1, 65536, 12, 64, 128, 1, _lib.M3_BF16, fake, fake, fake, fake, fake,
+    # f32 keeps U and S in f32: ~64 KB per segment record at d_state 128
+    cin = _lib.ScanInputsC(1, 65536, 12, 64, 128, 1, _lib.M3_F32, fake, fake, fake, fake, fake,
                            fake, fake, None, None, 64, 0, None, 0)
     need = int(L.m3_scan_workspace_bytes(C.byref(cin)))
     assert need > 32 << 20

@@ -146,6 +146,53 @@ def test_scan_features_against_f64(B, T, H, P, N, R, theta, skip, state, dtype, 
         assert angle_err(ang, ang64) <= (1e-4 if dtype == "f32" else 1e-3)
 
 
+# chunk_size sets the shortest segment of the chunk-parallel path (the state
+# passes between segments; inside one it advances in registers sub-chunk by
+# sub-chunk): segments of 1 to 64 sub-chunks, every rank, both storage types
+SEGMENT_CASES = [
+    # B, T, H, N, R, dtype, chunk_size
+    (1, 700, 2, 128, 1, "bf16", 128),
+    (1, 700, 2, 128, 1, "bf16", 256),
+    (2, 700, 1, 128, 1, "bf16", 448),
+    (1, 1000, 2, 64, 1, "bf16", 512),
+    (1, 576, 1, 128, 1, "bf16", 4096),
+    (1, 513, 2, 128, 2, "bf16", 192),
+    (1, 300, 2, 128, 4, "bf16", 256),
+    (1, 300, 1, 64, 4, "bf16", 1024),
+    (1, 333, 2, 128, 1, "f32", 160),
+    (1, 300, 1, 64, 4, "f32", 128),
+    (1, 257, 2, 64, 2, "f32", 96),
+]
+
+
+@pytest.mark.parametrize("B,T,H,N,R,dtype,chunk", SEGMENT_CASES)
+def test_segments_against_f64(B, T, H, N, R, dtype, chunk):
+    import ctypes as C
+    from mamba3 import _lib
+    rng = np.random.default_rng(zlib.crc32(repr((B, T, H, N, R, dtype, chunk)).encode()))
+    P = 64
+    inp = baseline_inputs(rng, B, T, H, P, N, R, theta=True, dtype=dtype,
+                          theta_per_head=False, state=True)
+    d_skip = rng.uniform(-1, 1, H).astype(np.float32)
+    st = (inp["h0"], inp["last_u0"], inp.get("angle0"))
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    # the chunk-parallel form runs, and longer segments need less workspace
+    need = lambda q: _lib.lib().m3_scan_workspace_bytes(C.byref(_lib.ScanInputsC(
+        B, T, H, P, N, R, _lib.M3_BF16 if dtype == "bf16" else _lib.M3_F32, 16, 16, 16, 16, 16,
+        16, 16, None, None, q, 1, None, 0)))
+    assert need(chunk) > 0
+    assert need(chunk) <= need(64)
+    y, h, lu, ang = run_scan(inp, dtype=tdt, chunk=chunk, skip=d_skip, state=st)
+    y64, h64, lu64, ang64 = oracle_scan(inp, skip=d_skip, state=st)
+    tol = BF16_TOL if dtype == "bf16" else F32_TOL
+    errs = dict(y=rel_l2(y, y64), h=rel_l2(h, h64), last_u=rel_l2(lu, lu64))
+    print(f"segments of >= {chunk} tokens, {dtype} R={R} N={N} T={T}: rel-L2 "
+          + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()) + f" (bar {tol:g})")
+    for k, v in errs.items():
+        assert v <= tol, (k, v)
+    assert angle_err(ang, ang64) <= (1e-4 if dtype == "f32" else 1e-3)
+
+
 def test_want_state_false_writes_no_state():
     rng = np.random.default_rng(5)
     inp = baseline_inputs(rng, 1, 20, 1, 16, 32, 1, theta=True)
@@ -203,6 +250,8 @@ def test_config1_bf16_two_heads_full_length():
     inp = baseline_inputs(rng, 1, 2048, 2, 64, 128, 1, theta=True, dtype="bf16")
     y, h, lu, ang = run_scan(inp, dtype=torch.bfloat16)
     y64, h64, lu64, ang64 = oracle_scan(inp)
+    print(f"config 1, 2 heads, L=2048: rel-L2 y {rel_l2(y, y64):.2e}, h {rel_l2(h, h64):.2e}, "
+          f"last_u {rel_l2(lu, lu64):.2e} (bar {BF16_TOL:g})")
     assert rel_l2(y, y64) <= BF16_TOL
     assert rel_l2(h, h64) <= BF16_TOL
     assert angle_err(ang, ang64) <= 1e-3
