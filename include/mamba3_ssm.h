@@ -173,8 +173,10 @@ m3_status m3_scan_no_alloc(const m3_scan_inputs *in, const m3_scan_output *out, 
  * scan.rs:458-638; its own adjoint kernels are ssd_band_backward fused.rs:
  * 2080-2138, exp_decay_backward 2326-2382 and trapezoid_weights_backward
  * 2513-2549).  Layouts as m3_scan_inputs; dx, db, dc and dtheta are in the
- * inputs' dtype, the rest f32.  The upstream gradient of the outgoing last_u
- * is not accepted (training runs with want_state false, mamba3.rs:518). */
+ * inputs' dtype, the rest f32.  Upstream gradients of the outgoing state (h,
+ * last_u, angle) are optional; last_u's flows into x, b and the angle of the
+ * last token (last_u = sum_r x_{L-1,r} B~_{L-1,r}^T, scan.rs:599-618), which is
+ * how a window chained to the next one through SsmState is differentiated. */
 typedef struct m3_scan_grads {
     const void *dy;           /* [B, T, H, P, R]: dL/dy (required) */
     const float *dh;          /* [B, H, P, N]: dL/d(output state h), or NULL */
@@ -190,6 +192,7 @@ typedef struct m3_scan_grads {
     float *dh0;               /* [B, H, P, N] or NULL (carried-in state only) */
     float *dlast_u0;          /* [B, H, P, N] or NULL (carried-in state only) */
     float *dangle0;           /* [B, H, N/2] or NULL (carried-in angle only) */
+    const float *dlast_u;     /* [B, H, P, N]: dL/d(output state last_u), or NULL */
 } m3_scan_grads;
 
 /* Backward of m3_scan on the same inputs (`in`, whose workspace must hold

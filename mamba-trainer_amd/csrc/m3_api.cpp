@@ -415,7 +415,10 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
         if (e == hipSuccess && g->dh0)
             e = g->dh ? hipMemcpyAsync(g->dh0, g->dh, sbytes, hipMemcpyDeviceToDevice, s)
                       : hipMemsetAsync(g->dh0, 0, sbytes, s);
-        if (e == hipSuccess && g->dlast_u0) e = hipMemsetAsync(g->dlast_u0, 0, sbytes, s);
+        // the outgoing last_u is the incoming one
+        if (e == hipSuccess && g->dlast_u0)
+            e = g->dlast_u ? hipMemcpyAsync(g->dlast_u0, g->dlast_u, sbytes, hipMemcpyDeviceToDevice, s)
+                           : hipMemsetAsync(g->dlast_u0, 0, sbytes, s);
         if (e == hipSuccess && g->dangle0) {
             const size_t abytes = B * H * (N / 2) * sizeof(float);
             e = g->dangle ? hipMemcpyAsync(g->dangle0, g->dangle, abytes, hipMemcpyDeviceToDevice, s)
@@ -431,7 +434,7 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
                     "16-byte aligned buffers");
     {
         // gradient buffers are written (and dh read) in 8- and 16-byte pieces
-        const void *ptrs[] = {g->dx, g->db, g->dc, g->dtheta, g->dh, g->dh0, g->dlast_u0};
+        const void *ptrs[] = {g->dx, g->db, g->dc, g->dtheta, g->dh, g->dh0, g->dlast_u0, g->dlast_u};
         for (const void *q : ptrs)
             if ((reinterpret_cast<uintptr_t>(q) & 15u) != 0)
                 return fail(M3_ERR_UNSUPPORTED,
@@ -446,6 +449,7 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
     gr.dy = g->dy;
     gr.dh_out = g->dh;
     gr.dangle_out = in->theta ? g->dangle : nullptr;
+    gr.dlast_u_out = g->dlast_u;
     gr.dx = g->dx;
     gr.db = g->db;
     gr.dc = g->dc;
@@ -459,7 +463,7 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
     gr.dangle0 = (st && st->angle && in->theta) ? g->dangle0 : nullptr;
     e = m3::launch_scan_backward(a, gr, in->workspace, s);
     if (e != hipSuccess) return hip_fail(e, "scan backward launch");
-    g_launches.fetch_add(in->theta ? 7 : 6, std::memory_order_relaxed);
+    g_launches.fetch_add((in->theta ? 7 : 6) + (g->dlast_u ? 2 : 0), std::memory_order_relaxed);
     if (g->dd_skip != nullptr && in->d_skip == nullptr) {
         e = hipMemsetAsync(g->dd_skip, 0, H * sizeof(float), s);
         if (e != hipSuccess) return hip_fail(e, "dd_skip");

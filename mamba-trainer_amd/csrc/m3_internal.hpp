@@ -64,6 +64,7 @@ struct ScanGrads {
     const void *dy;                 // [B,T,H,P,R]
     const float *dh_out;            // [B,H,P,N] or null
     const float *dangle_out;        // [B,H,N/2] or null
+    const float *dlast_u_out;       // [B,H,P,N] or null
     void *dx, *db, *dc;             // like x, b, c
     float *ddt, *dlambda;           // [B,T,H]
     float *da_log;                  // [H]

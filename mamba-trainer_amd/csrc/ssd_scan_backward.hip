@@ -46,6 +46,7 @@ struct BwdArgs {
     const void *dy;           // [B,T,H,P,R]
     const float *dh_out;      // [B,H,P,N] or null
     const float *dangle_out;  // [B,H,N/2] or null
+    const float *dlast_u_out; // [B,H,P,N] or null
     void *dx, *db, *dc;       // storage type
     float *ddt, *dlambda;     // [B,T,H]
     float *da_log;            // [H]
@@ -59,13 +60,16 @@ struct BwdArgs {
 // U_k, S_k, V_k and Gh_k as f32 [p-tile][n-tile][lane][4] MFMA D-layout
 // records of the [P][N] state, the chunk decay e_k, and per rotation pair the
 // chunk's angle total Phi_k with its cosine and sine.
+// With an upstream gradient of the outgoing last_u: the angle seed (that
+// gradient's angle term plus dL/dangle) and the last token's dx and db terms.
 struct BwdLayout {
-    size_t u, s, v, gh, eda, phi, cph, sph, cin, ctot, off, da, dg, dw, pd, pa, pfirst, total;
+    size_t u, s, v, gh, eda, phi, cph, sph, cin, ctot, off, da, dg, dw, pd, pa, pfirst;
+    size_t seed, lux, lub, total;
 };
 
 size_t balign(size_t v) { return (v + 255) & ~size_t(255); }
 
-BwdLayout bwd_layout(size_t bh, size_t nck, size_t seq, size_t n) {
+BwdLayout bwd_layout(size_t bh, size_t nck, size_t seq, size_t n, size_t r) {
     const size_t bhk = bh * nck, rec = bhk * kP * n * 4, pairs = bhk * (n / 2) * 4;
     BwdLayout l;
     size_t o = 0;
@@ -86,6 +90,9 @@ BwdLayout bwd_layout(size_t bh, size_t nck, size_t seq, size_t n) {
     l.pd = o;     o = balign(o + bhk * 4);
     l.pa = o;     o = balign(o + bhk * 4);
     l.pfirst = o; o = balign(o + bh * (n / 32) * 4);
+    l.seed = o;   o = balign(o + bh * (n / 2) * 4);
+    l.lux = o;    o = balign(o + bh * kP * r * 4);
+    l.lub = o;    o = balign(o + bh * n * r * 4);
     l.total = o;
     return l;
 }
@@ -93,6 +100,7 @@ BwdLayout bwd_layout(size_t bh, size_t nck, size_t seq, size_t n) {
 struct BwdWs {
     float *u, *s, *v, *gh, *eda, *phi, *cph, *sph;
     float *cin, *ctot, *off, *da, *dg, *dw, *pd, *pa, *pfirst;
+    float *seed, *lux, *lub;
 };
 
 // element access in the storage type
@@ -1145,6 +1153,103 @@ __global__ void __launch_bounds__(256) bwd_head_kernel(ScanLaunch a, BwdArgs g, 
     }
 }
 
+// ---------------------------------------------------------------- outgoing last_u
+// last_u = sum_r x_{L-1,r} (R(-phi_{L-1}) B_{L-1,r})^T (scan.rs:599-618), so an
+// upstream gradient G of it adds, at the last token,
+//   dx[p][r]  += sum_n G[p][n] B~[n][r]
+//   dB~[n][r]  = sum_p G[p][n] x[p][r],   dB = R(+phi) dB~
+//   dphi_i    += sum_r dB~_1 B~_2 - dB~_2 B~_1   (d B~_1/dphi = B~_2, d B~_2/dphi = -B~_1)
+// The angle term joins dL/dangle as the seed of the angle gradient's reverse
+// cumsum (bwd_angle_kernel); the dx and db terms wait in the workspace for
+// bwd_last_add_kernel.  One workgroup per (batch, head).
+template <typename T, int N, int R>
+__global__ void __launch_bounds__(256) bwd_last_u_kernel(ScanLaunch a, BwdArgs g, BwdWs w) {
+    constexpr int NH = N / 2, P = kP;
+    __shared__ float sphi[4][NH];
+    __shared__ float sx[P * R];
+    __shared__ float sb[N * R];      // B~ of the last token
+    __shared__ float sdb[N * R];     // dB~
+    const int tid = threadIdx.x;
+    const size_t bh = blockIdx.x;
+    const size_t H = a.heads, L = a.seq;
+    const size_t bb = bh / H, hh = bh % H;
+    const bool rot = a.theta != nullptr;
+    const size_t tl = (bb * L + (L - 1)) * H + hh;   // (b, L-1, h)
+    // phi_{L-1} = angle0 + sum_t dt_t theta_t, four token stripes per pair
+    if (rot) {
+        const int i = tid % NH, q = tid / NH;        // NH <= 64: q < 4 covers 256 threads
+        float acc = 0.0f;
+        if (i < NH && q < 4) {
+            for (size_t t = q; t < L; t += 4) {
+                const size_t row = (bb * L + t) * H + hh;
+                acc += a.dt[row] * ldv<T>(a.theta, row * NH + i);
+            }
+            sphi[q][i] = acc;
+        }
+    }
+    for (int e = tid; e < P * R; e += 256) sx[e] = ldv<T>(a.x, tl * P * R + e);
+    __syncthreads();
+    for (int i = tid; i < NH; i += 256) {
+        float phi = 0.0f, cs = 1.0f, sn = 0.0f;
+        if (rot) {
+            phi = sphi[0][i] + sphi[1][i] + sphi[2][i] + sphi[3][i];
+            if (a.angle0 != nullptr) phi += a.angle0[bh * NH + i];
+            sincosf(wrap_angle(phi), &sn, &cs);
+        }
+        sphi[0][i] = cs;
+        sphi[1][i] = sn;
+        for (int r = 0; r < R; ++r) {
+            const float b1 = ldv<T>(a.b, (tl * N + i) * R + r);
+            const float b2 = ldv<T>(a.b, (tl * N + i + NH) * R + r);
+            sb[i * R + r] = b1 * cs + b2 * sn;              // fused.rs:610-617
+            sb[(i + NH) * R + r] = -b1 * sn + b2 * cs;
+        }
+    }
+    __syncthreads();
+    const float *G = g.dlast_u_out + bh * P * N;
+    // dB~[n][r] = sum_p G[p][n] x[p][r]
+    for (int e = tid; e < N * R; e += 256) {
+        const int n = e / R, r = e % R;
+        float acc = 0.0f;
+        for (int p = 0; p < P; ++p) acc += G[p * N + n] * sx[p * R + r];
+        sdb[e] = acc;
+    }
+    // dx[p][r] = sum_n G[p][n] B~[n][r]
+    for (int e = tid; e < P * R; e += 256) {
+        const int p = e / R, r = e % R;
+        float acc = 0.0f;
+        for (int n = 0; n < N; ++n) acc += G[p * N + n] * sb[n * R + r];
+        w.lux[bh * P * R + e] = acc;
+    }
+    __syncthreads();
+    for (int i = tid; i < NH; i += 256) {
+        const float cs = sphi[0][i], sn = sphi[1][i];
+        float dphi = 0.0f;
+        for (int r = 0; r < R; ++r) {
+            const float d1 = sdb[i * R + r], d2 = sdb[(i + NH) * R + r];
+            dphi += d1 * sb[(i + NH) * R + r] - d2 * sb[i * R + r];
+            w.lub[(bh * N + i) * R + r] = d1 * cs - d2 * sn;          // R(+phi) dB~
+            w.lub[(bh * N + i + NH) * R + r] = d1 * sn + d2 * cs;
+        }
+        if (rot) w.seed[bh * NH + i] = (g.dangle_out ? g.dangle_out[bh * NH + i] : 0.0f) + dphi;
+    }
+}
+
+// The last token's dx and db terms of the outgoing last_u, added to the
+// gradients the main passes wrote (in their storage type).
+template <typename T, int N, int R>
+__global__ void __launch_bounds__(256) bwd_last_add_kernel(ScanLaunch a, BwdArgs g, BwdWs w) {
+    constexpr int P = kP;
+    const size_t bh = blockIdx.x;
+    const size_t H = a.heads, L = a.seq;
+    const size_t bb = bh / H, hh = bh % H;
+    const size_t tl = (bb * L + (L - 1)) * H + hh;
+    for (int e = threadIdx.x; e < P * R; e += 256)
+        stv<T>(g.dx, tl * P * R + e, ldv<T>(g.dx, tl * P * R + e) + w.lux[bh * P * R + e]);
+    for (int e = threadIdx.x; e < N * R; e += 256)
+        stv<T>(g.db, tl * N * R + e, ldv<T>(g.db, tl * N * R + e) + w.lub[bh * N * R + e]);
+}
+
 template <typename K>
 hipError_t set_lds(K kern, size_t bytes) {
     return hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -1155,7 +1260,7 @@ template <typename T, int N, int R, int RW>
 hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStream_t s) {
     const int nck = static_cast<int>((a.seq + RW / R - 1) / (RW / R));
     const size_t bh = a.batch * a.heads, bhk = bh * nck;
-    const BwdLayout l = bwd_layout(bh, nck, a.seq, N);
+    const BwdLayout l = bwd_layout(bh, nck, a.seq, N, R);
     BwdWs w;
     auto f = [base](size_t off) { return reinterpret_cast<float *>(base + off); };
     w.u = f(l.u);
@@ -1175,6 +1280,9 @@ hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStre
     w.pd = f(l.pd);
     w.pa = f(l.pa);
     w.pfirst = f(l.pfirst);
+    w.seed = f(l.seed);
+    w.lux = f(l.lux);
+    w.lub = f(l.lub);
 
     static_assert(sizeof(Smem<N, R, RW>) <= 160 * 1024, "chunk kernel LDS over 160 KB");
     const size_t lds = sizeof(Smem<N, R, RW>), uvlds = sizeof(UVSmem<N, R, RW>);
@@ -1183,22 +1291,35 @@ hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStre
     if (a1 != hipSuccess) return a1;
     if (a2 != hipSuccess) return a2;
     hipError_t e;
-    hipLaunchKernelGGL((bwd_uv_kernel<T, N, R, RW>), dim3(bhk), dim3(kUVThreads), uvlds, s, a, g,
+    BwdArgs gm = g;
+    if (g.dlast_u_out != nullptr) {
+        // the outgoing last_u's terms; its angle term seeds the angle passes
+        hipLaunchKernelGGL((bwd_last_u_kernel<T, N, R>), dim3(bh), dim3(256), 0, s, a, g, w);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (a.theta != nullptr) gm.dangle_out = w.seed;
+    }
+    const BwdArgs &g2 = gm;
+    hipLaunchKernelGGL((bwd_uv_kernel<T, N, R, RW>), dim3(bhk), dim3(kUVThreads), uvlds, s, a, g2,
                        w, nck);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_passes_kernel<N>), dim3(2 * bh * (N / 32)), dim3(256), 0, s, a, g, w,
+    hipLaunchKernelGGL((bwd_passes_kernel<N>), dim3(2 * bh * (N / 32)), dim3(256), 0, s, a, g2, w,
                        nck);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_chunk_kernel<T, N, R, RW>), dim3(bhk), dim3(kBT), lds, s, a, g, w, nck);
+    hipLaunchKernelGGL((bwd_chunk_kernel<T, N, R, RW>), dim3(bhk), dim3(kBT), lds, s, a, g2, w, nck);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (a.theta != nullptr) {
-        hipLaunchKernelGGL((bwd_angle_kernel<N>), dim3(bh), dim3(64), 0, s, a, g, w, nck);
+        hipLaunchKernelGGL((bwd_angle_kernel<N>), dim3(bh), dim3(64), 0, s, a, g2, w, nck);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((bwd_token_kernel<T, N, R, RW>), dim3(bhk), dim3(256), 0, s, a, g, w, nck);
+    hipLaunchKernelGGL((bwd_token_kernel<T, N, R, RW>), dim3(bhk), dim3(256), 0, s, a, g2, w, nck);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(bwd_head_kernel, dim3(a.heads), dim3(256), 0, s, a, g, w, nck);
-    return hipGetLastError();
+    hipLaunchKernelGGL(bwd_head_kernel, dim3(a.heads), dim3(256), 0, s, a, g2, w, nck);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (g.dlast_u_out != nullptr) {
+        hipLaunchKernelGGL((bwd_last_add_kernel<T, N, R>), dim3(bh), dim3(256), 0, s, a, g, w);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 template <typename T, int N64ROWS>
@@ -1226,7 +1347,7 @@ size_t scan_backward_workspace(const ScanLaunch &a) {
     if (!scan_backward_supported(a)) return 0;
     const size_t qt = static_cast<size_t>(scan_backward_rows(a)) / a.rank;
     const size_t nck = (a.seq + qt - 1) / qt;
-    return bwd_layout(a.batch * a.heads, nck, a.seq, a.d_state).total;
+    return bwd_layout(a.batch * a.heads, nck, a.seq, a.d_state, a.rank).total;
 }
 
 hipError_t launch_scan_backward(const ScanLaunch &a, const ScanGrads &gr, void *workspace,
@@ -1236,6 +1357,7 @@ hipError_t launch_scan_backward(const ScanLaunch &a, const ScanGrads &gr, void *
     g.dy = gr.dy;
     g.dh_out = gr.dh_out;
     g.dangle_out = gr.dangle_out;
+    g.dlast_u_out = gr.dlast_u_out;
     g.dx = gr.dx;
     g.db = gr.db;
     g.dc = gr.dc;

@@ -54,7 +54,8 @@ class ScanInputsC(C.Structure):
 class ScanGradsC(C.Structure):
     """m3_scan_grads (include/mamba3_ssm.h)."""
     _fields_ = [(n, _P) for n in ("dy", "dh", "dangle", "dx", "db", "dc", "ddt", "dlambda",
-                                  "da_log", "dtheta", "dd_skip", "dh0", "dlast_u0", "dangle0")]
+                                  "da_log", "dtheta", "dd_skip", "dh0", "dlast_u0", "dangle0",
+                                  "dlast_u")]
 
 
 class ScanOutputC(C.Structure):

@@ -182,12 +182,10 @@ class _ScanFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy, dh, dlu, dang):
         tensors = ctx.saved_tensors
-        if dlu is not None and bool(torch.any(dlu != 0)):
-            raise UnsupportedError("unsupported: a gradient through the output state's last_u")
         x = tensors[0]
         if dy is None:
             dy = torch.zeros_like(x)
-        g = mamba3_scan_backward(_inputs_of(ctx.cfg, *tensors), dy, dh, dang)
+        g = mamba3_scan_backward(_inputs_of(ctx.cfg, *tensors), dy, dh, dang, dlu)
         order = (g.x, g.b, g.c, g.dt, g.a_log, g.lam, g.theta, g.d_skip, g.h0, g.last_u0,
                  g.angle0)
         grads = [None if (t is None or gt is None) else gt.to(t.dtype).view_as(t)
@@ -212,30 +210,52 @@ class ScanGrads:
 
 
 def mamba3_scan_backward(inputs: ScanInputs, dy: torch.Tensor, dh: Optional[torch.Tensor] = None,
-                         dangle: Optional[torch.Tensor] = None) -> ScanGrads:
+                         dangle: Optional[torch.Tensor] = None,
+                         dlast_u: Optional[torch.Tensor] = None) -> ScanGrads:
     """Gradients of the scan's inputs for dL/dy = dy (and dL/d state.h, dL/d
-    state.angle of the output state), through m3_scan_backward."""
+    state.angle, dL/d state.last_u of the output state), through
+    m3_scan_backward.  Every tensor's shape is checked before any launch."""
     x = _dev(inputs.x, "x")
     if x.dim() != 5:
         raise RankError(5, x.dim(), x.shape)
     B, T, H, P, R = x.shape
+    if inputs.b.dim() != 5:
+        raise RankError(5, inputs.b.dim(), inputs.b.shape)
     N = inputs.b.shape[3]
     code = _dtype_code(x)
     b, c = _dev(inputs.b, "b"), _dev(inputs.c, "c")
     _expect_shape(b, (B, T, H, N, R), "b")
     _expect_shape(c, (B, T, H, N, R), "c")
     dt, lam, a_log = _f32(inputs.dt, "dt"), _f32(inputs.lam, "lambda"), _f32(inputs.a_log, "a_log")
+    _expect_shape(dt, (B, T, H), "dt")
+    _expect_shape(lam, (B, T, H), "lambda")
+    _expect_shape(a_log, (H,), "a_log")
     theta = None if inputs.theta is None else _dev(inputs.theta, "theta").to(x.dtype)
+    if theta is not None:
+        _expect_shape(theta, (B, T, H, N // 2), "theta")
     d_skip = _f32(inputs.d_skip, "d_skip")
+    if d_skip is not None:
+        _expect_shape(d_skip, (H,), "d_skip")
     dy = _dev(dy, "dy").to(x.dtype)
     _expect_shape(dy, (B, T, H, P, R), "dy")
     dh = _f32(dh, "dh")
+    if dh is not None:
+        _expect_shape(dh, (B, H, P, N), "dh")
+    dlast_u = _f32(dlast_u, "dlast_u")
+    if dlast_u is not None:
+        _expect_shape(dlast_u, (B, H, P, N), "dlast_u")
     dangle = _f32(dangle, "dangle") if theta is not None else None
+    if dangle is not None:
+        _expect_shape(dangle, (B, H, N // 2), "dangle")
     st = inputs.state
     st_c, h0, l0, a0 = None, None, None, None
     if st is not None:
         h0, l0 = _f32(st.h, "state.h"), _f32(st.last_u, "state.last_u")
+        _expect_shape(h0, (B, H, P, N), "state.h")
+        _expect_shape(l0, (B, H, P, N), "state.last_u")
         a0 = _f32(st.angle, "state.angle") if (st.angle is not None and theta is not None) else None
+        if a0 is not None:
+            _expect_shape(a0, (B, H, N // 2), "state.angle")
         st_c = _lib.SsmStateC(h0.data_ptr(), l0.data_ptr(), None if a0 is None else a0.data_ptr())
     cin = _lib.ScanInputsC(
         B, T, H, P, N, R, code, x.data_ptr(), b.data_ptr(), c.data_ptr(), dt.data_ptr(),
@@ -253,7 +273,7 @@ def mamba3_scan_backward(inputs: ScanInputs, dy: torch.Tensor, dh: Optional[torc
     gc = _lib.ScanGradsC(dy.data_ptr(), _ptr(dh), _ptr(dangle), g.x.data_ptr(), g.b.data_ptr(),
                          g.c.data_ptr(), g.dt.data_ptr(), g.lam.data_ptr(), g.a_log.data_ptr(),
                          _ptr(g.theta), _ptr(g.d_skip), _ptr(g.h0), _ptr(g.last_u0),
-                         _ptr(g.angle0))
+                         _ptr(g.angle0), _ptr(dlast_u))
     _lib.check(_lib.lib().m3_scan_backward(C.byref(cin), C.byref(gc), _stream(x)))
     return g
 
@@ -378,7 +398,10 @@ def _step_args(x, b, c, dt, lam, a_log, theta, d_skip):
         theta = _dev(theta, "theta")
         if theta.dtype != x.dtype:
             theta = theta.to(x.dtype)
+        _expect_shape(theta.reshape(-1), (B * H * (N // 2),), "theta")
     d_skip = _f32(d_skip, "d_skip")
+    if d_skip is not None:
+        _expect_shape(d_skip, (H,), "d_skip")
     keep = (x, b, c, dt, lam, a_log, theta, d_skip)
     args = _lib.StepInputsC(B, H, P, N, R, code, x.data_ptr(), b.data_ptr(), c.data_ptr(),
                             dt.data_ptr(), lam.data_ptr(), a_log.data_ptr(),

@@ -55,6 +55,8 @@ def _run(case, upstream=True):
     dh = (rng.standard_normal((B, H, P, N)) * 0.1).astype(np.float32) if (state and upstream) else None
     dang = (rng.standard_normal((B, H, N // 2)) * 0.1).astype(np.float32) \
         if (state and theta and upstream) else None
+    # dL/d(output last_u): flows into x, b and the last token's angle
+    dlu = (rng.standard_normal((B, H, P, N)) * 0.1).astype(np.float32) if upstream else None
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     si = ScanInputs(dev(inp["x"], tdt), dev(inp["b"], tdt), dev(inp["c"], tdt), dev(inp["dt"]),
                     dev(inp["a_log"]), dev(inp["lam"]))
@@ -66,13 +68,14 @@ def _run(case, upstream=True):
         si = si.with_state(SsmState(dev(inp["h0"]), dev(inp["last_u0"]),
                                     dev(inp["angle0"]) if theta else None))
     g = mamba3_scan_backward(si, dev(dy, tdt), None if dh is None else dev(dh),
-                             None if dang is None else dev(dang))
+                             None if dang is None else dev(dang),
+                             None if dlu is None else dev(dlu))
     torch.cuda.synchronize()
     ref = oracle.scan_backward_f64(
         inp["x"], inp["b"], inp["c"], inp["dt"], inp["a_log"], inp["lam"], dy,
         inp["theta"] if theta else None, d_skip, inp.get("h0") if state else None,
         inp.get("last_u0") if state else None, inp.get("angle0") if (state and theta) else None,
-        dh, None, dang)
+        dh, dlu, dang)
     return g, ref
 
 
@@ -135,6 +138,92 @@ def test_autograd_node_matches_the_direct_backward():
                     ("lam", g.lam), ("theta", g.theta)):
         assert rel_l2(host(ts[k].grad), host(mine)) <= 1e-6, k
     assert rel_l2(host(d_skip.grad), host(g.d_skip)) <= 1e-6
+
+
+@pytest.mark.parametrize("dtype,R,rot", [("f32", 1, True), ("f32", 2, False), ("bf16", 1, True),
+                                         ("bf16", 4, True)])
+def test_two_windows_chained_through_the_state(dtype, R, rot):
+    """Two windows joined through SsmState (the second starts from the first's
+    h, last_u and angle), differentiated end to end by autograd: the
+    gradients equal those of the single window over the whole sequence.  The
+    first window's output last_u reaches the loss only through the second
+    window's carried state S = h + (1 - lambda_0) dt_0 last_u, so this needs
+    the last_u adjoint (scan.rs:521-535, 599-618)."""
+    from mamba3.ssm import ScanInputs, SsmState, mamba3_scan, mamba3_scan_backward
+    rng = np.random.default_rng(11 + R)
+    B, T, H, P, N, cut = 1, 150, 2, 64, 64, 70
+    inp = baseline_inputs(rng, B, T, H, P, N, R, theta=rot, dtype=dtype, theta_per_head=False)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    keys = ("x", "b", "c", "dt", "lam") + (("theta",) if rot else ())
+    full = {k: dev(inp[k], tdt if k in ("x", "b", "c", "theta") else torch.float32) for k in keys}
+    a_log = dev(inp["a_log"])
+    w = dev(rng.standard_normal((B, T, H, P, R)).astype(np.float32), tdt)
+    wh = dev(rng.standard_normal((B, H, P, N)).astype(np.float32) * 0.1)
+    parts = [{k: full[k][:, s].clone().requires_grad_(True) for k in keys}
+             for s in (slice(0, cut), slice(cut, T))]
+    al = a_log.clone().requires_grad_(True)
+
+    def inputs(d):
+        si = ScanInputs(d["x"], d["b"], d["c"], d["dt"], al, d["lam"])
+        return si.with_theta(d["theta"]) if rot else si
+
+    o1 = mamba3_scan(inputs(parts[0]))
+    o2 = mamba3_scan(inputs(parts[1]).with_state(o1.state))
+    loss = ((o1.y.float() * w[:, :cut].float()).sum() + (o2.y.float() * w[:, cut:].float()).sum()
+            + (o2.state.h * wh).sum())
+    loss.backward()
+    with torch.no_grad():
+        si = ScanInputs(full["x"], full["b"], full["c"], full["dt"], a_log, full["lam"])
+        if rot:
+            si = si.with_theta(full["theta"])
+        g = mamba3_scan_backward(si, w, wh)
+    tol = BF16_TOL if dtype == "bf16" else 1e-4
+    for k in keys:
+        joined = torch.cat([parts[0][k].grad.float(), parts[1][k].grad.float()], dim=1)
+        err = rel_l2(host(joined), host(getattr(g, k if k != "lam" else "lam")))
+        assert err <= tol, (k, err)
+    assert rel_l2(host(al.grad), host(g.a_log)) <= tol
+
+
+@pytest.mark.parametrize("what", ["dt", "lam", "a_log", "theta", "d_skip", "dh", "dangle",
+                                  "dlast_u", "state.h", "state.angle"])
+def test_backward_rejects_mis_shaped_tensors_before_any_launch(what):
+    """mamba3_scan_backward checks every tensor's shape on the host: a wrong
+    one raises ShapeError and no kernel runs."""
+    from mamba3 import ShapeError, _lib
+    from mamba3.ssm import ScanInputs, SsmState, mamba3_scan_backward
+    B, T, H, P, N = 1, 40, 2, 64, 64
+    t = lambda *s: torch.zeros(s, device="cuda")
+    ok = dict(dt=t(B, T, H), lam=t(B, T, H), a_log=t(H), theta=t(B, T, H, N // 2), d_skip=t(H),
+              dh=t(B, H, P, N), dangle=t(B, H, N // 2), dlast_u=t(B, H, P, N),
+              h=t(B, H, P, N), angle=t(B, H, N // 2))
+    bad = {"dt": t(B, T + 1, H), "lam": t(B, T, H + 1), "a_log": t(H + 1),
+           "theta": t(B, T, H, N // 2 - 1), "d_skip": t(1), "dh": t(B, H, P, N - 1),
+           "dangle": t(B, H, N), "dlast_u": t(B, H, P + 1, N), "state.h": t(B, H, P, N + 2),
+           "state.angle": t(B, H, 3)}[what]
+    k = what.split(".")[-1]
+    args = dict(ok)
+    args["h" if what == "state.h" else ("angle" if what == "state.angle" else k)] = bad
+    si = (ScanInputs(t(B, T, H, P, 1), t(B, T, H, N, 1), t(B, T, H, N, 1), args["dt"],
+                     args["a_log"], args["lam"]).with_theta(args["theta"]).with_skip(args["d_skip"])
+          .with_state(SsmState(args["h"], t(B, H, P, N), args["angle"])))
+    before = _lib.lib().m3_launch_count()
+    with pytest.raises(ShapeError, match=what.split(".")[-1] if what != "lam" else "lambda"):
+        mamba3_scan_backward(si, t(B, T, H, P, 1), args["dh"], args["dangle"], args["dlast_u"])
+    assert _lib.lib().m3_launch_count() == before
+
+
+def test_step_rejects_mis_shaped_theta_and_skip():
+    from mamba3 import ShapeError
+    from mamba3.ssm import SsmState, mamba3_step_
+    B, H, P, N = 2, 3, 64, 64
+    t = lambda *s: torch.zeros(s, device="cuda")
+    st = SsmState(t(B, H, P, N), t(B, H, P, N), t(B, H, N // 2))
+    x, b = t(B, H, P, 1), t(B, H, N, 1)
+    with pytest.raises(ShapeError, match="theta"):
+        mamba3_step_(x, b, b, t(B, H), t(B, H), t(H), t(B, H, N // 2 + 1), None, st)
+    with pytest.raises(ShapeError, match="d_skip"):
+        mamba3_step_(x, b, b, t(B, H), t(B, H), t(H), t(B, H, N // 2), t(H + 1), st)
 
 
 def test_config1_shape_two_heads_full_length():
