@@ -14,6 +14,10 @@
  *                                                         src/models/hybrid.rs:446-456
  *   m3_mixer_prologue           Mamba3Mixer::project after in_proj
  *                                                         src/models/mamba3.rs:376-466
+ *   m3_mixer_prologue_conv      the same with the causal convolution and its history
+ *                                                         src/models/mamba3.rs:386-400,
+ *                                                         src/nn/conv.rs:143-225,
+ *                                                         src/tensor/ops/fused.rs:780-865
  *   m3_mixer_gate               Mamba3Mixer::finish before out_proj
  *                                                         src/models/mamba3.rs:468-477
  *   m3_embedding_lookup         Embedding::lookup         src/nn/embedding.rs
@@ -86,6 +90,35 @@ m3_status m3_mixer_prologue(const m3_mixer_dims *d, const void *projected, const
                             const float *b_bias, const float *c_bias, const float *bc_norm,
                             void *x, void *b, void *c, float *dt, float *lambda, void *theta,
                             void *stream);
+
+/* The depthwise causal convolution of a mixer with conv_kernel = k
+ * (CausalConv1d, src/nn/conv.rs:60-225) over the channels [x | B | C] of the
+ * projection, channels = d_inner + 2 * G * N * R.  With the window
+ * w = history ++ input along the sequence (history: the k-1 positions before
+ * it), out[s, ch] = bias[ch] + sum_j weight[j, ch] * w[s + j, ch]
+ * (src/tensor/ops/fused.rs:780-832): tap j multiplies the input delayed by
+ * k-1-j positions.  The new history is the window's last k-1 positions
+ * (fused.rs:833-865). */
+typedef struct m3_conv1d {
+    size_t kernel_size;        /* k >= 2 */
+    size_t seq_len;            /* positions per sequence: tokens = batch * seq_len */
+    const float *weight;       /* [k, channels] f32 */
+    const float *bias;         /* [channels] f32, or NULL (no bias) */
+    const void *history;       /* bf16 [batch, k-1, channels], or NULL (zeros) */
+    void *new_history;         /* bf16 [batch, k-1, channels], or NULL (not written) */
+} m3_conv1d;
+
+/* Mamba3Mixer::project with the convolution (src/models/mamba3.rs:386-400):
+ * m3_mixer_prologue with x, B and C taken from the convolution's output
+ * before the silu.  conv NULL is m3_mixer_prologue.  new_history may equal
+ * history when seq_len is 1 (the decode step updates its cache in place);
+ * otherwise the two must not overlap (the history is read by other
+ * positions' workgroups while the new one is written). */
+m3_status m3_mixer_prologue_conv(const m3_mixer_dims *d, const m3_conv1d *conv,
+                                 const void *projected, const float *dt_bias,
+                                 const float *b_bias, const float *c_bias, const float *bc_norm,
+                                 void *x, void *b, void *c, float *dt, float *lambda, void *theta,
+                                 void *stream);
 
 /* out[t] = [RMSNorm(y[t]) * norm_weight] * silu(z[t]) over rows of d_inner;
  * z rows are z_stride elements apart (the z piece of the projection);

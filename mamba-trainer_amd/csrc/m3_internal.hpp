@@ -109,6 +109,13 @@ struct PrologueLaunch {
     void *x, *b, *c;                // bf16 [tokens, H, P, R], [tokens, H, N, R] x2
     float *dt, *lambda;             // [tokens, H]
     void *theta;                    // bf16 [tokens, H, N/2] (has_theta)
+    // Causal convolution over [x | B | C] (conv_k 0: none).  Token t is
+    // position t % seq_len of sequence t / seq_len.
+    size_t conv_k, seq_len;
+    const float *conv_w;            // [conv_k, channels]
+    const float *conv_b;            // [channels] or null
+    const void *hist;               // bf16 [batch, conv_k-1, channels] or null (zeros)
+    void *new_hist;                 // bf16 [batch, conv_k-1, channels] or null
 };
 hipError_t launch_mixer_prologue(const PrologueLaunch &a, hipStream_t s);
 // out = [RMSNorm(y)] * silu(z), rows of d_inner.

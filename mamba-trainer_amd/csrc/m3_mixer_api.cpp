@@ -87,10 +87,28 @@ size_t m3_mixer_in_proj_width(const m3_mixer_dims *d) {
            (d->dynamics == M3_ROTATIONAL ? d->heads * d->d_state / 2 : 0);
 }
 
+namespace {
+
+bool ranges_overlap(const void *p, const void *q, size_t bytes) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
+    return a < b + bytes && b < a + bytes;
+}
+
+}  // namespace
+
 m3_status m3_mixer_prologue(const m3_mixer_dims *d, const void *projected, const float *dt_bias,
                             const float *b_bias, const float *c_bias, const float *bc_norm,
                             void *x, void *b, void *c, float *dt, float *lambda, void *theta,
                             void *stream) {
+    return m3_mixer_prologue_conv(d, nullptr, projected, dt_bias, b_bias, c_bias, bc_norm, x, b, c,
+                                  dt, lambda, theta, stream);
+}
+
+m3_status m3_mixer_prologue_conv(const m3_mixer_dims *d, const m3_conv1d *conv,
+                                 const void *projected, const float *dt_bias,
+                                 const float *b_bias, const float *c_bias, const float *bc_norm,
+                                 void *x, void *b, void *c, float *dt, float *lambda, void *theta,
+                                 void *stream) {
     if (d == nullptr) return m3::api_fail(M3_ERR_ARGUMENT, "mixer dims are NULL");
     if (d->heads == 0 || d->head_dim == 0 || d->d_state == 0 || d->rank == 0 || d->groups == 0)
         return m3::api_fail(M3_ERR_CONFIG, "heads, head_dim, d_state, rank and groups must be positive");
@@ -101,6 +119,24 @@ m3_status m3_mixer_prologue(const m3_mixer_dims *d, const void *projected, const
     if (rot && d->d_state % 2 != 0)
         return m3::api_fail(M3_ERR_CONFIG, "rotational dynamics need an even d_state, got %zu",
                             d->d_state);
+    if (conv != nullptr) {
+        if (conv->kernel_size < 2)   // config.rs:237-243
+            return m3::api_fail(M3_ERR_CONFIG, "conv_kernel must be at least 2, got %zu",
+                                conv->kernel_size);
+        if (conv->seq_len == 0 || d->tokens % conv->seq_len != 0)
+            return m3::api_fail(M3_ERR_SHAPE, "tokens (%zu) must be a whole number of sequences "
+                                "of seq_len %zu", d->tokens, conv->seq_len);
+        if (conv->weight == nullptr)
+            return m3::api_fail(M3_ERR_ARGUMENT, "convolution weight is NULL");
+        const size_t channels = d->heads * d->head_dim * d->rank + 2 * d->groups * d->d_state * d->rank;
+        const size_t hist_bytes = (d->tokens / conv->seq_len) * (conv->kernel_size - 1) * channels * 2;
+        if (conv->history != nullptr && conv->new_history != nullptr &&
+            ranges_overlap(conv->history, conv->new_history, hist_bytes) &&
+            !(conv->history == conv->new_history && conv->seq_len == 1))
+            return m3::api_fail(M3_ERR_ARGUMENT, "the new convolution history may overlap the "
+                                "history only as the same buffer with seq_len 1, got seq_len %zu",
+                                conv->seq_len);
+    }
     if (d->tokens == 0) return m3::api_ok();
     if (projected == nullptr || dt_bias == nullptr || x == nullptr || b == nullptr || c == nullptr ||
         dt == nullptr || lambda == nullptr || (rot && theta == nullptr))
@@ -132,6 +168,14 @@ m3_status m3_mixer_prologue(const m3_mixer_dims *d, const void *projected, const
     a.dt = dt;
     a.lambda = lambda;
     a.theta = theta;
+    if (conv != nullptr) {
+        a.conv_k = conv->kernel_size;
+        a.seq_len = conv->seq_len;
+        a.conv_w = conv->weight;
+        a.conv_b = conv->bias;
+        a.hist = conv->history;
+        a.new_hist = conv->new_history;
+    }
     return launched(m3::launch_mixer_prologue(a, as_stream(stream)), "prologue launch");
 }
 

@@ -96,20 +96,76 @@ quantize_columns_kernel(size_t k, size_t n, const float *w, uint16_t *codes, flo
     }
 }
 
+// ---------------------------------------------------------------- convolution
+// The causal convolution over [x | B | C] (nn/conv.rs:60-225, fused.rs:780-865)
+// is computed where the prologue reads those channels: a token's workgroup
+// reads the k rows ending at its own (its neighbours' rows, fetched by the
+// neighbouring workgroups, come from L2), or the history for positions before
+// the sequence start.  out[s, ch] = bias[ch] + sum_j w[j][ch] * in(s-(k-1)+j).
+// The workgroup of a sequence's last position writes the new history, the
+// last k-1 positions of history ++ input, after a barrier that ends every read
+// of the old history in the workgroup: with one position per sequence that is
+// every reader, so the history may be updated in place (the host allows
+// aliasing only then).  Each channel's k-1 positions are copied by one thread
+// in ascending order, which never reads a position it has already written.
+__device__ __forceinline__ float xbc_at(const PrologueLaunch &a, const uint16_t *xbc_t, size_t s,
+                                        size_t seqi, size_t C, size_t ch) {
+    if (a.conv_k == 0) return bf(xbc_t, ch);
+    const size_t k = a.conv_k;
+    const uint16_t *hist = static_cast<const uint16_t *>(a.hist);
+    float acc = a.conv_b ? a.conv_b[ch] : 0.0f;
+    for (size_t j = 0; j < k; ++j) {
+        const size_t back = k - 1 - j;                     // delay of tap j
+        float v = 0.0f;
+        if (back <= s) v = bf(xbc_t - back * a.width, ch);
+        else if (hist) v = bf(hist, (seqi * (k - 1) + (k - 1 + s - back)) * C + ch);
+        acc += a.conv_w[j * C + ch] * v;
+    }
+    return acc;
+}
+
+// The new history of sequence seqi, written by its last position's workgroup
+// (xbc_t is that position's [x | B | C]); `vec` moves 16-byte vectors.
+__device__ void write_history(const PrologueLaunch &a, const uint16_t *xbc_t, size_t seqi,
+                              size_t C, bool vec) {
+    __syncthreads();
+    const size_t k = a.conv_k, T = a.seq_len;
+    const uint16_t *hist = static_cast<const uint16_t *>(a.hist);
+    uint16_t *nh = static_cast<uint16_t *>(a.new_hist) + seqi * (k - 1) * C;
+    const uint16_t *oh = hist ? hist + seqi * (k - 1) * C : nullptr;
+    const size_t step = vec ? 8 : 1;
+    for (size_t ch = threadIdx.x * step; ch < C; ch += 256 * step) {
+        for (size_t i = 0; i + 1 < k; ++i) {
+            const size_t w = T + i;                        // window position
+            const uint16_t *src = w < k - 1 ? (oh ? oh + w * C + ch : nullptr)
+                                            : xbc_t - (T - 1 - (w - (k - 1))) * a.width + ch;
+            if (vec) {
+                const uint4 v = src ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
+                *reinterpret_cast<uint4 *>(nh + i * C + ch) = v;
+            } else {
+                nh[i * C + ch] = src ? *src : uint16_t(0);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- prologue
 // One workgroup per token.  The projection row is
 //   [z | x | B | C | dt | lambda? | theta?]  (mamba3.rs:356-381)
 // of widths d_inner, d_inner, G*R*N, G*R*N, H, H, H*N/2.  x, B and C pass
-// through silu (mamba3.rs:396); B and C are broadcast from groups to heads
-// (405-415), take the head's bias (418-423) and the RMSNorm over the state axis
-// (424-427), and go out rank-last (429-431).  dt = softplus(dt + dt_bias)
-// (435-438), lambda = sigmoid(lambda) or the fixed value (440-453).
+// through the convolution when there is one and then silu (mamba3.rs:386-396);
+// B and C are broadcast from groups to heads (405-415), take the head's bias
+// (418-423) and the RMSNorm over the state axis (424-427), and go out rank-last
+// (429-431).  dt = softplus(dt + dt_bias) (435-438), lambda = sigmoid(lambda)
+// or the fixed value (440-453).
 __global__ void __launch_bounds__(256)
 mixer_prologue_kernel(PrologueLaunch a) {
     const size_t t = blockIdx.x;
     const int tid = threadIdx.x;
     const size_t H = a.heads, P = a.head_dim, N = a.d_state, R = a.rank, G = a.groups;
     const size_t din = H * P * R, bcw = G * R * N;
+    const size_t C = din + 2 * bcw;
+    const size_t pos = a.conv_k ? t % a.seq_len : 0, seqi = a.conv_k ? t / a.seq_len : 0;
     const uint16_t *row = static_cast<const uint16_t *>(a.projected) + t * a.width;
     const uint16_t *px = row + din;
     const uint16_t *pb = px + din;
@@ -119,7 +175,7 @@ mixer_prologue_kernel(PrologueLaunch a) {
     const uint16_t *pth = plam + (a.learned_lambda ? H : 0);
 
     uint16_t *xo = static_cast<uint16_t *>(a.x) + t * din;
-    for (size_t i = tid; i < din; i += 256) xo[i] = to_bits(siluf_(bf(px, i)));
+    for (size_t i = tid; i < din; i += 256) xo[i] = to_bits(siluf_(xbc_at(a, px, pos, seqi, C, i)));
     if (a.has_theta) {
         uint16_t *to = static_cast<uint16_t *>(a.theta) + t * H * (N / 2);
         for (size_t i = tid; i < H * (N / 2); i += 256) to[i] = pth[i];
@@ -140,23 +196,24 @@ mixer_prologue_kernel(PrologueLaunch a) {
         for (size_t rr = tid >> 4; rr < ((nrows + 15) / 16) * 16; rr += 16) {
             const bool live = rr < nrows;
             const size_t h = live ? rr / R : 0, r = live ? rr % R : 0;
-            const uint16_t *s = src + ((h / per_group) * R + r) * N;
+            const size_t ch0 = static_cast<size_t>(src - px) + ((h / per_group) * R + r) * N;
             float ss = 0.0f;
             for (size_t n = sub; live && n < N; n += 16) {
-                float v = siluf_(bf(s, n));
+                float v = siluf_(xbc_at(a, px, pos, seqi, C, ch0 + n));
                 if (bias) v += bias[h * N + n];
                 ss += v * v;
             }
             ss = group_sum(ss, 16);
             const float scale = a.bc_norm ? 1.0f / sqrtf(ss / static_cast<float>(N) + a.norm_eps) : 1.0f;
             for (size_t n = sub; live && n < N; n += 16) {
-                float v = siluf_(bf(s, n));
+                float v = siluf_(xbc_at(a, px, pos, seqi, C, ch0 + n));
                 if (bias) v += bias[h * N + n];
                 if (a.bc_norm) v = v * scale * a.bc_norm[n];
                 dst[(h * N + n) * R + r] = to_bits(v);
             }
         }
     }
+    if (a.conv_k && a.new_hist && pos + 1 == a.seq_len) write_history(a, px, seqi, C, false);
 }
 
 // ---------------------------------------------------------------- prologue, 16-byte path
@@ -194,7 +251,43 @@ __device__ __forceinline__ unsigned int pack2(float a, float b) {
     return static_cast<unsigned int>(to_bits(a)) | (static_cast<unsigned int>(to_bits(b)) << 16);
 }
 
-template <int R>
+// Eight channels ch..ch+7 of [x | B | C] at a token (xbc_t its row's [x | B |
+// C]), through the convolution when CONV (see xbc_at).  The branch on the
+// position is uniform over the workgroup.
+template <bool CONV>
+__device__ __forceinline__ void xbc8(const PrologueLaunch &a, const uint16_t *xbc_t, size_t s,
+                                     size_t seqi, size_t C, size_t ch, float *f) {
+    if (!CONV) {
+        unpack8(*reinterpret_cast<const uint4 *>(xbc_t + ch), f);
+        return;
+    }
+    const size_t k = a.conv_k;
+    const uint16_t *hist = static_cast<const uint16_t *>(a.hist);
+    if (a.conv_b) {
+        const float4 b0 = *reinterpret_cast<const float4 *>(a.conv_b + ch);
+        const float4 b1 = *reinterpret_cast<const float4 *>(a.conv_b + ch + 4);
+        f[0] = b0.x; f[1] = b0.y; f[2] = b0.z; f[3] = b0.w;
+        f[4] = b1.x; f[5] = b1.y; f[6] = b1.z; f[7] = b1.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = 0.0f;
+    }
+    for (size_t j = 0; j < k; ++j) {
+        const size_t back = k - 1 - j;
+        const uint16_t *src = back <= s ? xbc_t - back * a.width + ch
+                            : hist ? hist + (seqi * (k - 1) + (k - 1 + s - back)) * C + ch : nullptr;
+        if (src == nullptr) continue;
+        float v[8];
+        unpack8(*reinterpret_cast<const uint4 *>(src), v);
+        const float4 w0 = *reinterpret_cast<const float4 *>(a.conv_w + j * C + ch);
+        const float4 w1 = *reinterpret_cast<const float4 *>(a.conv_w + j * C + ch + 4);
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] += w[e] * v[e];
+    }
+}
+
+template <int R, bool CONV>
 __global__ void __launch_bounds__(256)
 mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
     const size_t t = blockIdx.x;
@@ -202,6 +295,8 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
     const int H = static_cast<int>(a.heads), N = static_cast<int>(a.d_state);
     const int din = static_cast<int>(a.heads * a.head_dim) * R;
     const int bcw = static_cast<int>(a.groups) * R * N;
+    const size_t C = static_cast<size_t>(din) + 2 * static_cast<size_t>(bcw);
+    const size_t pos = CONV ? t % a.seq_len : 0, seqi = CONV ? t / a.seq_len : 0;
     const int per_group = H / static_cast<int>(a.groups);
     const uint16_t *__restrict__ row = static_cast<const uint16_t *>(a.projected) + t * a.width;
     const uint16_t *px = row + din;
@@ -222,9 +317,10 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
             const int h = u - which * H;
             const uint16_t *s = (which ? pc : pb) + (h / per_group) * R * N + q * 8;
             const float *bias = which ? a.c_bias : a.b_bias;
+            const size_t ch0 = static_cast<size_t>(s - px);
             float v[R][8];
 #pragma unroll
-            for (int r = 0; r < R; ++r) unpack8(*reinterpret_cast<const uint4 *>(s + r * N), v[r]);
+            for (int r = 0; r < R; ++r) xbc8<CONV>(a, px, pos, seqi, C, ch0 + r * N, v[r]);
             float bb[8];
             if (bias) {
                 const float4 b0 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8);
@@ -266,7 +362,7 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
         } else if (i < nbc + nx) {
             const int k = i - nbc;
             float f[8];
-            unpack8(*reinterpret_cast<const uint4 *>(px + k * 8), f);
+            xbc8<CONV>(a, px, pos, seqi, C, static_cast<size_t>(k) * 8, f);
             uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.x) + t * din) + k;
             *dst = make_uint4(pack2(silu_fast(f[0]), silu_fast(f[1])), pack2(silu_fast(f[2]), silu_fast(f[3])),
                               pack2(silu_fast(f[4]), silu_fast(f[5])), pack2(silu_fast(f[6]), silu_fast(f[7])));
@@ -280,6 +376,7 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
         a.dt[t * H + h] = softplusf_(bf(pdt, h) + a.dt_bias[h]);
         a.lambda[t * H + h] = a.learned_lambda ? sigmoidf_(bf(plam, h)) : a.fixed_lambda;
     }
+    if (CONV && a.new_hist && pos + 1 == a.seq_len) write_history(a, px, seqi, C, true);
 }
 
 // ---------------------------------------------------------------- gate
@@ -404,16 +501,27 @@ hipError_t launch_mixer_prologue(const PrologueLaunch &a, hipStream_t s) {
                      a.width % 8 == 0 && (a.rank == 1 || a.rank == 2 || a.rank == 4) &&
                      aligned16(a.projected) && aligned16(a.x) && aligned16(a.b) && aligned16(a.c) &&
                      aligned16(a.b_bias) && aligned16(a.c_bias) && aligned16(a.bc_norm) &&
-                     aligned16(a.theta) && a.width < (1u << 30);
+                     aligned16(a.theta) && a.width < (1u << 30) && aligned16(a.conv_w) &&
+                     aligned16(a.conv_b) && aligned16(a.hist) && aligned16(a.new_hist);
     if (!vec) {
         hipLaunchKernelGGL(mixer_prologue_kernel, grid, dim3(256), 0, s, a);
         return hipGetLastError();
     }
     const int l = static_cast<int>(lq);
+    const bool conv = a.conv_k != 0;
     switch (a.rank) {
-    case 1: hipLaunchKernelGGL(mixer_prologue_vec_kernel<1>, grid, dim3(256), 0, s, a, l); break;
-    case 2: hipLaunchKernelGGL(mixer_prologue_vec_kernel<2>, grid, dim3(256), 0, s, a, l); break;
-    default: hipLaunchKernelGGL(mixer_prologue_vec_kernel<4>, grid, dim3(256), 0, s, a, l); break;
+    case 1:
+        if (conv) hipLaunchKernelGGL((mixer_prologue_vec_kernel<1, true>), grid, dim3(256), 0, s, a, l);
+        else hipLaunchKernelGGL((mixer_prologue_vec_kernel<1, false>), grid, dim3(256), 0, s, a, l);
+        break;
+    case 2:
+        if (conv) hipLaunchKernelGGL((mixer_prologue_vec_kernel<2, true>), grid, dim3(256), 0, s, a, l);
+        else hipLaunchKernelGGL((mixer_prologue_vec_kernel<2, false>), grid, dim3(256), 0, s, a, l);
+        break;
+    default:
+        if (conv) hipLaunchKernelGGL((mixer_prologue_vec_kernel<4, true>), grid, dim3(256), 0, s, a, l);
+        else hipLaunchKernelGGL((mixer_prologue_vec_kernel<4, false>), grid, dim3(256), 0, s, a, l);
+        break;
     }
     return hipGetLastError();
 }

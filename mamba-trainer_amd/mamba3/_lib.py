@@ -88,6 +88,12 @@ class MixerDimsC(C.Structure):
                 ("norm_eps", C.c_float)]
 
 
+class Conv1dC(C.Structure):
+    """m3_conv1d (mamba3_mixer.h)."""
+    _fields_ = [("kernel_size", _Z), ("seq_len", _Z), ("weight", _P), ("bias", _P),
+                ("history", _P), ("new_history", _P)]
+
+
 SIGNATURES = {
     "m3_config_default": (C.c_int, [C.POINTER(SsmConfigC)]),
     "m3_config_validate": (C.c_int, [C.POINTER(SsmConfigC)]),
@@ -115,6 +121,7 @@ SIGNATURES = {
     "m3_linear": (C.c_int, [_Z, _Z, _Z, _P, _P, _P, _P, _P, _P, _Z, _P]),
     "m3_mixer_in_proj_width": (_Z, [C.POINTER(MixerDimsC)]),
     "m3_mixer_prologue": (C.c_int, [C.POINTER(MixerDimsC)] + [_P] * 12),
+    "m3_mixer_prologue_conv": (C.c_int, [C.POINTER(MixerDimsC), C.POINTER(Conv1dC)] + [_P] * 12),
     "m3_mixer_gate": (C.c_int, [_Z, _Z, _P, _P, _Z, _P, C.c_float, _P, _P]),
     "m3_embedding_lookup": (C.c_int, [_Z, _Z, _P, _Z, _P, _P, _P]),
     # mamba3_checkpoint.h

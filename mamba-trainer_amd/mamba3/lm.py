@@ -144,16 +144,17 @@ class DecodeGraph:
     sends the step's ~150 kernels to the GPU as one graph launch, with none of
     the host work of issuing them one by one.
 
-    Capture records the cache's buffers: replays read and update those same
-    tensors, so the cache must stay alive and keep its storage.  The warm-up
-    before capture runs on copies of the states (it settles the GEMM plans,
-    whose first call times candidates and blocks, which capture forbids), so
-    capturing does not advance the caller's states."""
+    Capture records the cache's buffers (states and convolution histories):
+    replays read and update those same tensors, so the cache must stay alive
+    and keep its storage.  The warm-up before capture runs on copies of the
+    cache (it settles the GEMM plans, whose first call times candidates and
+    blocks, which capture forbids), so capturing does not advance the
+    caller's states."""
 
     def __init__(self, lm: Mamba3Lm, cache: List[MixerCache], batch: int):
         dev = cache[0].ssm.h.device
         self.ids = torch.zeros((batch, 1), dtype=torch.int64, device=dev)
-        scratch = [MixerCache(c.ssm.clone()) for c in cache]
+        scratch = [c.clone() for c in cache]
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):

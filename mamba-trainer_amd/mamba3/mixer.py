@@ -4,11 +4,11 @@ Mirrors `Mamba3Mixer` (BectorVoom/mamba-trainer src/models/mamba3.rs):
 init (168-266), project (350-466), finish (468-477), apply / apply_with_state
 (479-567) and step (569-630).  The projections are hipBLASLt GEMMs with the
 int8 per-output-channel weight grid applied in their epilogue; the prologue
-(split, silu, B/C bias + RMSNorm, softplus, sigmoid), the scan or the decode
-step, and the gate are the library's own gfx950 kernels.
+(split, the causal convolution over [x | B | C] with its history, silu, B/C
+bias + RMSNorm, softplus, sigmoid), the scan or the decode step, and the gate
+are the library's own gfx950 kernels.
 
-Not covered (raise UnsupportedError): the causal convolution (conv_kernel),
-the bidirectional form and LoRA adapters.
+Not covered (raise UnsupportedError): the bidirectional form and LoRA adapters.
 """
 from __future__ import annotations
 
@@ -27,8 +27,14 @@ from .ssm import ScanInputs, SsmConfig, SsmState, StateDynamics, mamba3_scan, ma
 
 @dataclasses.dataclass
 class MixerCache:
-    """mamba3.rs:35-70 (no convolution history: conv_kernel is None)."""
+    """mamba3.rs:35-70: the scan state and, for a mixer with a convolution,
+    its history, the last conv_kernel-1 convolution inputs [B, k-1, channels]
+    (bf16, copies of projection values)."""
     ssm: SsmState
+    conv: Optional[torch.Tensor] = None
+
+    def clone(self) -> "MixerCache":
+        return MixerCache(self.ssm.clone(), None if self.conv is None else self.conv.clone())
 
 
 @dataclasses.dataclass
@@ -52,9 +58,6 @@ class Mamba3Mixer:
         """Mamba3MixerConfig::init (mamba3.rs:168-266), parameters drawn as there
         from a torch generator (the reference's ChaCha stream is not reproduced)."""
         cfg.validate()
-        if cfg.conv_kernel is not None:
-            raise UnsupportedError("unsupported: the causal convolution (conv_kernel) is not on "
-                                   "the gfx950 path; use conv_kernel=None")
         if cfg.bias:
             raise UnsupportedError("unsupported: projection biases are not on the gfx950 path")
         self.cfg = cfg
@@ -63,6 +66,16 @@ class Mamba3Mixer:
                               int8_weights=int8_weights)
         self.out_proj = Linear(residual_scaled((cfg.d_inner(), cfg.d_model), 0.02, n_layers,
                                                device, gen), int8_weights=int8_weights)
+        # CausalConv1dConfig::new(d_inner + 2 bc_width, k).init (mamba3.rs:205, 228-230;
+        # nn/conv.rs:60-110): weight [k, channels] KaimingUniform with fan_in k
+        # (bound sqrt(3 / k), nn/init.rs:82-93), bias zeros.
+        self.conv_weight = self.conv_bias = None
+        if cfg.conv_kernel is not None:
+            k, ch = cfg.conv_kernel, self.conv_channels()
+            bound = math.sqrt(3.0 / k)
+            self.conv_weight = ((torch.rand((k, ch), generator=gen, device=device) * 2.0 - 1.0)
+                                * bound).float().contiguous()
+            self.conv_bias = torch.zeros(ch, device=device)
         # dt_bias: softplus(dt_bias) log-uniform over [dt_min, dt_max] (mamba3.rs:198-209)
         u = torch.rand(H, generator=gen, device=device)
         dt = torch.exp(math.log(cfg.dt_min) + u * (math.log(cfg.dt_max) - math.log(cfg.dt_min)))
@@ -80,8 +93,11 @@ class Mamba3Mixer:
 
     def named_parameters(self):
         """mamba3.rs:634-656: the reference's visit order and paths."""
-        out = [("in_proj.weight", self.in_proj.param()), ("out_proj.weight", self.out_proj.param()),
-               ("dt_bias", tensor_param(self, "dt_bias")), ("a_log", tensor_param(self, "a_log"))]
+        out = [("in_proj.weight", self.in_proj.param()), ("out_proj.weight", self.out_proj.param())]
+        if self.conv_weight is not None:     # nn/conv.rs visit: weight, then bias
+            out += [("conv.weight", tensor_param(self, "conv_weight")),
+                    ("conv.bias", tensor_param(self, "conv_bias"))]
+        out += [("dt_bias", tensor_param(self, "dt_bias")), ("a_log", tensor_param(self, "a_log"))]
         if self.d_skip is not None:
             out.append(("d", tensor_param(self, "d_skip")))
         if self.b_bias is not None:
@@ -94,14 +110,27 @@ class Mamba3Mixer:
         return out
 
     # ------------------------------------------------------------ pieces
+    def conv_channels(self) -> int:
+        """mamba3.rs:205: the convolution runs over [x | B | C]."""
+        return self.cfg.d_inner() + 2 * self.cfg.bc_width()
+
+    def _history(self, batch: int, device) -> torch.Tensor:
+        """CausalConv1d::empty_history (nn/conv.rs:221-225)."""
+        return torch.zeros((batch, self.cfg.conv_kernel - 1, self.conv_channels()),
+                           dtype=torch.bfloat16, device=device)
+
     def _dims(self, tokens: int) -> _lib.MixerDimsC:
         c = self.cfg
         return _lib.MixerDimsC(tokens, c.n_heads, c.head_dim, c.d_state, c.mode.rank(),
                                c.n_groups, int(c.discretization), int(c.dynamics),
                                1e-5 if self.bc_norm is None else self.bc_norm.eps)
 
-    def project(self, input: torch.Tensor) -> Projected:
-        """mamba3.rs:350-466 without the convolution."""
+    def project(self, input: torch.Tensor, history: Optional[torch.Tensor] = None,
+                new_history: Optional[torch.Tensor] = None) -> Projected:
+        """mamba3.rs:350-466.  With a convolution, `history` [B, k-1, channels]
+        (None: zeros, as CausalConv1d::apply) precedes the window, and the
+        window's last k-1 convolution inputs go to `new_history` when given
+        (which may be `history` itself for a one-position window)."""
         c = self.cfg
         input = _bf16_dev(input, "mixer input")
         if input.dim() != 3 or input.shape[2] != c.d_model:
@@ -120,8 +149,20 @@ class Mamba3Mixer:
         theta = torch.empty((B, T, H, N // 2), dtype=torch.bfloat16, device=dev) if rot else None
         dims = self._dims(B * T)
         ptr = lambda t: None if t is None else t.data_ptr()
-        _lib.check(_lib.lib().m3_mixer_prologue(
-            C.byref(dims), projected.data_ptr(), self.dt_bias.data_ptr(), ptr(self.b_bias),
+        conv = None
+        if self.conv_weight is not None:
+            hshape = (B, c.conv_kernel - 1, self.conv_channels())
+            for name, h in (("history", history), ("new history", new_history)):
+                if h is not None and (tuple(h.shape) != hshape or h.dtype != torch.bfloat16
+                                      or not h.is_contiguous() or h.device != dev):
+                    raise ShapeError(f"shape error: the convolution {name} must be a contiguous "
+                                     f"bf16 {hshape} tensor on {dev}, got {h.dtype} "
+                                     f"{tuple(h.shape)} on {h.device}")
+            conv = _lib.Conv1dC(c.conv_kernel, T, self.conv_weight.data_ptr(),
+                                ptr(self.conv_bias), ptr(history), ptr(new_history))
+        _lib.check(_lib.lib().m3_mixer_prologue_conv(
+            C.byref(dims), None if conv is None else C.byref(conv), projected.data_ptr(),
+            self.dt_bias.data_ptr(), ptr(self.b_bias),
             ptr(self.c_bias), None if self.bc_norm is None else self.bc_norm.weight.data_ptr(),
             x.data_ptr(), b.data_ptr(), cc.data_ptr(), dt.data_ptr(), lam.data_ptr(), ptr(theta),
             _stream(input)))
@@ -144,9 +185,11 @@ class Mamba3Mixer:
 
     # ------------------------------------------------------------ entry points
     def empty_cache(self, batch: int, device) -> MixerCache:
+        """mamba3.rs:303-316: a zero state and, with a convolution, a zero history."""
         c = self.cfg
         return MixerCache(SsmState.zeros(batch, c.n_heads, c.head_dim, c.d_state,
-                                         c.dynamics == StateDynamics.Rotational, device))
+                                         c.dynamics == StateDynamics.Rotational, device),
+                          None if self.conv_weight is None else self._history(batch, device))
 
     def apply(self, input: torch.Tensor, residual: Optional[torch.Tensor] = None,
               out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -156,8 +199,13 @@ class Mamba3Mixer:
                          residual: Optional[torch.Tensor] = None,
                          out: Optional[torch.Tensor] = None):
         """mamba3.rs:498-567: the mixer over a window; with a cache the scan
-        starts from its state and the boundary state is returned."""
-        proj = self.project(input)
+        starts from its state (and the convolution from its history) and the
+        boundary state is returned in a new cache."""
+        hist = new_hist = None
+        if cache is not None and self.conv_weight is not None:
+            hist = cache.conv
+            new_hist = self._history(input.shape[0], input.device) if input.dim() == 3 else None
+        proj = self.project(input, hist, new_hist)
         si = ScanInputs(proj.x, proj.b, proj.c, proj.dt, self.a_log, proj.lam)
         si = si.with_chunk_size(self.cfg.chunk_size).with_state_output(cache is not None)
         if proj.theta is not None:
@@ -168,7 +216,7 @@ class Mamba3Mixer:
             si = si.with_state(cache.ssm)
         scan = mamba3_scan(si)
         y = self.finish(scan.y, proj, residual=residual, out=out)
-        new = MixerCache(scan.state) if cache is not None else None
+        new = MixerCache(scan.state, new_hist) if cache is not None else None
         return y, new
 
     def step_(self, input: torch.Tensor, cache: MixerCache,
@@ -180,8 +228,10 @@ class Mamba3Mixer:
             raise ShapeError("shape error: step() expects a single position; use "
                              "apply_with_state for a window")
         c = self.cfg
-        proj = self.project(input)
         B = input.shape[0]
+        if self.conv_weight is not None and cache.conv is None:
+            cache.conv = self._history(B, input.device)
+        proj = self.project(input, cache.conv, cache.conv)
         sq = lambda t: None if t is None else t.reshape((B,) + tuple(t.shape[2:]))
         y = mamba3_step_(sq(proj.x), sq(proj.b), sq(proj.c), sq(proj.dt), sq(proj.lam),
                          self.a_log, sq(proj.theta), self.d_skip, cache.ssm)
@@ -189,7 +239,7 @@ class Mamba3Mixer:
 
     def step(self, input: torch.Tensor, cache: MixerCache):
         """mamba3.rs:569-630: returns (output, new cache) like the reference."""
-        new = MixerCache(cache.ssm.clone())
+        new = cache.clone()
         if new.ssm.angle is None and self.cfg.dynamics == StateDynamics.Rotational:
             B = input.shape[0]
             new.ssm.angle = torch.zeros((B, self.cfg.n_heads, self.cfg.d_state // 2),

@@ -178,13 +178,13 @@ def test_filter_and_repeated_keys(tmp_path):
 
 
 # ------------------------------------------------------------------ models on the CPU
-def _cpu_lm(seed=0, layers=2):
+def _cpu_lm(seed=0, layers=2, conv=None):
     from mamba3 import Discretization, SsmConfig, SsmMode, StateDynamics
     from mamba3.lm import Mamba3Lm, Mamba3LmConfig
     ssm = SsmConfig(d_model=16, n_heads=2, head_dim=8, d_state=8, n_groups=1,
                     discretization=Discretization.LearnedTrapezoid,
                     dynamics=StateDynamics.Rotational, mode=SsmMode(1), chunk_size=64,
-                    conv_kernel=None, bc_norm=True, post_gate_norm=True)
+                    conv_kernel=conv, bc_norm=True, post_gate_norm=True)
     return Mamba3Lm(Mamba3LmConfig(vocab_size=11, d_model=16, n_layers=layers, ssm=ssm, seed=seed),
                     "cpu")
 
@@ -206,6 +206,27 @@ def test_parameter_paths_are_the_references():
     assert shapes["stack.layers.0.mixer.out_proj.weight"] == (16, 16)
     assert shapes["stack.layers.0.mixer.b_bias"] == (2, 8)
     assert shapes["embed.weight"] == (11, 16) and shapes["head.weight"] == (16, 11)
+
+
+def test_convolution_parameters_follow_out_proj():
+    """mamba3.rs:634-640 and nn/conv.rs: with conv_kernel k the mixer visits
+    conv.weight [k, d_inner + 2 bc_width] and conv.bias right after out_proj;
+    the weight starts in U(-sqrt(3/k), sqrt(3/k)) (KaimingUniform, fan_in k,
+    nn/init.rs:82-93), the bias at zero."""
+    lm = _cpu_lm(conv=4)
+    names = [n for n, _ in lm.named_parameters()]
+    i = names.index("stack.layers.0.mixer.out_proj.weight")
+    assert names[i + 1:i + 4] == ["stack.layers.0.mixer.conv.weight",
+                                  "stack.layers.0.mixer.conv.bias", "stack.layers.0.mixer.dt_bias"]
+    params = dict(lm.named_parameters())
+    ch = 16 + 2 * 8
+    assert params["stack.layers.1.mixer.conv.weight"].shape == (4, ch)
+    assert params["stack.layers.1.mixer.conv.bias"].shape == (ch,)
+    w = params["stack.layers.1.mixer.conv.weight"].get().numpy()
+    assert np.abs(w).max() <= math.sqrt(3.0 / 4) and np.abs(w).max() > 0.5 * math.sqrt(3.0 / 4)
+    assert not params["stack.layers.1.mixer.conv.bias"].get().numpy().any()
+    cache = lm.empty_cache(3, "cpu")
+    assert tuple(cache[0].conv.shape) == (3, 3, ch) and not cache[0].conv.float().any()
 
 
 def test_state_dict_rules(tmp_path):

@@ -146,6 +146,110 @@ def test_prologue_against_oracle(H, G, P, N, R, learned, rot, plain):
         assert np.array_equal(host(th), ref["theta"])
 
 
+# The causal convolution in the prologue (m3_mixer_prologue_conv).  Shapes as
+# above: the first three take the 16-byte path (ranks 1, 2 and 4, groups
+# shared by heads in the second), the last two the element-wise one.  `hist`:
+# "none" convolves from zeros and writes no history; "fresh" reads a history
+# and writes the new one to another buffer; "inplace" (one position per
+# sequence, the decode step) writes it over the history it reads.
+CONV_SHAPES = [(4, 2, 4, 8, 1, True, True), (8, 4, 8, 64, 2, False, False),
+               (4, 4, 16, 32, 4, True, True), (2, 1, 4, 4, 2, True, True),
+               (3, 3, 8, 8, 1, False, True)]
+
+
+def _run_prologue_conv(shape, k, batch, seq, hist, seed):
+    import ctypes as C
+    from mamba3 import Discretization, StateDynamics
+    H, G, P, N, R, learned, rot = shape
+    rng = np.random.default_rng(seed)
+    cfg = dict(heads=H, head_dim=P, d_state=N, rank=R, groups=G, learned_lambda=learned,
+               fixed_lambda=0.5, rotational=rot, eps=1e-5)
+    din, bcw, lw, tw = mo.widths(cfg)
+    width = 2 * din + 2 * bcw + H + lw + tw
+    ch = din + 2 * bcw
+    M = batch * seq
+    proj = mo.bf16(rng.normal(0, 1.5, (M, width)))
+    bound = np.sqrt(3.0 / k)
+    p = dict(dt_bias=rng.normal(-2, 1, H).astype(np.float32),
+             b_bias=rng.normal(0, 0.3, (H, N)).astype(np.float32),
+             c_bias=rng.normal(0, 0.3, (H, N)).astype(np.float32),
+             bc_norm=rng.uniform(0.5, 1.5, N).astype(np.float32),
+             conv_w=rng.uniform(-bound, bound, (k, ch)).astype(np.float32),
+             conv_b=rng.normal(0, 0.3, ch).astype(np.float32))
+    h0 = None if hist == "none" else mo.bf16(rng.normal(0, 1.5, (batch, k - 1, ch)))
+    ref = mo.mixer_project(proj, cfg, p, rnd=True, batch=batch, history=h0)
+    L = lib()
+    disc = Discretization.LearnedTrapezoid if learned else Discretization.Trapezoid
+    dyn = StateDynamics.Rotational if rot else StateDynamics.Real
+    dims = L.MixerDimsC(M, H, P, N, R, G, int(disc), int(dyn), 1e-5)
+    x = torch.empty((M, H, P, R), dtype=torch.bfloat16, device=DEV)
+    b = torch.empty((M, H, N, R), dtype=torch.bfloat16, device=DEV)
+    c = torch.empty_like(b)
+    dt = torch.empty((M, H), device=DEV)
+    lam = torch.empty_like(dt)
+    th = torch.empty((M, H, N // 2), dtype=torch.bfloat16, device=DEV) if rot else None
+    keep = [t_f32(p[k_]) for k_ in ("dt_bias", "b_bias", "c_bias", "bc_norm")]
+    w, cb = t_f32(p["conv_w"]), t_f32(p["conv_b"])
+    hd = None if h0 is None else t_bf16(h0)
+    nh = {"none": None, "fresh": torch.full((batch, k - 1, ch), 7.0, dtype=torch.bfloat16,
+                                            device=DEV), "inplace": hd}[hist]
+    conv = L.Conv1dC(k, seq, w.data_ptr(), cb.data_ptr(), None if hd is None else hd.data_ptr(),
+                     None if nh is None else nh.data_ptr())
+    projd = t_bf16(proj)
+    print(f"prologue_conv shape={shape} k={k} batch={batch} seq={seq} hist={hist}", flush=True)
+    L.check(L.lib().m3_mixer_prologue_conv(C.byref(dims), C.byref(conv), projd.data_ptr(),
+                                           *[None if t is None else t.data_ptr() for t in keep],
+                                           x.data_ptr(), b.data_ptr(), c.data_ptr(), dt.data_ptr(),
+                                           lam.data_ptr(), None if th is None else th.data_ptr(),
+                                           None))
+    torch.cuda.synchronize()
+    assert rel_l2(host(x), ref["x"]) <= 1e-2
+    assert rel_l2(host(b), ref["b"]) <= 1e-2
+    assert rel_l2(host(c), ref["c"]) <= 1e-2
+    assert rel_l2(host(dt), ref["dt"]) <= 1e-5
+    assert rel_l2(host(lam), ref["lam"]) <= 1e-5
+    if rot:
+        assert np.array_equal(host(th), ref["theta"])
+    if nh is not None:       # copies of bf16 inputs: bit-exact
+        assert np.array_equal(host(nh), ref["conv_history"])
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES)
+@pytest.mark.parametrize("k,batch,seq,hist", [(4, 2, 37, "none"), (4, 3, 21, "fresh"),
+                                              (2, 2, 5, "fresh"), (4, 2, 2, "fresh"),
+                                              (4, 5, 1, "inplace"), (3, 4, 1, "fresh")])
+def test_prologue_conv_against_oracle(shape, k, batch, seq, hist):
+    _run_prologue_conv(shape, k, batch, seq, hist, seed=100 + k + 3 * seq + batch)
+
+
+def test_prologue_conv_rejects_overlapping_histories():
+    """The new history may share the history's buffer only for one-position
+    windows; an overlap is refused before any launch."""
+    import ctypes as C
+    from mamba3 import Discretization, StateDynamics
+    from mamba3.error import ArgumentError, ConfigError, ShapeError
+    L = lib()
+    H, P, N, R, G, k, batch, seq = 2, 8, 8, 1, 2, 4, 2, 3
+    dims = L.MixerDimsC(batch * seq, H, P, N, R, G, int(Discretization.LearnedTrapezoid),
+                        int(StateDynamics.Real), 1e-5)
+    ch = H * P * R + 2 * G * N * R
+    hist = torch.zeros((batch + 1, k - 1, ch), dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros((k, ch), device=DEV)
+    bufs = [None] * 12
+
+    def call(kk, sl, h, nh):
+        conv = L.Conv1dC(kk, sl, w.data_ptr(), None, h, nh)
+        return L.check(L.lib().m3_mixer_prologue_conv(C.byref(dims), C.byref(conv), *bufs))
+    with pytest.raises(ArgumentError, match="overlap"):
+        call(k, seq, hist.data_ptr(), hist.data_ptr())
+    with pytest.raises(ArgumentError, match="overlap"):
+        call(k, seq, hist.data_ptr(), hist[1].data_ptr())
+    with pytest.raises(ConfigError, match="at least 2"):
+        call(1, seq, None, None)
+    with pytest.raises(ShapeError, match="whole number of sequences"):
+        call(k, 4, None, None)
+
+
 # z stride 200 takes the 16-byte path, 201 the element-wise one.
 @pytest.mark.parametrize("zs", [200, 201])
 @pytest.mark.parametrize("norm", [False, True])
@@ -191,7 +295,9 @@ def gpu_lm_from_oracle(model, int8, learned=True, rot=True):
                     d_state=cfg["d_state"], n_groups=cfg["groups"],
                     discretization=Discretization.LearnedTrapezoid if learned else Discretization.Trapezoid,
                     dynamics=StateDynamics.Rotational if rot else StateDynamics.Real,
-                    mode=SsmMode(cfg["rank"]), chunk_size=64, conv_kernel=None)
+                    mode=SsmMode(cfg["rank"]), chunk_size=64,
+                    conv_kernel=(None if model["layers"][0].get("conv_w") is None
+                                 else model["layers"][0]["conv_w"].shape[0]))
     lmc = Mamba3LmConfig(vocab_size=model["embed"].shape[0], d_model=model["embed"].shape[1],
                          n_layers=len(model["layers"]), ssm=ssm, int8_weights=int8)
     lm = Mamba3Lm(lmc, DEV)
@@ -208,16 +314,23 @@ def gpu_lm_from_oracle(model, int8, learned=True, rot=True):
         mixer.b_bias = t_f32(layer["b_bias"])
         mixer.c_bias = t_f32(layer["c_bias"])
         mixer.bc_norm.weight = t_f32(layer["bc_norm"])
+        if layer.get("conv_w") is not None:
+            mixer.conv_weight = t_f32(layer["conv_w"])
+            mixer.conv_bias = t_f32(layer["conv_b"])
     return lm
 
 
-@pytest.mark.parametrize("int8,rot,learned,rank", [(True, True, True, 1), (False, True, True, 1),
-                                                   (True, False, False, 1), (True, True, True, 2)])
-def test_lm_forward_against_oracle(int8, rot, learned, rank):
-    rng = np.random.default_rng(20 + int8 + 2 * rot + 4 * rank)
+@pytest.mark.parametrize("int8,rot,learned,rank,conv", [(True, True, True, 1, None),
+                                                        (False, True, True, 1, None),
+                                                        (True, False, False, 1, None),
+                                                        (True, True, True, 2, None),
+                                                        (True, True, True, 1, 4),
+                                                        (False, False, True, 2, 3)])
+def test_lm_forward_against_oracle(int8, rot, learned, rank, conv):
+    rng = np.random.default_rng(20 + int8 + 2 * rot + 4 * rank + 8 * (conv or 0))
     model = mo.random_model(rng, vocab=32, d_model=32, n_layers=2, heads=2, head_dim=8,
                             d_state=8, rank=rank, rotational=rot, learned_lambda=learned,
-                            fixed_lambda=0.5, int8=int8, bias_scale=0.3)
+                            fixed_lambda=0.5, int8=int8, bias_scale=0.3, conv_kernel=conv)
     lm = gpu_lm_from_oracle(model, int8, learned, rot)
     ids = rng.integers(0, 32, (2, 45))
     got = host(lm.forward(torch.from_numpy(ids).to(DEV)))
@@ -225,12 +338,14 @@ def test_lm_forward_against_oracle(int8, rot, learned, rank):
     assert rel_l2(got, ref) <= 1e-2, rel_l2(got, ref)
 
 
-def test_cached_decoding_matches_the_parallel_pass_on_device():
+@pytest.mark.parametrize("conv", [None, 4])
+def test_cached_decoding_matches_the_parallel_pass_on_device(conv):
     """tests/model.rs:99-139 on the gfx950 path: one token at a time, and a
-    prefill of 5 followed by steps, reproduce the parallel pass."""
+    prefill of 5 followed by steps, reproduce the parallel pass; with a
+    convolution its history is carried (in place by the steps)."""
     rng = np.random.default_rng(31)
     model = mo.random_model(rng, vocab=16, d_model=32, n_layers=2, heads=2, head_dim=8,
-                            d_state=8, int8=True, bias_scale=0.3)
+                            d_state=8, int8=True, bias_scale=0.3, conv_kernel=conv)
     lm = gpu_lm_from_oracle(model, True)
     seq = torch.tensor([[3, 1, 4, 1, 5, 9, 2, 6]], device=DEV)
     full = host(lm.forward(seq))
@@ -264,15 +379,16 @@ def test_config4_layer_shapes_against_oracle():
     assert rel_l2(got, ref) <= 1e-2, rel_l2(got, ref)
 
 
-def test_decode_graph_replays_match_eager_steps():
+@pytest.mark.parametrize("conv", [None, 4])
+def test_decode_graph_replays_match_eager_steps(conv):
     """Mamba3Lm.capture_decode: a captured decode step replayed six times, with
     eager steps and host synchronisation between the replays; every replay's
-    logits and states equal the eager step's bit for bit (the same kernels on
-    the same inputs), and capturing leaves the states where they were."""
-    from mamba3.mixer import MixerCache
+    logits, states and convolution histories equal the eager step's bit for
+    bit (the same kernels on the same inputs), and capturing leaves the states
+    where they were."""
     rng = np.random.default_rng(61)
     model = mo.random_model(rng, vocab=64, d_model=64, n_layers=2, heads=4, head_dim=16,
-                            d_state=16, int8=True, bias_scale=0.3)
+                            d_state=16, int8=True, bias_scale=0.3, conv_kernel=conv)
     lm = gpu_lm_from_oracle(model, True)
     B = 8
     gen = torch.Generator(device=DEV).manual_seed(62)
@@ -281,11 +397,14 @@ def test_decode_graph_replays_match_eager_steps():
         c.ssm.h.normal_(0.0, 0.1, generator=gen)
         c.ssm.last_u.normal_(0.0, 0.1, generator=gen)
         c.ssm.angle.uniform_(-3.0, 3.0, generator=gen)
-    cache_g = [MixerCache(c.ssm.clone()) for c in cache_e]
+        if c.conv is not None:
+            c.conv.normal_(0.0, 1.0, generator=gen)
+    cache_g = [c.clone() for c in cache_e]
     graph = lm.capture_decode(cache_g, B)
     torch.cuda.synchronize()
     for ce, cg in zip(cache_e, cache_g):
         assert torch.equal(ce.ssm.h, cg.ssm.h) and torch.equal(ce.ssm.angle, cg.ssm.angle)
+        assert conv is None or torch.equal(ce.conv, cg.conv)
     for step in range(6):
         ids = torch.randint(0, 64, (B, 1), device=DEV, generator=gen)
         want = lm.forward_cached(ids, cache_e).clone()
@@ -297,4 +416,59 @@ def test_decode_graph_replays_match_eager_steps():
             assert torch.equal(ce.ssm.h, cg.ssm.h), step
             assert torch.equal(ce.ssm.last_u, cg.ssm.last_u), step
             assert torch.equal(ce.ssm.angle, cg.ssm.angle), step
+            assert conv is None or torch.equal(ce.conv, cg.conv), step
     assert torch.isfinite(got.float()).all()
+
+
+def _default_mixer_and_layer(rng):
+    """A Mamba3Mixer of the reference's default SsmConfig (config.rs:131-156:
+    d_model 768, 24 heads x 64, d_state 64, 24 groups, conv_kernel 4, bc_norm,
+    B/C biases, D skip, rotational, learned trapezoid) carrying an oracle
+    layer's weights."""
+    from mamba3 import SsmConfig
+    from mamba3.mixer import Mamba3Mixer
+    from mamba3.nn import Linear
+    cfg = SsmConfig()
+    assert cfg.conv_kernel == 4 and cfg.d_state == 64 and cfg.n_heads == 24
+    model = mo.random_model(rng, vocab=4, d_model=768, n_layers=1, heads=24, head_dim=64,
+                            d_state=64, groups=24, int8=False, bias_scale=0.2, conv_kernel=4)
+    layer = model["layers"][0]
+    layer["in_proj_master"] = (layer["in_proj_master"] * (0.02 / 0.3)).astype(np.float32)
+    layer["in_proj"] = mo.bf16(layer["in_proj_master"])
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    mixer = Mamba3Mixer(cfg, device=DEV, gen=gen)
+    assert tuple(mixer.conv_weight.shape) == layer["conv_w"].shape
+    mixer.in_proj = Linear(t_f32(layer["in_proj_master"]))
+    mixer.out_proj = Linear(t_f32(layer["out_proj_master"]))
+    mixer.conv_weight, mixer.conv_bias = t_f32(layer["conv_w"]), t_f32(layer["conv_b"])
+    mixer.dt_bias, mixer.a_log = t_f32(layer["dt_bias"]), t_f32(layer["a_log"])
+    mixer.d_skip = t_f32(layer["d_skip"])
+    mixer.b_bias, mixer.c_bias = t_f32(layer["b_bias"]), t_f32(layer["c_bias"])
+    mixer.bc_norm.weight = t_f32(layer["bc_norm"])
+    return mixer, layer, model["cfg"]
+
+
+def test_default_config_mixer_prefill_and_step_against_oracle():
+    """The reference's default SsmConfig on the device: a prefill window
+    (Mamba3Mixer::apply), then a window through apply_with_state and three
+    single-position steps carrying the state and the convolution history,
+    each against the oracle mixer."""
+    rng = np.random.default_rng(80)
+    mixer, layer, ocfg = _default_mixer_and_layer(rng)
+    B, T = 2, 100
+    inp = mo.bf16(rng.normal(0, 1, (B, T + 3, 768)))
+    got = host(mixer.apply(t_bf16(inp[:, :T])))
+    ref, _ = mo.mixer_apply(inp[:, :T], layer, ocfg, None, rnd=True)
+    assert rel_l2(got, ref) <= 1e-2, rel_l2(got, ref)
+    cache = mixer.empty_cache(B, DEV)
+    y, cache = mixer.apply_with_state(t_bf16(inp[:, :T]), cache)
+    outs = [host(y)]
+    for t in range(T, T + 3):
+        outs.append(host(mixer.step_(t_bf16(inp[:, t:t + 1]), cache)))
+    got = np.concatenate(outs, axis=1)
+    ref, st = mo.mixer_apply(inp, layer, ocfg, None, rnd=True)
+    assert rel_l2(got, ref) <= 1e-2, rel_l2(got, ref)
+    # the history holds the last 3 projected [x | B | C] rows (bf16 products
+    # of the device GEMM, so compared at the bf16 bar rather than bit for bit)
+    assert rel_l2(host(cache.conv), st[3]) <= 1e-2
+    assert rel_l2(host(cache.ssm.h), st[0]) <= 1e-2

@@ -6,8 +6,11 @@ guarantees (the reference's tests/model.rs:318-361 adapted to per-channel
 int8), how the projection row splits (perturbing one piece moves only its
 own output), the rank-last layout, and the reference's decoding invariant
 (tests/model.rs:99-139: one token at a time through the carried state equals
-the parallel pass).  test_planted_mistakes_are_caught plants each fault in
-the oracle and requires that some check fails.
+the parallel pass).  The causal convolution is pinned by a delta input (which
+reads the taps back), by numpy.convolve per channel, and by windows chained
+through the carried history (including windows shorter than the history).
+test_planted_mistakes_are_caught plants each fault in the oracle and requires
+that some check fails.
 """
 import math
 
@@ -159,23 +162,81 @@ def check_zero_projection_is_silent():
 
 def check_cached_decoding_matches_parallel():
     """tests/model.rs:99-139: stepwise and prefill + steps equal the parallel pass."""
-    for rot, learned in ((True, True), (False, False)):
+    for rot, learned, conv in ((True, True, None), (False, False, None), (True, True, 4)):
         rng = np.random.default_rng(6)
         model = mo.random_model(rng, rotational=rot, learned_lambda=learned, fixed_lambda=0.5,
-                                bias_scale=0.3)
+                                bias_scale=0.3, conv_kernel=conv)
         ids = np.array([[3, 1, 4, 1, 5, 9, 2, 6]]) % 16
         full = mo.lm_forward(ids, model)
         for split in (0, 5):
             step = mo.lm_forward_stepwise(ids, model, split)
-            assert np.max(np.abs(step - full)) < 2e-3, (rot, split, np.max(np.abs(step - full)))
+            assert np.max(np.abs(step - full)) < 2e-3, (rot, conv, split,
+                                                        np.max(np.abs(step - full)))
     # the pieces really move the logits (the invariant is not vacuous)
     assert np.std(full) > 1e-2
+
+
+def check_conv_delta_reproduces_taps():
+    """A unit impulse at position s0 of channel c gives bias + w[k-1-d, c] at
+    position s0 + d for d < k, and the bias everywhere else."""
+    rng = np.random.default_rng(7)
+    k, S, C = 4, 9, 3
+    w = rng.normal(0, 1, (k, C))
+    bias = rng.normal(0, 1, C)
+    x = np.zeros((1, S, C))
+    x[0, 2, 1] = 1.0
+    out, _ = mo.causal_conv1d(x, w, bias)
+    want = np.broadcast_to(bias, (1, S, C)).copy()
+    for d in range(k):
+        want[0, 2 + d, 1] += w[k - 1 - d, 1]
+    assert np.allclose(out, want, rtol=0, atol=1e-15)
+
+
+def check_conv_matches_numpy_convolve():
+    """Per channel, the causal convolution is numpy's full convolution of
+    history ++ x with the reversed taps, read at the positions of x."""
+    rng = np.random.default_rng(8)
+    for k, S, hist in ((2, 7, False), (4, 11, True), (5, 3, True)):
+        B, C = 2, 5
+        w = rng.normal(0, 1, (k, C))
+        bias = rng.normal(0, 1, C)
+        x = rng.normal(0, 1, (B, S, C))
+        h = rng.normal(0, 1, (B, k - 1, C)) if hist else None
+        out, _ = mo.causal_conv1d(x, w, bias, h)
+        for b in range(B):
+            for c in range(C):
+                seq = np.concatenate([np.zeros(k - 1) if h is None else h[b, :, c], x[b, :, c]])
+                full = np.convolve(seq, w[::-1, c])
+                assert np.allclose(out[b, :, c], full[k - 1:k - 1 + S] + bias[c], rtol=1e-13,
+                                   atol=1e-13), (k, S, b, c)
+
+
+def check_conv_history_chains_windows():
+    """The convolution of a sequence equals the convolution of its pieces, each
+    started from the history the previous piece returned; pieces of one
+    position and pieces shorter than the history included."""
+    rng = np.random.default_rng(9)
+    k, S, B, C = 4, 12, 2, 3
+    w = rng.normal(0, 1, (k, C))
+    bias = rng.normal(0, 1, C)
+    x = rng.normal(0, 1, (B, S, C))
+    whole, last = mo.causal_conv1d(x, w, bias)
+    for cuts in ((5,), (1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11), (2, 7), (10,)):
+        hist, outs, lo = None, [], 0
+        for hi in list(cuts) + [S]:
+            o, hist = mo.causal_conv1d(x[:, lo:hi], w, bias, hist)
+            outs.append(o)
+            lo = hi
+        assert np.allclose(np.concatenate(outs, axis=1), whole, rtol=1e-13, atol=1e-13), cuts
+        assert np.allclose(hist, last, rtol=0, atol=0), cuts
+    assert np.array_equal(last, x[:, S - (k - 1):])           # the last k-1 inputs
 
 
 CHECKS = [check_bf16_rounding, check_activation_values, check_rms_norm_closed_forms,
           check_quantizer_grid, check_projection_pieces, check_rank_last_layout,
           check_bc_norm_unit_rms, check_known_mixer_values, check_zero_projection_is_silent,
-          check_cached_decoding_matches_parallel]
+          check_cached_decoding_matches_parallel, check_conv_delta_reproduces_taps,
+          check_conv_matches_numpy_convolve, check_conv_history_chains_windows]
 
 
 @pytest.mark.parametrize("check", CHECKS, ids=[c.__name__ for c in CHECKS])
