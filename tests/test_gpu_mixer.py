@@ -380,6 +380,62 @@ def test_config4_layer_shapes_against_oracle():
 
 
 @pytest.mark.parametrize("conv", [None, 4])
+def _device_rel_l2(a, b):
+    a, b = a.double(), b.double()
+    return float(torch.linalg.vector_norm(a - b) / torch.linalg.vector_norm(b))
+
+
+def test_config4_full_model_split_prefill_property():
+    """The whole BASELINE config-4 model (vocab 32000, d_model 768, 24 layers,
+    12 x 64 heads, N 128, groups 12, bc_norm, no conv, int8 projections,
+    random init) at B16 L2048, the reference's cached-decoding invariant
+    (tests/model.rs:100-140) at the benchmark shape: a 1024-token prefill
+    followed by a 1024-token window through the carried caches reproduces the
+    logits of one 2048-token prefill.
+
+    The bar is the device's own noise floor at this depth, measured here: the
+    same 2048-token prefill run as two batches of 8 (which takes the
+    chunk-parallel scan instead of the single-pass one, the same arithmetic in
+    another order).  With bf16 activations, rounding differences of ~1e-4 in
+    one layer flip bf16 roundings of the residual stream and compound over 24
+    layers to ~2.4e-2 in the logits (1e-3 at one layer), so no bf16
+    implementation meets 1e-2 on the 24-layer logits; the carried path must
+    be within 1.25x of that floor.  The first window must be bit-identical,
+    and the second window run without the carried caches must miss by at
+    least 5x more, so the check is not vacuous.  Compared on the device (the
+    logits are 2 GB)."""
+    from mamba3 import Discretization, SsmConfig, SsmMode, StateDynamics
+    from mamba3.lm import Mamba3Lm, Mamba3LmConfig
+    ssm = SsmConfig(d_model=768, n_heads=12, head_dim=64, d_state=128, n_groups=12,
+                    discretization=Discretization.LearnedTrapezoid,
+                    dynamics=StateDynamics.Rotational, mode=SsmMode(1), chunk_size=64,
+                    conv_kernel=None, bc_norm=True)
+    lm = Mamba3Lm(Mamba3LmConfig(vocab_size=32000, d_model=768, n_layers=24, ssm=ssm,
+                                 int8_weights=True, seed=4), DEV)
+    g = torch.Generator(device=DEV).manual_seed(44)
+    B, T, cut = 16, 2048, 1024
+    ids = torch.randint(0, 32000, (B, T), device=DEV, generator=g)
+    full = lm.forward(ids)
+    cache = lm.empty_cache(B, DEV)
+    first = lm.forward_cached(ids[:, :cut], cache)
+    second = lm.forward_cached(ids[:, cut:], cache)
+    torch.cuda.synchronize()
+    e1 = _device_rel_l2(first, full[:, :cut])
+    e2 = _device_rel_l2(second, full[:, cut:])
+    del first
+    halves = [lm.forward(ids[:B // 2])[:, cut:], lm.forward(ids[B // 2:])[:, cut:]]
+    floor = _device_rel_l2(torch.cat(halves, 0), full[:, cut:])
+    del halves
+    cold = _device_rel_l2(lm.forward(ids[:, cut:]), full[:, cut:])
+    print(f"config 4 full model, prefill {cut} + carried {T - cut} vs {T}: rel-L2 first "
+          f"{e1:.2e}, second {e2:.2e}; noise floor (the same prefill on the chunk-parallel "
+          f"scan) {floor:.2e}; without the carried caches {cold:.2e}", flush=True)
+    assert e1 == 0.0
+    assert e2 <= 1.25 * floor
+    assert cold >= 5 * e2
+    assert torch.isfinite(full.float()).all()
+
+
 def test_decode_graph_replays_match_eager_steps(conv):
     """Mamba3Lm.capture_decode: a captured decode step replayed six times, with
     eager steps and host synchronisation between the replays; every replay's
