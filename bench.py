@@ -18,6 +18,8 @@ Also reported on the same line:
   decode         BASELINE config 3: one token for 256 sequences through
                  24 layers x 24 heads (P=64, N=128) of f32 state cache, in place,
                  timed over consecutive steps: us per step, GB/s, fraction of HBM peak;
+  decode_factored the same steps on the second cache format (m3_step_factored:
+                 last_u carried as the previous token's x and b), on its own bytes;
   backward       config 1's scan backward (every input gradient from dL/dy):
                  us per call, fwd+bwd tokens/s, HBM fraction of its minimum bytes;
   decode_lm      the whole Mamba3Lm decode step around it (d_model 1536, int8
@@ -85,6 +87,16 @@ def decode_algorithmic(B, H, P, N, R):
     state = 16 * B * H * P * N
     io = B * H * (P * R + 2 * N * R + N // 2 + 2 + 2 * (N // 2) + P * R) * 4
     return state + io
+
+
+def decode_factored_algorithmic(B, H, P, N, R):
+    """Bytes per layer step of the factored form (m3_step_factored): h read +
+    written (8 B per state element), the inputs and outputs of
+    decode_algorithmic, and the previous token's x and b read + written."""
+    state = 8 * B * H * P * N
+    io = B * H * (P * R + 2 * N * R + N // 2 + 2 + 2 * (N // 2) + P * R) * 4
+    prev = B * H * 2 * (P * R + N * R) * 4
+    return state + io + prev
 
 
 def make_scan_inputs(torch, dev, B, L, H, P, N, R, seed):
@@ -568,13 +580,21 @@ def bench_other_scans(torch, lib, L_, args):
     return out
 
 
-def bench_decode(torch, lib, L_, args):
+def bench_decode(torch, lib, L_, args, factored=False):
+    """Config 3: 24 layers x one step each per pass over the f32 cache, in
+    place, rotating over `sets` input sets.  factored: the same steps through
+    m3_step_factored, the cache holding h and the previous token's x and b
+    (a second cache format, reported on its own byte count)."""
     dev = "cuda:0"
     d = DECODE
     B, NL, H, P, N, R, K = d["B"], d["layers"], d["H"], d["P"], d["N"], d["R"], d["sets"]
     g = torch.Generator(device=dev).manual_seed(0x4D414D45)
     h = torch.randn(NL, B, H, P, N, device=dev, generator=g) * 0.1
-    lu = torch.randn(NL, B, H, P, N, device=dev, generator=g) * 0.1
+    if factored:
+        xp = torch.randn(NL, B, H, P, R, device=dev, generator=g)
+        bp = torch.randn(NL, B, H, N, R, device=dev, generator=g) / math.sqrt(N)
+    else:
+        lu = torch.randn(NL, B, H, P, N, device=dev, generator=g) * 0.1
     ang = (torch.rand(NL, B, H, N // 2, device=dev, generator=g) * 2 - 1) * math.pi
     a_log = torch.rand(NL, H, device=dev, generator=g) * math.log(16.0)
     d_skip = torch.ones(H, device=dev)
@@ -597,12 +617,16 @@ def bench_decode(torch, lib, L_, args):
             args_c = L_.StepInputsC(B, H, P, N, R, L_.M3_F32, x.data_ptr(), b.data_ptr(),
                                     c.data_ptr(), dt.data_ptr(), lam.data_ptr(),
                                     a_log[l].data_ptr(), th.data_ptr(), d_skip.data_ptr())
-            st = L_.SsmStateC(h[l].data_ptr(), lu[l].data_ptr(), ang[l].data_ptr())
+            if factored:
+                st = L_.SsmStateFactoredC(h[l].data_ptr(), xp[l].data_ptr(), bp[l].data_ptr(),
+                                          ang[l].data_ptr())
+            else:
+                st = L_.SsmStateC(h[l].data_ptr(), lu[l].data_ptr(), ang[l].data_ptr())
             per_layer.append((args_c, st))
         calls.append(per_layer)
     stream = torch.cuda.current_stream()
     sp = C.c_void_p(stream.cuda_stream)
-    fn = lib.m3_step
+    fn = lib.m3_step_factored if factored else lib.m3_step
     yp = C.c_void_p(y.data_ptr())
     refs = [[(C.byref(a), C.byref(s)) for a, s in per] for per in calls]
 
@@ -623,8 +647,15 @@ def bench_decode(torch, lib, L_, args):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.decode_steps
     assert torch.isfinite(h).all(), "non-finite decode state"
-    nbytes = NL * decode_algorithmic(B, H, P, N, R)
+    nbytes = NL * (decode_factored_algorithmic if factored else decode_algorithmic)(B, H, P, N, R)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    if factored:
+        return dict(us_per_step=round(ms * 1e3, 2), steps=args.decode_steps, layers=NL,
+                    bytes_per_step=nbytes, achieved_GBps=round(gbs, 1),
+                    frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4),
+                    us_per_layer=round(ms * 1e3 / NL, 2),
+                    cache="h f32 [B,H,P,N] + the previous token's x [B,H,P,R] and b [B,H,N,R] "
+                          "(m3_step_factored; last_u formed in registers)")
     # a practical stream ceiling beside it: torch's device copy of one layer's
     # h and last_u (the same bytes read and written as one layer's update)
     src = torch.cat([h[0].reshape(-1), lu[0].reshape(-1)])
@@ -696,7 +727,7 @@ def main():
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--only", choices=("prefill", "decode_lm", "ingest", "backward", "other_scans",
-                                       "decode"), default=None,
+                                       "decode", "decode_factored"), default=None,
                     help="run one model leg alone and print its object (for kernel traces)")
     ap.add_argument("--scan-only", action="store_true",
                     help="run only the headline scan --steps times (for counter runs)")
@@ -736,9 +767,13 @@ def main():
         print(json.dumps({"backward": bench_backward(torch, lib, L_, args, inp, None)}),
               flush=True)
         return
-    if args.only in ("other_scans", "decode"):
-        fn = bench_other_scans if args.only == "other_scans" else bench_decode
-        print(json.dumps({args.only: fn(torch, lib, L_, args)}), flush=True)
+    if args.only in ("other_scans", "decode", "decode_factored"):
+        if args.only == "decode_factored":
+            leg = bench_decode(torch, lib, L_, args, factored=True)
+        else:
+            leg = (bench_other_scans if args.only == "other_scans" else bench_decode)(
+                torch, lib, L_, args)
+        print(json.dumps({args.only: leg}), flush=True)
         return
     if args.only:
         leg = {"prefill": bench_prefill, "decode_lm": bench_decode_lm,
@@ -765,6 +800,7 @@ def main():
                                                        sc["kernel_ms"])
     other = bench_other_scans(torch, lib, L_, args)
     dec = None if args.no_decode else bench_decode(torch, lib, L_, args)
+    dec_f = None if args.no_decode else bench_decode(torch, lib, L_, args, factored=True)
     pre = None if args.no_prefill else bench_prefill(torch, args)
     dlm = None if args.no_decode_lm else bench_decode_lm(torch, args)
     cpu = None if args.no_cpu else cpu_baseline(args)
@@ -805,6 +841,7 @@ def main():
         "other_scans": other,
         "backward": bwd,
         "decode": dec,
+        "decode_factored": dec_f,
         "prefill": pre,
         "decode_lm": dlm,
         "cpu_baseline": cpu,

@@ -16,6 +16,8 @@
  *                                 src/tensor/ops/fused.rs:2080-2138, 2326-2382, 2513-2549
  *   m3_ssd_args / m3_ssd_chunked  ssd_chunked               src/ssm/scan.rs:98-291
  *   m3_step_inputs / m3_step      mamba3_step               src/ssm/scan.rs:640-712
+ *   m3_step_factored              the same on a cache with last_u factored (no
+ *                                 reference counterpart; see its declaration)
  *   m3_status / m3_last_error     Error / Result            src/error.rs:5-61
  *
  * Conventions
@@ -243,6 +245,32 @@ typedef struct m3_step_inputs {
 /* mamba3_step (scan.rs:649-712), in place: `state` (h, last_u and, with
  * theta, angle) is read and overwritten; y [B, H, P, R] is written. */
 m3_status m3_step(const m3_step_inputs *in, m3_ssm_state *state, void *y, void *stream);
+
+/* A second decode-cache format with last_u factored.  No reference
+ * counterpart: the reference's SsmState.last_u is a full [B,H,P,N] tensor
+ * (scan.rs:293-303).  It is, after any window or step, the last token's
+ * rank-R outer product sum_r x_r B~_r^T with B~ = R(-angle) B
+ * (scan.rs:599-618, 683-691), so carrying that token's x and unrotated B
+ * with the angle holds the same information, and a step streams h alone:
+ * 8 bytes per state element instead of 16. */
+typedef struct m3_ssm_state_factored {
+    float *h;        /* [B, H, P, N] f32 */
+    void *x_prev;    /* [B, H, P, R] in the step inputs' dtype */
+    void *b_prev;    /* [B, H, N, R] in the step inputs' dtype, unrotated */
+    float *angle;    /* [B, H, N/2], NULL for real dynamics */
+} m3_ssm_state_factored;
+
+/* mamba3_step on the factored state, in place: h, x_prev, b_prev and angle
+ * are read and overwritten (x_prev and b_prev take this step's x and b).
+ * y and the new h equal m3_step's, bit for bit, on the full state whose
+ * last_u = x_prev B~_prev^T as m3_step itself stored it.  A state from a
+ * window of m3_scan starts with the window's last x and b (and the scan's h
+ * and angle); a zero state has zero x_prev and b_prev.  Covers d_state a
+ * multiple of 4 with d_state / 4 a power of two up to 64 and rank 1, 2, 3,
+ * 4 or 8 (else M3_ERR_UNSUPPORTED); x_prev and b_prev must not overlap the
+ * inputs. */
+m3_status m3_step_factored(const m3_step_inputs *in, m3_ssm_state_factored *state, void *y,
+                           void *stream);
 
 /* Status name and this thread's last error message ("" after success). */
 const char *m3_status_string(m3_status status);

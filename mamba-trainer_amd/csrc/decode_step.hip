@@ -14,6 +14,13 @@
 // minimum traffic of 16 bytes per state element -- the reference's step
 // reads and writes the state about twice that (new u tensor, a separate
 // update pass, and a materialised transpose of h for the readout).
+//
+// Factored form (FACT): last_u is the previous token's rank-R outer product
+// x_prev B~_prev^T (scan.rs:683-691), so the state carries that token's x and
+// unrotated b instead, with B~_prev = R(-angle) b_prev from the angle as it
+// stood before this step's advance.  The body forms last_u in registers with
+// the same f32 products the previous step stored, so the results equal the
+// full form's bit for bit, and the state streams h only: 8 bytes per element.
 #include "m3_device.hpp"
 #include "m3_internal.hpp"
 
@@ -31,10 +38,11 @@ __device__ __forceinline__ float ld(const void *p, size_t i) {
 
 // Prologue shared by both bodies: angle advance, rotation of B and C into
 // LDS (rank-last [N][R] layout kept), x into LDS, and the coefficients.
-template <typename T>
+template <typename T, bool FACT = false>
 __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, float *bt,
                                               float *ct, float *xs, float &alpha,
-                                              float &beta, float &gamma) {
+                                              float &beta, float &gamma, float *bpt = nullptr,
+                                              float *xps = nullptr) {
     const int tid = threadIdx.x;
     const size_t N = a.d_state, P = a.head_dim, R = a.rank;
     const size_t half = N / 2;
@@ -45,11 +53,23 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
     if (a.theta != nullptr) {
         for (size_t i = tid; i < half; i += kStepThreads) {
             // phi = wrap(prev + dt * theta)   (fused.rs:1549-1553)
-            float raw = ld<T>(a.theta, bh * half + i) * step + a.angle[bh * half + i];
+            const float prev = a.angle[bh * half + i];
+            float raw = ld<T>(a.theta, bh * half + i) * step + prev;
             float phi = wrap_angle(raw);
             a.angle[bh * half + i] = phi;
             float sn, cs;
             sincosf(phi, &sn, &cs);
+            if constexpr (FACT) {
+                // the previous token's B~, rotated by the angle it was taken at
+                float ps, pc;
+                sincosf(prev, &ps, &pc);
+                for (size_t r = 0; r < R; ++r) {
+                    const float b1 = ld<T>(a.b_prev, bc_base + i * R + r);
+                    const float b2 = ld<T>(a.b_prev, bc_base + (i + half) * R + r);
+                    bpt[i * R + r] = b1 * pc + b2 * ps;
+                    bpt[(i + half) * R + r] = -b1 * ps + b2 * pc;
+                }
+            }
             for (size_t r = 0; r < R; ++r) {
                 float b1 = ld<T>(a.b, bc_base + i * R + r);
                 float b2 = ld<T>(a.b, bc_base + (i + half) * R + r);
@@ -68,9 +88,13 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
         for (size_t i = tid; i < N * R; i += kStepThreads) {
             bt[i] = ld<T>(a.b, bc_base + i);
             ct[i] = ld<T>(a.c, bc_base + i);
+            if constexpr (FACT) bpt[i] = ld<T>(a.b_prev, bc_base + i);
         }
     }
-    for (size_t i = tid; i < P * R; i += kStepThreads) xs[i] = ld<T>(a.x, bh * P * R + i);
+    for (size_t i = tid; i < P * R; i += kStepThreads) {
+        xs[i] = ld<T>(a.x, bh * P * R + i);
+        if constexpr (FACT) xps[i] = ld<T>(a.x_prev, bh * P * R + i);
+    }
     // alpha = exp(dt * -exp(a_log)), beta = (1 - lambda) dt alpha, gamma = lambda dt
     const float A = 0.0f - expf(a.a_log[hh]);
     alpha = expf(step * A);
@@ -80,7 +104,7 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
 
 // Vector body: N % 4 == 0 and G = N / 4 lanes per row with G a power of two
 // that divides 64.  Each lane owns four consecutive state columns of a row.
-template <typename T, int RK>
+template <typename T, int RK, bool FACT>
 __global__ void __launch_bounds__(kStepThreads)
 step_kernel_vec(StepLaunch a) {
     extern __shared__ float smem[];
@@ -89,10 +113,22 @@ step_kernel_vec(StepLaunch a) {
     float *bt = smem;
     float *ct = bt + N * R;
     float *xs = ct + N * R;
+    float *bpt = xs + P * R;         // FACT: B~_prev [N][R], x_prev [P][R]
+    float *xps = bpt + N * R;
     const size_t bh = blockIdx.x;
     float alpha, beta, gamma;
-    step_prologue<T>(a, bh, bt, ct, xs, alpha, beta, gamma);
+    step_prologue<T, FACT>(a, bh, bt, ct, xs, alpha, beta, gamma, bpt, xps);
     __syncthreads();
+    if constexpr (FACT) {
+        // this step's x and b become the state's previous token (every read of
+        // the old ones happened before the barrier)
+        const T *xb = static_cast<const T *>(a.x) + bh * P * R;
+        const T *bb = static_cast<const T *>(a.b) + bh * N * R;
+        T *xp = static_cast<T *>(a.x_prev) + bh * P * R;
+        T *bp = static_cast<T *>(a.b_prev) + bh * N * R;
+        for (size_t i = threadIdx.x; i < P * R; i += kStepThreads) xp[i] = xb[i];
+        for (size_t i = threadIdx.x; i < N * R; i += kStepThreads) bp[i] = bb[i];
+    }
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -105,13 +141,14 @@ step_kernel_vec(StepLaunch a) {
     f32x4 *u4 = reinterpret_cast<f32x4 *>(a.last_u + bh * P * N);
 
     // B~ columns this lane touches, hoisted out of the row loop.
-    float bcol[4][R], ccol[4][R];
+    float bcol[4][R], ccol[4][R], pcol[4][FACT ? R : 1];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             bcol[j][r] = bt[(col4 + j) * R + r];
             ccol[j][r] = ct[(col4 + j) * R + r];
+            if constexpr (FACT) pcol[j][r] = bpt[(col4 + j) * R + r];
         }
 
     constexpr int kBatch = 4;   // rows in flight per lane
@@ -125,7 +162,7 @@ step_kernel_vec(StepLaunch a) {
             if (rows[k] < static_cast<int>(P)) {
                 size_t idx = (static_cast<size_t>(rows[k]) * N + col4) / 4;
                 hv[k] = __builtin_nontemporal_load(&h4[idx]);
-                lv[k] = __builtin_nontemporal_load(&u4[idx]);
+                if constexpr (!FACT) lv[k] = __builtin_nontemporal_load(&u4[idx]);
             }
         }
 #pragma unroll
@@ -137,17 +174,29 @@ step_kernel_vec(StepLaunch a) {
 #pragma unroll
             for (int r = 0; r < R; ++r) ypart[r] = 0.0f;
             if (live) {
-                float xr[R];
+                float xr[R], xq[FACT ? R : 1];
 #pragma unroll
-                for (int r = 0; r < R; ++r) xr[r] = xs[p * R + r];
+                for (int r = 0; r < R; ++r) {
+                    xr[r] = xs[p * R + r];
+                    if constexpr (FACT) xq[r] = xps[p * R + r];
+                }
                 f32x4 hn, un;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     float u = 0.0f;
 #pragma unroll
                     for (int r = 0; r < R; ++r) u += xr[r] * bcol[j][r];
+                    float lu;
+                    if constexpr (FACT) {
+                        // the previous step's u, the same products in the same order
+                        lu = 0.0f;
+#pragma unroll
+                        for (int r = 0; r < R; ++r) lu += xq[r] * pcol[j][r];
+                    } else {
+                        lu = lv[k][j];
+                    }
                     // h' = h*alpha + last_u*beta + u*gamma   (fused.rs:1360-1362)
-                    float hnew = hv[k][j] * alpha + lv[k][j] * beta + u * gamma;
+                    float hnew = hv[k][j] * alpha + lu * beta + u * gamma;
                     hn[j] = hnew;
                     un[j] = u;
 #pragma unroll
@@ -155,7 +204,7 @@ step_kernel_vec(StepLaunch a) {
                 }
                 size_t idx = (static_cast<size_t>(p) * N + col4) / 4;
                 __builtin_nontemporal_store(hn, &h4[idx]);
-                __builtin_nontemporal_store(un, &u4[idx]);
+                if constexpr (!FACT) __builtin_nontemporal_store(un, &u4[idx]);
             }
 #pragma unroll
             for (int r = 0; r < R; ++r) ypart[r] = group_sum(ypart[r], G);
@@ -205,15 +254,21 @@ step_kernel_generic(StepLaunch a) {
 
 template <typename T, int RK>
 hipError_t launch_vec(const StepLaunch &a, size_t smem, hipStream_t s) {
-    hipLaunchKernelGGL((step_kernel_vec<T, RK>), dim3(a.batch * a.heads), dim3(kStepThreads),
-                       smem, s, a);
+    if (a.last_u == nullptr)
+        hipLaunchKernelGGL((step_kernel_vec<T, RK, true>), dim3(a.batch * a.heads),
+                           dim3(kStepThreads), smem, s, a);
+    else
+        hipLaunchKernelGGL((step_kernel_vec<T, RK, false>), dim3(a.batch * a.heads),
+                           dim3(kStepThreads), smem, s, a);
     return hipGetLastError();
 }
 
 template <typename T>
 hipError_t dispatch(const StepLaunch &a, hipStream_t s) {
     const size_t N = a.d_state, R = a.rank;
-    const size_t smem = (2 * N * R + a.head_dim * R) * sizeof(float);
+    const bool fact = a.last_u == nullptr;
+    const size_t smem = ((fact ? 3 : 2) * N * R + (fact ? 2 : 1) * a.head_dim * R) * sizeof(float);
+    if (fact && !step_factored_supported(N, R)) return hipErrorNotSupported;
     const size_t G = N / 4;
     const bool vec = (N % 4 == 0) && G >= 1 && G <= 64 && (G & (G - 1)) == 0;
     if (vec) {
@@ -232,6 +287,12 @@ hipError_t dispatch(const StepLaunch &a, hipStream_t s) {
 }
 
 }  // namespace
+
+bool step_factored_supported(size_t d_state, size_t rank) {
+    const size_t G = d_state / 4;
+    return d_state % 4 == 0 && G >= 1 && G <= 64 && (G & (G - 1)) == 0 &&
+           (rank == 1 || rank == 2 || rank == 3 || rank == 4 || rank == 8);
+}
 
 hipError_t launch_step(const StepLaunch &a, hipStream_t stream) {
     if (a.batch * a.heads == 0) return hipSuccess;

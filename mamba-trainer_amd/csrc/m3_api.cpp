@@ -579,6 +579,69 @@ m3_status m3_step(const m3_step_inputs *in, m3_ssm_state *state, void *y, void *
     return ok();
 }
 
+m3_status m3_step_factored(const m3_step_inputs *in, m3_ssm_state_factored *state, void *y,
+                           void *stream) {
+    if (in == nullptr || state == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/state are NULL");
+    if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
+    if (in->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
+    if (in->head_dim == 0 || in->d_state == 0)
+        return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
+    if (in->theta != nullptr && in->d_state % 2 != 0)
+        return fail(M3_ERR_CONFIG, "rotational dynamics require an even d_state");
+    if (!m3::step_factored_supported(in->d_state, in->rank))
+        return fail(M3_ERR_UNSUPPORTED, "the factored step needs d_state a multiple of 4 with "
+                    "d_state/4 a power of two up to 64 and rank 1, 2, 3, 4 or 8 (got %zu, %zu)",
+                    in->d_state, in->rank);
+    if (state->h == nullptr || state->x_prev == nullptr || state->b_prev == nullptr)
+        return fail(M3_ERR_ARGUMENT, "the factored state needs h, x_prev and b_prev");
+    if (in->theta != nullptr && state->angle == nullptr)
+        return fail(M3_ERR_ARGUMENT, "theta needs the state's angle buffer (updated in place)");
+    if (in->batch * in->heads == 0) return ok();
+    if (in->x == nullptr || in->b == nullptr || in->c == nullptr || in->dt == nullptr ||
+        in->lambda == nullptr || in->a_log == nullptr || y == nullptr)
+        return fail(M3_ERR_ARGUMENT, "x, b, c, dt, lambda, a_log and y are required");
+    if (in->d_state * in->rank * 3 + in->head_dim * in->rank * 2 > 16384)
+        return fail(M3_ERR_UNSUPPORTED, "d_state/head_dim/rank too large for the step kernel");
+    const size_t es = in->dtype == M3_BF16 ? 2 : 4;
+    const size_t xb = in->batch * in->heads * in->head_dim * in->rank * es;
+    const size_t bb = in->batch * in->heads * in->d_state * in->rank * es;
+    auto overlap = [](const void *p, size_t pn, const void *q, size_t qn) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
+        return a < b + qn && b < a + pn;
+    };
+    if (overlap(state->x_prev, xb, in->x, xb) || overlap(state->b_prev, bb, in->b, bb) ||
+        overlap(state->x_prev, xb, in->b, bb) || overlap(state->b_prev, bb, in->x, xb) ||
+        overlap(state->x_prev, xb, state->b_prev, bb))
+        return fail(M3_ERR_ARGUMENT, "x_prev and b_prev must not overlap each other or the inputs");
+    m3::StepLaunch a{};
+    a.batch = in->batch;
+    a.heads = in->heads;
+    a.head_dim = in->head_dim;
+    a.d_state = in->d_state;
+    a.rank = in->rank;
+    a.bf16 = in->dtype == M3_BF16;
+    a.x = in->x;
+    a.b = in->b;
+    a.c = in->c;
+    a.dt = in->dt;
+    a.lambda = in->lambda;
+    a.a_log = in->a_log;
+    a.theta = in->theta;
+    a.d_skip = in->d_skip;
+    a.h = state->h;
+    a.last_u = nullptr;
+    a.x_prev = state->x_prev;
+    a.b_prev = state->b_prev;
+    a.angle = in->theta ? state->angle : nullptr;
+    a.y = y;
+    if (reinterpret_cast<uintptr_t>(a.h) % 16 != 0)
+        return fail(M3_ERR_ARGUMENT, "state buffers must be 16-byte aligned");
+    hipError_t e = m3::launch_step(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "step launch");
+    g_launches.fetch_add(1, std::memory_order_relaxed);
+    return ok();
+}
+
 const char *m3_status_string(m3_status s) {
     switch (s) {
         case M3_OK: return "M3_OK";

@@ -19,8 +19,13 @@ struct StepLaunch {
     const float *d_skip;            // [H] or null
     float *h, *last_u, *angle;      // [B,H,P,N] x2, [B,H,N/2] (null without theta)
     void *y;                        // [B,H,P,R]
+    // Factored last_u (last_u null): the previous token's x [B,H,P,R] and
+    // unrotated b [B,H,N,R] in the storage type, overwritten with this step's.
+    void *x_prev, *b_prev;
 };
 hipError_t launch_step(const StepLaunch &a, hipStream_t stream);
+// Shapes the factored form (last_u null) covers: the vector body's.
+bool step_factored_supported(size_t d_state, size_t rank);
 
 // Chunked scan.  `mode_raw` selects the mamba3_scan prologue (a, g, w built
 // from dt, lambda, a_log) versus ssd_chunked's precomputed a, g, w.

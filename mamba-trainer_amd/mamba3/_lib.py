@@ -40,6 +40,11 @@ class SsmStateC(C.Structure):
     _fields_ = [("h", _P), ("last_u", _P), ("angle", _P)]
 
 
+class SsmStateFactoredC(C.Structure):
+    """m3_ssm_state_factored."""
+    _fields_ = [("h", _P), ("x_prev", _P), ("b_prev", _P), ("angle", _P)]
+
+
 class ScanInputsC(C.Structure):
     _fields_ = [
         ("batch", _Z), ("seq", _Z), ("heads", _Z), ("head_dim", _Z), ("d_state", _Z),
@@ -110,6 +115,7 @@ SIGNATURES = {
     "m3_scan_backward_workspace_bytes": (_Z, [C.POINTER(ScanInputsC)]),
     "m3_ssd_chunked": (C.c_int, [C.POINTER(SsdArgsC), _P, _P, _P]),
     "m3_step": (C.c_int, [C.POINTER(StepInputsC), C.POINTER(SsmStateC), _P, _P]),
+    "m3_step_factored": (C.c_int, [C.POINTER(StepInputsC), C.POINTER(SsmStateFactoredC), _P, _P]),
     "m3_status_string": (C.c_char_p, [C.c_int]),
     "m3_last_error": (C.c_char_p, []),
     "m3_launch_count": (C.c_uint64, []),

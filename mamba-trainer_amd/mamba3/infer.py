@@ -5,14 +5,19 @@ field ([layers, B, H, P, N] f32 for h and last_u, [layers, B, H, N/2] for the
 angle), so the whole cache is two (three) contiguous HBM regions.  Steps run
 in place through mamba3_step_, which is what keeps decode at the 16 bytes per
 state element the recurrence needs.
+
+With `factored=True` the cache holds the second format instead (no reference
+counterpart): h plus the previous token's x [layers, B, H, P, R] and
+unrotated b [layers, B, H, N, R], last_u being that token's outer product;
+steps go through mamba3_step_factored_ and stream 8 bytes per state element.
 """
 from __future__ import annotations
 
-from typing import List, Optional
+from typing import List, Optional, Union
 
 import torch
 
-from .ssm.scan import SsmState, mamba3_step_
+from .ssm.scan import SsmState, SsmStateFactored, mamba3_step_, mamba3_step_factored_
 
 
 class StateCache:
@@ -20,37 +25,59 @@ class StateCache:
 
     def __init__(self, n_layers: int, batch: int, heads: int, head_dim: int, d_state: int,
                  rotational: bool, device, init_std: Optional[float] = None,
-                 generator: Optional[torch.Generator] = None):
+                 generator: Optional[torch.Generator] = None, factored: bool = False,
+                 rank: int = 1, dtype: torch.dtype = torch.bfloat16):
         shape = (n_layers, batch, heads, head_dim, d_state)
+        self.factored = factored
         if init_std is None:
             self.h = torch.zeros(shape, dtype=torch.float32, device=device)
-            self.last_u = torch.zeros(shape, dtype=torch.float32, device=device)
         else:
             self.h = torch.randn(shape, dtype=torch.float32, device=device,
                                  generator=generator) * init_std
+        self.last_u = self.x_prev = self.b_prev = None
+        if factored:
+            # a zero previous token (zero last_u); with init_std, random x and b
+            xs, bs = (n_layers, batch, heads, head_dim, rank), (n_layers, batch, heads, d_state, rank)
+            if init_std is None:
+                self.x_prev = torch.zeros(xs, dtype=dtype, device=device)
+                self.b_prev = torch.zeros(bs, dtype=dtype, device=device)
+            else:
+                self.x_prev = torch.randn(xs, device=device, generator=generator).to(dtype)
+                self.b_prev = (torch.randn(bs, device=device, generator=generator)
+                               / d_state ** 0.5).to(dtype)
+        elif init_std is None:
+            self.last_u = torch.zeros(shape, dtype=torch.float32, device=device)
+        else:
             self.last_u = torch.randn(shape, dtype=torch.float32, device=device,
                                       generator=generator) * init_std
         self.angle = (torch.zeros((n_layers, batch, heads, d_state // 2), dtype=torch.float32,
                                   device=device) if rotational else None)
-        self._layers: List[SsmState] = [
-            SsmState(self.h[i], self.last_u[i], None if self.angle is None else self.angle[i])
-            for i in range(n_layers)]
+        ang = lambda i: None if self.angle is None else self.angle[i]
+        if factored:
+            self._layers = [SsmStateFactored(self.h[i], self.x_prev[i], self.b_prev[i], ang(i))
+                            for i in range(n_layers)]
+        else:
+            self._layers = [SsmState(self.h[i], self.last_u[i], ang(i)) for i in range(n_layers)]
         self._position = 0
 
     def position(self) -> int:
         """Number of tokens consumed so far."""
         return self._position
 
-    def layers_mut(self) -> List[SsmState]:
+    def layers_mut(self) -> List[Union[SsmState, SsmStateFactored]]:
         return self._layers
 
     def advance(self, tokens: int) -> None:
         self._position += tokens
 
     def num_bytes(self) -> int:
-        n = self.h.numel() + self.last_u.numel() + (0 if self.angle is None else self.angle.numel())
-        return 4 * n
+        n = 4 * (self.h.numel() + (0 if self.angle is None else self.angle.numel()))
+        if self.factored:
+            return n + self.x_prev.numel() * self.x_prev.element_size() + \
+                self.b_prev.numel() * self.b_prev.element_size()
+        return n + 4 * self.last_u.numel()
 
     def step_layer(self, layer: int, x, b, c, dt, lam, a_log, theta=None, d_skip=None):
         """mamba3_step on one layer's slot, in place; returns y [B, H, P, R]."""
-        return mamba3_step_(x, b, c, dt, lam, a_log, theta, d_skip, self._layers[layer])
+        step = mamba3_step_factored_ if self.factored else mamba3_step_
+        return step(x, b, c, dt, lam, a_log, theta, d_skip, self._layers[layer])

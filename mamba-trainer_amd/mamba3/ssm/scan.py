@@ -430,6 +430,70 @@ def mamba3_step_(x, b, c, dt, lam, a_log, theta, d_skip, state: SsmState) -> tor
     return y
 
 
+@dataclass
+class SsmStateFactored:
+    """The decode cache with last_u factored (m3_ssm_state_factored; no
+    reference counterpart).  last_u is always the last token's outer product
+    sum_r x_r B~_r^T (scan.rs:599-618, 683-691), so the state keeps that
+    token's x [B, H, P, R] and unrotated b [B, H, N, R] (in the inputs'
+    dtype) with h and the angle, and a step streams h alone."""
+    h: torch.Tensor
+    x_prev: torch.Tensor
+    b_prev: torch.Tensor
+    angle: Optional[torch.Tensor] = None
+
+    @staticmethod
+    def zeros(batch, heads, head_dim, d_state, rank, rotational, device,
+              dtype=torch.bfloat16) -> "SsmStateFactored":
+        return SsmStateFactored(
+            torch.zeros((batch, heads, head_dim, d_state), dtype=torch.float32, device=device),
+            torch.zeros((batch, heads, head_dim, rank), dtype=dtype, device=device),
+            torch.zeros((batch, heads, d_state, rank), dtype=dtype, device=device),
+            torch.zeros((batch, heads, d_state // 2), dtype=torch.float32, device=device)
+            if rotational else None)
+
+    @staticmethod
+    def after_window(inputs: "ScanInputs", out: "ScanOutput") -> "SsmStateFactored":
+        """The factored state a window leaves: the scan's h and angle, and
+        the window's last x and b (copies)."""
+        st = out.state
+        return SsmStateFactored(st.h, inputs.x[:, -1].contiguous(), inputs.b[:, -1].contiguous(),
+                                st.angle)
+
+    def clone(self) -> "SsmStateFactored":
+        return SsmStateFactored(self.h.clone(), self.x_prev.clone(), self.b_prev.clone(),
+                                None if self.angle is None else self.angle.clone())
+
+
+def mamba3_step_factored_(x, b, c, dt, lam, a_log, theta, d_skip,
+                          state: SsmStateFactored) -> torch.Tensor:
+    """mamba3_step on the factored cache, in place (m3_step_factored);
+    returns y.  Equal to mamba3_step_ on the full state it stands for."""
+    args, keep = _step_args(x, b, c, dt, lam, a_log, theta, d_skip)
+    B, H, P, R = keep[0].shape
+    N = keep[1].shape[2]
+    t = state.h
+    if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+        raise ArgumentError("state.h must be a contiguous float32 device tensor")
+    _expect_shape(t, (B, H, P, N), "state.h")
+    for t, shape, what in ((state.x_prev, (B, H, P, R), "state.x_prev"),
+                           (state.b_prev, (B, H, N, R), "state.b_prev")):
+        if t.dtype != keep[0].dtype or not t.is_contiguous() or not t.is_cuda:
+            raise ArgumentError(f"{what} must be a contiguous {keep[0].dtype} device tensor")
+        _expect_shape(t, shape, what)
+    if theta is not None:
+        if state.angle is None:
+            raise ArgumentError("theta needs the state's angle tensor (updated in place)")
+        _expect_shape(state.angle, (B, H, N // 2), "state.angle")
+    y = torch.empty_like(keep[0])
+    st_c = _lib.SsmStateFactoredC(state.h.data_ptr(), state.x_prev.data_ptr(),
+                                  state.b_prev.data_ptr(),
+                                  None if theta is None else state.angle.data_ptr())
+    _lib.check(_lib.lib().m3_step_factored(C.byref(args), C.byref(st_c), C.c_void_p(y.data_ptr()),
+                                           _stream(keep[0])))
+    return y
+
+
 def mamba3_step(x, b, c, dt, lam, a_log, theta, d_skip,
                 state: SsmState) -> Tuple[torch.Tensor, SsmState]:
     """scan.rs:640-712: one decoding step; returns (y, new SsmState) like the reference."""

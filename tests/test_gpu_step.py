@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from cases import Case, assert_close, rel_l2
+from cases import Case, assert_close, baseline_inputs, rel_l2
 from gpu_util import dev, host
 
 pytestmark = pytest.mark.gpu
@@ -125,6 +125,144 @@ def test_config3_shape_one_layer_many_steps():
         assert rel_l2(host(y), yo) <= F32_TOL, step
     assert rel_l2(host(state.h), ho) <= F32_TOL
     assert rel_l2(host(state.last_u), luo) <= F32_TOL
+
+
+# ------------------------------------------------------------------ factored last_u
+def _step_inputs(rng, B, H, P, N, R, theta, dtype):
+    f = np.float32
+    x = rng.standard_normal((B, H, P, R), dtype=f)
+    b = (rng.standard_normal((B, H, N, R), dtype=f) / f(math.sqrt(N))).astype(f)
+    c = (rng.standard_normal((B, H, N, R), dtype=f) / f(math.sqrt(N))).astype(f)
+    th = rng.uniform(0, math.pi, (B, H, N // 2)).astype(f) if theta else None
+    dt = np.clip(np.log1p(np.exp(rng.standard_normal((B, H)) - 3)), 1e-3, 0.1).astype(f)
+    lam = (1 / (1 + np.exp(-rng.standard_normal((B, H))))).astype(f)
+    st = torch.bfloat16 if dtype == "bf16" else torch.float32
+    return (dev(x).to(st), dev(b).to(st), dev(c).to(st), dev(dt), dev(lam),
+            None if th is None else dev(th).to(st))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("B,H,P,N,R,theta,skip", [(3, 2, 64, 128, 1, True, True),
+                                                   (2, 3, 16, 32, 2, True, False),
+                                                   (2, 2, 8, 16, 4, False, True),
+                                                   (1, 2, 24, 64, 8, True, True),
+                                                   (2, 1, 5, 4, 3, True, False)])
+def test_factored_step_equals_the_full_step_bit_for_bit(B, H, P, N, R, theta, skip, dtype):
+    """m3_step_factored against m3_step over five steps from the same state
+    (last_u zero, the previous token zero): y, h and the angle equal bit for
+    bit at every step (the factored form forms last_u from the same f32
+    products the full form stored), and x_prev / b_prev hold the last
+    token's x and b."""
+    from mamba3.ssm import SsmState, SsmStateFactored, mamba3_step_, mamba3_step_factored_
+    rng = np.random.default_rng(B * 100 + N + R)
+    f = np.float32
+    st = torch.bfloat16 if dtype == "bf16" else torch.float32
+    h0 = dev((rng.standard_normal((B, H, P, N), dtype=f) * f(0.1)).astype(f))
+    ang = dev(rng.uniform(-math.pi, math.pi, (B, H, N // 2)).astype(f)) if theta else None
+    full = SsmState(h0.clone(), torch.zeros_like(h0), None if ang is None else ang.clone())
+    fac = SsmStateFactored.zeros(B, H, P, N, R, theta, "cuda", dtype=st)
+    fac.h.copy_(h0)
+    if theta:
+        fac.angle.copy_(ang)
+    a_log = dev(rng.uniform(0, math.log(16), H).astype(f))
+    d_skip = dev(rng.uniform(0.5, 1.5, H).astype(f)) if skip else None
+    for step in range(5):
+        x, b, c, dt, lam, th = _step_inputs(rng, B, H, P, N, R, theta, dtype)
+        y1 = mamba3_step_(x, b, c, dt, lam, a_log, th, d_skip, full)
+        y2 = mamba3_step_factored_(x, b, c, dt, lam, a_log, th, d_skip, fac)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), step
+        assert torch.equal(full.h, fac.h), step
+        if theta:
+            assert torch.equal(full.angle, fac.angle), step
+        assert torch.equal(fac.x_prev, x) and torch.equal(fac.b_prev, b), step
+
+
+def test_factored_step_continues_a_window():
+    """A window through m3_scan, then steps: from SsmStateFactored.after_window
+    (the scan's h and angle, the window's last x and b) the factored steps
+    follow the full steps from the scan's own state (whose last_u the scan
+    formed from the same token)."""
+    from mamba3.ssm import (ScanInputs, SsmStateFactored, mamba3_scan, mamba3_step_,
+                            mamba3_step_factored_)
+    rng = np.random.default_rng(5)
+    inp = baseline_inputs(rng, 2, 130, 3, 64, 128, 1, theta=True, dtype="bf16")
+    st = torch.bfloat16
+    si = (ScanInputs(dev(inp["x"]).to(st), dev(inp["b"]).to(st), dev(inp["c"]).to(st),
+                     dev(inp["dt"]), dev(inp["a_log"]), dev(inp["lam"]))
+          .with_theta(dev(inp["theta"]).to(st)).with_state_output(True))
+    out = mamba3_scan(si)
+    full = out.state.clone()
+    fac = SsmStateFactored.after_window(si, out).clone()
+    assert torch.equal(fac.x_prev, si.x[:, -1]) and torch.equal(fac.b_prev, si.b[:, -1])
+    for step in range(4):
+        x, b, c, dt, lam, th = _step_inputs(rng, 2, 3, 64, 128, 1, True, "bf16")
+        y1 = mamba3_step_(x, b, c, dt, lam, si.a_log, th, None, full)
+        y2 = mamba3_step_factored_(x, b, c, dt, lam, si.a_log, th, None, fac)
+        assert rel_l2(host(y2), host(y1)) <= 1e-5, step
+        assert rel_l2(host(fac.h), host(full.h)) <= 1e-5, step
+
+
+def test_factored_step_config3_shape_against_oracle():
+    """The config-3 layer shape (batch 256, 24 heads, P64, N128, bf16 inputs):
+    eight factored steps against the f32 restatement of mamba3_step carrying
+    the full last_u, from h ~ N(0, 0.1) and last_u zero."""
+    from mamba3.ssm import SsmStateFactored, mamba3_step_factored_
+    B, H, P, N = 256, 24, 64, 128
+    rng = np.random.default_rng(33)
+    f = np.float32
+    h = (rng.standard_normal((B, H, P, N), dtype=f) * f(0.1)).astype(f)
+    ang = rng.uniform(-math.pi, math.pi, (B, H, N // 2)).astype(f)
+    a_log = rng.uniform(0, math.log(16), H).astype(f)
+    d_skip = np.ones(H, f)
+    fac = SsmStateFactored.zeros(B, H, P, N, 1, True, "cuda")
+    fac.h.copy_(dev(h))
+    fac.angle.copy_(dev(ang))
+    ho, luo, ango = h.copy(), np.zeros_like(h), ang.copy()
+    for step in range(8):
+        x, b, c, dt, lam, th = _step_inputs(rng, B, H, P, N, 1, True, "bf16")
+        y = mamba3_step_factored_(x, b, c, dt, lam, dev(a_log), th, dev(d_skip), fac)
+        yo, ho, luo, ango = oracle.step_f32(host(x), host(b), host(c), host(dt), host(lam), a_log,
+                                            host(th), d_skip, ho, luo, ango)
+        assert rel_l2(host(y), yo) <= 1e-2, step
+    assert rel_l2(host(fac.h), ho) <= 1e-5
+
+
+def test_factored_step_errors():
+    import ctypes as C
+    from mamba3 import _lib
+    from mamba3.error import ArgumentError, UnsupportedError
+    from mamba3.ssm import SsmStateFactored, mamba3_step_factored_
+    rng = np.random.default_rng(1)
+    x, b, c, dt, lam, th = _step_inputs(rng, 2, 2, 8, 12, 1, True, "f32")
+    a_log = dev(np.zeros(2, np.float32))
+    fac = SsmStateFactored.zeros(2, 2, 8, 12, 1, True, "cuda", dtype=torch.float32)
+    with pytest.raises(UnsupportedError, match="factored step needs"):
+        mamba3_step_factored_(x, b, c, dt, lam, a_log, th, None, fac)   # d_state 12: 12/4 = 3
+    x, b, c, dt, lam, th = _step_inputs(rng, 2, 2, 8, 16, 1, True, "f32")
+    fac = SsmStateFactored.zeros(2, 2, 8, 16, 1, True, "cuda", dtype=torch.float32)
+    alias = SsmStateFactored(fac.h, x, fac.b_prev, fac.angle)          # x_prev is the input x
+    with pytest.raises(ArgumentError, match="must not overlap"):
+        mamba3_step_factored_(x, b, c, dt, lam, a_log, th, None, alias)
+
+
+def test_factored_state_cache_steps_like_the_full_one():
+    """StateCache(factored=True): three steps of layer 1 equal the full cache's
+    bit for bit (both from zero), and the other layers stay untouched."""
+    from mamba3 import StateCache
+    rng = np.random.default_rng(9)
+    full = StateCache(3, 2, 2, 16, 32, True, "cuda")
+    fac = StateCache(3, 2, 2, 16, 32, True, "cuda", factored=True, rank=1,
+                     dtype=torch.float32)
+    assert fac.num_bytes() < full.num_bytes()
+    a_log = dev(rng.uniform(0, 2, 2).astype(np.float32))
+    for _ in range(3):
+        x, b, c, dt, lam, th = _step_inputs(rng, 2, 2, 16, 32, 1, True, "f32")
+        y1 = full.step_layer(1, x, b, c, dt, lam, a_log, th)
+        y2 = fac.step_layer(1, x, b, c, dt, lam, a_log, th)
+        assert torch.equal(y1, y2)
+    assert torch.equal(full.h, fac.h) and torch.equal(full.angle, fac.angle)
+    assert not fac.h[0].any() and not fac.h[2].any()
 
 
 def test_state_cache_layers_are_independent():
