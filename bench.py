@@ -649,11 +649,38 @@ def bench_decode(torch, lib, L_, args, factored=False):
     assert torch.isfinite(h).all(), "non-finite decode state"
     nbytes = NL * (decode_factored_algorithmic if factored else decode_algorithmic)(B, H, P, N, R)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    # the same passes with all 24 layers in one launch (m3_step_layers)
+    tabs = []
+    for per in calls:
+        ins = (L_.StepInputsC * NL)(*[a for a, _ in per])
+        sts = ((L_.SsmStateFactoredC if factored else L_.SsmStateC) * NL)(*[s for _, s in per])
+        ysa = (C.c_void_p * NL)(*([y.data_ptr()] * NL))
+        tabs.append((ins, sts, ysa))
+    fl = lib.m3_step_layers
+
+    def step_one(i):
+        ins, sts, ysa = tabs[i % K]
+        st = (fl(NL, ins, None, sts, ysa, sp) if factored else fl(NL, ins, sts, None, ysa, sp))
+        if st != 0:
+            L_.check(st)
+
+    for i in range(args.decode_warmup):
+        step_one(i)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.decode_steps):
+        step_one(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_one = e0.elapsed_time(e1) / args.decode_steps
+    assert torch.isfinite(h).all(), "non-finite decode state"
     if factored:
         return dict(us_per_step=round(ms * 1e3, 2), steps=args.decode_steps, layers=NL,
                     bytes_per_step=nbytes, achieved_GBps=round(gbs, 1),
                     frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4),
                     us_per_layer=round(ms * 1e3 / NL, 2),
+                    us_per_step_one_launch=round(ms_one * 1e3, 2),
+                    frac_hbm_peak_one_launch=round(nbytes / (ms_one * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     cache="h f32 [B,H,P,N] + the previous token's x [B,H,P,R] and b [B,H,N,R] "
                           "(m3_step_factored; last_u formed in registers)")
     # a practical stream ceiling beside it: torch's device copy of one layer's
@@ -674,6 +701,9 @@ def bench_decode(torch, lib, L_, args, factored=False):
                 bytes_per_step=nbytes, achieved_GBps=round(gbs, 1),
                 frac_hbm_peak=round(gbs / HBM_PEAK_GBS, 4),
                 us_per_layer=round(ms * 1e3 / NL, 2),
+                launch="one m3_step launch per layer, 24 per pass",
+                us_per_step_one_launch=round(ms_one * 1e3, 2),
+                frac_hbm_peak_one_launch=round(nbytes / (ms_one * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 device_copy_GBps=round(copy_gbs, 1))
 
 

@@ -18,6 +18,8 @@
  *   m3_step_inputs / m3_step      mamba3_step               src/ssm/scan.rs:640-712
  *   m3_step_factored              the same on a cache with last_u factored (no
  *                                 reference counterpart; see its declaration)
+ *   m3_step_layers                several layers' steps in one launch (no
+ *                                 reference counterpart; see its declaration)
  *   m3_status / m3_last_error     Error / Result            src/error.rs:5-61
  *
  * Conventions
@@ -271,6 +273,19 @@ typedef struct m3_ssm_state_factored {
  * inputs. */
 m3_status m3_step_factored(const m3_step_inputs *in, m3_ssm_state_factored *state, void *y,
                            void *stream);
+
+/* n_layers steps in one launch (up to 24 layers a launch; more are split):
+ * layer l is m3_step(&inputs[l], &states[l], ys[l]) or, with `factored`
+ * instead of `states`, m3_step_factored(&inputs[l], &factored[l], ys[l]),
+ * with the same results bit for bit.  No reference counterpart (the
+ * reference steps each layer by itself): for callers that hold every
+ * layer's inputs at once, such as a benchmark over a whole cache.  All
+ * layers share batch, heads, head_dim, d_state, rank, dtype and whether
+ * theta and d_skip are given (else M3_ERR_SHAPE); the shapes are the
+ * factored step's (else M3_ERR_UNSUPPORTED).  Exactly one of states and
+ * factored is non-NULL. */
+m3_status m3_step_layers(size_t n_layers, const m3_step_inputs *inputs, m3_ssm_state *states,
+                         m3_ssm_state_factored *factored, void *const *ys, void *stream);
 
 /* Status name and this thread's last error message ("" after success). */
 const char *m3_status_string(m3_status status);

@@ -36,6 +36,17 @@ __device__ __forceinline__ float ld(const void *p, size_t i) {
     return to_f32(static_cast<const T *>(p)[i]);
 }
 
+// A pair rotated by -phi, (x1 cos + x2 sin, -x1 sin + x2 cos), with explicit
+// fused multiply-adds so that every instantiation rounds the same way (the
+// factored form rotates the previous token's B again and must reproduce the
+// B~ the step that took it used).
+__device__ __forceinline__ float rot_lo(float x1, float x2, float cs, float sn) {
+    return __builtin_fmaf(x1, cs, x2 * sn);
+}
+__device__ __forceinline__ float rot_hi(float x1, float x2, float cs, float sn) {
+    return __builtin_fmaf(x2, cs, -(x1 * sn));
+}
+
 // Prologue shared by both bodies: angle advance, rotation of B and C into
 // LDS (rank-last [N][R] layout kept), x into LDS, and the coefficients.
 template <typename T, bool FACT = false>
@@ -61,13 +72,14 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
             sincosf(phi, &sn, &cs);
             if constexpr (FACT) {
                 // the previous token's B~, rotated by the angle it was taken at
+                // with the roundings the previous step used (rot_lo / rot_hi)
                 float ps, pc;
                 sincosf(prev, &ps, &pc);
                 for (size_t r = 0; r < R; ++r) {
                     const float b1 = ld<T>(a.b_prev, bc_base + i * R + r);
                     const float b2 = ld<T>(a.b_prev, bc_base + (i + half) * R + r);
-                    bpt[i * R + r] = b1 * pc + b2 * ps;
-                    bpt[(i + half) * R + r] = -b1 * ps + b2 * pc;
+                    bpt[i * R + r] = rot_lo(b1, b2, pc, ps);
+                    bpt[(i + half) * R + r] = rot_hi(b1, b2, pc, ps);
                 }
             }
             for (size_t r = 0; r < R; ++r) {
@@ -76,10 +88,10 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
                 float c1 = ld<T>(a.c, bc_base + i * R + r);
                 float c2 = ld<T>(a.c, bc_base + (i + half) * R + r);
                 // rotation by -phi: (x1 cos + x2 sin, -x1 sin + x2 cos)
-                bt[i * R + r] = b1 * cs + b2 * sn;
-                bt[(i + half) * R + r] = -b1 * sn + b2 * cs;
-                ct[i * R + r] = c1 * cs + c2 * sn;
-                ct[(i + half) * R + r] = -c1 * sn + c2 * cs;
+                bt[i * R + r] = rot_lo(b1, b2, cs, sn);
+                bt[(i + half) * R + r] = rot_hi(b1, b2, cs, sn);
+                ct[i * R + r] = rot_lo(c1, c2, cs, sn);
+                ct[(i + half) * R + r] = rot_hi(c1, c2, cs, sn);
             }
         }
         // odd N: the unpaired last component is not rotated (N is even whenever
@@ -105,8 +117,7 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
 // Vector body: N % 4 == 0 and G = N / 4 lanes per row with G a power of two
 // that divides 64.  Each lane owns four consecutive state columns of a row.
 template <typename T, int RK, bool FACT>
-__global__ void __launch_bounds__(kStepThreads)
-step_kernel_vec(StepLaunch a) {
+__device__ __forceinline__ void step_body_vec(const StepLaunch &a, size_t bh) {
     extern __shared__ float smem[];
     const size_t N = a.d_state, P = a.head_dim;
     constexpr int R = RK;
@@ -115,7 +126,6 @@ step_kernel_vec(StepLaunch a) {
     float *xs = ct + N * R;
     float *bpt = xs + P * R;         // FACT: B~_prev [N][R], x_prev [P][R]
     float *xps = bpt + N * R;
-    const size_t bh = blockIdx.x;
     float alpha, beta, gamma;
     step_prologue<T, FACT>(a, bh, bt, ct, xs, alpha, beta, gamma, bpt, xps);
     __syncthreads();
@@ -183,24 +193,29 @@ step_kernel_vec(StepLaunch a) {
                 f32x4 hn, un;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    float u = 0.0f;
+                    // explicit fused multiply-adds: the rounding of u (stored as
+                    // last_u, or formed again by the factored form from the same
+                    // operands) and of h' must not depend on how the compiler
+                    // contracts each instantiation
+                    float u = xr[0] * bcol[j][0];
 #pragma unroll
-                    for (int r = 0; r < R; ++r) u += xr[r] * bcol[j][r];
+                    for (int r = 1; r < R; ++r) u = __builtin_fmaf(xr[r], bcol[j][r], u);
                     float lu;
                     if constexpr (FACT) {
                         // the previous step's u, the same products in the same order
-                        lu = 0.0f;
+                        lu = xq[0] * pcol[j][0];
 #pragma unroll
-                        for (int r = 0; r < R; ++r) lu += xq[r] * pcol[j][r];
+                        for (int r = 1; r < R; ++r) lu = __builtin_fmaf(xq[r], pcol[j][r], lu);
                     } else {
                         lu = lv[k][j];
                     }
                     // h' = h*alpha + last_u*beta + u*gamma   (fused.rs:1360-1362)
-                    float hnew = hv[k][j] * alpha + lu * beta + u * gamma;
+                    const float ha = hv[k][j] * alpha;
+                    float hnew = __builtin_fmaf(u, gamma, __builtin_fmaf(lu, beta, ha));
                     hn[j] = hnew;
                     un[j] = u;
 #pragma unroll
-                    for (int r = 0; r < R; ++r) ypart[r] += ccol[j][r] * hnew;
+                    for (int r = 0; r < R; ++r) ypart[r] = __builtin_fmaf(ccol[j][r], hnew, ypart[r]);
                 }
                 size_t idx = (static_cast<size_t>(p) * N + col4) / 4;
                 __builtin_nontemporal_store(hn, &h4[idx]);
@@ -212,10 +227,43 @@ step_kernel_vec(StepLaunch a) {
                 T *y = static_cast<T *>(a.y);
 #pragma unroll
                 for (int r = 0; r < R; ++r)
-                    y[(bh * P + p) * R + r] = from_f32<T>(ypart[r] + xs[p * R + r] * dskip);
+                    y[(bh * P + p) * R + r] = from_f32<T>(__builtin_fmaf(xs[p * R + r], dskip, ypart[r]));
             }
         }
     }
+}
+
+template <typename T, int RK, bool FACT>
+__global__ void __launch_bounds__(kStepThreads)
+step_kernel_vec(StepLaunch a) {
+    step_body_vec<T, RK, FACT>(a, blockIdx.x);
+}
+
+// Several layers' steps in one launch: workgroup w steps (batch, head)
+// w % (B H) of layer w / (B H), whose buffers the table names (the shapes are
+// the layers' common ones).
+template <typename T, int RK, bool FACT>
+__global__ void __launch_bounds__(kStepThreads)
+step_kernel_vec_layers(StepLaunch base, StepLayerTable t) {
+    const size_t per = base.batch * base.heads;
+    const size_t l = blockIdx.x / per;
+    StepLaunch a = base;
+    const StepLayer &L = t.layer[l];
+    a.x = L.x;
+    a.b = L.b;
+    a.c = L.c;
+    a.dt = L.dt;
+    a.lambda = L.lambda;
+    a.a_log = L.a_log;
+    a.theta = L.theta;
+    a.d_skip = L.d_skip;
+    a.h = L.h;
+    a.last_u = L.last_u;
+    a.angle = L.angle;
+    a.y = L.y;
+    a.x_prev = L.x_prev;
+    a.b_prev = L.b_prev;
+    step_body_vec<T, RK, FACT>(a, blockIdx.x - l * per);
 }
 
 // Generic body for shapes the vector body does not cover (odd N, N > 256,
@@ -286,7 +334,45 @@ hipError_t dispatch(const StepLaunch &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <typename T, int RK>
+hipError_t launch_vec_layers(const StepLaunch &a, const StepLayerTable &t, size_t n, size_t smem,
+                             hipStream_t s) {
+    const dim3 grid(static_cast<unsigned int>(n * a.batch * a.heads));
+    if (a.last_u == nullptr)
+        hipLaunchKernelGGL((step_kernel_vec_layers<T, RK, true>), grid, dim3(kStepThreads), smem, s,
+                           a, t);
+    else
+        hipLaunchKernelGGL((step_kernel_vec_layers<T, RK, false>), grid, dim3(kStepThreads), smem,
+                           s, a, t);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t dispatch_layers(const StepLaunch &a, const StepLayerTable &t, size_t n, hipStream_t s) {
+    const size_t N = a.d_state, R = a.rank;
+    const bool fact = a.last_u == nullptr;
+    const size_t smem = ((fact ? 3 : 2) * N * R + (fact ? 2 : 1) * a.head_dim * R) * sizeof(float);
+    switch (R) {
+        case 1: return launch_vec_layers<T, 1>(a, t, n, smem, s);
+        case 2: return launch_vec_layers<T, 2>(a, t, n, smem, s);
+        case 3: return launch_vec_layers<T, 3>(a, t, n, smem, s);
+        case 4: return launch_vec_layers<T, 4>(a, t, n, smem, s);
+        case 8: return launch_vec_layers<T, 8>(a, t, n, smem, s);
+        default: return hipErrorNotSupported;
+    }
+}
+
 }  // namespace
+
+bool step_layers_supported(size_t d_state, size_t rank) { return step_factored_supported(d_state, rank); }
+
+hipError_t launch_step_layers(const StepLaunch &a, const StepLayerTable &t, size_t n,
+                              hipStream_t stream) {
+    if (n == 0 || a.batch * a.heads == 0) return hipSuccess;
+    if (n > kStepLayersPerLaunch || !step_layers_supported(a.d_state, a.rank))
+        return hipErrorNotSupported;
+    return a.bf16 ? dispatch_layers<bf16_t>(a, t, n, stream) : dispatch_layers<float>(a, t, n, stream);
+}
 
 bool step_factored_supported(size_t d_state, size_t rank) {
     const size_t G = d_state / 4;

@@ -532,25 +532,59 @@ m3_status m3_ssd_chunked(const m3_ssd_args *in, void *y, float *final_state, voi
     return ok();
 }
 
-m3_status m3_step(const m3_step_inputs *in, m3_ssm_state *state, void *y, void *stream) {
-    if (in == nullptr || state == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/state are NULL");
+}  // extern "C"
+
+namespace {
+
+// Validates one step's arguments (the full state or, with fst, the factored
+// one) and fills `a`; *empty when there is nothing to launch (B H == 0).
+m3_status build_step(const m3_step_inputs *in, const m3_ssm_state *state,
+                     const m3_ssm_state_factored *fst, void *y, m3::StepLaunch &a, bool *empty) {
+    *empty = false;
+    if (in == nullptr || (state == nullptr && fst == nullptr))
+        return fail(M3_ERR_ARGUMENT, "inputs/state are NULL");
     if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
     if (in->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
     if (in->head_dim == 0 || in->d_state == 0)
         return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
     if (in->theta != nullptr && in->d_state % 2 != 0)
         return fail(M3_ERR_CONFIG, "rotational dynamics require an even d_state");
-    if (state->h == nullptr || state->last_u == nullptr)
+    if (fst != nullptr && !m3::step_factored_supported(in->d_state, in->rank))
+        return fail(M3_ERR_UNSUPPORTED, "the factored step needs d_state a multiple of 4 with "
+                    "d_state/4 a power of two up to 64 and rank 1, 2, 3, 4 or 8 (got %zu, %zu)",
+                    in->d_state, in->rank);
+    if (fst == nullptr && (state->h == nullptr || state->last_u == nullptr))
         return fail(M3_ERR_ARGUMENT, "state needs both h and last_u");
-    if (in->theta != nullptr && state->angle == nullptr)
+    if (fst != nullptr && (fst->h == nullptr || fst->x_prev == nullptr || fst->b_prev == nullptr))
+        return fail(M3_ERR_ARGUMENT, "the factored state needs h, x_prev and b_prev");
+    float *angle = fst ? fst->angle : state->angle;
+    if (in->theta != nullptr && angle == nullptr)
         return fail(M3_ERR_ARGUMENT, "theta needs the state's angle buffer (updated in place)");
-    if (in->batch * in->heads == 0) return ok();
+    if (in->batch * in->heads == 0) {
+        *empty = true;
+        return ok();
+    }
     if (in->x == nullptr || in->b == nullptr || in->c == nullptr || in->dt == nullptr ||
         in->lambda == nullptr || in->a_log == nullptr || y == nullptr)
         return fail(M3_ERR_ARGUMENT, "x, b, c, dt, lambda, a_log and y are required");
-    if (in->d_state * in->rank * 2 + in->head_dim * in->rank > 16384)
+    const size_t lds = fst ? in->d_state * in->rank * 3 + in->head_dim * in->rank * 2
+                           : in->d_state * in->rank * 2 + in->head_dim * in->rank;
+    if (lds > 16384)
         return fail(M3_ERR_UNSUPPORTED, "d_state/head_dim/rank too large for the step kernel");
-    m3::StepLaunch a{};
+    if (fst != nullptr) {
+        const size_t es = in->dtype == M3_BF16 ? 2 : 4;
+        const size_t xb = in->batch * in->heads * in->head_dim * in->rank * es;
+        const size_t bb = in->batch * in->heads * in->d_state * in->rank * es;
+        auto overlap = [](const void *p, size_t pn, const void *q, size_t qn) {
+            const uintptr_t u = reinterpret_cast<uintptr_t>(p), v = reinterpret_cast<uintptr_t>(q);
+            return u < v + qn && v < u + pn;
+        };
+        if (overlap(fst->x_prev, xb, in->x, xb) || overlap(fst->b_prev, bb, in->b, bb) ||
+            overlap(fst->x_prev, xb, in->b, bb) || overlap(fst->b_prev, bb, in->x, xb) ||
+            overlap(fst->x_prev, xb, fst->b_prev, bb))
+            return fail(M3_ERR_ARGUMENT, "x_prev and b_prev must not overlap each other or the inputs");
+    }
+    a = m3::StepLaunch{};
     a.batch = in->batch;
     a.heads = in->heads;
     a.head_dim = in->head_dim;
@@ -565,14 +599,29 @@ m3_status m3_step(const m3_step_inputs *in, m3_ssm_state *state, void *y, void *
     a.a_log = in->a_log;
     a.theta = in->theta;
     a.d_skip = in->d_skip;
-    a.h = state->h;
-    a.last_u = state->last_u;
-    a.angle = in->theta ? state->angle : nullptr;
+    a.h = fst ? fst->h : state->h;
+    a.last_u = fst ? nullptr : state->last_u;
+    a.x_prev = fst ? fst->x_prev : nullptr;
+    a.b_prev = fst ? fst->b_prev : nullptr;
+    a.angle = in->theta ? angle : nullptr;
     a.y = y;
     // the vector body issues 16-byte state accesses
-    const bool aligned = (reinterpret_cast<uintptr_t>(a.h) % 16 == 0) &&
-                         (reinterpret_cast<uintptr_t>(a.last_u) % 16 == 0);
-    if (!aligned) return fail(M3_ERR_ARGUMENT, "state buffers must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(a.h) % 16 != 0 ||
+        (a.last_u != nullptr && reinterpret_cast<uintptr_t>(a.last_u) % 16 != 0))
+        return fail(M3_ERR_ARGUMENT, "state buffers must be 16-byte aligned");
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+m3_status m3_step(const m3_step_inputs *in, m3_ssm_state *state, void *y, void *stream) {
+    m3::StepLaunch a;
+    bool empty = false;
+    if (state == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/state are NULL");
+    const m3_status st = build_step(in, state, nullptr, y, a, &empty);
+    if (st != M3_OK || empty) return st;
     hipError_t e = m3::launch_step(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "step launch");
     g_launches.fetch_add(1, std::memory_order_relaxed);
@@ -581,64 +630,69 @@ m3_status m3_step(const m3_step_inputs *in, m3_ssm_state *state, void *y, void *
 
 m3_status m3_step_factored(const m3_step_inputs *in, m3_ssm_state_factored *state, void *y,
                            void *stream) {
-    if (in == nullptr || state == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/state are NULL");
-    if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
-    if (in->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
-    if (in->head_dim == 0 || in->d_state == 0)
-        return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
-    if (in->theta != nullptr && in->d_state % 2 != 0)
-        return fail(M3_ERR_CONFIG, "rotational dynamics require an even d_state");
-    if (!m3::step_factored_supported(in->d_state, in->rank))
-        return fail(M3_ERR_UNSUPPORTED, "the factored step needs d_state a multiple of 4 with "
-                    "d_state/4 a power of two up to 64 and rank 1, 2, 3, 4 or 8 (got %zu, %zu)",
-                    in->d_state, in->rank);
-    if (state->h == nullptr || state->x_prev == nullptr || state->b_prev == nullptr)
-        return fail(M3_ERR_ARGUMENT, "the factored state needs h, x_prev and b_prev");
-    if (in->theta != nullptr && state->angle == nullptr)
-        return fail(M3_ERR_ARGUMENT, "theta needs the state's angle buffer (updated in place)");
-    if (in->batch * in->heads == 0) return ok();
-    if (in->x == nullptr || in->b == nullptr || in->c == nullptr || in->dt == nullptr ||
-        in->lambda == nullptr || in->a_log == nullptr || y == nullptr)
-        return fail(M3_ERR_ARGUMENT, "x, b, c, dt, lambda, a_log and y are required");
-    if (in->d_state * in->rank * 3 + in->head_dim * in->rank * 2 > 16384)
-        return fail(M3_ERR_UNSUPPORTED, "d_state/head_dim/rank too large for the step kernel");
-    const size_t es = in->dtype == M3_BF16 ? 2 : 4;
-    const size_t xb = in->batch * in->heads * in->head_dim * in->rank * es;
-    const size_t bb = in->batch * in->heads * in->d_state * in->rank * es;
-    auto overlap = [](const void *p, size_t pn, const void *q, size_t qn) {
-        const uintptr_t a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(q);
-        return a < b + qn && b < a + pn;
-    };
-    if (overlap(state->x_prev, xb, in->x, xb) || overlap(state->b_prev, bb, in->b, bb) ||
-        overlap(state->x_prev, xb, in->b, bb) || overlap(state->b_prev, bb, in->x, xb) ||
-        overlap(state->x_prev, xb, state->b_prev, bb))
-        return fail(M3_ERR_ARGUMENT, "x_prev and b_prev must not overlap each other or the inputs");
-    m3::StepLaunch a{};
-    a.batch = in->batch;
-    a.heads = in->heads;
-    a.head_dim = in->head_dim;
-    a.d_state = in->d_state;
-    a.rank = in->rank;
-    a.bf16 = in->dtype == M3_BF16;
-    a.x = in->x;
-    a.b = in->b;
-    a.c = in->c;
-    a.dt = in->dt;
-    a.lambda = in->lambda;
-    a.a_log = in->a_log;
-    a.theta = in->theta;
-    a.d_skip = in->d_skip;
-    a.h = state->h;
-    a.last_u = nullptr;
-    a.x_prev = state->x_prev;
-    a.b_prev = state->b_prev;
-    a.angle = in->theta ? state->angle : nullptr;
-    a.y = y;
-    if (reinterpret_cast<uintptr_t>(a.h) % 16 != 0)
-        return fail(M3_ERR_ARGUMENT, "state buffers must be 16-byte aligned");
+    m3::StepLaunch a;
+    bool empty = false;
+    if (state == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/state are NULL");
+    const m3_status st = build_step(in, nullptr, state, y, a, &empty);
+    if (st != M3_OK || empty) return st;
     hipError_t e = m3::launch_step(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "step launch");
     g_launches.fetch_add(1, std::memory_order_relaxed);
+    return ok();
+}
+
+m3_status m3_step_layers(size_t n_layers, const m3_step_inputs *inputs, m3_ssm_state *states,
+                         m3_ssm_state_factored *factored, void *const *ys, void *stream) {
+    if (n_layers == 0) return ok();
+    if (inputs == nullptr || ys == nullptr || (states == nullptr) == (factored == nullptr))
+        return fail(M3_ERR_ARGUMENT, "m3_step_layers needs inputs, ys and exactly one of "
+                    "states / factored");
+    m3::StepLaunch base{};
+    m3::StepLayerTable table{};
+    size_t n = 0;
+    for (size_t l = 0; l < n_layers; ++l) {
+        const m3_step_inputs &in = inputs[l];
+        const m3_step_inputs &in0 = inputs[0];
+        if (in.batch != in0.batch || in.heads != in0.heads || in.head_dim != in0.head_dim ||
+            in.d_state != in0.d_state || in.rank != in0.rank || in.dtype != in0.dtype ||
+            (in.theta == nullptr) != (in0.theta == nullptr) ||
+            (in.d_skip == nullptr) != (in0.d_skip == nullptr))
+            return fail(M3_ERR_SHAPE, "layer %zu's shapes, dtype or theta / d_skip presence differ "
+                        "from layer 0's", l);
+        if (!m3::step_layers_supported(in.d_state, in.rank))
+            return fail(M3_ERR_UNSUPPORTED, "m3_step_layers covers d_state a multiple of 4 with "
+                        "d_state/4 a power of two up to 64 and rank 1, 2, 3, 4 or 8");
+    }
+    for (size_t l = 0; l < n_layers; ++l) {
+        m3::StepLaunch a;
+        bool empty = false;
+        const m3_status st = build_step(&inputs[l], states ? &states[l] : nullptr,
+                                        factored ? &factored[l] : nullptr, ys[l], a, &empty);
+        if (st != M3_OK) return st;
+        if (empty) return ok();
+        if (n == 0) base = a;
+        m3::StepLayer &L = table.layer[n++];
+        L.x = a.x;
+        L.b = a.b;
+        L.c = a.c;
+        L.dt = a.dt;
+        L.lambda = a.lambda;
+        L.a_log = a.a_log;
+        L.theta = a.theta;
+        L.d_skip = a.d_skip;
+        L.h = a.h;
+        L.last_u = a.last_u;
+        L.angle = a.angle;
+        L.y = a.y;
+        L.x_prev = a.x_prev;
+        L.b_prev = a.b_prev;
+        if (n == m3::kStepLayersPerLaunch || l + 1 == n_layers) {
+            hipError_t e = m3::launch_step_layers(base, table, n, static_cast<hipStream_t>(stream));
+            if (e != hipSuccess) return hip_fail(e, "step launch");
+            g_launches.fetch_add(1, std::memory_order_relaxed);
+            n = 0;
+        }
+    }
     return ok();
 }
 

@@ -26,6 +26,24 @@ struct StepLaunch {
 hipError_t launch_step(const StepLaunch &a, hipStream_t stream);
 // Shapes the factored form (last_u null) covers: the vector body's.
 bool step_factored_supported(size_t d_state, size_t rank);
+// Several layers' steps in one launch: per-layer buffers in a table passed by
+// value (kernel arguments), the shapes shared.
+struct StepLayer {
+    const void *x, *b, *c;
+    const float *dt, *lambda, *a_log;
+    const void *theta;
+    const float *d_skip;
+    float *h, *last_u, *angle;
+    void *y;
+    void *x_prev, *b_prev;
+};
+constexpr size_t kStepLayersPerLaunch = 24;
+struct StepLayerTable {
+    StepLayer layer[kStepLayersPerLaunch];
+};
+bool step_layers_supported(size_t d_state, size_t rank);
+hipError_t launch_step_layers(const StepLaunch &a, const StepLayerTable &t, size_t n,
+                              hipStream_t stream);
 
 // Chunked scan.  `mode_raw` selects the mamba3_scan prologue (a, g, w built
 // from dt, lambda, a_log) versus ssd_chunked's precomputed a, g, w.

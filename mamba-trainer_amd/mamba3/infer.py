@@ -17,6 +17,7 @@ from typing import List, Optional, Union
 
 import torch
 
+from .error import ArgumentError
 from .ssm.scan import SsmState, SsmStateFactored, mamba3_step_, mamba3_step_factored_
 
 
@@ -76,6 +77,37 @@ class StateCache:
             return n + self.x_prev.numel() * self.x_prev.element_size() + \
                 self.b_prev.numel() * self.b_prev.element_size()
         return n + 4 * self.last_u.numel()
+
+    def step_all(self, inputs) -> List[torch.Tensor]:
+        """One step of every layer in one launch (m3_step_layers), in place:
+        inputs[l] = (x, b, c, dt, lam, a_log, theta, d_skip) of layer l, all
+        of one shape.  Returns each layer's y; the same results as
+        step_layer on each layer in turn."""
+        import ctypes as C
+        from . import _lib
+        from .ssm.scan import _step_args, _stream
+        if len(inputs) != len(self._layers):
+            raise ArgumentError(f"step_all needs one input tuple per layer "
+                                f"({len(self._layers)}), got {len(inputs)}")
+        n = len(inputs)
+        args = (_lib.StepInputsC * n)()
+        keep, ys = [], []
+        for l, inp in enumerate(inputs):
+            a, k = _step_args(*inp)
+            args[l] = a
+            keep.append(k)
+            ys.append(torch.empty_like(k[0]))
+        yp = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
+        st = self._layers
+        if self.factored:
+            fs = (_lib.SsmStateFactoredC * n)(*[_lib.SsmStateFactoredC(
+                s.h.data_ptr(), s.x_prev.data_ptr(), s.b_prev.data_ptr(),
+                None if s.angle is None else s.angle.data_ptr()) for s in st])
+            _lib.check(_lib.lib().m3_step_layers(n, args, None, fs, yp, _stream(ys[0])))
+        else:
+            ss = (_lib.SsmStateC * n)(*[s._c() for s in st])
+            _lib.check(_lib.lib().m3_step_layers(n, args, ss, None, yp, _stream(ys[0])))
+        return ys
 
     def step_layer(self, layer: int, x, b, c, dt, lam, a_log, theta=None, d_skip=None):
         """mamba3_step on one layer's slot, in place; returns y [B, H, P, R]."""

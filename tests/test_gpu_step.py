@@ -265,6 +265,58 @@ def test_factored_state_cache_steps_like_the_full_one():
     assert not fac.h[0].any() and not fac.h[2].any()
 
 
+@pytest.mark.parametrize("factored", [False, True])
+@pytest.mark.parametrize("layers,B,H,P,N,R", [(3, 4, 3, 64, 128, 1), (26, 2, 2, 8, 16, 2)])
+def test_all_layers_in_one_launch_equal_layer_by_layer(layers, B, H, P, N, R, factored):
+    """StateCache.step_all (m3_step_layers: every layer's step in one launch,
+    split at 24 layers) against step_layer on each layer in turn: y, h,
+    last_u (or the previous token) and the angle equal bit for bit over
+    three steps."""
+    from mamba3 import StateCache
+    rng = np.random.default_rng(layers + R)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    kw = dict(factored=True, rank=R, dtype=torch.float32) if factored else {}
+    one = StateCache(layers, B, H, P, N, True, "cuda", init_std=0.1, generator=g, **kw)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    per = StateCache(layers, B, H, P, N, True, "cuda", init_std=0.1, generator=g, **kw)
+    a_logs = [dev(rng.uniform(0, 2, H).astype(np.float32)) for _ in range(layers)]
+    skip = dev(np.ones(H, np.float32))
+    for _ in range(3):
+        inputs = []
+        for l in range(layers):
+            x, b, c, dt, lam, th = _step_inputs(rng, B, H, P, N, R, True, "f32")
+            inputs.append((x, b, c, dt, lam, a_logs[l], th, skip))
+        ys = one.step_all(inputs)
+        for l in range(layers):
+            y = per.step_layer(l, *inputs[l])
+            assert torch.equal(ys[l], y), l
+    assert torch.equal(one.h, per.h) and torch.equal(one.angle, per.angle)
+    if factored:
+        assert torch.equal(one.x_prev, per.x_prev) and torch.equal(one.b_prev, per.b_prev)
+    else:
+        assert torch.equal(one.last_u, per.last_u)
+
+
+def test_step_layers_rejects_mixed_shapes():
+    import ctypes as C
+    from mamba3 import _lib
+    from mamba3.error import ShapeError
+    from mamba3.ssm.scan import _step_args
+    rng = np.random.default_rng(2)
+    a_log = dev(np.zeros(2, np.float32))
+    args = (_lib.StepInputsC * 2)()
+    keep = []
+    for l, n in enumerate((16, 32)):
+        x, b, c, dt, lam, th = _step_inputs(rng, 2, 2, 8, n, 1, True, "f32")
+        a, k = _step_args(x, b, c, dt, lam, a_log, th, None)
+        args[l] = a
+        keep.append(k)
+    st = (_lib.SsmStateC * 2)()
+    ys = (C.c_void_p * 2)()
+    with pytest.raises(ShapeError, match="layer 1's shapes"):
+        _lib.check(_lib.lib().m3_step_layers(2, args, st, None, ys, None))
+
+
 def test_state_cache_layers_are_independent():
     """infer::StateCache: stepping one layer leaves the others untouched."""
     from mamba3 import StateCache
