@@ -493,6 +493,30 @@ def bench_decode_lm(torch, args):
     weights = NL * (d * width * 2 + width * 4 + d * d * 2 + d * 4) + d * p["vocab"] * 2
     nbytes = NL * decode_algorithmic(B, H, P, N, 1) + weights + B * p["vocab"] * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
+    # the same model on factored caches (h plus the previous token's x and b
+    # per layer; decode steps stream h only), as a graph replay
+    cache_f = lm.empty_cache(B, dev, factored=True)
+    for c in cache_f:
+        c.ssm.h.normal_(0.0, 0.1, generator=g)
+        c.ssm.x_prev.normal_(0.0, 1.0, generator=g)
+        c.ssm.b_prev.normal_(0.0, 1.0 / math.sqrt(N), generator=g)
+        c.ssm.angle.uniform_(-math.pi, math.pi, generator=g)
+    graph_f = lm.capture_decode(cache_f, B)
+    for i in range(2):
+        graph_f.step(ids[i])
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(steps):
+        logits = graph_f.step(ids[i % 16])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_f = e0.elapsed_time(e1) / steps
+    assert torch.isfinite(logits.float()).all(), "non-finite logits (factored caches)"
+    nbytes_f = NL * decode_factored_algorithmic(B, H, P, N, 1) + weights + B * p["vocab"] * 2
+    factored = {"us_per_step": round(ms_f * 1e3, 1), "tokens_per_s": round(B / (ms_f * 1e-3), 1),
+                "bytes_per_step": nbytes_f,
+                "frac_hbm_peak": round(nbytes_f / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "cache": "factored (Mamba3Lm.empty_cache(factored=True)), graph replay"}
     return {"workload": "Mamba3Lm decode step, batch 256 x 1 token, vocab 32000, d_model 1536, "
                         "24 layers x 24 heads x 64, N 128, groups 24, bc_norm, no conv, int8 "
                         "per-output-channel fake-quant projections, f32 state cache in place",
@@ -500,7 +524,8 @@ def bench_decode_lm(torch, args):
             "bytes_per_step": nbytes, "achieved_GBps": round(gbs, 1),
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "steps": steps,
             "launch": "one HIP graph replay per step (Mamba3Lm.capture_decode)",
-            "us_per_step_eager": round(ms_eager * 1e3, 1), "batch1": small}
+            "us_per_step_eager": round(ms_eager * 1e3, 1), "batch1": small,
+            "factored_cache": factored}
 
 
 # BASELINE configs 0 and 2 (parity cases; their forward scans are reported beside

@@ -20,6 +20,7 @@
  *                                 reference counterpart; see its declaration)
  *   m3_step_layers                several layers' steps in one launch (no
  *                                 reference counterpart; see its declaration)
+ *   m3_state_unfactor             the full last_u of a factored state
  *   m3_status / m3_last_error     Error / Result            src/error.rs:5-61
  *
  * Conventions
@@ -273,6 +274,15 @@ typedef struct m3_ssm_state_factored {
  * inputs. */
 m3_status m3_step_factored(const m3_step_inputs *in, m3_ssm_state_factored *state, void *y,
                            void *stream);
+
+/* The last_u [B, H, P, N] a factored state stands for:
+ * last_u = sum_r x_prev_r (R(-angle) b_prev_r)^T, with the roundings
+ * m3_step_factored uses (angle NULL: no rotation).  Callers that hand a
+ * factored cache to m3_scan (a window after decoding) rebuild the full state
+ * with it.  dtype is that of x_prev and b_prev. */
+m3_status m3_state_unfactor(size_t batch, size_t heads, size_t head_dim, size_t d_state,
+                            size_t rank, int32_t dtype, const void *x_prev, const void *b_prev,
+                            const float *angle, float *last_u, void *stream);
 
 /* n_layers steps in one launch (up to 24 layers a launch; more are split):
  * layer l is m3_step(&inputs[l], &states[l], ys[l]) or, with `factored`

@@ -362,7 +362,59 @@ hipError_t dispatch_layers(const StepLaunch &a, const StepLayerTable &t, size_t 
     }
 }
 
+// last_u = x_prev (R(-angle) b_prev)^T for one (batch, head): the full state a
+// factored one stands for.  One workgroup per (batch, head); the rotated b
+// goes through LDS with the roundings the step used for it.
+template <typename T>
+__global__ void __launch_bounds__(kStepThreads)
+unfactor_kernel(size_t heads, size_t P, size_t N, size_t R, const void *x_prev, const void *b_prev,
+                const float *angle, float *last_u) {
+    extern __shared__ float smem[];
+    float *bt = smem;             // [N][R]
+    float *xs = bt + N * R;       // [P][R]
+    const size_t bh = blockIdx.x;
+    const size_t half = N / 2;
+    const size_t base = bh * N * R;
+    for (size_t i = threadIdx.x; i < (angle ? half : N); i += kStepThreads) {
+        if (angle != nullptr) {
+            float sn, cs;
+            sincosf(angle[bh * half + i], &sn, &cs);
+            for (size_t r = 0; r < R; ++r) {
+                const float b1 = ld<T>(b_prev, base + i * R + r);
+                const float b2 = ld<T>(b_prev, base + (i + half) * R + r);
+                bt[i * R + r] = rot_lo(b1, b2, cs, sn);
+                bt[(i + half) * R + r] = rot_hi(b1, b2, cs, sn);
+            }
+        } else {
+            for (size_t r = 0; r < R; ++r) bt[i * R + r] = ld<T>(b_prev, base + i * R + r);
+        }
+    }
+    for (size_t i = threadIdx.x; i < P * R; i += kStepThreads) xs[i] = ld<T>(x_prev, bh * P * R + i);
+    __syncthreads();
+    float *lu = last_u + bh * P * N;
+    for (size_t e = threadIdx.x; e < P * N; e += kStepThreads) {
+        const size_t p = e / N, n = e % N;
+        float u = xs[p * R] * bt[n * R];
+        for (size_t r = 1; r < R; ++r) u = __builtin_fmaf(xs[p * R + r], bt[n * R + r], u);
+        lu[e] = u;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_unfactor(size_t batch, size_t heads, size_t P, size_t N, size_t R, bool bf16,
+                           const void *x_prev, const void *b_prev, const float *angle,
+                           float *last_u, hipStream_t s) {
+    if (batch * heads == 0) return hipSuccess;
+    const size_t smem = (N * R + P * R) * sizeof(float);
+    if (bf16)
+        hipLaunchKernelGGL(unfactor_kernel<bf16_t>, dim3(static_cast<unsigned int>(batch * heads)),
+                           dim3(kStepThreads), smem, s, heads, P, N, R, x_prev, b_prev, angle, last_u);
+    else
+        hipLaunchKernelGGL(unfactor_kernel<float>, dim3(static_cast<unsigned int>(batch * heads)),
+                           dim3(kStepThreads), smem, s, heads, P, N, R, x_prev, b_prev, angle, last_u);
+    return hipGetLastError();
+}
 
 bool step_layers_supported(size_t d_state, size_t rank) { return step_factored_supported(d_state, rank); }
 

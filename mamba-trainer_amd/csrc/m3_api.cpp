@@ -641,6 +641,27 @@ m3_status m3_step_factored(const m3_step_inputs *in, m3_ssm_state_factored *stat
     return ok();
 }
 
+m3_status m3_state_unfactor(size_t batch, size_t heads, size_t head_dim, size_t d_state,
+                            size_t rank, int32_t dtype, const void *x_prev, const void *b_prev,
+                            const float *angle, float *last_u, void *stream) {
+    if (!dtype_ok(dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", dtype);
+    if (head_dim == 0 || d_state == 0 || rank == 0)
+        return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
+    if (angle != nullptr && d_state % 2 != 0)
+        return fail(M3_ERR_CONFIG, "rotational dynamics require an even d_state");
+    if ((d_state + head_dim) * rank > 16384)
+        return fail(M3_ERR_UNSUPPORTED, "d_state/head_dim/rank too large for the step kernel");
+    if (batch * heads == 0) return ok();
+    if (x_prev == nullptr || b_prev == nullptr || last_u == nullptr)
+        return fail(M3_ERR_ARGUMENT, "x_prev, b_prev and last_u are required");
+    hipError_t e = m3::launch_unfactor(batch, heads, head_dim, d_state, rank, dtype == M3_BF16,
+                                       x_prev, b_prev, angle, last_u,
+                                       static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "unfactor launch");
+    g_launches.fetch_add(1, std::memory_order_relaxed);
+    return ok();
+}
+
 m3_status m3_step_layers(size_t n_layers, const m3_step_inputs *inputs, m3_ssm_state *states,
                          m3_ssm_state_factored *factored, void *const *ys, void *stream) {
     if (n_layers == 0) return ok();

@@ -42,6 +42,10 @@ struct StepLayerTable {
     StepLayer layer[kStepLayersPerLaunch];
 };
 bool step_layers_supported(size_t d_state, size_t rank);
+// last_u [B,H,P,N] = x_prev (R(-angle) b_prev)^T (angle null: no rotation).
+hipError_t launch_unfactor(size_t batch, size_t heads, size_t P, size_t N, size_t R, bool bf16,
+                           const void *x_prev, const void *b_prev, const float *angle,
+                           float *last_u, hipStream_t s);
 hipError_t launch_step_layers(const StepLaunch &a, const StepLayerTable &t, size_t n,
                               hipStream_t stream);
 

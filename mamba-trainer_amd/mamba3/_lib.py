@@ -116,6 +116,7 @@ SIGNATURES = {
     "m3_ssd_chunked": (C.c_int, [C.POINTER(SsdArgsC), _P, _P, _P]),
     "m3_step": (C.c_int, [C.POINTER(StepInputsC), C.POINTER(SsmStateC), _P, _P]),
     "m3_step_factored": (C.c_int, [C.POINTER(StepInputsC), C.POINTER(SsmStateFactoredC), _P, _P]),
+    "m3_state_unfactor": (C.c_int, [_Z, _Z, _Z, _Z, _Z, C.c_int32, _P, _P, _P, _P, _P]),
     "m3_step_layers": (C.c_int, [_Z, C.POINTER(StepInputsC), C.POINTER(SsmStateC),
                                  C.POINTER(SsmStateFactoredC), C.POINTER(_P), _P]),
     "m3_status_string": (C.c_char_p, [C.c_int]),

@@ -109,9 +109,11 @@ class Mamba3Lm:
         """lm.rs:319-327 (inference: no autodiff)."""
         return self.logits_from(self.hidden(ids))
 
-    def empty_cache(self, batch: int, device) -> List[Optional[MixerCache]]:
-        """lm.rs:330-335: one (zeroed) mixer cache per layer."""
-        return [mixer.empty_cache(batch, device) for _, mixer in self.layers]
+    def empty_cache(self, batch: int, device, factored: bool = False) -> List[Optional[MixerCache]]:
+        """lm.rs:330-335: one (zeroed) mixer cache per layer; factored=True
+        keeps each layer's state in the factored form (decode steps stream h
+        only; no reference counterpart)."""
+        return [mixer.empty_cache(batch, device, factored) for _, mixer in self.layers]
 
     def forward_cached(self, ids: torch.Tensor, cache: List[MixerCache]) -> torch.Tensor:
         """lm.rs:337-353 / hybrid.rs:424-493: a window or one token through the

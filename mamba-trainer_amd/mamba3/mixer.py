@@ -22,15 +22,19 @@ import torch
 from . import _lib
 from .error import ShapeError, UnsupportedError
 from .nn import Linear, RmsNorm, _bf16_dev, _stream, normal, residual_scaled, tensor_param
-from .ssm import ScanInputs, SsmConfig, SsmState, StateDynamics, mamba3_scan, mamba3_step_
+from .ssm import (ScanInputs, SsmConfig, SsmState, SsmStateFactored, StateDynamics, mamba3_scan,
+                  mamba3_step_, mamba3_step_factored_)
 
 
 @dataclasses.dataclass
 class MixerCache:
     """mamba3.rs:35-70: the scan state and, for a mixer with a convolution,
     its history, the last conv_kernel-1 convolution inputs [B, k-1, channels]
-    (bf16, copies of projection values)."""
-    ssm: SsmState
+    (bf16, copies of projection values).  `ssm` is an SsmState, or the
+    factored form (SsmStateFactored: last_u carried as the previous token's
+    x and b, no reference counterpart) when the cache was made with
+    factored=True."""
+    ssm: "SsmState | SsmStateFactored"
     conv: Optional[torch.Tensor] = None
 
     def clone(self) -> "MixerCache":
@@ -184,12 +188,16 @@ class Mamba3Mixer:
         return self.out_proj.apply(gated, residual=residual, out=out)
 
     # ------------------------------------------------------------ entry points
-    def empty_cache(self, batch: int, device) -> MixerCache:
-        """mamba3.rs:303-316: a zero state and, with a convolution, a zero history."""
+    def empty_cache(self, batch: int, device, factored: bool = False) -> MixerCache:
+        """mamba3.rs:303-316: a zero state and, with a convolution, a zero
+        history.  factored: the state in the factored form (decode steps
+        stream h only)."""
         c = self.cfg
-        return MixerCache(SsmState.zeros(batch, c.n_heads, c.head_dim, c.d_state,
-                                         c.dynamics == StateDynamics.Rotational, device),
-                          None if self.conv_weight is None else self._history(batch, device))
+        rot = c.dynamics == StateDynamics.Rotational
+        ssm = (SsmStateFactored.zeros(batch, c.n_heads, c.head_dim, c.d_state, c.mode.rank(), rot,
+                                      device, dtype=torch.bfloat16) if factored
+               else SsmState.zeros(batch, c.n_heads, c.head_dim, c.d_state, rot, device))
+        return MixerCache(ssm, None if self.conv_weight is None else self._history(batch, device))
 
     def apply(self, input: torch.Tensor, residual: Optional[torch.Tensor] = None,
               out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -212,11 +220,21 @@ class Mamba3Mixer:
             si = si.with_theta(proj.theta)
         if self.d_skip is not None:
             si = si.with_skip(self.d_skip)
+        factored = cache is not None and isinstance(cache.ssm, SsmStateFactored)
         if cache is not None:
-            si = si.with_state(cache.ssm)
+            si = si.with_state(cache.ssm.to_full() if factored else cache.ssm)
         scan = mamba3_scan(si)
         y = self.finish(scan.y, proj, residual=residual, out=out)
-        new = MixerCache(scan.state, new_hist) if cache is not None else None
+        new = None
+        if cache is not None:
+            st = scan.state
+            if factored and proj.x.shape[1] > 0:
+                # the window's last token carries last_u
+                st = SsmStateFactored(st.h, proj.x[:, -1].contiguous(), proj.b[:, -1].contiguous(),
+                                      st.angle)
+            elif factored:
+                st = cache.ssm
+            new = MixerCache(st, new_hist)
         return y, new
 
     def step_(self, input: torch.Tensor, cache: MixerCache,
@@ -233,8 +251,9 @@ class Mamba3Mixer:
             cache.conv = self._history(B, input.device)
         proj = self.project(input, cache.conv, cache.conv)
         sq = lambda t: None if t is None else t.reshape((B,) + tuple(t.shape[2:]))
-        y = mamba3_step_(sq(proj.x), sq(proj.b), sq(proj.c), sq(proj.dt), sq(proj.lam),
-                         self.a_log, sq(proj.theta), self.d_skip, cache.ssm)
+        step = mamba3_step_factored_ if isinstance(cache.ssm, SsmStateFactored) else mamba3_step_
+        y = step(sq(proj.x), sq(proj.b), sq(proj.c), sq(proj.dt), sq(proj.lam),
+                 self.a_log, sq(proj.theta), self.d_skip, cache.ssm)
         return self.finish(y.reshape(proj.x.shape), proj, residual=residual, out=out)
 
     def step(self, input: torch.Tensor, cache: MixerCache):

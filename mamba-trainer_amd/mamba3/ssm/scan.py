@@ -464,6 +464,19 @@ class SsmStateFactored:
         return SsmStateFactored(self.h.clone(), self.x_prev.clone(), self.b_prev.clone(),
                                 None if self.angle is None else self.angle.clone())
 
+    def to_full(self) -> SsmState:
+        """The reference-format SsmState this stands for (m3_state_unfactor
+        forms last_u = x_prev (R(-angle) b_prev)^T; h and the angle are
+        shared, not copied)."""
+        B, H, P, N = self.h.shape
+        R = self.x_prev.shape[-1]
+        last_u = torch.empty_like(self.h)
+        _lib.check(_lib.lib().m3_state_unfactor(
+            B, H, P, N, R, _dtype_code(self.x_prev), self.x_prev.data_ptr(),
+            self.b_prev.data_ptr(), None if self.angle is None else self.angle.data_ptr(),
+            last_u.data_ptr(), _stream(self.h)))
+        return SsmState(self.h, last_u, self.angle)
+
 
 def mamba3_step_factored_(x, b, c, dt, lam, a_log, theta, d_skip,
                           state: SsmStateFactored) -> torch.Tensor:

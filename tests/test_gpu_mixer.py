@@ -362,6 +362,34 @@ def test_cached_decoding_matches_the_parallel_pass_on_device(conv):
     assert rel_l2(step, ref) <= 1e-2
 
 
+@pytest.mark.parametrize("conv", [None, 4])
+def test_factored_cache_decodes_like_the_full_cache(conv):
+    """Mamba3Lm with factored caches (empty_cache(factored=True)): one token at
+    a time from empty caches gives the full caches' logits bit for bit (the
+    steps are the same arithmetic); a 5-token window then steps (the window
+    re-factors its state, the next step re-forms last_u) within 1e-3 of them,
+    and within the bf16 bar of the parallel pass."""
+    rng = np.random.default_rng(32)
+    model = mo.random_model(rng, vocab=16, d_model=32, n_layers=2, heads=2, head_dim=8,
+                            d_state=8, int8=True, bias_scale=0.3, conv_kernel=conv)
+    lm = gpu_lm_from_oracle(model, True)
+    seq = torch.tensor([[3, 1, 4, 1, 5, 9, 2, 6], [2, 7, 1, 8, 2, 8, 1, 8]], device=DEV)
+    full = host(lm.forward(seq))
+    outs = {}
+    for factored in (False, True):
+        for split in (0, 5):
+            cache = lm.empty_cache(2, DEV, factored=factored)
+            o = []
+            if split:
+                o.append(lm.forward_cached(seq[:, :split], cache).clone())
+            for t in range(split, seq.shape[1]):
+                o.append(lm.forward_cached(seq[:, t:t + 1], cache).clone())
+            outs[factored, split] = torch.cat(o, dim=1)
+    assert torch.equal(outs[True, 0], outs[False, 0])
+    assert rel_l2(host(outs[True, 5]), host(outs[False, 5])) <= 1e-3
+    assert rel_l2(host(outs[True, 5]), full) <= 1e-2
+
+
 def test_config4_layer_shapes_against_oracle():
     """One layer of BASELINE config 4 (d_model 768, 12 x 64 heads, N 128, groups
     12, int8 projections, bc_norm) at batch 2 x 256 tokens."""
@@ -435,8 +463,8 @@ def test_config4_full_model_split_prefill_property():
     assert torch.isfinite(full.float()).all()
 
 
-@pytest.mark.parametrize("conv", [None, 4])
-def test_decode_graph_replays_match_eager_steps(conv):
+@pytest.mark.parametrize("conv,factored", [(None, False), (4, False), (None, True)])
+def test_decode_graph_replays_match_eager_steps(conv, factored):
     """Mamba3Lm.capture_decode: a captured decode step replayed six times, with
     eager steps and host synchronisation between the replays; every replay's
     logits, states and convolution histories equal the eager step's bit for
@@ -448,10 +476,14 @@ def test_decode_graph_replays_match_eager_steps(conv):
     lm = gpu_lm_from_oracle(model, True)
     B = 8
     gen = torch.Generator(device=DEV).manual_seed(62)
-    cache_e = lm.empty_cache(B, DEV)
+    cache_e = lm.empty_cache(B, DEV, factored=factored)
     for c in cache_e:
         c.ssm.h.normal_(0.0, 0.1, generator=gen)
-        c.ssm.last_u.normal_(0.0, 0.1, generator=gen)
+        if factored:
+            c.ssm.x_prev.normal_(0.0, 1.0, generator=gen)
+            c.ssm.b_prev.normal_(0.0, 0.3, generator=gen)
+        else:
+            c.ssm.last_u.normal_(0.0, 0.1, generator=gen)
         c.ssm.angle.uniform_(-3.0, 3.0, generator=gen)
         if c.conv is not None:
             c.conv.normal_(0.0, 1.0, generator=gen)
@@ -470,7 +502,11 @@ def test_decode_graph_replays_match_eager_steps(conv):
         assert torch.equal(got, want), step
         for ce, cg in zip(cache_e, cache_g):
             assert torch.equal(ce.ssm.h, cg.ssm.h), step
-            assert torch.equal(ce.ssm.last_u, cg.ssm.last_u), step
+            if factored:
+                assert torch.equal(ce.ssm.x_prev, cg.ssm.x_prev), step
+                assert torch.equal(ce.ssm.b_prev, cg.ssm.b_prev), step
+            else:
+                assert torch.equal(ce.ssm.last_u, cg.ssm.last_u), step
             assert torch.equal(ce.ssm.angle, cg.ssm.angle), step
             assert conv is None or torch.equal(ce.conv, cg.conv), step
     assert torch.isfinite(got.float()).all()

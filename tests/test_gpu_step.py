@@ -228,6 +228,26 @@ def test_factored_step_config3_shape_against_oracle():
     assert rel_l2(host(fac.h), ho) <= 1e-5
 
 
+@pytest.mark.parametrize("theta", [True, False])
+def test_unfactored_last_u_equals_the_stored_one(theta):
+    """SsmStateFactored.to_full (m3_state_unfactor) after three steps gives
+    the last_u the full form stored, bit for bit."""
+    from mamba3.ssm import SsmState, SsmStateFactored, mamba3_step_, mamba3_step_factored_
+    rng = np.random.default_rng(12)
+    B, H, P, N, R = 3, 2, 16, 32, 2
+    full = SsmState.zeros(B, H, P, N, theta, "cuda")
+    fac = SsmStateFactored.zeros(B, H, P, N, R, theta, "cuda", dtype=torch.bfloat16)
+    a_log = dev(rng.uniform(0, 2, H).astype(np.float32))
+    for _ in range(3):
+        x, b, c, dt, lam, th = _step_inputs(rng, B, H, P, N, R, theta, "bf16")
+        mamba3_step_(x, b, c, dt, lam, a_log, th, None, full)
+        mamba3_step_factored_(x, b, c, dt, lam, a_log, th, None, fac)
+    back = fac.to_full()
+    torch.cuda.synchronize()
+    assert torch.equal(back.last_u, full.last_u)
+    assert torch.equal(back.h, full.h)
+
+
 def test_factored_step_errors():
     import ctypes as C
     from mamba3 import _lib
