@@ -457,6 +457,7 @@ def bench_decode_lm(torch, args):
     for i in range(2):
         graph.step(ids[i])
     torch.cuda.synchronize()
+    _pause_for_trace(args)
     e0.record(stream)
     for i in range(steps):
         logits = graph.step(ids[i % 16])
@@ -505,6 +506,7 @@ def bench_decode_lm(torch, args):
     for i in range(2):
         graph_f.step(ids[i])
     torch.cuda.synchronize()
+    _pause_for_trace(args)
     e0.record(stream)
     for i in range(steps):
         logits = graph_f.step(ids[i % 16])
