@@ -70,7 +70,11 @@ __device__ __forceinline__ float wave_inclusive_scan(float v, int lane) {
 // Inclusive scan over each aligned segment of SW lanes (SW = 16, 32 or 64):
 // DPP row_shr steps within 16-lane rows, then row_bcast:15 / row_bcast:31
 // carries across rows.  Lanes whose shifted source falls outside the row
-// read zero (bound_ctrl), rows masked out of a broadcast add zero.
+// read zero (bound_ctrl).  Each carry is one in-place DPP add under a row
+// mask (rows outside it keep their value), written out because the compiler
+// otherwise moves the broadcast into a zeroed temporary and adds it: three
+// instructions.  The s_nop 1 gives the two wait states a DPP read of a VGPR
+// that the previous VALU instruction wrote needs.
 template <int CTRL, int ROWM, bool BC>
 __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWM, 0xf, BC));
@@ -82,10 +86,46 @@ __device__ __forceinline__ float seg_scan(float v) {
     v += dpp_f<0x112, 0xf, true>(v);   // row_shr:2
     v += dpp_f<0x114, 0xf, true>(v);   // row_shr:4
     v += dpp_f<0x118, 0xf, true>(v);   // row_shr:8
-    if constexpr (SW >= 32) v += dpp_f<0x142, 0xa, false>(v);   // row_bcast:15 -> rows 1, 3
-    if constexpr (SW >= 64) v += dpp_f<0x143, 0xc, false>(v);   // row_bcast:31 -> rows 2, 3
+    if constexpr (SW == 32)   // row_bcast:15 -> rows 1, 3
+        asm("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf"
+            : "+v"(v));
+    if constexpr (SW == 64)   // then row_bcast:31 -> rows 2, 3
+        asm("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+            "s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf"
+            : "+v"(v));
     return v;
 }
+
+// Four independent seg_scans, interleaved step by step in one block: each
+// DPP add then reads a value written three instructions earlier, past the two
+// wait states it needs, so a single s_nop serves the four chains (the
+// compiler schedules DPP chains one after another, a nop between steps).
+#define M3_DPP4(CTRL)                                                                 \
+    "v_add_f32_dpp %0, %0, %0 " CTRL "\n\tv_add_f32_dpp %1, %1, %1 " CTRL "\n\t"     \
+    "v_add_f32_dpp %2, %2, %2 " CTRL "\n\tv_add_f32_dpp %3, %3, %3 " CTRL "\n\t"
+#define M3_SHR(n) "row_shr:" #n " row_mask:0xf bank_mask:0xf bound_ctrl:1"
+#define M3_BC15 "row_bcast:15 row_mask:0xa bank_mask:0xf"
+#define M3_BC31 "row_bcast:31 row_mask:0xc bank_mask:0xf"
+template <int SW>
+__device__ __forceinline__ void seg_scan4(float &a, float &b, float &c, float &d) {
+    static_assert(SW == 16 || SW == 32 || SW == 64, "segments of 16, 32 or 64 lanes");
+    if constexpr (SW == 16)
+        asm("s_nop 1\n\t" M3_DPP4(M3_SHR(1)) M3_DPP4(M3_SHR(2)) M3_DPP4(M3_SHR(4))
+                M3_DPP4(M3_SHR(8))
+            : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+    if constexpr (SW == 32)
+        asm("s_nop 1\n\t" M3_DPP4(M3_SHR(1)) M3_DPP4(M3_SHR(2)) M3_DPP4(M3_SHR(4))
+                M3_DPP4(M3_SHR(8)) M3_DPP4(M3_BC15)
+            : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+    if constexpr (SW == 64)
+        asm("s_nop 1\n\t" M3_DPP4(M3_SHR(1)) M3_DPP4(M3_SHR(2)) M3_DPP4(M3_SHR(4))
+                M3_DPP4(M3_SHR(8)) M3_DPP4(M3_BC15) M3_DPP4(M3_BC31)
+            : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+#undef M3_DPP4
+#undef M3_SHR
+#undef M3_BC15
+#undef M3_BC31
 
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
 __device__ __forceinline__ float group_sum(float v, int width) {

@@ -74,6 +74,17 @@ template <> __device__ __forceinline__ float welem<float>(const unsigned int *w,
     return __uint_as_float(w[i]);
 }
 
+// Element i of loaded vectors in the operand type, without arithmetic (a
+// bf16 element is its 16 raw bits, not a round trip through f32).
+template <typename T> __device__ __forceinline__ typename Op<T>::t op_elem(const u32x4 *v, int i);
+template <> __device__ __forceinline__ __bf16 op_elem<bf16_t>(const u32x4 *v, int i) {
+    const unsigned int w = v[i >> 3][(i >> 1) & 3];
+    return __builtin_bit_cast(__bf16, static_cast<unsigned short>((i & 1) ? (w >> 16) : w));
+}
+template <> __device__ __forceinline__ float op_elem<float>(const u32x4 *v, int i) {
+    return __uint_as_float(v[i >> 2][i & 3]);
+}
+
 template <typename O> __device__ __forceinline__ O to_op(float v);
 template <> __device__ __forceinline__ float to_op<float>(float v) { return v; }
 template <> __device__ __forceinline__ __bf16 to_op<__bf16>(float v) {
@@ -93,6 +104,20 @@ __device__ __forceinline__ int npos(int n) {
     return (n & ~31) | ((n & 12) << 1) | ((n & 16) >> 2) | (n & 3);
 }
 
+// Element (row, col) of an unpadded row-major operand tile of COLS columns
+// whose 16-byte groups are permuted per row by f(row) = (row & 7) ^
+// ((row >> 3) & 1).  An MFMA operand read takes one 16-byte group from each
+// of sixteen consecutive rows; f sends every eight of them to distinct groups
+// of a 128-byte window and all sixteen to distinct groups of a 256-byte one,
+// so the read is conflict-free with 32 or 64 banks, at no padding.  A row
+// written by the 64 lanes of a wave stays one contiguous row.
+template <typename O, int COLS>
+__device__ __forceinline__ int swz(int row, int col) {
+    constexpr int E = 16 / static_cast<int>(sizeof(O));
+    static_assert(COLS % (8 * E) == 0, "rows of whole 128-byte windows");
+    return row * COLS + (col ^ (((row & 7) ^ ((row >> 3) & 1)) * E));
+}
+
 // exp(clamp(d, -60, 0)), the scan's decay with its log floor (scan.rs:57,
 // fused.rs:2064).  bf16 storage takes the hardware exp2; f32 keeps expf.
 template <bool FAST>
@@ -100,6 +125,64 @@ __device__ __forceinline__ float dexp(float d) {
     d = fminf(fmaxf(d, -60.0f), 0.0f);
     if constexpr (FAST) return __builtin_amdgcn_exp2f(d * 1.44269504088896341f);
     return expf(d);
+}
+
+// The wrapped angle of one rotation pair at this lane's token, relative to
+// the segment start: the running angle entering the sub-chunk plus the
+// in-sub-chunk inclusive prefix `pre`.  The sub-chunk's last token (lane
+// QT - 1 of its token segment) carries it to the next sub-chunk.  With one
+// token segment per wave (UNI) every lane of the wave owns the same pair, so
+// the running angle is a wave-uniform value `run` (a scalar register, by a
+// readlane); otherwise it lives in LDS at `slot`, read and rewritten by the
+// one wave whose lanes own the pair (a wave's LDS accesses execute in order).
+template <bool UNI, int QT>
+__device__ __forceinline__ float pair_angle(float pre, float &run, float *slot, bool last_lane) {
+    if constexpr (UNI) {
+        const float phi = wrap_angle(run + pre);
+        run = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(phi), QT - 1));
+        return phi;
+    } else {
+        const float phi = wrap_angle(*slot + pre);
+        if (last_lane) *slot = phi;
+        return phi;
+    }
+}
+
+// ---- raw row tiles staged by direct-to-LDS buffer loads (gfx950)
+// A tile holds 64 rows (tokens) of CH 16-byte chunks as they lie in memory,
+// except that chunk m of row t sits at chunk m ^ rsw<CH>(t) of the row.  The
+// permutation keeps two kinds of reads free of bank conflicts: a wave's
+// lane = token reads of one chunk from 64 consecutive rows (each 16
+// consecutive rows land in 16 distinct 16-byte slots of a 256-byte window),
+// and transposed operand reads, whose 16 lanes take two adjacent chunks from
+// each of four consecutive rows (8 distinct slots).
+template <int CH>
+__device__ __forceinline__ int rsw(int t) {
+    static_assert(CH == 4 || CH == 8 || CH == 16, "rows of 64, 128 or 256 bytes");
+    const int u = t & 15;
+    if constexpr (CH == 16) return ((u & 3) << 1) | ((u >> 2) & 1) | (u & 8);
+    if constexpr (CH == 8) return (((u >> 1) & 3) << 1) | ((u >> 3) & 1);
+    return (u >> 2) & 3;
+}
+// Byte offset of element `col` (16-bit elements) of row t in such a tile.
+template <int CH>
+__device__ __forceinline__ int rtile_off(int t, int col) {
+    return t * CH * 16 + ((((col >> 3) ^ rsw<CH>(t))) << 4) + ((col & 7) << 1);
+}
+// One direct-to-LDS load instruction (16 bytes a lane) of rows
+// [I * 64 / CH, (I + 1) * 64 / CH) of a tile at `tile`: lane l fills slot l of
+// the instruction's kilobyte, i.e. chunk l % CH of row I * 64 / CH + l / CH,
+// with the memory chunk that the permutation places there.  Row t is read
+// from byte t * stride + first of the buffer; rows past its range read zeros.
+template <int CH>
+__device__ __forceinline__ void lds_load_rows(rsrc_t r, uint32_t first, uint32_t stride,
+                                              unsigned char *tile, int I, int lane) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    const int t = I * (64 / CH) + lane / CH;
+    const int m = (lane % CH) ^ rsw<CH>(t);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(tile + I * 1024), 16,
+                                             first + static_cast<uint32_t>(t) * stride + m * 16, 0,
+                                             0, 0);
 }
 
 // Transposed LDS read (ds_read_b64_tr_b16, gfx950).  Within each group of 16
@@ -254,6 +337,12 @@ __device__ __forceinline__ void load_chunk(const SeqBufs &rs, int ck, int wave, 
     for (int v = 0; v < G::XV; ++v) raw.x[v] = bld16(rs.x, ox + 16 * v);
     __builtin_amdgcn_sched_barrier(0);
 }
+
+// The per-token scalars of a lane's token as loaded (the fields of Raw that
+// token_scalars reads).
+struct TokScalars {
+    float s0, s1, s2, s3;
+};
 
 // Per-token scalars of this lane's token: log decay a, diagonal weight g,
 // off-diagonal weight w (fused.rs:2483-2503), zero for tokens past the end.

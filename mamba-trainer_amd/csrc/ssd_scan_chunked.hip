@@ -124,10 +124,10 @@ __device__ __forceinline__ f32x4 load_u(const void *u, size_t e) {
 template <typename T, int N, int R, int ROWS>
 struct StateSmem {
     using op_t = typename Op<T>::t;
-    static constexpr int PAD = 16 / static_cast<int>(sizeof(op_t));
-    static constexpr int LDR = ROWS + PAD;
-    op_t Bwt[N * LDR];      // (B~ * w * decay-to-end)^T [n][rho], segment frame
-    op_t Xt[kP * LDR];      // X^T [p][rho]
+    // unpadded swizzled tiles (swz): 24.8 KB at N = 128, so six workgroups
+    // share a CU
+    op_t Bwt[N * ROWS];     // (B~ * w * decay-to-end)^T [n][rho], segment frame
+    op_t Xt[kP * ROWS];     // X^T [p][rho]
     // wrapped angle per pair entering the sub-chunk, relative to the segment
     // start; each pair is read and rewritten by the one wave whose lanes own
     // it, so one copy serves every sub-chunk (a wave's LDS accesses execute
@@ -154,7 +154,7 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     using RawT = Raw<T, N, P, R, ROWS, 4, false>;
     using op_t = typename S::op_t;
     constexpr int KB = sizeof(typename S::op_t) == 2 ? 32 : 16;
-    constexpr int LDR = S::LDR;
+    constexpr int E16 = 16 / static_cast<int>(sizeof(op_t));
     constexpr int QT = G::QT, NH = G::NH, PPL = G::PPL;
     constexpr int NTN = N / 16;
     constexpr bool kBf16 = sizeof(op_t) == 2;
@@ -191,6 +191,10 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     for (int i = 0; i < NTN; ++i) uacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float eacc = 1.0f;
     if (tid < NH) sm.psi[tid] = 0.0f;
+    constexpr bool kUni = G::SUBS == 1;   // pair angles wave-uniform (pair_angle)
+    float run[kUni ? PPL : 1];
+#pragma unroll
+    for (int j = 0; j < (kUni ? PPL : 1); ++j) run[j] = 0.0f;
     __syncthreads();
 
     const int h_end = min(kseg, nsub - seg * kseg);
@@ -231,22 +235,33 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             for (int e = 0; e < G::XE; ++e) {
                 const int o = wave * (P / 4) * R + sub * G::XE + e;
                 const int p = o / R, r = o % R;
-                sm.Xt[p * LDR + my_t * R + r] = to_op<op_t>(elem<T>(cur.x, e));
+                sm.Xt[swz<op_t, ROWS>(p, my_t * R + r)] = op_elem<T>(cur.x, e);
             }
         }
         // per pair: the angle within the segment (the running angle plus the
         // in-sub-chunk inclusive cumsum of dt * theta), its sine and cosine,
         // and B rotated by its negative (fused.rs:610-617), weighted and
-        // stored -- one pair's values live at a time
+        // stored -- one pair's values live at a time.  Without theta its
+        // loads read zeros: every angle is 0 (cosine 1, sine 0), with no
+        // branch to keep the pairs from interleaving.
         const float dtt = live ? cur.s0 : 0.0f;
+        // the prefixes four pairs at a time (interleaved DPP chains)
+        constexpr int GP = PPL % 4 == 0 ? 4 : 1;
+        float pre[GP];
 #pragma unroll
         for (int j = 0; j < PPL; ++j) {
-            float cs = 1.0f, sn = 0.0f;
-            if (rot) {
-                const float pre = seg_scan<G::SW>(dtt * welem<T>(cur.th, j));
-                const float phi = wrap_angle(sm.psi[i0 + j] + pre);
-                // the sub-chunk's last token carries the angle to the next one
-                if (my_t == QT - 1) sm.psi[i0 + j] = phi;
+            float cs, sn;
+            if (j % GP == 0) {
+#pragma unroll
+                for (int jj = 0; jj < GP; ++jj) pre[jj] = dtt * welem<T>(cur.th, j + jj);
+                if constexpr (GP == 4)
+                    seg_scan4<G::SW>(pre[0], pre[1], pre[2], pre[3]);
+                else
+                    pre[0] = seg_scan<G::SW>(pre[0]);
+            }
+            {
+                const float phi = pair_angle<kUni, QT>(pre[j % GP], run[kUni ? j : 0],
+                                                       &sm.psi[i0 + j], my_t == QT - 1);
                 if constexpr (kBf16) {
                     // the hardware sine takes revolutions; |phi| <= pi
                     const float rev = phi * 0.15915494309189533577f;
@@ -262,8 +277,9 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
                     const int rho = my_t * R + r;
                     const float b1 = elem<T>(cur.b[0], j * R + r);
                     const float b2 = elem<T>(cur.b[1], j * R + r);
-                    sm.Bwt[(i0 + j) * LDR + rho] = to_op<op_t>((b1 * cs + b2 * sn) * wd);
-                    sm.Bwt[(i0 + NH + j) * LDR + rho] = to_op<op_t>((-b1 * sn + b2 * cs) * wd);
+                    sm.Bwt[swz<op_t, ROWS>(i0 + j, rho)] = to_op<op_t>((b1 * cs + b2 * sn) * wd);
+                    sm.Bwt[swz<op_t, ROWS>(i0 + NH + j, rho)] =
+                        to_op<op_t>((-b1 * sn + b2 * cs) * wd);
                 }
             }
         }
@@ -271,13 +287,16 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 
         // U = e_h U + U_h, U_h^T[n][p] = sum_rho Bwt[n][rho] X^T[p][rho]; wave w
         // takes p-tile w
-        const op_t *xr = &sm.Xt[(16 * wave + c) * LDR];
+        // (rows 16 i + c share the swizzle of row c: one column offset per kb)
 #pragma unroll
         for (int i = 0; i < NTN; ++i) {
             f32x4 acc = uacc[i] * eh;
-            const op_t *ar = &sm.Bwt[(16 * i + c) * LDR];
 #pragma unroll
-            for (int kb = 0; kb < ROWS / KB; ++kb) acc = mma_kb(ar + kb * KB, xr + kb * KB, acc, g);
+            for (int kb = 0; kb < ROWS / KB; ++kb) {
+                const int col = kb * KB + g * E16;
+                acc = mma_kb(&sm.Bwt[swz<op_t, ROWS>(16 * i + c, col)],
+                             &sm.Xt[swz<op_t, ROWS>(16 * wave + c, col)], acc, 0);
+            }
             uacc[i] = acc;
         }
         eacc *= eh;
@@ -288,10 +307,223 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 #pragma unroll
     for (int i = 0; i < NTN; ++i) store_u<kBf16>(ws.u, uo + i * 256, uacc[i]);
     if (tid == 0) ws.eda[bhs] = eacc;
+    if constexpr (kUni) {   // each wave's pair angles into LDS
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < PPL; ++j) sm.psi[i0 + j] = run[j];
+        }
+        __syncthreads();
+    }
     // the segment's angle total per pair (wrapped), with its cosine and sine:
     // one thread per pair (the loop's last barrier ordered the angle writes)
     if (tid < NH) {
         const float tot = rot ? sm.psi[tid] : 0.0f;
+        float ts = 0.0f, tc = 1.0f;
+        if (rot) sincosf(tot, &ts, &tc);
+        ws.phi[bhs * NH + tid] = tot;
+        ws.cph[bhs * NH + tid] = tc;
+        ws.sph[bhs * NH + tid] = ts;
+    }
+}
+
+// The same for bf16 storage at rank 1, with the inputs staged by coalesced
+// direct-to-LDS loads.  Lane = token loads put each lane of a load
+// instruction on its own cache line (rows of one head are H * N * 2 bytes
+// apart), and the L1's per-line work, not HBM, then bounds the kernel; here
+// each instruction fetches whole rows (eight lines a kilobyte) into raw row
+// tiles (rsw).  The stage reads its pair slices from the tiles, and writes B
+// rotated and weighted back in place; the MFMA takes (B~w)^T and X^T from the
+// row-major tiles by transposed reads.
+template <int N>
+struct StateDmaSmem {
+    static constexpr int CB = N / 8, CT = N / 16, CX = kP / 8;   // chunks per row
+    unsigned char b[64 * CB * 16];    // B, then B~ w decay-to-end, [t][n]
+    unsigned char th[64 * CT * 16];   // theta [t][pair]; the pair angle totals at the end
+    unsigned char x[64 * CX * 16];    // X [t][p]
+};
+
+template <int N>
+__global__ void __launch_bounds__(kThreads, 2)
+chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
+    constexpr int P = kP;
+    using G = Geo<bf16_t, N, P, 1, 64, 4>;
+    using S = StateDmaSmem<N>;
+    constexpr int CB = S::CB, CT = S::CT, CX = S::CX;
+    constexpr int QT = G::QT, NH = G::NH, PPL = G::PPL, PW = G::PW;
+    constexpr int NTN = N / 16;
+    constexpr int HV = PW / 8;        // 16-byte chunks of a lane's half-row slice
+    static_assert(G::SUBS == 1 && QT == 64 && PPL == PW, "lane = token, one segment per wave");
+
+    __shared__ __attribute__((aligned(16))) S sm;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+
+    const size_t H = a.heads, L = a.seq;
+    const size_t bhs = blockIdx.x;
+    const int seg = static_cast<int>(bhs % nseg);
+    const size_t bh = bhs / nseg;
+    const size_t bb = bh / H, hh = bh % H;
+    const bool rot = a.theta != nullptr;
+    const SeqBufs rs = seq_bufs<bf16_t, N, P, 1>(a, bb, hh);
+
+    float A = 0.0f;
+    if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);   // a_log.exp().neg() (scan.rs:470-474)
+
+    f32x4 uacc[NTN];
+#pragma unroll
+    for (int i = 0; i < NTN; ++i) uacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float eacc = 1.0f;
+    float run[PPL];   // wave-uniform running pair angles (pair_angle)
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) run[j] = 0.0f;
+
+    const int h_end = min(kseg, nsub - seg * kseg);
+#pragma unroll 1
+    for (int h = 0; h < h_end; ++h) {
+        int lane_v = lane;
+        asm volatile("" : "+v"(lane_v));
+        const int lane = lane_v;
+        const int g = lane >> 4;
+        const int c = lane & 15;
+        const int sck = seg * kseg + h;
+        const uint32_t tok0 = static_cast<uint32_t>(sck) * QT;
+
+        // per-token scalars first (vmcnt counts in issue order), then the
+        // tiles: B 16, theta and X 8 instructions each at N = 128
+        TokScalars sc;
+        {
+            const uint32_t tok = tok0 + lane;
+            sc.s0 = bldf(rs.s0, tok * rs.tok_s);
+            sc.s1 = bldf(rs.s1, tok * rs.tok_s);
+            sc.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
+            sc.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
+        }
+#pragma unroll
+        for (int I = wave; I < CB; I += 4) lds_load_rows<CB>(rs.b, tok0 * rs.tok_bc, rs.tok_bc, sm.b, I, lane);
+#pragma unroll
+        for (int I = wave; I < CT; I += 4) lds_load_rows<CT>(rs.th, tok0 * rs.tok_th, rs.tok_th, sm.th, I, lane);
+#pragma unroll
+        for (int I = wave; I < CX; I += 4) lds_load_rows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.x, I, lane);
+
+        const bool live = tok0 + lane < L;
+        float av, gv, wv;
+        token_scalars(a, sc, A, live, av, gv, wv);
+        const float acum = seg_scan<64>(av);
+        const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
+        const float wd = dexp<true>(last - acum) * wv;   // exp_decay(last, acum, w)
+        const float eh = dexp<true>(last);
+        const float dtt = live ? sc.s0 : 0.0f;
+
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's tile loads
+        __syncthreads();                      // ... and every other wave's
+
+        // ---- stage: this lane's token, this wave's pairs
+        {
+            const int i0 = wave * PW;
+            u32x4 th[HV], bv[2][HV];
+#pragma unroll
+            for (int v = 0; v < HV; ++v) {
+                th[v] = *reinterpret_cast<const u32x4 *>(sm.th + rtile_off<CT>(lane, i0 + 8 * v));
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+                    bv[hf][v] = *reinterpret_cast<const u32x4 *>(
+                        sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v));
+            }
+            constexpr int GP = PPL % 4 == 0 ? 4 : 1;
+            float pre[GP];
+            u32x4 out[2];
+#pragma unroll
+            for (int j = 0; j < PPL; ++j) {
+                if (j % GP == 0) {
+#pragma unroll
+                    for (int jj = 0; jj < GP; ++jj)
+                        pre[jj] = dtt * elem<bf16_t>(th, j + jj);
+                    if constexpr (GP == 4)
+                        seg_scan4<64>(pre[0], pre[1], pre[2], pre[3]);
+                    else
+                        pre[0] = seg_scan<64>(pre[0]);
+                }
+                float dummy = 0.0f;
+                const float phi = pair_angle<true, QT>(pre[j % GP], run[j], &dummy, false);
+                // the hardware sine takes revolutions; |phi| <= pi
+                const float rev = phi * 0.15915494309189533577f;
+                const float sn = __builtin_amdgcn_sinf(rev);
+                const float cs = __builtin_amdgcn_cosf(rev);
+                const float b1 = elem<bf16_t>(bv[0], j);
+                const float b2 = elem<bf16_t>(bv[1], j);
+                const float o1 = (b1 * cs + b2 * sn) * wd;   // R(-phi) b, weighted (fused.rs:610-617)
+                const float o2 = (-b1 * sn + b2 * cs) * wd;
+                // pack two bf16 per word; a chunk is written once its 8 pairs are done
+                const int w = (j & 7) >> 1;
+                const unsigned int q1 = static_cast<unsigned int>(from_f32<bf16_t>(o1).bits);
+                const unsigned int q2 = static_cast<unsigned int>(from_f32<bf16_t>(o2).bits);
+                if ((j & 1) == 0) {
+                    out[0][w] = q1;
+                    out[1][w] = q2;
+                } else {
+                    out[0][w] |= q1 << 16;
+                    out[1][w] |= q2 << 16;
+                }
+                if ((j & 7) == 7) {
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf)
+                        *reinterpret_cast<u32x4 *>(sm.b + rtile_off<CB>(lane, hf * NH + i0 + (j & ~7))) =
+                            out[hf];
+                }
+            }
+        }
+        __syncthreads();
+
+        // ---- U = e_h U + U_h, U_h^T[n][p] = sum_rho (B~w)[rho][n] X[rho][p]:
+        // A operand (n = 16 i + c, k = rho = 32 kb + 8 g + 0..7) and B operand
+        // (p = 16 wave + c, same k) by two transposed reads each
+        {
+            const int r0 = 8 * g + (c >> 2);
+            const int cq = 4 * (c & 3);
+            bf16x8 xo[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(
+                    sm.x + rtile_off<CX>(32 * kb + r0, 16 * wave + cq)));
+                const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(
+                    sm.x + rtile_off<CX>(32 * kb + r0 + 4, 16 * wave + cq)));
+                xo[kb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+#pragma unroll
+            for (int i = 0; i < NTN; ++i) {
+                f32x4 acc = uacc[i] * eh;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(
+                        sm.b + rtile_off<CB>(32 * kb + r0, 16 * i + cq)));
+                    const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(
+                        sm.b + rtile_off<CB>(32 * kb + r0 + 4, 16 * i + cq)));
+                    const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    acc = mfma_bf16(av, xo[kb], acc);
+                }
+                uacc[i] = acc;
+            }
+        }
+        eacc *= eh;
+        __syncthreads();   // every read of this sub-chunk's tiles is done
+    }
+
+    const size_t uo = (bhs * 4 + wave) * NTN * 256 + lane * 4;
+#pragma unroll
+    for (int i = 0; i < NTN; ++i) store_u<true>(ws.u, uo + i * 256, uacc[i]);
+    if (tid == 0) ws.eda[bhs] = eacc;
+    // the segment's angle total per pair (wrapped), with its cosine and sine,
+    // one thread per pair: each wave's uniform angles through LDS
+    float *psi = reinterpret_cast<float *>(sm.th);
+    if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < PPL; ++j) psi[wave * PW + j] = run[j];
+    }
+    __syncthreads();
+    if (tid < NH) {
+        const float tot = rot ? psi[tid] : 0.0f;
         float ts = 0.0f, tc = 1.0f;
         if (rot) sincosf(tot, &ts, &tc);
         ws.phi[bhs * NH + tid] = tot;
@@ -543,6 +775,10 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     const bool skip = a.d_skip != nullptr;
     // the angle of every pair relative to the segment start is zero on entry
     if (tid < NH) sm.psi[tid] = 0.0f;
+    constexpr bool kUni = G::SUBS == 1;   // pair angles wave-uniform (pair_angle)
+    float run[kUni ? PPL : 1];
+#pragma unroll
+    for (int j = 0; j < (kUni ? PPL : 1); ++j) run[j] = 0.0f;
     // With the prefetch, the state fragments and the first sub-chunk's inputs
     // land before the loop: a wait for them inside it would also cover the
     // next sub-chunk's prefetch on every pass (vmcnt counts in issue order).
@@ -594,35 +830,37 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             for (int e = 0; e < G::XE; ++e) {
                 const int o = wave * (P / 4) * R + sub * G::XE + e;
                 const int p = o / R, r = o % R;
-                sm.Xt[p * LDR + my_t * R + r] = to_op<op_t>(elem<T>(cur.x, e));
+                sm.Xt[p * LDR + my_t * R + r] = op_elem<T>(cur.x, e);
             }
         }
         // per group of (up to) four pairs: the angle within the segment (the
         // running angle plus the in-sub-chunk inclusive cumsum of dt * theta),
         // its sine and cosine, and B and C rotated by its negative
-        // (fused.rs:610-617) and stored -- one group's values live at a time
+        // (fused.rs:610-617) and stored -- one group's values live at a time.
+        // Without theta its loads read zeros: every angle is 0 (cosine 1,
+        // sine 0), with no branch to keep the group's pairs from interleaving.
         const float dtt = live ? cur.s0 : 0.0f;
         constexpr int GP = PPL % 4 == 0 ? 4 : 1;
 #pragma unroll
         for (int q = 0; q < PPL; q += GP) {
-            float cs[GP], sn[GP];
+            float cs[GP], sn[GP], pre[GP];
+#pragma unroll
+            for (int jj = 0; jj < GP; ++jj) pre[jj] = dtt * welem<T>(cur.th, q + jj);
+            if constexpr (GP == 4)
+                seg_scan4<G::SW>(pre[0], pre[1], pre[2], pre[3]);
+            else
+                pre[0] = seg_scan<G::SW>(pre[0]);
 #pragma unroll
             for (int jj = 0; jj < GP; ++jj) {
                 const int j = q + jj;
-                cs[jj] = 1.0f;
-                sn[jj] = 0.0f;
-                if (rot) {
-                    const float pre = seg_scan<G::SW>(dtt * welem<T>(cur.th, j));
-                    const float phi = wrap_angle(sm.psi[i0 + j] + pre);
-                    // the sub-chunk's last token carries the angle to the next one
-                    if (my_t == QT - 1) sm.psi[i0 + j] = phi;
-                    if constexpr (kBf16) {
-                        const float rev = phi * 0.15915494309189533577f;
-                        sn[jj] = __builtin_amdgcn_sinf(rev);
-                        cs[jj] = __builtin_amdgcn_cosf(rev);
-                    } else {
-                        sincosf(phi, &sn[jj], &cs[jj]);
-                    }
+                const float phi = pair_angle<kUni, QT>(pre[jj], run[kUni ? j : 0], &sm.psi[i0 + j],
+                                                       my_t == QT - 1);
+                if constexpr (kBf16) {
+                    const float rev = phi * 0.15915494309189533577f;
+                    sn[jj] = __builtin_amdgcn_sinf(rev);
+                    cs[jj] = __builtin_amdgcn_cosf(rev);
+                } else {
+                    sincosf(phi, &sn[jj], &cs[jj]);
                 }
             }
             if (tok_lane) {
@@ -822,6 +1060,292 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     }   // sub-chunks
 }
 
+// The same for bf16 storage at rank 1, with B, C, theta and X staged by
+// coalesced direct-to-LDS loads into raw row tiles (as chunk_state_dma_kernel
+// does).  The stage rotates B and C in place; the band reads B~ and C~ rows in
+// memory order (any k order serves when both operands share it); the carry-in
+// takes C~ in the state fragments' k order by two 8-byte reads; X^T comes by
+// transposed reads, once per sub-chunk, for the band product and the advance.
+template <int N>
+struct ScanDmaSmem {
+    static constexpr int CB = N / 8, CT = N / 16, CX = kP / 8;   // chunks per row
+    static constexpr int LDM = 64 + 8;                           // band row stride
+    unsigned char b[64 * CB * 16];    // B, then B~ [t][n]
+    unsigned char c[64 * CB * 16];    // C, then C~ [t][n]
+    unsigned char x[64 * CX * 16];    // X [t][p]
+    union {                           // theta in the stage, the band after it
+        unsigned char th[64 * CT * 16];
+        __bf16 ms[64 * LDM];          // (C B^T o L)[t][s]
+    } u;
+    float acum[64], gw[64], ww[64], wdv[64];
+};
+
+template <int N>
+__global__ void __launch_bounds__(kThreads, 3)
+chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
+    constexpr int P = kP;
+    using G = Geo<bf16_t, N, P, 1, 64, 4>;
+    using S = ScanDmaSmem<N>;
+    constexpr int CB = S::CB, CT = S::CT, CX = S::CX, LDM = S::LDM;
+    constexpr int QT = G::QT, NH = G::NH, PPL = G::PPL, PW = G::PW;
+    constexpr int NT = 4;             // 16-row tiles of a sub-chunk
+    constexpr int NF = N / 32;        // state fragments (k-blocks of n)
+    constexpr int HV = PW / 8;
+    static_assert(G::SUBS == 1 && QT == 64 && PPL == PW, "lane = token, one segment per wave");
+
+    __shared__ __attribute__((aligned(16))) S sm;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+
+    const size_t H = a.heads, L = a.seq;
+    const size_t bhs = blockIdx.x;
+    const int seg = static_cast<int>(bhs % nseg);
+    const size_t bh = bhs / nseg;
+    const size_t bb = bh / H, hh = bh % H;
+    const SeqBufs rs = seq_bufs<bf16_t, N, P, 1>(a, bb, hh);
+    const int h_end = min(kseg, nsub - seg * kseg);
+
+    // the state entering this segment, in its frame, as carry-in A operands
+    // (n-tiles 2f and 2f + 1 form k-block f: n = 32 f + 16 h + 4 g + r)
+    bf16x8 sf[NF];
+    {
+        const bf16x4 *src = static_cast<const bf16x4 *>(ws.s) + (bhs * 4 + wave) * (N / 16) * 64 + lane;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const bf16x4 lo = src[(2 * f) * 64], hi = src[(2 * f + 1) * 64];
+            sf[f] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+    }
+    float A = 0.0f;
+    if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);
+    const float dskip = a.d_skip ? a.d_skip[hh] : 0.0f;
+    const bool skip = a.d_skip != nullptr;
+    float run[PPL];   // wave-uniform running pair angles (pair_angle)
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) run[j] = 0.0f;
+
+#pragma unroll 1
+    for (int h = 0; h < h_end; ++h) {
+    int lane_v = lane;
+    asm volatile("" : "+v"(lane_v));
+    const int lane = lane_v;
+    const int g = lane >> 4;
+    const int c = lane & 15;
+    const int sck = seg * kseg + h;
+    const uint32_t tok0 = static_cast<uint32_t>(sck) * QT;
+    const bool advance = h + 1 < h_end;
+
+    TokScalars sc;
+    {
+        const uint32_t tok = tok0 + lane;
+        sc.s0 = bldf(rs.s0, tok * rs.tok_s);
+        sc.s1 = bldf(rs.s1, tok * rs.tok_s);
+        sc.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
+        sc.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
+    }
+#pragma unroll
+    for (int I = wave; I < CB; I += 4) {
+        lds_load_rows<CB>(rs.b, tok0 * rs.tok_bc, rs.tok_bc, sm.b, I, lane);
+        lds_load_rows<CB>(rs.c, tok0 * rs.tok_bc, rs.tok_bc, sm.c, I, lane);
+    }
+#pragma unroll
+    for (int I = wave; I < CT; I += 4) lds_load_rows<CT>(rs.th, tok0 * rs.tok_th, rs.tok_th, sm.u.th, I, lane);
+#pragma unroll
+    for (int I = wave; I < CX; I += 4) lds_load_rows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.x, I, lane);
+
+    const bool live = tok0 + lane < L;
+    float av, gv, wv;
+    token_scalars(a, sc, A, live, av, gv, wv);
+    const float acum = seg_scan<64>(av);
+    if (wave == 0) {
+        sm.acum[lane] = acum;
+        sm.gw[lane] = gv;
+        sm.ww[lane] = wv;
+        const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
+        sm.wdv[lane] = dexp<true>(last - acum) * wv;   // w x decay to the end
+    }
+    const float dtt = live ? sc.s0 : 0.0f;
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's tile loads
+    __syncthreads();                      // ... and every other wave's
+
+    // ---- stage: per group of four pairs the angle within the segment, its
+    //      sine and cosine, and B and C rotated by its negative
+    //      (fused.rs:610-617), written back in place
+    {
+        const int i0 = wave * PW;
+        u32x4 th[HV];
+#pragma unroll
+        for (int v = 0; v < HV; ++v)
+            th[v] = *reinterpret_cast<const u32x4 *>(sm.u.th + rtile_off<CT>(lane, i0 + 8 * v));
+#pragma unroll
+        for (int v = 0; v < HV; ++v) {
+            u32x4 bv[2], cv[2], bo[2], co[2];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                bv[hf] = *reinterpret_cast<const u32x4 *>(sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v));
+                cv[hf] = *reinterpret_cast<const u32x4 *>(sm.c + rtile_off<CB>(lane, hf * NH + i0 + 8 * v));
+            }
+#pragma unroll
+            for (int q = 0; q < 8; q += 4) {
+                float pre[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) pre[jj] = dtt * elem<bf16_t>(th, 8 * v + q + jj);
+                seg_scan4<64>(pre[0], pre[1], pre[2], pre[3]);
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int e = q + jj;   // element within the chunk
+                    float dummy = 0.0f;
+                    const float phi = pair_angle<true, QT>(pre[jj], run[8 * v + e], &dummy, false);
+                    const float rev = phi * 0.15915494309189533577f;
+                    const float sn = __builtin_amdgcn_sinf(rev);
+                    const float cs = __builtin_amdgcn_cosf(rev);
+                    const float b1 = elem<bf16_t>(bv, e), b2 = elem<bf16_t>(bv + 1, e);
+                    const float c1 = elem<bf16_t>(cv, e), c2 = elem<bf16_t>(cv + 1, e);
+                    const unsigned int rb1 = from_f32<bf16_t>(b1 * cs + b2 * sn).bits;
+                    const unsigned int rb2 = from_f32<bf16_t>(-b1 * sn + b2 * cs).bits;
+                    const unsigned int rc1 = from_f32<bf16_t>(c1 * cs + c2 * sn).bits;
+                    const unsigned int rc2 = from_f32<bf16_t>(-c1 * sn + c2 * cs).bits;
+                    const int w = e >> 1;
+                    if ((e & 1) == 0) {
+                        bo[0][w] = rb1; bo[1][w] = rb2; co[0][w] = rc1; co[1][w] = rc2;
+                    } else {
+                        bo[0][w] |= rb1 << 16; bo[1][w] |= rb2 << 16;
+                        co[0][w] |= rc1 << 16; co[1][w] |= rc2 << 16;
+                    }
+                }
+            }
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                *reinterpret_cast<u32x4 *>(sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v)) = bo[hf];
+                *reinterpret_cast<u32x4 *>(sm.c + rtile_off<CB>(lane, hf * NH + i0 + 8 * v)) = co[hf];
+            }
+        }
+    }
+    __syncthreads();   // B~, C~ complete; theta's space is the band's from here
+
+    // ---- masked band into ms (tiles (tj, si) with si <= tj, plus the zero
+    //      tiles above the diagonal that the y product's 32-row k-blocks read)
+    {
+        int idx = 0;
+#pragma unroll
+        for (int tj = 0; tj < NT; ++tj) {
+            const int ncol = tj < 2 ? 2 : 4;
+#pragma unroll
+            for (int si = 0; si < ncol; ++si) {
+                if ((idx++) % 4 != wave) continue;
+                const int trow = 16 * tj + c;
+                float vals[4] = {0.f, 0.f, 0.f, 0.f};
+                if (si <= tj) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kb = 0; kb < N / 32; ++kb) {
+                        const bf16x8 av = *reinterpret_cast<const bf16x8 *>(
+                            sm.b + rtile_off<CB>(16 * si + c, 32 * kb + 8 * g));
+                        const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(
+                            sm.c + rtile_off<CB>(trow, 32 * kb + 8 * g));
+                        acc = mfma_bf16(av, bv, acc);
+                    }
+                    const float at = sm.acum[trow];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int srow = 16 * si + 4 * g + r;
+                        float v = 0.0f;
+                        if (srow <= trow) {
+                            const float wgt = (srow == trow) ? sm.gw[srow] : sm.ww[srow];
+                            v = acc[r] * wgt * dexp<true>(at - sm.acum[srow]);
+                        }
+                        if (skip && srow == trow) v += dskip;   // scan.rs:593-597
+                        vals[r] = v;
+                    }
+                }
+                st4(&sm.u.ms[trow * LDM + 16 * si + 4 * g], vals);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- X^T operand fragments (p = 16 wave + c, s = 32 kb + 8 g + 0..7)
+    bf16x8 xf[2];
+    {
+        const int r0 = 8 * g + (c >> 2);
+        const int cq = 16 * wave + 4 * (c & 3);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.x + rtile_off<CX>(32 * kb + r0, cq)));
+            const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.x + rtile_off<CX>(32 * kb + r0 + 4, cq)));
+            xf[kb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+    }
+
+    // ---- y^T[p][t] = exp(acum_t) sum_n S[p][n] C~[t][n] + sum_s X^T[p][s] M[t][s]
+#pragma unroll
+    for (int tj = 0; tj < NT; ++tj) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const int t = 16 * tj + c;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
+            const bf16x4v lo = *reinterpret_cast<const bf16x4v *>(sm.c + rtile_off<CB>(t, 32 * f + 4 * g));
+            const bf16x4v hi = *reinterpret_cast<const bf16x4v *>(sm.c + rtile_off<CB>(t, 32 * f + 16 + 4 * g));
+            const bf16x8 cv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            acc = mfma_bf16(sf[f], cv, acc);
+        }
+        acc = acc * dexp<true>(sm.acum[t]);   // exp_decay(acum)
+        const int nkb = tj < 2 ? 1 : 2;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+            if (kb < nkb)
+                acc = mfma_bf16(xf[kb], *reinterpret_cast<const bf16x8 *>(&sm.u.ms[t * LDM + 32 * kb + 8 * g]), acc);
+        // rows past the sequence end fall outside the buffer: dropped
+        const uint32_t oy = (tok0 + t) * rs.tok_x + (16 * wave + 4 * g) * 2;
+        u32x2 pk;
+        pk[0] = static_cast<unsigned int>(from_f32<bf16_t>(acc[0]).bits) |
+                (static_cast<unsigned int>(from_f32<bf16_t>(acc[1]).bits) << 16);
+        pk[1] = static_cast<unsigned int>(from_f32<bf16_t>(acc[2]).bits) |
+                (static_cast<unsigned int>(from_f32<bf16_t>(acc[3]).bits) << 16);
+        bst8(pk, rs.y, oy);
+    }
+
+    if (advance) {
+        // ---- S' = e_h S + U_h, U_h^T[n][p] = sum_s B~[s][n] (w decay X^T)[p][s]
+        // over this wave's p-tile: A operand B~^T by transposed reads, B
+        // operand the weighted X^T fragments (rounded to bf16 once)
+        const float eh = dexp<true>(sm.acum[QT - 1]);
+        bf16x8 xw[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                xw[kb][j] = static_cast<__bf16>(static_cast<float>(xf[kb][j]) * sm.wdv[32 * kb + 8 * g + j]);
+        const int r0 = 8 * g + (c >> 2);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            f32x4 st[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) st[q][r] = static_cast<float>(sf[f][q * 4 + r]) * eh;
+                const int col = 16 * (2 * f + q) + 4 * (c & 3);
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + rtile_off<CB>(32 * kb + r0, col)));
+                    const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + rtile_off<CB>(32 * kb + r0 + 4, col)));
+                    const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    st[q] = mfma_bf16(av, xw[kb], st[q]);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sf[f][q * 4 + r] = static_cast<__bf16>(st[q][r]);
+        }
+    }
+    __syncthreads();   // every read of this sub-chunk's tiles is done
+    }   // sub-chunks
+}
+
 // The single pass walks each (batch, head) sequence with one workgroup per CU,
 // so its time goes in whole rounds of one sequence per CU; the three
 // chunk-parallel launches cost about the same per sequence at any count.  The
@@ -888,16 +1412,24 @@ hipError_t launch_three(const ScanLaunch &a, char *base, hipStream_t s) {
     const size_t bh = a.batch * a.heads;
     const size_t bhs = bh * sp.nseg;
     const ChunkWs ws = chunk_ws(base, chunked_layout(bhs, N, sizeof(T) == 2));
-    hipLaunchKernelGGL((chunk_state_kernel<T, N, R, ROWS, kPf>), dim3(bhs),
-                       dim3(kThreads), 0, s, a, ws, sp.nsub, sp.kseg, sp.nseg);
+    if constexpr (sizeof(T) == 2 && R == 1)
+        hipLaunchKernelGGL((chunk_state_dma_kernel<N>), dim3(bhs), dim3(kThreads), 0, s, a, ws,
+                           sp.nsub, sp.kseg, sp.nseg);
+    else
+        hipLaunchKernelGGL((chunk_state_kernel<T, N, R, ROWS, kPf>), dim3(bhs),
+                           dim3(kThreads), 0, s, a, ws, sp.nsub, sp.kseg, sp.nseg);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((state_pass_kernel<T, N>), dim3(bh * (N / 32)), dim3(kThreads), 0, s, a, ws,
                        sp.nseg);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((chunk_scan_kernel<T, N, R, ROWS, kPf>), dim3(bhs), dim3(kThreads), 0, s, a,
-                       ws, sp.nsub, sp.kseg, sp.nseg);
+    if constexpr (sizeof(T) == 2 && R == 1)
+        hipLaunchKernelGGL((chunk_scan_dma_kernel<N>), dim3(bhs), dim3(kThreads), 0, s, a, ws,
+                           sp.nsub, sp.kseg, sp.nseg);
+    else
+        hipLaunchKernelGGL((chunk_scan_kernel<T, N, R, ROWS, kPf>), dim3(bhs), dim3(kThreads), 0,
+                           s, a, ws, sp.nsub, sp.kseg, sp.nseg);
     return hipGetLastError();
 }
 
