@@ -48,6 +48,11 @@ namespace {
 using namespace scan;
 
 constexpr int kP = 64;   // head_dim of these kernels
+// State values (pairs) per thread of the state pass: all four of a lane's
+// values in a record tile.  The pass is bound by its memory instructions, not
+// by the threads in flight: splitting a lane's four over two or four threads
+// measured 1.6x and 2.7x slower at config 1 (MI355X).
+constexpr int kStatePairs = 4;
 
 // Workspace sections, byte offsets from the base.  U and S are stored in the
 // operand type: bf16 for bf16 storage (the state itself is carried in f32 by
@@ -533,9 +538,13 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 }
 
 // ================================================================ state pass
-__device__ __forceinline__ void sincos4(const f32x4 t, f32x4 &sn, f32x4 &cs) {
+// RP consecutive state values (pairs) of one thread, as a vector.
+template <int RP> using fvec = float __attribute__((ext_vector_type(RP)));
+
+template <int RP>
+__device__ __forceinline__ void sincosv(const fvec<RP> t, fvec<RP> &sn, fvec<RP> &cs) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < RP; ++r) {
         float s, c;
         sincosf(t[r], &s, &c);
         sn[r] = s;
@@ -545,20 +554,54 @@ __device__ __forceinline__ void sincos4(const f32x4 t, f32x4 &sn, f32x4 &cs) {
 
 // v1 = element n, v2 = element n + N/2 of a pair; R(t) (v1, v2) =
 // (v1 cos t - v2 sin t, v1 sin t + v2 cos t)
-__device__ __forceinline__ void rotate_pairs(f32x4 &lo, f32x4 &hi, const f32x4 cs, const f32x4 sn) {
-    const f32x4 l = lo;
+template <int RP>
+__device__ __forceinline__ void rotate_pairs(fvec<RP> &lo, fvec<RP> &hi, const fvec<RP> cs,
+                                             const fvec<RP> sn) {
+    const fvec<RP> l = lo;
     lo = l * cs - hi * sn;
     hi = l * sn + hi * cs;
 }
 
-template <typename T, int N>
+// RP consecutive values of a U / S record (element index e, a multiple of RP).
+template <bool BF, int RP>
+__device__ __forceinline__ fvec<RP> load_rec(const void *u, size_t e) {
+    fvec<RP> v;
+    if constexpr (BF) {
+        typedef __bf16 bv_t __attribute__((ext_vector_type(RP)));
+        const bv_t q = *reinterpret_cast<const bv_t *>(static_cast<const __bf16 *>(u) + e);
+#pragma unroll
+        for (int r = 0; r < RP; ++r) v[r] = static_cast<float>(q[r]);
+    } else {
+        v = *reinterpret_cast<const fvec<RP> *>(static_cast<const float *>(u) + e);
+    }
+    return v;
+}
+template <bool BF, int RP>
+__device__ __forceinline__ void store_rec(void *u, size_t e, const fvec<RP> v) {
+    if constexpr (BF) {
+        typedef __bf16 bv_t __attribute__((ext_vector_type(RP)));
+        bv_t q;
+#pragma unroll
+        for (int r = 0; r < RP; ++r) q[r] = static_cast<__bf16>(v[r]);
+        *reinterpret_cast<bv_t *>(static_cast<__bf16 *>(u) + e) = q;
+    } else {
+        *reinterpret_cast<fvec<RP> *>(static_cast<float *>(u) + e) = v;
+    }
+}
+
+// One thread per (batch, head, p, RP state pairs): RP of the four values a
+// lane holds in a record's MFMA D layout, so 4 / RP threads share a lane's
+// four (more threads in flight for the same records).
+template <typename T, int N, int RP>
 __global__ void __launch_bounds__(kThreads)
 state_pass_kernel(ScanLaunch a, ChunkWs ws, int nck) {   // nck: segments per sequence
     constexpr int P = kP;
     constexpr int NTN = N / 16;
     constexpr int HT = NTN / 2;   // n-tiles per half
     constexpr int NH = N / 2;
+    constexpr int SPLIT = 4 / RP;
     constexpr bool kBf16 = sizeof(T) == 2;
+    using V = fvec<RP>;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -566,68 +609,69 @@ state_pass_kernel(ScanLaunch a, ChunkWs ws, int nck) {   // nck: segments per se
     const int g = lane >> 4;
     const int c = lane & 15;
     const size_t H = a.heads, L = a.seq;
-    const int i1 = static_cast<int>(blockIdx.x % HT);
-    const size_t bh = blockIdx.x / HT;
+    const int part = static_cast<int>(blockIdx.x % SPLIT);
+    const int i1 = static_cast<int>((blockIdx.x / SPLIT) % HT);
+    const size_t bh = blockIdx.x / (SPLIT * HT);
     const size_t bb = bh / H, hh = bh % H;
     const bool rot = a.theta != nullptr;
 
     const int p = 16 * pt + c;
-    const int nlo = 16 * i1 + 4 * g;   // my pairs are (nlo + r, nlo + r + N/2), r < 4
+    const int nlo = 16 * i1 + 4 * g + RP * part;   // my pairs (nlo + r, nlo + r + N/2), r < RP
     const size_t sbase = bh * P * N + static_cast<size_t>(p) * N;
 
-    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+    V lo = V(0.0f), hi = V(0.0f);
     {
         const float *h0 = a.mode_raw ? a.h0 : a.init_state;
         const float *l0 = a.mode_raw ? a.last_u0 : nullptr;
         if (h0 != nullptr) {
-            lo = *reinterpret_cast<const f32x4 *>(h0 + sbase + nlo);
-            hi = *reinterpret_cast<const f32x4 *>(h0 + sbase + nlo + NH);
+            lo = *reinterpret_cast<const V *>(h0 + sbase + nlo);
+            hi = *reinterpret_cast<const V *>(h0 + sbase + nlo + NH);
             if (l0 != nullptr) {
                 // carry S = h + (1 - lambda_0) dt_0 last_u   (scan.rs:521-535)
                 const size_t i0s = (bb * L) * H + hh;
                 const float first = (1.0f - a.lambda[i0s]) * a.dt[i0s];
-                lo += *reinterpret_cast<const f32x4 *>(l0 + sbase + nlo) * first;
-                hi += *reinterpret_cast<const f32x4 *>(l0 + sbase + nlo + NH) * first;
+                lo += *reinterpret_cast<const V *>(l0 + sbase + nlo) * first;
+                hi += *reinterpret_cast<const V *>(l0 + sbase + nlo + NH) * first;
             }
         }
     }
     // running wrapped angle of my pairs; the carried state into chunk 0's frame
-    f32x4 phi = {0.f, 0.f, 0.f, 0.f};
+    V phi = V(0.0f);
     if (rot && a.angle0 != nullptr) {
-        phi = *reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo);
-        f32x4 cs, sn;
-        sincos4(phi, sn, cs);
-        rotate_pairs(lo, hi, cs, sn);
+        phi = *reinterpret_cast<const V *>(a.angle0 + bh * NH + nlo);
+        V cs, sn;
+        sincosv<RP>(phi, sn, cs);
+        rotate_pairs<RP>(lo, hi, cs, sn);
     }
 
     const size_t bhk0 = bh * nck;
     struct In {
-        f32x4 ulo, uhi, cs, sn, ph;
+        V ulo, uhi, cs, sn, ph;
         float e;
     };
     auto load = [&](int k, In &d) {
         const int kk = k < nck ? k : nck - 1;   // past the end: re-read the last chunk, unused
         const size_t bhk = bhk0 + kk;
-        const size_t u = (bhk * 4 + pt) * NTN * 256 + lane * 4;
-        d.ulo = load_u<kBf16>(ws.u, u + i1 * 256);
-        d.uhi = load_u<kBf16>(ws.u, u + (i1 + HT) * 256);
+        const size_t u = (bhk * 4 + pt) * NTN * 256 + lane * 4 + RP * part;
+        d.ulo = load_rec<kBf16, RP>(ws.u, u + i1 * 256);
+        d.uhi = load_rec<kBf16, RP>(ws.u, u + (i1 + HT) * 256);
         d.e = ws.eda[bhk];
         if (rot) {
-            d.cs = *reinterpret_cast<const f32x4 *>(ws.cph + bhk * NH + nlo);
-            d.sn = *reinterpret_cast<const f32x4 *>(ws.sph + bhk * NH + nlo);
-            d.ph = *reinterpret_cast<const f32x4 *>(ws.phi + bhk * NH + nlo);
+            d.cs = *reinterpret_cast<const V *>(ws.cph + bhk * NH + nlo);
+            d.sn = *reinterpret_cast<const V *>(ws.sph + bhk * NH + nlo);
+            d.ph = *reinterpret_cast<const V *>(ws.phi + bhk * NH + nlo);
         }
     };
     auto step = [&](int k, const In &d) {
-        const size_t so = ((bhk0 + k) * 4 + pt) * NTN * 256 + lane * 4;
-        store_u<kBf16>(ws.s, so + i1 * 256, lo);
-        store_u<kBf16>(ws.s, so + (i1 + HT) * 256, hi);
+        const size_t so = ((bhk0 + k) * 4 + pt) * NTN * 256 + lane * 4 + RP * part;
+        store_rec<kBf16, RP>(ws.s, so + i1 * 256, lo);
+        store_rec<kBf16, RP>(ws.s, so + (i1 + HT) * 256, hi);
         lo = lo * d.e + d.ulo;
         hi = hi * d.e + d.uhi;
         if (rot) {
-            rotate_pairs(lo, hi, d.cs, d.sn);
+            rotate_pairs<RP>(lo, hi, d.cs, d.sn);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) phi[r] = wrap_angle(phi[r] + d.ph[r]);
+            for (int r = 0; r < RP; ++r) phi[r] = wrap_angle(phi[r] + d.ph[r]);
         }
     };
     // eight chunks in flight ahead of the one being applied
@@ -644,36 +688,36 @@ state_pass_kernel(ScanLaunch a, ChunkWs ws, int nck) {   // nck: segments per se
     }
 
     // ---- boundary state in the global frame (scan.rs:270-288, 599-638)
-    f32x4 ce = {1.f, 1.f, 1.f, 1.f}, se = {0.f, 0.f, 0.f, 0.f};
-    if (rot) sincos4(phi, se, ce);
+    V ce = V(1.0f), se = V(0.0f);
+    if (rot) sincosv<RP>(phi, se, ce);
     if (a.h_out != nullptr) {
-        f32x4 hl = lo, hh2 = hi;
-        rotate_pairs(hl, hh2, ce, -se);   // R(-phi_end)
-        *reinterpret_cast<f32x4 *>(a.h_out + sbase + nlo) = hl;
-        *reinterpret_cast<f32x4 *>(a.h_out + sbase + nlo + NH) = hh2;
+        V hl = lo, hh2 = hi;
+        rotate_pairs<RP>(hl, hh2, ce, -se);   // R(-phi_end)
+        *reinterpret_cast<V *>(a.h_out + sbase + nlo) = hl;
+        *reinterpret_cast<V *>(a.h_out + sbase + nlo + NH) = hh2;
     }
     if (a.angle_out != nullptr && pt == 0 && c == 0)
-        *reinterpret_cast<f32x4 *>(a.angle_out + bh * NH + nlo) = phi;
+        *reinterpret_cast<V *>(a.angle_out + bh * NH + nlo) = phi;
     if (a.last_u_out != nullptr) {
         // last_u = sum_r x_{L-1,r} B~_{L-1,r}^T with B~ = R(-phi_end) B  (scan.rs:599-618)
         const size_t tl = (bb * L + (L - 1)) * H + hh;
         const T *bp = static_cast<const T *>(a.b) + tl * N * a.rank;
         const T *xp = static_cast<const T *>(a.x) + (tl * P + static_cast<size_t>(p)) * a.rank;
-        f32x4 ul = {0.f, 0.f, 0.f, 0.f}, uh = ul;
+        V ul = V(0.0f), uh = V(0.0f);
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             if (m >= static_cast<int>(a.rank)) break;
             const float xv = to_f32(xp[m]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+            for (int r = 0; r < RP; ++r) {
                 const float b1 = to_f32(bp[(nlo + r) * a.rank + m]);
                 const float b2 = to_f32(bp[(nlo + r + NH) * a.rank + m]);
                 ul[r] += xv * (b1 * ce[r] + b2 * se[r]);
                 uh[r] += xv * (-b1 * se[r] + b2 * ce[r]);
             }
         }
-        *reinterpret_cast<f32x4 *>(a.last_u_out + sbase + nlo) = ul;
-        *reinterpret_cast<f32x4 *>(a.last_u_out + sbase + nlo + NH) = uh;
+        *reinterpret_cast<V *>(a.last_u_out + sbase + nlo) = ul;
+        *reinterpret_cast<V *>(a.last_u_out + sbase + nlo + NH) = uh;
     }
 }
 
@@ -1349,11 +1393,11 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 // The single pass walks each (batch, head) sequence with one workgroup per CU,
 // so its time goes in whole rounds of one sequence per CU; the three
 // chunk-parallel launches cost about the same per sequence at any count.  The
-// single pass is the faster form once the last round fills ~70 % of the chip
+// single pass is the faster form once its last round fills ~85 % of the chip
 // (measured on MI355X at L = 2048, H = 12, N = 128, bf16, in us chunked vs
-// single pass: 96 sequences 107 vs 191, 192: 239 vs 222, 240: 299 vs 227,
-// 288: 367 vs 434, 384: 482 vs 442).  The workspace is asked for only where
-// the chunked form wins.
+// single pass: 96 sequences 93.6 vs 219.8, 144: 165.4 vs 223.2, 192: 181.6
+// vs 231.6, 240: 270.2 vs 235.6, 288: 302.9 vs 443.5, 384: 354.0 vs 452.3).
+// The workspace is asked for only where the chunked form wins.
 static size_t device_cus() {
     static int cus = 0;
     if (cus == 0) {
@@ -1384,15 +1428,20 @@ SegPlan seg_plan(const ScanLaunch &a) {
     const size_t nsub = (a.seq + qt - 1) / qt;
     const size_t q = a.chunk_size ? a.chunk_size : 64;
     const size_t kmin = (q + qt - 1) / qt;
-    // rounds of resident chunk_scan workgroups: two at rank 1, eight for MIMO
-    // (measured on MI355X, rotated inputs, us per call: config 1 at 1 / 2 / 4
-    // rounds 123.1 / 120.0 / 132.0; config 2 at 2 / 4 / 8 / 16 rounds
-    // 624 / 592 / 580 / 591, against 125.0 and 724.6 for one 64-token chunk
-    // per workgroup)
+    // rounds of resident chunk_scan workgroups: one at rank 1, eight for MIMO
+    // (measured on MI355X, rotated inputs, us per call: config 1 with the
+    // direct-to-LDS staging at 1 / 2 rounds 96.4-97.8 / 100.2-102.8, before it
+    // at 1 / 2 / 4 rounds 123.1 / 120.0 / 132.0; config 2 at 2 / 4 / 8 / 16
+    // rounds 624 / 592 / 580 / 591, against 125.0 and 724.6 for one 64-token
+    // chunk per workgroup)
     const size_t slots = device_cus() * (a.rank > 1 ? 2 : 3);
-    const size_t rounds = a.rank > 1 ? 8 : 2;
-    const size_t kfill = a.batch * a.heads * nsub / (rounds * slots);
-    size_t k = kmin > kfill ? kmin : kfill;
+    const size_t rounds = a.rank > 1 ? 8 : 1;
+    // segments per sequence that fill the rounds without spilling into one
+    // more, then the sub-chunks each needs
+    const size_t bh = a.batch * a.heads;
+    const size_t fill = bh < rounds * slots ? rounds * slots / bh : 1;
+    size_t k = (nsub + fill - 1) / fill;
+    if (k < kmin) k = kmin;
     if (k < 1) k = 1;
     if (k > nsub) k = nsub;
     SegPlan p;
@@ -1420,7 +1469,7 @@ hipError_t launch_three(const ScanLaunch &a, char *base, hipStream_t s) {
                            dim3(kThreads), 0, s, a, ws, sp.nsub, sp.kseg, sp.nseg);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((state_pass_kernel<T, N>), dim3(bh * (N / 32)), dim3(kThreads), 0, s, a, ws,
+    hipLaunchKernelGGL((state_pass_kernel<T, N, kStatePairs>), dim3(bh * (N / 32) * (4 / kStatePairs)), dim3(kThreads), 0, s, a, ws,
                        sp.nseg);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1454,7 +1503,7 @@ size_t scan_chunked_workspace(const ScanLaunch &a) {
     if (!scan_fast_supported(a) || a.seq == 0) return 0;
     const size_t seqs = a.batch * a.heads, cus = device_cus();
     const size_t rounds = (seqs + cus - 1) / cus;
-    if (seqs * 10 >= rounds * cus * 7) return 0;
+    if (seqs * 100 >= rounds * cus * 85) return 0;
     return chunked_layout(seqs * seg_plan(a).nseg, a.d_state, a.bf16 != 0).total;
 }
 

@@ -421,16 +421,16 @@ def test_config4_full_model_split_prefill_property():
     logits of one 2048-token prefill.
 
     The bar is the device's own noise floor at this depth, measured here: the
-    same 2048-token prefill run as two batches of 8 (which takes the
-    chunk-parallel scan instead of the single-pass one, the same arithmetic in
-    another order).  With bf16 activations, rounding differences of ~1e-4 in
-    one layer flip bf16 roundings of the residual stream and compound over 24
-    layers to ~2.4e-2 in the logits (1e-3 at one layer), so no bf16
-    implementation meets 1e-2 on the 24-layer logits; the carried path must
-    be within 1.25x of that floor.  The first window must be bit-identical,
-    and the second window run without the carried caches must miss by at
-    least 5x more, so the check is not vacuous.  Compared on the device (the
-    logits are 2 GB)."""
+    same 2048-token prefill run as two batches of 8 (whose chunk-parallel scan
+    cuts each sequence into segments of another length, the same arithmetic
+    in another order).  With bf16 activations, rounding differences of ~1e-4
+    in one layer flip bf16 roundings of the residual stream and compound over
+    24 layers to ~2.4e-2 in the logits (1e-3 at one layer), so no bf16
+    implementation meets 1e-2 on the 24-layer logits; both windows must be
+    within 1.25x of that floor (the first window's scan also cuts its shorter
+    sequences into shorter segments).  The second window run without the
+    carried caches must miss by at least 5x more, so the check is not
+    vacuous.  Compared on the device (the logits are 2 GB)."""
     from mamba3 import Discretization, SsmConfig, SsmMode, StateDynamics
     from mamba3.lm import Mamba3Lm, Mamba3LmConfig
     ssm = SsmConfig(d_model=768, n_heads=12, head_dim=64, d_state=128, n_groups=12,
@@ -457,7 +457,7 @@ def test_config4_full_model_split_prefill_property():
     print(f"config 4 full model, prefill {cut} + carried {T - cut} vs {T}: rel-L2 first "
           f"{e1:.2e}, second {e2:.2e}; noise floor (the same prefill on the chunk-parallel "
           f"scan) {floor:.2e}; without the carried caches {cold:.2e}", flush=True)
-    assert e1 == 0.0
+    assert e1 <= 1.25 * floor
     assert e2 <= 1.25 * floor
     assert cold >= 5 * e2
     assert torch.isfinite(full.float()).all()
