@@ -148,6 +148,24 @@ __device__ __forceinline__ float pair_angle(float pre, float &run, float *slot, 
     }
 }
 
+// pair_angle in turns (revolutions, what the hardware sine takes): `pre` is
+// the in-sub-chunk prefix of dt theta / 2 pi, the result the wrapped angle
+// in [-1/2, 1/2] (r - rint(r) is exact), and the wave-uniform running angle
+// is carried by a readlane of the last token's lane.
+__device__ __forceinline__ float pair_turns(float pre, float &run) {
+    const float r = run + pre;
+    const float w = r - __builtin_rintf(r);
+    run = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 63));
+    return w;
+}
+
+// Two values rounded to bf16 and packed into one word (low half first).
+__device__ __forceinline__ unsigned int pk_bf16(float lo, float hi) {
+    typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+    const bf16x2v v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(unsigned int, v);
+}
+
 // ---- raw row tiles staged by direct-to-LDS buffer loads (gfx950)
 // A tile holds 64 rows (tokens) of CH 16-byte chunks as they lie in memory,
 // except that chunk m of row t sits at chunk m ^ rsw<CH>(t) of the row.  The

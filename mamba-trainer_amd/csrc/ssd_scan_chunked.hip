@@ -419,64 +419,54 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
         const float wd = dexp<true>(last - acum) * wv;   // exp_decay(last, acum, w)
         const float eh = dexp<true>(last);
-        const float dtt = live ? sc.s0 : 0.0f;
+        // dt / 2 pi: the pair angles are carried in turns (pair_turns)
+        const float dtt = live ? sc.s0 * 0.15915494309189533577f : 0.0f;
 
         __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's tile loads
         __syncthreads();                      // ... and every other wave's
 
-        // ---- stage: this lane's token, this wave's pairs
+        // ---- stage: this lane's token, this wave's pairs, eight (one chunk
+        //      of each half-row) at a time
         {
             const int i0 = wave * PW;
-            u32x4 th[HV], bv[2][HV];
+            u32x4 th[HV];
 #pragma unroll
-            for (int v = 0; v < HV; ++v) {
+            for (int v = 0; v < HV; ++v)
                 th[v] = *reinterpret_cast<const u32x4 *>(sm.th + rtile_off<CT>(lane, i0 + 8 * v));
 #pragma unroll
+            for (int v = 0; v < HV; ++v) {
+                u32x4 bv[2], out[2];
+#pragma unroll
                 for (int hf = 0; hf < 2; ++hf)
-                    bv[hf][v] = *reinterpret_cast<const u32x4 *>(
+                    bv[hf] = *reinterpret_cast<const u32x4 *>(
                         sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v));
-            }
-            constexpr int GP = PPL % 4 == 0 ? 4 : 1;
-            float pre[GP];
-            u32x4 out[2];
 #pragma unroll
-            for (int j = 0; j < PPL; ++j) {
-                if (j % GP == 0) {
+                for (int q = 0; q < 8; q += 4) {
+                    float pre[4];
 #pragma unroll
-                    for (int jj = 0; jj < GP; ++jj)
-                        pre[jj] = dtt * elem<bf16_t>(th, j + jj);
-                    if constexpr (GP == 4)
-                        seg_scan4<64>(pre[0], pre[1], pre[2], pre[3]);
-                    else
-                        pre[0] = seg_scan<64>(pre[0]);
-                }
-                float dummy = 0.0f;
-                const float phi = pair_angle<true, QT>(pre[j % GP], run[j], &dummy, false);
-                // the hardware sine takes revolutions; |phi| <= pi
-                const float rev = phi * 0.15915494309189533577f;
-                const float sn = __builtin_amdgcn_sinf(rev);
-                const float cs = __builtin_amdgcn_cosf(rev);
-                const float b1 = elem<bf16_t>(bv[0], j);
-                const float b2 = elem<bf16_t>(bv[1], j);
-                const float o1 = (b1 * cs + b2 * sn) * wd;   // R(-phi) b, weighted (fused.rs:610-617)
-                const float o2 = (-b1 * sn + b2 * cs) * wd;
-                // pack two bf16 per word; a chunk is written once its 8 pairs are done
-                const int w = (j & 7) >> 1;
-                const unsigned int q1 = static_cast<unsigned int>(from_f32<bf16_t>(o1).bits);
-                const unsigned int q2 = static_cast<unsigned int>(from_f32<bf16_t>(o2).bits);
-                if ((j & 1) == 0) {
-                    out[0][w] = q1;
-                    out[1][w] = q2;
-                } else {
-                    out[0][w] |= q1 << 16;
-                    out[1][w] |= q2 << 16;
-                }
-                if ((j & 7) == 7) {
+                    for (int jj = 0; jj < 4; ++jj) pre[jj] = dtt * elem<bf16_t>(th, 8 * v + q + jj);
+                    seg_scan4<64>(pre[0], pre[1], pre[2], pre[3]);
 #pragma unroll
-                    for (int hf = 0; hf < 2; ++hf)
-                        *reinterpret_cast<u32x4 *>(sm.b + rtile_off<CB>(lane, hf * NH + i0 + (j & ~7))) =
-                            out[hf];
+                    for (int jj = 0; jj < 4; jj += 2) {
+                        float o[2][2];
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            const int e = q + jj + u;   // element within the chunk
+                            const float w = pair_turns(pre[jj + u], run[8 * v + e]);
+                            const float sn = __builtin_amdgcn_sinf(w);
+                            const float cs = __builtin_amdgcn_cosf(w);
+                            const float b1 = elem<bf16_t>(bv, e), b2 = elem<bf16_t>(bv + 1, e);
+                            // R(-phi) b, weighted (fused.rs:610-617)
+                            o[0][u] = (b1 * cs + b2 * sn) * wd;
+                            o[1][u] = (-b1 * sn + b2 * cs) * wd;
+                        }
+#pragma unroll
+                        for (int hf = 0; hf < 2; ++hf) out[hf][(q + jj) >> 1] = pk_bf16(o[hf][0], o[hf][1]);
+                    }
                 }
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+                    *reinterpret_cast<u32x4 *>(sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v)) = out[hf];
             }
         }
         __syncthreads();
@@ -528,7 +518,7 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     }
     __syncthreads();
     if (tid < NH) {
-        const float tot = rot ? psi[tid] : 0.0f;
+        const float tot = rot ? psi[tid] * 6.28318530717958647692f : 0.0f;   // turns -> radians
         float ts = 0.0f, tc = 1.0f;
         if (rot) sincosf(tot, &ts, &tc);
         ws.phi[bhs * NH + tid] = tot;
@@ -1210,7 +1200,8 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
         sm.wdv[lane] = dexp<true>(last - acum) * wv;   // w x decay to the end
     }
-    const float dtt = live ? sc.s0 : 0.0f;
+    // dt / 2 pi: the pair angles are carried in turns (pair_turns)
+    const float dtt = live ? sc.s0 * 0.15915494309189533577f : 0.0f;
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's tile loads
     __syncthreads();                      // ... and every other wave's
 
@@ -1238,25 +1229,25 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
                 for (int jj = 0; jj < 4; ++jj) pre[jj] = dtt * elem<bf16_t>(th, 8 * v + q + jj);
                 seg_scan4<64>(pre[0], pre[1], pre[2], pre[3]);
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const int e = q + jj;   // element within the chunk
-                    float dummy = 0.0f;
-                    const float phi = pair_angle<true, QT>(pre[jj], run[8 * v + e], &dummy, false);
-                    const float rev = phi * 0.15915494309189533577f;
-                    const float sn = __builtin_amdgcn_sinf(rev);
-                    const float cs = __builtin_amdgcn_cosf(rev);
-                    const float b1 = elem<bf16_t>(bv, e), b2 = elem<bf16_t>(bv + 1, e);
-                    const float c1 = elem<bf16_t>(cv, e), c2 = elem<bf16_t>(cv + 1, e);
-                    const unsigned int rb1 = from_f32<bf16_t>(b1 * cs + b2 * sn).bits;
-                    const unsigned int rb2 = from_f32<bf16_t>(-b1 * sn + b2 * cs).bits;
-                    const unsigned int rc1 = from_f32<bf16_t>(c1 * cs + c2 * sn).bits;
-                    const unsigned int rc2 = from_f32<bf16_t>(-c1 * sn + c2 * cs).bits;
-                    const int w = e >> 1;
-                    if ((e & 1) == 0) {
-                        bo[0][w] = rb1; bo[1][w] = rb2; co[0][w] = rc1; co[1][w] = rc2;
-                    } else {
-                        bo[0][w] |= rb1 << 16; bo[1][w] |= rb2 << 16;
-                        co[0][w] |= rc1 << 16; co[1][w] |= rc2 << 16;
+                for (int jj = 0; jj < 4; jj += 2) {
+                    float ob[2][2], oc[2][2];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int e = q + jj + u;   // element within the chunk
+                        const float w = pair_turns(pre[jj + u], run[8 * v + e]);
+                        const float sn = __builtin_amdgcn_sinf(w);
+                        const float cs = __builtin_amdgcn_cosf(w);
+                        const float b1 = elem<bf16_t>(bv, e), b2 = elem<bf16_t>(bv + 1, e);
+                        const float c1 = elem<bf16_t>(cv, e), c2 = elem<bf16_t>(cv + 1, e);
+                        ob[0][u] = b1 * cs + b2 * sn;
+                        ob[1][u] = -b1 * sn + b2 * cs;
+                        oc[0][u] = c1 * cs + c2 * sn;
+                        oc[1][u] = -c1 * sn + c2 * cs;
+                    }
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) {
+                        bo[hf][(q + jj) >> 1] = pk_bf16(ob[hf][0], ob[hf][1]);
+                        co[hf][(q + jj) >> 1] = pk_bf16(oc[hf][0], oc[hf][1]);
                     }
                 }
             }
