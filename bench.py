@@ -54,10 +54,10 @@ MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA, TFLOP/s
 # chunk_scan) and the MFMA-busy fraction of its two MFMA kernels, from
 # profiles/scan_config1_kernels.txt (rocprofv3 FETCH_SIZE / WRITE_SIZE per
 # dispatch scaled by a 256 MiB copy, SQ_VALU_MFMA_BUSY_CYCLES over
-# GRBM_GUI_ACTIVE): 310.2 MB read + 83.0 MB written.  Counters cannot be read
+# GRBM_GUI_ACTIVE): 282.0 MB read + 57.3 MB written.  Counters cannot be read
 # inside this process; re-measured when the kernels change.
-SCAN_TRAFFIC_BYTES = 393_200_000
-SCAN_MFMA_BUSY = {"chunk_scan_kernel": 0.048, "chunk_state_kernel": 0.028}
+SCAN_TRAFFIC_BYTES = 339_300_000
+SCAN_MFMA_BUSY = {"chunk_scan_dma_kernel": 0.069, "chunk_state_dma_kernel": 0.036}
 
 # BASELINE config 1 (the headline) and config 3 (decode)
 SCAN = dict(B=8, L=2048, H=12, P=64, N=128, R=1, Q=64)
@@ -883,8 +883,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": SCAN_TRAFFIC_BYTES,
-                     "kernel": "m3_scan: chunk_state_kernel + state_pass_kernel + "
-                               "chunk_scan_kernel (one scan call)",
+                     "kernel": "m3_scan: chunk_state_dma_kernel + state_pass_kernel + "
+                               "chunk_scan_dma_kernel (one scan call)",
                      "kernel_us": round(sc["kernel_ms"] * 1e3, 2),
                      "input_sets": sc["sets"], "input_MB_total": sc["input_MB"],
                      "kernel_us_resident_inputs": round(sc_res["kernel_ms"] * 1e3, 2),
