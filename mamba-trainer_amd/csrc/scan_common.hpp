@@ -159,6 +159,14 @@ __device__ __forceinline__ float pair_turns(float pre, float &run) {
     return w;
 }
 
+// s_waitcnt immediate for vmcnt(V) alone (expcnt and lgkmcnt at their
+// maxima), gfx9 encoding: vmcnt bits [3:0] and [15:14].
+template <int V>
+constexpr int vmcnt_imm() {
+    static_assert(V >= 0 && V < 64, "vmcnt range");
+    return (V & 15) | ((V >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+}
+
 // Two values rounded to bf16 and packed into one word (low half first).
 __device__ __forceinline__ unsigned int pk_bf16(float lo, float hi) {
     typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
@@ -187,20 +195,48 @@ template <int CH>
 __device__ __forceinline__ int rtile_off(int t, int col) {
     return t * CH * 16 + ((((col >> 3) ^ rsw<CH>(t))) << 4) + ((col & 7) << 1);
 }
-// One direct-to-LDS load instruction (16 bytes a lane) of rows
-// [I * 64 / CH, (I + 1) * 64 / CH) of a tile at `tile`: lane l fills slot l of
-// the instruction's kilobyte, i.e. chunk l % CH of row I * 64 / CH + l / CH,
-// with the memory chunk that the permutation places there.  Row t is read
-// from byte t * stride + first of the buffer; rows past its range read zeros.
+// Direct-to-LDS buffer loads, issued as inline asm.  Lane l of one
+// instruction writes its 4 or 16 bytes to LDS at base + l * size (M0 holds
+// the base; it is saved and restored around the load).  The compiler's wait
+// insertion treats an outstanding LDS DMA it knows of as a write to all of
+// LDS and waits for it (vmcnt(0)) before any later LDS read, which would
+// serialise a pipelined stage; these loads are unknown to it, so every read
+// of their destination must follow an explicit vmcnt wait (and a barrier
+// for other waves' loads).  Its own waits stay correct: loads it does not
+// see only make a counted wait stricter.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    typedef __attribute__((address_space(3))) const unsigned char lds_u8;
+    return __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u8 *)(p))));
+}
+__device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t base, uint32_t voff) {
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "buffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep)
+                 : "s"(base), "v"(voff), "s"(r)
+                 : "memory");
+}
+__device__ __forceinline__ void lds_dma4(rsrc_t r, uint32_t base, uint32_t voff) {
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+                 "buffer_load_dword %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep)
+                 : "s"(base), "v"(voff), "s"(r)
+                 : "memory");
+}
+
+// One such load (16 bytes a lane) of rows [I * 64 / CH, (I + 1) * 64 / CH)
+// of a tile at `tile`: lane l fills slot l of the instruction's kilobyte,
+// i.e. chunk l % CH of row I * 64 / CH + l / CH, with the memory chunk that
+// the permutation places there.  Row t is read from byte t * stride + first
+// of the buffer; rows past its range read zeros.
 template <int CH>
 __device__ __forceinline__ void lds_load_rows(rsrc_t r, uint32_t first, uint32_t stride,
                                               unsigned char *tile, int I, int lane) {
-    typedef __attribute__((address_space(3))) void lds_void;
     const int t = I * (64 / CH) + lane / CH;
     const int m = (lane % CH) ^ rsw<CH>(t);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(tile + I * 1024), 16,
-                                             first + static_cast<uint32_t>(t) * stride + m * 16, 0,
-                                             0, 0);
+    lds_dma16(r, lds_addr(tile + I * 1024), first + static_cast<uint32_t>(t) * stride + m * 16);
 }
 
 // Transposed LDS read (ds_read_b64_tr_b16, gfx950).  Within each group of 16

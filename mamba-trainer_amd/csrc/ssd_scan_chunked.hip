@@ -339,12 +339,20 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 // tiles (rsw).  The stage reads its pair slices from the tiles, and writes B
 // rotated and weighted back in place; the MFMA takes (B~w)^T and X^T from the
 // row-major tiles by transposed reads.
+//
+// The loads are pipelined one sub-chunk ahead.  theta, X and the per-token
+// scalars are double-buffered and fetched at the start of the previous
+// sub-chunk; B, single-buffered, is fetched once the previous MFMA has read
+// it, and arrives while the stage forms the angles, sines and cosines (which
+// need theta only).  The waits count this wave's loads in issue order
+// (vmcnt; the loop issues no stores).
 template <int N>
 struct StateDmaSmem {
     static constexpr int CB = N / 8, CT = N / 16, CX = kP / 8;   // chunks per row
-    unsigned char b[64 * CB * 16];    // B, then B~ w decay-to-end, [t][n]
-    unsigned char th[64 * CT * 16];   // theta [t][pair]; the pair angle totals at the end
-    unsigned char x[64 * CX * 16];    // X [t][p]
+    unsigned char b[64 * CB * 16];       // B, then B~ w decay-to-end, [t][n]
+    unsigned char th[2][64 * CT * 16];   // theta [t][pair]; the pair angle totals at the end
+    unsigned char x[2][64 * CX * 16];    // X [t][p]
+    float sc[2][4][64];                  // dt, lambda, next dt, next lambda (or a, g, w)
 };
 
 template <int N>
@@ -358,12 +366,15 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     constexpr int NTN = N / 16;
     constexpr int HV = PW / 8;        // 16-byte chunks of a lane's half-row slice
     static_assert(G::SUBS == 1 && QT == 64 && PPL == PW, "lane = token, one segment per wave");
+    static_assert(CB % 4 == 0 && CT % 4 == 0 && CX % 4 == 0, "row loads spread over four waves");
+    // load instructions a wave issues per sub-chunk: theta + X + one scalar, and B
+    constexpr int kTX = CT / 4 + CX / 4 + 1, kB = CB / 4;
 
     __shared__ __attribute__((aligned(16))) S sm;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     const size_t H = a.heads, L = a.seq;
     const size_t bhs = blockIdx.x;
@@ -376,15 +387,46 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     float A = 0.0f;
     if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);   // a_log.exp().neg() (scan.rs:470-474)
 
+    // theta, X and the scalars of sub-chunk k into buffer k & 1; B of sub-chunk k
+    auto load_tx = [&](int k) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+        const int buf = k & 1;
+#pragma unroll
+        for (int q = 0; q < CT / 4; ++q)
+            lds_load_rows<CT>(rs.th, tok0 * rs.tok_th, rs.tok_th, sm.th[buf], wave + 4 * q, lane);
+#pragma unroll
+        for (int q = 0; q < CX / 4; ++q)
+            lds_load_rows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.x[buf], wave + 4 * q, lane);
+        // wave w fetches scalar w: s0, s1 at the token, s2, s3 at the next one
+        // (a uniform branch per resource: a selected resource would go
+        // through scratch)
+        const uint32_t dst = lds_addr(&sm.sc[buf][wave][0]);
+        const uint32_t o0 = (tok0 + lane) * rs.tok_s, o1 = (tok0 + rs.nxt_s + lane) * rs.tok_s;
+        switch (wave) {
+        case 0: lds_dma4(rs.s0, dst, o0); break;
+        case 1: lds_dma4(rs.s1, dst, o0); break;
+        case 2: lds_dma4(rs.s2, dst, o1); break;
+        default: lds_dma4(rs.s3, dst, o1); break;
+        }
+    };
+    auto load_b = [&](int k) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < CB / 4; ++q)
+            lds_load_rows<CB>(rs.b, tok0 * rs.tok_bc, rs.tok_bc, sm.b, wave + 4 * q, lane);
+    };
+
     f32x4 uacc[NTN];
 #pragma unroll
     for (int i = 0; i < NTN; ++i) uacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float eacc = 1.0f;
-    float run[PPL];   // wave-uniform running pair angles (pair_angle)
+    float run[PPL];   // wave-uniform running pair angles, in turns (pair_turns)
 #pragma unroll
     for (int j = 0; j < PPL; ++j) run[j] = 0.0f;
 
     const int h_end = min(kseg, nsub - seg * kseg);
+    load_tx(seg * kseg);
+    load_b(seg * kseg);
 #pragma unroll 1
     for (int h = 0; h < h_end; ++h) {
         int lane_v = lane;
@@ -393,26 +435,20 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         const int g = lane >> 4;
         const int c = lane & 15;
         const int sck = seg * kseg + h;
-        const uint32_t tok0 = static_cast<uint32_t>(sck) * QT;
+        const int buf = sck & 1;
+        const bool more = h + 1 < h_end;
 
-        // per-token scalars first (vmcnt counts in issue order), then the
-        // tiles: B 16, theta and X 8 instructions each at N = 128
+        // theta, X, scalars of this sub-chunk landed (only its B may be out)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm<kB>());
+        __syncthreads();
+        if (more) load_tx(sck + 1);
+
         TokScalars sc;
-        {
-            const uint32_t tok = tok0 + lane;
-            sc.s0 = bldf(rs.s0, tok * rs.tok_s);
-            sc.s1 = bldf(rs.s1, tok * rs.tok_s);
-            sc.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
-            sc.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
-        }
-#pragma unroll
-        for (int I = wave; I < CB; I += 4) lds_load_rows<CB>(rs.b, tok0 * rs.tok_bc, rs.tok_bc, sm.b, I, lane);
-#pragma unroll
-        for (int I = wave; I < CT; I += 4) lds_load_rows<CT>(rs.th, tok0 * rs.tok_th, rs.tok_th, sm.th, I, lane);
-#pragma unroll
-        for (int I = wave; I < CX; I += 4) lds_load_rows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.x, I, lane);
-
-        const bool live = tok0 + lane < L;
+        sc.s0 = sm.sc[buf][0][lane];
+        sc.s1 = sm.sc[buf][1][lane];
+        sc.s2 = sm.sc[buf][2][lane];
+        sc.s3 = sm.sc[buf][3][lane];
+        const bool live = static_cast<size_t>(sck) * QT + lane < L;
         float av, gv, wv;
         token_scalars(a, sc, A, live, av, gv, wv);
         const float acum = seg_scan<64>(av);
@@ -422,52 +458,61 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         // dt / 2 pi: the pair angles are carried in turns (pair_turns)
         const float dtt = live ? sc.s0 * 0.15915494309189533577f : 0.0f;
 
-        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's tile loads
-        __syncthreads();                      // ... and every other wave's
-
-        // ---- stage: this lane's token, this wave's pairs, eight (one chunk
-        //      of each half-row) at a time
+        // ---- stage, first half: every pair's angle within the segment and its
+        //      sine and cosine (theta only; B is still arriving)
+        const int i0 = wave * PW;
+        float cs[PPL], sn[PPL];
         {
-            const int i0 = wave * PW;
             u32x4 th[HV];
 #pragma unroll
             for (int v = 0; v < HV; ++v)
-                th[v] = *reinterpret_cast<const u32x4 *>(sm.th + rtile_off<CT>(lane, i0 + 8 * v));
+                th[v] = *reinterpret_cast<const u32x4 *>(sm.th[buf] + rtile_off<CT>(lane, i0 + 8 * v));
 #pragma unroll
-            for (int v = 0; v < HV; ++v) {
-                u32x4 bv[2], out[2];
+            for (int q = 0; q < PPL; q += 4) {
+                float pre[4];
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf)
-                    bv[hf] = *reinterpret_cast<const u32x4 *>(
-                        sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v));
+                for (int jj = 0; jj < 4; ++jj) pre[jj] = dtt * elem<bf16_t>(th, q + jj);
+                seg_scan4<64>(pre[0], pre[1], pre[2], pre[3]);
 #pragma unroll
-                for (int q = 0; q < 8; q += 4) {
-                    float pre[4];
+                for (int jj = 0; jj < 4; ++jj) {
+                    const float w = pair_turns(pre[jj], run[q + jj]);
+                    sn[q + jj] = __builtin_amdgcn_sinf(w);
+                    cs[q + jj] = __builtin_amdgcn_cosf(w);
+                }
+            }
+        }
+        // B landed (the next sub-chunk's theta, X and scalars may be out)
+        if (more)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm<kTX>());
+        else
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+        __syncthreads();
+
+        // ---- stage, second half: B rotated by the negative angle (fused.rs:610-617)
+        //      and weighted, back in place, eight pairs (one chunk of each
+        //      half-row) at a time
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) pre[jj] = dtt * elem<bf16_t>(th, 8 * v + q + jj);
-                    seg_scan4<64>(pre[0], pre[1], pre[2], pre[3]);
+        for (int v = 0; v < HV; ++v) {
+            u32x4 bv[2], out[2];
 #pragma unroll
-                    for (int jj = 0; jj < 4; jj += 2) {
-                        float o[2][2];
+            for (int hf = 0; hf < 2; ++hf)
+                bv[hf] = *reinterpret_cast<const u32x4 *>(sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v));
 #pragma unroll
-                        for (int u = 0; u < 2; ++u) {
-                            const int e = q + jj + u;   // element within the chunk
-                            const float w = pair_turns(pre[jj + u], run[8 * v + e]);
-                            const float sn = __builtin_amdgcn_sinf(w);
-                            const float cs = __builtin_amdgcn_cosf(w);
-                            const float b1 = elem<bf16_t>(bv, e), b2 = elem<bf16_t>(bv + 1, e);
-                            // R(-phi) b, weighted (fused.rs:610-617)
-                            o[0][u] = (b1 * cs + b2 * sn) * wd;
-                            o[1][u] = (-b1 * sn + b2 * cs) * wd;
-                        }
+            for (int e = 0; e < 8; e += 2) {
+                float o[2][2];
 #pragma unroll
-                        for (int hf = 0; hf < 2; ++hf) out[hf][(q + jj) >> 1] = pk_bf16(o[hf][0], o[hf][1]);
-                    }
+                for (int u = 0; u < 2; ++u) {
+                    const int j = 8 * v + e + u;
+                    const float b1 = elem<bf16_t>(bv, e + u), b2 = elem<bf16_t>(bv + 1, e + u);
+                    o[0][u] = (b1 * cs[j] + b2 * sn[j]) * wd;
+                    o[1][u] = (-b1 * sn[j] + b2 * cs[j]) * wd;
                 }
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf)
-                    *reinterpret_cast<u32x4 *>(sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v)) = out[hf];
+                for (int hf = 0; hf < 2; ++hf) out[hf][e >> 1] = pk_bf16(o[hf][0], o[hf][1]);
             }
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+                *reinterpret_cast<u32x4 *>(sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v)) = out[hf];
         }
         __syncthreads();
 
@@ -481,9 +526,9 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(
-                    sm.x + rtile_off<CX>(32 * kb + r0, 16 * wave + cq)));
+                    sm.x[buf] + rtile_off<CX>(32 * kb + r0, 16 * wave + cq)));
                 const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(
-                    sm.x + rtile_off<CX>(32 * kb + r0 + 4, 16 * wave + cq)));
+                    sm.x[buf] + rtile_off<CX>(32 * kb + r0 + 4, 16 * wave + cq)));
                 xo[kb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             }
 #pragma unroll
@@ -502,7 +547,8 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             }
         }
         eacc *= eh;
-        __syncthreads();   // every read of this sub-chunk's tiles is done
+        __syncthreads();   // every read of B is done
+        if (more) load_b(sck + 1);
     }
 
     const size_t uo = (bhs * 4 + wave) * NTN * 256 + lane * 4;
@@ -511,7 +557,7 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     if (tid == 0) ws.eda[bhs] = eacc;
     // the segment's angle total per pair (wrapped), with its cosine and sine,
     // one thread per pair: each wave's uniform angles through LDS
-    float *psi = reinterpret_cast<float *>(sm.th);
+    float *psi = reinterpret_cast<float *>(sm.th[0]);
     if (lane == 0) {
 #pragma unroll
         for (int j = 0; j < PPL; ++j) psi[wave * PW + j] = run[j];
