@@ -1465,14 +1465,15 @@ SegPlan seg_plan(const ScanLaunch &a) {
     const size_t nsub = (a.seq + qt - 1) / qt;
     const size_t q = a.chunk_size ? a.chunk_size : 64;
     const size_t kmin = (q + qt - 1) / qt;
-    // rounds of resident chunk_scan workgroups: one at rank 1, eight for MIMO
+    // rounds of resident chunk_scan workgroups: one at rank 1, six for MIMO
     // (measured on MI355X, rotated inputs, us per call: config 1 with the
     // direct-to-LDS staging at 1 / 2 rounds 96.4-97.8 / 100.2-102.8, before it
-    // at 1 / 2 / 4 rounds 123.1 / 120.0 / 132.0; config 2 at 2 / 4 / 8 / 16
-    // rounds 624 / 592 / 580 / 591, against 125.0 and 724.6 for one 64-token
-    // chunk per workgroup)
+    // at 1 / 2 / 4 rounds 123.1 / 120.0 / 132.0; config 2 at 4 / 5 / 6 / 7 /
+    // 8 / 10 / 12 / 16 rounds, two passes on one box, 570-593 / 575-586 /
+    // 556-574 / 573-596 / 581-590 / 596-603 / 596-615 / 594-609, against
+    // 125.0 and 724.6 for one 64-token chunk per workgroup)
     const size_t slots = device_cus() * (a.rank > 1 ? 2 : 3);
-    const size_t rounds = a.rank > 1 ? 8 : 1;
+    const size_t rounds = a.rank > 1 ? 6 : 1;
     // segments per sequence that fill the rounds without spilling into one
     // more, then the sub-chunks each needs
     const size_t bh = a.batch * a.heads;
