@@ -1146,17 +1146,25 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 // memory order (any k order serves when both operands share it); the carry-in
 // takes C~ in the state fragments' k order by two 8-byte reads; X^T comes by
 // transposed reads, once per sub-chunk, for the band product and the advance.
+//
+// The loads run one sub-chunk ahead, each into a region as soon as its last
+// reader is done.  Per sub-chunk h (p = h & 1; theta(h) sits in region R[p],
+// X(h) in R[1 - p]):
+//   wait for B, C, theta (X may still be out); stage; band into R[p] and the
+//   carry-in product C~ S (C~ is then dead): load C(h+1) and the scalars;
+//   wait for X; X^T fragments and the advance (B~ and R[1 - p] are then
+//   dead): load B(h+1) and theta(h+1) into R[1 - p]; y; load X(h+1) into R[p].
+// Loads complete in issue order, so each wait counts the loads issued after
+// the ones it needs (the y stores in between only add to the count).
 template <int N>
 struct ScanDmaSmem {
     static constexpr int CB = N / 8, CT = N / 16, CX = kP / 8;   // chunks per row
     static constexpr int LDM = 64 + 8;                           // band row stride
+    static constexpr int RB = 64 * CX * 16 > 64 * LDM * 2 ? 64 * CX * 16 : 64 * LDM * 2;
+    static_assert(64 * CT * 16 <= RB, "theta fits a region");
     unsigned char b[64 * CB * 16];    // B, then B~ [t][n]
     unsigned char c[64 * CB * 16];    // C, then C~ [t][n]
-    unsigned char x[64 * CX * 16];    // X [t][p]
-    union {                           // theta in the stage, the band after it
-        unsigned char th[64 * CT * 16];
-        __bf16 ms[64 * LDM];          // (C B^T o L)[t][s]
-    } u;
+    unsigned char r[2][RB];           // theta, then the band (C B^T o L)[t][s]; X [t][p]
     float acum[64], gw[64], ww[64], wdv[64];
 };
 
@@ -1172,12 +1180,16 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     constexpr int NF = N / 32;        // state fragments (k-blocks of n)
     constexpr int HV = PW / 8;
     static_assert(G::SUBS == 1 && QT == 64 && PPL == PW, "lane = token, one segment per wave");
+    static_assert(CB % 4 == 0 && CT % 4 == 0 && CX % 4 == 0, "row loads spread over four waves");
+    // loads a wave issues per sub-chunk: C with the four scalars, B with
+    // theta, and X
+    constexpr int kC = CB / 4 + 4, kX = CX / 4;
 
     __shared__ __attribute__((aligned(16))) S sm;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     const size_t H = a.heads, L = a.seq;
     const size_t bhs = blockIdx.x;
@@ -1202,9 +1214,41 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);
     const float dskip = a.d_skip ? a.d_skip[hh] : 0.0f;
     const bool skip = a.d_skip != nullptr;
-    float run[PPL];   // wave-uniform running pair angles (pair_angle)
+    float run[PPL];   // wave-uniform running pair angles, in turns (pair_turns)
 #pragma unroll
     for (int j = 0; j < PPL; ++j) run[j] = 0.0f;
+
+    auto load_c = [&](int k, TokScalars &sc) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < CB / 4; ++q)
+            lds_load_rows<CB>(rs.c, tok0 * rs.tok_bc, rs.tok_bc, sm.c, wave + 4 * q, lane);
+        const uint32_t tok = tok0 + lane;
+        sc.s0 = bldf(rs.s0, tok * rs.tok_s);
+        sc.s1 = bldf(rs.s1, tok * rs.tok_s);
+        sc.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
+        sc.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
+    };
+    auto load_bt = [&](int k) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < CB / 4; ++q)
+            lds_load_rows<CB>(rs.b, tok0 * rs.tok_bc, rs.tok_bc, sm.b, wave + 4 * q, lane);
+#pragma unroll
+        for (int q = 0; q < CT / 4; ++q)
+            lds_load_rows<CT>(rs.th, tok0 * rs.tok_th, rs.tok_th, sm.r[k & 1], wave + 4 * q, lane);
+    };
+    auto load_x = [&](int k) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < CX / 4; ++q)
+            lds_load_rows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.r[(k & 1) ^ 1], wave + 4 * q, lane);
+    };
+
+    TokScalars sc_next;
+    load_c(seg * kseg, sc_next);
+    load_bt(seg * kseg);
+    load_x(seg * kseg);
 
 #pragma unroll 1
     for (int h = 0; h < h_end; ++h) {
@@ -1214,26 +1258,17 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     const int g = lane >> 4;
     const int c = lane & 15;
     const int sck = seg * kseg + h;
+    const int par = sck & 1;
     const uint32_t tok0 = static_cast<uint32_t>(sck) * QT;
-    const bool advance = h + 1 < h_end;
+    const bool more = h + 1 < h_end;
 
-    TokScalars sc;
-    {
-        const uint32_t tok = tok0 + lane;
-        sc.s0 = bldf(rs.s0, tok * rs.tok_s);
-        sc.s1 = bldf(rs.s1, tok * rs.tok_s);
-        sc.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
-        sc.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
-    }
-#pragma unroll
-    for (int I = wave; I < CB; I += 4) {
-        lds_load_rows<CB>(rs.b, tok0 * rs.tok_bc, rs.tok_bc, sm.b, I, lane);
-        lds_load_rows<CB>(rs.c, tok0 * rs.tok_bc, rs.tok_bc, sm.c, I, lane);
-    }
-#pragma unroll
-    for (int I = wave; I < CT; I += 4) lds_load_rows<CT>(rs.th, tok0 * rs.tok_th, rs.tok_th, sm.u.th, I, lane);
-#pragma unroll
-    for (int I = wave; I < CX; I += 4) lds_load_rows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.x, I, lane);
+    // B, C, theta and the scalars of this sub-chunk landed (X may be out)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm<kX>());
+    __syncthreads();
+    const TokScalars sc = sc_next;
+    unsigned char *const rth = sm.r[par];         // theta, then the band
+    unsigned char *const rx = sm.r[par ^ 1];      // X
+    __bf16 *const ms = reinterpret_cast<__bf16 *>(rth);
 
     const bool live = tok0 + lane < L;
     float av, gv, wv;
@@ -1248,8 +1283,6 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     }
     // dt / 2 pi: the pair angles are carried in turns (pair_turns)
     const float dtt = live ? sc.s0 * 0.15915494309189533577f : 0.0f;
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's tile loads
-    __syncthreads();                      // ... and every other wave's
 
     // ---- stage: per group of four pairs the angle within the segment, its
     //      sine and cosine, and B and C rotated by its negative
@@ -1259,7 +1292,7 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         u32x4 th[HV];
 #pragma unroll
         for (int v = 0; v < HV; ++v)
-            th[v] = *reinterpret_cast<const u32x4 *>(sm.u.th + rtile_off<CT>(lane, i0 + 8 * v));
+            th[v] = *reinterpret_cast<const u32x4 *>(rth + rtile_off<CT>(lane, i0 + 8 * v));
 #pragma unroll
         for (int v = 0; v < HV; ++v) {
             u32x4 bv[2], cv[2], bo[2], co[2];
@@ -1304,10 +1337,11 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             }
         }
     }
-    __syncthreads();   // B~, C~ complete; theta's space is the band's from here
+    __syncthreads();   // B~, C~ complete; theta is dead, its region takes the band
 
-    // ---- masked band into ms (tiles (tj, si) with si <= tj, plus the zero
-    //      tiles above the diagonal that the y product's 32-row k-blocks read)
+    // ---- masked band into R[p] (tiles (tj, si) with si <= tj, plus the zero
+    //      tiles above the diagonal that the y product's 32-row k-blocks
+    //      read), and the carry-in product sum_n S[p][n] C~[t][n] per t-tile
     {
         int idx = 0;
 #pragma unroll
@@ -1341,26 +1375,11 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
                         vals[r] = v;
                     }
                 }
-                st4(&sm.u.ms[trow * LDM + 16 * si + 4 * g], vals);
+                st4(&ms[trow * LDM + 16 * si + 4 * g], vals);
             }
         }
     }
-    __syncthreads();
-
-    // ---- X^T operand fragments (p = 16 wave + c, s = 32 kb + 8 g + 0..7)
-    bf16x8 xf[2];
-    {
-        const int r0 = 8 * g + (c >> 2);
-        const int cq = 16 * wave + 4 * (c & 3);
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.x + rtile_off<CX>(32 * kb + r0, cq)));
-            const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.x + rtile_off<CX>(32 * kb + r0 + 4, cq)));
-            xf[kb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-    }
-
-    // ---- y^T[p][t] = exp(acum_t) sum_n S[p][n] C~[t][n] + sum_s X^T[p][s] M[t][s]
+    f32x4 yc[NT];   // the carry-in part of y^T[p][t], scaled by exp_decay(acum_t)
 #pragma unroll
     for (int tj = 0; tj < NT; ++tj) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -1373,23 +1392,31 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             const bf16x8 cv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             acc = mfma_bf16(sf[f], cv, acc);
         }
-        acc = acc * dexp<true>(sm.acum[t]);   // exp_decay(acum)
-        const int nkb = tj < 2 ? 1 : 2;
+        yc[tj] = acc * dexp<true>(sm.acum[t]);
+    }
+    __syncthreads();   // the band is complete; C~ is dead
+    if (more) load_c(sck + 1, sc_next);
+    // X landed (the next sub-chunk's C and scalars may be out)
+    if (more)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm<kC>());
+    else
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+    __syncthreads();
+
+    // ---- X^T operand fragments (p = 16 wave + c, s = 32 kb + 8 g + 0..7)
+    bf16x8 xf[2];
+    {
+        const int r0 = 8 * g + (c >> 2);
+        const int cq = 16 * wave + 4 * (c & 3);
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-            if (kb < nkb)
-                acc = mfma_bf16(xf[kb], *reinterpret_cast<const bf16x8 *>(&sm.u.ms[t * LDM + 32 * kb + 8 * g]), acc);
-        // rows past the sequence end fall outside the buffer: dropped
-        const uint32_t oy = (tok0 + t) * rs.tok_x + (16 * wave + 4 * g) * 2;
-        u32x2 pk;
-        pk[0] = static_cast<unsigned int>(from_f32<bf16_t>(acc[0]).bits) |
-                (static_cast<unsigned int>(from_f32<bf16_t>(acc[1]).bits) << 16);
-        pk[1] = static_cast<unsigned int>(from_f32<bf16_t>(acc[2]).bits) |
-                (static_cast<unsigned int>(from_f32<bf16_t>(acc[3]).bits) << 16);
-        bst8(pk, rs.y, oy);
+        for (int kb = 0; kb < 2; ++kb) {
+            const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(rx + rtile_off<CX>(32 * kb + r0, cq)));
+            const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(rx + rtile_off<CX>(32 * kb + r0 + 4, cq)));
+            xf[kb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
     }
 
-    if (advance) {
+    if (more) {
         // ---- S' = e_h S + U_h, U_h^T[n][p] = sum_s B~[s][n] (w decay X^T)[p][s]
         // over this wave's p-tile: A operand B~^T by transposed reads, B
         // operand the weighted X^T fragments (rounded to bf16 once)
@@ -1422,8 +1449,31 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sf[f][q * 4 + r] = static_cast<__bf16>(st[q][r]);
         }
+        __syncthreads();   // B~ and X are dead
+        load_bt(sck + 1);
     }
-    __syncthreads();   // every read of this sub-chunk's tiles is done
+
+    // ---- y^T[p][t] = exp(acum_t) sum_n S[p][n] C~[t][n] + sum_s X^T[p][s] M[t][s]
+#pragma unroll
+    for (int tj = 0; tj < NT; ++tj) {
+        f32x4 acc = yc[tj];
+        const int t = 16 * tj + c;
+        const int nkb = tj < 2 ? 1 : 2;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+            if (kb < nkb)
+                acc = mfma_bf16(xf[kb], *reinterpret_cast<const bf16x8 *>(&ms[t * LDM + 32 * kb + 8 * g]), acc);
+        // rows past the sequence end fall outside the buffer: dropped
+        const uint32_t oy = (tok0 + t) * rs.tok_x + (16 * wave + 4 * g) * 2;
+        u32x2 pk;
+        pk[0] = pk_bf16(acc[0], acc[1]);
+        pk[1] = pk_bf16(acc[2], acc[3]);
+        bst8(pk, rs.y, oy);
+    }
+    if (more) {
+        __syncthreads();   // every read of the band is done
+        load_x(sck + 1);
+    }
     }   // sub-chunks
 }
 
