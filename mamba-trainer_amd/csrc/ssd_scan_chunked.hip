@@ -114,6 +114,18 @@ __device__ __forceinline__ void store_u(void *u, size_t e, const f32x4 v) {
         *reinterpret_cast<f32x4 *>(static_cast<float *>(u) + e) = v;
     }
 }
+// Element offset, within one (segment, p-tile) record of NTN n-tiles, of a
+// lane's four values of n-tile i (the MFMA D layout: n = 16 i + 4 g + r,
+// p = 16 w + c).  The tiles of a rotation pair's two halves, i and
+// i + NTN / 2, sit side by side per lane, so a 16-byte access (bf16) moves
+// both halves: the state pass, which rotates each pair, reads and writes one
+// vector per record and lane.
+template <int NTN>
+__device__ __forceinline__ size_t rec_off(int i, int lane) {
+    constexpr int HT = NTN / 2;
+    return static_cast<size_t>(i % HT) * 512 + static_cast<size_t>(lane) * 8 + (i / HT) * 4;
+}
+
 template <bool BF>
 __device__ __forceinline__ f32x4 load_u(const void *u, size_t e) {
     if constexpr (BF) {
@@ -308,9 +320,9 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         __syncthreads();   // every read of this sub-chunk's LDS is done
     }
 
-    const size_t uo = (bhs * 4 + wave) * NTN * 256 + lane * 4;
+    const size_t uo = (bhs * 4 + wave) * NTN * 256;
 #pragma unroll
-    for (int i = 0; i < NTN; ++i) store_u<kBf16>(ws.u, uo + i * 256, uacc[i]);
+    for (int i = 0; i < NTN; ++i) store_u<kBf16>(ws.u, uo + rec_off<NTN>(i, lane), uacc[i]);
     if (tid == 0) ws.eda[bhs] = eacc;
     if constexpr (kUni) {   // each wave's pair angles into LDS
         if (lane == 0) {
@@ -551,9 +563,17 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         if (more) load_b(sck + 1);
     }
 
-    const size_t uo = (bhs * 4 + wave) * NTN * 256 + lane * 4;
+    const size_t uo = (bhs * 4 + wave) * NTN * 256;
 #pragma unroll
-    for (int i = 0; i < NTN; ++i) store_u<true>(ws.u, uo + i * 256, uacc[i]);
+    for (int i = 0; i < NTN / 2; ++i) {   // both halves of a pair in one 16-byte store
+        bf16x8 q;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            q[r] = static_cast<__bf16>(uacc[i][r]);
+            q[4 + r] = static_cast<__bf16>(uacc[i + NTN / 2][r]);
+        }
+        *reinterpret_cast<bf16x8 *>(static_cast<__bf16 *>(ws.u) + uo + rec_off<NTN>(i, lane)) = q;
+    }
     if (tid == 0) ws.eda[bhs] = eacc;
     // the segment's angle total per pair (wrapped), with its cosine and sine,
     // one thread per pair: each wave's uniform angles through LDS
@@ -625,6 +645,39 @@ __device__ __forceinline__ void store_rec(void *u, size_t e, const fvec<RP> v) {
     }
 }
 
+// A pair's two halves, RP values each, of a record at element e (the low
+// half at e, the high half four elements on: rec_off); all four pairs of a
+// lane in one 16-byte access for bf16.
+template <bool BF, int RP>
+__device__ __forceinline__ void load_pair(const void *u, size_t e, fvec<RP> &lo, fvec<RP> &hi) {
+    if constexpr (BF && RP == 4) {
+        const bf16x8 q = *reinterpret_cast<const bf16x8 *>(static_cast<const __bf16 *>(u) + e);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            lo[r] = static_cast<float>(q[r]);
+            hi[r] = static_cast<float>(q[4 + r]);
+        }
+    } else {
+        lo = load_rec<BF, RP>(u, e);
+        hi = load_rec<BF, RP>(u, e + 4);
+    }
+}
+template <bool BF, int RP>
+__device__ __forceinline__ void store_pair(void *u, size_t e, const fvec<RP> lo, const fvec<RP> hi) {
+    if constexpr (BF && RP == 4) {
+        bf16x8 q;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            q[r] = static_cast<__bf16>(lo[r]);
+            q[4 + r] = static_cast<__bf16>(hi[r]);
+        }
+        *reinterpret_cast<bf16x8 *>(static_cast<__bf16 *>(u) + e) = q;
+    } else {
+        store_rec<BF, RP>(u, e, lo);
+        store_rec<BF, RP>(u, e + 4, hi);
+    }
+}
+
 // One thread per (batch, head, p, RP state pairs): RP of the four values a
 // lane holds in a record's MFMA D layout, so 4 / RP threads share a lane's
 // four (more threads in flight for the same records).
@@ -688,9 +741,8 @@ state_pass_kernel(ScanLaunch a, ChunkWs ws, int nck) {   // nck: segments per se
     auto load = [&](int k, In &d) {
         const int kk = k < nck ? k : nck - 1;   // past the end: re-read the last chunk, unused
         const size_t bhk = bhk0 + kk;
-        const size_t u = (bhk * 4 + pt) * NTN * 256 + lane * 4 + RP * part;
-        d.ulo = load_rec<kBf16, RP>(ws.u, u + i1 * 256);
-        d.uhi = load_rec<kBf16, RP>(ws.u, u + (i1 + HT) * 256);
+        const size_t u = (bhk * 4 + pt) * NTN * 256 + rec_off<NTN>(i1, lane) + RP * part;
+        load_pair<kBf16, RP>(ws.u, u, d.ulo, d.uhi);
         d.e = ws.eda[bhk];
         if (rot) {
             d.cs = *reinterpret_cast<const V *>(ws.cph + bhk * NH + nlo);
@@ -699,9 +751,8 @@ state_pass_kernel(ScanLaunch a, ChunkWs ws, int nck) {   // nck: segments per se
         }
     };
     auto step = [&](int k, const In &d) {
-        const size_t so = ((bhk0 + k) * 4 + pt) * NTN * 256 + lane * 4 + RP * part;
-        store_rec<kBf16, RP>(ws.s, so + i1 * 256, lo);
-        store_rec<kBf16, RP>(ws.s, so + (i1 + HT) * 256, hi);
+        const size_t so = ((bhk0 + k) * 4 + pt) * NTN * 256 + rec_off<NTN>(i1, lane) + RP * part;
+        store_pair<kBf16, RP>(ws.s, so, lo, hi);
         lo = lo * d.e + d.ulo;
         hi = hi * d.e + d.uhi;
         if (rot) {
@@ -837,16 +888,17 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     constexpr int NF = kBf16 ? N / 32 : NTN;
     frag_t sf[NF];
     if constexpr (kBf16) {
-        const bf16x4 *src = static_cast<const bf16x4 *>(ws.s) + (bhs * 4 + wave) * NTN * 64 + lane;
+        const __bf16 *src = static_cast<const __bf16 *>(ws.s) + (bhs * 4 + wave) * NTN * 256;
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
-            const bf16x4 lo = src[(2 * f) * 64], hi = src[(2 * f + 1) * 64];
+            const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(src + rec_off<NTN>(2 * f, lane));
+            const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(src + rec_off<NTN>(2 * f + 1, lane));
             sf[f] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
     } else {
-        const f32x4 *src = static_cast<const f32x4 *>(ws.s) + (bhs * 4 + wave) * NTN * 64 + lane;
+        const float *src = static_cast<const float *>(ws.s) + (bhs * 4 + wave) * NTN * 256;
 #pragma unroll
-        for (int f = 0; f < NF; ++f) sf[f] = src[f * 64];
+        for (int f = 0; f < NF; ++f) sf[f] = *reinterpret_cast<const f32x4 *>(src + rec_off<NTN>(f, lane));
     }
 
     float A = 0.0f;
@@ -1199,16 +1251,15 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     const SeqBufs rs = seq_bufs<bf16_t, N, P, 1>(a, bb, hh);
     const int h_end = min(kseg, nsub - seg * kseg);
 
-    // the state entering this segment, in its frame, as carry-in A operands
-    // (n-tiles 2f and 2f + 1 form k-block f: n = 32 f + 16 h + 4 g + r)
+    // the state entering this segment, in its frame, as carry-in A operands:
+    // n-tiles f and f + NF (a rotation pair's halves, side by side in the
+    // record) form k-block f, n = 16 f + 16 NF h + 4 g + r for k-slot 4 h + r
     bf16x8 sf[NF];
     {
-        const bf16x4 *src = static_cast<const bf16x4 *>(ws.s) + (bhs * 4 + wave) * (N / 16) * 64 + lane;
+        const __bf16 *src = static_cast<const __bf16 *>(ws.s) + (bhs * 4 + wave) * (N / 16) * 256;
 #pragma unroll
-        for (int f = 0; f < NF; ++f) {
-            const bf16x4 lo = src[(2 * f) * 64], hi = src[(2 * f + 1) * 64];
-            sf[f] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
+        for (int f = 0; f < NF; ++f)
+            sf[f] = *reinterpret_cast<const bf16x8 *>(src + rec_off<N / 16>(f, lane));
     }
     float A = 0.0f;
     if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);
@@ -1387,8 +1438,8 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
             typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
-            const bf16x4v lo = *reinterpret_cast<const bf16x4v *>(sm.c + rtile_off<CB>(t, 32 * f + 4 * g));
-            const bf16x4v hi = *reinterpret_cast<const bf16x4v *>(sm.c + rtile_off<CB>(t, 32 * f + 16 + 4 * g));
+            const bf16x4v lo = *reinterpret_cast<const bf16x4v *>(sm.c + rtile_off<CB>(t, 16 * f + 4 * g));
+            const bf16x4v hi = *reinterpret_cast<const bf16x4v *>(sm.c + rtile_off<CB>(t, 16 * (f + NF) + 4 * g));
             const bf16x8 cv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             acc = mfma_bf16(sf[f], cv, acc);
         }
@@ -1435,7 +1486,7 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             for (int q = 0; q < 2; ++q) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) st[q][r] = static_cast<float>(sf[f][q * 4 + r]) * eh;
-                const int col = 16 * (2 * f + q) + 4 * (c & 3);
+                const int col = 16 * (f + q * NF) + 4 * (c & 3);
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
                     const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + rtile_off<CB>(32 * kb + r0, col)));
