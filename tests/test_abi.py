@@ -163,23 +163,24 @@ def test_scan_workspace_query():
 
     # per segment: U and S (bf16 64x128 each), the segment decay, and angle
     # total / cosine / sine per pair (3 x 64 f32).  At config 1 (96 sequences
-    # of 32 sub-chunks of 64 tokens) segments of 2 sub-chunks give 1536
-    # chunk_scan workgroups: two rounds of three per CU on the 256 CUs the
+    # of 32 sub-chunks of 64 tokens) segments of 4 sub-chunks give 768
+    # chunk_scan workgroups: one round of three per CU on the 256 CUs the
     # query assumes without a device
     record = 2 * 64 * 128 * 2 + 4 + 3 * 64 * 4
-    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 8 * 12 * 16 * record
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 8 * 12 * 8 * record
     # chunk_size is the shortest segment: 512 tokens -> 4 segments per sequence
     assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16, chunk=512) == 8 * 12 * 4 * record
-    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16, chunk=1) == 8 * 12 * 16 * record
-    # f32 storage: 32-token sub-chunks, 4 per segment, and f32 U and S
-    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) == 8 * 12 * 16 * (64 * 128 * 8 + 4 + 3 * 64 * 4)
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16, chunk=1) == 8 * 12 * 8 * record
+    # f32 storage: 32-token sub-chunks, 8 per segment, and f32 U and S
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) == 8 * 12 * 8 * (64 * 128 * 8 + 4 + 3 * 64 * 4)
     # the single pass runs one sequence per CU (256 CUs here, the CPU
     # fallback of the query): it is the faster form once its last round of
-    # sequences fills 70 % of the CUs
-    assert need(16, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 0   # 192 sequences
+    # sequences fills 85 % of the CUs
+    assert need(16, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 8 * 12 * 2 * 4 * record  # 192: 75 %
+    assert need(20, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 0   # 240 sequences: 94 %
     assert need(14, 2048, 12, 64, 128, 1, _lib.M3_BF16) > 0    # 168
     assert need(24, 2048, 12, 64, 128, 1, _lib.M3_BF16) > 0    # 288: 1.13 rounds
-    assert need(32, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 0   # 384: 1.5 rounds
+    assert need(40, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 0   # 480: 1.88 rounds
     assert need(1, 100, 2, 48, 128, 1, _lib.M3_BF16) == 0      # head_dim 48
     assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) == 0       # d_state 96
     assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) == 0      # rank 3
