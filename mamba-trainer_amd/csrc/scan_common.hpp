@@ -127,6 +127,13 @@ __device__ __forceinline__ float dexp(float d) {
     return expf(d);
 }
 
+// dexp for a log decay given in log2 units (d * log2 e): the clamp is one
+// median-of-three and the exponential the hardware exp2.
+constexpr float kLog2e = 1.44269504088896341f;
+__device__ __forceinline__ float dexp2(float d2) {
+    return __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(d2, -60.0f * kLog2e, 0.0f));
+}
+
 // The wrapped angle of one rotation pair at this lane's token, relative to
 // the segment start: the running angle entering the sub-chunk plus the
 // in-sub-chunk inclusive prefix `pre`.  The sub-chunk's last token (lane

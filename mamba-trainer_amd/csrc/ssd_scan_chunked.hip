@@ -1231,6 +1231,7 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     constexpr int NT = 4;             // 16-row tiles of a sub-chunk
     constexpr int NF = N / 32;        // state fragments (k-blocks of n)
     constexpr int HV = PW / 8;
+    constexpr int RB = CB * 16;       // bytes per row of the B / C tiles
     static_assert(G::SUBS == 1 && QT == 64 && PPL == PW, "lane = token, one segment per wave");
     static_assert(CB % 4 == 0 && CT % 4 == 0 && CX % 4 == 0, "row loads spread over four waves");
     // loads a wave issues per sub-chunk: C with the four scalars, B with
@@ -1251,20 +1252,27 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     const SeqBufs rs = seq_bufs<bf16_t, N, P, 1>(a, bb, hh);
     const int h_end = min(kseg, nsub - seg * kseg);
 
-    // the state entering this segment, in its frame, as carry-in A operands:
-    // n-tiles f and f + NF (a rotation pair's halves, side by side in the
-    // record) form k-block f, n = 16 f + 16 NF h + 4 g + r for k-slot 4 h + r
-    bf16x8 sf[NF];
+    // the state entering this segment, in its frame, in the carry-in A
+    // operand layout: n-tiles f and f + NF (a rotation pair's halves, side by
+    // side in the record) form k-block f, n = 16 f + 16 NF h + 4 g + r for
+    // k-slot 4 h + r.  Carried in f32 across the sub-chunks; its bf16 copy
+    // is the carry-in operand.
+    f32x4 sacc[NF][2];
     {
         const __bf16 *src = static_cast<const __bf16 *>(ws.s) + (bhs * 4 + wave) * (N / 16) * 256;
 #pragma unroll
-        for (int f = 0; f < NF; ++f)
-            sf[f] = *reinterpret_cast<const bf16x8 *>(src + rec_off<N / 16>(f, lane));
+        for (int f = 0; f < NF; ++f) {
+            const bf16x8 v = *reinterpret_cast<const bf16x8 *>(src + rec_off<N / 16>(f, lane));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sacc[f][0][r] = static_cast<float>(v[r]);
+                sacc[f][1][r] = static_cast<float>(v[4 + r]);
+            }
+        }
     }
     float A = 0.0f;
     if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);
     const float dskip = a.d_skip ? a.d_skip[hh] : 0.0f;
-    const bool skip = a.d_skip != nullptr;
     float run[PPL];   // wave-uniform running pair angles, in turns (pair_turns)
 #pragma unroll
     for (int j = 0; j < PPL; ++j) run[j] = 0.0f;
@@ -1312,6 +1320,12 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     const int par = sck & 1;
     const uint32_t tok0 = static_cast<uint32_t>(sck) * QT;
     const bool more = h + 1 < h_end;
+    // Tile addressing.  Rows 16 i + c of a B / C tile share the chunk
+    // permutation rsw(c), and the k-chunk indices XORed with it below have
+    // bits disjoint from the lane's own part, so every operand address is a
+    // per-lane offset plus a constant (the LDS instruction's immediate).
+    const int sw = rsw<CB>(c);
+    const int crow = c * RB;
 
     // B, C, theta and the scalars of this sub-chunk landed (X may be out)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm<kX>());
@@ -1326,7 +1340,9 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     token_scalars(a, sc, A, live, av, gv, wv);
     const float acum = seg_scan<64>(av);
     if (wave == 0) {
-        sm.acum[lane] = acum;
+        // the log decay prefix in log2 units, as the band and the carry-in
+        // take it (dexp2)
+        sm.acum[lane] = acum * kLog2e;
         sm.gw[lane] = gv;
         sm.ww[lane] = wv;
         const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
@@ -1390,60 +1406,98 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     }
     __syncthreads();   // B~, C~ complete; theta is dead, its region takes the band
 
-    // ---- masked band into R[p] (tiles (tj, si) with si <= tj, plus the zero
-    //      tiles above the diagonal that the y product's 32-row k-blocks
-    //      read), and the carry-in product sum_n S[p][n] C~[t][n] per t-tile
+    // ---- masked band into R[p]: tile (TJ, SI) of (C~ B~^T o L)[t][s],
+    //      t = 16 TJ + c, s = 16 SI + 4 g + r, for SI <= TJ, and the zero
+    //      tiles above the diagonal that the y product's 32-row k-blocks read
     {
-        int idx = 0;
+        // the k-block kb of a row: chunk 4 kb + g, permuted
+        const int zg = (g ^ sw) << 4;
+        const int mrow = c * (LDM * 2) + 8 * g;   // this lane's band slot, bytes
+        auto tile = [&](auto tj_c, auto si_c) {
+            constexpr int TJ = decltype(tj_c)::value, SI = decltype(si_c)::value;
+            __bf16 *const dst = reinterpret_cast<__bf16 *>(reinterpret_cast<unsigned char *>(ms) + mrow +
+                                                           TJ * 16 * LDM * 2 + SI * 32);
+            if constexpr (SI > TJ) {
+                const float z[4] = {0.f, 0.f, 0.f, 0.f};
+                st4(dst, z);
+            } else {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int tj = 0; tj < NT; ++tj) {
-            const int ncol = tj < 2 ? 2 : 4;
+                for (int kb = 0; kb < N / 32; ++kb) {
+                    const int o = ((kb << 6) ^ zg) + crow;
+                    const bf16x8 av = *reinterpret_cast<const bf16x8 *>(sm.b + SI * 16 * RB + o);
+                    const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(sm.c + TJ * 16 * RB + o);
+                    acc = mfma_bf16(av, bv, acc);
+                }
+                const float at = sm.acum[16 * TJ + c];
+                const f32x4 as = *reinterpret_cast<const f32x4 *>(&sm.acum[16 * SI + 4 * g]);
+                const f32x4 ws4 = *reinterpret_cast<const f32x4 *>(&sm.ww[16 * SI + 4 * g]);
+                float vals[4];
+                if constexpr (SI < TJ) {
 #pragma unroll
-            for (int si = 0; si < ncol; ++si) {
-                if ((idx++) % 4 != wave) continue;
-                const int trow = 16 * tj + c;
-                float vals[4] = {0.f, 0.f, 0.f, 0.f};
-                if (si <= tj) {
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int kb = 0; kb < N / 32; ++kb) {
-                        const bf16x8 av = *reinterpret_cast<const bf16x8 *>(
-                            sm.b + rtile_off<CB>(16 * si + c, 32 * kb + 8 * g));
-                        const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(
-                            sm.c + rtile_off<CB>(trow, 32 * kb + 8 * g));
-                        acc = mfma_bf16(av, bv, acc);
-                    }
-                    const float at = sm.acum[trow];
+                    for (int r = 0; r < 4; ++r) vals[r] = acc[r] * ws4[r] * dexp2(at - as[r]);
+                } else {
+                    // the diagonal tile: s < t off-diagonal weight, s = t the
+                    // diagonal weight and the skip D (scan.rs:593-597)
+                    const f32x4 gs4 = *reinterpret_cast<const f32x4 *>(&sm.gw[16 * SI + 4 * g]);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int srow = 16 * si + 4 * g + r;
-                        float v = 0.0f;
-                        if (srow <= trow) {
-                            const float wgt = (srow == trow) ? sm.gw[srow] : sm.ww[srow];
-                            v = acc[r] * wgt * dexp<true>(at - sm.acum[srow]);
-                        }
-                        if (skip && srow == trow) v += dskip;   // scan.rs:593-597
-                        vals[r] = v;
+                        const int d = 4 * g + r - c;
+                        const float off = acc[r] * ws4[r] * dexp2(at - as[r]);
+                        const float dia = acc[r] * gs4[r] + dskip;
+                        vals[r] = d < 0 ? off : (d == 0 ? dia : 0.0f);
                     }
                 }
-                st4(&ms[trow * LDM + 16 * si + 4 * g], vals);
+                st4(dst, vals);
             }
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I3 = std::integral_constant<int, 3>;
+        // three or two product tiles per wave
+        if (wave == 0) {
+            tile(I0{}, I0{}); tile(I2{}, I0{}); tile(I3{}, I0{});
+        } else if (wave == 1) {
+            tile(I0{}, I1{}); tile(I2{}, I1{}); tile(I3{}, I1{});
+        } else if (wave == 2) {
+            tile(I1{}, I0{}); tile(I2{}, I2{}); tile(I3{}, I2{});
+        } else {
+            tile(I1{}, I1{}); tile(I2{}, I3{}); tile(I3{}, I3{});
         }
     }
-    f32x4 yc[NT];   // the carry-in part of y^T[p][t], scaled by exp_decay(acum_t)
+    // ---- the carry-in product sum_n S[p][n] C~[t][n] per t-tile: k-slots
+    //      4 h + 0..3 of block f are n = 16 (f + NF h) + 4 g + 0..3, i.e.
+    //      chunk 2 (f + NF h) + (g >> 1) of the row, half g & 1
+    bf16x8 sf[NF];
 #pragma unroll
-    for (int tj = 0; tj < NT; ++tj) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const int t = 16 * tj + c;
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sf[f][r] = static_cast<__bf16>(sacc[f][0][r]);
+            sf[f][4 + r] = static_cast<__bf16>(sacc[f][1][r]);
+        }
+    f32x4 yc[NT];   // the carry-in part of y^T[p][t], scaled by exp_decay(acum_t)
+    {
+        const int zc = ((g >> 1) ^ sw) << 4;
+        const int cbase = crow + (g & 1) * 8;
+#pragma unroll
+        for (int tj = 0; tj < NT; ++tj) yc[tj] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
-            typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
-            const bf16x4v lo = *reinterpret_cast<const bf16x4v *>(sm.c + rtile_off<CB>(t, 16 * f + 4 * g));
-            const bf16x4v hi = *reinterpret_cast<const bf16x4v *>(sm.c + rtile_off<CB>(t, 16 * (f + NF) + 4 * g));
-            const bf16x8 cv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            acc = mfma_bf16(sf[f], cv, acc);
+            const int olo = (((2 * f) << 4) ^ zc) + cbase;
+            const int ohi = (((2 * (f + NF)) << 4) ^ zc) + cbase;
+#pragma unroll
+            for (int tj = 0; tj < NT; ++tj) {
+                typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
+                const bf16x4v lo = *reinterpret_cast<const bf16x4v *>(sm.c + tj * 16 * RB + olo);
+                const bf16x4v hi = *reinterpret_cast<const bf16x4v *>(sm.c + tj * 16 * RB + ohi);
+                const bf16x8 cv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                yc[tj] = mfma_bf16(sf[f], cv, yc[tj]);
+            }
         }
-        yc[tj] = acc * dexp<true>(sm.acum[t]);
+#pragma unroll
+        for (int tj = 0; tj < NT; ++tj) yc[tj] = yc[tj] * dexp2(sm.acum[16 * tj + c]);
     }
     __syncthreads();   // the band is complete; C~ is dead
     if (more) load_c(sck + 1, sc_next);
@@ -1469,9 +1523,11 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 
     if (more) {
         // ---- S' = e_h S + U_h, U_h^T[n][p] = sum_s B~[s][n] (w decay X^T)[p][s]
-        // over this wave's p-tile: A operand B~^T by transposed reads, B
-        // operand the weighted X^T fragments (rounded to bf16 once)
-        const float eh = dexp<true>(sm.acum[QT - 1]);
+        // over this wave's p-tile: A operand B~^T by transposed reads (row
+        // 32 kb + r0 (+ 4), columns 16 (f + q NF) + 4 (c & 3) + 0..3: chunk
+        // 2 (f + q NF) + ((c & 3) >> 1), half c & 1), B operand the weighted
+        // X^T fragments (rounded to bf16 once)
+        const float eh = dexp2(sm.acum[QT - 1]);
         bf16x8 xw[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -1479,47 +1535,49 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             for (int j = 0; j < 8; ++j)
                 xw[kb][j] = static_cast<__bf16>(static_cast<float>(xf[kb][j]) * sm.wdv[32 * kb + 8 * g + j]);
         const int r0 = 8 * g + (c >> 2);
+        const int zlo = (((c & 3) >> 1) ^ rsw<CB>(r0 & 15)) << 4;
+        const int zhi = (((c & 3) >> 1) ^ rsw<CB>((r0 + 4) & 15)) << 4;
+        const int blo = r0 * RB + (c & 1) * 8, bhi = (r0 + 4) * RB + (c & 1) * 8;
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
-            f32x4 st[2];
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) st[q][r] = static_cast<float>(sf[f][q * 4 + r]) * eh;
-                const int col = 16 * (f + q * NF) + 4 * (c & 3);
+                f32x4 st = sacc[f][q] * eh;
+                const int ch = (2 * (f + q * NF)) << 4;
+                const int olo = (ch ^ zlo) + blo, ohi = (ch ^ zhi) + bhi;
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
-                    const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + rtile_off<CB>(32 * kb + r0, col)));
-                    const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + rtile_off<CB>(32 * kb + r0 + 4, col)));
+                    const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + 32 * kb * RB + olo));
+                    const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + 32 * kb * RB + ohi));
                     const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    st[q] = mfma_bf16(av, xw[kb], st[q]);
+                    st = mfma_bf16(av, xw[kb], st);
                 }
+                sacc[f][q] = st;
             }
-#pragma unroll
-            for (int q = 0; q < 2; ++q)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) sf[f][q * 4 + r] = static_cast<__bf16>(st[q][r]);
         }
         __syncthreads();   // B~ and X are dead
         load_bt(sck + 1);
     }
 
     // ---- y^T[p][t] = exp(acum_t) sum_n S[p][n] C~[t][n] + sum_s X^T[p][s] M[t][s]
+    {
+        const unsigned char *const mb = reinterpret_cast<const unsigned char *>(ms) + c * (LDM * 2) + 16 * g;
 #pragma unroll
-    for (int tj = 0; tj < NT; ++tj) {
-        f32x4 acc = yc[tj];
-        const int t = 16 * tj + c;
-        const int nkb = tj < 2 ? 1 : 2;
+        for (int tj = 0; tj < NT; ++tj) {
+            f32x4 acc = yc[tj];
+            const int t = 16 * tj + c;
+            const int nkb = tj < 2 ? 1 : 2;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-            if (kb < nkb)
-                acc = mfma_bf16(xf[kb], *reinterpret_cast<const bf16x8 *>(&ms[t * LDM + 32 * kb + 8 * g]), acc);
-        // rows past the sequence end fall outside the buffer: dropped
-        const uint32_t oy = (tok0 + t) * rs.tok_x + (16 * wave + 4 * g) * 2;
-        u32x2 pk;
-        pk[0] = pk_bf16(acc[0], acc[1]);
-        pk[1] = pk_bf16(acc[2], acc[3]);
-        bst8(pk, rs.y, oy);
+            for (int kb = 0; kb < 2; ++kb)
+                if (kb < nkb)
+                    acc = mfma_bf16(xf[kb], *reinterpret_cast<const bf16x8 *>(mb + tj * 16 * LDM * 2 + kb * 64), acc);
+            // rows past the sequence end fall outside the buffer: dropped
+            const uint32_t oy = (tok0 + t) * rs.tok_x + (16 * wave + 4 * g) * 2;
+            u32x2 pk;
+            pk[0] = pk_bf16(acc[0], acc[1]);
+            pk[1] = pk_bf16(acc[2], acc[3]);
+            bst8(pk, rs.y, oy);
+        }
     }
     if (more) {
         __syncthreads();   // every read of the band is done
