@@ -57,7 +57,7 @@ MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA, TFLOP/s
 # GRBM_GUI_ACTIVE): 282.0 MB read + 57.3 MB written.  Counters cannot be read
 # inside this process; re-measured when the kernels change.
 SCAN_TRAFFIC_BYTES = 339_300_000
-SCAN_MFMA_BUSY = {"chunk_scan_dma_kernel": 0.069, "chunk_state_dma_kernel": 0.036}
+SCAN_MFMA_BUSY = {"chunk_scan_dma_kernel": 0.077, "chunk_state_dma_kernel": 0.037}
 
 # BASELINE config 1 (the headline) and config 3 (decode)
 SCAN = dict(B=8, L=2048, H=12, P=64, N=128, R=1, Q=64)
