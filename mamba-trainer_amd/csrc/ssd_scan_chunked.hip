@@ -543,18 +543,24 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
                     sm.x[buf] + rtile_off<CX>(32 * kb + r0 + 4, 16 * wave + cq)));
                 xo[kb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             }
+            // every fragment read first, so the LDS reads stream back to back
+            // and the products follow without a wait between them
+            bf16x8 av[NTN][2];
 #pragma unroll
-            for (int i = 0; i < NTN; ++i) {
-                f32x4 acc = uacc[i] * eh;
+            for (int i = 0; i < NTN; ++i)
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
                     const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(
                         sm.b + rtile_off<CB>(32 * kb + r0, 16 * i + cq)));
                     const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(
                         sm.b + rtile_off<CB>(32 * kb + r0 + 4, 16 * i + cq)));
-                    const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    acc = mfma_bf16(av, xo[kb], acc);
+                    av[i][kb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 }
+#pragma unroll
+            for (int i = 0; i < NTN; ++i) {
+                f32x4 acc = uacc[i] * eh;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) acc = mfma_bf16(av[i][kb], xo[kb], acc);
                 uacc[i] = acc;
             }
         }
@@ -1538,23 +1544,30 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         const int zlo = (((c & 3) >> 1) ^ rsw<CB>(r0 & 15)) << 4;
         const int zhi = (((c & 3) >> 1) ^ rsw<CB>((r0 + 4) & 15)) << 4;
         const int blo = r0 * RB + (c & 1) * 8, bhi = (r0 + 4) * RB + (c & 1) * 8;
+        // every fragment read first, so the LDS reads stream back to back
+        bf16x8 av[NF][2][2];
 #pragma unroll
-        for (int f = 0; f < NF; ++f) {
+        for (int f = 0; f < NF; ++f)
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
-                f32x4 st = sacc[f][q] * eh;
                 const int ch = (2 * (f + q * NF)) << 4;
                 const int olo = (ch ^ zlo) + blo, ohi = (ch ^ zhi) + bhi;
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
                     const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + 32 * kb * RB + olo));
                     const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + 32 * kb * RB + ohi));
-                    const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    st = mfma_bf16(av, xw[kb], st);
+                    av[f][q][kb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 }
+            }
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                f32x4 st = sacc[f][q] * eh;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) st = mfma_bf16(av[f][q][kb], xw[kb], st);
                 sacc[f][q] = st;
             }
-        }
         __syncthreads();   // B~ and X are dead
         load_bt(sck + 1);
     }
