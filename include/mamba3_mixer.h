@@ -21,6 +21,9 @@
  *   m3_mixer_gate               Mamba3Mixer::finish before out_proj
  *                                                         src/models/mamba3.rs:468-477
  *   m3_embedding_lookup         Embedding::lookup         src/nn/embedding.rs
+ *   m3_mixer_step               Mamba3Mixer::step between in_proj and out_proj in
+ *                               one launch (prologue, mamba3_step, gate)
+ *                                                         src/models/mamba3.rs:569-630
  *
  * Conventions are those of mamba3_ssm.h: caller-allocated contiguous device
  * buffers, asynchronous on `stream`, status codes with m3_last_error().
@@ -126,6 +129,23 @@ m3_status m3_mixer_prologue_conv(const m3_mixer_dims *d, const m3_conv1d *conv,
 m3_status m3_mixer_gate(size_t tokens, size_t d_inner, const void *y, const void *z,
                         size_t z_stride, const float *norm_weight, float eps, void *out,
                         void *stream);
+
+/* Mamba3Mixer::step between its two projections (src/models/mamba3.rs:569-630,
+ * after in_proj and before out_proj) in one launch, for one token per
+ * sequence (d->tokens is the batch): m3_mixer_prologue on `projected`
+ * [batch, in_proj_width], then m3_step on `state` (or m3_step_factored on
+ * `factored`; exactly one is non-NULL) in place with a_log [H] and d_skip [H]
+ * (or NULL), then m3_mixer_gate without a post-gate norm into out
+ * [batch, d_inner] (bf16).  The results equal those three calls bit for bit;
+ * the scan inputs and y never go through memory.  No reference counterpart
+ * as one call (the reference issues the three pieces).  No convolution and
+ * no post-gate norm: compose the calls for those.  Shapes: d_state a multiple
+ * of 8 up to 128 with d_state / 8 a power of two, head_dim * rank a multiple
+ * of 8 up to 512, rank 1, 2, 4 or 8 (else M3_ERR_UNSUPPORTED). */
+m3_status m3_mixer_step(const m3_mixer_dims *d, const void *projected, const float *dt_bias,
+                        const float *b_bias, const float *c_bias, const float *bc_norm,
+                        const float *a_log, const float *d_skip, m3_ssm_state *state,
+                        m3_ssm_state_factored *factored, void *out, void *stream);
 
 /* out[i] = table[ids[i]] for bf16 rows of dim (table [vocab, dim]).  The
  * ids live on the device, so they are not checked on the host: an id outside

@@ -23,6 +23,7 @@
 // full form's bit for bit, and the state streams h only: 8 bytes per element.
 #include "m3_device.hpp"
 #include "m3_internal.hpp"
+#include "mixer_math.hpp"
 
 namespace m3 {
 
@@ -114,10 +115,126 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
     gamma = lam * step;
 }
 
+// The fused step's prologue (MixerStepLaunch): the projection row of this
+// sequence through the 16-byte prologue's arithmetic (mixer_math.hpp, the
+// same roundings: every value is rounded to bf16 where m3_mixer_prologue
+// stores it) into LDS -- B and C raw [N][R] (braw, craw), x, theta, dt and
+// lambda -- then step_prologue's angle advance, rotation and coefficients on
+// those values.
+template <int R, bool FACT>
+__device__ __forceinline__ void mix_prologue(const MixerStepLaunch &m, size_t bh, float *bt,
+                                             float *ct, float *xs, float &alpha, float &beta,
+                                             float &gamma, float *bpt, float *braw, float *craw,
+                                             float *thv, float *scal) {
+    using namespace mixm;
+    const StepLaunch &a = m.s;
+    const int tid = threadIdx.x;
+    const int H = static_cast<int>(a.heads), P = static_cast<int>(a.head_dim);
+    const int N = static_cast<int>(a.d_state), half = N / 2;
+    const size_t bq = bh / a.heads;
+    const int h = static_cast<int>(bh % a.heads);
+    const int din = H * P * R;
+    const int bcw = static_cast<int>(m.groups) * R * N;
+    const uint16_t *row = static_cast<const uint16_t *>(m.projected) + bq * m.width;
+    const uint16_t *px = row + din;
+    const uint16_t *pb = px + din;
+    const uint16_t *pc = pb + bcw;
+    const uint16_t *pdt = pc + bcw;
+    const uint16_t *plam = pdt + H;
+    const uint16_t *pth = plam + (m.learned_lambda ? H : 0);
+    const int lq = N / 8;
+    const int grp = h / (H / static_cast<int>(m.groups));
+    const int nx = P * R / 8;
+    if (tid < 2 * lq) {
+        // B (lanes 0 .. lq-1) and C (lq .. 2 lq-1): eight states of every rank
+        const int which = tid / lq, q = tid - which * lq;
+        const uint16_t *src = (which ? pc : pb) + grp * R * N + q * 8;
+        const float *bias = which ? m.c_bias : m.b_bias;
+        float v[R][8], bb[8], w[8];
+#pragma unroll
+        for (int r = 0; r < R; ++r) unpack8(*reinterpret_cast<const uint4 *>(src + r * N), v[r]);
+        if (bias) {
+            const float4 b0 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8);
+            const float4 b1 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8 + 4);
+            bb[0] = b0.x; bb[1] = b0.y; bb[2] = b0.z; bb[3] = b0.w;
+            bb[4] = b1.x; bb[5] = b1.y; bb[6] = b1.z; bb[7] = b1.w;
+        }
+        if (m.bc_norm) {
+            const float4 w0 = *reinterpret_cast<const float4 *>(m.bc_norm + q * 8);
+            const float4 w1 = *reinterpret_cast<const float4 *>(m.bc_norm + q * 8 + 4);
+            w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
+            w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
+        }
+        bc_row8<R>(v, bb, bias != nullptr, w, m.bc_norm != nullptr, lq, N, m.norm_eps);
+        float *dst = which ? craw : braw;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < R; ++r) dst[(q * 8 + j) * R + r] = bf16_bits_to_f32(to_bits(v[r][j]));
+    } else if (tid >= 64 && tid < 64 + nx) {
+        const int k = tid - 64;
+        float f[8];
+        unpack8(*reinterpret_cast<const uint4 *>(px + h * P * R + k * 8), f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xs[k * 8 + j] = bf16_bits_to_f32(to_bits(silu_fast(f[j])));
+    } else if (tid >= 128 && tid < 128 + half && a.theta != nullptr) {
+        thv[tid - 128] = bf(pth, static_cast<size_t>(h) * half + (tid - 128));
+    } else if (tid == 255) {
+        scal[0] = softplusf_(bf(pdt, h) + m.dt_bias[h]);
+        scal[1] = m.learned_lambda ? sigmoidf_(bf(plam, h)) : m.fixed_lambda;
+    }
+    __syncthreads();
+
+    const float step = scal[0];
+    const float lam = scal[1];
+    const size_t bc_base = bh * N * R;
+    if (a.theta != nullptr) {
+        for (int i = tid; i < half; i += kStepThreads) {
+            // phi = wrap(prev + dt * theta)   (fused.rs:1549-1553)
+            const float prev = a.angle[bh * half + i];
+            float raw = thv[i] * step + prev;
+            float phi = wrap_angle(raw);
+            a.angle[bh * half + i] = phi;
+            float sn, cs;
+            sincosf(phi, &sn, &cs);
+            if constexpr (FACT) {
+                float ps, pc;
+                sincosf(prev, &ps, &pc);
+                for (int r = 0; r < R; ++r) {
+                    const float b1 = ld<bf16_t>(a.b_prev, bc_base + i * R + r);
+                    const float b2 = ld<bf16_t>(a.b_prev, bc_base + (i + half) * R + r);
+                    bpt[i * R + r] = rot_lo(b1, b2, pc, ps);
+                    bpt[(i + half) * R + r] = rot_hi(b1, b2, pc, ps);
+                }
+            }
+            for (int r = 0; r < R; ++r) {
+                const float b1 = braw[i * R + r], b2 = braw[(i + half) * R + r];
+                const float c1 = craw[i * R + r], c2 = craw[(i + half) * R + r];
+                bt[i * R + r] = rot_lo(b1, b2, cs, sn);
+                bt[(i + half) * R + r] = rot_hi(b1, b2, cs, sn);
+                ct[i * R + r] = rot_lo(c1, c2, cs, sn);
+                ct[(i + half) * R + r] = rot_hi(c1, c2, cs, sn);
+            }
+        }
+    } else {
+        for (int i = tid; i < N * R; i += kStepThreads) {
+            bt[i] = braw[i];
+            ct[i] = craw[i];
+            if constexpr (FACT) bpt[i] = ld<bf16_t>(a.b_prev, bc_base + i);
+        }
+    }
+    const float A = 0.0f - expf(a.a_log[h]);
+    alpha = expf(step * A);
+    beta = (1.0f - lam) * step * alpha;
+    gamma = lam * step;
+}
+
 // Vector body: N % 4 == 0 and G = N / 4 lanes per row with G a power of two
 // that divides 64.  Each lane owns four consecutive state columns of a row.
-template <typename T, int RK, bool FACT>
-__device__ __forceinline__ void step_body_vec(const StepLaunch &a, size_t bh) {
+// MIX: the fused mixer step (mix_prologue in, the gate out).
+template <typename T, int RK, bool FACT, bool MIX = false>
+__device__ __forceinline__ void step_body_vec(const StepLaunch &a, size_t bh,
+                                              const MixerStepLaunch *m = nullptr) {
     extern __shared__ float smem[];
     const size_t N = a.d_state, P = a.head_dim;
     constexpr int R = RK;
@@ -126,18 +243,36 @@ __device__ __forceinline__ void step_body_vec(const StepLaunch &a, size_t bh) {
     float *xs = ct + N * R;
     float *bpt = xs + P * R;         // FACT: B~_prev [N][R], x_prev [P][R]
     float *xps = bpt + N * R;
+    // MIX: raw B, C [N][R], theta, dt and lambda (over B~_prev's slot when
+    // the state is not factored)
+    float *braw = FACT ? xps + P * R : bpt;
+    float *craw = braw + N * R;
+    float *thv = craw + N * R;
+    float *scal = thv + N / 2;
     float alpha, beta, gamma;
-    step_prologue<T, FACT>(a, bh, bt, ct, xs, alpha, beta, gamma, bpt, xps);
+    if constexpr (MIX)
+        mix_prologue<R, FACT>(*m, bh, bt, ct, xs, alpha, beta, gamma, bpt, braw, craw, thv, scal);
+    else
+        step_prologue<T, FACT>(a, bh, bt, ct, xs, alpha, beta, gamma, bpt, xps);
+    if constexpr (FACT && MIX) {
+        for (size_t i = threadIdx.x; i < P * R; i += kStepThreads)
+            xps[i] = ld<T>(a.x_prev, bh * P * R + i);
+    }
     __syncthreads();
     if constexpr (FACT) {
         // this step's x and b become the state's previous token (every read of
         // the old ones happened before the barrier)
-        const T *xb = static_cast<const T *>(a.x) + bh * P * R;
-        const T *bb = static_cast<const T *>(a.b) + bh * N * R;
         T *xp = static_cast<T *>(a.x_prev) + bh * P * R;
         T *bp = static_cast<T *>(a.b_prev) + bh * N * R;
-        for (size_t i = threadIdx.x; i < P * R; i += kStepThreads) xp[i] = xb[i];
-        for (size_t i = threadIdx.x; i < N * R; i += kStepThreads) bp[i] = bb[i];
+        if constexpr (MIX) {
+            for (size_t i = threadIdx.x; i < P * R; i += kStepThreads) xp[i] = from_f32<T>(xs[i]);
+            for (size_t i = threadIdx.x; i < N * R; i += kStepThreads) bp[i] = from_f32<T>(braw[i]);
+        } else {
+            const T *xb = static_cast<const T *>(a.x) + bh * P * R;
+            const T *bb = static_cast<const T *>(a.b) + bh * N * R;
+            for (size_t i = threadIdx.x; i < P * R; i += kStepThreads) xp[i] = xb[i];
+            for (size_t i = threadIdx.x; i < N * R; i += kStepThreads) bp[i] = bb[i];
+        }
     }
 
     const int lane = threadIdx.x & 63;
@@ -224,10 +359,24 @@ __device__ __forceinline__ void step_body_vec(const StepLaunch &a, size_t bh) {
 #pragma unroll
             for (int r = 0; r < R; ++r) ypart[r] = group_sum(ypart[r], G);
             if (live && (lane % G) == 0) {
-                T *y = static_cast<T *>(a.y);
+                if constexpr (MIX) {
+                    // the gate: silu(z) * y with y rounded to bf16 first, as
+                    // m3_mixer_gate reads it (models/mamba3.rs:468-477)
+                    const uint16_t *z = static_cast<const uint16_t *>(m->projected) +
+                                        (bh / a.heads) * m->width + (bh % a.heads) * P * R;
+                    uint16_t *o = static_cast<uint16_t *>(m->out) + bh * P * R;
 #pragma unroll
-                for (int r = 0; r < R; ++r)
-                    y[(bh * P + p) * R + r] = from_f32<T>(__builtin_fmaf(xs[p * R + r], dskip, ypart[r]));
+                    for (int r = 0; r < R; ++r) {
+                        const float yv =
+                            bf16_bits_to_f32(mixm::to_bits(__builtin_fmaf(xs[p * R + r], dskip, ypart[r])));
+                        o[p * R + r] = mixm::to_bits(yv * mixm::silu_fast(mixm::bf(z, p * R + r)));
+                    }
+                } else {
+                    T *y = static_cast<T *>(a.y);
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        y[(bh * P + p) * R + r] = from_f32<T>(__builtin_fmaf(xs[p * R + r], dskip, ypart[r]));
+                }
             }
         }
     }
@@ -264,6 +413,12 @@ step_kernel_vec_layers(StepLaunch base, StepLayerTable t) {
     a.x_prev = L.x_prev;
     a.b_prev = L.b_prev;
     step_body_vec<T, RK, FACT>(a, blockIdx.x - l * per);
+}
+
+template <int RK, bool FACT>
+__global__ void __launch_bounds__(kStepThreads)
+mixer_step_kernel(MixerStepLaunch m) {
+    step_body_vec<bf16_t, RK, FACT, true>(m.s, blockIdx.x, &m);
 }
 
 // Generic body for shapes the vector body does not cover (odd N, N > 256,
@@ -430,6 +585,40 @@ bool step_factored_supported(size_t d_state, size_t rank) {
     const size_t G = d_state / 4;
     return d_state % 4 == 0 && G >= 1 && G <= 64 && (G & (G - 1)) == 0 &&
            (rank == 1 || rank == 2 || rank == 3 || rank == 4 || rank == 8);
+}
+
+bool mixer_step_supported(size_t head_dim, size_t d_state, size_t rank, size_t width) {
+    const size_t lq = d_state / 8;
+    // (d_state <= 128: the prologue's theta lanes are threads 128 .. 128 + N/2 - 1,
+    // below the dt / lambda thread 255)
+    return d_state % 8 == 0 && lq >= 1 && lq <= 16 && (lq & (lq - 1)) == 0 &&
+           (head_dim * rank) % 8 == 0 && head_dim * rank / 8 <= 64 && width % 8 == 0 &&
+           (rank == 1 || rank == 2 || rank == 4 || rank == 8) &&
+           step_factored_supported(d_state, rank);
+}
+
+hipError_t launch_mixer_step(const MixerStepLaunch &m, hipStream_t stream) {
+    const StepLaunch &a = m.s;
+    if (a.batch * a.heads == 0) return hipSuccess;
+    const size_t N = a.d_state, P = a.head_dim, R = a.rank;
+    const bool fact = a.last_u == nullptr;
+    const size_t smem =
+        ((fact ? 5 : 4) * N * R + (fact ? 2 : 1) * P * R + N / 2 + 2) * sizeof(float);
+    const dim3 grid(static_cast<unsigned int>(a.batch * a.heads));
+#define M3_MIX(RK)                                                                                 \
+    if (fact)                                                                                      \
+        hipLaunchKernelGGL((mixer_step_kernel<RK, true>), grid, dim3(kStepThreads), smem, stream, m); \
+    else                                                                                           \
+        hipLaunchKernelGGL((mixer_step_kernel<RK, false>), grid, dim3(kStepThreads), smem, stream, m);
+    switch (R) {
+        case 1: M3_MIX(1) break;
+        case 2: M3_MIX(2) break;
+        case 4: M3_MIX(4) break;
+        case 8: M3_MIX(8) break;
+        default: return hipErrorNotSupported;
+    }
+#undef M3_MIX
+    return hipGetLastError();
 }
 
 hipError_t launch_step(const StepLaunch &a, hipStream_t stream) {

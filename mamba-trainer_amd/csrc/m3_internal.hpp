@@ -37,6 +37,27 @@ struct StepLayer {
     void *y;
     void *x_prev, *b_prev;
 };
+// The mixer's decode step between its two projections in one launch
+// (decode_step.hip): the 16-byte prologue's arithmetic on the projection row
+// of each sequence, the SSM step on the state in place, and the gate without
+// a post-gate norm.  `s` carries the shapes, a_log, d_skip and the state
+// buffers; its x, b, c, dt, lambda, theta and y are not used.
+struct MixerStepLaunch {
+    StepLaunch s;
+    size_t groups, width;
+    int learned_lambda;
+    float fixed_lambda, norm_eps;
+    const void *projected;          // bf16 [B, width]
+    const float *dt_bias;           // [H]
+    const float *b_bias, *c_bias;   // [H, N] or null
+    const float *bc_norm;           // [N] or null
+    void *out;                      // bf16 [B, H*P*R]: silu(z) * y
+};
+// Shapes the fused step covers: the 16-byte prologue's (d_state a multiple
+// of 8 with d_state / 8 a power of two, head_dim * rank and the row width
+// multiples of 8) and the vector step body's (rank 1, 2, 4 or 8).
+bool mixer_step_supported(size_t head_dim, size_t d_state, size_t rank, size_t width);
+hipError_t launch_mixer_step(const MixerStepLaunch &a, hipStream_t stream);
 constexpr size_t kStepLayersPerLaunch = 24;
 struct StepLayerTable {
     StepLayer layer[kStepLayersPerLaunch];

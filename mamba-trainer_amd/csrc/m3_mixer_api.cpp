@@ -192,6 +192,77 @@ m3_status m3_mixer_gate(size_t tokens, size_t d_inner, const void *y, const void
                     "gate launch");
 }
 
+m3_status m3_mixer_step(const m3_mixer_dims *d, const void *projected, const float *dt_bias,
+                        const float *b_bias, const float *c_bias, const float *bc_norm,
+                        const float *a_log, const float *d_skip, m3_ssm_state *state,
+                        m3_ssm_state_factored *factored, void *out, void *stream) {
+    if (d == nullptr) return m3::api_fail(M3_ERR_ARGUMENT, "mixer dims are NULL");
+    if ((state == nullptr) == (factored == nullptr))
+        return m3::api_fail(M3_ERR_ARGUMENT, "m3_mixer_step needs exactly one of state / factored");
+    if (d->heads == 0 || d->head_dim == 0 || d->d_state == 0 || d->rank == 0 || d->groups == 0)
+        return m3::api_fail(M3_ERR_CONFIG, "heads, head_dim, d_state, rank and groups must be positive");
+    if (d->heads % d->groups != 0)   // config.rs:207-212
+        return m3::api_fail(M3_ERR_CONFIG, "n_heads (%zu) must be a multiple of n_groups (%zu)",
+                            d->heads, d->groups);
+    const bool rot = d->dynamics == M3_ROTATIONAL;
+    if (rot && d->d_state % 2 != 0)
+        return m3::api_fail(M3_ERR_CONFIG, "rotational dynamics need an even d_state, got %zu",
+                            d->d_state);
+    const bool learned = lambda_learned(d->discretization);
+    const float fixed = m3_discretization_fixed_lambda(d->discretization);
+    if (!learned && !(fixed == fixed))
+        return m3::api_fail(M3_ERR_CONFIG, "unknown discretization %d", d->discretization);
+    const size_t width = m3_mixer_in_proj_width(d);
+    if (!m3::mixer_step_supported(d->head_dim, d->d_state, d->rank, width))
+        return m3::api_fail(M3_ERR_UNSUPPORTED, "m3_mixer_step covers d_state a multiple of 8 up to "
+                            "128 with d_state/8 a power of two, head_dim*rank a multiple of 8 up "
+                            "to 512 and rank 1, 2, 4 or 8; compose m3_mixer_prologue, m3_step "
+                            "and m3_mixer_gate");
+    if (d->tokens == 0) return m3::api_ok();
+    float *h = state ? state->h : factored->h;
+    float *angle = state ? state->angle : factored->angle;
+    if (projected == nullptr || dt_bias == nullptr || a_log == nullptr || out == nullptr ||
+        h == nullptr || (state && state->last_u == nullptr) ||
+        (factored && (factored->x_prev == nullptr || factored->b_prev == nullptr)))
+        return m3::api_fail(M3_ERR_ARGUMENT, "mixer step buffers are NULL");
+    if (rot && angle == nullptr)
+        return m3::api_fail(M3_ERR_ARGUMENT, "rotational dynamics need the state's angle buffer "
+                            "(updated in place)");
+    auto al16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (!al16(projected) || !al16(out) || !al16(h) || (state && !al16(state->last_u)) ||
+        (b_bias && !al16(b_bias)) || (c_bias && !al16(c_bias)) || (bc_norm && !al16(bc_norm)))
+        return m3::api_fail(M3_ERR_ARGUMENT, "projected, out, the state and the bias / norm "
+                            "vectors must be 16-byte aligned");
+    m3::MixerStepLaunch m{};
+    m3::StepLaunch &a = m.s;
+    a.batch = d->tokens;
+    a.heads = d->heads;
+    a.head_dim = d->head_dim;
+    a.d_state = d->d_state;
+    a.rank = d->rank;
+    a.bf16 = 1;
+    a.a_log = a_log;
+    a.d_skip = d_skip;
+    a.theta = rot ? projected : nullptr;   // presence only: theta comes from the projection row
+    a.h = h;
+    a.last_u = state ? state->last_u : nullptr;
+    a.angle = rot ? angle : nullptr;
+    a.x_prev = factored ? factored->x_prev : nullptr;
+    a.b_prev = factored ? factored->b_prev : nullptr;
+    m.groups = d->groups;
+    m.width = width;
+    m.learned_lambda = learned ? 1 : 0;
+    m.fixed_lambda = learned ? 0.0f : fixed;
+    m.norm_eps = d->norm_eps;
+    m.projected = projected;
+    m.dt_bias = dt_bias;
+    m.b_bias = b_bias;
+    m.c_bias = c_bias;
+    m.bc_norm = bc_norm;
+    m.out = out;
+    return launched(m3::launch_mixer_step(m, as_stream(stream)), "mixer step launch");
+}
+
 m3_status m3_embedding_lookup(size_t n, size_t dim, const int32_t *ids, size_t vocab,
                               const void *table, void *out, void *stream) {
     if (dim == 0 || vocab == 0) return m3::api_fail(M3_ERR_SHAPE, "empty embedding table");

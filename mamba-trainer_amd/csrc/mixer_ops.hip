@@ -8,17 +8,13 @@
 // writes its outputs once, with f32 arithmetic in registers.
 #include "m3_device.hpp"
 #include "m3_internal.hpp"
+#include "mixer_math.hpp"
 
 namespace m3 {
 
 namespace {
 
-__device__ __forceinline__ float bf(const uint16_t *p, size_t i) { return bf16_bits_to_f32(p[i]); }
-__device__ __forceinline__ uint16_t to_bits(float v) { return from_f32<bf16_t>(v).bits; }
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
-__device__ __forceinline__ float siluf_(float x) { return x * sigmoidf_(x); }
-// max(x, 0) + ln(1 + exp(-|x|))  (fused.rs:1291-1293)
-__device__ __forceinline__ float softplusf_(float x) { return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x))); }
+using namespace mixm;
 
 // ---------------------------------------------------------------- RMSNorm
 // One wave per row.  Rows whose width is a multiple of 8 and whose base is
@@ -231,25 +227,7 @@ mixer_prologue_kernel(PrologueLaunch a) {
 // A (B|C, head) row's lq lanes are consecutive and lq-aligned, so the RMSNorm
 // sum over the state axis is a reduction over those lanes.  The rank-last
 // output of a lane is the 8 x R block of states q*8.. of all ranks: R whole
-// vectors.  silu uses exp(-v) = 2^(-v log2 e) on v_exp_f32 and v_rcp_f32,
-// within a few f32 ulps of the exact value, below bf16 rounding.
-__device__ __forceinline__ float silu_fast(float v) {
-    const float e = __builtin_amdgcn_exp2f(-v * 1.4426950408889634f);
-    return v * __builtin_amdgcn_rcpf(1.0f + e);
-}
-
-__device__ __forceinline__ void unpack8(const uint4 q, float *f) {
-    const unsigned int u[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        f[2 * j] = __uint_as_float(u[j] << 16);
-        f[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
-    }
-}
-
-__device__ __forceinline__ unsigned int pack2(float a, float b) {
-    return static_cast<unsigned int>(to_bits(a)) | (static_cast<unsigned int>(to_bits(b)) << 16);
-}
+// vectors.  silu is silu_fast (mixer_math.hpp).
 
 // Eight channels ch..ch+7 of [x | B | C] at a token (xbc_t its row's [x | B |
 // C]), through the convolution when CONV (see xbc_at).  The branch on the
@@ -321,32 +299,20 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
             float v[R][8];
 #pragma unroll
             for (int r = 0; r < R; ++r) xbc8<CONV>(a, px, pos, seqi, C, ch0 + r * N, v[r]);
-            float bb[8];
+            float bb[8], w[8];
             if (bias) {
                 const float4 b0 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8);
                 const float4 b1 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8 + 4);
                 bb[0] = b0.x; bb[1] = b0.y; bb[2] = b0.z; bb[3] = b0.w;
                 bb[4] = b1.x; bb[5] = b1.y; bb[6] = b1.z; bb[7] = b1.w;
             }
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[r][j] = silu_fast(v[r][j]) + (bias ? bb[j] : 0.0f);
             if (a.bc_norm) {
                 const float4 w0 = *reinterpret_cast<const float4 *>(a.bc_norm + q * 8);
                 const float4 w1 = *reinterpret_cast<const float4 *>(a.bc_norm + q * 8 + 4);
-                const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float ss = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) ss += v[r][j] * v[r][j];
-                    ss = group_sum(ss, lq);
-                    const float scale = 1.0f / sqrtf(ss / static_cast<float>(N) + a.norm_eps);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) v[r][j] = v[r][j] * scale * w[j];
-                }
+                w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
+                w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
             }
+            bc_row8<R>(v, bb, bias != nullptr, w, a.bc_norm != nullptr, lq, N, a.norm_eps);
             uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(which ? a.c : a.b) +
                                                    ((t * H + h) * N + q * 8) * R);
 #pragma unroll

@@ -247,6 +247,10 @@ class Mamba3Mixer:
                              "apply_with_state for a window")
         c = self.cfg
         B = input.shape[0]
+        if self.conv_weight is None and self.post_gate_norm is None:
+            out_fused = self._step_fused(input, cache, residual, out)
+            if out_fused is not None:
+                return out_fused
         if self.conv_weight is not None and cache.conv is None:
             cache.conv = self._history(B, input.device)
         proj = self.project(input, cache.conv, cache.conv)
@@ -255,6 +259,53 @@ class Mamba3Mixer:
         y = step(sq(proj.x), sq(proj.b), sq(proj.c), sq(proj.dt), sq(proj.lam),
                  self.a_log, sq(proj.theta), self.d_skip, cache.ssm)
         return self.finish(y.reshape(proj.x.shape), proj, residual=residual, out=out)
+
+    def _step_fused(self, input: torch.Tensor, cache: MixerCache, residual, out):
+        """step_ through m3_mixer_step (prologue, state step and gate in one
+        launch; the same results as the composed path bit for bit), or None
+        where it does not apply (its shapes, or a cache it cannot take)."""
+        c = self.cfg
+        if input.dim() != 3 or input.shape[2] != c.d_model:
+            return None
+        B = input.shape[0]
+        H, P, N, R = c.n_heads, c.head_dim, c.d_state, c.mode.rank()
+        st = cache.ssm
+        factored = isinstance(st, SsmStateFactored)
+        rot = c.dynamics == StateDynamics.Rotational
+        ok = st.h.shape == (B, H, P, N) and st.h.is_contiguous() and (not rot or st.angle is not None)
+        if factored:
+            ok = ok and st.x_prev.shape == (B, H, P, R) and st.b_prev.shape == (B, H, N, R) and \
+                st.x_prev.dtype == torch.bfloat16 and st.b_prev.dtype == torch.bfloat16 and \
+                st.x_prev.is_contiguous() and st.b_prev.is_contiguous()
+        else:
+            ok = ok and st.last_u.shape == (B, H, P, N) and st.last_u.is_contiguous()
+        if not ok:
+            return None
+        if getattr(self, "_fused_step_ok", None) is None:
+            # an empty call reports whether the library covers these shapes
+            probe = _lib.lib().m3_mixer_step(C.byref(self._dims(0)), None, None, None, None, None,
+                                             None, None, C.byref(_lib.SsmStateC()), None, None, None)
+            if probe not in (_lib.M3_OK, _lib.M3_ERR_UNSUPPORTED):
+                _lib.check(probe)
+            self._fused_step_ok = probe == _lib.M3_OK
+        if not self._fused_step_ok:
+            return None
+        dims = self._dims(B)
+        input = _bf16_dev(input, "mixer input")
+        projected = self.in_proj.apply(input)
+        gated = torch.empty((B, 1, c.d_inner()), dtype=torch.bfloat16, device=input.device)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        ang = ptr(st.angle) if rot else None
+        if factored:
+            sc, fc = None, C.byref(_lib.SsmStateFactoredC(st.h.data_ptr(), st.x_prev.data_ptr(),
+                                                          st.b_prev.data_ptr(), ang))
+        else:
+            sc, fc = C.byref(_lib.SsmStateC(st.h.data_ptr(), st.last_u.data_ptr(), ang)), None
+        _lib.check(_lib.lib().m3_mixer_step(
+            C.byref(dims), projected.data_ptr(), self.dt_bias.data_ptr(), ptr(self.b_bias),
+            ptr(self.c_bias), None if self.bc_norm is None else self.bc_norm.weight.data_ptr(),
+            self.a_log.data_ptr(), ptr(self.d_skip), sc, fc, gated.data_ptr(), _stream(input)))
+        return self.out_proj.apply(gated, residual=residual, out=out)
 
     def step(self, input: torch.Tensor, cache: MixerCache):
         """mamba3.rs:569-630: returns (output, new cache) like the reference."""

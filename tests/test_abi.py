@@ -253,3 +253,36 @@ def test_no_alloc_scan_rejects_beyond_its_scratch():
     msg = L.m3_last_error().decode()
     assert "static scratch holds 33554432 (32 MiB)" in msg and str(need) in msg
     assert L.m3_scan_no_alloc(None, C.byref(cout), None) == _lib.M3_ERR_ARGUMENT
+
+
+def test_mixer_step_shape_cover_and_argument_checks():
+    """m3_mixer_step's host-side checks (an empty call launches nothing): the
+    shapes it covers, the ones it leaves to the composed calls, and its
+    argument errors."""
+    import ctypes as C
+    from mamba3 import _lib
+    L = _lib.lib()
+
+    def call(H=4, P=64, N=128, R=1, G=4, state=True, factored=False, rot=True):
+        d = _lib.MixerDimsC(0, H, P, N, R, G, 2, 1 if rot else 0, 1e-5)   # learned lambda
+        st = C.byref(_lib.SsmStateC()) if state else None
+        fc = C.byref(_lib.SsmStateFactoredC()) if factored else None
+        return int(L.m3_mixer_step(C.byref(d), None, None, None, None, None, None, None, st, fc,
+                                   None, None))
+
+    assert call() == _lib.M3_OK
+    assert call(R=2, N=64, P=32) == _lib.M3_OK
+    assert call(state=False, factored=True) == _lib.M3_OK
+    assert call(N=256) == _lib.M3_ERR_UNSUPPORTED      # d_state above 128
+    assert call(N=96) == _lib.M3_ERR_UNSUPPORTED       # d_state / 8 not a power of two
+    assert call(R=3) == _lib.M3_ERR_UNSUPPORTED
+    assert call(P=4) == _lib.M3_ERR_UNSUPPORTED        # head_dim * rank not a multiple of 8
+    assert call(state=True, factored=True) == _lib.M3_ERR_ARGUMENT
+    assert call(state=False, factored=False) == _lib.M3_ERR_ARGUMENT
+    assert call(H=4, G=3) == _lib.M3_ERR_CONFIG
+    assert call(N=9) == _lib.M3_ERR_CONFIG               # odd d_state, rotational
+    # the 16-byte prologue's rows: an in_proj width of 1796 (fixed lambda, H=4)
+    d = _lib.MixerDimsC(0, 4, 64, 128, 1, 4, 1, 1, 1e-5)
+    assert int(L.m3_mixer_in_proj_width(C.byref(d))) % 8 == 4
+    assert int(L.m3_mixer_step(C.byref(d), None, None, None, None, None, None, None,
+                               C.byref(_lib.SsmStateC()), None, None, None)) == _lib.M3_ERR_UNSUPPORTED

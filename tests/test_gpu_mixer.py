@@ -564,3 +564,58 @@ def test_default_config_mixer_prefill_and_step_against_oracle():
     # of the device GEMM, so compared at the bf16 bar rather than bit for bit)
     assert rel_l2(host(cache.conv), st[3]) <= 1e-2
     assert rel_l2(host(cache.ssm.h), st[0]) <= 1e-2
+
+
+FUSED_STEP_CASES = [
+    # H, G, P, N, R, rotational, learned lambda, plain (no bias, norm, skip),
+    # factored; in_proj widths multiples of 8 (the 16-byte prologue's rows)
+    (4, 2, 16, 16, 1, True, True, False, False),
+    (8, 4, 8, 32, 2, True, False, False, True),
+    (4, 1, 8, 8, 1, False, True, True, False),
+    (4, 4, 64, 128, 1, True, True, False, True),
+    (4, 1, 16, 64, 4, True, True, False, False),
+    (8, 2, 8, 16, 8, False, False, True, True),
+]
+
+
+@pytest.mark.parametrize("H,G,P,N,R,rot,learned,plain,factored", FUSED_STEP_CASES)
+def test_fused_mixer_step_equals_the_composed_calls(H, G, P, N, R, rot, learned, plain, factored):
+    """m3_mixer_step (prologue, state step and gate in one launch) against
+    m3_mixer_prologue + m3_step (or m3_step_factored) + m3_mixer_gate on the
+    same layer and cache: outputs and every cache tensor equal bit for bit,
+    over three steps in a row."""
+    rng = np.random.default_rng(700 + H + N + 3 * R + 11 * factored)
+    model = mo.random_model(rng, vocab=16, d_model=32, n_layers=1, heads=H, head_dim=P,
+                            d_state=N, rank=R, groups=G, rotational=rot, learned_lambda=learned,
+                            fixed_lambda=0.5, int8=True, bias_scale=0.3)
+    lm = gpu_lm_from_oracle(model, True, learned, rot)
+    _, mixer = lm.layers[0]
+    if plain:
+        mixer.b_bias = mixer.c_bias = mixer.d_skip = None
+        mixer.bc_norm = None
+    B = 5
+    g = torch.Generator(device=DEV).manual_seed(int(rng.integers(1 << 30)))
+    cache = mixer.empty_cache(B, DEV, factored=factored)
+    st = cache.ssm
+    st.h.normal_(0.0, 0.1, generator=g)
+    if factored:
+        st.x_prev.copy_(torch.randn(st.x_prev.shape, device=DEV, generator=g).to(torch.bfloat16))
+        st.b_prev.copy_(torch.randn(st.b_prev.shape, device=DEV, generator=g).to(torch.bfloat16))
+    else:
+        st.last_u.normal_(0.0, 0.1, generator=g)
+    if st.angle is not None:
+        st.angle.uniform_(-3.0, 3.0, generator=g)
+    fused, composed = cache.clone(), cache.clone()
+    for step in range(3):
+        x = (torch.randn(B, 1, 32, device=DEV, generator=g) * 0.5).to(torch.bfloat16)
+        mixer._fused_step_ok = None
+        ya = mixer.step_(x, fused)
+        assert mixer._fused_step_ok, "the shapes should take the fused step"
+        mixer._fused_step_ok = False
+        yb = mixer.step_(x, composed)
+        torch.cuda.synchronize()
+        assert torch.equal(ya, yb), (step, (ya.float() - yb.float()).abs().max().item())
+        for name in ("h", "last_u", "x_prev", "b_prev", "angle"):
+            a, b = getattr(fused.ssm, name, None), getattr(composed.ssm, name, None)
+            if a is not None:
+                assert torch.equal(a, b), (step, name)
