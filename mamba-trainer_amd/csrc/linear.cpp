@@ -9,6 +9,10 @@
 // X (K x M), so the output channels are D's rows and the scale vector is
 // hipBLASLt's per-row alpha vector.
 //
+// Up to 512 rows and 4096 columns (K a multiple of 128, N of 8, 16-byte
+// aligned buffers) the product runs on the weight-streaming kernel of
+// skinny_gemm.hip instead, with the same epilogue.
+//
 // Plan choice follows the reference's tuned plans (tensor/matmul.rs:1636-1943:
 // timing probes once per shape): the first call for a shape asks hipBLASLt's
 // heuristic for up to kCandidates algorithms, runs each a few times on the
@@ -145,6 +149,9 @@ hipError_t launch_linear(size_t m, size_t k, size_t n, const void *x, const void
                          const float *col_scale, const void *residual, void *y, void *workspace,
                          size_t workspace_bytes, hipStream_t s) {
     if (m == 0 || n == 0) return hipSuccess;
+    // few rows (a decode step's tokens): the weight-streaming kernel
+    if (skinny_gemm_supported(m, k, n, x, w, col_scale, residual, y))
+        return launch_skinny_gemm(m, k, n, x, w, col_scale, residual, y, s);
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;

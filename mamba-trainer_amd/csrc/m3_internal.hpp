@@ -174,6 +174,12 @@ hipError_t launch_mixer_gate(size_t tokens, size_t d_inner, const void *y, const
 hipError_t launch_embedding(size_t n, size_t dim, const int32_t *ids, size_t vocab, const void *table,
                             void *out, hipStream_t s);
 // y = (x @ w) * col_scale + residual through hipBLASLt (bf16, f32 accumulate).
+// The few-row product (skinny_gemm.hip): up to 512 rows, K a multiple of
+// 128, N a multiple of 8 below 4096, 16-byte aligned buffers.
+bool skinny_gemm_supported(size_t m, size_t k, size_t n, const void *x, const void *w,
+                           const float *scale, const void *res, const void *y);
+hipError_t launch_skinny_gemm(size_t m, size_t k, size_t n, const void *x, const void *w,
+                              const float *scale, const void *res, void *y, hipStream_t s);
 hipError_t launch_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
                          const float *col_scale, const void *residual, void *y, void *workspace,
                          size_t workspace_bytes, hipStream_t s);
