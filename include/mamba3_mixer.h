@@ -9,7 +9,7 @@
  *                               (fused rms_norm_kernel    src/tensor/ops/fused.rs:140-185)
  *   m3_quantize_int8_columns    Quantizer::quantize, QuantConfig::int8_weights
  *                                                         src/nn/quant.rs:95-103, 231-245, 282-330
- *   m3_linear                   Linear::apply (+ the stack's residual add)
+ *   m3_linear, m3_linear_nt     Linear::apply (+ the stack's residual add)
  *                                                         src/nn/linear.rs:155-185,
  *                                                         src/models/hybrid.rs:446-456
  *   m3_mixer_prologue           Mamba3Mixer::project after in_proj
@@ -71,6 +71,17 @@ size_t m3_linear_workspace_bytes(void);
 m3_status m3_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
                     const float *col_scale, const void *residual, void *y, void *workspace,
                     size_t workspace_bytes, void *stream);
+
+/* m3_linear with the weight given transposed, w_t [n, k] (row-major): the
+ * same product, y[m, n] = (x[m, k] @ w_t[n, k]^T) * col_scale[n] +
+ * residual[m, n].  hipBLASLt's kernels for this layout are the faster ones
+ * at large m; a caller that holds the weight only for the product (the
+ * int8 codes) keeps it this way.  Up to 512 rows and 4096 columns (k a
+ * multiple of 128, n of 8, 16-byte aligned buffers) both forms run on the
+ * library's own few-row kernel instead of hipBLASLt. */
+m3_status m3_linear_nt(size_t m, size_t k, size_t n, const void *x, const void *w_t,
+                       const float *col_scale, const void *residual, void *y, void *workspace,
+                       size_t workspace_bytes, void *stream);
 
 /* Shapes of one mixer (SsmConfig fields, config.rs:84-128). */
 typedef struct m3_mixer_dims {

@@ -179,10 +179,11 @@ hipError_t launch_embedding(size_t n, size_t dim, const int32_t *ids, size_t voc
 bool skinny_gemm_supported(size_t m, size_t k, size_t n, const void *x, const void *w,
                            const float *scale, const void *res, const void *y);
 hipError_t launch_skinny_gemm(size_t m, size_t k, size_t n, const void *x, const void *w,
-                              const float *scale, const void *res, void *y, hipStream_t s);
+                              bool w_transposed, const float *scale, const void *res, void *y,
+                              hipStream_t s);
 hipError_t launch_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
-                         const float *col_scale, const void *residual, void *y, void *workspace,
-                         size_t workspace_bytes, hipStream_t s);
+                         bool w_transposed, const float *col_scale, const void *residual, void *y,
+                         void *workspace, size_t workspace_bytes, hipStream_t s);
 constexpr size_t kLinearWorkspace = size_t(32) << 20;
 
 }  // namespace m3

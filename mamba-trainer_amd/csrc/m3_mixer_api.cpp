@@ -60,9 +60,10 @@ m3_status m3_quantize_int8_columns(size_t in_features, size_t out_features, cons
 
 size_t m3_linear_workspace_bytes(void) { return m3::kLinearWorkspace; }
 
-m3_status m3_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
-                    const float *col_scale, const void *residual, void *y, void *workspace,
-                    size_t workspace_bytes, void *stream) {
+namespace {
+m3_status linear_call(size_t m, size_t k, size_t n, const void *x, const void *w, bool wt,
+                      const float *col_scale, const void *residual, void *y, void *workspace,
+                      size_t workspace_bytes, void *stream) {
     if (k == 0) return m3::api_fail(M3_ERR_SHAPE, "Linear with zero input features");
     if (m > 0 && n > 0 && (x == nullptr || w == nullptr || y == nullptr))
         return m3::api_fail(M3_ERR_ARGUMENT, "linear buffers are NULL");
@@ -71,12 +72,27 @@ m3_status m3_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
     const size_t ws = workspace ? (workspace_bytes < m3::kLinearWorkspace ? workspace_bytes
                                                                            : m3::kLinearWorkspace)
                                 : 0;
-    const hipError_t e = m3::launch_linear(m, k, n, x, w, col_scale, residual, y, workspace, ws,
-                                           as_stream(stream));
+    const hipError_t e = m3::launch_linear(m, k, n, x, w, wt, col_scale, residual, y, workspace,
+                                           ws, as_stream(stream));
     if (e == hipErrorNotSupported)
         return m3::api_fail(M3_ERR_UNSUPPORTED, "no hipBLASLt kernel for a [%zu x %zu] @ [%zu x %zu] "
                             "bf16 product", m, k, k, n);
     return launched(e, "linear launch");
+}
+}  // namespace
+
+m3_status m3_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
+                    const float *col_scale, const void *residual, void *y, void *workspace,
+                    size_t workspace_bytes, void *stream) {
+    return linear_call(m, k, n, x, w, false, col_scale, residual, y, workspace, workspace_bytes,
+                       stream);
+}
+
+m3_status m3_linear_nt(size_t m, size_t k, size_t n, const void *x, const void *w_t,
+                       const float *col_scale, const void *residual, void *y, void *workspace,
+                       size_t workspace_bytes, void *stream) {
+    return linear_call(m, k, n, x, w_t, true, col_scale, residual, y, workspace, workspace_bytes,
+                       stream);
 }
 
 size_t m3_mixer_in_proj_width(const m3_mixer_dims *d) {

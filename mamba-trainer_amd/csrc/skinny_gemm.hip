@@ -2,9 +2,9 @@
 // sequence, a few hundred rows) on gfx950:
 //   y[m, n] = (x[m, :] . w[:, n]) * scale[n] + res[m, n]
 // bf16 x [M, K] and w [K, N] (row-major, as nn/linear.rs:155-185 stores the
-// weight; the int8 projections hold their codes, whole numbers exact in
-// bf16), f32 accumulation, the per-column scale and the residual in the
-// epilogue, bf16 y.
+// weight) or its transpose w^T [N, K] (WT; the int8 projections hold their
+// codes, whole numbers exact in bf16), f32 accumulation, the per-column scale
+// and the residual in the epilogue, bf16 y.
 //
 // With M this small the product is a stream over the weights: every weight
 // is read once, and x (M x K, under 1 MB) is re-read from L2 by each column
@@ -13,7 +13,8 @@
 // (16 bytes a lane, whole rows, the permuted-chunk tiles of scan_common.hpp)
 // NS steps ahead, and y^T = W^T X^T is formed by bf16 MFMA 16x16x32 with the
 // W^T operand read transposed (ds_read_b64_tr_b16) from the row-major w tile
-// and the X^T operand read straight from x's rows.  The y^T accumulator
+// and the X^T operand read straight from x's rows (with WT both operands are
+// row reads: w^T's tile is [n][k] like x's).  The y^T accumulator
 // layout gives each lane four consecutive columns of one row: 8-byte stores.
 #include "m3_internal.hpp"
 #include "scan_common.hpp"
@@ -34,12 +35,13 @@ constexpr int kStages = 3;     // stages in flight
 // with the column blocks, so wide products stay on hipBLASLt.
 constexpr int kBM = 64, kBN = 32;
 
-template <int BM, int BN>
+template <int BM, int BN, bool WT>
 struct GemmSmem {
     static constexpr int CX = kKStep * 2 / 16;   // 16-byte chunks per x row
-    static constexpr int CW = BN * 2 / 16;       // ... per w row
+    static constexpr int CW = WT ? CX : BN * 2 / 16;   // ... per w row
+    static constexpr int RW = WT ? BN : kKStep;        // w tile rows
     unsigned char x[kStages][BM * CX * 16];      // [m][k]
-    unsigned char w[kStages][kKStep * CW * 16];  // [k][n]
+    unsigned char w[kStages][RW * CW * 16];      // [k][n], or [n][k] (WT)
 };
 
 template <int V>
@@ -47,16 +49,16 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt(vmcnt_imm<V>());
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool WT>
 __global__ void __launch_bounds__(kThreads, 2)
 skinny_gemm_kernel(uint32_t M, uint32_t K, uint32_t N, const void *x, const void *w,
                    const float *scale, const void *res, void *y) {
-    using S = GemmSmem<BM, BN>;
+    using S = GemmSmem<BM, BN, WT>;
     constexpr int CX = S::CX, CW = S::CW;
     constexpr int NTW = BN / 32, MTW = BM / 32;          // 16-wide tiles per wave (2 x 2 waves)
-    constexpr int LX = BM * CX / 64 / 4, LW = kKStep * CW / 64 / 4;   // loads per wave per stage
+    constexpr int LX = BM * CX / 64 / 4, LW = S::RW * CW / 64 / 4;   // loads per wave per stage
     constexpr int LPS = LX + LW;
-    static_assert(LX >= 1 && LW >= 1 && BM * CX % 256 == 0 && kKStep * CW % 256 == 0,
+    static_assert(LX >= 1 && LW >= 1 && BM * CX % 256 == 0 && S::RW * CW % 256 == 0,
                   "tiles in whole kilobytes per wave");
 
     __shared__ __attribute__((aligned(16))) S sm;
@@ -69,8 +71,10 @@ skinny_gemm_kernel(uint32_t M, uint32_t K, uint32_t N, const void *x, const void
     const uint32_t n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
 
     const rsrc_t rx = make_rsrc(x, M * K * 2u);
-    const rsrc_t rw = make_rsrc(static_cast<const char *>(w) + static_cast<size_t>(n0) * 2,
-                                (K * N - n0) * 2u);
+    // w's columns from n0 on (rows past the end read as zeros); w^T whole
+    const rsrc_t rw = WT ? make_rsrc(w, N * K * 2u)
+                         : make_rsrc(static_cast<const char *>(w) + static_cast<size_t>(n0) * 2,
+                                     (K * N - n0) * 2u);
     const int steps = static_cast<int>(K / kKStep);
     auto load = [&](int s) {
         const int b = s % kStages;
@@ -79,8 +83,12 @@ skinny_gemm_kernel(uint32_t M, uint32_t K, uint32_t N, const void *x, const void
         for (int q = 0; q < LX; ++q)
             lds_load_rows<CX>(rx, (m0 * K + k0) * 2u, K * 2u, sm.x[b], wave + 4 * q, lane);
 #pragma unroll
-        for (int q = 0; q < LW; ++q)
-            lds_load_rows<CW>(rw, k0 * N * 2u, N * 2u, sm.w[b], wave + 4 * q, lane);
+        for (int q = 0; q < LW; ++q) {
+            if constexpr (WT)
+                lds_load_rows<CW>(rw, (n0 * K + k0) * 2u, K * 2u, sm.w[b], wave + 4 * q, lane);
+            else
+                lds_load_rows<CW>(rw, k0 * N * 2u, N * 2u, sm.w[b], wave + 4 * q, lane);
+        }
     };
 
     f32x4 acc[NTW][MTW];
@@ -111,14 +119,19 @@ skinny_gemm_kernel(uint32_t M, uint32_t K, uint32_t N, const void *x, const void
         const int r0 = 8 * g + (c >> 2);
 #pragma unroll
         for (int kb = 0; kb < kKStep / 32; ++kb) {
-            // W^T[n][k]: column n of the w tile, k = 32 kb + 8 g + 0..7
+            // W^T[n][k], k = 32 kb + 8 g + 0..7: row n of w^T's tile, or
+            // column n of w's (transposed reads)
             bf16x8 af[NTW];
 #pragma unroll
             for (int i = 0; i < NTW; ++i) {
-                const int col = 16 * (NTW * wn + i) + 4 * (c & 3);
-                const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(wt + rtile_off<CW>(32 * kb + r0, col)));
-                const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(wt + rtile_off<CW>(32 * kb + r0 + 4, col)));
-                af[i] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                if constexpr (WT) {
+                    af[i] = *reinterpret_cast<const bf16x8 *>(wt + rtile_off<CW>(16 * (NTW * wn + i) + c, 32 * kb + 8 * g));
+                } else {
+                    const int col = 16 * (NTW * wn + i) + 4 * (c & 3);
+                    const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(wt + rtile_off<CW>(32 * kb + r0, col)));
+                    const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(wt + rtile_off<CW>(32 * kb + r0 + 4, col)));
+                    af[i] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
             }
             // X^T[k][m]: row m of the x tile, the same k
             bf16x8 bfr[MTW];
@@ -177,12 +190,17 @@ bool skinny_gemm_supported(size_t m, size_t k, size_t n, const void *x, const vo
 }
 
 hipError_t launch_skinny_gemm(size_t m, size_t k, size_t n, const void *x, const void *w,
-                              const float *scale, const void *res, void *y, hipStream_t s) {
+                              bool w_transposed, const float *scale, const void *res, void *y,
+                              hipStream_t s) {
     const uint32_t M = static_cast<uint32_t>(m), K = static_cast<uint32_t>(k),
                    N = static_cast<uint32_t>(n);
     const dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM);
-    hipLaunchKernelGGL((skinny_gemm_kernel<kBM, kBN>), grid, dim3(kThreads), 0, s, M, K, N, x, w,
-                       scale, res, y);
+    if (w_transposed)
+        hipLaunchKernelGGL((skinny_gemm_kernel<kBM, kBN, true>), grid, dim3(kThreads), 0, s, M, K, N,
+                           x, w, scale, res, y);
+    else
+        hipLaunchKernelGGL((skinny_gemm_kernel<kBM, kBN, false>), grid, dim3(kThreads), 0, s, M, K, N,
+                           x, w, scale, res, y);
     return hipGetLastError();
 }
 

@@ -128,6 +128,7 @@ SIGNATURES = {
     "m3_quantize_int8_columns": (C.c_int, [_Z, _Z, _P, _P, _P, _P]),
     "m3_linear_workspace_bytes": (_Z, []),
     "m3_linear": (C.c_int, [_Z, _Z, _Z, _P, _P, _P, _P, _P, _P, _Z, _P]),
+    "m3_linear_nt": (C.c_int, [_Z, _Z, _Z, _P, _P, _P, _P, _P, _P, _Z, _P]),
     "m3_mixer_in_proj_width": (_Z, [C.POINTER(MixerDimsC)]),
     "m3_mixer_prologue": (C.c_int, [C.POINTER(MixerDimsC)] + [_P] * 12),
     "m3_mixer_prologue_conv": (C.c_int, [C.POINTER(MixerDimsC), C.POINTER(Conv1dC)] + [_P] * 12),

@@ -90,7 +90,8 @@ class Linear:
     used is the fake-quantized w' = code * scale (per output channel); the
     codes go to the GEMM as exact bf16 and the scales are applied in its
     epilogue, so w' is never rounded to bf16.  Without it the weight is used
-    as bf16.
+    as bf16.  The GEMM operand is held transposed, codes_t [out, in]
+    (m3_linear_nt); `codes` is its [in, out] view.
     """
 
     def __init__(self, weight: torch.Tensor, int8_weights: bool = False,
@@ -103,6 +104,7 @@ class Linear:
         self.weight = weight.float().contiguous()          # master copy, f32
         self.int8_weights = int8_weights
         self.codes: Optional[torch.Tensor] = None
+        self.codes_t: Optional[torch.Tensor] = None
         self.scales: Optional[torch.Tensor] = None
         self.prepare()
 
@@ -118,14 +120,16 @@ class Linear:
         """Derive the GEMM operands from the master weight (after any update)."""
         k, n = self.weight.shape
         if self.int8_weights:
-            self.codes = torch.empty((k, n), dtype=torch.bfloat16, device=self.weight.device)
+            codes = torch.empty((k, n), dtype=torch.bfloat16, device=self.weight.device)
             self.scales = torch.empty(n, dtype=torch.float32, device=self.weight.device)
             _lib.check(_lib.lib().m3_quantize_int8_columns(
-                k, n, self.weight.data_ptr(), self.codes.data_ptr(), self.scales.data_ptr(),
+                k, n, self.weight.data_ptr(), codes.data_ptr(), self.scales.data_ptr(),
                 _stream(self.weight)))
         else:
-            self.codes = self.weight.to(torch.bfloat16)
+            codes = self.weight.to(torch.bfloat16)
             self.scales = None
+        self.codes_t = codes.t().contiguous()
+        self.codes = self.codes_t.t()
 
     def param(self):
         """The master weight [in, out] as a checkpoint Param; setting it
@@ -156,8 +160,8 @@ class Linear:
         if residual is not None:
             residual = _bf16_dev(residual, "Linear residual")
         ws = linear_workspace(x.device)
-        _lib.check(_lib.lib().m3_linear(
-            m, self.in_features, self.out_features, x.data_ptr(), self.codes.data_ptr(),
+        _lib.check(_lib.lib().m3_linear_nt(
+            m, self.in_features, self.out_features, x.data_ptr(), self.codes_t.data_ptr(),
             None if self.scales is None else self.scales.data_ptr(),
             None if residual is None else residual.data_ptr(), y.data_ptr(), ws.data_ptr(),
             ws.numel(), _stream(x)))

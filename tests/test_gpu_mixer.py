@@ -96,14 +96,30 @@ def test_linear_against_f64(m, k, n, int8, resid):
     else:
         w_eff = mo.bf16(w)
     r = mo.bf16(rng.normal(0, 1, (m, n))) if resid else None
-    out = t_bf16(r) if resid else None
-    y = lin.apply(t_bf16(x), residual=out, out=out)
     ref = x @ w_eff + (r if resid else 0.0)
-    got = host(y)
-    assert rel_l2(got, ref) <= 1e-2
-    # f32 accumulation: each output within a few bf16 roundings of the f64 value
-    assert np.all(np.abs(got - ref) <= 2.0 ** -7 * np.abs(ref) + 1e-3 * np.abs(ref).max()), \
-        np.abs(got - ref).max()
+    # Linear.apply: the weight held transposed (m3_linear_nt); then m3_linear
+    # on the [in, out] weight, the residual added in place both times
+    from mamba3 import _lib
+    from mamba3.nn import _stream, linear_workspace
+    xd = t_bf16(x)
+    ws = linear_workspace(xd.device)
+    codes_kn = lin.codes.contiguous()
+    for form in ("nt", "nn"):
+        out = t_bf16(r) if resid else None
+        if form == "nt":
+            y = lin.apply(xd, residual=out, out=out)
+        else:
+            y = out if resid else torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+            _lib.check(_lib.lib().m3_linear(
+                m, k, n, xd.data_ptr(), codes_kn.data_ptr(),
+                None if lin.scales is None else lin.scales.data_ptr(),
+                None if out is None else out.data_ptr(), y.data_ptr(), ws.data_ptr(), ws.numel(),
+                _stream(xd)))
+        got = host(y)
+        assert rel_l2(got, ref) <= 1e-2, form
+        # f32 accumulation: each output within a few bf16 roundings of the f64 value
+        assert np.all(np.abs(got - ref) <= 2.0 ** -7 * np.abs(ref) + 1e-3 * np.abs(ref).max()), \
+            (form, np.abs(got - ref).max())
 
 
 # The first, second, fourth and fifth shapes take the 16-byte path (ranks 1, 4
