@@ -23,10 +23,10 @@
 //              under the frame rotation, so the global angle gradient is its
 //              reverse cumsum over the whole sequence.
 //
-// Launches: bwd_uv_kernel (per chunk U_k, the forward's chunk state, and
-// V_k, the chunk's direct share of G, with f32 operands), bwd_passes_kernel
-// (the forward recurrence giving S_k and the reverse one giving G and Gh per
-// chunk with dh0 / dlast_u0, side by side), bwd_chunk_kernel (dx, db, dc and
+// Launches: bwd_passes_kernel (the forward recurrence giving S_k, each
+// chunk's U_k, the forward's chunk state, formed in place with f32 operands;
+// and the reverse one giving G and Gh per chunk, with each chunk's V_k, its
+// direct share of G, and dh0 / dlast_u0; side by side), bwd_chunk_kernel (dx, db, dc and
 // the per-token da, dg, dw and angle sums), bwd_angle_kernel (the angle sums
 // of later chunks), bwd_token_kernel (dtheta, ddt, dlambda: trapezoid_weights
 // backward, the decay and angle chains) and bwd_head_kernel (da_log, dD).
@@ -57,13 +57,12 @@ struct BwdArgs {
 };
 
 // Backward workspace, 256-byte aligned sections.  Per (batch, head, chunk):
-// U_k, S_k, V_k and Gh_k as f32 [p-tile][n-tile][lane][4] MFMA D-layout
-// records of the [P][N] state, the chunk decay e_k, and per rotation pair the
-// chunk's angle total Phi_k with its cosine and sine.
+// S_k and Gh_k as f32 [p-tile][n-tile][lane][4] MFMA D-layout records of the
+// [P][N] state and the chunk decay e_k.
 // With an upstream gradient of the outgoing last_u: the angle seed (that
 // gradient's angle term plus dL/dangle) and the last token's dx and db terms.
 struct BwdLayout {
-    size_t u, s, v, gh, eda, phi, cph, sph, cin, ctot, off, da, dg, dw, pd, pa, pfirst;
+    size_t s, gh, eda, cin, ctot, off, da, dg, dw, pd, pa, pfirst;
     size_t seed, lux, lub, total;
 };
 
@@ -73,14 +72,9 @@ BwdLayout bwd_layout(size_t bh, size_t nck, size_t seq, size_t n, size_t r) {
     const size_t bhk = bh * nck, rec = bhk * kP * n * 4, pairs = bhk * (n / 2) * 4;
     BwdLayout l;
     size_t o = 0;
-    l.u = o;      o = balign(o + rec);
     l.s = o;      o = balign(o + rec);
-    l.v = o;      o = balign(o + rec);
     l.gh = o;     o = balign(o + rec);
     l.eda = o;    o = balign(o + bhk * 4);
-    l.phi = o;    o = balign(o + pairs);
-    l.cph = o;    o = balign(o + pairs);
-    l.sph = o;    o = balign(o + pairs);
     l.cin = o;    o = balign(o + bh * seq * (n / 2) * 4);
     l.ctot = o;   o = balign(o + pairs);
     l.off = o;    o = balign(o + pairs);
@@ -98,7 +92,7 @@ BwdLayout bwd_layout(size_t bh, size_t nck, size_t seq, size_t n, size_t r) {
 }
 
 struct BwdWs {
-    float *u, *s, *v, *gh, *eda, *phi, *cph, *sph;
+    float *s, *gh, *eda;
     float *cin, *ctot, *off, *da, *dg, *dw, *pd, *pa, *pfirst;
     float *seed, *lux, *lub;
 };
@@ -254,23 +248,6 @@ struct Smem {
     float dgv[QT], dal[QT];
     float red[32];
     float gs, pdsum;
-};
-
-// What bwd_uv_kernel stages: B~, C~, X, dY transposed ([n][rho], [p][rho],
-// rows of LDR = rows + 4 words: an MFMA lane reads four consecutive rho in one
-// 16-byte access), the angles and the per-token scalars.
-template <int N, int R, int kRows>
-struct UVSmem {
-    static constexpr int QT = kRows / R, NH = N / 2, NTN = N / 16;
-    static constexpr int LDR = kRows + 4;
-    float Bs[N * LDR], Cs[N * LDR];
-    float Xs[kP * LDR], Ys[kP * LDR];
-    static constexpr int AP = NH + 3;
-    float acs[QT * AP], asn[QT * AP];
-    float phi_end[NH];
-    float dtv[QT], lamv[QT], acum[QT], gw[QT], ww[QT], eac[QT], ebar[QT], wbar[QT];
-    __device__ static int bi(int rho, int n) { return n * LDR + rho; }
-    __device__ static int xi(int rho, int p) { return p * LDR + rho; }
 };
 
 // Per-token scalars, the in-chunk angles, and (X, dY) / (B~, C~) as asked.
@@ -433,169 +410,64 @@ __device__ void stage(const ScanLaunch &a, const BwdArgs &g, S &sm, size_t bh, i
     }
 }
 
-// ---------------------------------------------------------------- U_k, V_k
-// Per chunk, in its own frame:
-//   U_k^T[n][p] = sum_rho wbar B~[rho][n] X[rho][p], the chunk's contribution to
-//     the state (the forward's chunk state, scan.rs:207-251), with f32 operands;
-//   V_k^T[n][p] = sum_rho C~[rho][n] e^{alpha} dY[rho][p], the chunk's direct
-//     share of dL/dS_k (the carry-in product y += e^alpha C~ S, scan.rs:253-263);
-// and the chunk decay e_k and per pair the angle total Phi_k, cos Phi_k, sin Phi_k.
-constexpr int kUVThreads = 512;
-template <typename T, int N, int R, int kRows>
-__global__ void __launch_bounds__(kUVThreads) bwd_uv_kernel(ScanLaunch a, BwdArgs g, BwdWs w,
-                                                            int nck) {
-    using S = UVSmem<N, R, kRows>;
-    constexpr int NTN = N / 16, QT = S::QT, NH = S::NH;
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    S &sm = *reinterpret_cast<S *>(smem_raw);
-    const int tid = threadIdx.x;
-    const size_t bhk = blockIdx.x;
-    const int ck = static_cast<int>(bhk % nck);
-    const size_t bh = bhk / nck;
-    stage<T, N, R, kRows, true, true, kUVThreads>(a, g, sm, bh, ck);
-    __syncthreads();
-    // the chunk's scalars; B~ rows scaled by wbar, dY rows by e^{alpha}
-    if (tid == 0) w.eda[bhk] = clamp_exp(sm.acum[QT - 1]);
-    if (tid < NH) {
-        const float tot = a.theta != nullptr ? sm.phi_end[tid] : 0.0f;
-        float ts = 0.0f, tc = 1.0f;
-        if (a.theta != nullptr) sincosf(tot, &ts, &tc);
-        w.phi[bhk * NH + tid] = tot;
-        w.cph[bhk * NH + tid] = tc;
-        w.sph[bhk * NH + tid] = ts;
-    }
-    for (int e = tid; e < kRows * N; e += kUVThreads) {
-        const int n = e / kRows, rho = e % kRows;
-        sm.Bs[S::bi(rho, n)] *= sm.wbar[rho / R];
-    }
-    for (int e = tid; e < kRows * kP; e += kUVThreads) {
-        const int p = e / kRows, rho = e % kRows;
-        sm.Ys[S::xi(rho, p)] *= sm.eac[rho / R];
-    }
-    __syncthreads();
-    const int lane = tid & 63, wave = tid >> 6;
-    const int c = lane & 15, gq = lane >> 4;
-    float *u = w.u + bhk * kP * N, *v = w.v + bhk * kP * N;
-    for (int tile = wave; tile < 8 * NTN; tile += kUVThreads / 64) {
-        const bool isv = tile >= 4 * NTN;
-        const int tt = isv ? tile - 4 * NTN : tile;
-        const int pt = tt / NTN, i = tt % NTN;
-        // A(m = n, k = rho) = B~' or C~ [n][rho]; B(k = rho, col = p) = X or dY' [p][rho]
-        const float *ar = (isv ? sm.Cs : sm.Bs) + (16 * i + c) * S::LDR;
-        const float *br = (isv ? sm.Ys : sm.Xs) + (16 * pt + c) * S::LDR;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < kRows / 16; ++kb) acc = scan::mma_kb(ar + 16 * kb, br + 16 * kb, acc, gq);
-        *reinterpret_cast<f32x4 *>((isv ? v : u) + ((pt * NTN + i) * 64 + lane) * 4) = acc;
-    }
-}
+// ---------------------------------------------------------------- state passes
+// The recompute's sequential parts, each with its chunk term formed in place:
+//   forward: S_0 = R(angle0)(h0 + (1 - lambda_0) dt_0 last_u0) (scan.rs:521-535),
+//     S_{k+1} = R(Phi_k)(e_k S_k + U_k), S_k written for every chunk
+//     (scan.rs:244-251 in chunk frames), with
+//     U_k^T[n][p] = sum_rho wbar B~[rho][n] X[rho][p], the chunk's contribution
+//     to the state (the forward's chunk state, scan.rs:207-251), f32 operands;
+//   reverse: G_C = R(phi_end) dh_out (or 0); for k = C-1 .. 0: Gh_k =
+//     R(-Phi_k) G_{k+1}, G_k = e_k Gh_k + V_k, with V_k^T[n][p] =
+//     sum_rho C~[rho][n] e^{alpha} dY[rho][p], the chunk's direct share of
+//     dL/dS_k (the carry-in product y += e^alpha C~ S, scan.rs:253-263); then
+//     dh0, dlast_u0 and the gradient of (1 - lambda_0) dt_0.
+// One workgroup per (batch, head, 16 rotation pairs) and direction; thread =
+// (p, four pairs): the state's 32 columns of those pairs stay in registers.
+// Per chunk the workgroup stages the token scalars and its pairs' in-chunk
+// angles (the scans of the chunk kernel's stage, so every value is the
+// same), rotates its 32 columns of B (or C) into LDS scaled by wbar (or not),
+// stages X (or e^alpha dY), and forms U^T (or V^T) by f32 MFMA directly in the
+// state's lane layout.  The raw inputs of the next chunks are loaded ahead
+// into registers; no per-chunk record but S_k (Gh_k) leaves the workgroup.
+template <int R, int kRows>
+struct PassSmem {
+    static constexpr int QT = kRows / R, LDR = kRows + 4, AP = 17;
+    float As[32 * LDR];      // rotated columns: [column][rho], lo pairs then hi
+    float Xs[kP * LDR];      // X or e^alpha dY: [p][rho]
+    float acs[QT * AP], asn[QT * AP];   // cos / sin of the in-chunk angle [token][pair]
+    float dtv[QT], acum[QT], ww[QT], scal[QT];
+    float phi[16];           // the sequence's angle total per pair (reverse pass)
+    float red[16];
+};
 
-// ---------------------------------------------------------------- forward state pass
-// The recompute's sequential part: S_0 = R(angle0)(h0 + (1 - lambda_0) dt_0
-// last_u0) (scan.rs:521-535), S_{k+1} = R(Phi_k)(e_k S_k + U_k), S_k written
-// for every chunk (scan.rs:244-251 in chunk frames).  One workgroup per
-// (batch, head, n-tile pair); thread = (p, four state pairs).
-template <int N>
-__device__ void forward_pass(const ScanLaunch &a, const BwdWs &w, int nck, size_t blk) {
-    constexpr int NTN = N / 16, HT = NTN / 2, NH = N / 2;
+template <typename T, int N, int R, int kRows, bool FWD>
+__device__ void state_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs &w, int nck,
+                           size_t blk, PassSmem<R, kRows> &sm) {
+    using S = PassSmem<R, kRows>;
+    constexpr int NTN = N / 16, HT = NTN / 2, NH = N / 2, QT = S::QT, LDR = S::LDR, AP = S::AP;
+    constexpr int NW = 4;                       // waves
+    constexpr int TI = 16 / NW;                 // pairs per wave in the angle scans
+    constexpr bool PACK = QT <= 32;             // two 32-token scans per wave
+    constexpr int PK = PACK ? 2 : 1, TS = TI / PK;
+    constexpr int JB = 16 * kRows / 256;        // (row, pair) items per thread
+    constexpr int JX = kP * kRows / 256;        // (row, p) items per thread
+    constexpr int D = kRows == 32 ? 3 : 2;      // chunks loaded ahead
+    static_assert(TI % PK == 0 && JB >= 1 && JX >= 1, "pass split");
     const int tid = threadIdx.x, lane = tid & 63, pt = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(pt);
     const int c = lane & 15, gq = lane >> 4;
     const int i1 = static_cast<int>(blk % HT);
     const size_t bh = blk / HT;
     const size_t H = a.heads, L = a.seq;
     const size_t bb = bh / H, hh = bh % H;
     const bool rot = a.theta != nullptr;
+    const float A = 0.0f - expf(a.a_log[hh]);
     const int p = 16 * pt + c, nlo = 16 * i1 + 4 * gq;
     const size_t sbase = bh * kP * N + static_cast<size_t>(p) * N;
-    auto rot4 = [](f32x4 &lo, f32x4 &hi, f32x4 cs, f32x4 sn) {
-        const f32x4 l = lo;
-        lo = l * cs - hi * sn;
-        hi = l * sn + hi * cs;
-    };
-    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
-    if (a.h0 != nullptr) {
-        lo = *reinterpret_cast<const f32x4 *>(a.h0 + sbase + nlo);
-        hi = *reinterpret_cast<const f32x4 *>(a.h0 + sbase + nlo + NH);
-        if (a.last_u0 != nullptr) {
-            const size_t i0 = (bb * L) * H + hh;
-            const float first = (1.0f - a.lambda[i0]) * a.dt[i0];
-            lo += *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo) * first;
-            hi += *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo + NH) * first;
-        }
-    }
-    if (rot && a.angle0 != nullptr) {
-        const f32x4 ph = *reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo);
-        f32x4 sn, cs;
-        for (int r = 0; r < 4; ++r) {
-            float sv, cv;
-            sincosf(ph[r], &sv, &cv);
-            sn[r] = sv;
-            cs[r] = cv;
-        }
-        rot4(lo, hi, cs, sn);
-    }
-    struct In {
-        f32x4 ulo, uhi, cs, sn;
-        float e;
-    };
-    auto offs = [&](int k, size_t &o, size_t &oh) {
-        const size_t bhk = bh * nck + k;
-        o = bhk * kP * N + ((pt * NTN + i1) * 64 + lane) * 4;
-        oh = bhk * kP * N + ((pt * NTN + i1 + HT) * 64 + lane) * 4;
-    };
-    auto load = [&](int k, In &d) {
-        const int kk = k < nck ? k : nck - 1;   // past the end: re-read the last chunk, unused
-        const size_t bhk = bh * nck + kk;
-        size_t o, oh;
-        offs(kk, o, oh);
-        d.ulo = *reinterpret_cast<const f32x4 *>(w.u + o);
-        d.uhi = *reinterpret_cast<const f32x4 *>(w.u + oh);
-        d.e = w.eda[bhk];
-        if (rot) {
-            d.cs = *reinterpret_cast<const f32x4 *>(w.cph + bhk * NH + nlo);
-            d.sn = *reinterpret_cast<const f32x4 *>(w.sph + bhk * NH + nlo);
-        }
-    };
-    auto step = [&](int k, const In &d) {
-        size_t o, oh;
-        offs(k, o, oh);
-        *reinterpret_cast<f32x4 *>(w.s + o) = lo;
-        *reinterpret_cast<f32x4 *>(w.s + oh) = hi;
-        lo = lo * d.e + d.ulo;
-        hi = hi * d.e + d.uhi;
-        if (rot) rot4(lo, hi, d.cs, d.sn);   // R(Phi_k)
-    };
-    // eight chunks in flight ahead of the one being applied
-    constexpr int D = 8;
-    In d[D];
-#pragma unroll
-    for (int j = 0; j < D; ++j) load(j, d[j]);
-    for (int k = 0; k < nck; k += D) {
-#pragma unroll
-        for (int j = 0; j < D; ++j) {
-            if (k + j < nck) step(k + j, d[j]);
-            load(k + D + j, d[j]);
-        }
-    }
-}
-
-// ---------------------------------------------------------------- reverse state pass
-// G_C = R(phi_end) dh_out (or 0); for k = C-1 .. 0: Gh_k = R(-Phi_k) G_{k+1},
-// G_k = e_k Gh_k + V_k.  Then S_0 = R(angle0)(h0 + (1 - lambda_0) dt_0 last_u0)
-// gives dh0, dlast_u0 and the gradient of (1 - lambda_0) dt_0 (scan.rs:521-535).
-template <int N>
-__device__ void reverse_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs &w, int nck,
-                             size_t blk) {
-    constexpr int NTN = N / 16, HT = NTN / 2, NH = N / 2;
-    const int tid = threadIdx.x, lane = tid & 63, pt = tid >> 6;
-    const int c = lane & 15, gq = lane >> 4;
-    const int i1 = static_cast<int>(blk % HT);
-    const size_t bh = blk / HT;
-    const size_t H = a.heads, L = a.seq;
-    const size_t bb = bh / H, hh = bh % H;
-    const bool rot = a.theta != nullptr;
-    const int p = 16 * pt + c, nlo = 16 * i1 + 4 * gq;
-    const size_t sbase = bh * kP * N + static_cast<size_t>(p) * N;
+    const int tl = PACK ? (lane & 31) : lane, hl = PACK ? (lane >> 5) : 0;
+    const void *bc = FWD ? a.b : a.c;
+    const void *xy = FWD ? a.x : g.dy;
     auto rot4 = [](f32x4 &lo, f32x4 &hi, f32x4 cs, f32x4 sn) {
         const f32x4 l = lo;
         lo = l * cs - hi * sn;
@@ -609,103 +481,315 @@ __device__ void reverse_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs 
             cs[r] = cc;
         }
     };
-    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
-    if (g.dh_out != nullptr) {
-        lo = *reinterpret_cast<const f32x4 *>(g.dh_out + sbase + nlo);
-        hi = *reinterpret_cast<const f32x4 *>(g.dh_out + sbase + nlo + NH);
-        if (rot) {
-            // phi_end = angle0 + sum_k Phi_k: the final frame, S_C = R(phi_end) h_out
-            f32x4 ph = {0.f, 0.f, 0.f, 0.f};
-            if (a.angle0 != nullptr) ph = *reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo);
-            for (int k = 0; k < nck; ++k)
-                ph += *reinterpret_cast<const f32x4 *>(w.phi + (bh * nck + k) * NH + nlo);
-            f32x4 sn, cs;
-            sincos4(ph, sn, cs);
-            rot4(lo, hi, cs, sn);
-        }
-    }
+
     struct In {
-        f32x4 vlo, vhi, cs, sn;
-        float e;
+        float dt, lam, dtn, lamn;
+        float th[TS];
+        float b1[JB], b2[JB];
+        float xv[JX];
+    };
+    // Chunk k's raw inputs, by buffer loads over this sequence's tokens: a
+    // token at or past the sequence end reads as zero, as the chunk kernel's
+    // stage zeroes it.  A thread's items sit at fixed byte offsets from its
+    // chunk-0 offsets (256 threads cover whole tokens of every array).
+    constexpr uint32_t SZ = sizeof(T);
+    const scan::SeqBufs rs = scan::seq_bufs<T, N, kP, R>(a, bb, hh);
+    const rsrc_t rbc = FWD ? rs.b : rs.c;
+    const rsrc_t rxy = FWD ? rs.x
+                           : make_rsrc(static_cast<const char *>(g.dy) + (bb * L * H + hh) * kP * R * SZ,
+                                       static_cast<uint32_t>((L * H - hh) * kP * R * SZ));
+    auto ld = [](rsrc_t r, uint32_t off) -> float {
+        if constexpr (sizeof(T) == 4)
+            return bldf(r, off);
+        else
+            return __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)) << 16);
+    };
+    const int ts = tid < QT ? tid : 0;
+    const uint32_t o_s = ts * rs.tok_s;
+    const uint32_t o_th = tl * rs.tok_th + (16 * i1) * SZ;
+    const int tb = tid / (16 * R), qr = tid % (16 * R);
+    const uint32_t o_bc = tb * rs.tok_bc + (16 * i1 * R + qr) * SZ;
+    const uint32_t bc_j = (16 / R) * rs.tok_bc;
+    const int tx = tid / (kP * R), pr = tid % (kP * R);
+    const uint32_t o_xy = tx * rs.tok_x + pr * SZ;
+    const uint32_t xy_j = (256 / (kP * R)) * rs.tok_x;
+    auto load = [&](int k, In &d) {
+        const int kk = k < 0 ? 0 : (k < nck ? k : nck - 1);   // outside: re-read, unused
+        const uint32_t t0 = static_cast<uint32_t>(kk) * QT;
+        d.dt = bldf(rs.s0, o_s + t0 * rs.tok_s);
+        d.lam = bldf(rs.s1, o_s + t0 * rs.tok_s);
+        d.dtn = bldf(rs.s0, o_s + (t0 + 1) * rs.tok_s);
+        d.lamn = bldf(rs.s1, o_s + (t0 + 1) * rs.tok_s);
+        if (rot) {
+            const uint32_t o = o_th + t0 * rs.tok_th;
+#pragma unroll
+            for (int j = 0; j < TS; ++j) {
+                const float v = ld(rs.th, o + (wave + (PK * j + hl) * NW) * SZ);
+                d.th[j] = tl < QT ? v : 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < TS; ++j) d.th[j] = 0.0f;
+        }
+        const uint32_t ob = o_bc + t0 * rs.tok_bc;
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+            d.b1[j] = ld(rbc, ob + j * bc_j);
+            d.b2[j] = ld(rbc, ob + j * bc_j + NH * R * SZ);
+        }
+        const uint32_t ox = o_xy + t0 * rs.tok_x;
+#pragma unroll
+        for (int j = 0; j < JX; ++j) d.xv[j] = ld(rxy, ox + j * xy_j);
+    };
+    // Chunk k's term of this lane's state columns (acc), its decay e and the
+    // rotation by its angle totals (pc, ps).
+    auto chunk = [&](int k, const In &d, f32x4 &alo, f32x4 &ahi, f32x4 &pc, f32x4 &ps,
+                     float &e) {
+        const size_t t0 = static_cast<size_t>(k) * QT;
+        // token scalars, the decay prefix (fused.rs:2494-2498)
+        if (tid < QT) {
+            sm.dtv[tid] = d.dt;
+            sm.ww[tid] = d.lam * d.dt + (1.0f - d.lamn) * d.dtn;
+        }
+        if (wave == 0) {
+            const float v = seg_scan<64>(tid < QT ? d.dt * A : 0.0f);
+            if (lane < QT) sm.acum[lane] = v;
+        }
+        __syncthreads();
+        // the in-chunk angle of this workgroup's pairs, its cos / sin, the total
+        if (rot) {
+            const float dtl = (tl < QT && t0 + tl < L) ? sm.dtv[tl] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < TS; ++j) {
+                const int i = wave + (PK * j + hl) * NW;
+                const float v = PACK ? seg_scan<32>(dtl * d.th[j]) : seg_scan<64>(dtl * d.th[j]);
+                if (tl < QT) {
+                    float sv, cv;
+                    sincos_any<true>(v, sv, cv);
+                    sm.acs[tl * AP + i] = cv;
+                    sm.asn[tl * AP + i] = sv;
+                }
+            }
+        }
+        // per token: wbar (B~'s scale) or e^alpha (dY's)
+        if (tid < QT) {
+            const float et = sm.acum[QT - 1];
+            sm.scal[tid] = FWD ? clamp_exp(et - sm.acum[tid]) * sm.ww[tid] : clamp_exp(sm.acum[tid]);
+        }
+        __syncthreads();
+        // rotation by the negative in-chunk angle (fused.rs:610-617) into LDS
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+            const int ee = tid + 256 * j, t = ee / (16 * R), qr = ee % (16 * R);
+            const int q = qr / R, rho = t * R + qr % R;
+            float sn = 0.0f, cs = 1.0f;
+            if (rot) {
+                cs = sm.acs[t * AP + q];
+                sn = sm.asn[t * AP + q];
+            }
+            float lo = d.b1[j] * cs + d.b2[j] * sn;
+            float hi = -d.b1[j] * sn + d.b2[j] * cs;
+            if constexpr (FWD) {
+                lo *= sm.scal[t];
+                hi *= sm.scal[t];
+            }
+            sm.As[q * LDR + rho] = lo;
+            sm.As[(16 + q) * LDR + rho] = hi;
+        }
+#pragma unroll
+        for (int j = 0; j < JX; ++j) {
+            const int ee = tid + 256 * j, t = ee / (kP * R), pr = ee % (kP * R);
+            float v = d.xv[j];
+            if constexpr (!FWD) v *= sm.scal[t];
+            sm.Xs[(pr / R) * LDR + t * R + pr % R] = v;
+        }
+        e = clamp_exp(sm.acum[QT - 1]);
+        __syncthreads();
+        // U^T (V^T) at this lane's (n, p): A(m = n, k = rho), B(k = rho, col = p)
+        alo = f32x4{0.f, 0.f, 0.f, 0.f};
+        ahi = alo;
+        const float *br = sm.Xs + p * LDR;
+#pragma unroll
+        for (int kb = 0; kb < kRows / 16; ++kb) {
+            alo = scan::mma_kb(sm.As + c * LDR + 16 * kb, br + 16 * kb, alo, gq);
+            ahi = scan::mma_kb(sm.As + (16 + c) * LDR + 16 * kb, br + 16 * kb, ahi, gq);
+        }
+        if (rot) {
+            // the chunk's angle total is the in-chunk angle of its last row
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pc[r] = sm.acs[(QT - 1) * AP + 4 * gq + r];
+                ps[r] = sm.asn[(QT - 1) * AP + 4 * gq + r];
+            }
+        }
+        // No barrier here: the next chunk's first LDS writes (dtv, ww, acum)
+        // are of values read only before the staging barrier above, and its
+        // later writes follow its first barrier, which every wave reaches
+        // only after these reads.
     };
     auto offs = [&](int k, size_t &o, size_t &oh) {
         const size_t bhk = bh * nck + k;
         o = bhk * kP * N + ((pt * NTN + i1) * 64 + lane) * 4;
         oh = bhk * kP * N + ((pt * NTN + i1 + HT) * 64 + lane) * 4;
     };
-    auto load = [&](int k, In &d) {
-        const int kk = k >= 0 ? k : 0;   // past the start: re-read chunk 0, unused
-        const size_t bhk = bh * nck + kk;
-        size_t o, oh;
-        offs(kk, o, oh);
-        d.vlo = *reinterpret_cast<const f32x4 *>(w.v + o);
-        d.vhi = *reinterpret_cast<const f32x4 *>(w.v + oh);
-        d.e = w.eda[bhk];
-        if (rot) {
-            d.cs = *reinterpret_cast<const f32x4 *>(w.cph + bhk * NH + nlo);
-            d.sn = *reinterpret_cast<const f32x4 *>(w.sph + bhk * NH + nlo);
-        }
-    };
-    auto step = [&](int k, const In &d) {
-        if (rot) rot4(lo, hi, d.cs, -d.sn);   // R(-Phi_k)
-        size_t o, oh;
-        offs(k, o, oh);
-        *reinterpret_cast<f32x4 *>(w.gh + o) = lo;
-        *reinterpret_cast<f32x4 *>(w.gh + oh) = hi;
-        lo = lo * d.e + d.vlo;
-        hi = hi * d.e + d.vhi;
-    };
-    // eight chunks in flight ahead of the one being applied
-    constexpr int D = 8;
-    In d[D];
-#pragma unroll
-    for (int j = 0; j < D; ++j) load(nck - 1 - j, d[j]);
-    for (int k = nck - 1; k >= 0; k -= D) {
-#pragma unroll
-        for (int j = 0; j < D; ++j) {
-            if (k - j >= 0) step(k - j, d[j]);
-            load(k - D - j, d[j]);
-        }
-    }
-    // into the global frame: dZ0 = R(-angle0) G_0
-    if (rot && a.angle0 != nullptr) {
-        f32x4 sn, cs;
-        sincos4(*reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo), sn, cs);
-        rot4(lo, hi, cs, -sn);
-    }
-    float dfirst = 0.0f;
-    if (a.h0 != nullptr) {
-        if (g.dh0 != nullptr) {
-            *reinterpret_cast<f32x4 *>(g.dh0 + sbase + nlo) = lo;
-            *reinterpret_cast<f32x4 *>(g.dh0 + sbase + nlo + NH) = hi;
-        }
-        if (a.last_u0 != nullptr) {
-            const size_t i0 = (bb * L) * H + hh;
-            const float first = (1.0f - a.lambda[i0]) * a.dt[i0];
-            const f32x4 ul = *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo);
-            const f32x4 uh = *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo + NH);
-            for (int r = 0; r < 4; ++r) dfirst += lo[r] * ul[r] + hi[r] * uh[r];
-            if (g.dlast_u0 != nullptr) {
-                *reinterpret_cast<f32x4 *>(g.dlast_u0 + sbase + nlo) = lo * first;
-                *reinterpret_cast<f32x4 *>(g.dlast_u0 + sbase + nlo + NH) = hi * first;
+
+    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+    if constexpr (FWD) {
+        if (a.h0 != nullptr) {
+            lo = *reinterpret_cast<const f32x4 *>(a.h0 + sbase + nlo);
+            hi = *reinterpret_cast<const f32x4 *>(a.h0 + sbase + nlo + NH);
+            if (a.last_u0 != nullptr) {
+                const size_t i0 = (bb * L) * H + hh;
+                const float first = (1.0f - a.lambda[i0]) * a.dt[i0];
+                lo += *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo) * first;
+                hi += *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo + NH) * first;
             }
         }
+        if (rot && a.angle0 != nullptr) {
+            f32x4 sn, cs;
+            sincos4(*reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo), sn, cs);
+            rot4(lo, hi, cs, sn);
+        }
+        In d[D];
+#pragma unroll
+        for (int j = 0; j < D; ++j) load(j, d[j]);
+        for (int k = 0; k < nck; k += D) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                if (k + j < nck) {
+                    f32x4 ulo, uhi, pc = {1.f, 1.f, 1.f, 1.f}, ps = {0.f, 0.f, 0.f, 0.f};
+                    float e;
+                    chunk(k + j, d[j], ulo, uhi, pc, ps, e);
+                    size_t o, oh;
+                    offs(k + j, o, oh);
+                    *reinterpret_cast<f32x4 *>(w.s + o) = lo;
+                    *reinterpret_cast<f32x4 *>(w.s + oh) = hi;
+                    lo = lo * e + ulo;
+                    hi = hi * e + uhi;
+                    if (rot) rot4(lo, hi, pc, ps);   // R(Phi_k)
+                    if (i1 == 0 && tid == 0) w.eda[bh * nck + k + j] = e;
+                }
+                load(k + D + j, d[j]);
+            }
+        }
+    } else {
+        if (g.dh_out != nullptr) {
+            lo = *reinterpret_cast<const f32x4 *>(g.dh_out + sbase + nlo);
+            hi = *reinterpret_cast<const f32x4 *>(g.dh_out + sbase + nlo + NH);
+            if (rot) {
+                // phi_end = angle0 + sum_k Phi_k: the final frame, S_C = R(phi_end) h_out.
+                // Each Phi_k is the in-chunk scan's last value, summed in chunk order.
+                constexpr int DT = 8;
+                float ph[TS], dq[DT], tq[DT][TS];
+#pragma unroll
+                for (int j = 0; j < TS; ++j) {
+                    const int i = wave + (PK * j + hl) * NW;
+                    ph[j] = a.angle0 != nullptr ? a.angle0[bh * NH + 16 * i1 + i] : 0.0f;
+                }
+                auto tload = [&](int k, float &dv, float (&tv)[TS]) {
+                    const int kk = k < nck ? k : nck - 1;
+                    const size_t tg = static_cast<size_t>(kk) * QT + tl;
+                    const bool tlive = tl < QT && tg < L;
+                    const size_t row = (bb * L + (tlive ? tg : 0)) * H + hh;
+                    const float v = a.dt[row];
+                    dv = tlive ? v : 0.0f;
+#pragma unroll
+                    for (int j = 0; j < TS; ++j) {
+                        const float u = ldv<T>(a.theta, row * NH + 16 * i1 + wave + (PK * j + hl) * NW);
+                        tv[j] = tlive ? u : 0.0f;
+                    }
+                };
+#pragma unroll
+                for (int q = 0; q < DT; ++q) tload(q, dq[q], tq[q]);
+                for (int k = 0; k < nck; k += DT) {
+#pragma unroll
+                    for (int q = 0; q < DT; ++q) {
+                        if (k + q < nck) {
+#pragma unroll
+                            for (int j = 0; j < TS; ++j) {
+                                const float v = PACK ? seg_scan<32>(dq[q] * tq[q][j])
+                                                     : seg_scan<64>(dq[q] * tq[q][j]);
+                                ph[j] += v;
+                            }
+                        }
+                        tload(k + DT + q, dq[q], tq[q]);
+                    }
+                }
+                if (tl == QT - 1) {
+#pragma unroll
+                    for (int j = 0; j < TS; ++j) sm.phi[wave + (PK * j + hl) * NW] = ph[j];
+                }
+                __syncthreads();
+                f32x4 pe;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) pe[r] = sm.phi[4 * gq + r];
+                __syncthreads();
+                f32x4 sn, cs;
+                sincos4(pe, sn, cs);
+                rot4(lo, hi, cs, sn);
+            }
+        }
+        In d[D];
+#pragma unroll
+        for (int j = 0; j < D; ++j) load(nck - 1 - j, d[j]);
+        for (int k = nck - 1; k >= 0; k -= D) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                if (k - j >= 0) {
+                    f32x4 vlo, vhi, pc = {1.f, 1.f, 1.f, 1.f}, ps = {0.f, 0.f, 0.f, 0.f};
+                    float e;
+                    chunk(k - j, d[j], vlo, vhi, pc, ps, e);
+                    if (rot) rot4(lo, hi, pc, -ps);   // R(-Phi_k)
+                    size_t o, oh;
+                    offs(k - j, o, oh);
+                    *reinterpret_cast<f32x4 *>(w.gh + o) = lo;
+                    *reinterpret_cast<f32x4 *>(w.gh + oh) = hi;
+                    lo = lo * e + vlo;
+                    hi = hi * e + vhi;
+                }
+                load(k - D - j, d[j]);
+            }
+        }
+        // into the global frame: dZ0 = R(-angle0) G_0
+        if (rot && a.angle0 != nullptr) {
+            f32x4 sn, cs;
+            sincos4(*reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo), sn, cs);
+            rot4(lo, hi, cs, -sn);
+        }
+        float dfirst = 0.0f;
+        if (a.h0 != nullptr) {
+            if (g.dh0 != nullptr) {
+                *reinterpret_cast<f32x4 *>(g.dh0 + sbase + nlo) = lo;
+                *reinterpret_cast<f32x4 *>(g.dh0 + sbase + nlo + NH) = hi;
+            }
+            if (a.last_u0 != nullptr) {
+                const size_t i0 = (bb * L) * H + hh;
+                const float first = (1.0f - a.lambda[i0]) * a.dt[i0];
+                const f32x4 ul = *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo);
+                const f32x4 uh = *reinterpret_cast<const f32x4 *>(a.last_u0 + sbase + nlo + NH);
+                for (int r = 0; r < 4; ++r) dfirst += lo[r] * ul[r] + hi[r] * uh[r];
+                if (g.dlast_u0 != nullptr) {
+                    *reinterpret_cast<f32x4 *>(g.dlast_u0 + sbase + nlo) = lo * first;
+                    *reinterpret_cast<f32x4 *>(g.dlast_u0 + sbase + nlo + NH) = hi * first;
+                }
+            }
+        }
+        dfirst = block_sum(dfirst, sm.red);
+        if (tid == 0) w.pfirst[blk] = dfirst;
     }
-    __shared__ float red[16];
-    dfirst = block_sum(dfirst, red);
-    if (tid == 0) w.pfirst[blk] = dfirst;
 }
 
 // Both sequential passes in one launch (they are independent): workgroups
 // [0, nb) run the forward recurrence, [nb, 2 nb) the reverse one.
-template <int N>
+template <typename T, int N, int R, int kRows>
 __global__ void __launch_bounds__(256) bwd_passes_kernel(ScanLaunch a, BwdArgs g, BwdWs w,
                                                          int nck) {
+    __shared__ __attribute__((aligned(16))) PassSmem<R, kRows> sm;
     const size_t nb = a.batch * a.heads * (N / 32);
     if (blockIdx.x < nb)
-        forward_pass<N>(a, w, nck, blockIdx.x);
+        state_pass<T, N, R, kRows, true>(a, g, w, nck, blockIdx.x, sm);
     else
-        reverse_pass<N>(a, g, w, nck, blockIdx.x - nb);
+        state_pass<T, N, R, kRows, false>(a, g, w, nck, blockIdx.x - nb, sm);
 }
 
 // ---------------------------------------------------------------- chunk gradients
@@ -1263,14 +1347,9 @@ hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStre
     const BwdLayout l = bwd_layout(bh, nck, a.seq, N, R);
     BwdWs w;
     auto f = [base](size_t off) { return reinterpret_cast<float *>(base + off); };
-    w.u = f(l.u);
     w.s = f(l.s);
-    w.v = f(l.v);
     w.gh = f(l.gh);
     w.eda = f(l.eda);
-    w.phi = f(l.phi);
-    w.cph = f(l.cph);
-    w.sph = f(l.sph);
     w.cin = f(l.cin);
     w.ctot = f(l.ctot);
     w.off = f(l.off);
@@ -1285,10 +1364,8 @@ hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStre
     w.lub = f(l.lub);
 
     static_assert(sizeof(Smem<N, R, RW>) <= 160 * 1024, "chunk kernel LDS over 160 KB");
-    const size_t lds = sizeof(Smem<N, R, RW>), uvlds = sizeof(UVSmem<N, R, RW>);
-    static const hipError_t a1 = set_lds(bwd_uv_kernel<T, N, R, RW>, uvlds);
+    const size_t lds = sizeof(Smem<N, R, RW>);
     static const hipError_t a2 = set_lds(bwd_chunk_kernel<T, N, R, RW>, lds);
-    if (a1 != hipSuccess) return a1;
     if (a2 != hipSuccess) return a2;
     hipError_t e;
     BwdArgs gm = g;
@@ -1299,10 +1376,7 @@ hipError_t launch_bwd(const ScanLaunch &a, const BwdArgs &g, char *base, hipStre
         if (a.theta != nullptr) gm.dangle_out = w.seed;
     }
     const BwdArgs &g2 = gm;
-    hipLaunchKernelGGL((bwd_uv_kernel<T, N, R, RW>), dim3(bhk), dim3(kUVThreads), uvlds, s, a, g2,
-                       w, nck);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_passes_kernel<N>), dim3(2 * bh * (N / 32)), dim3(256), 0, s, a, g2, w,
+    hipLaunchKernelGGL((bwd_passes_kernel<T, N, R, RW>), dim3(2 * bh * (N / 32)), dim3(256), 0, s, a, g2, w,
                        nck);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_chunk_kernel<T, N, R, RW>), dim3(bhk), dim3(kBT), lds, s, a, g2, w, nck);
