@@ -435,8 +435,10 @@ struct PassSmem {
     static constexpr int QT = kRows / R, LDR = kRows + 4, AP = 17;
     float As[32 * LDR];      // rotated columns: [column][rho], lo pairs then hi
     float Xs[kP * LDR];      // X or e^alpha dY: [p][rho]
-    float acs[QT * AP], asn[QT * AP];   // cos / sin of the in-chunk angle [token][pair]
-    float dtv[QT], acum[QT], ww[QT], scal[QT];
+    // per chunk parity: cos / sin of the in-chunk angle [token][pair], the
+    // token scalars, the decay prefix and the per-token scale
+    float acs[2][QT * AP], asn[2][QT * AP];
+    float dtv[2][QT], acum[2][QT], ww[2][QT], scal[2][QT];
     float phi[16];           // the sequence's angle total per pair (reverse pass)
     float red[16];
 };
@@ -543,22 +545,28 @@ __device__ void state_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs &w
     };
     // Chunk k's term of this lane's state columns (acc), its decay e and the
     // rotation by its angle totals (pc, ps).
-    auto chunk = [&](int k, const In &d, f32x4 &alo, f32x4 &ahi, f32x4 &pc, f32x4 &ps,
-                     float &e) {
-        const size_t t0 = static_cast<size_t>(k) * QT;
-        // token scalars, the decay prefix (fused.rs:2494-2498)
+    // The chunk's work in four pieces, software-pipelined over two sets of
+    // the per-chunk tables (sb = chunk parity): the scalars and decay prefix
+    // (p1) and the angles (p2) of chunk k + 1 run in the same two barrier
+    // phases as the staging (p3) and the products (p4) of chunk k.
+    //   phase X: p3(k), p1(k + 1);  barrier;  phase Y: p4(k), p2(k + 1);  barrier
+    // token scalars, the decay prefix (fused.rs:2494-2498)
+    auto p1 = [&](const In &d, int sb) {
         if (tid < QT) {
-            sm.dtv[tid] = d.dt;
-            sm.ww[tid] = d.lam * d.dt + (1.0f - d.lamn) * d.dtn;
+            sm.dtv[sb][tid] = d.dt;
+            sm.ww[sb][tid] = d.lam * d.dt + (1.0f - d.lamn) * d.dtn;
         }
         if (wave == 0) {
             const float v = seg_scan<64>(tid < QT ? d.dt * A : 0.0f);
-            if (lane < QT) sm.acum[lane] = v;
+            if (lane < QT) sm.acum[sb][lane] = v;
         }
-        __syncthreads();
-        // the in-chunk angle of this workgroup's pairs, its cos / sin, the total
+    };
+    // the in-chunk angle of this workgroup's pairs and its cos / sin; per
+    // token wbar (B~'s scale) or e^alpha (dY's)
+    auto p2 = [&](int k, const In &d, int sb) {
         if (rot) {
-            const float dtl = (tl < QT && t0 + tl < L) ? sm.dtv[tl] : 0.0f;
+            const size_t t0 = static_cast<size_t>(k) * QT;
+            const float dtl = (tl < QT && t0 + tl < L) ? sm.dtv[sb][tl] : 0.0f;
 #pragma unroll
             for (int j = 0; j < TS; ++j) {
                 const int i = wave + (PK * j + hl) * NW;
@@ -566,32 +574,34 @@ __device__ void state_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs &w
                 if (tl < QT) {
                     float sv, cv;
                     sincos_any<true>(v, sv, cv);
-                    sm.acs[tl * AP + i] = cv;
-                    sm.asn[tl * AP + i] = sv;
+                    sm.acs[sb][tl * AP + i] = cv;
+                    sm.asn[sb][tl * AP + i] = sv;
                 }
             }
         }
-        // per token: wbar (B~'s scale) or e^alpha (dY's)
         if (tid < QT) {
-            const float et = sm.acum[QT - 1];
-            sm.scal[tid] = FWD ? clamp_exp(et - sm.acum[tid]) * sm.ww[tid] : clamp_exp(sm.acum[tid]);
+            const float et = sm.acum[sb][QT - 1];
+            sm.scal[sb][tid] = FWD ? clamp_exp(et - sm.acum[sb][tid]) * sm.ww[sb][tid]
+                                   : clamp_exp(sm.acum[sb][tid]);
         }
-        __syncthreads();
-        // rotation by the negative in-chunk angle (fused.rs:610-617) into LDS
+    };
+    // rotation by the negative in-chunk angle (fused.rs:610-617) into LDS;
+    // the chunk decay
+    auto p3 = [&](const In &d, int sb, float &e) {
 #pragma unroll
         for (int j = 0; j < JB; ++j) {
             const int ee = tid + 256 * j, t = ee / (16 * R), qr = ee % (16 * R);
             const int q = qr / R, rho = t * R + qr % R;
             float sn = 0.0f, cs = 1.0f;
             if (rot) {
-                cs = sm.acs[t * AP + q];
-                sn = sm.asn[t * AP + q];
+                cs = sm.acs[sb][t * AP + q];
+                sn = sm.asn[sb][t * AP + q];
             }
             float lo = d.b1[j] * cs + d.b2[j] * sn;
             float hi = -d.b1[j] * sn + d.b2[j] * cs;
             if constexpr (FWD) {
-                lo *= sm.scal[t];
-                hi *= sm.scal[t];
+                lo *= sm.scal[sb][t];
+                hi *= sm.scal[sb][t];
             }
             sm.As[q * LDR + rho] = lo;
             sm.As[(16 + q) * LDR + rho] = hi;
@@ -600,12 +610,15 @@ __device__ void state_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs &w
         for (int j = 0; j < JX; ++j) {
             const int ee = tid + 256 * j, t = ee / (kP * R), pr = ee % (kP * R);
             float v = d.xv[j];
-            if constexpr (!FWD) v *= sm.scal[t];
+            if constexpr (!FWD) v *= sm.scal[sb][t];
             sm.Xs[(pr / R) * LDR + t * R + pr % R] = v;
         }
-        e = clamp_exp(sm.acum[QT - 1]);
-        __syncthreads();
-        // U^T (V^T) at this lane's (n, p): A(m = n, k = rho), B(k = rho, col = p)
+        e = clamp_exp(sm.acum[sb][QT - 1]);
+    };
+    // U^T (V^T) at this lane's (n, p): A(m = n, k = rho), B(k = rho, col = p);
+    // the rotation by the chunk's angle totals, the in-chunk angles of its
+    // last row
+    auto p4 = [&](int sb, f32x4 &alo, f32x4 &ahi, f32x4 &pc, f32x4 &ps) {
         alo = f32x4{0.f, 0.f, 0.f, 0.f};
         ahi = alo;
         const float *br = sm.Xs + p * LDR;
@@ -614,18 +627,15 @@ __device__ void state_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs &w
             alo = scan::mma_kb(sm.As + c * LDR + 16 * kb, br + 16 * kb, alo, gq);
             ahi = scan::mma_kb(sm.As + (16 + c) * LDR + 16 * kb, br + 16 * kb, ahi, gq);
         }
+        pc = f32x4{1.f, 1.f, 1.f, 1.f};
+        ps = f32x4{0.f, 0.f, 0.f, 0.f};
         if (rot) {
-            // the chunk's angle total is the in-chunk angle of its last row
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                pc[r] = sm.acs[(QT - 1) * AP + 4 * gq + r];
-                ps[r] = sm.asn[(QT - 1) * AP + 4 * gq + r];
+                pc[r] = sm.acs[sb][(QT - 1) * AP + 4 * gq + r];
+                ps[r] = sm.asn[sb][(QT - 1) * AP + 4 * gq + r];
             }
         }
-        // No barrier here: the next chunk's first LDS writes (dtv, ww, acum)
-        // are of values read only before the staging barrier above, and its
-        // later writes follow its first barrier, which every wave reaches
-        // only after these reads.
     };
     auto offs = [&](int k, size_t &o, size_t &oh) {
         const size_t bhk = bh * nck + k;
@@ -653,23 +663,35 @@ __device__ void state_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs &w
         In d[D];
 #pragma unroll
         for (int j = 0; j < D; ++j) load(j, d[j]);
+        p1(d[0], 0);
+        __syncthreads();
+        p2(0, d[0], 0);
+        __syncthreads();
         for (int k = 0; k < nck; k += D) {
 #pragma unroll
             for (int j = 0; j < D; ++j) {
-                if (k + j < nck) {
-                    f32x4 ulo, uhi, pc = {1.f, 1.f, 1.f, 1.f}, ps = {0.f, 0.f, 0.f, 0.f};
+                const int kc = k + j;
+                if (kc < nck) {
+                    const int sb = kc & 1;
+                    const bool more = kc + 1 < nck;
                     float e;
-                    chunk(k + j, d[j], ulo, uhi, pc, ps, e);
+                    p3(d[j], sb, e);
+                    if (more) p1(d[(j + 1) % D], sb ^ 1);
+                    __syncthreads();
+                    f32x4 ulo, uhi, pc, ps;
+                    p4(sb, ulo, uhi, pc, ps);
+                    if (more) p2(kc + 1, d[(j + 1) % D], sb ^ 1);
                     size_t o, oh;
-                    offs(k + j, o, oh);
+                    offs(kc, o, oh);
                     *reinterpret_cast<f32x4 *>(w.s + o) = lo;
                     *reinterpret_cast<f32x4 *>(w.s + oh) = hi;
                     lo = lo * e + ulo;
                     hi = hi * e + uhi;
                     if (rot) rot4(lo, hi, pc, ps);   // R(Phi_k)
-                    if (i1 == 0 && tid == 0) w.eda[bh * nck + k + j] = e;
+                    if (i1 == 0 && tid == 0) w.eda[bh * nck + kc] = e;
+                    __syncthreads();
                 }
-                load(k + D + j, d[j]);
+                load(kc + D, d[j]);
             }
         }
     } else {
@@ -732,22 +754,34 @@ __device__ void state_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs &w
         In d[D];
 #pragma unroll
         for (int j = 0; j < D; ++j) load(nck - 1 - j, d[j]);
+        p1(d[0], (nck - 1) & 1);
+        __syncthreads();
+        p2(nck - 1, d[0], (nck - 1) & 1);
+        __syncthreads();
         for (int k = nck - 1; k >= 0; k -= D) {
 #pragma unroll
             for (int j = 0; j < D; ++j) {
-                if (k - j >= 0) {
-                    f32x4 vlo, vhi, pc = {1.f, 1.f, 1.f, 1.f}, ps = {0.f, 0.f, 0.f, 0.f};
+                const int kc = k - j;
+                if (kc >= 0) {
+                    const int sb = kc & 1;
+                    const bool more = kc > 0;
                     float e;
-                    chunk(k - j, d[j], vlo, vhi, pc, ps, e);
+                    p3(d[j], sb, e);
+                    if (more) p1(d[(j + 1) % D], sb ^ 1);
+                    __syncthreads();
+                    f32x4 vlo, vhi, pc, ps;
+                    p4(sb, vlo, vhi, pc, ps);
+                    if (more) p2(kc - 1, d[(j + 1) % D], sb ^ 1);
                     if (rot) rot4(lo, hi, pc, -ps);   // R(-Phi_k)
                     size_t o, oh;
-                    offs(k - j, o, oh);
+                    offs(kc, o, oh);
                     *reinterpret_cast<f32x4 *>(w.gh + o) = lo;
                     *reinterpret_cast<f32x4 *>(w.gh + oh) = hi;
                     lo = lo * e + vlo;
                     hi = hi * e + vhi;
+                    __syncthreads();
                 }
-                load(k - D - j, d[j]);
+                load(kc - D, d[j]);
             }
         }
         // into the global frame: dZ0 = R(-angle0) G_0
