@@ -29,6 +29,55 @@ rms_norm_kernel(size_t rows, size_t dim, const uint16_t *x, size_t xs, const flo
     uint16_t *yr = y + row * ys;
     const bool vec = (dim % 8 == 0) && ((reinterpret_cast<uintptr_t>(xr) & 15) == 0) &&
                      ((reinterpret_cast<uintptr_t>(yr) & 15) == 0);
+    if (vec && dim <= 2048 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+        // the whole row in registers (up to four 16-byte pieces a lane): the
+        // row's and the gain's loads all in flight at once, no second read
+        uint4 q[4];
+        f32x4 wv[4][2];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const size_t i = lane * 8 + c * 512;
+            q[c] = make_uint4(0u, 0u, 0u, 0u);
+            wv[c][0] = wv[c][1] = f32x4{1.f, 1.f, 1.f, 1.f};
+            if (i < dim) {
+                q[c] = *reinterpret_cast<const uint4 *>(xr + i);
+                if (w) {
+                    wv[c][0] = *reinterpret_cast<const f32x4 *>(w + i);
+                    wv[c][1] = *reinterpret_cast<const f32x4 *>(w + i + 4);
+                }
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const unsigned int u[4] = {q[c].x, q[c].y, q[c].z, q[c].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float a = __uint_as_float(u[j] << 16), b = __uint_as_float(u[j] & 0xFFFF0000u);
+                ss += a * a + b * b;
+            }
+        }
+        ss = group_sum(ss, 64);
+        const float scale = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const size_t i = lane * 8 + c * 512;
+            if (i >= dim) continue;
+            const unsigned int u[4] = {q[c].x, q[c].y, q[c].z, q[c].w};
+            unsigned int o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float a = __uint_as_float(u[j] << 16) * scale, b = __uint_as_float(u[j] & 0xFFFF0000u) * scale;
+                if (w) {
+                    a *= wv[c][j >> 1][2 * (j & 1)];
+                    b *= wv[c][j >> 1][2 * (j & 1) + 1];
+                }
+                o[j] = static_cast<unsigned int>(to_bits(a)) | (static_cast<unsigned int>(to_bits(b)) << 16);
+            }
+            *reinterpret_cast<uint4 *>(yr + i) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        return;
+    }
     float ss = 0.0f;
     if (vec) {
         for (size_t i = lane * 8; i < dim; i += 512) {
