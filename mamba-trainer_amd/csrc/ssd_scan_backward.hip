@@ -468,8 +468,6 @@ __device__ void state_pass(const ScanLaunch &a, const BwdArgs &g, const BwdWs &w
     const int p = 16 * pt + c, nlo = 16 * i1 + 4 * gq;
     const size_t sbase = bh * kP * N + static_cast<size_t>(p) * N;
     const int tl = PACK ? (lane & 31) : lane, hl = PACK ? (lane >> 5) : 0;
-    const void *bc = FWD ? a.b : a.c;
-    const void *xy = FWD ? a.x : g.dy;
     auto rot4 = [](f32x4 &lo, f32x4 &hi, f32x4 cs, f32x4 sn) {
         const f32x4 l = lo;
         lo = l * cs - hi * sn;
