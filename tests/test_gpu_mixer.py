@@ -37,7 +37,12 @@ def lib():
 
 
 # ------------------------------------------------------------------ kernels
-@pytest.mark.parametrize("rows,dim,stride", [(37, 768, 768), (5, 4, 4), (9, 24, 40), (3, 130, 130)])
+# rows up to 2048 wide and 16-byte aligned are held in registers (one to four
+# 16-byte pieces a lane, the last possibly partial); wider rows and unaligned
+# ones take the streaming loops
+@pytest.mark.parametrize("rows,dim,stride", [(37, 768, 768), (5, 4, 4), (9, 24, 40), (3, 130, 130),
+                                             (256, 1536, 1536), (7, 2048, 2048), (7, 2056, 2056),
+                                             (4, 520, 528)])
 def test_rms_norm_rows(rows, dim, stride):
     import ctypes as C
     rng = np.random.default_rng(rows * dim)
