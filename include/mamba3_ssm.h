@@ -9,6 +9,8 @@
  *   m3_ssm_config / m3_config_*   SsmConfig and its enums   src/ssm/config.rs:19-347
  *   m3_ssm_state                  SsmState                  src/ssm/scan.rs:293-358
  *   m3_scan_inputs / m3_scan      ScanInputs, mamba3_scan   src/ssm/scan.rs:360-618
+ *   m3_scan_gated                 mamba3_scan then Mamba3Mixer::finish's gate
+ *                                                           src/models/mamba3.rs:468-477
  *   m3_scan_output                ScanOutput                src/ssm/scan.rs:445-452
  *   m3_scan_grads / m3_scan_backward
  *                                 gradient of mamba3_scan   src/ssm/scan.rs:458-638 under
@@ -148,6 +150,17 @@ typedef struct m3_scan_output {
 /* mamba3_scan (scan.rs:458-618): trapezoid weights, rotating frame, MIMO
  * fold, carried state, skip path and boundary state in one launch. */
 m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *stream);
+
+/* m3_scan, then the mixer's gate on its y in place (Mamba3Mixer::finish
+ * without a post-gate norm, src/models/mamba3.rs:468-477):
+ * y = bf16(y) * silu(z), z bf16 [B*T rows of z_stride, the first
+ * heads*head_dim*rank columns].  The same bytes as m3_scan followed by
+ * m3_mixer_gate(..., norm_weight = NULL, out = y).  bf16 storage only
+ * (else M3_ERR_UNSUPPORTED); z_stride < heads*head_dim*rank is M3_ERR_SHAPE.
+ * Where the chunk-parallel form runs at rank 1 the gate rides on its output
+ * kernel (no y round trip); elsewhere it is a second launch. */
+m3_status m3_scan_gated(const m3_scan_inputs *in, const m3_scan_output *out, const void *z,
+                        size_t z_stride, void *stream);
 
 /* Workspace bytes the chunk-parallel scan needs for these inputs (shapes and
  * dtype are read; pointers are not); 0 when the shape runs single-pass only.

@@ -171,7 +171,11 @@ float m3_discretization_fixed_lambda(int32_t d) {
     return std::nanf("");
 }
 
-m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *stream) {
+// The scan, and with gate_z the mixer's gate on its y (in place): fused into
+// the chunk-parallel kernel where that form runs (bf16, rank 1), else the
+// gate kernel after the scan.
+static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
+                            const void *gate_z, size_t gate_stride, void *stream) {
     if (in == nullptr || out == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/outputs are NULL");
     if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
     if (in->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
@@ -263,7 +267,18 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
     hipError_t e;
     const size_t need = m3::scan_chunked_workspace(a);
     const bool ws_aligned = (reinterpret_cast<uintptr_t>(in->workspace) & 255u) == 0;
-    if (need > 0 && in->workspace != nullptr && in->workspace_bytes >= need && ws_aligned) {
+    const bool chunked =
+        need > 0 && in->workspace != nullptr && in->workspace_bytes >= need && ws_aligned;
+    // the fused gate reads z in 8-byte pieces through one 32-bit buffer range
+    // per sequence
+    const bool fuse_gate = gate_z != nullptr && chunked && a.bf16 && a.rank == 1 &&
+                           (reinterpret_cast<uintptr_t>(gate_z) & 7u) == 0 && gate_stride % 4 == 0 &&
+                           a.seq * gate_stride * 2 < (size_t(1) << 31);
+    if (fuse_gate) {
+        a.gate_z = gate_z;
+        a.gate_stride = gate_stride;
+    }
+    if (chunked) {
         e = m3::launch_scan_chunked(a, in->workspace, s);
         if (e == hipSuccess) g_launches.fetch_add(3, std::memory_order_relaxed);
     } else {
@@ -271,7 +286,29 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
         if (e == hipSuccess) g_launches.fetch_add(1, std::memory_order_relaxed);
     }
     if (e != hipSuccess) return hip_fail(e, "scan launch");
+    if (gate_z != nullptr && !fuse_gate) {
+        e = m3::launch_mixer_gate(B * in->seq, H * P * in->rank, out->y, gate_z, gate_stride,
+                                  nullptr, 0.0f, out->y, s);
+        if (e != hipSuccess) return hip_fail(e, "gate launch");
+        g_launches.fetch_add(1, std::memory_order_relaxed);
+    }
     return ok();
+}
+
+m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *stream) {
+    return scan_entry(in, out, nullptr, 0, stream);
+}
+
+m3_status m3_scan_gated(const m3_scan_inputs *in, const m3_scan_output *out, const void *z,
+                        size_t z_stride, void *stream) {
+    if (in == nullptr || out == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/outputs are NULL");
+    if (in->dtype != M3_BF16)
+        return fail(M3_ERR_UNSUPPORTED, "the gated scan covers bf16 storage");
+    if (z == nullptr) return fail(M3_ERR_ARGUMENT, "the gate's z is NULL");
+    const size_t d_inner = in->heads * in->head_dim * in->rank;
+    if (z_stride < d_inner)
+        return fail(M3_ERR_SHAPE, "z stride %zu is shorter than d_inner %zu", z_stride, d_inner);
+    return scan_entry(in, out, z, z_stride, stream);
 }
 
 size_t m3_scan_workspace_bytes(const m3_scan_inputs *in) {
@@ -463,7 +500,7 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
     gr.dangle0 = (st && st->angle && in->theta) ? g->dangle0 : nullptr;
     e = m3::launch_scan_backward(a, gr, in->workspace, s);
     if (e != hipSuccess) return hip_fail(e, "scan backward launch");
-    g_launches.fetch_add((in->theta ? 7 : 6) + (g->dlast_u ? 2 : 0), std::memory_order_relaxed);
+    g_launches.fetch_add((in->theta ? 5 : 4) + (g->dlast_u ? 2 : 0), std::memory_order_relaxed);
     if (g->dd_skip != nullptr && in->d_skip == nullptr) {
         e = hipMemsetAsync(g->dd_skip, 0, H * sizeof(float), s);
         if (e != hipSuccess) return hip_fail(e, "dd_skip");

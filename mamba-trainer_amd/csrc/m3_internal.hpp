@@ -85,6 +85,11 @@ struct ScanLaunch {
     const float *angle0;            // [B,H,N/2] or null
     const float *init_state;        // ssd_chunked's initial_state or null
     void *y;                        // [B,T,H,P,R]
+    // Optional gate on y (Mamba3Mixer::finish, models/mamba3.rs:468-477),
+    // taken by the bf16 rank-1 chunk-parallel path only: y = bf16(y) *
+    // silu(z), z bf16 at gate_z + token * gate_stride + h * head_dim + p.
+    const void *gate_z;
+    size_t gate_stride;
     float *h_out, *last_u_out, *angle_out;  // null when not wanted
     // the caller's chunk_size (tokens; 0 = 64): the chunk-parallel path passes
     // the state between segments of at least this many tokens

@@ -40,6 +40,7 @@
 #include <type_traits>
 
 #include "scan_common.hpp"
+#include "mixer_math.hpp"
 
 namespace m3 {
 
@@ -1226,7 +1227,12 @@ struct ScanDmaSmem {
     float acum[64], gw[64], ww[64], wdv[64];
 };
 
-template <int N>
+// GATE: y leaves through the mixer's gate, bf16(y) * silu(z) (the rounding
+// of mixer_gate_vec_kernel).  A sub-chunk's gated y is stored during the next
+// sub-chunk, once its z has landed: z's loads are ordinary (the compiler waits
+// for them), so they are consumed where the only loads issued after them are
+// that sub-chunk's X, which is waited for there anyway.
+template <int N, bool GATE>
 __global__ void __launch_bounds__(kThreads, 3)
 chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     constexpr int P = kP;
@@ -1308,6 +1314,35 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 #pragma unroll
         for (int q = 0; q < CX / 4; ++q)
             lds_load_rows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.r[(k & 1) ^ 1], wave + 4 * q, lane);
+    };
+
+    // the gate: z of this sequence (tokens past its end read as zero), and
+    // the previous sub-chunk's y (bf16) and z awaiting the gate
+    const rsrc_t rz =
+        GATE ? make_rsrc(static_cast<const char *>(a.gate_z) + (bb * L * a.gate_stride + hh * P) * 2,
+                         static_cast<uint32_t>((L * a.gate_stride - hh * P) * 2))
+             : make_rsrc(a.x, 0u);
+    const uint32_t zs = GATE ? static_cast<uint32_t>(a.gate_stride * 2) : 0u;
+    u32x2 ypend[NT], zpend[NT];
+    uint32_t ytok0 = 0;
+    bool pend = false;
+    auto gate_store = [&]() {
+        const int gg = lane >> 4, cc = lane & 15;
+#pragma unroll
+        for (int tj = 0; tj < NT; ++tj) {
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t yw = ypend[tj][r >> 1], zw = zpend[tj][r >> 1];
+                const float yv = __uint_as_float((r & 1) ? (yw & 0xFFFF0000u) : (yw << 16));
+                const float zv = __uint_as_float((r & 1) ? (zw & 0xFFFF0000u) : (zw << 16));
+                v[r] = yv * mixm::silu_fast(zv);
+            }
+            u32x2 pk;
+            pk[0] = pk_bf16(v[0], v[1]);
+            pk[1] = pk_bf16(v[2], v[3]);
+            bst8(pk, rs.y, (ytok0 + 16 * tj + cc) * rs.tok_x + (16 * wave + 4 * gg) * 2);
+        }
     };
 
     TokScalars sc_next;
@@ -1506,6 +1541,12 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         for (int tj = 0; tj < NT; ++tj) yc[tj] = yc[tj] * dexp2(sm.acum[16 * tj + c]);
     }
     __syncthreads();   // the band is complete; C~ is dead
+    if constexpr (GATE) {
+        // the previous sub-chunk's gated y: its z was loaded before this
+        // sub-chunk's X, which the wait below needs anyway
+        if (pend) gate_store();
+        pend = false;
+    }
     if (more) load_c(sck + 1, sc_next);
     // X landed (the next sub-chunk's C and scalars may be out)
     if (more)
@@ -1589,7 +1630,20 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             u32x2 pk;
             pk[0] = pk_bf16(acc[0], acc[1]);
             pk[1] = pk_bf16(acc[2], acc[3]);
-            bst8(pk, rs.y, oy);
+            if constexpr (GATE) {
+                ypend[tj] = pk;
+                zpend[tj] = bld8(rz, (tok0 + t) * zs + (16 * wave + 4 * g) * 2);
+            } else {
+                bst8(pk, rs.y, oy);
+            }
+        }
+        if constexpr (GATE) {
+            ytok0 = tok0;
+            pend = true;
+            if (!more) {
+                gate_store();
+                pend = false;
+            }
         }
     }
     if (more) {
@@ -1683,12 +1737,18 @@ hipError_t launch_three(const ScanLaunch &a, char *base, hipStream_t s) {
                        sp.nseg);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if constexpr (sizeof(T) == 2 && R == 1)
-        hipLaunchKernelGGL((chunk_scan_dma_kernel<N>), dim3(bhs), dim3(kThreads), 0, s, a, ws,
-                           sp.nsub, sp.kseg, sp.nseg);
-    else
+    if constexpr (sizeof(T) == 2 && R == 1) {
+        if (a.gate_z != nullptr)
+            hipLaunchKernelGGL((chunk_scan_dma_kernel<N, true>), dim3(bhs), dim3(kThreads), 0, s, a,
+                               ws, sp.nsub, sp.kseg, sp.nseg);
+        else
+            hipLaunchKernelGGL((chunk_scan_dma_kernel<N, false>), dim3(bhs), dim3(kThreads), 0, s, a,
+                               ws, sp.nsub, sp.kseg, sp.nseg);
+    } else {
+        if (a.gate_z != nullptr) return hipErrorNotSupported;   // the caller gates separately
         hipLaunchKernelGGL((chunk_scan_kernel<T, N, R, ROWS, kPf>), dim3(bhs), dim3(kThreads), 0,
                            s, a, ws, sp.nsub, sp.kseg, sp.nseg);
+    }
     return hipGetLastError();
 }
 

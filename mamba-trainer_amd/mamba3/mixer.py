@@ -23,6 +23,7 @@ from . import _lib
 from .error import ShapeError, UnsupportedError
 from .nn import Linear, RmsNorm, _bf16_dev, _stream, normal, residual_scaled, tensor_param
 from .ssm import (ScanInputs, SsmConfig, SsmState, SsmStateFactored, StateDynamics, mamba3_scan,
+                  mamba3_scan_gated,
                   mamba3_step_, mamba3_step_factored_)
 
 
@@ -223,8 +224,18 @@ class Mamba3Mixer:
         factored = cache is not None and isinstance(cache.ssm, SsmStateFactored)
         if cache is not None:
             si = si.with_state(cache.ssm.to_full() if factored else cache.ssm)
-        scan = mamba3_scan(si)
-        y = self.finish(scan.y, proj, residual=residual, out=out)
+        grad = torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (proj.x, proj.b, proj.c, proj.dt, proj.lam,
+                                                         proj.theta, self.a_log, self.d_skip))
+        if self.post_gate_norm is None and not grad and proj.x.dtype == torch.bfloat16:
+            # the gate on the scan's output (fused into its last kernel where
+            # that form runs), then out_proj
+            scan = mamba3_scan_gated(si, proj.projected)
+            B, T = proj.x.shape[0], proj.x.shape[1]
+            y = self.out_proj.apply(scan.y.view(B, T, self.cfg.d_inner()), residual=residual, out=out)
+        else:
+            scan = mamba3_scan(si)
+            y = self.finish(scan.y, proj, residual=residual, out=out)
         new = None
         if cache is not None:
             st = scan.state

@@ -278,7 +278,15 @@ def mamba3_scan_backward(inputs: ScanInputs, dy: torch.Tensor, dh: Optional[torc
     return g
 
 
-def _scan_forward(inputs: ScanInputs) -> ScanOutput:
+def mamba3_scan_gated(inputs: ScanInputs, z: torch.Tensor) -> ScanOutput:
+    """mamba3_scan followed by the mixer's gate (mamba3.rs:468-477, no
+    post-gate norm): the returned y is bf16(y) * silu(z).  z holds B*T rows
+    whose first H*P*R columns are the gate (e.g. the in_proj output, z its
+    leading columns).  Inference only: no autograd node."""
+    return _scan_forward(inputs, z)
+
+
+def _scan_forward(inputs: ScanInputs, gate: Optional[torch.Tensor] = None) -> ScanOutput:
     x = inputs.x
     if x.dim() != 5:
         raise RankError(5, x.dim(), x.shape)
@@ -347,7 +355,18 @@ def _scan_forward(inputs: ScanInputs) -> ScanOutput:
             cin.workspace = ws.data_ptr()
             cin.workspace_bytes = need
     cout = _lib.ScanOutputC(y.data_ptr(), out_state._c() if out_state else _lib.SsmStateC())
-    _lib.check(_lib.lib().m3_scan(C.byref(cin), C.byref(cout), _stream(x)))
+    if gate is None:
+        _lib.check(_lib.lib().m3_scan(C.byref(cin), C.byref(cout), _stream(x)))
+    else:
+        zt = _dev(gate, "z")
+        if zt.dtype != torch.bfloat16 or zt.stride(-1) != 1 or zt.dim() < 2:
+            raise ShapeError("shape error: z must be bf16 rows with unit column stride")
+        rows = zt.numel() // zt.shape[-1] if zt.is_contiguous() else None
+        if rows != B * T or zt.shape[-1] < H * P * R:
+            raise ShapeError(f"shape error: z must hold {B * T} rows of at least {H * P * R} columns, "
+                             f"got {tuple(zt.shape)}")
+        _lib.check(_lib.lib().m3_scan_gated(C.byref(cin), C.byref(cout), zt.data_ptr(),
+                                            zt.shape[-1], _stream(x)))
     return ScanOutput(y, out_state)
 
 

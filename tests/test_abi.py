@@ -289,3 +289,24 @@ def test_mixer_step_shape_cover_and_argument_checks():
     assert int(L.m3_mixer_in_proj_width(C.byref(d))) % 8 == 4
     assert int(L.m3_mixer_step(C.byref(d), None, None, None, None, None, None, None,
                                C.byref(_lib.SsmStateC()), None, None, None)) == _lib.M3_ERR_UNSUPPORTED
+
+
+def test_gated_scan_argument_checks_before_any_launch():
+    """m3_scan_gated rejects f32 storage, a NULL z and a z row shorter than
+    heads*head_dim*rank before any device work (the pointers are stand-ins
+    that are never dereferenced)."""
+    from mamba3 import _lib
+    L = _lib.lib()
+    fake = 1 << 20
+    before = L.m3_launch_count()
+
+    def call(dtype=_lib.M3_BF16, z=fake, stride=64 * 3):
+        cin = _lib.ScanInputsC(1, 8, 3, 64, 128, 1, dtype, fake, fake, fake, fake, fake, fake,
+                               None, None, None, 64, 0, None, 0)
+        cout = _lib.ScanOutputC(fake, _lib.SsmStateC())
+        return L.m3_scan_gated(C.byref(cin), C.byref(cout), z, stride, None)
+
+    assert call(dtype=_lib.M3_F32) == _lib.M3_ERR_UNSUPPORTED
+    assert call(z=None) == _lib.M3_ERR_ARGUMENT
+    assert call(stride=64 * 3 - 1) == _lib.M3_ERR_SHAPE
+    assert L.m3_launch_count() == before

@@ -386,3 +386,46 @@ def test_config2_full_size_split_window_and_f64():
         print(f"config 2 full size, sequence {bb} (24 heads, L=4096) against f64: rel-L2 y "
               f"{e[0]:.2e}, h {e[1]:.2e}, last_u {e[2]:.2e} (bar {BF16_TOL:g})", flush=True)
         assert max(e) <= BF16_TOL
+
+
+# ------------------------------------------------------------------ gated scan
+@pytest.mark.parametrize("B,T,H,N,R,theta,skip,state,chunk_parallel", [
+    (2, 300, 3, 128, 1, True, True, True, True),     # chunk-parallel, rank 1: the gate in its last kernel
+    (1, 700, 2, 64, 1, True, False, False, True),    # d_state 64, ragged end
+    (2, 256, 2, 128, 1, False, True, False, True),   # real dynamics
+    (1, 300, 2, 128, 2, True, True, False, True),    # MIMO chunk-parallel: the gate as a second launch
+    (2, 300, 3, 128, 1, True, True, True, False),    # single pass: a second launch
+])
+def test_gated_scan_equals_scan_then_gate(B, T, H, N, R, theta, skip, state, chunk_parallel):
+    """m3_scan_gated gives m3_scan's y through m3_mixer_gate (no post-gate
+    norm) bit for bit, with the same output state, on every path."""
+    import ctypes as C
+    from mamba3 import _lib
+    from mamba3.ssm import ScanInputs, SsmState, mamba3_scan, mamba3_scan_gated
+    P = 64
+    rng = np.random.default_rng(zlib.crc32(repr((B, T, H, N, R)).encode()))
+    inp = baseline_inputs(rng, B, T, H, P, N, R, theta=theta, dtype="bf16", state=state)
+    bf = torch.bfloat16
+    si = ScanInputs(dev(inp["x"], bf), dev(inp["b"], bf), dev(inp["c"], bf), dev(inp["dt"]),
+                    dev(inp["a_log"]), dev(inp["lam"]))
+    if theta:
+        si = si.with_theta(dev(inp["theta"], bf))
+    if skip:
+        si = si.with_skip(dev(rng.uniform(-1, 1, H).astype(np.float32)))
+    if state:
+        si = si.with_state(SsmState(dev(inp["h0"]), dev(inp["last_u0"]),
+                                    dev(inp["angle0"]) if theta else None))
+    si = si.with_state_output(True).with_chunk_parallel(chunk_parallel)
+    d = H * P * R
+    width = d + 72                       # z leads a wider row, as in the in_proj output
+    proj = torch.randn(B, T, width, device="cuda:0").to(bf)
+    ref = mamba3_scan(si)
+    gated = torch.empty(B, T, d, dtype=bf, device="cuda:0")
+    _lib.check(_lib.lib().m3_mixer_gate(B * T, d, ref.y.data_ptr(), proj.data_ptr(), width, None,
+                                        C.c_float(1e-5), gated.data_ptr(), None))
+    got = mamba3_scan_gated(si, proj)
+    torch.cuda.synchronize()
+    assert torch.equal(got.y.view(B, T, d), gated)
+    assert torch.equal(got.state.h, ref.state.h) and torch.equal(got.state.last_u, ref.state.last_u)
+    if theta:
+        assert torch.equal(got.state.angle, ref.state.angle)
