@@ -391,6 +391,7 @@ def test_config2_full_size_split_window_and_f64():
 # ------------------------------------------------------------------ gated scan
 @pytest.mark.parametrize("B,T,H,N,R,theta,skip,state,chunk_parallel", [
     (2, 300, 3, 128, 1, True, True, True, True),     # chunk-parallel, rank 1: the gate in its last kernel
+    (8, 2048, 12, 128, 1, True, True, False, True),  # config 1's shape: segments of several sub-chunks
     (1, 700, 2, 64, 1, True, False, False, True),    # d_state 64, ragged end
     (2, 256, 2, 128, 1, False, True, False, True),   # real dynamics
     (1, 300, 2, 128, 2, True, True, False, True),    # MIMO chunk-parallel: the gate as a second launch
