@@ -175,8 +175,10 @@ size_t m3_scan_workspace_bytes(const m3_scan_inputs *in);
  * loops, harnesses that forbid hipMalloc).  The chunk-parallel path's workspace
  * is a file-scope device array of M3_NO_ALLOC_SCRATCH_MIB MiB instead of the
  * caller's buffer (in->workspace and in->workspace_bytes are ignored).  Each GPU
- * holds its own copy of that array from the first call on that device until the
- * process ends.  Shapes whose workspace (m3_scan_workspace_bytes) exceeds it
+ * holds its own copy of that array from the moment the library's code object is
+ * loaded on that device (the first launch of any of its kernels there) until
+ * the process ends, so every process that uses the library on a GPU holds those
+ * M3_NO_ALLOC_SCRATCH_MIB MiB there whether or not it calls this function.  Shapes whose workspace (m3_scan_workspace_bytes) exceeds it
  * return M3_ERR_UNSUPPORTED before any device work.  Results are those of
  * m3_scan with a caller workspace, bit for bit.  Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (different streams, or

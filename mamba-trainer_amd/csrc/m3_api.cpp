@@ -721,6 +721,8 @@ m3_status m3_step_layers(size_t n_layers, const m3_step_inputs *inputs, m3_ssm_s
             return fail(M3_ERR_UNSUPPORTED, "m3_step_layers covers d_state a multiple of 4 with "
                         "d_state/4 a power of two up to 64 and rank 1, 2, 3, 4 or 8");
     }
+    // every layer's arguments are validated before the first launch, so an
+    // error leaves no layer of the cache stepped
     for (size_t l = 0; l < n_layers; ++l) {
         m3::StepLaunch a;
         bool empty = false;
@@ -728,6 +730,13 @@ m3_status m3_step_layers(size_t n_layers, const m3_step_inputs *inputs, m3_ssm_s
                                         factored ? &factored[l] : nullptr, ys[l], a, &empty);
         if (st != M3_OK) return st;
         if (empty) return ok();
+    }
+    for (size_t l = 0; l < n_layers; ++l) {
+        m3::StepLaunch a;
+        bool empty = false;
+        const m3_status st = build_step(&inputs[l], states ? &states[l] : nullptr,
+                                        factored ? &factored[l] : nullptr, ys[l], a, &empty);
+        if (st != M3_OK) return st;
         if (n == 0) base = a;
         m3::StepLayer &L = table.layer[n++];
         L.x = a.x;

@@ -396,7 +396,8 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
 
 // ---------------------------------------------------------------- gate
 // out = [RMSNorm(y)] * silu(z) over rows of d_inner (mamba3.rs:468-477); one
-// wave per token.
+// wave per token.  silu is silu_fast here as in the vector kernel and the
+// gate fused into the scan's output kernel, so every path rounds alike.
 __global__ void __launch_bounds__(256)
 mixer_gate_kernel(size_t tokens, size_t d, const uint16_t *y, const uint16_t *z, size_t zs,
                   const float *nw, float eps, uint16_t *out) {
@@ -419,7 +420,7 @@ mixer_gate_kernel(size_t tokens, size_t d, const uint16_t *y, const uint16_t *z,
     for (size_t i = lane; i < d; i += 64) {
         float v = bf(yr, i);
         if (nw) v = v * scale * nw[i];
-        orow[i] = to_bits(v * siluf_(bf(zr, i)));
+        orow[i] = to_bits(v * silu_fast(bf(zr, i)));
     }
 }
 

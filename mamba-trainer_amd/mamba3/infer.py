@@ -85,15 +85,22 @@ class StateCache:
         step_layer on each layer in turn."""
         import ctypes as C
         from . import _lib
-        from .ssm.scan import _step_args, _stream
+        from .ssm.scan import _step_args, _stream, check_step_state
         if len(inputs) != len(self._layers):
             raise ArgumentError(f"step_all needs one input tuple per layer "
                                 f"({len(self._layers)}), got {len(inputs)}")
         n = len(inputs)
-        args = (_lib.StepInputsC * n)()
-        keep, ys = [], []
+        # every layer's inputs and state are checked before anything is
+        # launched: the kernel steps each layer's cache slice in place at the
+        # inputs' element size and shape
+        checked = []
         for l, inp in enumerate(inputs):
             a, k = _step_args(*inp)
+            check_step_state(k, inp[6] is not None, self._layers[l])
+            checked.append((a, k))
+        args = (_lib.StepInputsC * n)()
+        keep, ys = [], []
+        for l, (a, k) in enumerate(checked):
             args[l] = a
             keep.append(k)
             ys.append(torch.empty_like(k[0]))

@@ -429,19 +429,42 @@ def _step_args(x, b, c, dt, lam, a_log, theta, d_skip):
     return args, keep
 
 
+def check_step_state(keep, rotational: bool, state) -> None:
+    """The checks every in-place step runs on its state before a launch: h
+    (and last_u, or the factored cache's x_prev / b_prev in the inputs'
+    dtype) contiguous device tensors of the step inputs' [B, H, P, N] (x
+    [B, H, P, R], b [B, H, N, R]) shape, and the angle when theta is given.
+    keep is _step_args' tensors (x, b, ...)."""
+    B, H, P, R = keep[0].shape
+    N = keep[1].shape[2]
+    t = state.h
+    if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+        raise ArgumentError("state.h must be a contiguous float32 device tensor")
+    _expect_shape(t, (B, H, P, N), "state.h")
+    if isinstance(state, SsmStateFactored):
+        for t, shape, what in ((state.x_prev, (B, H, P, R), "state.x_prev"),
+                               (state.b_prev, (B, H, N, R), "state.b_prev")):
+            if t.dtype != keep[0].dtype or not t.is_contiguous() or not t.is_cuda:
+                raise ArgumentError(f"{what} must be a contiguous {keep[0].dtype} device tensor")
+            _expect_shape(t, shape, what)
+    else:
+        t = state.last_u
+        if t is None or t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+            raise ArgumentError("state.last_u must be a contiguous float32 device tensor")
+        _expect_shape(t, (B, H, P, N), "state.last_u")
+    if rotational:
+        if state.angle is None:
+            raise ArgumentError("theta needs the state's angle tensor (updated in place)")
+        a = state.angle
+        if a.dtype != torch.float32 or not a.is_contiguous() or not a.is_cuda:
+            raise ArgumentError("state.angle must be a contiguous float32 device tensor")
+        _expect_shape(a, (B, H, N // 2), "state.angle")
+
+
 def mamba3_step_(x, b, c, dt, lam, a_log, theta, d_skip, state: SsmState) -> torch.Tensor:
     """mamba3_step with the state updated IN PLACE (the C ABI's semantics); returns y."""
     args, keep = _step_args(x, b, c, dt, lam, a_log, theta, d_skip)
-    B, H, P, R = keep[0].shape
-    N = keep[1].shape[2]
-    for t, what in ((state.h, "state.h"), (state.last_u, "state.last_u")):
-        if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
-            raise ArgumentError(f"{what} must be a contiguous float32 device tensor")
-        _expect_shape(t, (B, H, P, N), what)
-    if theta is not None:
-        if state.angle is None:
-            raise ArgumentError("theta needs the state's angle tensor (updated in place)")
-        _expect_shape(state.angle, (B, H, N // 2), "state.angle")
+    check_step_state(keep, theta is not None, state)
     y = torch.empty_like(keep[0])
     st_c = state._c()
     _lib.check(_lib.lib().m3_step(C.byref(args), C.byref(st_c), C.c_void_p(y.data_ptr()),
@@ -502,21 +525,7 @@ def mamba3_step_factored_(x, b, c, dt, lam, a_log, theta, d_skip,
     """mamba3_step on the factored cache, in place (m3_step_factored);
     returns y.  Equal to mamba3_step_ on the full state it stands for."""
     args, keep = _step_args(x, b, c, dt, lam, a_log, theta, d_skip)
-    B, H, P, R = keep[0].shape
-    N = keep[1].shape[2]
-    t = state.h
-    if t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
-        raise ArgumentError("state.h must be a contiguous float32 device tensor")
-    _expect_shape(t, (B, H, P, N), "state.h")
-    for t, shape, what in ((state.x_prev, (B, H, P, R), "state.x_prev"),
-                           (state.b_prev, (B, H, N, R), "state.b_prev")):
-        if t.dtype != keep[0].dtype or not t.is_contiguous() or not t.is_cuda:
-            raise ArgumentError(f"{what} must be a contiguous {keep[0].dtype} device tensor")
-        _expect_shape(t, shape, what)
-    if theta is not None:
-        if state.angle is None:
-            raise ArgumentError("theta needs the state's angle tensor (updated in place)")
-        _expect_shape(state.angle, (B, H, N // 2), "state.angle")
+    check_step_state(keep, theta is not None, state)
     y = torch.empty_like(keep[0])
     st_c = _lib.SsmStateFactoredC(state.h.data_ptr(), state.x_prev.data_ptr(),
                                   state.b_prev.data_ptr(),

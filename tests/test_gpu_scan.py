@@ -337,6 +337,44 @@ def test_config1_full_size_split_window_property():
     assert torch.isfinite(full.y.float()).all()
 
 
+def test_config1_full_size_every_sequence_against_f64():
+    """Full config 1 (B8 L2048 H12 P64 N128, bf16, rotational with per-token
+    theta, LearnedTrapezoid, skip D) through the benchmark's chunk-parallel
+    plan, every one of the 96 sequences against the f64 recurrence: y, h,
+    last_u and the angle.  Margins are printed."""
+    from mamba3.ssm import ScanInputs, mamba3_scan
+    g = torch.Generator(device="cuda").manual_seed(11)
+    B, T, H, P, N = 8, 2048, 12, 64, 128
+    x = torch.randn(B, T, H, P, 1, device="cuda", generator=g).to(torch.bfloat16)
+    b = (torch.randn(B, T, H, N, 1, device="cuda", generator=g) / math.sqrt(N)).to(torch.bfloat16)
+    c = (torch.randn(B, T, H, N, 1, device="cuda", generator=g) / math.sqrt(N)).to(torch.bfloat16)
+    dt = torch.nn.functional.softplus(torch.randn(B, T, H, device="cuda", generator=g) - 3
+                                      ).clamp(1e-3, 0.1)
+    lam = torch.sigmoid(torch.randn(B, T, H, device="cuda", generator=g))
+    a_log = torch.rand(H, device="cuda", generator=g) * math.log(16)
+    th = (torch.rand(B, T, H, N // 2, device="cuda", generator=g) * math.pi).to(torch.bfloat16)
+    d_skip = torch.rand(H, device="cuda", generator=g) * 2 - 1
+    out = mamba3_scan(ScanInputs(x, b, c, dt, a_log, lam).with_theta(th).with_skip(d_skip)
+                      .with_state_output(True))
+    torch.cuda.synchronize()
+    hx, hb, hc, hdt, hlam, hth = (host(t) for t in (x, b, c, dt, lam, th))
+    hy, hh, hlu, hang = (host(t) for t in (out.y, out.state.h, out.state.last_u, out.state.angle))
+    worst = np.zeros(4)
+    for bb in range(B):
+        sl = lambda a: a[bb:bb + 1]
+        y64, h64, lu64, a64 = oracle.scan_recurrence_f64(sl(hx), sl(hb), sl(hc), sl(hdt),
+                                                         host(a_log), sl(hlam), sl(hth),
+                                                         d_skip=host(d_skip))
+        e = np.array([rel_l2(sl(hy), y64), rel_l2(sl(hh), h64), rel_l2(sl(hlu), lu64),
+                      angle_err(sl(hang), a64)])
+        worst = np.maximum(worst, e)
+    print(f"config 1 full size, all {B * H} sequences against f64: worst rel-L2 y {worst[0]:.2e}, "
+          f"h {worst[1]:.2e}, last_u {worst[2]:.2e} (bar {BF16_TOL:g}); angle {worst[3]:.1e}",
+          flush=True)
+    assert max(worst[:3]) <= BF16_TOL
+    assert worst[3] <= 1e-3
+
+
 def _device_rel_l2(a, b):
     """rel-L2 of two device tensors, accumulated in f64 on the device."""
     a, b = a.double(), b.double()
@@ -389,15 +427,18 @@ def test_config2_full_size_split_window_and_f64():
 
 
 # ------------------------------------------------------------------ gated scan
-@pytest.mark.parametrize("B,T,H,N,R,theta,skip,state,chunk_parallel", [
-    (2, 300, 3, 128, 1, True, True, True, True),     # chunk-parallel, rank 1: the gate in its last kernel
-    (8, 2048, 12, 128, 1, True, True, False, True),  # config 1's shape: segments of several sub-chunks
-    (1, 700, 2, 64, 1, True, False, False, True),    # d_state 64, ragged end
-    (2, 256, 2, 128, 1, False, True, False, True),   # real dynamics
-    (1, 300, 2, 128, 2, True, True, False, True),    # MIMO chunk-parallel: the gate as a second launch
-    (2, 300, 3, 128, 1, True, True, True, False),    # single pass: a second launch
+@pytest.mark.parametrize("B,T,H,N,R,theta,skip,state,chunk_parallel,extra", [
+    (2, 300, 3, 128, 1, True, True, True, True, 72),     # chunk-parallel, rank 1: the gate in its last kernel
+    # a z row of width 4 mod 8 (a fixed-lambda in_proj row): the fused gate
+    # and the composed gate's scalar kernel
+    (2, 300, 3, 128, 1, True, True, True, True, 68),
+    (8, 2048, 12, 128, 1, True, True, False, True, 72),  # config 1's shape: segments of several sub-chunks
+    (1, 700, 2, 64, 1, True, False, False, True, 72),    # d_state 64, ragged end
+    (2, 256, 2, 128, 1, False, True, False, True, 72),   # real dynamics
+    (1, 300, 2, 128, 2, True, True, False, True, 72),    # MIMO chunk-parallel: the gate as a second launch
+    (2, 300, 3, 128, 1, True, True, True, False, 72),    # single pass: a second launch
 ])
-def test_gated_scan_equals_scan_then_gate(B, T, H, N, R, theta, skip, state, chunk_parallel):
+def test_gated_scan_equals_scan_then_gate(B, T, H, N, R, theta, skip, state, chunk_parallel, extra):
     """m3_scan_gated gives m3_scan's y through m3_mixer_gate (no post-gate
     norm) bit for bit, with the same output state, on every path."""
     import ctypes as C
@@ -418,7 +459,7 @@ def test_gated_scan_equals_scan_then_gate(B, T, H, N, R, theta, skip, state, chu
                                     dev(inp["angle0"]) if theta else None))
     si = si.with_state_output(True).with_chunk_parallel(chunk_parallel)
     d = H * P * R
-    width = d + 72                       # z leads a wider row, as in the in_proj output
+    width = d + extra                    # z leads a wider row, as in the in_proj output
     proj = torch.randn(B, T, width, device="cuda:0").to(bf)
     ref = mamba3_scan(si)
     gated = torch.empty(B, T, d, dtype=bf, device="cuda:0")

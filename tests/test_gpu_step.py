@@ -337,6 +337,35 @@ def test_step_layers_rejects_mixed_shapes():
         _lib.check(_lib.lib().m3_step_layers(2, args, st, None, ys, None))
 
 
+@pytest.mark.parametrize("mismatch", ["dtype", "rank", "batch"])
+def test_step_all_checks_every_layer_state_before_any_launch(mismatch):
+    """StateCache.step_all on a factored cache (bf16, rank 1) with inputs that
+    do not fit it (f32 storage, rank 2, or a larger batch) raises before any
+    launch: the kernel would step each layer's slice at the inputs' element
+    size and shape, past the slices.  The cache is left untouched."""
+    from mamba3 import StateCache
+    from mamba3.error import ArgumentError, ShapeError
+    rng = np.random.default_rng(7)
+    layers, B, H, P, N = 3, 2, 2, 16, 32
+    cache = StateCache(layers, B, H, P, N, True, "cuda", init_std=0.1,
+                       generator=torch.Generator(device="cuda").manual_seed(1), factored=True,
+                       rank=1, dtype=torch.bfloat16)
+    before = (cache.h.clone(), cache.x_prev.clone(), cache.b_prev.clone(), cache.angle.clone())
+    R = 2 if mismatch == "rank" else 1
+    Bi = B + 1 if mismatch == "batch" else B
+    dtype = "f32" if mismatch == "dtype" else "bf16"
+    a_log = dev(np.zeros(H, np.float32))
+    inputs = []
+    for _ in range(layers):
+        x, b, c, dt, lam, th = _step_inputs(rng, Bi, H, P, N, R, True, dtype)
+        inputs.append((x, b, c, dt, lam, a_log, th, None))
+    with pytest.raises((ArgumentError, ShapeError)):
+        cache.step_all(inputs)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.h, before[0]) and torch.equal(cache.x_prev, before[1])
+    assert torch.equal(cache.b_prev, before[2]) and torch.equal(cache.angle, before[3])
+
+
 def test_state_cache_layers_are_independent():
     """infer::StateCache: stepping one layer leaves the others untouched."""
     from mamba3 import StateCache
