@@ -788,6 +788,9 @@ def main():
                     help="run one model leg alone and print its object (for kernel traces)")
     ap.add_argument("--scan-only", action="store_true",
                     help="run only the headline scan --steps times (for counter runs)")
+    ap.add_argument("--scan-path", choices=("fused", "three"), default="fused",
+                    help="the chunk-parallel scan's form for bf16 at rank 1: the fused single "
+                         "launch (the library's default) or the three launches")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="copy MIB MiB device to device --steps times and exit (the known-size "
                          "kernel that scales FETCH_SIZE / WRITE_SIZE)")
@@ -813,6 +816,7 @@ def main():
         return
     from mamba3 import _lib as L_
     lib = L_.lib()
+    L_.check(lib.m3_debug_scan_options(0 if args.scan_path == "fused" else 1, 0, 0))
 
     torch.cuda.synchronize()
     if args.only == "backward":

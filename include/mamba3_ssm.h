@@ -126,16 +126,31 @@ typedef struct m3_scan_inputs {
     const void *theta;        /* [B, T, H, N/2] or NULL (real dynamics) */
     const float *d_skip;      /* [H] or NULL */
     const m3_ssm_state *state;/* carried-in state or NULL */
-    size_t chunk_size;        /* > 0; the chunk-parallel kernels pass the state
-                               * between segments of at least this many tokens
-                               * (tiles inside a segment are the kernel's own) */
+    size_t chunk_size;        /* > 0; the three-launch chunk-parallel form passes
+                               * the state between segments of at least this many
+                               * tokens (tiles inside a segment are the kernel's
+                               * own); the fused single launch always uses
+                               * segments of 128 tokens */
     int32_t want_state;       /* ScanInputs::want_state */
     /* Device scratch for the chunk-parallel scan (no reference counterpart:
      * the reference allocates its intermediates per call): 256-byte aligned,
      * at least m3_scan_workspace_bytes() bytes.  NULL, a smaller or unaligned
      * buffer selects the single-pass kernel, which gives the same results to
      * rounding and needs no scratch.  The contents need no initialisation;
-     * calls that share a workspace must be ordered on one stream. */
+     * calls that share a workspace must be ordered on one stream.
+     *
+     * The chunk-parallel scan takes one of two forms.  The fused single
+     * launch (bf16 storage, rank 1, d_state 64 or 128, while its grid of one
+     * workgroup per 128-token segment fits three rounds of two workgroups per
+     * CU) reads every input once: each segment publishes its contribution to
+     * the state in the workspace and takes the state entering it from the
+     * segments before it by a bounded wait on their flags.  A segment whose
+     * wait gives up (about a second without an answer, which needs the GPU to
+     * stop running the earlier segments' workgroups) takes NaN as its entering
+     * state, so its outputs, those of the later segments of its sequence and
+     * the sequence's boundary state are NaN, never stale.  Results do not
+     * depend on the order in which workgroups run.  Other shapes take three
+     * launches (segment states, a state pass, segment outputs). */
     void *workspace;
     size_t workspace_bytes;
 } m3_scan_inputs;
@@ -178,9 +193,12 @@ size_t m3_scan_workspace_bytes(const m3_scan_inputs *in);
  * holds its own copy of that array from the moment the library's code object is
  * loaded on that device (the first launch of any of its kernels there) until
  * the process ends, so every process that uses the library on a GPU holds those
- * M3_NO_ALLOC_SCRATCH_MIB MiB there whether or not it calls this function.  Shapes whose workspace (m3_scan_workspace_bytes) exceeds it
- * return M3_ERR_UNSUPPORTED before any device work.  Results are those of
- * m3_scan with a caller workspace, bit for bit.  Every call on a GPU shares
+ * M3_NO_ALLOC_SCRATCH_MIB MiB there whether or not it calls this function.
+ * Where the fused launch's workspace (m3_scan_workspace_bytes) exceeds it and
+ * the three launches' fits, the three launches run (results equal to rounding);
+ * shapes whose workspace exceeds it on either form return M3_ERR_UNSUPPORTED
+ * before any device work.  Otherwise results are those of m3_scan with a
+ * caller workspace, bit for bit.  Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (different streams, or
  * different host threads without ordering) race and give wrong results.  The
  * scratch needs no clearing: the chunk-parallel kernels write every byte they
@@ -319,6 +337,17 @@ const char *m3_last_error(void);
 /* Kernel launches issued by this library since load (the reference's
  * launch counter, src/backend.rs:231-281). */
 uint64_t m3_launch_count(void);
+
+/* Test and benchmark settings of the chunk-parallel scan, process-wide.  No
+ * reference counterpart.  path 0 (the default) runs the fused single launch
+ * where it covers the shape (bf16 storage, rank 1) and the three launches
+ * elsewhere; path 1 runs the three launches everywhere (m3_scan_workspace_bytes
+ * follows the setting).  lookback_mode 1 makes every fused-launch segment after
+ * a sequence's first give up its look-back at once, as a segment does after
+ * lookback_spin unanswered polls (0: the default, about a second): its outputs,
+ * those of the sequence's later segments and the sequence's boundary state
+ * come out NaN.  Returns M3_ERR_ARGUMENT for values outside those ranges. */
+m3_status m3_debug_scan_options(int32_t path, int32_t lookback_mode, int32_t lookback_spin);
 
 /* Runs the MFMA lane-layout self test on the current device: *result is 0
  * when the layouts the kernels assume hold.  Synchronous; allocates 4 bytes. */

@@ -171,11 +171,17 @@ float m3_discretization_fixed_lambda(int32_t d) {
     return std::nanf("");
 }
 
+// Test and benchmark settings of the chunk-parallel scan (m3_debug_scan_options):
+// the form (0 the fused single launch where it covers the shape, 1 the three
+// launches) and the fused launch's look-back (give up at once; polls).
+static std::atomic<int> g_scan_path{0}, g_lb_mode{0}, g_lb_spin{0};
+
 // The scan, and with gate_z the mixer's gate on its y (in place): fused into
 // the chunk-parallel kernel where that form runs (bf16, rank 1), else the
-// gate kernel after the scan.
+// gate kernel after the scan.  path: the chunk-parallel form (-1 the setting).
 static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
-                            const void *gate_z, size_t gate_stride, void *stream) {
+                            const void *gate_z, size_t gate_stride, void *stream,
+                            int path = -1) {
     if (in == nullptr || out == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/outputs are NULL");
     if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
     if (in->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
@@ -259,6 +265,9 @@ static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
     a.last_u0 = st ? st->last_u : nullptr;
     a.angle0 = (st && in->theta) ? st->angle : nullptr;
     a.y = out->y;
+    a.path = path >= 0 ? path : g_scan_path.load(std::memory_order_relaxed);
+    a.lb_mode = g_lb_mode.load(std::memory_order_relaxed);
+    a.lb_spin = g_lb_spin.load(std::memory_order_relaxed);
     if (in->want_state) {
         a.h_out = out->state.h;
         a.last_u_out = out->state.last_u;
@@ -280,7 +289,8 @@ static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
     }
     if (chunked) {
         e = m3::launch_scan_chunked(a, in->workspace, s);
-        if (e == hipSuccess) g_launches.fetch_add(3, std::memory_order_relaxed);
+        if (e == hipSuccess)
+            g_launches.fetch_add(m3::scan_chunked_launches(a), std::memory_order_relaxed);
     } else {
         e = m3::launch_scan(a, s);
         if (e == hipSuccess) g_launches.fetch_add(1, std::memory_order_relaxed);
@@ -311,9 +321,12 @@ m3_status m3_scan_gated(const m3_scan_inputs *in, const m3_scan_output *out, con
     return scan_entry(in, out, z, z_stride, stream);
 }
 
-size_t m3_scan_workspace_bytes(const m3_scan_inputs *in) {
+}  // extern "C"
+
+static size_t workspace_bytes_for(const m3_scan_inputs *in, int path) {
     if (in == nullptr || !dtype_ok(in->dtype) || in->seq == 0) return 0;
     m3::ScanLaunch a{};
+    a.path = path;
     a.batch = in->batch;
     a.seq = in->seq;
     a.heads = in->heads;
@@ -328,6 +341,21 @@ size_t m3_scan_workspace_bytes(const m3_scan_inputs *in) {
     a.x = a.b = a.c = dummy;
     a.y = dummy;
     return m3::scan_chunked_workspace(a);
+}
+
+extern "C" {
+
+size_t m3_scan_workspace_bytes(const m3_scan_inputs *in) {
+    return workspace_bytes_for(in, g_scan_path.load(std::memory_order_relaxed));
+}
+
+m3_status m3_debug_scan_options(int32_t path, int32_t lookback_mode, int32_t lookback_spin) {
+    if (path < 0 || path > 1 || lookback_mode < 0 || lookback_mode > 1 || lookback_spin < 0)
+        return fail(M3_ERR_ARGUMENT, "scan options: path 0 or 1, look-back mode 0 or 1, spin >= 0");
+    g_scan_path.store(path, std::memory_order_relaxed);
+    g_lb_mode.store(lookback_mode, std::memory_order_relaxed);
+    g_lb_spin.store(lookback_spin, std::memory_order_relaxed);
+    return ok();
 }
 
 }  // extern "C"
@@ -381,7 +409,16 @@ m3_status m3_scan_no_alloc(const m3_scan_inputs *in, const m3_scan_output *out, 
     m3_scan_inputs local = *in;
     local.workspace = nullptr;
     local.workspace_bytes = 0;
-    const size_t need = m3_scan_workspace_bytes(&local);
+    int path = g_scan_path.load(std::memory_order_relaxed);
+    size_t need = workspace_bytes_for(&local, path);
+    if (need > kNoAllocScratchBytes && path == 0) {
+        // the fused launch's records do not fit: the three launches' may
+        const size_t three = workspace_bytes_for(&local, 1);
+        if (three <= kNoAllocScratchBytes) {
+            path = 1;
+            need = three;
+        }
+    }
     if (need > kNoAllocScratchBytes)
         return fail(M3_ERR_UNSUPPORTED,
                     "this scan needs %zu bytes of scratch; m3_scan_no_alloc's static scratch holds "
@@ -393,7 +430,7 @@ m3_status m3_scan_no_alloc(const m3_scan_inputs *in, const m3_scan_output *out, 
         local.workspace = p;
         local.workspace_bytes = kNoAllocScratchBytes;
     }
-    return m3_scan(&local, out, stream);
+    return scan_entry(&local, out, nullptr, 0, stream, path);
 }
 
 static m3::ScanLaunch scan_launch_of(const m3_scan_inputs *in) {

@@ -94,6 +94,12 @@ struct ScanLaunch {
     // the caller's chunk_size (tokens; 0 = 64): the chunk-parallel path passes
     // the state between segments of at least this many tokens
     size_t chunk_size;
+    // chunk-parallel form: 0 the fused single launch where it covers the
+    // shape (bf16, rank 1), 1 the three launches
+    int path;
+    // the fused launch's look-back: lb_mode 1 gives up at once (tests);
+    // lb_spin polls of one flag before giving up (0: the default)
+    int lb_mode, lb_spin;
 };
 hipError_t launch_scan(const ScanLaunch &a, hipStream_t stream);
 // The specialised kernel (head_dim 64, d_state 64/128, rank 1/2/4, 16-byte
@@ -106,6 +112,10 @@ hipError_t launch_scan_fast(const ScanLaunch &a, hipStream_t stream);
 // and the launch.
 size_t scan_chunked_workspace(const ScanLaunch &a);
 hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream);
+// Kernel launches the chunk-parallel form makes for these inputs: 1 for the
+// fused single launch (bf16, rank 1, up to three rounds of its workgroups), 3
+// otherwise.
+int scan_chunked_launches(const ScanLaunch &a);
 // Rows (token, rank) per chunk of the backward: 32, or 64 for bf16 storage
 // with d_state 64 (whose 16-byte staging needs the longer chunk).
 inline int scan_backward_rows(const ScanLaunch &a) { return (a.bf16 && a.d_state == 64) ? 64 : 32; }

@@ -37,6 +37,8 @@
 // over every segment of every sequence; the sequential pass is a few FMAs per
 // element and streams U from HBM.  Segments of several sub-chunks keep the U
 // and S records (and the state pass) small while still filling the chip.
+#include <atomic>
+#include <chrono>
 #include <type_traits>
 
 #include "scan_common.hpp"
@@ -1653,6 +1655,894 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     }   // sub-chunks
 }
 
+// ================================================================ fused single launch
+// The whole scan in one launch that reads its inputs once.  One workgroup per
+// segment of at most two sub-chunks (KS rows of 64 tokens), in three steps:
+//   1. local pass: chunk_scan's stage, band, carry-in and advance over the
+//      segment's sub-chunks starting from a zero state, in the segment's own
+//      frame.  This yields y_local (kept in registers), C~ of every sub-chunk
+//      (kept in LDS) and the segment's contribution U (the local state at its
+//      end), decay e and angle total Phi (scan.rs:207-251 over the segment).
+//   2. the state entering the segment, S_j, by a decoupled look-back: the
+//      workgroup publishes (U, e, Phi) as its aggregate, then walks back
+//      over the segments before it to the nearest one that has published
+//      its inclusive state and applies S_{m+1} = R(Phi_m) (e_m S_m + U_m)
+//      forward from there.  Every step is the same f32 arithmetic on the same
+//      values whichever segment performs it, so S_j does not depend on the
+//      order in which workgroups ran.  It publishes S_{j+1}.
+//   3. y = y_local + decay(t) C~_t . S_j for every token (the carry-in of the
+//      entering state, scan.rs:253-263), stored once; the last segment writes
+//      the boundary state (scan.rs:270-288, 599-638).
+// So B, C, x, theta, dt and lambda are read from HBM once and B and C are
+// rotated once; the records of a segment are 16 KB of U (bf16), 32 KB of the
+// inclusive state (f32) and a few hundred bytes of scalars.
+//
+// Records move through device-coherent (sc1) buffer loads and stores; a
+// record is written, the writer waits for its stores (vmcnt(0)), the
+// workgroup synchronises, and then one thread stores the segment's flag
+// (epoch << 2 | state, a relaxed device-scope atomic).  A reader polls the
+// flag and reads the record after it.  Every wait is bounded (lb_spin polls
+// with a sleep between them); a workgroup that gives up takes S_j = NaN, so
+// its outputs and every later segment of the sequence come out NaN, never
+// stale.  Workgroups are numbered segment-major, so a segment's predecessor
+// was dispatched before it on the same XCD; the bound covers any other order.
+constexpr uint64_t kFlagAgg = 1, kFlagInc = 2;
+constexpr int kCoh = 16;   // buffer cache policy sc1: coherent across the device
+
+struct FusedWs {
+    unsigned long long *flag;   // [segments] epoch << 2 | state
+    __bf16 *u;                  // [segments][wave][n-tile][lane][4]: U in the rec_off layout
+    float *eda;                 // [segments] decay of the segment
+    float *phi, *cph, *sph;     // [segments][N/2] angle total (wrapped), cos, sin
+    float *inc;                 // [segments][wave][f][half][lane][4]: S after the segment (f32)
+    float *incphi;              // [segments][N/2] angle after the segment, from the sequence start
+    size_t u_bytes, inc_bytes;
+};
+
+struct FusedLayout {
+    size_t flag, u, eda, phi, cph, sph, inc, incphi, total;
+};
+
+FusedLayout fused_layout(size_t segs, size_t n) {
+    FusedLayout l;
+    size_t o = 0;
+    l.flag = o;
+    o = align256(o + segs * 8);
+    l.u = o;
+    o = align256(o + segs * kP * n * 2);
+    l.eda = o;
+    o = align256(o + segs * 4);
+    l.phi = o;
+    o = align256(o + segs * (n / 2) * 4);
+    l.cph = o;
+    o = align256(o + segs * (n / 2) * 4);
+    l.sph = o;
+    o = align256(o + segs * (n / 2) * 4);
+    l.inc = o;
+    o = align256(o + segs * kP * n * 4);
+    l.incphi = o;
+    o = align256(o + segs * (n / 2) * 4);
+    l.total = o;
+    return l;
+}
+
+FusedWs fused_ws(char *base, const FusedLayout &l, size_t segs, size_t n) {
+    FusedWs w;
+    w.flag = reinterpret_cast<unsigned long long *>(base + l.flag);
+    w.u = reinterpret_cast<__bf16 *>(base + l.u);
+    w.eda = reinterpret_cast<float *>(base + l.eda);
+    w.phi = reinterpret_cast<float *>(base + l.phi);
+    w.cph = reinterpret_cast<float *>(base + l.cph);
+    w.sph = reinterpret_cast<float *>(base + l.sph);
+    w.inc = reinterpret_cast<float *>(base + l.inc);
+    w.incphi = reinterpret_cast<float *>(base + l.incphi);
+    w.u_bytes = segs * kP * n * 2;
+    w.inc_bytes = segs * kP * n * 4;
+    return w;
+}
+
+// One step of the state chain for a lane's four pairs (lo: n, hi: n + N/2):
+// S' = R(phi) (e S + U), R(phi) (v1, v2) = (v1 cos - v2 sin, v1 sin + v2 cos),
+// with explicit fused multiply-adds so that every caller rounds alike.
+__device__ __forceinline__ void chain_step(f32x4 &lo, f32x4 &hi, float e, const f32x4 &ulo,
+                                           const f32x4 &uhi, const f32x4 &cs, const f32x4 &sn) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float l = __builtin_fmaf(lo[r], e, ulo[r]);
+        const float h = __builtin_fmaf(hi[r], e, uhi[r]);
+        lo[r] = __builtin_fmaf(l, cs[r], -(h * sn[r]));
+        hi[r] = __builtin_fmaf(l, sn[r], h * cs[r]);
+    }
+}
+
+__device__ __forceinline__ f32x4 cld16f(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoh));
+}
+__device__ __forceinline__ void cst16f(rsrc_t r, uint32_t off, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kCoh);
+}
+
+template <int N>
+struct FusedSmem {
+    static constexpr int CB = N / 8, CT = N / 16, CX = kP / 8;   // chunks a row
+    static constexpr int LDM = 64 + 8;                           // band row stride
+    unsigned char b[64 * CB * 16];       // B, then B~ [t][n]
+    unsigned char c[2][64 * CB * 16];    // C, then C~ [t][n], of each sub-chunk (kept)
+    unsigned char th[64 * CT * 16];      // theta [t][pair]
+    unsigned char x[64 * CX * 16];       // X [t][p]
+    __bf16 band[64 * LDM];               // (C~ B~^T o L)[t][s]
+    float sc[2][4][64];                  // dt, lambda, next dt, next lambda
+    float acum[2][64];                   // decay prefix (log2 units) of each sub-chunk
+    float gw[64], ww[64], wdv[64];
+    float ang[N / 2];                    // the segment's angle total per pair (turns, then radians)
+    float cph[N / 2], sph[N / 2];        // its cosine and sine
+    float phc[N / 2];                    // the angle entering / leaving the segment from the sequence start
+    int lb[2];                           // look-back: nearest inclusive segment, gave up
+};
+
+// The part of the fused launch after its local pass: the segment's
+// aggregate, the look-back for the state entering it, its inclusive state,
+// y with the entering state's part, and the boundary state: KS sub-chunks of
+// QT tokens (NT 16-row tiles) per segment, C~ of each in sm.c[h] (rows of RB bytes, the rsw<RB/16>
+// permutation), the decay prefix of each in sm.acum[h], y_local in ykeep;
+// sm.ang holds the segment's angle total per pair in turns.
+template <int N, int KS, int QT, bool GATE, typename Sm>
+__device__ __forceinline__ void fused_tail(const ScanLaunch &a, const FusedWs &ws, Sm &sm,
+                                           f32x4 (&sacc)[N / 32][2], f32x4 (&ykeep)[KS][QT / 16],
+                                           const float (&eprod)[KS], float eacc, int k0, int h_end,
+                                           int seg, int nseg, size_t bh, size_t bhs, const SeqBufs &rs,
+                                           uint64_t epoch, int lb_mode, int lb_spin) {
+    constexpr int P = kP;
+    constexpr int NH = N / 2;
+    constexpr int NT = QT / 16;
+    constexpr int NF = N / 32;
+    constexpr int NTN = N / 16;
+    constexpr int CB = N / 8;
+    constexpr int RB = CB * 16;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const size_t H = a.heads, L = a.seq;
+    const size_t bb = bh / H, hh = bh % H;
+    // ---- the segment's aggregate: U (rounded to bf16, the record's values),
+    //      its decay, and per pair its wrapped angle total with cos and sin
+    const int lg = lane >> 4, lc = lane & 15;
+    const size_t urec = (bhs * 4 + wave) * NTN * 256;
+    const rsrc_t ru = make_rsrc(ws.u, static_cast<uint32_t>(ws.u_bytes));
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        bf16x8 q;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            q[r] = static_cast<__bf16>(sacc[f][0][r]);
+            q[4 + r] = static_cast<__bf16>(sacc[f][1][r]);
+        }
+        if (seg > 0)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, q), ru,
+                                                   static_cast<uint32_t>((urec + rec_off<NTN>(f, lane)) * 2), 0, kCoh);
+    }
+    __syncthreads();   // sm.ang holds every pair's angle total in turns
+    if (tid < NH) {
+        const float tot = a.theta != nullptr ? sm.ang[tid] * 6.28318530717958647692f : 0.0f;
+        float ts = 0.0f, tc = 1.0f;
+        if (a.theta != nullptr) sincosf(tot, &ts, &tc);
+        sm.ang[tid] = tot;
+        sm.cph[tid] = tc;
+        sm.sph[tid] = ts;
+        if (seg > 0) {
+            __hip_atomic_store(&ws.phi[bhs * NH + tid], tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&ws.cph[bhs * NH + tid], tc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&ws.sph[bhs * NH + tid], ts, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (seg > 0 && tid == 0)
+        __hip_atomic_store(&ws.eda[bhs], eacc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());   // the record's stores are done
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (seg > 0 && tid == 0)
+        __hip_atomic_store(&ws.flag[bhs], (epoch << 2) | kFlagAgg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- the state entering the segment, S_j (in its frame), and the angle
+    //      entering it from the sequence start
+    f32x4 slo[NF], shi[NF];
+    const size_t seq0 = bh * nseg;   // record index of segment 0 of this sequence
+    const rsrc_t rinc = make_rsrc(ws.inc, static_cast<uint32_t>(ws.inc_bytes));
+    auto inc_off = [&](size_t rec, int f, int q) {
+        return static_cast<uint32_t>(((((rec * 4 + wave) * NF + f) * 2 + q) * 64 + lane) * 16);
+    };
+    const int p = 16 * wave + lc;
+    if (seg == 0) {
+        // S_0 = R(angle0) (h0 + (1 - lambda_0) dt_0 last_u0)   (scan.rs:521-535)
+        const float *h0 = a.mode_raw ? a.h0 : a.init_state;
+        const float *l0 = a.mode_raw ? a.last_u0 : nullptr;
+        float first = 0.0f;
+        if (h0 != nullptr && l0 != nullptr) {
+            const size_t i0s = (bb * L) * H + hh;
+            first = (1.0f - a.lambda[i0s]) * a.dt[i0s];
+        }
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const int nlo = 16 * f + 4 * lg;
+            f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
+            if (h0 != nullptr) {
+                const size_t sb = (bh * P + p) * N;
+                lo = *reinterpret_cast<const f32x4 *>(h0 + sb + nlo);
+                hi = *reinterpret_cast<const f32x4 *>(h0 + sb + nlo + NH);
+                if (l0 != nullptr) {
+                    lo += *reinterpret_cast<const f32x4 *>(l0 + sb + nlo) * first;
+                    hi += *reinterpret_cast<const f32x4 *>(l0 + sb + nlo + NH) * first;
+                }
+            }
+            if (a.theta != nullptr && a.angle0 != nullptr) {
+                const f32x4 ph = *reinterpret_cast<const f32x4 *>(a.angle0 + bh * NH + nlo);
+                f32x4 cs, sn;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float s1, c1;
+                    sincosf(ph[r], &s1, &c1);
+                    sn[r] = s1;
+                    cs[r] = c1;
+                }
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                chain_step(lo, hi, 1.0f, z, z, cs, sn);
+            }
+            slo[f] = lo;
+            shi[f] = hi;
+        }
+        if (tid < NH)
+            sm.phc[tid] = (a.theta != nullptr && a.angle0 != nullptr) ? a.angle0[bh * NH + tid] : 0.0f;
+        __syncthreads();
+    } else {
+        if (wave == 0) {
+            // the look-back, all at once: lane l reads the flag of segment
+            // seg - 1 - l; the walk ends at the nearest segment with an
+            // inclusive state once every segment after it has published its
+            // aggregate (the first segment of a sequence publishes an
+            // inclusive state, and a segment's inclusive state never waits
+            // for a later one, so the condition is eventually met)
+            int kinc = -1;
+            int gave = lb_mode != 0 ? 1 : 0;
+            const int back = min(seg, 64);
+            int n = 0;
+            while (!gave) {
+                unsigned long long v = 0;
+                if (lane < back)
+                    v = __hip_atomic_load(&ws.flag[seq0 + seg - 1 - lane], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+                const bool cur = lane < back && (v >> 2) == epoch;
+                const uint64_t inc = __ballot(cur && (v & 3) == kFlagInc);
+                const uint64_t ready = __ballot(cur && (v & 3) != 0);
+                if (inc != 0) {
+                    const int l = __builtin_ctzll(inc);   // nearest inclusive state
+                    const uint64_t need = (l == 63) ? ~0ull : ((2ull << l) - 1);
+                    if ((ready & need) == need) {
+                        kinc = seg - 1 - l;
+                        break;
+                    }
+                }
+                if (++n > lb_spin) {
+                    gave = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            if (lane == 0) {
+                sm.lb[0] = kinc;
+                sm.lb[1] = gave;
+            }
+        }
+        __syncthreads();
+        const int kinc = sm.lb[0];
+        const bool gave = sm.lb[1] != 0;
+        if (gave) {
+            const float qnan = __builtin_nanf("");
+#pragma unroll
+            for (int f = 0; f < NF; ++f) slo[f] = shi[f] = f32x4{qnan, qnan, qnan, qnan};
+            if (tid < NH) sm.phc[tid] = qnan;
+        } else {
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                slo[f] = cld16f(rinc, inc_off(seq0 + kinc, f, 0));
+                shi[f] = cld16f(rinc, inc_off(seq0 + kinc, f, 1));
+            }
+            float phc = 0.0f;
+            if (tid < NH)
+                phc = __hip_atomic_load(&ws.incphi[(seq0 + kinc) * NH + tid], __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+            // fold forward through the aggregates of segments kinc + 1 .. seg
+            // - 1, two at a time: their scalars through LDS (the band region,
+            // dead by now), every load of a pair of steps issued before its use
+            float *fsc = reinterpret_cast<float *>(sm.band);   // [2][e | phi, cos, sin x NH]
+            constexpr int FS = 1 + 3 * NH;
+            for (int m0 = kinc + 1; m0 < seg; m0 += 2) {
+                const int nm = min(2, seg - m0);
+                __syncthreads();   // the previous pair's scalars are read
+                for (int i = tid; i < nm * FS; i += kThreads) {
+                    const int st = i / FS, w = i % FS;
+                    const size_t rec = seq0 + m0 + st;
+                    float v;
+                    if (w == 0)
+                        v = __hip_atomic_load(&ws.eda[rec], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    else if (w <= NH)
+                        v = __hip_atomic_load(&ws.phi[rec * NH + (w - 1)], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                    else if (w <= 2 * NH)
+                        v = __hip_atomic_load(&ws.cph[rec * NH + (w - 1 - NH)], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                    else
+                        v = __hip_atomic_load(&ws.sph[rec * NH + (w - 1 - 2 * NH)], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                    fsc[i] = v;
+                }
+                bf16x8 uq[2][NF];
+#pragma unroll
+                for (int st = 0; st < 2; ++st)
+                    if (st < nm) {
+                        const size_t rec = seq0 + m0 + st;
+#pragma unroll
+                        for (int f = 0; f < NF; ++f) {
+                            const uint32_t uo =
+                                static_cast<uint32_t>(((rec * 4 + wave) * NTN * 256 + rec_off<NTN>(f, lane)) * 2);
+                            uq[st][f] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ru, uo, 0, kCoh));
+                        }
+                    }
+                __syncthreads();   // the pair's scalars are in LDS
+#pragma unroll
+                for (int st = 0; st < 2; ++st)
+                    if (st < nm) {
+                        const float *sc = fsc + st * FS;
+#pragma unroll
+                        for (int f = 0; f < NF; ++f) {
+                            f32x4 ul, uh, cs, sn;
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                ul[r] = static_cast<float>(uq[st][f][r]);
+                                uh[r] = static_cast<float>(uq[st][f][4 + r]);
+                                cs[r] = sc[1 + NH + 16 * f + 4 * lg + r];
+                                sn[r] = sc[1 + 2 * NH + 16 * f + 4 * lg + r];
+                            }
+                            chain_step(slo[f], shi[f], sc[0], ul, uh, cs, sn);
+                        }
+                        if (tid < NH) phc = wrap_angle(phc + sc[1 + tid]);
+                    }
+            }
+            if (tid < NH) sm.phc[tid] = phc;
+        }
+        __syncthreads();
+    }
+
+    // ---- publish the state after the segment: S_{j+1} = R(Phi_j) (e_j S_j + U_j),
+    //      U rounded to bf16 as its record holds it; after the last segment
+    //      the boundary state (scan.rs:270-288, 599-638)
+    float phe = 0.0f;   // the angle after the segment (pair tid)
+    if (tid < NH) {
+        phe = wrap_angle(sm.phc[tid] + sm.ang[tid]);
+        __hip_atomic_store(&ws.incphi[bhs * NH + tid], phe, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const bool last_seg = seg == nseg - 1;
+    if (last_seg) {
+        __syncthreads();   // every pair's angle entering the segment is read
+        if (tid < NH) sm.phc[tid] = phe;
+        __syncthreads();
+    }
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        f32x4 olo = slo[f], ohi = shi[f], ul, uh, cs, sn;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            ul[r] = static_cast<float>(static_cast<__bf16>(sacc[f][0][r]));
+            uh[r] = static_cast<float>(static_cast<__bf16>(sacc[f][1][r]));
+            cs[r] = sm.cph[16 * f + 4 * lg + r];
+            sn[r] = sm.sph[16 * f + 4 * lg + r];
+        }
+        chain_step(olo, ohi, eacc, ul, uh, cs, sn);
+        cst16f(rinc, inc_off(bhs, f, 0), olo);
+        cst16f(rinc, inc_off(bhs, f, 1), ohi);
+        if (last_seg) {
+            const size_t sb = (bh * P + p) * N;
+            const int nlo = 16 * f + 4 * lg;
+            f32x4 ce, se;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (a.theta != nullptr) {
+                    float s1, c1;
+                    sincosf(sm.phc[nlo + r], &s1, &c1);
+                    se[r] = s1;
+                    ce[r] = c1;
+                } else {
+                    se[r] = 0.0f;
+                    ce[r] = 1.0f;
+                }
+            }
+            if (a.h_out != nullptr) {
+                f32x4 hl, hh2;   // R(-phi_end) S
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    hl[r] = __builtin_fmaf(olo[r], ce[r], ohi[r] * se[r]);
+                    hh2[r] = __builtin_fmaf(ohi[r], ce[r], -(olo[r] * se[r]));
+                }
+                *reinterpret_cast<f32x4 *>(a.h_out + sb + nlo) = hl;
+                *reinterpret_cast<f32x4 *>(a.h_out + sb + nlo + NH) = hh2;
+            }
+            if (a.last_u_out != nullptr) {
+                // last_u = x_{L-1} B~_{L-1}^T with B~ = R(-phi_end) B  (scan.rs:599-618)
+                const size_t tl = (bb * L + (L - 1)) * H + hh;
+                const bf16_t *bp = static_cast<const bf16_t *>(a.b) + tl * N;
+                const float xv = to_f32(static_cast<const bf16_t *>(a.x)[tl * P + p]);
+                f32x4 ulu, uhu;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float b1 = to_f32(bp[nlo + r]);
+                    const float b2 = to_f32(bp[nlo + r + NH]);
+                    ulu[r] = xv * (b1 * ce[r] + b2 * se[r]);
+                    uhu[r] = xv * (-b1 * se[r] + b2 * ce[r]);
+                }
+                *reinterpret_cast<f32x4 *>(a.last_u_out + sb + nlo) = ulu;
+                *reinterpret_cast<f32x4 *>(a.last_u_out + sb + nlo + NH) = uhu;
+            }
+        }
+    }
+    if (last_seg && a.angle_out != nullptr && tid < NH) a.angle_out[bh * NH + tid] = phe;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0)
+        __hip_atomic_store(&ws.flag[bhs], (epoch << 2) | kFlagInc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- y = y_local + decay(t) C~_t . S_j, stored (or gated) once
+    {
+        const int g = lg, c = lc;
+        const int sw = rsw<CB>(c);
+        const int crow = c * RB;
+        bf16x8 sf[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sf[f][r] = static_cast<__bf16>(slo[f][r]);
+                sf[f][4 + r] = static_cast<__bf16>(shi[f][r]);
+            }
+        const int zc = ((g >> 1) ^ sw) << 4;
+        const int cbase = crow + (g & 1) * 8;
+        const rsrc_t rz =
+            GATE ? make_rsrc(static_cast<const char *>(a.gate_z) + (bb * L * a.gate_stride + hh * P) * 2,
+                             static_cast<uint32_t>((L * a.gate_stride - hh * P) * 2))
+                 : make_rsrc(a.x, 0u);
+        const uint32_t zs = GATE ? static_cast<uint32_t>(a.gate_stride * 2) : 0u;
+#pragma unroll
+        for (int h = 0; h < KS; ++h) {
+            if (h >= h_end) break;
+            const unsigned char *const cth = sm.c[h];
+            const uint32_t tok0 = static_cast<uint32_t>(k0 + h) * QT;
+            f32x4 yc[NT];
+#pragma unroll
+            for (int tj = 0; tj < NT; ++tj) yc[tj] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const int olo2 = (((2 * f) << 4) ^ zc) + cbase;
+                const int ohi2 = (((2 * (f + NF)) << 4) ^ zc) + cbase;
+#pragma unroll
+                for (int tj = 0; tj < NT; ++tj) {
+                    typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
+                    const bf16x4v lo = *reinterpret_cast<const bf16x4v *>(cth + tj * 16 * RB + olo2);
+                    const bf16x4v hi = *reinterpret_cast<const bf16x4v *>(cth + tj * 16 * RB + ohi2);
+                    const bf16x8 cv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    yc[tj] = mfma_bf16(sf[f], cv, yc[tj]);
+                }
+            }
+#pragma unroll
+            for (int tj = 0; tj < NT; ++tj) {
+                const int t = 16 * tj + c;
+                const f32x4 yl = ykeep[h][tj];
+                const float dec = dexp2(sm.acum[h][t]) * eprod[h];
+                f32x4 yv;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) yv[r] = __builtin_fmaf(yc[tj][r], dec, yl[r]);
+                const uint32_t oy = (tok0 + t) * rs.tok_x + (16 * wave + 4 * g) * 2;
+                u32x2 pk;
+                pk[0] = pk_bf16(yv[0], yv[1]);
+                pk[1] = pk_bf16(yv[2], yv[3]);
+                if constexpr (GATE) {
+                    // the gate: bf16(y) * silu(z)   (the rounding of mixer_gate_vec_kernel)
+                    const u32x2 zw = bld8(rz, (tok0 + t) * zs + (16 * wave + 4 * g) * 2);
+                    float v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t yw = pk[r >> 1], zz = zw[r >> 1];
+                        const float y1 = __uint_as_float((r & 1) ? (yw & 0xFFFF0000u) : (yw << 16));
+                        const float z1 = __uint_as_float((r & 1) ? (zz & 0xFFFF0000u) : (zz << 16));
+                        v[r] = y1 * mixm::silu_fast(z1);
+                    }
+                    pk[0] = pk_bf16(v[0], v[1]);
+                    pk[1] = pk_bf16(v[2], v[3]);
+                }
+                bst8(pk, rs.y, oy);
+            }
+        }
+    }
+
+}
+
+template <int N, bool GATE>
+__global__ void __launch_bounds__(kThreads, 2)
+chunk_scan_fused_kernel(ScanLaunch a, FusedWs ws, int nsub, int kseg, int nseg, uint64_t epoch,
+                        int lb_mode, int lb_spin) {
+    constexpr int P = kP;
+    using G = Geo<bf16_t, N, P, 1, 64, 4>;
+    using S = FusedSmem<N>;
+    constexpr int CB = S::CB, CT = S::CT, CX = S::CX, LDM = S::LDM;
+    constexpr int QT = G::QT, NH = G::NH, PPL = G::PPL, PW = G::PW;
+    constexpr int NT = 4;             // 16-row tiles of a sub-chunk
+    constexpr int NF = N / 32;        // state k-blocks (a pair's halves side by side)
+    constexpr int NTN = N / 16;
+    constexpr int HV = PW / 8;
+    constexpr int RB = CB * 16;       // bytes a row of the B / C tiles
+    static_assert(G::SUBS == 1 && QT == 64 && PPL == PW, "lane = token, one segment a wave");
+    static_assert(CB % 4 == 0 && CT % 4 == 0 && CX % 4 == 0, "row loads spread over four waves");
+    // load instructions a wave issues: a B or C tile, theta, X, one scalar
+    constexpr int kBC = CB / 4, kT = CT / 4, kX = CX / 4;
+
+    __shared__ __attribute__((aligned(16))) S sm;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    const size_t H = a.heads, L = a.seq;
+    // segment-major numbering: workgroup seg * (B H) + bh
+    const size_t nbh = a.batch * a.heads;
+    const int seg = static_cast<int>(blockIdx.x / nbh);
+    const size_t bh = blockIdx.x % nbh;
+    const size_t bhs = bh * nseg + seg;             // record index
+    const size_t bb = bh / H, hh = bh % H;
+    const SeqBufs rs = seq_bufs<bf16_t, N, P, 1>(a, bb, hh);
+    const int k0 = seg * kseg;
+    const int h_end = min(kseg, nsub - k0);
+    const bool two = h_end > 1;
+
+    float A = 0.0f;
+    if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);
+    const float dskip = a.d_skip ? a.d_skip[hh] : 0.0f;
+    float run[PPL];   // wave-uniform running pair angles, in turns (pair_turns)
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) run[j] = 0.0f;
+
+    auto load_c = [&](int k, int slot) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < kBC; ++q)
+            lds_load_rows<CB>(rs.c, tok0 * rs.tok_bc, rs.tok_bc, sm.c[slot], wave + 4 * q, lane);
+    };
+    auto load_b = [&](int k) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < kBC; ++q)
+            lds_load_rows<CB>(rs.b, tok0 * rs.tok_bc, rs.tok_bc, sm.b, wave + 4 * q, lane);
+    };
+    auto load_t = [&](int k) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < kT; ++q)
+            lds_load_rows<CT>(rs.th, tok0 * rs.tok_th, rs.tok_th, sm.th, wave + 4 * q, lane);
+    };
+    auto load_x = [&](int k) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < kX; ++q)
+            lds_load_rows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.x, wave + 4 * q, lane);
+    };
+    // scalar `wave` of every token of sub-chunk k: s0, s1 at the token, s2, s3 at the next
+    auto load_s = [&](int k, int slot) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+        const uint32_t dst = lds_addr(&sm.sc[slot][wave][0]);
+        const uint32_t o0 = (tok0 + lane) * rs.tok_s, o1 = (tok0 + rs.nxt_s + lane) * rs.tok_s;
+        switch (wave) {   // a uniform branch per resource
+        case 0: lds_dma4(rs.s0, dst, o0); break;
+        case 1: lds_dma4(rs.s1, dst, o0); break;
+        case 2: lds_dma4(rs.s2, dst, o1); break;
+        default: lds_dma4(rs.s3, dst, o1); break;
+        }
+    };
+
+    // local state (from zero) in the carry-in operand layout: sacc[f][q] is
+    // n-tile f + q NF, n = 16 (f + q NF) + 4 g + r, p = 16 wave + c
+    f32x4 sacc[NF][2];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) sacc[f][0] = sacc[f][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 ykeep[2][NT];               // y of each sub-chunk before the entering state's part
+    float eprod[2] = {1.0f, 1.0f};    // decay from the segment start to each sub-chunk's start
+    float eacc = 1.0f;
+
+    // prologue: C, scalars, B, theta, X of the first sub-chunk; C and the scalars of the second
+    load_c(k0, 0);
+    load_s(k0, 0);
+    load_b(k0);
+    load_t(k0);
+    load_x(k0);
+    if (two) {
+        load_c(k0 + 1, 1);
+        load_s(k0 + 1, 1);
+    }
+
+    // ---- the local pass over the segment's sub-chunks
+#pragma unroll 1
+    for (int h = 0; h < h_end; ++h) {
+    int lane_v = lane;
+    asm volatile("" : "+v"(lane_v));
+    const int lane = lane_v;
+    const int g = lane >> 4;
+    const int c = lane & 15;
+    const int sck = k0 + h;
+    const uint32_t tok0 = static_cast<uint32_t>(sck) * QT;
+    const bool more = h + 1 < h_end;
+    const int sw = rsw<CB>(c);
+    const int crow = c * RB;
+    unsigned char *const cth = sm.c[h];
+
+    // C, the scalars, B and theta of this sub-chunk landed (X and later ones may be out)
+    if (h == 0) {
+        if (two)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm<kX + kBC + 1>());
+        else
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm<kX>());
+    } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm<kX>());
+    }
+    __syncthreads();
+
+    TokScalars sc;
+    sc.s0 = sm.sc[h][0][lane];
+    sc.s1 = sm.sc[h][1][lane];
+    sc.s2 = sm.sc[h][2][lane];
+    sc.s3 = sm.sc[h][3][lane];
+    const bool live = tok0 + lane < L;
+    float av, gv, wv;
+    token_scalars(a, sc, A, live, av, gv, wv);
+    const float acum = seg_scan<64>(av);
+    if (wave == 0) {
+        sm.acum[h][lane] = acum * kLog2e;
+        sm.gw[lane] = gv;
+        sm.ww[lane] = wv;
+        const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
+        sm.wdv[lane] = dexp<true>(last - acum) * wv;
+    }
+    const float dtt = live ? sc.s0 * 0.15915494309189533577f : 0.0f;
+
+    // ---- stage: the angle within the segment, B and C rotated by its negative
+    {
+        const int i0 = wave * PW;
+        u32x4 th[HV];
+#pragma unroll
+        for (int v = 0; v < HV; ++v)
+            th[v] = *reinterpret_cast<const u32x4 *>(sm.th + rtile_off<CT>(lane, i0 + 8 * v));
+#pragma unroll
+        for (int v = 0; v < HV; ++v) {
+            u32x4 bv[2], cv[2], bo[2], co[2];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                bv[hf] = *reinterpret_cast<const u32x4 *>(sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v));
+                cv[hf] = *reinterpret_cast<const u32x4 *>(cth + rtile_off<CB>(lane, hf * NH + i0 + 8 * v));
+            }
+#pragma unroll
+            for (int q = 0; q < 8; q += 4) {
+                float pre[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) pre[jj] = dtt * elem<bf16_t>(th, 8 * v + q + jj);
+                seg_scan4<64>(pre[0], pre[1], pre[2], pre[3]);
+#pragma unroll
+                for (int jj = 0; jj < 4; jj += 2) {
+                    float ob[2][2], oc[2][2];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int e = q + jj + u;
+                        const float w = pair_turns(pre[jj + u], run[8 * v + e]);
+                        const float sn = __builtin_amdgcn_sinf(w);
+                        const float cs = __builtin_amdgcn_cosf(w);
+                        const float b1 = elem<bf16_t>(bv, e), b2 = elem<bf16_t>(bv + 1, e);
+                        const float c1 = elem<bf16_t>(cv, e), c2 = elem<bf16_t>(cv + 1, e);
+                        ob[0][u] = b1 * cs + b2 * sn;
+                        ob[1][u] = -b1 * sn + b2 * cs;
+                        oc[0][u] = c1 * cs + c2 * sn;
+                        oc[1][u] = -c1 * sn + c2 * cs;
+                    }
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) {
+                        bo[hf][(q + jj) >> 1] = pk_bf16(ob[hf][0], ob[hf][1]);
+                        co[hf][(q + jj) >> 1] = pk_bf16(oc[hf][0], oc[hf][1]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                *reinterpret_cast<u32x4 *>(sm.b + rtile_off<CB>(lane, hf * NH + i0 + 8 * v)) = bo[hf];
+                *reinterpret_cast<u32x4 *>(cth + rtile_off<CB>(lane, hf * NH + i0 + 8 * v)) = co[hf];
+            }
+        }
+    }
+    __syncthreads();   // B~, C~ complete; theta is dead
+    if (more) load_t(sck + 1);
+
+    // ---- masked band (C~ B~^T o L)[t][s], D on the diagonal (scan.rs:593-597)
+    {
+        const int zg = (g ^ sw) << 4;
+        const int mrow = c * (LDM * 2) + 8 * g;
+        const float *acs = sm.acum[h];
+        auto tile = [&](auto tj_c, auto si_c) {
+            constexpr int TJ = decltype(tj_c)::value, SI = decltype(si_c)::value;
+            __bf16 *const dst = reinterpret_cast<__bf16 *>(reinterpret_cast<unsigned char *>(sm.band) +
+                                                           mrow + TJ * 16 * LDM * 2 + SI * 32);
+            if constexpr (SI > TJ) {
+                const float z[4] = {0.f, 0.f, 0.f, 0.f};
+                st4(dst, z);
+            } else {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kb = 0; kb < N / 32; ++kb) {
+                    const int o = ((kb << 6) ^ zg) + crow;
+                    const bf16x8 av8 = *reinterpret_cast<const bf16x8 *>(sm.b + SI * 16 * RB + o);
+                    const bf16x8 bv8 = *reinterpret_cast<const bf16x8 *>(cth + TJ * 16 * RB + o);
+                    acc = mfma_bf16(av8, bv8, acc);
+                }
+                const float at = acs[16 * TJ + c];
+                const f32x4 as = *reinterpret_cast<const f32x4 *>(&acs[16 * SI + 4 * g]);
+                const f32x4 ws4 = *reinterpret_cast<const f32x4 *>(&sm.ww[16 * SI + 4 * g]);
+                float vals[4];
+                if constexpr (SI < TJ) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) vals[r] = acc[r] * ws4[r] * dexp2(at - as[r]);
+                } else {
+                    const f32x4 gs4 = *reinterpret_cast<const f32x4 *>(&sm.gw[16 * SI + 4 * g]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int d = 4 * g + r - c;
+                        const float off = acc[r] * ws4[r] * dexp2(at - as[r]);
+                        const float dia = acc[r] * gs4[r] + dskip;
+                        vals[r] = d < 0 ? off : (d == 0 ? dia : 0.0f);
+                    }
+                }
+                st4(dst, vals);
+            }
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I3 = std::integral_constant<int, 3>;
+        if (wave == 0) {
+            tile(I0{}, I0{}); tile(I2{}, I0{}); tile(I3{}, I0{});
+        } else if (wave == 1) {
+            tile(I0{}, I1{}); tile(I2{}, I1{}); tile(I3{}, I1{});
+        } else if (wave == 2) {
+            tile(I1{}, I0{}); tile(I2{}, I2{}); tile(I3{}, I2{});
+        } else {
+            tile(I1{}, I1{}); tile(I2{}, I3{}); tile(I3{}, I3{});
+        }
+    }
+    // ---- carry-in of the local state (zero in the first sub-chunk)
+    f32x4 yc[NT];
+#pragma unroll
+    for (int tj = 0; tj < NT; ++tj) yc[tj] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (h > 0) {
+        bf16x8 sf[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sf[f][r] = static_cast<__bf16>(sacc[f][0][r]);
+                sf[f][4 + r] = static_cast<__bf16>(sacc[f][1][r]);
+            }
+        const int zc = ((g >> 1) ^ sw) << 4;
+        const int cbase = crow + (g & 1) * 8;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const int olo = (((2 * f) << 4) ^ zc) + cbase;
+            const int ohi = (((2 * (f + NF)) << 4) ^ zc) + cbase;
+#pragma unroll
+            for (int tj = 0; tj < NT; ++tj) {
+                typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
+                const bf16x4v lo = *reinterpret_cast<const bf16x4v *>(cth + tj * 16 * RB + olo);
+                const bf16x4v hi = *reinterpret_cast<const bf16x4v *>(cth + tj * 16 * RB + ohi);
+                const bf16x8 cv = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                yc[tj] = mfma_bf16(sf[f], cv, yc[tj]);
+            }
+        }
+#pragma unroll
+        for (int tj = 0; tj < NT; ++tj) yc[tj] = yc[tj] * dexp2(sm.acum[h][16 * tj + c]);
+    }
+    // X landed (theta of the next sub-chunk may be out)
+    if (more)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm<kT>());
+    else
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+    __syncthreads();   // the band is complete
+
+    // ---- X^T operand fragments (p = 16 wave + c, s = 32 kb + 8 g + 0..7)
+    bf16x8 xf[2];
+    {
+        const int r0 = 8 * g + (c >> 2);
+        const int cq = 16 * wave + 4 * (c & 3);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.x + rtile_off<CX>(32 * kb + r0, cq)));
+            const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.x + rtile_off<CX>(32 * kb + r0 + 4, cq)));
+            xf[kb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+    }
+    // ---- advance: S <- e_h S + U_h (as chunk_scan_dma_kernel)
+    {
+        const float eh = dexp2(sm.acum[h][QT - 1]);
+        bf16x8 xw[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                xw[kb][j] = static_cast<__bf16>(static_cast<float>(xf[kb][j]) * sm.wdv[32 * kb + 8 * g + j]);
+        const int r0 = 8 * g + (c >> 2);
+        const int zlo = (((c & 3) >> 1) ^ rsw<CB>(r0 & 15)) << 4;
+        const int zhi = (((c & 3) >> 1) ^ rsw<CB>((r0 + 4) & 15)) << 4;
+        const int blo = r0 * RB + (c & 1) * 8, bhi = (r0 + 4) * RB + (c & 1) * 8;
+        bf16x8 afr[NF][2][2];
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int ch = (2 * (f + q * NF)) << 4;
+                const int olo = (ch ^ zlo) + blo, ohi = (ch ^ zhi) + bhi;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + 32 * kb * RB + olo));
+                    const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(sm.b + 32 * kb * RB + ohi));
+                    afr[f][q][kb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+            }
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                f32x4 st = sacc[f][q] * eh;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) st = mfma_bf16(afr[f][q][kb], xw[kb], st);
+                sacc[f][q] = st;
+            }
+        if (h == 0) eprod[1] = eh;
+        eacc *= eh;
+    }
+    __syncthreads();   // B~ is dead
+    if (more) load_b(sck + 1);
+
+    // ---- y_local^T[p][t] = carry-in + sum_s X^T[p][s] M[t][s], kept
+    {
+        const unsigned char *const mb = reinterpret_cast<const unsigned char *>(sm.band) + c * (LDM * 2) + 16 * g;
+#pragma unroll
+        for (int tj = 0; tj < NT; ++tj) {
+            f32x4 acc = yc[tj];
+            const int nkb = tj < 2 ? 1 : 2;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+                if (kb < nkb)
+                    acc = mfma_bf16(xf[kb], *reinterpret_cast<const bf16x8 *>(mb + tj * 16 * LDM * 2 + kb * 64), acc);
+            if (h == 0)
+                ykeep[0][tj] = acc;
+            else
+                ykeep[1][tj] = acc;
+        }
+    }
+    if (more) {
+        __syncthreads();   // every read of the band and X is done
+        load_x(sck + 1);
+    }
+    }   // sub-chunks
+
+    if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < PPL; ++j) sm.ang[wave * PW + j] = run[j];
+    }
+    fused_tail<N, 2, 64, GATE>(a, ws, sm, sacc, ykeep, eprod, eacc, k0, h_end, seg, nseg, bh, bhs, rs,
+                               epoch, lb_mode, lb_spin);
+}
+
 // The single pass walks each (batch, head) sequence with one workgroup per CU,
 // so its time goes in whole rounds of one sequence per CU; the three
 // chunk-parallel launches cost about the same per sequence at any count.  The
@@ -1752,6 +2642,68 @@ hipError_t launch_three(const ScanLaunch &a, char *base, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Segments of the fused launch: two sub-chunks each (the C~ of both stay in
+// LDS for the entering state's part of y).
+struct FusedPlan {
+    int nsub, kseg, nseg;
+};
+FusedPlan fused_plan(const ScanLaunch &a) {
+    FusedPlan p;
+    p.nsub = static_cast<int>((a.seq + 63) / 64);
+    p.kseg = p.nsub > 1 ? 2 : 1;
+    p.nseg = (p.nsub + p.kseg - 1) / p.kseg;
+    return p;
+}
+
+// The fused single launch covers bf16 storage at rank 1 (d_state 64 or 128)
+// and is taken while its grid fits three rounds of two workgroups per CU.
+// Each round ends in a look-back, while the three launches' cost grows with
+// the sequences alone; measured on MI355X (us per call, fused vs three
+// launches): config 1, 96 sequences of 2048 tokens (3 rounds), 81.5 vs 83.3
+// summed over the kernels; the config-4 prefill's 192 sequences (6 rounds),
+// 17.22 vs 16.94 ms per 24-layer prefill.
+bool fused_covered(const ScanLaunch &a) {
+    if (!(a.bf16 && a.rank == 1 && (a.d_state == 64 || a.d_state == 128) && a.path == 0)) return false;
+    const size_t segs = a.batch * a.heads * static_cast<size_t>(fused_plan(a).nseg);
+    return segs <= 3 * 2 * device_cus();
+}
+
+// Each call gets a fresh epoch, so flags left in a reused workspace by an
+// earlier call never read as published (62 bits, seeded from the clock).
+std::atomic<uint64_t> g_epoch{0};
+uint64_t next_epoch() {
+    uint64_t e = g_epoch.fetch_add(1, std::memory_order_relaxed);
+    if (e == 0) {
+        const uint64_t seed = static_cast<uint64_t>(
+                                  std::chrono::steady_clock::now().time_since_epoch().count()) |
+                              1u;
+        uint64_t expected = 1;
+        g_epoch.compare_exchange_strong(expected, (seed & ((uint64_t(1) << 61) - 1)) + 2);
+        e = g_epoch.fetch_add(1, std::memory_order_relaxed);
+    }
+    return e & ((uint64_t(1) << 62) - 1);
+}
+
+template <int N>
+hipError_t launch_fused(const ScanLaunch &a, char *base, hipStream_t s) {
+    const FusedPlan fp = fused_plan(a);
+    const size_t bh = a.batch * a.heads;
+    const size_t segs = bh * fp.nseg;
+    const FusedWs ws = fused_ws(base, fused_layout(segs, N), segs, N);
+    const uint64_t epoch = next_epoch();
+    // polls of one flag before a look-back gives up (each poll sleeps ~128
+    // cycles and waits a memory round trip: about a second in all)
+    const int spin = a.lb_spin > 0 ? a.lb_spin : (1 << 20);
+    const dim3 grid(static_cast<unsigned int>(segs));
+    if (a.gate_z != nullptr)
+        hipLaunchKernelGGL((chunk_scan_fused_kernel<N, true>), grid, dim3(kThreads), 0, s, a, ws,
+                           fp.nsub, fp.kseg, fp.nseg, epoch, a.lb_mode, spin);
+    else
+        hipLaunchKernelGGL((chunk_scan_fused_kernel<N, false>), grid, dim3(kThreads), 0, s, a, ws,
+                           fp.nsub, fp.kseg, fp.nseg, epoch, a.lb_mode, spin);
+    return hipGetLastError();
+}
+
 template <typename T, int ROWS>
 hipError_t launch_t(const ScanLaunch &a, char *ws, hipStream_t s) {
     const size_t n = a.d_state, r = a.rank;
@@ -1774,12 +2726,19 @@ size_t scan_chunked_workspace(const ScanLaunch &a) {
     const size_t seqs = a.batch * a.heads, cus = device_cus();
     const size_t rounds = (seqs + cus - 1) / cus;
     if (seqs * 100 >= rounds * cus * 85) return 0;
+    if (fused_covered(a)) return fused_layout(seqs * fused_plan(a).nseg, a.d_state).total;
     return chunked_layout(seqs * seg_plan(a).nseg, a.d_state, a.bf16 != 0).total;
 }
+
+int scan_chunked_launches(const ScanLaunch &a) { return fused_covered(a) ? 1 : 3; }
 
 hipError_t launch_scan_chunked(const ScanLaunch &a, void *workspace, hipStream_t stream) {
     if (!scan_fast_supported(a) || a.seq == 0) return hipErrorNotSupported;
     char *ws = static_cast<char *>(workspace);
+    if (fused_covered(a)) {
+        if (a.d_state == 128) return launch_fused<128>(a, ws, stream);
+        return launch_fused<64>(a, ws, stream);
+    }
     if (a.bf16) return launch_t<bf16_t, 64>(a, ws, stream);
     return launch_t<float, 32>(a, ws, stream);
 }

@@ -123,6 +123,7 @@ SIGNATURES = {
     "m3_status_string": (C.c_char_p, [C.c_int]),
     "m3_last_error": (C.c_char_p, []),
     "m3_launch_count": (C.c_uint64, []),
+    "m3_debug_scan_options": (C.c_int, [C.c_int32, C.c_int32, C.c_int32]),
     "m3_selftest_mfma": (C.c_int, [C.POINTER(C.c_int32)]),
     # mamba3_mixer.h
     "m3_rms_norm": (C.c_int, [_Z, _Z, _P, _Z, _P, C.c_float, _P, _Z, _P]),

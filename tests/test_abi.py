@@ -161,6 +161,38 @@ def test_scan_workspace_query():
                                None, None, None, chunk, 1, None, 0)
         return int(L.m3_scan_workspace_bytes(C.byref(cin)))
 
+    # bf16 at rank 1 runs the fused single launch: per segment of two 64-token
+    # sub-chunks a flag (8 bytes), U (bf16 64 x 128), the decay, the angle
+    # total / cosine / sine per pair (3 x 64 f32), the state after the segment
+    # (f32 64 x 128) and its angle (64 f32), each section 256-byte aligned
+    def fused(segs, n=128):
+        a = lambda v: (v + 255) // 256 * 256
+        return (a(segs * 8) + a(segs * 64 * n * 2) + a(segs * 4) + 3 * a(segs * n // 2 * 4)
+                + a(segs * 64 * n * 4) + a(segs * n // 2 * 4))
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16) == fused(8 * 12 * 16)
+    assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16, chunk=512) == fused(8 * 12 * 16)
+    assert need(2, 700, 3, 64, 64, 1, _lib.M3_BF16) == fused(2 * 3 * 6, 64)
+    # 192 sequences: the fused grid would take six rounds of two workgroups a
+    # CU, so the three launches run (segments of 256 tokens; 75 % of a
+    # single-pass round)
+    three = 2 * 64 * 128 * 2 + 4 + 3 * 64 * 4
+    assert need(16, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 16 * 12 * 4 * three
+    assert need(20, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 0   # 240 sequences: single pass
+    _lib.check(L.m3_debug_scan_options(1, 0, 0))   # the three launches everywhere
+    try:
+        _three_launch_sizes(need, _lib)
+    finally:
+        _lib.check(L.m3_debug_scan_options(0, 0, 0))
+    from mamba3.error import ArgumentError
+    with pytest.raises(ArgumentError):
+        _lib.check(L.m3_debug_scan_options(2, 0, 0))
+    assert need(1, 100, 2, 48, 128, 1, _lib.M3_BF16) == 0      # head_dim 48
+    assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) == 0       # d_state 96
+    assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) == 0      # rank 3
+    assert need(1, 0, 2, 64, 128, 1, _lib.M3_BF16) == 0        # empty window
+
+
+def _three_launch_sizes(need, _lib):
     # per segment: U and S (bf16 64x128 each), the segment decay, and angle
     # total / cosine / sine per pair (3 x 64 f32).  At config 1 (96 sequences
     # of 32 sub-chunks of 64 tokens) segments of 4 sub-chunks give 768
@@ -181,10 +213,6 @@ def test_scan_workspace_query():
     assert need(14, 2048, 12, 64, 128, 1, _lib.M3_BF16) > 0    # 168
     assert need(24, 2048, 12, 64, 128, 1, _lib.M3_BF16) > 0    # 288: 1.13 rounds
     assert need(40, 2048, 12, 64, 128, 1, _lib.M3_BF16) == 0   # 480: 1.88 rounds
-    assert need(1, 100, 2, 48, 128, 1, _lib.M3_BF16) == 0      # head_dim 48
-    assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) == 0       # d_state 96
-    assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) == 0      # rank 3
-    assert need(1, 0, 2, 64, 128, 1, _lib.M3_BF16) == 0        # empty window
 
 
 @pytest.mark.parametrize("kw,grads,status,message", [

@@ -375,6 +375,116 @@ def test_config1_full_size_every_sequence_against_f64():
     assert worst[3] <= 1e-3
 
 
+# ------------------------------------------------------- the fused single launch
+def _scan_options(path, lookback_mode=0, spin=0):
+    from mamba3 import _lib
+    _lib.check(_lib.lib().m3_debug_scan_options(path, lookback_mode, spin))
+
+
+def _fused_inputs(seed, B, T, H, N, theta=True, state=True, skip=True):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    P = 64
+    x = torch.randn(B, T, H, P, 1, device="cuda", generator=g).to(torch.bfloat16)
+    b = (torch.randn(B, T, H, N, 1, device="cuda", generator=g) / math.sqrt(N)).to(torch.bfloat16)
+    c = (torch.randn(B, T, H, N, 1, device="cuda", generator=g) / math.sqrt(N)).to(torch.bfloat16)
+    dt = torch.nn.functional.softplus(torch.randn(B, T, H, device="cuda", generator=g) - 3
+                                      ).clamp(1e-3, 0.1)
+    lam = torch.sigmoid(torch.randn(B, T, H, device="cuda", generator=g))
+    a_log = torch.rand(H, device="cuda", generator=g) * math.log(16)
+    th = ((torch.rand(B, T, H, N // 2, device="cuda", generator=g) * math.pi).to(torch.bfloat16)
+          if theta else None)
+    d = (torch.rand(H, device="cuda", generator=g) * 2 - 1) if skip else None
+    st = None
+    if state:
+        st = (0.1 * torch.randn(B, H, P, N, device="cuda", generator=g),
+              0.1 * torch.randn(B, H, P, N, device="cuda", generator=g),
+              (torch.rand(B, H, N // 2, device="cuda", generator=g) - 0.5) * 6 if theta else None)
+    return x, b, c, dt, a_log, lam, th, d, st
+
+
+def _run_inputs(t):
+    from mamba3.ssm import ScanInputs, SsmState, mamba3_scan
+    x, b, c, dt, a_log, lam, th, d, st = t
+    si = ScanInputs(x, b, c, dt, a_log, lam)
+    if th is not None:
+        si = si.with_theta(th)
+    if d is not None:
+        si = si.with_skip(d)
+    if st is not None:
+        si = si.with_state(SsmState(*st))
+    out = mamba3_scan(si.with_state_output(True).with_chunk_parallel(True))
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("B,T,H,N,theta,state,skip", [
+    (8, 2048, 12, 128, True, False, True),   # config 1: segments of 128 tokens, 16 a sequence
+    (2, 700, 3, 128, True, True, True),      # ragged end, carried state
+    (1, 64, 4, 128, True, True, False),      # one sub-chunk: one segment
+    (1, 130, 5, 128, True, False, False),    # a last segment of one sub-chunk
+    (2, 1000, 3, 64, True, True, True),      # d_state 64
+    (2, 513, 4, 128, False, True, True),     # real dynamics
+])
+def test_fused_launch_matches_the_three_launches_and_f64(B, T, H, N, theta, state, skip):
+    """The fused single launch (default for bf16 at rank 1) against the three
+    launches (m3_debug_scan_options path 1) on the same inputs, and both
+    against the f64 recurrence on two sequences; the fused launch's outputs
+    repeat bit for bit."""
+    t = _fused_inputs(B * 1000 + T, B, T, H, N, theta, state, skip)
+    fused = _run_inputs(t)
+    again = _run_inputs(t)
+    _scan_options(1)
+    try:
+        three = _run_inputs(t)
+    finally:
+        _scan_options(0)
+    assert torch.equal(fused.y, again.y) and torch.equal(fused.state.h, again.state.h)
+    assert torch.equal(fused.state.last_u, again.state.last_u)
+    e = [_device_rel_l2(fused.y, three.y), _device_rel_l2(fused.state.h, three.state.h),
+         _device_rel_l2(fused.state.last_u, three.state.last_u)]
+    x, b, c, dt, a_log, lam, th, d, st = t
+    worst = 0.0
+    for bb, hh in ((0, 0), (B - 1, H - 1)):
+        sl = lambda v: host(v[bb:bb + 1, :, hh:hh + 1])
+        y64, h64, lu64, a64 = oracle.scan_recurrence_f64(
+            sl(x), sl(b), sl(c), sl(dt), host(a_log[hh:hh + 1]), sl(lam),
+            None if th is None else sl(th), None if d is None else host(d[hh:hh + 1]),
+            None if st is None else host(st[0][bb:bb + 1, hh:hh + 1]),
+            None if st is None else host(st[1][bb:bb + 1, hh:hh + 1]),
+            None if (st is None or st[2] is None) else host(st[2][bb:bb + 1, hh:hh + 1]))
+        ys = host(fused.y[bb:bb + 1, :, hh:hh + 1])
+        worst = max(worst, rel_l2(ys, y64), rel_l2(host(fused.state.h[bb:bb + 1, hh:hh + 1]), h64))
+        if th is not None:
+            assert angle_err(host(fused.state.angle[bb:bb + 1, hh:hh + 1]), a64) <= 1e-3
+    print(f"fused vs three launches B{B} T{T} H{H} N{N}: rel-L2 y {e[0]:.2e} h {e[1]:.2e} "
+          f"last_u {e[2]:.2e}; fused vs f64 worst {worst:.2e} (bar {BF16_TOL:g})", flush=True)
+    assert max(e) <= BF16_TOL
+    assert worst <= BF16_TOL
+
+
+def test_fused_lookback_give_up_surfaces_as_nan():
+    """A segment whose look-back gives up (forced from the host: every segment
+    after a sequence's first gives up at once) takes NaN for the state
+    entering it: its outputs, those of every later segment and the boundary
+    state come out NaN, never stale; the first segment's outputs (the first
+    128 tokens) are the normal run's; every kernel exits, and the next call
+    is normal again."""
+    B, T, H, N = 2, 700, 3, 128
+    t = _fused_inputs(5, B, T, H, N)
+    normal = _run_inputs(t)
+    _scan_options(0, 1, 0)
+    try:
+        gave = _run_inputs(t)
+    finally:
+        _scan_options(0)
+    after = _run_inputs(t)
+    assert torch.equal(after.y, normal.y) and torch.equal(after.state.h, normal.state.h)
+    assert torch.equal(gave.y[:, :128], normal.y[:, :128])
+    assert torch.isnan(gave.y[:, 128:].float()).all()
+    assert torch.isnan(gave.state.h).all() and torch.isnan(gave.state.angle).all()
+    assert torch.isfinite(normal.y.float()).all()
+
+
 def _device_rel_l2(a, b):
     """rel-L2 of two device tensors, accumulated in f64 on the device."""
     a, b = a.double(), b.double()
