@@ -770,7 +770,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--decode-steps", type=int, default=512,
+                    help="timed decode steps (BASELINE config 3: 512 consecutive steps)")
     ap.add_argument("--decode-warmup", type=int, default=8)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill leg")
