@@ -25,7 +25,9 @@ Also reported on the same line:
   decode_lm      the whole Mamba3Lm decode step around it (d_model 1536, int8
                  projections, head): us per step, tokens/s, GB/s over the state,
                  weight and logit bytes;
-  cpu_baseline   the CPU restatement of the reference's composed algorithm
+  decode_lm_default the same with the reference's default mixer (conv_kernel 4,
+                 bc_bias): the convolution history joins the in-place caches;
+  cpu_baseline  the CPU restatement of the reference's composed algorithm
                  (oracle/, OpenMP) on the same config-1 workload, on the host.
 
 Inputs are synthetic (seeded torch RNG on the device, the distributions of
@@ -530,6 +532,76 @@ def bench_decode_lm(torch, args):
             "factored_cache": factored}
 
 
+def bench_decode_lm_default(torch, args):
+    """The decode step of bench_decode_lm with the reference's default mixer
+    (config.rs:131-156: conv_kernel 4, bc_bias, bc_norm, D skip, no post-gate
+    norm) at the same widths: each layer's cache adds the convolution history
+    [256, 3, 7680] bf16, read and rewritten in place by the fused mixer step
+    (m3_mixer_step_conv, one launch a layer).  Graph replay on full-format
+    and on factored caches."""
+    from mamba3 import Discretization, SsmConfig, SsmMode, StateDynamics
+    from mamba3.lm import Mamba3Lm, Mamba3LmConfig
+    p = DECODE_LM
+    dev = "cuda:0"
+    B, H, P, N, K = p["B"], p["H"], p["P"], p["N"], 4
+    ssm = SsmConfig(d_model=p["d_model"], n_heads=H, head_dim=P, d_state=N, n_groups=p["G"],
+                    discretization=Discretization.LearnedTrapezoid,
+                    dynamics=StateDynamics.Rotational, mode=SsmMode(1), chunk_size=64,
+                    conv_kernel=K, bc_norm=True, bc_bias=True, post_gate_norm=False)
+    lm = Mamba3Lm(Mamba3LmConfig(vocab_size=p["vocab"], d_model=p["d_model"],
+                                 n_layers=p["layers"], ssm=ssm, int8_weights=True, seed=5), dev)
+    g = torch.Generator(device=dev).manual_seed(0x4D414D48)
+    ids = torch.randint(0, p["vocab"], (16, B, 1), device=dev, generator=g)
+    d, NL = p["d_model"], p["layers"]
+    width = ssm.in_proj_width()
+    chans = H * P + 2 * p["G"] * N
+    weights = NL * (d * width * 2 + width * 4 + d * d * 2 + d * 4) + d * p["vocab"] * 2
+    conv_bytes = NL * (2 * B * (K - 1) * chans * 2 + (K + 1) * chans * 4)
+    steps = args.decode_lm_steps
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = {"workload": "Mamba3Lm decode step, batch 256 x 1 token, vocab 32000, d_model 1536, "
+                       "24 layers x 24 heads x 64, N 128, groups 24, the reference's default "
+                       "mixer (conv_kernel 4, bc_bias, bc_norm), int8 per-output-channel "
+                       "fake-quant projections, state and history caches in place",
+           "steps": steps, "launch": "one HIP graph replay per step (Mamba3Lm.capture_decode)"}
+    for factored in (False, True):
+        cache = lm.empty_cache(B, dev, factored=factored)
+        for c in cache:
+            c.ssm.h.normal_(0.0, 0.1, generator=g)
+            if factored:
+                c.ssm.x_prev.normal_(0.0, 1.0, generator=g)
+                c.ssm.b_prev.normal_(0.0, 1.0 / math.sqrt(N), generator=g)
+            else:
+                c.ssm.last_u.normal_(0.0, 0.1, generator=g)
+            c.ssm.angle.uniform_(-math.pi, math.pi, generator=g)
+            c.conv.normal_(0.0, 1.0, generator=g)
+        graph = lm.capture_decode(cache, B)
+        for i in range(2):
+            graph.step(ids[i])
+        torch.cuda.synchronize()
+        _pause_for_trace(args)
+        e0.record(stream)
+        for i in range(steps):
+            logits = graph.step(ids[i % 16])
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        assert torch.isfinite(logits.float()).all(), "non-finite logits (default mixer)"
+        per_layer = (decode_factored_algorithmic if factored else decode_algorithmic)(B, H, P, N, 1)
+        nbytes = NL * per_layer + conv_bytes + weights + B * p["vocab"] * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        leg = {"us_per_step": round(ms * 1e3, 1), "tokens_per_s": round(B / (ms * 1e-3), 1),
+               "bytes_per_step": nbytes, "achieved_GBps": round(gbs, 1),
+               "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        if factored:
+            out["factored_cache"] = leg
+        else:
+            out.update(leg)
+        del graph, cache
+    return out
+
+
 # BASELINE configs 0 and 2 (parity cases; their forward scans are reported beside
 # the headline): name -> (B, L, H, P, N, R, bf16, rotational)
 OTHER_SCANS = {"config0": (2, 512, 4, 64, 64, 1, False, False),
@@ -784,8 +856,9 @@ def main():
                     help="input/output sets the scan legs rotate over (4 x 152 MB at config 1)")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-reps", type=int, default=3)
-    ap.add_argument("--only", choices=("prefill", "decode_lm", "ingest", "backward", "other_scans",
-                                       "decode", "decode_factored"), default=None,
+    ap.add_argument("--only", choices=("prefill", "decode_lm", "decode_lm_default", "ingest",
+                                       "backward", "other_scans", "decode", "decode_factored"),
+                    default=None,
                     help="run one model leg alone and print its object (for kernel traces)")
     ap.add_argument("--scan-only", action="store_true",
                     help="run only the headline scan --steps times (for counter runs)")
@@ -839,6 +912,7 @@ def main():
         return
     if args.only:
         leg = {"prefill": bench_prefill, "decode_lm": bench_decode_lm,
+               "decode_lm_default": bench_decode_lm_default,
                "ingest": bench_ingest}[args.only](torch, args)
         print(json.dumps({args.only: leg}), flush=True)
         return
@@ -865,6 +939,7 @@ def main():
     dec_f = None if args.no_decode else bench_decode(torch, lib, L_, args, factored=True)
     pre = None if args.no_prefill else bench_prefill(torch, args)
     dlm = None if args.no_decode_lm else bench_decode_lm(torch, args)
+    dlm_def = None if args.no_decode_lm else bench_decode_lm_default(torch, args)
     cpu = None if args.no_cpu else cpu_baseline(args)
 
     line = {
@@ -906,6 +981,7 @@ def main():
         "decode_factored": dec_f,
         "prefill": pre,
         "decode_lm": dlm,
+        "decode_lm_default": dlm_def,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -24,6 +24,10 @@
  *   m3_mixer_step               Mamba3Mixer::step between in_proj and out_proj in
  *                               one launch (prologue, mamba3_step, gate)
  *                                                         src/models/mamba3.rs:569-630
+ *   m3_mixer_step_conv          the same with the convolution's history step
+ *                               (one launch) and the post-gate norm (+1)
+ *                                                         src/models/mamba3.rs:569-630,
+ *                                                         src/tensor/ops/fused.rs:833-865
  *
  * Conventions are those of mamba3_ssm.h: caller-allocated contiguous device
  * buffers, asynchronous on `stream`, status codes with m3_last_error().
@@ -150,13 +154,37 @@ m3_status m3_mixer_gate(size_t tokens, size_t d_inner, const void *y, const void
  * [batch, d_inner] (bf16).  The results equal those three calls bit for bit;
  * the scan inputs and y never go through memory.  No reference counterpart
  * as one call (the reference issues the three pieces).  No convolution and
- * no post-gate norm: compose the calls for those.  Shapes: d_state a multiple
+ * no post-gate norm: m3_mixer_step_conv takes those.  Shapes: d_state a multiple
  * of 8 up to 128 with d_state / 8 a power of two, head_dim * rank a multiple
  * of 8 up to 512, rank 1, 2, 4 or 8 (else M3_ERR_UNSUPPORTED). */
 m3_status m3_mixer_step(const m3_mixer_dims *d, const void *projected, const float *dt_bias,
                         const float *b_bias, const float *c_bias, const float *bc_norm,
                         const float *a_log, const float *d_skip, m3_ssm_state *state,
                         m3_ssm_state_factored *factored, void *out, void *stream);
+
+/* m3_mixer_step for a mixer with the causal convolution and/or the post-gate
+ * norm, such as the reference's default mixer (conv_kernel Some(4),
+ * src/ssm/config.rs:143) stepped by Mamba3Mixer::step
+ * (src/models/mamba3.rs:569-630) with its history update
+ * (src/tensor/ops/fused.rs:833-865).  conv (or NULL) has seq_len 1: x, B and
+ * C come from the convolution over history ++ this token, as
+ * m3_mixer_prologue_conv computes them, and new_history receives the last
+ * k-1 positions.  new_history may be history itself (the cache updated in
+ * place) when groups == heads, where every channel belongs to one
+ * (sequence, head); with groups < heads an in-place history is
+ * M3_ERR_UNSUPPORTED (pass a separate buffer, or compose the calls).  The
+ * weight, bias and histories are 16-byte aligned.  post_norm_weight
+ * [d_inner] (or NULL) is the post-gate RMSNorm gain (eps post_norm_eps): the
+ * norm spans every head of a row, so the step writes y to out and
+ * m3_mixer_gate with the norm follows on out in place (two launches; one
+ * without the norm).  The results equal m3_mixer_prologue_conv, m3_step (or
+ * m3_step_factored) and m3_mixer_gate bit for bit.  Shapes as m3_mixer_step. */
+m3_status m3_mixer_step_conv(const m3_mixer_dims *d, const m3_conv1d *conv, const void *projected,
+                             const float *dt_bias, const float *b_bias, const float *c_bias,
+                             const float *bc_norm, const float *a_log, const float *d_skip,
+                             const float *post_norm_weight, float post_norm_eps,
+                             m3_ssm_state *state, m3_ssm_state_factored *factored, void *out,
+                             void *stream);
 
 /* out[i] = table[ids[i]] for bf16 rows of dim (table [vocab, dim]).  The
  * ids live on the device, so they are not checked on the host: an id outside

@@ -115,13 +115,41 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
     gamma = lam * step;
 }
 
+// Eight channels ch .. ch+7 of the causal convolution over [x | B | C] (px
+// is this sequence's row from x on) at its one position: taps 0 .. k-2 read
+// the history, tap k-1 the row (conv_taps8: the same arithmetic as
+// m3_mixer_prologue_conv).  With `write`, the lane then stores the new
+// history of these channels, the window's last k-1 positions: row i takes
+// the old row i+1, the last row this token.  The lane reads every old row of
+// its channels before it writes any and copies in ascending order, so the
+// history may be updated in place where no other lane or workgroup reads
+// these channels (the host allows that only for groups == heads, where every
+// channel belongs to one (sequence, head) workgroup).
+__device__ __forceinline__ void step_conv8(const MixerStepLaunch &m, size_t bq, size_t C,
+                                           const uint16_t *px, size_t ch, bool write, float *f) {
+    const size_t k = m.conv_k;
+    const uint16_t *hist =
+        m.hist ? static_cast<const uint16_t *>(m.hist) + bq * (k - 1) * C : nullptr;
+    mixm::conv_taps8(m.conv_w, m.conv_b, C, k, ch, [&](size_t j) -> const uint16_t * {
+        return j + 1 == k ? px + ch : hist ? hist + j * C + ch : nullptr;
+    }, f);
+    if (!write || m.new_hist == nullptr) return;
+    uint16_t *nh = static_cast<uint16_t *>(m.new_hist) + bq * (k - 1) * C;
+    for (size_t i = 0; i + 1 < k; ++i) {
+        const uint16_t *src = i + 2 < k ? (hist ? hist + (i + 1) * C + ch : nullptr) : px + ch;
+        const uint4 v = src ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4 *>(nh + i * C + ch) = v;
+    }
+}
+
 // The fused step's prologue (MixerStepLaunch): the projection row of this
 // sequence through the 16-byte prologue's arithmetic (mixer_math.hpp, the
 // same roundings: every value is rounded to bf16 where m3_mixer_prologue
 // stores it) into LDS -- B and C raw [N][R] (braw, craw), x, theta, dt and
 // lambda -- then step_prologue's angle advance, rotation and coefficients on
-// those values.
-template <int R, bool FACT>
+// those values.  CONV: x, B and C through the causal convolution first
+// (step_conv8), which also writes the new history of this head's channels.
+template <int R, bool FACT, bool CONV>
 __device__ __forceinline__ void mix_prologue(const MixerStepLaunch &m, size_t bh, float *bt,
                                              float *ct, float *xs, float &alpha, float &beta,
                                              float &gamma, float *bpt, float *braw, float *craw,
@@ -143,16 +171,26 @@ __device__ __forceinline__ void mix_prologue(const MixerStepLaunch &m, size_t bh
     const uint16_t *plam = pdt + H;
     const uint16_t *pth = plam + (m.learned_lambda ? H : 0);
     const int lq = N / 8;
-    const int grp = h / (H / static_cast<int>(m.groups));
+    const int per_group = H / static_cast<int>(m.groups);
+    const int grp = h / per_group;
     const int nx = P * R / 8;
+    const size_t C = static_cast<size_t>(din) + 2 * static_cast<size_t>(bcw);
     if (tid < 2 * lq) {
         // B (lanes 0 .. lq-1) and C (lq .. 2 lq-1): eight states of every rank
         const int which = tid / lq, q = tid - which * lq;
         const uint16_t *src = (which ? pc : pb) + grp * R * N + q * 8;
         const float *bias = which ? m.c_bias : m.b_bias;
         float v[R][8], bb[8], w[8];
+        if constexpr (CONV) {
+            // the group's channels: their history is written by its first head
+            const size_t ch0 = static_cast<size_t>(src - px);
 #pragma unroll
-        for (int r = 0; r < R; ++r) unpack8(*reinterpret_cast<const uint4 *>(src + r * N), v[r]);
+            for (int r = 0; r < R; ++r)
+                step_conv8(m, bq, C, px, ch0 + r * N, h % per_group == 0, v[r]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) unpack8(*reinterpret_cast<const uint4 *>(src + r * N), v[r]);
+        }
         if (bias) {
             const float4 b0 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8);
             const float4 b1 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8 + 4);
@@ -174,7 +212,10 @@ __device__ __forceinline__ void mix_prologue(const MixerStepLaunch &m, size_t bh
     } else if (tid >= 64 && tid < 64 + nx) {
         const int k = tid - 64;
         float f[8];
-        unpack8(*reinterpret_cast<const uint4 *>(px + h * P * R + k * 8), f);
+        if constexpr (CONV)
+            step_conv8(m, bq, C, px, static_cast<size_t>(h * P * R + k * 8), true, f);
+        else
+            unpack8(*reinterpret_cast<const uint4 *>(px + h * P * R + k * 8), f);
 #pragma unroll
         for (int j = 0; j < 8; ++j) xs[k * 8 + j] = bf16_bits_to_f32(to_bits(silu_fast(f[j])));
     } else if (tid >= 128 && tid < 128 + half && a.theta != nullptr) {
@@ -231,8 +272,9 @@ __device__ __forceinline__ void mix_prologue(const MixerStepLaunch &m, size_t bh
 
 // Vector body: N % 4 == 0 and G = N / 4 lanes per row with G a power of two
 // that divides 64.  Each lane owns four consecutive state columns of a row.
-// MIX: the fused mixer step (mix_prologue in, the gate out).
-template <typename T, int RK, bool FACT, bool MIX = false>
+// MIX: the fused mixer step (mix_prologue in, the gate out); CONV: its
+// convolution.
+template <typename T, int RK, bool FACT, bool MIX = false, bool CONV = false>
 __device__ __forceinline__ void step_body_vec(const StepLaunch &a, size_t bh,
                                               const MixerStepLaunch *m = nullptr) {
     extern __shared__ float smem[];
@@ -251,7 +293,8 @@ __device__ __forceinline__ void step_body_vec(const StepLaunch &a, size_t bh,
     float *scal = thv + N / 2;
     float alpha, beta, gamma;
     if constexpr (MIX)
-        mix_prologue<R, FACT>(*m, bh, bt, ct, xs, alpha, beta, gamma, bpt, braw, craw, thv, scal);
+        mix_prologue<R, FACT, CONV>(*m, bh, bt, ct, xs, alpha, beta, gamma, bpt, braw, craw, thv,
+                                    scal);
     else
         step_prologue<T, FACT>(a, bh, bt, ct, xs, alpha, beta, gamma, bpt, xps);
     if constexpr (FACT && MIX) {
@@ -361,15 +404,17 @@ __device__ __forceinline__ void step_body_vec(const StepLaunch &a, size_t bh,
             if (live && (lane % G) == 0) {
                 if constexpr (MIX) {
                     // the gate: silu(z) * y with y rounded to bf16 first, as
-                    // m3_mixer_gate reads it (models/mamba3.rs:468-477)
+                    // m3_mixer_gate reads it (models/mamba3.rs:468-477); y
+                    // alone where a post-gate norm comes between
                     const uint16_t *z = static_cast<const uint16_t *>(m->projected) +
                                         (bh / a.heads) * m->width + (bh % a.heads) * P * R;
                     uint16_t *o = static_cast<uint16_t *>(m->out) + bh * P * R;
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
-                        const float yv =
-                            bf16_bits_to_f32(mixm::to_bits(__builtin_fmaf(xs[p * R + r], dskip, ypart[r])));
-                        o[p * R + r] = mixm::to_bits(yv * mixm::silu_fast(mixm::bf(z, p * R + r)));
+                        const uint16_t yb = mixm::to_bits(__builtin_fmaf(xs[p * R + r], dskip, ypart[r]));
+                        o[p * R + r] = m->gate ? mixm::to_bits(bf16_bits_to_f32(yb) *
+                                                               mixm::silu_fast(mixm::bf(z, p * R + r)))
+                                               : yb;
                     }
                 } else {
                     T *y = static_cast<T *>(a.y);
@@ -415,10 +460,10 @@ step_kernel_vec_layers(StepLaunch base, StepLayerTable t) {
     step_body_vec<T, RK, FACT>(a, blockIdx.x - l * per);
 }
 
-template <int RK, bool FACT>
+template <int RK, bool FACT, bool CONV>
 __global__ void __launch_bounds__(kStepThreads)
 mixer_step_kernel(MixerStepLaunch m) {
-    step_body_vec<bf16_t, RK, FACT, true>(m.s, blockIdx.x, &m);
+    step_body_vec<bf16_t, RK, FACT, true, CONV>(m.s, blockIdx.x, &m);
 }
 
 // Generic body for shapes the vector body does not cover (odd N, N > 256,
@@ -605,11 +650,19 @@ hipError_t launch_mixer_step(const MixerStepLaunch &m, hipStream_t stream) {
     const size_t smem =
         ((fact ? 5 : 4) * N * R + (fact ? 2 : 1) * P * R + N / 2 + 2) * sizeof(float);
     const dim3 grid(static_cast<unsigned int>(a.batch * a.heads));
-#define M3_MIX(RK)                                                                                 \
+#define M3_MIX2(RK, CV)                                                                            \
     if (fact)                                                                                      \
-        hipLaunchKernelGGL((mixer_step_kernel<RK, true>), grid, dim3(kStepThreads), smem, stream, m); \
+        hipLaunchKernelGGL((mixer_step_kernel<RK, true, CV>), grid, dim3(kStepThreads), smem,      \
+                           stream, m);                                                             \
     else                                                                                           \
-        hipLaunchKernelGGL((mixer_step_kernel<RK, false>), grid, dim3(kStepThreads), smem, stream, m);
+        hipLaunchKernelGGL((mixer_step_kernel<RK, false, CV>), grid, dim3(kStepThreads), smem,     \
+                           stream, m);
+#define M3_MIX(RK)                                                                                 \
+    if (m.conv_k) {                                                                                \
+        M3_MIX2(RK, true)                                                                          \
+    } else {                                                                                       \
+        M3_MIX2(RK, false)                                                                         \
+    }
     switch (R) {
         case 1: M3_MIX(1) break;
         case 2: M3_MIX(2) break;
@@ -618,6 +671,7 @@ hipError_t launch_mixer_step(const MixerStepLaunch &m, hipStream_t stream) {
         default: return hipErrorNotSupported;
     }
 #undef M3_MIX
+#undef M3_MIX2
     return hipGetLastError();
 }
 

@@ -51,7 +51,14 @@ struct MixerStepLaunch {
     const float *dt_bias;           // [H]
     const float *b_bias, *c_bias;   // [H, N] or null
     const float *bc_norm;           // [N] or null
-    void *out;                      // bf16 [B, H*P*R]: silu(z) * y
+    void *out;                      // bf16 [B, H*P*R]: silu(z) * y, or y when !gate
+    int gate;                       // 0: y alone (a post-gate norm and the gate follow)
+    // the causal convolution over [x | B | C] (conv_k 0: none), one position
+    // per sequence: taps 0 .. k-2 from the history, k-1 from the row
+    size_t conv_k;
+    const float *conv_w, *conv_b;   // [k, C] and [C] (or null), C = d_inner + 2 G R N
+    const void *hist;               // bf16 [B, k-1, C], or null (zeros)
+    void *new_hist;                 // bf16 [B, k-1, C], or null; may be hist when G == H
 };
 // Shapes the fused step covers: the 16-byte prologue's (d_state a multiple
 // of 8 with d_state / 8 a power of two, head_dim * rank and the row width

@@ -208,13 +208,20 @@ m3_status m3_mixer_gate(size_t tokens, size_t d_inner, const void *y, const void
                     "gate launch");
 }
 
-m3_status m3_mixer_step(const m3_mixer_dims *d, const void *projected, const float *dt_bias,
-                        const float *b_bias, const float *c_bias, const float *bc_norm,
-                        const float *a_log, const float *d_skip, m3_ssm_state *state,
-                        m3_ssm_state_factored *factored, void *out, void *stream) {
+namespace {
+
+// m3_mixer_step and m3_mixer_step_conv: the checks, then one launch (and the
+// gate with the post-gate norm after it when there is one).
+m3_status mixer_step_call(const m3_mixer_dims *d, const m3_conv1d *conv, const void *projected,
+                          const float *dt_bias, const float *b_bias, const float *c_bias,
+                          const float *bc_norm, const float *a_log, const float *d_skip,
+                          const float *post_norm_weight, float post_norm_eps,
+                          m3_ssm_state *state, m3_ssm_state_factored *factored, void *out,
+                          void *stream) {
+    const char *fn = conv || post_norm_weight ? "m3_mixer_step_conv" : "m3_mixer_step";
     if (d == nullptr) return m3::api_fail(M3_ERR_ARGUMENT, "mixer dims are NULL");
     if ((state == nullptr) == (factored == nullptr))
-        return m3::api_fail(M3_ERR_ARGUMENT, "m3_mixer_step needs exactly one of state / factored");
+        return m3::api_fail(M3_ERR_ARGUMENT, "%s needs exactly one of state / factored", fn);
     if (d->heads == 0 || d->head_dim == 0 || d->d_state == 0 || d->rank == 0 || d->groups == 0)
         return m3::api_fail(M3_ERR_CONFIG, "heads, head_dim, d_state, rank and groups must be positive");
     if (d->heads % d->groups != 0)   // config.rs:207-212
@@ -230,10 +237,40 @@ m3_status m3_mixer_step(const m3_mixer_dims *d, const void *projected, const flo
         return m3::api_fail(M3_ERR_CONFIG, "unknown discretization %d", d->discretization);
     const size_t width = m3_mixer_in_proj_width(d);
     if (!m3::mixer_step_supported(d->head_dim, d->d_state, d->rank, width))
-        return m3::api_fail(M3_ERR_UNSUPPORTED, "m3_mixer_step covers d_state a multiple of 8 up to "
+        return m3::api_fail(M3_ERR_UNSUPPORTED, "%s covers d_state a multiple of 8 up to "
                             "128 with d_state/8 a power of two, head_dim*rank a multiple of 8 up "
-                            "to 512 and rank 1, 2, 4 or 8; compose m3_mixer_prologue, m3_step "
-                            "and m3_mixer_gate");
+                            "to 512 and rank 1, 2, 4 or 8; compose m3_mixer_prologue(_conv), "
+                            "m3_step and m3_mixer_gate", fn);
+    auto al16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const size_t din = d->heads * d->head_dim * d->rank;
+    if (conv != nullptr) {
+        if (conv->kernel_size < 2)   // config.rs:237-243
+            return m3::api_fail(M3_ERR_CONFIG, "conv_kernel must be at least 2, got %zu",
+                                conv->kernel_size);
+        if (conv->seq_len != 1)
+            return m3::api_fail(M3_ERR_SHAPE, "%s steps one position per sequence (seq_len 1), "
+                                "got seq_len %zu", fn, conv->seq_len);
+        if (conv->weight == nullptr)
+            return m3::api_fail(M3_ERR_ARGUMENT, "convolution weight is NULL");
+        if (!al16(conv->weight) || !al16(conv->bias) || !al16(conv->history) ||
+            !al16(conv->new_history))
+            return m3::api_fail(M3_ERR_ARGUMENT, "the convolution weight, bias and histories must "
+                                "be 16-byte aligned");
+        const size_t channels = din + 2 * d->groups * d->d_state * d->rank;
+        const size_t hist_bytes = d->tokens * (conv->kernel_size - 1) * channels * 2;
+        const bool in_place = conv->history != nullptr && conv->history == conv->new_history;
+        if (in_place && d->groups != d->heads)
+            return m3::api_fail(M3_ERR_UNSUPPORTED, "%s updates the history in place only "
+                                "with n_groups == n_heads (got %zu groups of %zu heads): "
+                                "pass a separate new_history or compose the calls", fn,
+                                d->groups, d->heads);
+        if (!in_place && conv->history != nullptr && conv->new_history != nullptr &&
+            ranges_overlap(conv->history, conv->new_history, hist_bytes))
+            return m3::api_fail(M3_ERR_ARGUMENT, "the new convolution history overlaps the "
+                                "history without being the same buffer");
+    }
+    if (post_norm_weight != nullptr && !(post_norm_eps >= 0.0f))
+        return m3::api_fail(M3_ERR_CONFIG, "RmsNorm eps must be non-negative");
     if (d->tokens == 0) return m3::api_ok();
     float *h = state ? state->h : factored->h;
     float *angle = state ? state->angle : factored->angle;
@@ -244,7 +281,6 @@ m3_status m3_mixer_step(const m3_mixer_dims *d, const void *projected, const flo
     if (rot && angle == nullptr)
         return m3::api_fail(M3_ERR_ARGUMENT, "rotational dynamics need the state's angle buffer "
                             "(updated in place)");
-    auto al16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (!al16(projected) || !al16(out) || !al16(h) || (state && !al16(state->last_u)) ||
         (b_bias && !al16(b_bias)) || (c_bias && !al16(c_bias)) || (bc_norm && !al16(bc_norm)))
         return m3::api_fail(M3_ERR_ARGUMENT, "projected, out, the state and the bias / norm "
@@ -276,7 +312,40 @@ m3_status m3_mixer_step(const m3_mixer_dims *d, const void *projected, const flo
     m.c_bias = c_bias;
     m.bc_norm = bc_norm;
     m.out = out;
-    return launched(m3::launch_mixer_step(m, as_stream(stream)), "mixer step launch");
+    m.gate = post_norm_weight == nullptr ? 1 : 0;
+    if (conv != nullptr) {
+        m.conv_k = conv->kernel_size;
+        m.conv_w = conv->weight;
+        m.conv_b = conv->bias;
+        m.hist = conv->history;
+        m.new_hist = conv->new_history;
+    }
+    const m3_status st = launched(m3::launch_mixer_step(m, as_stream(stream)), "mixer step launch");
+    if (st != M3_OK || post_norm_weight == nullptr) return st;
+    // the post-gate norm spans every head of a row: the gate runs on y in place
+    return launched(m3::launch_mixer_gate(d->tokens, din, out, projected, width, post_norm_weight,
+                                          post_norm_eps, out, as_stream(stream)),
+                    "gate launch");
+}
+
+}  // namespace
+
+m3_status m3_mixer_step(const m3_mixer_dims *d, const void *projected, const float *dt_bias,
+                        const float *b_bias, const float *c_bias, const float *bc_norm,
+                        const float *a_log, const float *d_skip, m3_ssm_state *state,
+                        m3_ssm_state_factored *factored, void *out, void *stream) {
+    return mixer_step_call(d, nullptr, projected, dt_bias, b_bias, c_bias, bc_norm, a_log, d_skip,
+                           nullptr, 0.0f, state, factored, out, stream);
+}
+
+m3_status m3_mixer_step_conv(const m3_mixer_dims *d, const m3_conv1d *conv, const void *projected,
+                             const float *dt_bias, const float *b_bias, const float *c_bias,
+                             const float *bc_norm, const float *a_log, const float *d_skip,
+                             const float *post_norm_weight, float post_norm_eps,
+                             m3_ssm_state *state, m3_ssm_state_factored *factored, void *out,
+                             void *stream) {
+    return mixer_step_call(d, conv, projected, dt_bias, b_bias, c_bias, bc_norm, a_log, d_skip,
+                           post_norm_weight, post_norm_eps, state, factored, out, stream);
 }
 
 m3_status m3_embedding_lookup(size_t n, size_t dim, const int32_t *ids, size_t vocab,

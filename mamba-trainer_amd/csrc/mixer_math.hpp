@@ -36,6 +36,38 @@ __device__ __forceinline__ unsigned int pack2(float a, float b) {
     return static_cast<unsigned int>(to_bits(a)) | (static_cast<unsigned int>(to_bits(b)) << 16);
 }
 
+// Eight channels ch .. ch+7 of the depthwise causal convolution at one
+// position (nn/conv.rs:60-225, fused.rs:780-832): f = bias + sum_j w[j] x_j
+// over taps j = 0 .. k-1 in ascending order, one fused multiply-add each, so
+// that every kernel computing it rounds alike.  `tap(j)` gives tap j's eight
+// bf16 inputs (the position k-1-j before this one), or null for a position
+// before the sequence with no history (the tap is skipped).  w is the
+// [k, C] f32 weight, bias [C] or null.
+template <typename Tap>
+__device__ __forceinline__ void conv_taps8(const float *w, const float *bias, size_t C, size_t k,
+                                           size_t ch, Tap tap, float *f) {
+    if (bias) {
+        const float4 b0 = *reinterpret_cast<const float4 *>(bias + ch);
+        const float4 b1 = *reinterpret_cast<const float4 *>(bias + ch + 4);
+        f[0] = b0.x; f[1] = b0.y; f[2] = b0.z; f[3] = b0.w;
+        f[4] = b1.x; f[5] = b1.y; f[6] = b1.z; f[7] = b1.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = 0.0f;
+    }
+    for (size_t j = 0; j < k; ++j) {
+        const uint16_t *src = tap(j);
+        if (src == nullptr) continue;
+        float v[8];
+        unpack8(*reinterpret_cast<const uint4 *>(src), v);
+        const float4 w0 = *reinterpret_cast<const float4 *>(w + j * C + ch);
+        const float4 w1 = *reinterpret_cast<const float4 *>(w + j * C + ch + 4);
+        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = __builtin_fmaf(wv[e], v[e], f[e]);
+    }
+}
+
 // Eight states q*8 .. q*8+7 of every rank of one (B | C, head) row after the
 // silu (v holds the pre-silu values in, the final ones out): + bias8 (when
 // has_bias), then the RMSNorm over the state axis with gain w8 (when

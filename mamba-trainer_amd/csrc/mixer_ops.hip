@@ -164,7 +164,7 @@ __device__ __forceinline__ float xbc_at(const PrologueLaunch &a, const uint16_t 
         float v = 0.0f;
         if (back <= s) v = bf(xbc_t - back * a.width, ch);
         else if (hist) v = bf(hist, (seqi * (k - 1) + (k - 1 + s - back)) * C + ch);
-        acc += a.conv_w[j * C + ch] * v;
+        acc = __builtin_fmaf(a.conv_w[j * C + ch], v, acc);
     }
     return acc;
 }
@@ -290,28 +290,11 @@ __device__ __forceinline__ void xbc8(const PrologueLaunch &a, const uint16_t *xb
     }
     const size_t k = a.conv_k;
     const uint16_t *hist = static_cast<const uint16_t *>(a.hist);
-    if (a.conv_b) {
-        const float4 b0 = *reinterpret_cast<const float4 *>(a.conv_b + ch);
-        const float4 b1 = *reinterpret_cast<const float4 *>(a.conv_b + ch + 4);
-        f[0] = b0.x; f[1] = b0.y; f[2] = b0.z; f[3] = b0.w;
-        f[4] = b1.x; f[5] = b1.y; f[6] = b1.z; f[7] = b1.w;
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = 0.0f;
-    }
-    for (size_t j = 0; j < k; ++j) {
+    conv_taps8(a.conv_w, a.conv_b, C, k, ch, [&](size_t j) -> const uint16_t * {
         const size_t back = k - 1 - j;
-        const uint16_t *src = back <= s ? xbc_t - back * a.width + ch
-                            : hist ? hist + (seqi * (k - 1) + (k - 1 + s - back)) * C + ch : nullptr;
-        if (src == nullptr) continue;
-        float v[8];
-        unpack8(*reinterpret_cast<const uint4 *>(src), v);
-        const float4 w0 = *reinterpret_cast<const float4 *>(a.conv_w + j * C + ch);
-        const float4 w1 = *reinterpret_cast<const float4 *>(a.conv_w + j * C + ch + 4);
-        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] += w[e] * v[e];
-    }
+        return back <= s ? xbc_t - back * a.width + ch
+               : hist ? hist + (seqi * (k - 1) + (k - 1 + s - back)) * C + ch : nullptr;
+    }, f);
 }
 
 template <int R, bool CONV>

@@ -138,6 +138,8 @@ SIGNATURES = {
     "m3_embedding_lookup": (C.c_int, [_Z, _Z, _P, _Z, _P, _P, _P]),
     "m3_mixer_step": (C.c_int, [C.POINTER(MixerDimsC)] + [_P] * 7 +
                       [C.POINTER(SsmStateC), C.POINTER(SsmStateFactoredC), _P, _P]),
+    "m3_mixer_step_conv": (C.c_int, [C.POINTER(MixerDimsC), C.POINTER(Conv1dC)] + [_P] * 8 +
+                           [C.c_float, C.POINTER(SsmStateC), C.POINTER(SsmStateFactoredC), _P, _P]),
     # mamba3_checkpoint.h
     "m3_checkpoint_load": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
     "m3_state_dict_load": (C.c_int, [C.c_char_p, C.POINTER(_P)]),

@@ -258,10 +258,9 @@ class Mamba3Mixer:
                              "apply_with_state for a window")
         c = self.cfg
         B = input.shape[0]
-        if self.conv_weight is None and self.post_gate_norm is None:
-            out_fused = self._step_fused(input, cache, residual, out)
-            if out_fused is not None:
-                return out_fused
+        out_fused = self._step_fused(input, cache, residual, out)
+        if out_fused is not None:
+            return out_fused
         if self.conv_weight is not None and cache.conv is None:
             cache.conv = self._history(B, input.device)
         proj = self.project(input, cache.conv, cache.conv)
@@ -273,8 +272,11 @@ class Mamba3Mixer:
 
     def _step_fused(self, input: torch.Tensor, cache: MixerCache, residual, out):
         """step_ through m3_mixer_step (prologue, state step and gate in one
-        launch; the same results as the composed path bit for bit), or None
-        where it does not apply (its shapes, or a cache it cannot take)."""
+        launch; the same results as the composed path bit for bit), or
+        m3_mixer_step_conv with the convolution (its history updated in place
+        by the same launch) or the post-gate norm (the gate after it, a second
+        launch); None where it does not apply (its shapes, a cache it cannot
+        take, or an in-place history shared by several heads of a group)."""
         c = self.cfg
         if input.dim() != 3 or input.shape[2] != c.d_model:
             return None
@@ -292,6 +294,17 @@ class Mamba3Mixer:
             ok = ok and st.last_u.shape == (B, H, P, N) and st.last_u.is_contiguous()
         if not ok:
             return None
+        hist = None
+        if self.conv_weight is not None:
+            if c.n_groups != c.n_heads:
+                return None
+            if cache.conv is None:
+                cache.conv = self._history(B, input.device)
+            hist = cache.conv
+            if (tuple(hist.shape) != (B, c.conv_kernel - 1, self.conv_channels())
+                    or hist.dtype != torch.bfloat16 or not hist.is_contiguous()
+                    or hist.device != input.device):
+                return None
         if getattr(self, "_fused_step_ok", None) is None:
             # an empty call reports whether the library covers these shapes
             probe = _lib.lib().m3_mixer_step(C.byref(self._dims(0)), None, None, None, None, None,
@@ -312,10 +325,23 @@ class Mamba3Mixer:
                                                           st.b_prev.data_ptr(), ang))
         else:
             sc, fc = C.byref(_lib.SsmStateC(st.h.data_ptr(), st.last_u.data_ptr(), ang)), None
-        _lib.check(_lib.lib().m3_mixer_step(
-            C.byref(dims), projected.data_ptr(), self.dt_bias.data_ptr(), ptr(self.b_bias),
-            ptr(self.c_bias), None if self.bc_norm is None else self.bc_norm.weight.data_ptr(),
-            self.a_log.data_ptr(), ptr(self.d_skip), sc, fc, gated.data_ptr(), _stream(input)))
+        bcn = None if self.bc_norm is None else self.bc_norm.weight.data_ptr()
+        pn = self.post_gate_norm
+        if hist is None and pn is None:
+            _lib.check(_lib.lib().m3_mixer_step(
+                C.byref(dims), projected.data_ptr(), self.dt_bias.data_ptr(), ptr(self.b_bias),
+                ptr(self.c_bias), bcn, self.a_log.data_ptr(), ptr(self.d_skip), sc, fc,
+                gated.data_ptr(), _stream(input)))
+        else:
+            conv = None if hist is None else _lib.Conv1dC(
+                c.conv_kernel, 1, self.conv_weight.data_ptr(), ptr(self.conv_bias),
+                hist.data_ptr(), hist.data_ptr())
+            _lib.check(_lib.lib().m3_mixer_step_conv(
+                C.byref(dims), None if conv is None else C.byref(conv), projected.data_ptr(),
+                self.dt_bias.data_ptr(), ptr(self.b_bias), ptr(self.c_bias), bcn,
+                self.a_log.data_ptr(), ptr(self.d_skip), None if pn is None else pn.weight.data_ptr(),
+                C.c_float(1e-5 if pn is None else pn.eps), sc, fc, gated.data_ptr(),
+                _stream(input)))
         return self.out_proj.apply(gated, residual=residual, out=out)
 
     def step(self, input: torch.Tensor, cache: MixerCache):

@@ -319,6 +319,38 @@ def test_mixer_step_shape_cover_and_argument_checks():
                                C.byref(_lib.SsmStateC()), None, None, None)) == _lib.M3_ERR_UNSUPPORTED
 
 
+def test_conv_mixer_step_history_rules_before_any_launch():
+    """m3_mixer_step_conv's host-side checks on an empty call (the pointers are
+    stand-ins that are never dereferenced): one position per sequence, a
+    history updated in place only where every channel belongs to one head
+    (groups == heads), 16-byte aligned convolution buffers, and a
+    non-negative post-gate norm eps."""
+    import ctypes as C
+    from mamba3 import _lib
+    L = _lib.lib()
+    H, P, N = 4, 16, 32
+    chans = H * P + 2 * H * N          # groups == heads
+
+    def call(G=H, k=4, seq=1, hist=1 << 20, new=1 << 20, w=1 << 16, bias=None, norm=None,
+             eps=1e-5, conv=True):
+        d = _lib.MixerDimsC(0, H, P, N, 1, G, 2, 1, 1e-5)
+        cv = _lib.Conv1dC(k, seq, w, bias, hist, new)
+        return int(L.m3_mixer_step_conv(C.byref(d), C.byref(cv) if conv else None, None, None,
+                                        None, None, None, None, None, norm, C.c_float(eps),
+                                        C.byref(_lib.SsmStateC()), None, None, None))
+
+    assert call() == _lib.M3_OK                                   # in place, G == H
+    assert call(conv=False, norm=1 << 12) == _lib.M3_OK           # post-gate norm alone
+    assert call(G=2) == _lib.M3_ERR_UNSUPPORTED                   # in place, groups < heads
+    assert "n_groups == n_heads" in L.m3_last_error().decode()
+    assert call(G=2, new=(1 << 20) + 3 * chans * 2 * 4) == _lib.M3_OK   # separate, G < H
+    assert call(seq=2) == _lib.M3_ERR_SHAPE
+    assert call(k=1) == _lib.M3_ERR_CONFIG
+    assert call(w=None) == _lib.M3_ERR_ARGUMENT
+    assert call(bias=(1 << 12) + 4) == _lib.M3_ERR_ARGUMENT       # unaligned bias
+    assert call(conv=False, norm=1 << 12, eps=-1.0) == _lib.M3_ERR_CONFIG
+
+
 def test_gated_scan_argument_checks_before_any_launch():
     """m3_scan_gated rejects f32 storage, a NULL z and a z row shorter than
     heads*head_dim*rank before any device work (the pointers are stand-ins

@@ -482,9 +482,12 @@ def test_config4_full_model_split_prefill_property():
     logits of one 2048-token prefill.
 
     The bar is the device's own noise floor at this depth, measured here: the
-    same 2048-token prefill with the scan on its three-launch form (segments
-    of 256 tokens and a separate state pass instead of the fused launch's
-    128-token segments and look-back: the same arithmetic in another order).
+    same 2048-token prefill run as two batches of 8.  At batch 16 the scan's
+    grid is too large for the fused single launch and takes the three
+    launches (segments of 256 tokens and a separate state pass); at batch 8
+    it fits and takes the fused launch (128-token segments and look-back):
+    the same arithmetic in another order.  The 1024-token windows take the
+    fused launch as well.
     With bf16 activations, rounding differences of ~1e-4 in one layer flip
     bf16 roundings of the residual stream and compound over 24 layers to
     ~2.4e-2 in the logits (1e-3 at one layer), so no bf16 implementation meets
@@ -511,18 +514,14 @@ def test_config4_full_model_split_prefill_property():
     e1 = _device_rel_l2(first, full[:, :cut])
     e2 = _device_rel_l2(second, full[:, cut:])
     del first
-    L = lib()
-    L.check(L.lib().m3_debug_scan_options(1, 0, 0))
-    try:
-        other = lm.forward(ids)[:, cut:]
-    finally:
-        L.check(L.lib().m3_debug_scan_options(0, 0, 0))
+    other = torch.cat([lm.forward(ids[:8])[:, cut:], lm.forward(ids[8:])[:, cut:]])
     floor = _device_rel_l2(other, full[:, cut:])
+    assert floor > 0, "the floor's prefill should take the other scan form"
     del other
     cold = _device_rel_l2(lm.forward(ids[:, cut:]), full[:, cut:])
     print(f"config 4 full model, prefill {cut} + carried {T - cut} vs {T}: rel-L2 first "
-          f"{e1:.2e}, second {e2:.2e}; noise floor (the same prefill on the three-launch "
-          f"scan) {floor:.2e}; without the carried caches {cold:.2e}", flush=True)
+          f"{e1:.2e}, second {e2:.2e}; noise floor (the same prefill as two batches of 8, "
+          f"fused scan) {floor:.2e}; without the carried caches {cold:.2e}", flush=True)
     # absolute ceilings beside the floor-relative bars: a fault that corrupts
     # every path alike raises the floor with the windows, so the floor itself
     # and both windows are capped (the floor measures 2.4e-2 on MI355X)
@@ -692,3 +691,136 @@ def test_fused_mixer_step_equals_the_composed_calls(H, G, P, N, R, rot, learned,
             a, b = getattr(fused.ssm, name, None), getattr(composed.ssm, name, None)
             if a is not None:
                 assert torch.equal(a, b), (step, name)
+
+
+FUSED_CONV_CASES = [
+    # H, P, N, R, rotational, learned lambda, factored, post-gate norm (groups
+    # == heads: the history is updated in place by the step's own launch)
+    (4, 16, 16, 1, True, True, False, False),
+    (4, 64, 128, 1, True, True, True, False),
+    (8, 8, 32, 2, True, False, False, True),
+    (4, 16, 64, 4, True, True, True, True),
+    (4, 64, 128, 1, False, True, False, True),
+]
+
+
+def _conv_mixer(H, P, N, R, rot, learned, post_norm, groups=None, seed=0):
+    rng = np.random.default_rng(seed)
+    model = mo.random_model(rng, vocab=16, d_model=32, n_layers=1, heads=H, head_dim=P,
+                            d_state=N, rank=R, groups=groups or H, rotational=rot,
+                            learned_lambda=learned, fixed_lambda=0.5, int8=True, bias_scale=0.3,
+                            conv_kernel=4)
+    lm = gpu_lm_from_oracle(model, True, learned, rot)
+    _, mixer = lm.layers[0]
+    if post_norm:
+        from mamba3.nn import RmsNorm
+        mixer.post_gate_norm = RmsNorm(mixer.cfg.d_inner(), DEV)
+        mixer.post_gate_norm.weight = t_f32(rng.uniform(0.25, 1.75, mixer.cfg.d_inner()))
+    return mixer, rng
+
+
+def _random_cache(mixer, B, factored, g):
+    cache = mixer.empty_cache(B, DEV, factored=factored)
+    st = cache.ssm
+    st.h.normal_(0.0, 0.1, generator=g)
+    if factored:
+        st.x_prev.copy_(torch.randn(st.x_prev.shape, device=DEV, generator=g).to(torch.bfloat16))
+        st.b_prev.copy_(torch.randn(st.b_prev.shape, device=DEV, generator=g).to(torch.bfloat16))
+    else:
+        st.last_u.normal_(0.0, 0.1, generator=g)
+    if st.angle is not None:
+        st.angle.uniform_(-3.0, 3.0, generator=g)
+    cache.conv.copy_(torch.randn(cache.conv.shape, device=DEV, generator=g).to(torch.bfloat16))
+    return cache
+
+
+def _same_cache(a, b, step):
+    for name in ("h", "last_u", "x_prev", "b_prev", "angle"):
+        x, y = getattr(a.ssm, name, None), getattr(b.ssm, name, None)
+        if x is not None:
+            assert torch.equal(x, y), (step, name)
+    assert torch.equal(a.conv, b.conv), (step, "conv history")
+
+
+@pytest.mark.parametrize("H,P,N,R,rot,learned,factored,post_norm", FUSED_CONV_CASES)
+def test_fused_conv_mixer_step_equals_the_composed_calls(H, P, N, R, rot, learned, factored,
+                                                         post_norm):
+    """Mamba3Mixer.step_ with the reference-default convolution (k = 4) takes
+    m3_mixer_step_conv: the convolution, its in-place history update, the
+    state step and the gate in one launch (with a post-gate norm, the gate
+    with the norm as a second).  Against m3_mixer_prologue_conv + m3_step (or
+    m3_step_factored) + m3_mixer_gate on the same layer and cache: outputs,
+    every state tensor and the history equal bit for bit over three steps, and
+    the step issues 3 launches with its projections (4 with the norm) where
+    the composed calls issue 5."""
+    _lib = lib()
+    L = _lib.lib()
+    mixer, rng = _conv_mixer(H, P, N, R, rot, learned, post_norm, seed=900 + H + N + R)
+    B = 5
+    g = torch.Generator(device=DEV).manual_seed(int(rng.integers(1 << 30)))
+    cache = _random_cache(mixer, B, factored, g)
+    fused, composed = cache.clone(), cache.clone()
+    for step in range(3):
+        x = (torch.randn(B, 1, 32, device=DEV, generator=g) * 0.5).to(torch.bfloat16)
+        mixer._fused_step_ok = None
+        n0 = L.m3_launch_count()
+        ya = mixer.step_(x, fused)
+        n1 = L.m3_launch_count()
+        assert mixer._fused_step_ok, "the shapes should take the fused step"
+        mixer._fused_step_ok = False
+        yb = mixer.step_(x, composed)
+        n2 = L.m3_launch_count()
+        torch.cuda.synchronize()
+        assert (n1 - n0, n2 - n1) == (3 + post_norm, 5), (n1 - n0, n2 - n1)
+        assert torch.equal(ya, yb), (step, (ya.float() - yb.float()).abs().max().item())
+        _same_cache(fused, composed, step)
+
+
+def test_fused_conv_step_with_shared_groups_writes_a_separate_history():
+    """groups < heads: B and C channels are shared by several heads'
+    workgroups, so m3_mixer_step_conv takes the new history in a separate
+    buffer (in place it reports M3_ERR_UNSUPPORTED, and Mamba3Mixer.step_
+    composes the calls).  Against the composed calls: outputs, states and the
+    new history equal bit for bit, and the old history is left as it was."""
+    import ctypes as C
+    _lib = lib()
+    L = _lib.lib()
+    H, G, P, N, R = 8, 2, 16, 32, 1
+    mixer, rng = _conv_mixer(H, P, N, R, True, True, False, groups=G, seed=950)
+    c = mixer.cfg
+    B = 6
+    g = torch.Generator(device=DEV).manual_seed(951)
+    cache = _random_cache(mixer, B, False, g)
+    fused, composed = cache.clone(), cache.clone()
+    x = (torch.randn(B, 1, 32, device=DEV, generator=g) * 0.5).to(torch.bfloat16)
+    mixer._fused_step_ok = None
+    yb = mixer.step_(x, composed)           # composes: the in-place history needs G == H
+    assert mixer._fused_step_ok is None
+    projected = mixer.in_proj.apply(x)
+    old = fused.conv.clone()
+    new_hist = torch.full_like(fused.conv, 7.0)
+    gated = torch.empty((B, 1, c.d_inner()), dtype=torch.bfloat16, device=DEV)
+    st = fused.ssm
+    sc = _lib.SsmStateC(st.h.data_ptr(), st.last_u.data_ptr(), st.angle.data_ptr())
+    ptr = lambda t: None if t is None else t.data_ptr()
+    dims = mixer._dims(B)
+
+    def call(new):
+        conv = _lib.Conv1dC(4, 1, mixer.conv_weight.data_ptr(), ptr(mixer.conv_bias),
+                            fused.conv.data_ptr(), new.data_ptr())
+        return int(L.m3_mixer_step_conv(
+            C.byref(dims), C.byref(conv), projected.data_ptr(), mixer.dt_bias.data_ptr(),
+            ptr(mixer.b_bias), ptr(mixer.c_bias), mixer.bc_norm.weight.data_ptr(),
+            mixer.a_log.data_ptr(), ptr(mixer.d_skip), None, C.c_float(1e-5), C.byref(sc), None,
+            gated.data_ptr(), None))
+
+    assert call(fused.conv) == _lib.M3_ERR_UNSUPPORTED
+    assert call(new_hist) == _lib.M3_OK
+    ya = mixer.out_proj.apply(gated)
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yb), (ya.float() - yb.float()).abs().max().item()
+    assert torch.equal(new_hist, composed.conv)
+    assert torch.equal(fused.conv, old)
+    assert torch.equal(fused.ssm.h, composed.ssm.h)
+    assert torch.equal(fused.ssm.last_u, composed.ssm.last_u)
+    assert torch.equal(fused.ssm.angle, composed.ssm.angle)
