@@ -5,8 +5,9 @@ H=12, P=64, N=128, chunk 64, bf16 storage with f32 accumulation, Rotational
 dynamics with a learned trapezoid -- as whole-job tokens/s on one GPU.  A step
 is one m3_scan call over the batch with every input already resident in HBM.
 
-The scan runs as the library's chunk-parallel path (three kernels over a
-workspace from torch's allocator, allocated outside the timed region); the
+The scan runs as the library's chunk-parallel path over a workspace from
+torch's allocator, allocated outside the timed region: at config 1 the fused
+single launch (--scan-path three selects the three launches); the
 single-pass kernel's time on the same inputs is reported beside it.
 
 Also reported on the same line:
@@ -52,14 +53,15 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA, TFLOP/s
 
-# HBM-side bytes of one headline scan call (chunk_state + state_pass +
-# chunk_scan) and the MFMA-busy fraction of its two MFMA kernels, from
-# profiles/scan_config1_kernels.txt (rocprofv3 FETCH_SIZE / WRITE_SIZE per
-# dispatch scaled by a 256 MiB copy, SQ_VALU_MFMA_BUSY_CYCLES over
-# GRBM_GUI_ACTIVE): 282.0 MB read + 57.3 MB written.  Counters cannot be read
-# inside this process; re-measured when the kernels change.
-SCAN_TRAFFIC_BYTES = 339_300_000
-SCAN_MFMA_BUSY = {"chunk_scan_dma_kernel": 0.077, "chunk_state_dma_kernel": 0.037}
+# HBM-side bytes of one headline scan call and the MFMA-busy fraction of its
+# kernel, from profiles/scan_config1_kernels.txt (rocprofv3 FETCH_SIZE /
+# WRITE_SIZE per dispatch scaled by a 256 MiB copy, SQ_VALU_MFMA_BUSY_CYCLES
+# over GRBM_GUI_ACTIVE).  At config 1 the library runs the fused single
+# launch (chunk_scan_fused_kernel): 205.5 MB read + 107.0 MB written.
+# Counters cannot be read inside this process; re-measured when the kernels
+# change.
+SCAN_TRAFFIC_BYTES = 312_600_000
+SCAN_MFMA_BUSY = {"chunk_scan_fused_kernel": 0.044}
 
 # BASELINE config 1 (the headline) and config 3 (decode)
 SCAN = dict(B=8, L=2048, H=12, P=64, N=128, R=1, Q=64)
@@ -963,8 +965,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": SCAN_TRAFFIC_BYTES,
-                     "kernel": "m3_scan: chunk_state_dma_kernel + state_pass_kernel + "
-                               "chunk_scan_dma_kernel (one scan call)",
+                     "kernel": "m3_scan: chunk_scan_fused_kernel (one launch a call: each "
+                               "128-token segment's state, the look-back for the state "
+                               "entering it, its outputs)",
                      "kernel_us": round(sc["kernel_ms"] * 1e3, 2),
                      "input_sets": sc["sets"], "input_MB_total": sc["input_MB"],
                      "kernel_us_resident_inputs": round(sc_res["kernel_ms"] * 1e3, 2),

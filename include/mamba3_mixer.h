@@ -166,7 +166,8 @@ m3_status m3_mixer_step(const m3_mixer_dims *d, const void *projected, const flo
  * norm, such as the reference's default mixer (conv_kernel Some(4),
  * src/ssm/config.rs:143) stepped by Mamba3Mixer::step
  * (src/models/mamba3.rs:569-630) with its history update
- * (src/tensor/ops/fused.rs:833-865).  conv (or NULL) has seq_len 1: x, B and
+ * (src/tensor/ops/fused.rs:833-865).  conv (or NULL) has seq_len 1 and at
+ * most 4 taps (more: M3_ERR_UNSUPPORTED, compose the calls): x, B and
  * C come from the convolution over history ++ this token, as
  * m3_mixer_prologue_conv computes them, and new_history receives the last
  * k-1 positions.  new_history may be history itself (the cache updated in

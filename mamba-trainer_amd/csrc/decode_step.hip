@@ -31,6 +31,7 @@ namespace {
 
 constexpr int kStepThreads = 256;
 constexpr int kMaxRank = 8;        // register-resident y partials per row
+constexpr int kStepConvTaps = static_cast<int>(kMixerStepConvTaps);
 
 template <typename T>
 __device__ __forceinline__ float ld(const void *p, size_t i) {
@@ -117,29 +118,59 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
 
 // Eight channels ch .. ch+7 of the causal convolution over [x | B | C] (px
 // is this sequence's row from x on) at its one position: taps 0 .. k-2 read
-// the history, tap k-1 the row (conv_taps8: the same arithmetic as
-// m3_mixer_prologue_conv).  With `write`, the lane then stores the new
-// history of these channels, the window's last k-1 positions: row i takes
-// the old row i+1, the last row this token.  The lane reads every old row of
-// its channels before it writes any and copies in ascending order, so the
-// history may be updated in place where no other lane or workgroup reads
-// these channels (the host allows that only for groups == heads, where every
-// channel belongs to one (sequence, head) workgroup).
+// the history, tap k-1 the row, with the arithmetic of conv_taps8 (the same
+// fused multiply-adds in the same order as m3_mixer_prologue_conv).  Every
+// tap's inputs and weights are loaded before the first is used (k is at most
+// kStepConvTaps; the host checks), so the lane waits for memory once.  With
+// `write`, the lane then stores the new history of these channels from the
+// values it holds, the window's last k-1 positions: row i takes the old row
+// i+1, the last row this token.  The lane has read every old row of its
+// channels before it writes any, so the history may be updated in place
+// where no other lane or workgroup reads these channels (the host allows
+// that only for groups == heads, where every channel belongs to one
+// (sequence, head) workgroup).
 __device__ __forceinline__ void step_conv8(const MixerStepLaunch &m, size_t bq, size_t C,
                                            const uint16_t *px, size_t ch, bool write, float *f) {
-    const size_t k = m.conv_k;
+    const int k = static_cast<int>(m.conv_k);
     const uint16_t *hist =
         m.hist ? static_cast<const uint16_t *>(m.hist) + bq * (k - 1) * C : nullptr;
-    mixm::conv_taps8(m.conv_w, m.conv_b, C, k, ch, [&](size_t j) -> const uint16_t * {
-        return j + 1 == k ? px + ch : hist ? hist + j * C + ch : nullptr;
-    }, f);
+    uint4 raw[kStepConvTaps];
+    float4 w0[kStepConvTaps], w1[kStepConvTaps];
+#pragma unroll
+    for (int j = 0; j < kStepConvTaps; ++j) {
+        if (j < k) {
+            const uint16_t *src = j + 1 == k ? px + ch : hist ? hist + j * C + ch : nullptr;
+            raw[j] = src ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0u, 0u, 0u, 0u);
+            w0[j] = *reinterpret_cast<const float4 *>(m.conv_w + j * C + ch);
+            w1[j] = *reinterpret_cast<const float4 *>(m.conv_w + j * C + ch + 4);
+        }
+    }
+    if (m.conv_b) {
+        const float4 b0 = *reinterpret_cast<const float4 *>(m.conv_b + ch);
+        const float4 b1 = *reinterpret_cast<const float4 *>(m.conv_b + ch + 4);
+        f[0] = b0.x; f[1] = b0.y; f[2] = b0.z; f[3] = b0.w;
+        f[4] = b1.x; f[5] = b1.y; f[6] = b1.z; f[7] = b1.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kStepConvTaps; ++j) {
+        // a position before the sequence with no history is skipped, as conv_taps8 does
+        if (j < k && (hist != nullptr || j + 1 == k)) {
+            float v[8];
+            mixm::unpack8(raw[j], v);
+            const float wv[8] = {w0[j].x, w0[j].y, w0[j].z, w0[j].w,
+                                 w1[j].x, w1[j].y, w1[j].z, w1[j].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = __builtin_fmaf(wv[e], v[e], f[e]);
+        }
+    }
     if (!write || m.new_hist == nullptr) return;
     uint16_t *nh = static_cast<uint16_t *>(m.new_hist) + bq * (k - 1) * C;
-    for (size_t i = 0; i + 1 < k; ++i) {
-        const uint16_t *src = i + 2 < k ? (hist ? hist + (i + 1) * C + ch : nullptr) : px + ch;
-        const uint4 v = src ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4 *>(nh + i * C + ch) = v;
-    }
+#pragma unroll
+    for (int i = 0; i + 1 < kStepConvTaps; ++i)
+        if (i + 1 < k) *reinterpret_cast<uint4 *>(nh + i * C + ch) = raw[i + 1];
 }
 
 // The fused step's prologue (MixerStepLaunch): the projection row of this

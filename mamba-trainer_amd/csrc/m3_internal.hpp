@@ -64,6 +64,8 @@ struct MixerStepLaunch {
 // of 8 with d_state / 8 a power of two, head_dim * rank and the row width
 // multiples of 8) and the vector step body's (rank 1, 2, 4 or 8).
 bool mixer_step_supported(size_t head_dim, size_t d_state, size_t rank, size_t width);
+// Convolution taps the fused step holds in registers (the reference default is 4).
+constexpr size_t kMixerStepConvTaps = 4;
 hipError_t launch_mixer_step(const MixerStepLaunch &a, hipStream_t stream);
 constexpr size_t kStepLayersPerLaunch = 24;
 struct StepLayerTable {

@@ -247,6 +247,10 @@ m3_status mixer_step_call(const m3_mixer_dims *d, const m3_conv1d *conv, const v
         if (conv->kernel_size < 2)   // config.rs:237-243
             return m3::api_fail(M3_ERR_CONFIG, "conv_kernel must be at least 2, got %zu",
                                 conv->kernel_size);
+        if (conv->kernel_size > m3::kMixerStepConvTaps)
+            return m3::api_fail(M3_ERR_UNSUPPORTED, "%s holds up to %zu convolution taps, got "
+                                "conv_kernel %zu: compose m3_mixer_prologue_conv, m3_step and "
+                                "m3_mixer_gate", fn, m3::kMixerStepConvTaps, conv->kernel_size);
         if (conv->seq_len != 1)
             return m3::api_fail(M3_ERR_SHAPE, "%s steps one position per sequence (seq_len 1), "
                                 "got seq_len %zu", fn, conv->seq_len);

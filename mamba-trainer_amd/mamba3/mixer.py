@@ -296,7 +296,9 @@ class Mamba3Mixer:
             return None
         hist = None
         if self.conv_weight is not None:
-            if c.n_groups != c.n_heads:
+            # the fused step holds up to 4 taps, and updates the history in
+            # place only where every channel belongs to one head
+            if c.n_groups != c.n_heads or c.conv_kernel > 4:
                 return None
             if cache.conv is None:
                 cache.conv = self._history(B, input.device)

@@ -323,8 +323,8 @@ def test_conv_mixer_step_history_rules_before_any_launch():
     """m3_mixer_step_conv's host-side checks on an empty call (the pointers are
     stand-ins that are never dereferenced): one position per sequence, a
     history updated in place only where every channel belongs to one head
-    (groups == heads), 16-byte aligned convolution buffers, and a
-    non-negative post-gate norm eps."""
+    (groups == heads), at most 4 taps, 16-byte aligned convolution buffers,
+    and a non-negative post-gate norm eps."""
     import ctypes as C
     from mamba3 import _lib
     L = _lib.lib()
@@ -346,6 +346,7 @@ def test_conv_mixer_step_history_rules_before_any_launch():
     assert call(G=2, new=(1 << 20) + 3 * chans * 2 * 4) == _lib.M3_OK   # separate, G < H
     assert call(seq=2) == _lib.M3_ERR_SHAPE
     assert call(k=1) == _lib.M3_ERR_CONFIG
+    assert call(k=5) == _lib.M3_ERR_UNSUPPORTED                   # more taps than it holds
     assert call(w=None) == _lib.M3_ERR_ARGUMENT
     assert call(bias=(1 << 12) + 4) == _lib.M3_ERR_ARGUMENT       # unaligned bias
     assert call(conv=False, norm=1 << 12, eps=-1.0) == _lib.M3_ERR_CONFIG
