@@ -1655,6 +1655,426 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     }   // sub-chunks
 }
 
+// ================================================================ chunk scan, rank 4
+// Raw token tiles of the rank-4 (MIMO) inputs.  A row is one token as it lies
+// in memory: B and C rows hold [n][r], the four ranks of one state index in
+// 8 bytes; X rows [p][r]; theta rows [pair].  Chunk m (16 bytes) of row t
+// sits at chunk m ^ msw(t) of the row.  The operands of the products are
+// read straight from this layout:
+//   - band and carry-in: rows rho = (token, rank) with k = n.  In one
+//     transposed read (ds_read_b64_tr_b16) lane 4 i + m of a 16-lane group
+//     points at the ranks of n_i of token m; lane 4 m' + r then receives n_0
+//     .. n_3 of row (token m', rank r): rows (token, rank) in rank-fastest
+//     order with no rearranging of the tile;
+//   - B~^T and X^T (rows n or p, k = rho): the four ranks of one n (p) of a
+//     token are the four consecutive k of that token, one 8-byte read.
+// msw rotates the token's four low bits, so that 16 consecutive tokens reading
+// one chunk (the stage), and each 32-lane half of the transposed reads (four
+// tokens, two k-groups, two chunks) and of the 8-byte reads (two tokens,
+// sixteen columns), land in 16 distinct chunks of a 256-byte window.
+__device__ __forceinline__ int msw(int t) { return ((t & 3) << 2) | ((t >> 2) & 3); }
+template <int CH>
+__device__ __forceinline__ int mt_off(int t, int chunk) {
+    return t * CH * 16 + ((chunk ^ msw(t)) << 4);
+}
+// Rows of CH chunks (32 or 64), 1 KB per load instruction.
+template <int CH>
+__device__ __forceinline__ void lds_load_mrows(rsrc_t r, uint32_t first, uint32_t stride,
+                                               unsigned char *tile, int I, int lane) {
+    static_assert(CH == 32 || CH == 64, "rows of 512 or 1024 bytes");
+    const int t = I * (64 / CH) + lane / CH;
+    const int m = (lane % CH) ^ msw(t);
+    lds_dma16(r, lds_addr(tile + I * 1024), first + static_cast<uint32_t>(t) * stride + m * 16);
+}
+// theta rows of CT chunks (8 or 4; 128 or 64 bytes), chunk m at m ^ tsw(t):
+// the stage's 16 tokens reading one pair slice then fill a 256-byte window.
+// Four bytes a lane, 256 bytes per load instruction.
+template <int CT>
+__device__ __forceinline__ int tsw(int t) {
+    static_assert(CT == 8 || CT == 4, "theta rows of 128 or 64 bytes");
+    return CT == 8 ? (t >> 1) & 7 : (t >> 2) & 3;
+}
+template <int CT>
+__device__ __forceinline__ void lds_load_trows(rsrc_t r, uint32_t first, uint32_t stride,
+                                               unsigned char *tile, int I, int lane) {
+    constexpr int TB = CT * 16;
+    const int t = I * (256 / TB) + (lane * 4) / TB;
+    const int pos = ((lane * 4) % TB) >> 4;
+    lds_dma4(r, lds_addr(tile + I * 256),
+             first + static_cast<uint32_t>(t) * stride + ((pos ^ tsw<CT>(t)) << 4) + 4 * (lane & 3));
+}
+// Eight k-slots of a rank-4 operand row by two transposed reads of a B / C
+// tile: lane 4 i + m of each 16-lane group points at n = n0 + i (and n0 + 16
+// + i) of token t0 + m.
+template <int CB>
+__device__ __forceinline__ bf16x8 mimo_tr(const unsigned char *tile, int t0, int m, int n0,
+                                          int i) {
+    const int t = t0 + m;
+    const int na = n0 + i, nb = n0 + 16 + i;
+    const bf16x4 lo = lds_read_tr16(
+        reinterpret_cast<const __bf16 *>(tile + mt_off<CB>(t, na >> 1) + ((na & 1) << 3)));
+    const bf16x4 hi = lds_read_tr16(
+        reinterpret_cast<const __bf16 *>(tile + mt_off<CB>(t, nb >> 1) + ((nb & 1) << 3)));
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+// The four ranks of index col (n or p) of tokens t and t + 1 as one operand
+// fragment: k-slots 4 e + r = (token t + e, rank r).
+template <int CH>
+__device__ __forceinline__ bf16x8 mimo_pair(const unsigned char *tile, int t, int col) {
+    const int o = ((col & 1) << 3);
+    const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(tile + mt_off<CH>(t, col >> 1) + o);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(tile + mt_off<CH>(t + 1, col >> 1) + o);
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+template <int N>
+struct ScanMimoSmem {
+    static constexpr int CB = N / 2, CX = kP / 2, CT = N / 16;   // chunks per row
+    static constexpr int LDM = 64 + 8;                           // band row stride
+    static constexpr int RX = 16 * CX * 16;                      // an X tile
+    static constexpr int RB = RX > 64 * LDM * 2 ? RX : 64 * LDM * 2;
+    static_assert(16 * CT * 16 <= RB, "theta fits a region");
+    unsigned char b[16 * CB * 16];    // B, then B~ [t][n][r]
+    unsigned char c[16 * CB * 16];    // C, then C~ [t][n][r]
+    unsigned char r[2][RB];           // theta, then the band (C~ B~^T o L)[rho][sigma]; X [t][p][r]
+    float acum[16], gw[16], ww[16], wdv[16];
+};
+
+// chunk_scan_kernel for bf16 storage at rank 4: the sub-chunk's 16 tokens x
+// 4 ranks are the 64 rows rho = 4 t + r of the same products, with B, C,
+// theta and X staged by coalesced direct-to-LDS loads of whole token rows
+// into the tiles above and pipelined one sub-chunk ahead as in
+// chunk_scan_dma_kernel (the same regions, waits and barriers).  The stage
+// rotates B and C in place; each lane owns a token and PPT pairs, its 16-lane
+// row the row's pairs for all 16 tokens (the angle prefix runs along the row).
+// The state entering the segment is carried in f32 across the sub-chunks.
+template <int N>
+__global__ void __launch_bounds__(kThreads, 3)
+chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
+    constexpr int P = kP;
+    constexpr int QT = 16;            // tokens of a sub-chunk (64 rows)
+    using S = ScanMimoSmem<N>;
+    constexpr int CB = S::CB, CX = S::CX, CT = S::CT, LDM = S::LDM;
+    constexpr int RBB = CB * 16;      // bytes per B / C row
+    constexpr int NH = N / 2;         // rotation pairs
+    constexpr int PW = NH / 4;        // pairs per wave
+    constexpr int PPT = PW / 4;       // pairs per lane (one per 16-lane row)
+    constexpr int NT = 4;             // 16-row tiles of a sub-chunk
+    constexpr int NTN = N / 16;       // n-tiles of the state
+    constexpr int NKB = N / 32;       // k-blocks of n
+    static_assert(PPT == 4 || PPT == 2, "two or four pairs a lane");
+    // loads a wave issues per sub-chunk: B or C rows, theta, X
+    constexpr int kLB = 16 * RBB / 1024 / 4, kLT = 16 * CT * 16 / 256 / 4, kLX = 16 * CX * 16 / 1024 / 4;
+    static_assert(kLB >= 1 && kLT >= 1 && kLX >= 1, "loads spread over four waves");
+    constexpr int kC = kLB + 4, kX = kLX;
+
+    __shared__ __attribute__((aligned(16))) S sm;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    const size_t H = a.heads, L = a.seq;
+    const size_t bhs = blockIdx.x;
+    const int seg = static_cast<int>(bhs % nseg);
+    const size_t bh = bhs / nseg;
+    const size_t bb = bh / H, hh = bh % H;
+    const SeqBufs rs = seq_bufs<bf16_t, N, P, 4>(a, bb, hh);
+    const int h_end = min(kseg, nsub - seg * kseg);
+
+    // the state entering this segment, in its frame: S^T tiles in the D
+    // layout (n = 16 i + 4 g + r, p = 16 wave + c), carried in f32
+    f32x4 sacc[NTN];
+    {
+        const __bf16 *src = static_cast<const __bf16 *>(ws.s) + (bhs * 4 + wave) * NTN * 256;
+#pragma unroll
+        for (int i = 0; i < NTN; ++i) {
+            const bf16x4 v = *reinterpret_cast<const bf16x4 *>(src + rec_off<NTN>(i, lane));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sacc[i][r] = static_cast<float>(v[r]);
+        }
+    }
+    float A = 0.0f;
+    if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);
+    const float dskip = a.d_skip ? a.d_skip[hh] : 0.0f;
+    // running pair angles of this lane's row, in turns (every lane of a row
+    // holds the same values)
+    float run[PPT];
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) run[j] = 0.0f;
+
+    auto load_c = [&](int k, TokScalars &sc) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < kLB; ++q)
+            lds_load_mrows<CB>(rs.c, tok0 * rs.tok_bc, rs.tok_bc, sm.c, wave + 4 * q, lane);
+        const uint32_t tok = tok0 + (lane & 15);
+        sc.s0 = bldf(rs.s0, tok * rs.tok_s);
+        sc.s1 = bldf(rs.s1, tok * rs.tok_s);
+        sc.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
+        sc.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
+    };
+    auto load_bt = [&](int k) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < kLB; ++q)
+            lds_load_mrows<CB>(rs.b, tok0 * rs.tok_bc, rs.tok_bc, sm.b, wave + 4 * q, lane);
+#pragma unroll
+        for (int q = 0; q < kLT; ++q)
+            lds_load_trows<CT>(rs.th, tok0 * rs.tok_th, rs.tok_th, sm.r[k & 1], wave + 4 * q, lane);
+    };
+    auto load_x = [&](int k) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < kLX; ++q)
+            lds_load_mrows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.r[(k & 1) ^ 1], wave + 4 * q, lane);
+    };
+
+    TokScalars sc_next;
+    load_c(seg * kseg, sc_next);
+    load_bt(seg * kseg);
+    load_x(seg * kseg);
+
+#pragma unroll 1
+    for (int h = 0; h < h_end; ++h) {
+    int lane_v = lane;
+    asm volatile("" : "+v"(lane_v));
+    const int lane = lane_v;
+    const int g = lane >> 4;
+    const int c = lane & 15;
+    const int m = c & 3, i4 = c >> 2;   // transposed reads: lane 4 i4 + m
+    const int sck = seg * kseg + h;
+    const int par = sck & 1;
+    const uint32_t tok0 = static_cast<uint32_t>(sck) * QT;
+    const bool more = h + 1 < h_end;
+
+    // B, C, theta and the scalars of this sub-chunk landed (X may be out)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm<kX>());
+    __syncthreads();
+    const TokScalars sc = sc_next;
+    unsigned char *const rth = sm.r[par];         // theta, then the band
+    unsigned char *const rx = sm.r[par ^ 1];      // X
+    __bf16 *const ms = reinterpret_cast<__bf16 *>(rth);
+
+    // lane c of every row holds token c
+    const bool live = tok0 + c < L;
+    float av, gv, wv;
+    token_scalars(a, sc, A, live, av, gv, wv);
+    const float acum = seg_scan<16>(av);
+    if (wave == 0 && g == 0) {
+        sm.acum[c] = acum * kLog2e;   // log2 units, as dexp2 takes them
+        sm.gw[c] = gv;
+        sm.ww[c] = wv;
+        const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
+        sm.wdv[c] = dexp<true>(last - acum) * wv;   // w x decay to the end
+    }
+    const float dtt = live ? sc.s0 * 0.15915494309189533577f : 0.0f;
+
+    // ---- stage: this lane's PPT pairs at its token: the angle within the
+    //      segment, its sine and cosine, and B and C rotated by its negative
+    //      (fused.rs:610-617), written back in place
+    {
+        const int i0 = wave * PW + g * PPT;
+        const unsigned char *tp = rth + (c * CT * 16) + ((((2 * i0) >> 4) ^ tsw<CT>(c)) << 4) + ((2 * i0) & 15);
+        float pre[PPT];
+        if constexpr (PPT == 4) {
+            const u32x2 tv = *reinterpret_cast<const u32x2 *>(tp);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const unsigned int w = tv[j >> 1];
+                pre[j] = dtt * __uint_as_float((j & 1) ? (w & 0xFFFF0000u) : (w << 16));
+            }
+            seg_scan4<16>(pre[0], pre[1], pre[2], pre[3]);
+        } else {
+            const unsigned int w = *reinterpret_cast<const unsigned int *>(tp);
+            pre[0] = seg_scan<16>(dtt * __uint_as_float(w << 16));
+            pre[1] = seg_scan<16>(dtt * __uint_as_float(w & 0xFFFF0000u));
+        }
+        float cs[PPT], sn[PPT];
+#pragma unroll
+        for (int j = 0; j < PPT; ++j) {
+            const float r = run[j] + pre[j];
+            const float w = r - __builtin_rintf(r);
+            run[j] = dpp_f<0x15F, 0xf, false>(w);   // row_newbcast:15, the row's last token
+            sn[j] = __builtin_amdgcn_sinf(w);
+            cs[j] = __builtin_amdgcn_cosf(w);
+        }
+#pragma unroll
+        for (int v = 0; v < PPT / 2; ++v) {
+            const int olo = mt_off<CB>(c, i0 / 2 + v), ohi = mt_off<CB>(c, i0 / 2 + v + NH / 2);
+#pragma unroll
+            for (int which = 0; which < 2; ++which) {
+                unsigned char *tile = which == 0 ? sm.b : sm.c;
+                u32x4 vv[2], out[2];
+                vv[0] = *reinterpret_cast<const u32x4 *>(tile + olo);
+                vv[1] = *reinterpret_cast<const u32x4 *>(tile + ohi);
+                // element e: n = i0 + 2 v + (e >> 2) (pair 2 v + (e >> 2) of this lane), rank e & 3
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const int j = 2 * v + (e >> 2);
+                    float o[2][2];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const float v1 = elem<bf16_t>(vv, e + u), v2 = elem<bf16_t>(vv + 1, e + u);
+                        o[0][u] = v1 * cs[j] + v2 * sn[j];
+                        o[1][u] = -v1 * sn[j] + v2 * cs[j];
+                    }
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) out[hf][e >> 1] = pk_bf16(o[hf][0], o[hf][1]);
+                }
+                *reinterpret_cast<u32x4 *>(tile + olo) = out[0];
+                *reinterpret_cast<u32x4 *>(tile + ohi) = out[1];
+            }
+        }
+    }
+    __syncthreads();   // B~, C~ complete; theta is dead, its region takes the band
+
+    // ---- masked band into R[p]: tile (TJ, SI) of (C~ B~^T o L)[rho][sigma],
+    //      rho = 16 TJ + c (token 4 TJ + c / 4, rank c % 4), sigma = 16 SI +
+    //      4 g + r (token 4 SI + g, rank r), k = n in the order n = 32 kb +
+    //      16 (q / 4) + 4 g + q % 4 of k-slot q
+    {
+        auto tile = [&](auto tj_c, auto si_c) {
+            constexpr int TJ = decltype(tj_c)::value, SI = decltype(si_c)::value;
+            __bf16 *const dst = ms + (16 * TJ + c) * LDM + 16 * SI + 4 * g;
+            if constexpr (SI > TJ) {
+                const float z[4] = {0.f, 0.f, 0.f, 0.f};
+                st4(dst, z);
+            } else {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) {
+                    const bf16x8 bv = mimo_tr<CB>(sm.b, 4 * SI, m, 32 * kb + 4 * g, i4);
+                    const bf16x8 cv = mimo_tr<CB>(sm.c, 4 * TJ, m, 32 * kb + 4 * g, i4);
+                    acc = mfma_bf16(bv, cv, acc);
+                }
+                const int s = 4 * SI + g, t = 4 * TJ + (c >> 2);
+                const float wgt = sm.ww[s] * dexp2(sm.acum[t] - sm.acum[s]);
+                float vals[4];
+                if constexpr (SI < TJ) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) vals[r] = acc[r] * wgt;
+                } else {
+                    // the diagonal tile: s < t off-diagonal weight, s = t the
+                    // diagonal weight, plus the skip D on rho = sigma
+                    // (scan.rs:593-597)
+                    const float gs = sm.gw[s];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float dia = acc[r] * gs + (r == (c & 3) ? dskip : 0.0f);
+                        vals[r] = s < t ? acc[r] * wgt : (s == t ? dia : 0.0f);
+                    }
+                }
+                st4(dst, vals);
+            }
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I3 = std::integral_constant<int, 3>;
+        if (wave == 0) {
+            tile(I0{}, I0{}); tile(I2{}, I0{}); tile(I3{}, I0{});
+        } else if (wave == 1) {
+            tile(I0{}, I1{}); tile(I2{}, I1{}); tile(I3{}, I1{});
+        } else if (wave == 2) {
+            tile(I1{}, I0{}); tile(I2{}, I2{}); tile(I3{}, I2{});
+        } else {
+            tile(I1{}, I1{}); tile(I2{}, I3{}); tile(I3{}, I3{});
+        }
+    }
+    // ---- the carry-in product sum_n S[p][n] C~[rho][n] per rho-tile, k-slot
+    //      q of block kb at n = 32 kb + 16 (q / 4) + 4 g + q % 4: n-tiles 2 kb
+    //      and 2 kb + 1 of the state, as the lane holds them
+    f32x4 yc[NT];
+    {
+        bf16x8 sf[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sf[kb][r] = static_cast<__bf16>(sacc[2 * kb][r]);
+                sf[kb][4 + r] = static_cast<__bf16>(sacc[2 * kb + 1][r]);
+            }
+#pragma unroll
+        for (int tj = 0; tj < NT; ++tj) yc[tj] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int tj = 0; tj < NT; ++tj)
+                yc[tj] = mfma_bf16(sf[kb], mimo_tr<CB>(sm.c, 4 * tj, m, 32 * kb + 4 * g, i4), yc[tj]);
+#pragma unroll
+        for (int tj = 0; tj < NT; ++tj) yc[tj] = yc[tj] * dexp2(sm.acum[4 * tj + (c >> 2)]);
+    }
+    __syncthreads();   // the band is complete; C~ is dead
+    if (more) load_c(sck + 1, sc_next);
+    // X landed (the next sub-chunk's C and scalars may be out)
+    if (more)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm<kC>());
+    else
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+    __syncthreads();
+
+    // ---- X^T operand fragments (p = 16 wave + c, k-slot q of block kb at
+    //      rho = 32 kb + 8 g + q: token 8 kb + 2 g + q / 4, rank q % 4)
+    bf16x8 xf[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) xf[kb] = mimo_pair<CX>(rx, 8 * kb + 2 * g, 16 * wave + c);
+
+    if (more) {
+        // ---- S' = e_h S + U_h, U_h^T[n][p] = sum_rho B~[rho][n] (w decay X^T)[p][rho]:
+        //      A operand B~^T (row n = 16 i + c, the k order of the X^T
+        //      fragments), B operand the weighted X^T (rounded to bf16 once)
+        const float eh = dexp2(sm.acum[QT - 1]);
+        bf16x8 xw[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                xw[kb][q] = static_cast<__bf16>(static_cast<float>(xf[kb][q]) *
+                                                sm.wdv[8 * kb + 2 * g + (q >> 2)]);
+        // every fragment read first, so the LDS reads stream back to back
+        bf16x8 bt[NTN][2];
+#pragma unroll
+        for (int i = 0; i < NTN; ++i)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) bt[i][kb] = mimo_pair<CB>(sm.b, 8 * kb + 2 * g, 16 * i + c);
+#pragma unroll
+        for (int i = 0; i < NTN; ++i) {
+            f32x4 st = sacc[i] * eh;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) st = mfma_bf16(bt[i][kb], xw[kb], st);
+            sacc[i] = st;
+        }
+        __syncthreads();   // B~ and X are dead
+        load_bt(sck + 1);
+    }
+
+    // ---- y^T[p][rho] = exp(acum_t) sum_n S[p][n] C~[rho][n] + sum_sigma X^T[p][sigma] M[rho][sigma]
+    {
+        const unsigned char *const mb = reinterpret_cast<const unsigned char *>(ms) + c * (LDM * 2) + 16 * g;
+#pragma unroll
+        for (int tj = 0; tj < NT; ++tj) {
+            f32x4 acc = yc[tj];
+            const int nkb = tj < 2 ? 1 : 2;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+                if (kb < nkb)
+                    acc = mfma_bf16(xf[kb], *reinterpret_cast<const bf16x8 *>(mb + tj * 16 * LDM * 2 + kb * 64), acc);
+            // row rho = 16 tj + c: token tok0 + 4 tj + c / 4, rank c % 4;
+            // p = 16 wave + 4 g + r.  Tokens past the sequence end fall
+            // outside the buffer: dropped.
+            const uint32_t oy = (tok0 + 4 * tj + (c >> 2)) * rs.tok_x + ((16 * wave + 4 * g) * 4 + (c & 3)) * 2;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bst2(from_f32<bf16_t>(acc[r]).bits, rs.y, oy + r * 8);
+        }
+    }
+    if (more) {
+        __syncthreads();   // every read of the band is done
+        load_x(sck + 1);
+    }
+    }   // sub-chunks
+}
+
 // ================================================================ fused single launch
 // The whole scan in one launch that reads its inputs once.  One workgroup per
 // segment of at most two sub-chunks (KS rows of 64 tokens), in three steps:
@@ -2634,6 +3054,10 @@ hipError_t launch_three(const ScanLaunch &a, char *base, hipStream_t s) {
         else
             hipLaunchKernelGGL((chunk_scan_dma_kernel<N, false>), dim3(bhs), dim3(kThreads), 0, s, a,
                                ws, sp.nsub, sp.kseg, sp.nseg);
+    } else if constexpr (sizeof(T) == 2 && R == 4) {
+        if (a.gate_z != nullptr) return hipErrorNotSupported;   // the caller gates separately
+        hipLaunchKernelGGL((chunk_scan_mimo_kernel<N>), dim3(bhs), dim3(kThreads), 0, s, a, ws,
+                           sp.nsub, sp.kseg, sp.nseg);
     } else {
         if (a.gate_z != nullptr) return hipErrorNotSupported;   // the caller gates separately
         hipLaunchKernelGGL((chunk_scan_kernel<T, N, R, ROWS, kPf>), dim3(bhs), dim3(kThreads), 0,
