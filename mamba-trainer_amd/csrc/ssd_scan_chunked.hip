@@ -2075,6 +2075,233 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     }   // sub-chunks
 }
 
+// chunk_state_kernel for bf16 storage at rank 4, on the token tiles of
+// chunk_scan_mimo_kernel: theta, X and the per-token scalars of the next
+// sub-chunk are fetched at the start of the current one (theta and X
+// double-buffered), B once the previous product has read it.  The stage
+// forms the angles from theta while B arrives, then rotates B (fused.rs:
+// 610-617) and weights it by w x decay-to-end in place; U's operands are
+// 8-byte reads of the tiles, (B~ w)^T rows n and X^T rows p, k = rho.
+template <int N>
+struct StateMimoSmem {
+    static constexpr int CB = N / 2, CX = kP / 2, CT = N / 16;   // chunks per row
+    unsigned char b[16 * CB * 16];        // B, then B~ w decay-to-end [t][n][r]
+    unsigned char th[2][16 * CT * 16];    // theta [t][pair]; the pair angle totals at the end
+    unsigned char x[2][16 * CX * 16];     // X [t][p][r]
+};
+
+template <int N>
+__global__ void __launch_bounds__(kThreads, 3)
+chunk_state_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
+    constexpr int P = kP;
+    constexpr int QT = 16;
+    using S = StateMimoSmem<N>;
+    constexpr int CB = S::CB, CX = S::CX, CT = S::CT;
+    constexpr int RBB = CB * 16;
+    constexpr int NH = N / 2, PW = NH / 4, PPT = PW / 4;
+    constexpr int NTN = N / 16;
+    static_assert(PPT == 4 || PPT == 2, "two or four pairs a lane");
+    constexpr int kLB = 16 * RBB / 1024 / 4, kLT = 16 * CT * 16 / 256 / 4, kLX = 16 * CX * 16 / 1024 / 4;
+    // loads a wave issues per sub-chunk: theta + X + the four scalars, and B
+    constexpr int kTX = kLT + kLX + 4, kB = kLB;
+
+    __shared__ __attribute__((aligned(16))) S sm;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    const size_t H = a.heads, L = a.seq;
+    const size_t bhs = blockIdx.x;
+    const int seg = static_cast<int>(bhs % nseg);
+    const size_t bh = bhs / nseg;
+    const size_t bb = bh / H, hh = bh % H;
+    const bool rot = a.theta != nullptr;
+    const SeqBufs rs = seq_bufs<bf16_t, N, P, 4>(a, bb, hh);
+
+    float A = 0.0f;
+    if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);   // a_log.exp().neg() (scan.rs:470-474)
+
+    auto load_tx = [&](int k, TokScalars &sc) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+        const int buf = k & 1;
+#pragma unroll
+        for (int q = 0; q < kLT; ++q)
+            lds_load_trows<CT>(rs.th, tok0 * rs.tok_th, rs.tok_th, sm.th[buf], wave + 4 * q, lane);
+#pragma unroll
+        for (int q = 0; q < kLX; ++q)
+            lds_load_mrows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.x[buf], wave + 4 * q, lane);
+        const uint32_t tok = tok0 + (lane & 15);
+        sc.s0 = bldf(rs.s0, tok * rs.tok_s);
+        sc.s1 = bldf(rs.s1, tok * rs.tok_s);
+        sc.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
+        sc.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
+    };
+    auto load_b = [&](int k) {
+        const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
+#pragma unroll
+        for (int q = 0; q < kLB; ++q)
+            lds_load_mrows<CB>(rs.b, tok0 * rs.tok_bc, rs.tok_bc, sm.b, wave + 4 * q, lane);
+    };
+
+    f32x4 uacc[NTN];
+#pragma unroll
+    for (int i = 0; i < NTN; ++i) uacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float eacc = 1.0f;
+    float run[PPT];   // running pair angles of this lane's row, in turns
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) run[j] = 0.0f;
+
+    const int h_end = min(kseg, nsub - seg * kseg);
+    TokScalars sc_next;
+    load_tx(seg * kseg, sc_next);
+    load_b(seg * kseg);
+#pragma unroll 1
+    for (int h = 0; h < h_end; ++h) {
+        int lane_v = lane;
+        asm volatile("" : "+v"(lane_v));
+        const int lane = lane_v;
+        const int g = lane >> 4;
+        const int c = lane & 15;
+        const int sck = seg * kseg + h;
+        const int buf = sck & 1;
+        const bool more = h + 1 < h_end;
+
+        // theta, X, scalars of this sub-chunk landed (only its B may be out)
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm<kB>());
+        __syncthreads();
+        const TokScalars sc = sc_next;
+        if (more) load_tx(sck + 1, sc_next);
+
+        const bool live = static_cast<size_t>(sck) * QT + c < L;
+        float av, gv, wv;
+        token_scalars(a, sc, A, live, av, gv, wv);
+        const float acum = seg_scan<16>(av);
+        const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acum), QT - 1));
+        const float wd = dexp<true>(last - acum) * wv;   // exp_decay(last, acum, w)
+        const float eh = dexp<true>(last);
+        const float dtt = live ? sc.s0 * 0.15915494309189533577f : 0.0f;
+
+        // ---- stage, first half: this lane's pair angles at its token and their
+        //      sines and cosines (theta only; B is still arriving)
+        const int i0 = wave * PW + g * PPT;
+        float cs[PPT], sn[PPT];
+        {
+            const unsigned char *tp = sm.th[buf] + (c * CT * 16) +
+                                      ((((2 * i0) >> 4) ^ tsw<CT>(c)) << 4) + ((2 * i0) & 15);
+            float pre[PPT];
+            if constexpr (PPT == 4) {
+                const u32x2 tv = *reinterpret_cast<const u32x2 *>(tp);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const unsigned int w = tv[j >> 1];
+                    pre[j] = dtt * __uint_as_float((j & 1) ? (w & 0xFFFF0000u) : (w << 16));
+                }
+                seg_scan4<16>(pre[0], pre[1], pre[2], pre[3]);
+            } else {
+                const unsigned int w = *reinterpret_cast<const unsigned int *>(tp);
+                pre[0] = seg_scan<16>(dtt * __uint_as_float(w << 16));
+                pre[1] = seg_scan<16>(dtt * __uint_as_float(w & 0xFFFF0000u));
+            }
+#pragma unroll
+            for (int j = 0; j < PPT; ++j) {
+                const float r = run[j] + pre[j];
+                const float w = r - __builtin_rintf(r);
+                run[j] = dpp_f<0x15F, 0xf, false>(w);   // row_newbcast:15, the row's last token
+                sn[j] = __builtin_amdgcn_sinf(w);
+                cs[j] = __builtin_amdgcn_cosf(w);
+            }
+        }
+        // B landed (the next sub-chunk's theta, X and scalars may be out)
+        if (more)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm<kTX>());
+        else
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+        __syncthreads();
+
+        // ---- stage, second half: B rotated by the negative angle and weighted,
+        //      back in place (element e of a chunk: n = i0 + 2 v + e / 4, rank e % 4)
+#pragma unroll
+        for (int v = 0; v < PPT / 2; ++v) {
+            const int olo = mt_off<CB>(c, i0 / 2 + v), ohi = mt_off<CB>(c, i0 / 2 + v + NH / 2);
+            u32x4 vv[2], out[2];
+            vv[0] = *reinterpret_cast<const u32x4 *>(sm.b + olo);
+            vv[1] = *reinterpret_cast<const u32x4 *>(sm.b + ohi);
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const int j = 2 * v + (e >> 2);
+                float o[2][2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const float b1 = elem<bf16_t>(vv, e + u), b2 = elem<bf16_t>(vv + 1, e + u);
+                    o[0][u] = (b1 * cs[j] + b2 * sn[j]) * wd;
+                    o[1][u] = (-b1 * sn[j] + b2 * cs[j]) * wd;
+                }
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) out[hf][e >> 1] = pk_bf16(o[hf][0], o[hf][1]);
+            }
+            *reinterpret_cast<u32x4 *>(sm.b + olo) = out[0];
+            *reinterpret_cast<u32x4 *>(sm.b + ohi) = out[1];
+        }
+        __syncthreads();
+
+        // ---- U = e_h U + U_h, U_h^T[n][p] = sum_rho (B~w)[rho][n] X[rho][p]
+        //      over p-tile = wave: A operand row n = 16 i + c, B operand column
+        //      p = 16 wave + c, k-slot q of block kb at rho = 32 kb + 8 g + q
+        {
+            bf16x8 xo[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) xo[kb] = mimo_pair<CX>(sm.x[buf], 8 * kb + 2 * g, 16 * wave + c);
+            bf16x8 bt[NTN][2];
+#pragma unroll
+            for (int i = 0; i < NTN; ++i)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) bt[i][kb] = mimo_pair<CB>(sm.b, 8 * kb + 2 * g, 16 * i + c);
+#pragma unroll
+            for (int i = 0; i < NTN; ++i) {
+                f32x4 acc = uacc[i] * eh;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) acc = mfma_bf16(bt[i][kb], xo[kb], acc);
+                uacc[i] = acc;
+            }
+        }
+        eacc *= eh;
+        __syncthreads();   // every read of B is done
+        if (more) load_b(sck + 1);
+    }
+
+    const size_t uo = (bhs * 4 + wave) * NTN * 256;
+#pragma unroll
+    for (int i = 0; i < NTN / 2; ++i) {   // both halves of a pair in one 16-byte store
+        bf16x8 q;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            q[r] = static_cast<__bf16>(uacc[i][r]);
+            q[4 + r] = static_cast<__bf16>(uacc[i + NTN / 2][r]);
+        }
+        *reinterpret_cast<bf16x8 *>(static_cast<__bf16 *>(ws.u) + uo + rec_off<NTN>(i, lane)) = q;
+    }
+    if (tid == 0) ws.eda[bhs] = eacc;
+    // the segment's angle total per pair (wrapped), with its cosine and sine,
+    // one thread per pair: each row's angles through LDS (theta is dead: the
+    // loop's last barrier followed every read, and no load is in flight)
+    float *psi = reinterpret_cast<float *>(sm.th[0]);
+    if ((lane & 15) == 0) {
+        const int i0 = wave * PW + (lane >> 4) * PPT;
+#pragma unroll
+        for (int j = 0; j < PPT; ++j) psi[i0 + j] = run[j];
+    }
+    __syncthreads();
+    if (tid < NH) {
+        const float tot = rot ? psi[tid] * 6.28318530717958647692f : 0.0f;   // turns -> radians
+        float ts = 0.0f, tc = 1.0f;
+        if (rot) sincosf(tot, &ts, &tc);
+        ws.phi[bhs * NH + tid] = tot;
+        ws.cph[bhs * NH + tid] = tc;
+        ws.sph[bhs * NH + tid] = ts;
+    }
+}
+
 // ================================================================ fused single launch
 // The whole scan in one launch that reads its inputs once.  One workgroup per
 // segment of at most two sub-chunks (KS rows of 64 tokens), in three steps:
@@ -3037,6 +3264,9 @@ hipError_t launch_three(const ScanLaunch &a, char *base, hipStream_t s) {
     const ChunkWs ws = chunk_ws(base, chunked_layout(bhs, N, sizeof(T) == 2));
     if constexpr (sizeof(T) == 2 && R == 1)
         hipLaunchKernelGGL((chunk_state_dma_kernel<N>), dim3(bhs), dim3(kThreads), 0, s, a, ws,
+                           sp.nsub, sp.kseg, sp.nseg);
+    else if constexpr (sizeof(T) == 2 && R == 4)
+        hipLaunchKernelGGL((chunk_state_mimo_kernel<N>), dim3(bhs), dim3(kThreads), 0, s, a, ws,
                            sp.nsub, sp.kseg, sp.nseg);
     else
         hipLaunchKernelGGL((chunk_state_kernel<T, N, R, ROWS, kPf>), dim3(bhs),
