@@ -1703,28 +1703,34 @@ __device__ __forceinline__ void lds_load_trows(rsrc_t r, uint32_t first, uint32_
     lds_dma4(r, lds_addr(tile + I * 256),
              first + static_cast<uint32_t>(t) * stride + ((pos ^ tsw<CT>(t)) << 4) + 4 * (lane & 3));
 }
-// Eight k-slots of a rank-4 operand row by two transposed reads of a B / C
-// tile: lane 4 i + m of each 16-lane group points at n = n0 + i (and n0 + 16
-// + i) of token t0 + m.
-template <int CB>
-__device__ __forceinline__ bf16x8 mimo_tr(const unsigned char *tile, int t0, int m, int n0,
-                                          int i) {
-    const int t = t0 + m;
-    const int na = n0 + i, nb = n0 + 16 + i;
-    const bf16x4 lo = lds_read_tr16(
-        reinterpret_cast<const __bf16 *>(tile + mt_off<CB>(t, na >> 1) + ((na & 1) << 3)));
-    const bf16x4 hi = lds_read_tr16(
-        reinterpret_cast<const __bf16 *>(tile + mt_off<CB>(t, nb >> 1) + ((nb & 1) << 3)));
+// Operand reads of the token tiles (rows of RB bytes).  Both kinds address a
+// lane offset XORed with a few constants, plus an immediate:
+//   - transposed: lane 4 i + m of each 16-lane group g points at n = 32 kb +
+//     16 h + 4 g + i of token 4 T + m: chunk 16 kb + 8 h + 2 g + i / 2, which
+//     msw(4 T + m) = 4 m + T sends to 16 kb + (tl ^ (8 h + T)) with tl =
+//     (2 g + i / 2) ^ 4 m; tb = m RB + 8 (i % 2).  Eight k-slots of the
+//     operand row (token 4 T + c / 4, rank c % 4): n = 32 kb + 16 (q / 4) +
+//     4 g + q % 4 for slot q.
+//   - 8-byte: column 16 (2 hi + f) + c of tokens 8 kb + 2 g + e (e = 0, 1;
+//     kb < 2): chunk 16 hi + 8 f + c / 2, which msw(8 kb + 2 g + e) = 8 (g %
+//     2) + 4 e + 2 kb + g / 2 sends to 16 hi + (pl ^ (8 f + 4 e + 2 kb)) with
+//     pl = (c / 2) ^ 8 (g % 2) ^ (g / 2); pb = 2 g RB + 8 (c % 2).  Slot q of
+//     the fragment is (token 8 kb + 2 g + q / 4, rank q % 4).
+template <int RB>
+__device__ __forceinline__ bf16x8 mimo_tr(const unsigned char *tile, int tl, int tb, int T, int kb) {
+    const unsigned char *base = tile + tb + 4 * T * RB + 256 * kb;
+    const bf16x4 lo = lds_read_tr16(reinterpret_cast<const __bf16 *>(base + ((tl ^ T) << 4)));
+    const bf16x4 hi = lds_read_tr16(reinterpret_cast<const __bf16 *>(base + ((tl ^ (8 + T)) << 4)));
     return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
-// The four ranks of index col (n or p) of tokens t and t + 1 as one operand
-// fragment: k-slots 4 e + r = (token t + e, rank r).
-template <int CH>
-__device__ __forceinline__ bf16x8 mimo_pair(const unsigned char *tile, int t, int col) {
-    const int o = ((col & 1) << 3);
-    const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(tile + mt_off<CH>(t, col >> 1) + o);
-    const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(tile + mt_off<CH>(t + 1, col >> 1) + o);
-    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+template <int RB>
+__device__ __forceinline__ bf16x8 mimo_pair(const unsigned char *tile, int pl, int pb, int kb, int hi,
+                                            int f) {
+    const int k0 = (8 * f) ^ (2 * kb);
+    const unsigned char *base = tile + pb + 8 * kb * RB + 256 * hi;
+    const bf16x4 a = *reinterpret_cast<const bf16x4 *>(base + ((pl ^ k0) << 4));
+    const bf16x4 b = *reinterpret_cast<const bf16x4 *>(base + RB + ((pl ^ k0 ^ 4) << 4));
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
 template <int N>
@@ -1843,6 +1849,10 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     const int g = lane >> 4;
     const int c = lane & 15;
     const int m = c & 3, i4 = c >> 2;   // transposed reads: lane 4 i4 + m
+    // lane parts of the operand offsets (mimo_tr, mimo_pair)
+    const int tl = (2 * g + (i4 >> 1)) ^ (m << 2), tb = m * RBB + ((i4 & 1) << 3);
+    const int pl = (c >> 1) ^ ((g & 1) << 3) ^ (g >> 1);
+    const int pbb = 2 * g * RBB + ((c & 1) << 3), pbx = 2 * g * (CX * 16) + ((c & 1) << 3);
     const int sck = seg * kseg + h;
     const int par = sck & 1;
     const uint32_t tok0 = static_cast<uint32_t>(sck) * QT;
@@ -1944,8 +1954,8 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb) {
-                    const bf16x8 bv = mimo_tr<CB>(sm.b, 4 * SI, m, 32 * kb + 4 * g, i4);
-                    const bf16x8 cv = mimo_tr<CB>(sm.c, 4 * TJ, m, 32 * kb + 4 * g, i4);
+                    const bf16x8 bv = mimo_tr<RBB>(sm.b, tl, tb, SI, kb);
+                    const bf16x8 cv = mimo_tr<RBB>(sm.c, tl, tb, TJ, kb);
                     acc = mfma_bf16(bv, cv, acc);
                 }
                 const int s = 4 * SI + g, t = 4 * TJ + (c >> 2);
@@ -2001,7 +2011,7 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int tj = 0; tj < NT; ++tj)
-                yc[tj] = mfma_bf16(sf[kb], mimo_tr<CB>(sm.c, 4 * tj, m, 32 * kb + 4 * g, i4), yc[tj]);
+                yc[tj] = mfma_bf16(sf[kb], mimo_tr<RBB>(sm.c, tl, tb, tj, kb), yc[tj]);
 #pragma unroll
         for (int tj = 0; tj < NT; ++tj) yc[tj] = yc[tj] * dexp2(sm.acum[4 * tj + (c >> 2)]);
     }
@@ -2018,7 +2028,7 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     //      rho = 32 kb + 8 g + q: token 8 kb + 2 g + q / 4, rank q % 4)
     bf16x8 xf[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) xf[kb] = mimo_pair<CX>(rx, 8 * kb + 2 * g, 16 * wave + c);
+    for (int kb = 0; kb < 2; ++kb) xf[kb] = mimo_pair<CX * 16>(rx, pl, pbx, kb, wave >> 1, wave & 1);
 
     if (more) {
         // ---- S' = e_h S + U_h, U_h^T[n][p] = sum_rho B~[rho][n] (w decay X^T)[p][rho]:
@@ -2037,7 +2047,7 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 #pragma unroll
         for (int i = 0; i < NTN; ++i)
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) bt[i][kb] = mimo_pair<CB>(sm.b, 8 * kb + 2 * g, 16 * i + c);
+            for (int kb = 0; kb < 2; ++kb) bt[i][kb] = mimo_pair<RBB>(sm.b, pl, pbb, kb, i >> 1, i & 1);
 #pragma unroll
         for (int i = 0; i < NTN; ++i) {
             f32x4 st = sacc[i] * eh;
@@ -2166,6 +2176,9 @@ chunk_state_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) 
         const int sck = seg * kseg + h;
         const int buf = sck & 1;
         const bool more = h + 1 < h_end;
+        // lane parts of the 8-byte operand offsets (mimo_pair)
+        const int pl = (c >> 1) ^ ((g & 1) << 3) ^ (g >> 1);
+        const int pbb = 2 * g * RBB + ((c & 1) << 3), pbx = 2 * g * (CX * 16) + ((c & 1) << 3);
 
         // theta, X, scalars of this sub-chunk landed (only its B may be out)
         __builtin_amdgcn_s_waitcnt(vmcnt_imm<kB>());
@@ -2251,12 +2264,12 @@ chunk_state_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) 
         {
             bf16x8 xo[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) xo[kb] = mimo_pair<CX>(sm.x[buf], 8 * kb + 2 * g, 16 * wave + c);
+            for (int kb = 0; kb < 2; ++kb) xo[kb] = mimo_pair<CX * 16>(sm.x[buf], pl, pbx, kb, wave >> 1, wave & 1);
             bf16x8 bt[NTN][2];
 #pragma unroll
             for (int i = 0; i < NTN; ++i)
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) bt[i][kb] = mimo_pair<CB>(sm.b, 8 * kb + 2 * g, 16 * i + c);
+                for (int kb = 0; kb < 2; ++kb) bt[i][kb] = mimo_pair<RBB>(sm.b, pl, pbb, kb, i >> 1, i & 1);
 #pragma unroll
             for (int i = 0; i < NTN; ++i) {
                 f32x4 acc = uacc[i] * eh;
@@ -3235,8 +3248,13 @@ SegPlan seg_plan(const ScanLaunch &a) {
     // 8 / 10 / 12 / 16 rounds, two passes on one box, 570-593 / 575-586 /
     // 556-574 / 573-596 / 581-590 / 596-603 / 596-615 / 594-609, against
     // 125.0 and 724.6 for one 64-token chunk per workgroup)
-    const size_t slots = device_cus() * (a.rank > 1 ? 2 : 3);
-    const size_t rounds = a.rank > 1 ? 6 : 1;
+    // The bf16 rank-4 kernels (direct-to-LDS token tiles, three chunk_scan
+    // workgroups per CU) take one round too: at config 2, in us per call,
+    // segments of 128 / 192 / 256 / 384 / 512 tokens (4 / 2.75 / 2 / 1.4 / 1
+    // rounds) measured 445 / 472 / 431 / 485 / 415.
+    const bool mimo4 = a.bf16 && a.rank == 4;
+    const size_t slots = device_cus() * (a.rank > 1 && !mimo4 ? 2 : 3);
+    const size_t rounds = a.rank > 1 && !mimo4 ? 6 : 1;
     // segments per sequence that fill the rounds without spilling into one
     // more, then the sub-chunks each needs
     const size_t bh = a.batch * a.heads;

@@ -205,6 +205,13 @@ def _three_launch_sizes(need, _lib):
     assert need(8, 2048, 12, 64, 128, 1, _lib.M3_BF16, chunk=1) == 8 * 12 * 8 * record
     # f32 storage: 32-token sub-chunks, 8 per segment, and f32 U and S
     assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) == 8 * 12 * 8 * (64 * 128 * 8 + 4 + 3 * 64 * 4)
+    # bf16 rank 4 (config 2: 96 sequences of 256 sub-chunks of 16 tokens): one
+    # round of three chunk_scan workgroups per CU, 768 segments of 32
+    # sub-chunks, 8 per sequence
+    assert need(4, 4096, 24, 64, 128, 4, _lib.M3_BF16) == 4 * 24 * 8 * record
+    # rank 2 keeps six rounds of two per CU: 3072 segments of 4 sub-chunks of
+    # 32 tokens
+    assert need(4, 4096, 24, 64, 128, 2, _lib.M3_BF16) == 4 * 24 * 32 * record
     # the single pass runs one sequence per CU (256 CUs here, the CPU
     # fallback of the query): it is the faster form once its last round of
     # sequences fills 85 % of the CUs
