@@ -2070,12 +2070,36 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             for (int kb = 0; kb < 2; ++kb)
                 if (kb < nkb)
                     acc = mfma_bf16(xf[kb], *reinterpret_cast<const bf16x8 *>(mb + tj * 16 * LDM * 2 + kb * 64), acc);
-            // row rho = 16 tj + c: token tok0 + 4 tj + c / 4, rank c % 4;
-            // p = 16 wave + 4 g + r.  Tokens past the sequence end fall
-            // outside the buffer: dropped.
-            const uint32_t oy = (tok0 + 4 * tj + (c >> 2)) * rs.tok_x + ((16 * wave + 4 * g) * 4 + (c & 3)) * 2;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) bst2(from_f32<bf16_t>(acc[r]).bits, rs.y, oy + r * 8);
+            // acc[r] is y at row rho = 16 tj + c (token 4 tj + c / 4, rank
+            // q = c % 4) and p = 16 wave + 4 g + r.  A 4 x 4 transpose over
+            // the quad (two DPP exchange steps) gives lane q the four ranks
+            // of p = 16 wave + 4 g + q, which lie together in memory: one
+            // 8-byte store a lane, 128 contiguous bytes per token.  Tokens
+            // past the sequence end fall outside the buffer: dropped.
+            {
+                const bool q1 = (c & 1) != 0, q2 = (c & 2) != 0;
+                float v0 = acc[0], v1 = acc[1], v2 = acc[2], v3 = acc[3];
+                {   // lanes q, q ^ 1 swap registers j, j ^ 1 where q % 2 != j % 2
+                    const float o0 = dpp_f<0xB1, 0xf, false>(v1), o1 = dpp_f<0xB1, 0xf, false>(v0);
+                    const float o2 = dpp_f<0xB1, 0xf, false>(v3), o3 = dpp_f<0xB1, 0xf, false>(v2);
+                    v0 = q1 ? o0 : v0;
+                    v1 = q1 ? v1 : o1;
+                    v2 = q1 ? o2 : v2;
+                    v3 = q1 ? v3 : o3;
+                }
+                {   // lanes q, q ^ 2 swap registers j, j ^ 2 where q & 2 != j & 2
+                    const float o0 = dpp_f<0x4E, 0xf, false>(v2), o1 = dpp_f<0x4E, 0xf, false>(v3);
+                    const float o2 = dpp_f<0x4E, 0xf, false>(v0), o3 = dpp_f<0x4E, 0xf, false>(v1);
+                    v0 = q2 ? o0 : v0;
+                    v1 = q2 ? o1 : v1;
+                    v2 = q2 ? v2 : o2;
+                    v3 = q2 ? v3 : o3;
+                }
+                u32x2 pk;
+                pk[0] = pk_bf16(v0, v1);
+                pk[1] = pk_bf16(v2, v3);
+                bst8(pk, rs.y, (tok0 + 4 * tj + (c >> 2)) * rs.tok_x + (16 * wave + 4 * g + (c & 3)) * 8);
+            }
         }
     }
     if (more) {
