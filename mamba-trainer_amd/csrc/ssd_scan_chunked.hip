@@ -1733,6 +1733,26 @@ __device__ __forceinline__ bf16x8 mimo_pair(const unsigned char *tile, int pl, i
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// The per-token scalars of a 16-token sub-chunk into LDS, wave w < 4 taking
+// s_w (dt, lambda, next dt, next lambda; or a, g, w): one 4-byte load by
+// lanes 0..15 (a uniform branch per resource: a selected resource would go
+// through scratch).  Loaded into registers instead, they would carry the
+// compiler's own waits, which count only its own loads: a vmcnt(0) before
+// their first use that also waits for every tile load issued after them.
+__device__ __forceinline__ void lds_load_scalars16(const SeqBufs &rs, uint32_t tok0, float *dst,
+                                                   int wave, int lane) {
+    if (lane < 16) {
+        const uint32_t d = lds_addr(dst);
+        const uint32_t o0 = (tok0 + lane) * rs.tok_s, o1 = (tok0 + rs.nxt_s + lane) * rs.tok_s;
+        switch (wave) {
+        case 0: lds_dma4(rs.s0, d, o0); break;
+        case 1: lds_dma4(rs.s1, d, o0); break;
+        case 2: lds_dma4(rs.s2, d, o1); break;
+        default: lds_dma4(rs.s3, d, o1); break;
+        }
+    }
+}
+
 template <int N>
 struct ScanMimoSmem {
     static constexpr int CB = N / 2, CX = kP / 2, CT = N / 16;   // chunks per row
@@ -1743,6 +1763,7 @@ struct ScanMimoSmem {
     unsigned char b[16 * CB * 16];    // B, then B~ [t][n][r]
     unsigned char c[16 * CB * 16];    // C, then C~ [t][n][r]
     unsigned char r[2][RB];           // theta, then the band (C~ B~^T o L)[rho][sigma]; X [t][p][r]
+    float sc[4][16];                  // the next sub-chunk's per-token scalars
     float acum[16], gw[16], ww[16], wdv[16];
 };
 
@@ -1772,7 +1793,7 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     // loads a wave issues per sub-chunk: B or C rows, theta, X
     constexpr int kLB = 16 * RBB / 1024 / 4, kLT = 16 * CT * 16 / 256 / 4, kLX = 16 * CX * 16 / 1024 / 4;
     static_assert(kLB >= 1 && kLT >= 1 && kLX >= 1, "loads spread over four waves");
-    constexpr int kC = kLB + 4, kX = kLX;
+    constexpr int kC = kLB + 1, kX = kLX;
 
     __shared__ __attribute__((aligned(16))) S sm;
 
@@ -1809,16 +1830,12 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 #pragma unroll
     for (int j = 0; j < PPT; ++j) run[j] = 0.0f;
 
-    auto load_c = [&](int k, TokScalars &sc) {
+    auto load_c = [&](int k) {
         const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
 #pragma unroll
         for (int q = 0; q < kLB; ++q)
             lds_load_mrows<CB>(rs.c, tok0 * rs.tok_bc, rs.tok_bc, sm.c, wave + 4 * q, lane);
-        const uint32_t tok = tok0 + (lane & 15);
-        sc.s0 = bldf(rs.s0, tok * rs.tok_s);
-        sc.s1 = bldf(rs.s1, tok * rs.tok_s);
-        sc.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
-        sc.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
+        lds_load_scalars16(rs, tok0, &sm.sc[wave][0], wave, lane);
     };
     auto load_bt = [&](int k) {
         const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
@@ -1836,8 +1853,7 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             lds_load_mrows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.r[(k & 1) ^ 1], wave + 4 * q, lane);
     };
 
-    TokScalars sc_next;
-    load_c(seg * kseg, sc_next);
+    load_c(seg * kseg);
     load_bt(seg * kseg);
     load_x(seg * kseg);
 
@@ -1861,7 +1877,11 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     // B, C, theta and the scalars of this sub-chunk landed (X may be out)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm<kX>());
     __syncthreads();
-    const TokScalars sc = sc_next;
+    TokScalars sc;
+    sc.s0 = sm.sc[0][c];
+    sc.s1 = sm.sc[1][c];
+    sc.s2 = sm.sc[2][c];
+    sc.s3 = sm.sc[3][c];
     unsigned char *const rth = sm.r[par];         // theta, then the band
     unsigned char *const rx = sm.r[par ^ 1];      // X
     __bf16 *const ms = reinterpret_cast<__bf16 *>(rth);
@@ -2016,7 +2036,7 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         for (int tj = 0; tj < NT; ++tj) yc[tj] = yc[tj] * dexp2(sm.acum[4 * tj + (c >> 2)]);
     }
     __syncthreads();   // the band is complete; C~ is dead
-    if (more) load_c(sck + 1, sc_next);
+    if (more) load_c(sck + 1);   // sm.sc was last read before the stage's barrier
     // X landed (the next sub-chunk's C and scalars may be out)
     if (more)
         __builtin_amdgcn_s_waitcnt(vmcnt_imm<kC>());
@@ -2122,6 +2142,7 @@ struct StateMimoSmem {
     unsigned char b[16 * CB * 16];        // B, then B~ w decay-to-end [t][n][r]
     unsigned char th[2][16 * CT * 16];    // theta [t][pair]; the pair angle totals at the end
     unsigned char x[2][16 * CX * 16];     // X [t][p][r]
+    float sc[2][4][16];                   // per-token scalars (lds_load_scalars16)
 };
 
 template <int N>
@@ -2136,8 +2157,8 @@ chunk_state_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) 
     constexpr int NTN = N / 16;
     static_assert(PPT == 4 || PPT == 2, "two or four pairs a lane");
     constexpr int kLB = 16 * RBB / 1024 / 4, kLT = 16 * CT * 16 / 256 / 4, kLX = 16 * CX * 16 / 1024 / 4;
-    // loads a wave issues per sub-chunk: theta + X + the four scalars, and B
-    constexpr int kTX = kLT + kLX + 4, kB = kLB;
+    // loads a wave issues per sub-chunk: theta + X + one scalar, and B
+    constexpr int kTX = kLT + kLX + 1, kB = kLB;
 
     __shared__ __attribute__((aligned(16))) S sm;
 
@@ -2156,7 +2177,7 @@ chunk_state_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) 
     float A = 0.0f;
     if (a.mode_raw) A = 0.0f - expf(a.a_log[hh]);   // a_log.exp().neg() (scan.rs:470-474)
 
-    auto load_tx = [&](int k, TokScalars &sc) {
+    auto load_tx = [&](int k) {
         const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
         const int buf = k & 1;
 #pragma unroll
@@ -2165,11 +2186,7 @@ chunk_state_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) 
 #pragma unroll
         for (int q = 0; q < kLX; ++q)
             lds_load_mrows<CX>(rs.x, tok0 * rs.tok_x, rs.tok_x, sm.x[buf], wave + 4 * q, lane);
-        const uint32_t tok = tok0 + (lane & 15);
-        sc.s0 = bldf(rs.s0, tok * rs.tok_s);
-        sc.s1 = bldf(rs.s1, tok * rs.tok_s);
-        sc.s2 = bldf(rs.s2, (tok + rs.nxt_s) * rs.tok_s);
-        sc.s3 = bldf(rs.s3, (tok + rs.nxt_s) * rs.tok_s);
+        lds_load_scalars16(rs, tok0, &sm.sc[buf][wave][0], wave, lane);
     };
     auto load_b = [&](int k) {
         const uint32_t tok0 = static_cast<uint32_t>(k) * QT;
@@ -2187,8 +2204,7 @@ chunk_state_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) 
     for (int j = 0; j < PPT; ++j) run[j] = 0.0f;
 
     const int h_end = min(kseg, nsub - seg * kseg);
-    TokScalars sc_next;
-    load_tx(seg * kseg, sc_next);
+    load_tx(seg * kseg);
     load_b(seg * kseg);
 #pragma unroll 1
     for (int h = 0; h < h_end; ++h) {
@@ -2207,8 +2223,12 @@ chunk_state_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) 
         // theta, X, scalars of this sub-chunk landed (only its B may be out)
         __builtin_amdgcn_s_waitcnt(vmcnt_imm<kB>());
         __syncthreads();
-        const TokScalars sc = sc_next;
-        if (more) load_tx(sck + 1, sc_next);
+        TokScalars sc;
+        sc.s0 = sm.sc[buf][0][c];
+        sc.s1 = sm.sc[buf][1][c];
+        sc.s2 = sm.sc[buf][2][c];
+        sc.s3 = sm.sc[buf][3][c];
+        if (more) load_tx(sck + 1);
 
         const bool live = static_cast<size_t>(sck) * QT + c < L;
         float av, gv, wv;
