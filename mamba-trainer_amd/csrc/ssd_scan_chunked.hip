@@ -2012,9 +2012,12 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             tile(I1{}, I1{}); tile(I2{}, I3{}); tile(I3{}, I3{});
         }
     }
-    // ---- the carry-in product sum_n S[p][n] C~[rho][n] per rho-tile, k-slot
-    //      q of block kb at n = 32 kb + 16 (q / 4) + 4 g + q % 4: n-tiles 2 kb
-    //      and 2 kb + 1 of the state, as the lane holds them
+    // ---- the carry-in product y[rho][p] = sum_n C~[rho][n] S^T[n][p] per
+    //      rho-tile: A operand C~ (rows rho), B operand the state (column p =
+    //      16 wave + c), k-slot q of block kb at n = 32 kb + 16 (q / 4) + 4 g +
+    //      q % 4: n-tiles 2 kb and 2 kb + 1 of the state, as the lane holds them.
+    //      The D layout gives lane (c, g) rows rho = 16 tj + 4 g + r: the four
+    //      ranks of token 4 tj + g at p = 16 wave + c.
     f32x4 yc[NT];
     {
         bf16x8 sf[NKB];
@@ -2031,9 +2034,9 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int tj = 0; tj < NT; ++tj)
-                yc[tj] = mfma_bf16(sf[kb], mimo_tr<RBB>(sm.c, tl, tb, tj, kb), yc[tj]);
+                yc[tj] = mfma_bf16(mimo_tr<RBB>(sm.c, tl, tb, tj, kb), sf[kb], yc[tj]);
 #pragma unroll
-        for (int tj = 0; tj < NT; ++tj) yc[tj] = yc[tj] * dexp2(sm.acum[4 * tj + (c >> 2)]);
+        for (int tj = 0; tj < NT; ++tj) yc[tj] = yc[tj] * dexp2(sm.acum[4 * tj + g]);
     }
     __syncthreads();   // the band is complete; C~ is dead
     if (more) load_c(sck + 1);   // sm.sc was last read before the stage's barrier
@@ -2079,7 +2082,12 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         load_bt(sck + 1);
     }
 
-    // ---- y^T[p][rho] = exp(acum_t) sum_n S[p][n] C~[rho][n] + sum_sigma X^T[p][sigma] M[rho][sigma]
+    // ---- y[rho][p] = exp(acum_t) sum_n C~[rho][n] S^T[n][p] + sum_sigma M[rho][sigma] X[sigma][p]:
+    //      A operand the band row rho = 16 tj + c, B operand the X^T fragment
+    //      (column p).  Lane (c, g) holds the four ranks of token 4 tj + g at
+    //      p = 16 wave + c, which lie together in memory: one 8-byte store a
+    //      lane, 128 contiguous bytes per token.  Tokens past the sequence end
+    //      fall outside the buffer: dropped.
     {
         const unsigned char *const mb = reinterpret_cast<const unsigned char *>(ms) + c * (LDM * 2) + 16 * g;
 #pragma unroll
@@ -2089,37 +2097,11 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
                 if (kb < nkb)
-                    acc = mfma_bf16(xf[kb], *reinterpret_cast<const bf16x8 *>(mb + tj * 16 * LDM * 2 + kb * 64), acc);
-            // acc[r] is y at row rho = 16 tj + c (token 4 tj + c / 4, rank
-            // q = c % 4) and p = 16 wave + 4 g + r.  A 4 x 4 transpose over
-            // the quad (two DPP exchange steps) gives lane q the four ranks
-            // of p = 16 wave + 4 g + q, which lie together in memory: one
-            // 8-byte store a lane, 128 contiguous bytes per token.  Tokens
-            // past the sequence end fall outside the buffer: dropped.
-            {
-                const bool q1 = (c & 1) != 0, q2 = (c & 2) != 0;
-                float v0 = acc[0], v1 = acc[1], v2 = acc[2], v3 = acc[3];
-                {   // lanes q, q ^ 1 swap registers j, j ^ 1 where q % 2 != j % 2
-                    const float o0 = dpp_f<0xB1, 0xf, false>(v1), o1 = dpp_f<0xB1, 0xf, false>(v0);
-                    const float o2 = dpp_f<0xB1, 0xf, false>(v3), o3 = dpp_f<0xB1, 0xf, false>(v2);
-                    v0 = q1 ? o0 : v0;
-                    v1 = q1 ? v1 : o1;
-                    v2 = q1 ? o2 : v2;
-                    v3 = q1 ? v3 : o3;
-                }
-                {   // lanes q, q ^ 2 swap registers j, j ^ 2 where q & 2 != j & 2
-                    const float o0 = dpp_f<0x4E, 0xf, false>(v2), o1 = dpp_f<0x4E, 0xf, false>(v3);
-                    const float o2 = dpp_f<0x4E, 0xf, false>(v0), o3 = dpp_f<0x4E, 0xf, false>(v1);
-                    v0 = q2 ? o0 : v0;
-                    v1 = q2 ? o1 : v1;
-                    v2 = q2 ? v2 : o2;
-                    v3 = q2 ? v3 : o3;
-                }
-                u32x2 pk;
-                pk[0] = pk_bf16(v0, v1);
-                pk[1] = pk_bf16(v2, v3);
-                bst8(pk, rs.y, (tok0 + 4 * tj + (c >> 2)) * rs.tok_x + (16 * wave + 4 * g + (c & 3)) * 8);
-            }
+                    acc = mfma_bf16(*reinterpret_cast<const bf16x8 *>(mb + tj * 16 * LDM * 2 + kb * 64), xf[kb], acc);
+            u32x2 pk;
+            pk[0] = pk_bf16(acc[0], acc[1]);
+            pk[1] = pk_bf16(acc[2], acc[3]);
+            bst8(pk, rs.y, (tok0 + 4 * tj + g) * rs.tok_x + (16 * wave + c) * 8);
         }
     }
     if (more) {
