@@ -102,6 +102,8 @@ size_t m3_mixer_in_proj_width(const m3_mixer_dims *d);
 /* From the in_proj output `projected` [tokens, in_proj_width] (bf16) to the
  * scan inputs: x [tokens, H, P, R], b and c [tokens, H, N, R] (bf16), dt and
  * lambda [tokens, H] (f32), theta [tokens, H, N/2] (bf16, rotational only).
+ * theta is a copy of the row's last H*N/2 columns: NULL skips the copy, for
+ * a caller that reads theta in place (m3_scan_gated's theta_stride).
  * b_bias / c_bias [H, N] and bc_norm [N] (RMSNorm gain) are f32 or NULL when
  * the config has no bias / no norm.  No convolution (conv_kernel None). */
 m3_status m3_mixer_prologue(const m3_mixer_dims *d, const void *projected, const float *dt_bias,

@@ -173,9 +173,15 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
  * m3_mixer_gate(..., norm_weight = NULL, out = y).  bf16 storage only
  * (else M3_ERR_UNSUPPORTED); z_stride < heads*head_dim*rank is M3_ERR_SHAPE.
  * Where the chunk-parallel form runs at rank 1 the gate rides on its output
- * kernel (no y round trip); elsewhere it is a second launch. */
+ * kernel (no y round trip); elsewhere it is a second launch.
+ * theta_stride: elements between consecutive tokens' theta rows, so theta
+ * may be read in place from the in_proj output (theta_stride = its row
+ * width); 0 is the contiguous [B, T, H, N/2] layout.  A stride under
+ * heads*d_state/2 is M3_ERR_SHAPE; one other than 0 needs the specialised
+ * kernels' shapes (head_dim 64, d_state 64 or 128, rank 1, 2 or 4, 16-byte
+ * aligned buffers, rows of whole 16-byte pieces), else M3_ERR_UNSUPPORTED. */
 m3_status m3_scan_gated(const m3_scan_inputs *in, const m3_scan_output *out, const void *z,
-                        size_t z_stride, void *stream);
+                        size_t z_stride, size_t theta_stride, void *stream);
 
 /* Workspace bytes the chunk-parallel scan needs for these inputs (shapes and
  * dtype are read; pointers are not); 0 when the shape runs single-pass only.

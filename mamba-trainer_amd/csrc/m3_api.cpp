@@ -179,9 +179,11 @@ static std::atomic<int> g_scan_path{0}, g_lb_mode{0}, g_lb_spin{0};
 // The scan, and with gate_z the mixer's gate on its y (in place): fused into
 // the chunk-parallel kernel where that form runs (bf16, rank 1), else the
 // gate kernel after the scan.  path: the chunk-parallel form (-1 the setting).
+// theta_stride: elements between tokens' theta rows (0 contiguous), taken by
+// the specialised kernels only.
 static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
                             const void *gate_z, size_t gate_stride, void *stream,
-                            int path = -1) {
+                            int path = -1, size_t theta_stride = 0) {
     if (in == nullptr || out == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/outputs are NULL");
     if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
     if (in->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
@@ -260,6 +262,7 @@ static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
     a.lambda = in->lambda;
     a.a_log = in->a_log;
     a.theta = in->theta;
+    a.theta_stride = in->theta ? theta_stride : 0;
     a.d_skip = in->d_skip;
     a.h0 = st ? st->h : nullptr;
     a.last_u0 = st ? st->last_u : nullptr;
@@ -273,6 +276,10 @@ static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
         a.last_u_out = out->state.last_u;
         a.angle_out = in->theta ? out->state.angle : nullptr;
     }
+    if (a.theta_stride != 0 && !m3::scan_fast_supported(a))
+        return fail(M3_ERR_UNSUPPORTED, "theta at a token stride of %zu elements needs head_dim 64, "
+                    "d_state 64 or 128, rank 1, 2 or 4, 16-byte aligned buffers and rows of whole "
+                    "16-byte pieces", a.theta_stride);
     hipError_t e;
     const size_t need = m3::scan_chunked_workspace(a);
     const bool ws_aligned = (reinterpret_cast<uintptr_t>(in->workspace) & 255u) == 0;
@@ -310,7 +317,7 @@ m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *str
 }
 
 m3_status m3_scan_gated(const m3_scan_inputs *in, const m3_scan_output *out, const void *z,
-                        size_t z_stride, void *stream) {
+                        size_t z_stride, size_t theta_stride, void *stream) {
     if (in == nullptr || out == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/outputs are NULL");
     if (in->dtype != M3_BF16)
         return fail(M3_ERR_UNSUPPORTED, "the gated scan covers bf16 storage");
@@ -318,7 +325,12 @@ m3_status m3_scan_gated(const m3_scan_inputs *in, const m3_scan_output *out, con
     const size_t d_inner = in->heads * in->head_dim * in->rank;
     if (z_stride < d_inner)
         return fail(M3_ERR_SHAPE, "z stride %zu is shorter than d_inner %zu", z_stride, d_inner);
-    return scan_entry(in, out, z, z_stride, stream);
+    const size_t theta_row = in->heads * (in->d_state / 2);
+    if (in->theta != nullptr && theta_stride != 0 && theta_stride < theta_row)
+        return fail(M3_ERR_SHAPE, "theta stride %zu is shorter than a token's %zu angles",
+                    theta_stride, theta_row);
+    return scan_entry(in, out, z, z_stride, stream, -1,
+                      theta_stride == theta_row ? 0 : theta_stride);
 }
 
 }  // extern "C"

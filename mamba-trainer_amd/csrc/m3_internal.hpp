@@ -89,6 +89,10 @@ struct ScanLaunch {
     const float *dt, *lambda, *a_log;   // raw mode
     const float *a, *g, *w;             // ssd_chunked mode
     const void *theta;              // [B,T,H,N/2] or null (raw mode only)
+    // elements between consecutive tokens' theta rows; 0 is H*N/2 (the
+    // contiguous layout).  Taken by the specialised kernels only
+    // (scan_fast_supported), e.g. theta read in place from the in_proj rows.
+    size_t theta_stride;
     const float *d_skip;            // [H] or null
     const float *h0, *last_u0;      // incoming state or null (raw: both or neither)
     const float *angle0;            // [B,H,N/2] or null

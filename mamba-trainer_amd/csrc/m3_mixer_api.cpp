@@ -155,7 +155,7 @@ m3_status m3_mixer_prologue_conv(const m3_mixer_dims *d, const m3_conv1d *conv,
     }
     if (d->tokens == 0) return m3::api_ok();
     if (projected == nullptr || dt_bias == nullptr || x == nullptr || b == nullptr || c == nullptr ||
-        dt == nullptr || lambda == nullptr || (rot && theta == nullptr))
+        dt == nullptr || lambda == nullptr)
         return m3::api_fail(M3_ERR_ARGUMENT, "prologue buffers are NULL");
     const bool learned = lambda_learned(d->discretization);
     const float fixed = m3_discretization_fixed_lambda(d->discretization);
@@ -171,7 +171,7 @@ m3_status m3_mixer_prologue_conv(const m3_mixer_dims *d, const m3_conv1d *conv,
     a.width = m3_mixer_in_proj_width(d);
     a.learned_lambda = learned ? 1 : 0;
     a.fixed_lambda = learned ? 0.0f : fixed;
-    a.has_theta = rot ? 1 : 0;
+    a.has_theta = rot && theta != nullptr ? 1 : 0;   // NULL: theta stays in the row
     a.norm_eps = d->norm_eps;
     a.projected = projected;
     a.dt_bias = dt_bias;

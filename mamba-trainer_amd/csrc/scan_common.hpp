@@ -316,7 +316,17 @@ __device__ __forceinline__ SeqBufs seq_bufs(const ScanLaunch &a, size_t bb, size
     rs.c = mk(a.c, N * R * SZ);
     rs.x = mk(a.x, P * R * SZ);
     rs.y = mk(a.y, P * R * SZ);
-    rs.th = rot ? mk(a.theta, NH * SZ) : make_rsrc(a.x, 0u);   // no records: zeros
+    if (!rot) {
+        rs.th = make_rsrc(a.x, 0u);   // no records: zeros
+    } else if (a.theta_stride == 0) {
+        rs.th = mk(a.theta, NH * SZ);
+    } else {
+        // token rows theta_stride elements apart: the range ends with this
+        // head's row of the sequence's last token
+        const size_t tok = a.theta_stride * SZ;
+        rs.th = make_rsrc(static_cast<const char *>(a.theta) + bb * L * tok + hh * NH * SZ,
+                          live ? static_cast<uint32_t>((L - 1) * tok + NH * SZ) : 0u);
+    }
     if (a.mode_raw) {
         rs.s0 = rs.s2 = mk(a.dt, 4);
         rs.s1 = rs.s3 = mk(a.lambda, 4);
@@ -330,7 +340,7 @@ __device__ __forceinline__ SeqBufs seq_bufs(const ScanLaunch &a, size_t bb, size
     }
     rs.tok_bc = static_cast<uint32_t>(H * N * R * SZ);
     rs.tok_x = static_cast<uint32_t>(H * P * R * SZ);
-    rs.tok_th = static_cast<uint32_t>(H * NH * SZ);
+    rs.tok_th = static_cast<uint32_t>((a.theta_stride ? a.theta_stride : H * NH) * SZ);
     rs.tok_s = static_cast<uint32_t>(H * 4);
     return rs;
 }

@@ -533,6 +533,8 @@ hipError_t launch_t(const ScanLaunch &a, hipStream_t s) {
 hipError_t launch_scan(const ScanLaunch &a, hipStream_t stream) {
     if (a.batch * a.heads == 0 || a.seq == 0) return hipSuccess;
     if (scan_fast_supported(a)) return launch_scan_fast(a, stream);
+    // the generic kernel reads theta in the contiguous layout only
+    if (a.theta != nullptr && a.theta_stride != 0) return hipErrorNotSupported;
     if (a.bf16) return launch_t<bf16_t, 64, 32>(a, stream);
     return launch_t<float, 32, 16>(a, stream);
 }

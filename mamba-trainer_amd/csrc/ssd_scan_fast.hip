@@ -508,6 +508,12 @@ bool scan_fast_supported(const ScanLaunch &a) {
     const size_t esz = a.bf16 ? 2 : 4;
     const size_t row = a.d_state * a.rank * esz;
     if ((a.seq + 128) * a.heads * row >= (size_t(1) << 31)) return false;
+    // theta rows at their own token stride: whole 16-byte pieces, rows that
+    // do not overlap, the same 32-bit bound
+    if (a.theta != nullptr && a.theta_stride != 0 &&
+        (a.theta_stride * esz % 16 != 0 || a.theta_stride < a.heads * (a.d_state / 2) ||
+         (a.seq + 128) * a.theta_stride * esz >= (size_t(1) << 31)))
+        return false;
     return true;
 }
 

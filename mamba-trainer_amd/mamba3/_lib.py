@@ -109,7 +109,7 @@ SIGNATURES = {
     "m3_config_in_proj_width": (_Z, [C.POINTER(SsmConfigC)]),
     "m3_discretization_fixed_lambda": (C.c_float, [C.c_int32]),
     "m3_scan": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanOutputC), _P]),
-    "m3_scan_gated": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanOutputC), _P, _Z, _P]),
+    "m3_scan_gated": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanOutputC), _P, _Z, _Z, _P]),
     "m3_scan_workspace_bytes": (_Z, [C.POINTER(ScanInputsC)]),
     "m3_scan_no_alloc": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanOutputC), _P]),
     "m3_scan_backward": (C.c_int, [C.POINTER(ScanInputsC), C.POINTER(ScanGradsC), _P]),

@@ -131,11 +131,15 @@ class Mamba3Mixer:
                                1e-5 if self.bc_norm is None else self.bc_norm.eps)
 
     def project(self, input: torch.Tensor, history: Optional[torch.Tensor] = None,
-                new_history: Optional[torch.Tensor] = None) -> Projected:
+                new_history: Optional[torch.Tensor] = None,
+                theta_in_place: bool = False) -> Projected:
         """mamba3.rs:350-466.  With a convolution, `history` [B, k-1, channels]
         (None: zeros, as CausalConv1d::apply) precedes the window, and the
         window's last k-1 convolution inputs go to `new_history` when given
-        (which may be `history` itself for a one-position window)."""
+        (which may be `history` itself for a one-position window).
+        theta_in_place: theta is returned as a view of the projection's last
+        H*N/2 columns instead of a copy (for the gated scan, which reads it
+        at the projection's row stride)."""
         c = self.cfg
         input = _bf16_dev(input, "mixer input")
         if input.dim() != 3 or input.shape[2] != c.d_model:
@@ -151,7 +155,12 @@ class Mamba3Mixer:
         dt = torch.empty((B, T, H), dtype=torch.float32, device=dev)
         lam = torch.empty_like(dt)
         rot = c.dynamics == StateDynamics.Rotational
-        theta = torch.empty((B, T, H, N // 2), dtype=torch.bfloat16, device=dev) if rot else None
+        theta = None
+        if rot and theta_in_place:
+            w = projected.shape[-1]
+            theta = projected[..., w - H * (N // 2):].unflatten(-1, (H, N // 2))
+        elif rot:
+            theta = torch.empty((B, T, H, N // 2), dtype=torch.bfloat16, device=dev)
         dims = self._dims(B * T)
         ptr = lambda t: None if t is None else t.data_ptr()
         conv = None
@@ -169,8 +178,8 @@ class Mamba3Mixer:
             C.byref(dims), None if conv is None else C.byref(conv), projected.data_ptr(),
             self.dt_bias.data_ptr(), ptr(self.b_bias),
             ptr(self.c_bias), None if self.bc_norm is None else self.bc_norm.weight.data_ptr(),
-            x.data_ptr(), b.data_ptr(), cc.data_ptr(), dt.data_ptr(), lam.data_ptr(), ptr(theta),
-            _stream(input)))
+            x.data_ptr(), b.data_ptr(), cc.data_ptr(), dt.data_ptr(), lam.data_ptr(),
+            None if theta_in_place else ptr(theta), _stream(input)))
         return Projected(projected[..., :c.d_inner()], projected, x, b, cc, dt, lam, theta)
 
     def finish(self, y: torch.Tensor, proj: Projected, residual: Optional[torch.Tensor] = None,
@@ -214,7 +223,10 @@ class Mamba3Mixer:
         if cache is not None and self.conv_weight is not None:
             hist = cache.conv
             new_hist = self._history(input.shape[0], input.device) if input.dim() == 3 else None
-        proj = self.project(input, hist, new_hist)
+        # the gated scan (below) reads theta in place from the projection
+        gated = self.post_gate_norm is None and not (torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (self.a_log, self.d_skip)))
+        proj = self.project(input, hist, new_hist, theta_in_place=gated)
         si = ScanInputs(proj.x, proj.b, proj.c, proj.dt, self.a_log, proj.lam)
         si = si.with_chunk_size(self.cfg.chunk_size).with_state_output(cache is not None)
         if proj.theta is not None:

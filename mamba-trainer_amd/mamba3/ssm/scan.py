@@ -282,8 +282,23 @@ def mamba3_scan_gated(inputs: ScanInputs, z: torch.Tensor) -> ScanOutput:
     """mamba3_scan followed by the mixer's gate (mamba3.rs:468-477, no
     post-gate norm): the returned y is bf16(y) * silu(z).  z holds B*T rows
     whose first H*P*R columns are the gate (e.g. the in_proj output, z its
-    leading columns).  Inference only: no autograd node."""
+    leading columns).  theta may be a view of rows at a token stride (the
+    in_proj output's last H*N/2 columns): the kernels read it in place.
+    Inference only: no autograd node."""
     return _scan_forward(inputs, z)
+
+
+def _theta_rows(theta: torch.Tensor, B: int, T: int, H: int, NH: int) -> int:
+    """The token stride (elements) of a bf16 [B, T, H, NH] theta whose tokens'
+    rows are contiguous and evenly spaced, as a view into wider rows is;
+    0 for anything else (then it is made contiguous)."""
+    if (theta.dtype != torch.bfloat16 or theta.dim() != 4 or tuple(theta.shape) != (B, T, H, NH)
+            or theta.is_contiguous()):
+        return 0
+    st = theta.stride()
+    if st[3] != 1 or st[2] != NH or st[1] < H * NH or (B > 1 and st[0] != T * st[1]):
+        return 0
+    return st[1]
 
 
 def _scan_forward(inputs: ScanInputs, gate: Optional[torch.Tensor] = None) -> ScanOutput:
@@ -310,7 +325,13 @@ def _scan_forward(inputs: ScanInputs, gate: Optional[torch.Tensor] = None) -> Sc
     _expect_shape(lam, (B, T, H), "lambda")
     _expect_shape(a_log, (H,), "a_log")
     theta = None
-    if inputs.theta is not None:
+    theta_stride = 0
+    if inputs.theta is not None and gate is not None and inputs.theta.is_cuda and N % 2 == 0:
+        theta_stride = _theta_rows(inputs.theta, B, T, H, N // 2)
+        if theta_stride and x.dtype == torch.bfloat16:
+            theta = inputs.theta
+    if inputs.theta is not None and theta is None:
+        theta_stride = 0
         theta = _dev(inputs.theta, "theta")
         if theta.dtype != x.dtype:
             theta = theta.to(x.dtype)
@@ -365,8 +386,16 @@ def _scan_forward(inputs: ScanInputs, gate: Optional[torch.Tensor] = None) -> Sc
         if rows != B * T or zt.shape[-1] < H * P * R:
             raise ShapeError(f"shape error: z must hold {B * T} rows of at least {H * P * R} columns, "
                              f"got {tuple(zt.shape)}")
-        _lib.check(_lib.lib().m3_scan_gated(C.byref(cin), C.byref(cout), zt.data_ptr(),
-                                            zt.shape[-1], _stream(x)))
+        st = _lib.lib().m3_scan_gated(C.byref(cin), C.byref(cout), zt.data_ptr(), zt.shape[-1],
+                                      theta_stride, _stream(x))
+        if st == _lib.M3_ERR_UNSUPPORTED and theta_stride:
+            # a shape the kernels that read theta in place do not cover (the
+            # call checks this before any launch): theta made contiguous
+            theta = theta.contiguous()
+            cin.theta = theta.data_ptr()
+            st = _lib.lib().m3_scan_gated(C.byref(cin), C.byref(cout), zt.data_ptr(),
+                                          zt.shape[-1], 0, _stream(x))
+        _lib.check(st)
     return ScanOutput(y, out_state)
 
 

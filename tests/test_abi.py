@@ -360,21 +360,25 @@ def test_conv_mixer_step_history_rules_before_any_launch():
 
 
 def test_gated_scan_argument_checks_before_any_launch():
-    """m3_scan_gated rejects f32 storage, a NULL z and a z row shorter than
-    heads*head_dim*rank before any device work (the pointers are stand-ins
-    that are never dereferenced)."""
+    """m3_scan_gated rejects f32 storage, a NULL z, a z row shorter than
+    heads*head_dim*rank, a theta stride shorter than a token's heads*d_state/2
+    angles and one whose rows are not whole 16-byte pieces, before any device
+    work (the pointers are stand-ins that are never dereferenced)."""
     from mamba3 import _lib
     L = _lib.lib()
     fake = 1 << 20
     before = L.m3_launch_count()
 
-    def call(dtype=_lib.M3_BF16, z=fake, stride=64 * 3):
+    def call(dtype=_lib.M3_BF16, z=fake, stride=64 * 3, theta=None, theta_stride=0):
         cin = _lib.ScanInputsC(1, 8, 3, 64, 128, 1, dtype, fake, fake, fake, fake, fake, fake,
-                               None, None, None, 64, 0, None, 0)
+                               theta, None, None, 64, 0, None, 0)
         cout = _lib.ScanOutputC(fake, _lib.SsmStateC())
-        return L.m3_scan_gated(C.byref(cin), C.byref(cout), z, stride, None)
+        return L.m3_scan_gated(C.byref(cin), C.byref(cout), z, stride, theta_stride, None)
 
     assert call(dtype=_lib.M3_F32) == _lib.M3_ERR_UNSUPPORTED
     assert call(z=None) == _lib.M3_ERR_ARGUMENT
     assert call(stride=64 * 3 - 1) == _lib.M3_ERR_SHAPE
+    assert call(theta=fake, theta_stride=3 * 64 - 1) == _lib.M3_ERR_SHAPE
+    assert call(theta=fake, theta_stride=3 * 64 + 4) == _lib.M3_ERR_UNSUPPORTED   # 392-byte rows
+    assert b"16-byte pieces" in L.m3_last_error()
     assert L.m3_launch_count() == before

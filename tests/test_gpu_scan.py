@@ -581,3 +581,62 @@ def test_gated_scan_equals_scan_then_gate(B, T, H, N, R, theta, skip, state, chu
     assert torch.equal(got.state.h, ref.state.h) and torch.equal(got.state.last_u, ref.state.last_u)
     if theta:
         assert torch.equal(got.state.angle, ref.state.angle)
+
+
+@pytest.mark.parametrize("B,T,H,N,R,state,chunk_parallel,path,extra", [
+    (2, 300, 3, 128, 1, True, True, 0, 72),      # the fused single launch, gated
+    (16, 512, 12, 128, 1, True, True, 1, 4632 - 768),   # config 4's row, the three launches
+    (1, 700, 2, 64, 1, False, True, 1, 72),      # d_state 64, ragged end
+    (1, 300, 2, 128, 2, True, True, 1, 72),      # MIMO rank 2
+    (2, 300, 2, 128, 4, True, True, 1, 72),      # MIMO rank 4 (its own bf16 kernels)
+    (2, 300, 3, 128, 1, True, False, 0, 72),     # single pass
+    (2, 300, 3, 128, 1, True, True, 0, 68),      # theta not 16-byte aligned: made contiguous
+])
+def test_gated_scan_reads_theta_in_place(B, T, H, N, R, state, chunk_parallel, path, extra):
+    """theta as a view of the in_proj rows' last H*N/2 columns (read by the
+    kernels at the row stride) gives the same bytes as a contiguous copy:
+    y and the whole output state, on every path that takes it.  A row whose
+    theta pieces are not 16-byte aligned is copied first (one call with the
+    stride, refused before any launch, then one without)."""
+    from mamba3 import _lib
+    from mamba3.ssm import ScanInputs, SsmState, mamba3_scan_gated
+    P = 64
+    rng = np.random.default_rng(zlib.crc32(repr(("in place", B, T, H, N, R)).encode()))
+    inp = baseline_inputs(rng, B, T, H, P, N, R, theta=True, dtype="bf16", state=state)
+    bf = torch.bfloat16
+    d, NH = H * P * R, N // 2
+    width = d + extra + H * NH           # [z | ... | theta], theta last as in the in_proj row
+    proj = torch.randn(B, T, width, device="cuda:0").to(bf)
+    proj[..., width - H * NH:] = dev(inp["theta"], bf).view(B, T, H * NH)
+    view = proj[..., width - H * NH:].unflatten(-1, (H, NH))
+    assert not view.is_contiguous()
+
+    def run(theta):
+        si = ScanInputs(dev(inp["x"], bf), dev(inp["b"], bf), dev(inp["c"], bf), dev(inp["dt"]),
+                        dev(inp["a_log"]), dev(inp["lam"])).with_theta(theta)
+        si = si.with_skip(dev(np.linspace(-1, 1, H).astype(np.float32)))
+        if state:
+            si = si.with_state(SsmState(dev(inp["h0"]), dev(inp["last_u0"]), dev(inp["angle0"])))
+        return mamba3_scan_gated(si.with_state_output(True).with_chunk_parallel(chunk_parallel), proj)
+
+    L = _lib.lib()
+    orig, strides = L.m3_scan_gated, []
+
+    def spy(*a):
+        strides.append(a[4])
+        return orig(*a)
+
+    _lib.check(L.m3_debug_scan_options(path, 0, 0))
+    L.m3_scan_gated = spy
+    try:
+        ref = run(view.contiguous())
+        got = run(view)
+    finally:
+        L.m3_scan_gated = orig
+        _lib.check(L.m3_debug_scan_options(0, 0, 0))
+    torch.cuda.synchronize()
+    aligned = (width - H * NH) * 2 % 16 == 0
+    assert strides == ([0, width] if aligned else [0, width, 0])
+    assert torch.equal(got.y, ref.y)
+    for f in ("h", "last_u", "angle"):
+        assert torch.equal(getattr(got.state, f), getattr(ref.state, f)), f
