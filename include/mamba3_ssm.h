@@ -28,10 +28,18 @@
  * Conventions
  *   - All tensors are caller-allocated, contiguous, row-major device buffers
  *     with the reference's layouts (rank-last x/b/c, N contiguous in the state).
- *   - `dtype` selects the storage of x, b, c, theta and y (f32 or bf16, bf16 as
- *     raw 16-bit words).  dt, lambda, a_log, d_skip and the state are f32.
+ *   - `dtype` selects the storage of x, b, c, theta and y (f32, bf16 or f16,
+ *     the 16-bit forms as raw words).  dt, lambda, a_log, d_skip and the state
+ *     are f32.  f16 storage (FloatElem for half::f16, src/backend.rs:86-98)
+ *     runs the f32 kernels on f32 copies: the call widens its f16 inputs into
+ *     temporaries allocated in stream order (hipMallocAsync) on `stream`,
+ *     narrows its f16 outputs back (round to nearest even) and frees the
+ *     temporaries in stream order, so its results are exactly the f32 call's
+ *     on the widened inputs, rounded to f16.  m3_scan_no_alloc,
+ *     m3_scan_gated and m3_step_layers take f32 or bf16 only.
  *   - Calls are asynchronous on `stream` (a hipStream_t; NULL = the default
- *     stream) and never synchronise the host.  No call allocates device memory.
+ *     stream) and never synchronise the host.  No call allocates device memory
+ *     except those with f16 storage (above).
  *   - Errors return a status; m3_last_error() gives this thread's message.
  *     Validation mirrors the reference's rules and messages.
  *   - Deviations from the reference, by design:
@@ -67,7 +75,7 @@ typedef enum m3_status {
     M3_ERR_JSON = 9          /* Error::Json        */
 } m3_status;
 
-typedef enum m3_dtype { M3_F32 = 0, M3_BF16 = 1 } m3_dtype;
+typedef enum m3_dtype { M3_F32 = 0, M3_BF16 = 1, M3_F16 = 2 } m3_dtype;
 
 /* src/ssm/config.rs:19-26 */
 typedef enum m3_discretization {

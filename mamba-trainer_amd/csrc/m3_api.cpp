@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "m3_internal.hpp"
 
@@ -60,7 +61,7 @@ size_t scan_rows(int dtype, size_t d_state) {
     return d_state <= 128 ? 32 : 16;
 }
 
-bool dtype_ok(int32_t d) { return d == M3_F32 || d == M3_BF16; }
+bool dtype_ok(int32_t d) { return d == M3_F32 || d == M3_BF16 || d == M3_F16; }
 
 // Zero `n` floats on `s` with a kernel rather than hipMemsetAsync, so that a
 // caller who captures the call into a HIP graph records a kernel node only.
@@ -78,6 +79,76 @@ hipError_t zero_async(float *p, size_t n, hipStream_t s) {
     g_launches.fetch_add(1, std::memory_order_relaxed);
     return hipGetLastError();
 }
+
+// ---- f16 storage (the reference's FloatElem for half::f16, backend.rs:86-98).
+// The f32 kernels run on f32 copies of the caller's f16 tensors: inputs are
+// widened before the call, outputs narrowed after it (round to nearest even),
+// in temporaries allocated and freed in stream order on the call's stream.
+// So an f16 call gives exactly the f32 call's results on the widened inputs,
+// rounded to f16.
+__global__ void f16_widen_kernel(const _Float16 *src, float *dst, size_t n) {
+    for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n;
+         i += size_t(gridDim.x) * blockDim.x)
+        dst[i] = static_cast<float>(src[i]);
+}
+__global__ void f16_narrow_kernel(const float *src, _Float16 *dst, size_t n) {
+    for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n;
+         i += size_t(gridDim.x) * blockDim.x)
+        dst[i] = static_cast<_Float16>(src[i]);
+}
+
+class F16Copies {
+  public:
+    explicit F16Copies(hipStream_t s) : s_(s) {}
+    F16Copies(const F16Copies &) = delete;
+    F16Copies &operator=(const F16Copies &) = delete;
+    ~F16Copies() {
+        for (const Item &it : items_) (void)hipFreeAsync(it.f32, s_);
+    }
+    // An f32 copy of the n f16 values at p (NULL for a NULL p): widened now
+    // when `in`, narrowed back into p by narrow() when `out`.
+    float *add(const void *p, size_t n, bool in, bool out) {
+        if (p == nullptr || err_ != hipSuccess) return nullptr;
+        void *f = nullptr;
+        err_ = hipMallocAsync(&f, (n ? n : 1) * sizeof(float), s_);
+        if (err_ != hipSuccess) return nullptr;
+        items_.push_back({const_cast<void *>(p), static_cast<float *>(f), n, out});
+        if (in && n > 0) {
+            hipLaunchKernelGGL(f16_widen_kernel, dim3(grid(n)), dim3(256), 0, s_,
+                               static_cast<const _Float16 *>(p), static_cast<float *>(f), n);
+            g_launches.fetch_add(1, std::memory_order_relaxed);
+            err_ = hipGetLastError();
+        }
+        return static_cast<float *>(f);
+    }
+    hipError_t error() const { return err_; }
+    // every `out` copy back into its f16 tensor
+    hipError_t narrow() {
+        for (const Item &it : items_) {
+            if (!it.out || it.n == 0 || err_ != hipSuccess) continue;
+            hipLaunchKernelGGL(f16_narrow_kernel, dim3(grid(it.n)), dim3(256), 0, s_, it.f32,
+                               static_cast<_Float16 *>(it.dst), it.n);
+            g_launches.fetch_add(1, std::memory_order_relaxed);
+            err_ = hipGetLastError();
+        }
+        return err_;
+    }
+
+  private:
+    struct Item {
+        void *dst;
+        float *f32;
+        size_t n;
+        bool out;
+    };
+    static unsigned grid(size_t n) {
+        const size_t b = (n + 255) / 256;
+        return static_cast<unsigned>(b < 8192 ? b : 8192);
+    }
+    hipStream_t s_;
+    std::vector<Item> items_;
+    hipError_t err_ = hipSuccess;
+};
 
 }  // namespace
 
@@ -183,7 +254,33 @@ static std::atomic<int> g_scan_path{0}, g_lb_mode{0}, g_lb_spin{0};
 // the specialised kernels only.
 static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
                             const void *gate_z, size_t gate_stride, void *stream,
-                            int path = -1, size_t theta_stride = 0) {
+                            int path = -1, size_t theta_stride = 0);
+
+// m3_scan with f16 storage: the f32 scan on widened copies of x, b, c and
+// theta, y narrowed back (the arguments are validated by the caller).
+static m3_status scan_f16(const m3_scan_inputs *in, const m3_scan_output *out, void *stream,
+                          int path) {
+    const size_t rows = in->batch * in->seq * in->heads;
+    const size_t P = in->head_dim, N = in->d_state, R = in->rank;
+    F16Copies cp(static_cast<hipStream_t>(stream));
+    m3_scan_inputs local = *in;
+    local.dtype = M3_F32;
+    local.x = cp.add(in->x, rows * P * R, true, false);
+    local.b = cp.add(in->b, rows * N * R, true, false);
+    local.c = cp.add(in->c, rows * N * R, true, false);
+    local.theta = cp.add(in->theta, rows * (N / 2), true, false);
+    m3_scan_output o = *out;
+    o.y = cp.add(out->y, rows * P * R, false, true);
+    if (cp.error() != hipSuccess) return hip_fail(cp.error(), "f16 copies");
+    const m3_status st = scan_entry(&local, &o, nullptr, 0, stream, path);
+    if (st != M3_OK) return st;
+    if (cp.narrow() != hipSuccess) return hip_fail(cp.error(), "f16 narrowing");
+    return ok();
+}
+
+static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
+                            const void *gate_z, size_t gate_stride, void *stream,
+                            int path, size_t theta_stride) {
     if (in == nullptr || out == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/outputs are NULL");
     if (!dtype_ok(in->dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", in->dtype);
     if (in->rank == 0) return fail(M3_ERR_CONFIG, "MIMO rank must be positive");
@@ -244,6 +341,11 @@ static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
     if (in->x == nullptr || in->b == nullptr || in->c == nullptr || in->dt == nullptr ||
         in->a_log == nullptr || in->lambda == nullptr || out->y == nullptr)
         return fail(M3_ERR_ARGUMENT, "x, b, c, dt, a_log, lambda and y are required");
+    if (in->dtype == M3_F16) {
+        if (gate_z != nullptr || theta_stride != 0)
+            return fail(M3_ERR_UNSUPPORTED, "the gate and theta in place cover bf16 storage");
+        return scan_f16(in, out, stream, path);
+    }
 
     m3::ScanLaunch a{};
     a.batch = B;
@@ -418,6 +520,9 @@ extern "C" {
 
 m3_status m3_scan_no_alloc(const m3_scan_inputs *in, const m3_scan_output *out, void *stream) {
     if (in == nullptr || out == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/outputs are NULL");
+    if (in->dtype == M3_F16)
+        return fail(M3_ERR_UNSUPPORTED, "f16 storage widens into temporaries it allocates: "
+                    "call m3_scan instead");
     m3_scan_inputs local = *in;
     local.workspace = nullptr;
     local.workspace_bytes = 0;
@@ -493,6 +598,35 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
         return fail(M3_ERR_ARGUMENT, "theta is given: dtheta is required");
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e = hipSuccess;
+    if (in->dtype == M3_F16 && in->seq > 0) {
+        // the f32 backward on widened copies; dx, db, dc and dtheta narrowed back
+        m3_scan_inputs li = *in;
+        li.dtype = M3_F32;
+        m3::ScanLaunch chk = scan_launch_of(&li);
+        alignas(16) static float dummy[4] = {0, 0, 0, 0};
+        chk.x = chk.b = chk.c = dummy;   // the copies are aligned: the shape decides
+        chk.theta = in->theta ? dummy : nullptr;
+        if (!m3::scan_backward_supported(chk))
+            return fail(M3_ERR_UNSUPPORTED,
+                        "the scan backward covers head_dim 64, d_state 64/128, rank 1/2/4");
+        const size_t rows = B * in->seq * H, R = in->rank;
+        F16Copies cp(s);
+        li.x = cp.add(in->x, rows * P * R, true, false);
+        li.b = cp.add(in->b, rows * N * R, true, false);
+        li.c = cp.add(in->c, rows * N * R, true, false);
+        li.theta = cp.add(in->theta, rows * (N / 2), true, false);
+        m3_scan_grads lg = *g;
+        lg.dy = cp.add(g->dy, rows * P * R, true, false);
+        lg.dx = cp.add(g->dx, rows * P * R, false, true);
+        lg.db = cp.add(g->db, rows * N * R, false, true);
+        lg.dc = cp.add(g->dc, rows * N * R, false, true);
+        lg.dtheta = in->theta ? cp.add(g->dtheta, rows * (N / 2), false, true) : g->dtheta;
+        if (cp.error() != hipSuccess) return hip_fail(cp.error(), "f16 copies");
+        const m3_status st2 = m3_scan_backward(&li, &lg, stream);
+        if (st2 != M3_OK) return st2;
+        if (cp.narrow() != hipSuccess) return hip_fail(cp.error(), "f16 narrowing");
+        return ok();
+    }
     if (in->seq == 0) {
         // empty window: the state passed through, nothing else was read
         const size_t sbytes = B * H * P * N * sizeof(float);
@@ -594,6 +728,22 @@ m3_status m3_ssd_chunked(const m3_ssd_args *in, void *y, float *final_state, voi
     if (in->x == nullptr || in->b == nullptr || in->c == nullptr || in->a == nullptr ||
         in->g == nullptr || in->w == nullptr || y == nullptr)
         return fail(M3_ERR_ARGUMENT, "x, b, c, a, g, w and y are required");
+    if (in->dtype == M3_F16) {
+        // the f32 form on widened copies of x, b and c; y narrowed back
+        const size_t rows = B * in->seq * H;
+        F16Copies cp(s);
+        m3_ssd_args li = *in;
+        li.dtype = M3_F32;
+        li.x = cp.add(in->x, rows * P, true, false);
+        li.b = cp.add(in->b, rows * N, true, false);
+        li.c = cp.add(in->c, rows * N, true, false);
+        float *y32 = cp.add(y, rows * P, false, true);
+        if (cp.error() != hipSuccess) return hip_fail(cp.error(), "f16 copies");
+        const m3_status st = m3_ssd_chunked(&li, y32, final_state, stream);
+        if (st != M3_OK) return st;
+        if (cp.narrow() != hipSuccess) return hip_fail(cp.error(), "f16 narrowing");
+        return ok();
+    }
     m3::ScanLaunch a{};
     a.batch = B;
     a.seq = in->seq;
@@ -658,7 +808,7 @@ m3_status build_step(const m3_step_inputs *in, const m3_ssm_state *state,
     if (lds > 16384)
         return fail(M3_ERR_UNSUPPORTED, "d_state/head_dim/rank too large for the step kernel");
     if (fst != nullptr) {
-        const size_t es = in->dtype == M3_BF16 ? 2 : 4;
+        const size_t es = in->dtype == M3_F32 ? 4 : 2;
         const size_t xb = in->batch * in->heads * in->head_dim * in->rank * es;
         const size_t bb = in->batch * in->heads * in->d_state * in->rank * es;
         auto overlap = [](const void *p, size_t pn, const void *q, size_t qn) {
@@ -698,6 +848,39 @@ m3_status build_step(const m3_step_inputs *in, const m3_ssm_state *state,
     return ok();
 }
 
+// A step with f16 storage (validated by build_step): the f32 step on widened
+// copies of x, b, c and theta (and of the factored state's x_prev and b_prev,
+// narrowed back as the step rewrites them); y narrowed back.
+m3_status step_f16(const m3_step_inputs *in, m3_ssm_state *state,
+                   m3_ssm_state_factored *fst, void *y, void *stream) {
+    const size_t bh = in->batch * in->heads;
+    const size_t P = in->head_dim, N = in->d_state, R = in->rank;
+    F16Copies cp(static_cast<hipStream_t>(stream));
+    m3_step_inputs li = *in;
+    li.dtype = M3_F32;
+    li.x = cp.add(in->x, bh * P * R, true, false);
+    li.b = cp.add(in->b, bh * N * R, true, false);
+    li.c = cp.add(in->c, bh * N * R, true, false);
+    li.theta = cp.add(in->theta, bh * (N / 2), true, false);
+    float *y32 = cp.add(y, bh * P * R, false, true);
+    m3_ssm_state_factored lf{};
+    if (fst != nullptr) {
+        lf = *fst;
+        lf.x_prev = cp.add(fst->x_prev, bh * P * R, true, true);
+        lf.b_prev = cp.add(fst->b_prev, bh * N * R, true, true);
+    }
+    if (cp.error() != hipSuccess) return hip_fail(cp.error(), "f16 copies");
+    m3::StepLaunch a;
+    bool empty = false;
+    const m3_status st = build_step(&li, state, fst ? &lf : nullptr, y32, a, &empty);
+    if (st != M3_OK || empty) return st;
+    hipError_t e = m3::launch_step(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "step launch");
+    g_launches.fetch_add(1, std::memory_order_relaxed);
+    if (cp.narrow() != hipSuccess) return hip_fail(cp.error(), "f16 narrowing");
+    return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -708,6 +891,7 @@ m3_status m3_step(const m3_step_inputs *in, m3_ssm_state *state, void *y, void *
     if (state == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/state are NULL");
     const m3_status st = build_step(in, state, nullptr, y, a, &empty);
     if (st != M3_OK || empty) return st;
+    if (in->dtype == M3_F16) return step_f16(in, state, nullptr, y, stream);
     hipError_t e = m3::launch_step(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "step launch");
     g_launches.fetch_add(1, std::memory_order_relaxed);
@@ -721,6 +905,7 @@ m3_status m3_step_factored(const m3_step_inputs *in, m3_ssm_state_factored *stat
     if (state == nullptr) return fail(M3_ERR_ARGUMENT, "inputs/state are NULL");
     const m3_status st = build_step(in, nullptr, state, y, a, &empty);
     if (st != M3_OK || empty) return st;
+    if (in->dtype == M3_F16) return step_f16(in, nullptr, state, y, stream);
     hipError_t e = m3::launch_step(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "step launch");
     g_launches.fetch_add(1, std::memory_order_relaxed);
@@ -733,6 +918,7 @@ m3_status m3_state_unfactor(size_t batch, size_t heads, size_t head_dim, size_t 
     if (!dtype_ok(dtype)) return fail(M3_ERR_ARGUMENT, "unknown dtype %d", dtype);
     if (head_dim == 0 || d_state == 0 || rank == 0)
         return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
+    const bool f16 = dtype == M3_F16;
     if (angle != nullptr && d_state % 2 != 0)
         return fail(M3_ERR_CONFIG, "rotational dynamics require an even d_state");
     if ((d_state + head_dim) * rank > 16384)
@@ -740,6 +926,13 @@ m3_status m3_state_unfactor(size_t batch, size_t heads, size_t head_dim, size_t 
     if (batch * heads == 0) return ok();
     if (x_prev == nullptr || b_prev == nullptr || last_u == nullptr)
         return fail(M3_ERR_ARGUMENT, "x_prev, b_prev and last_u are required");
+    // f16: the f32 form on widened copies of x_prev and b_prev
+    F16Copies cp(static_cast<hipStream_t>(stream));
+    if (f16) {
+        x_prev = cp.add(x_prev, batch * heads * head_dim * rank, true, false);
+        b_prev = cp.add(b_prev, batch * heads * d_state * rank, true, false);
+        if (cp.error() != hipSuccess) return hip_fail(cp.error(), "f16 copies");
+    }
     hipError_t e = m3::launch_unfactor(batch, heads, head_dim, d_state, rank, dtype == M3_BF16,
                                        x_prev, b_prev, angle, last_u,
                                        static_cast<hipStream_t>(stream));
@@ -769,6 +962,9 @@ m3_status m3_step_layers(size_t n_layers, const m3_step_inputs *inputs, m3_ssm_s
         if (!m3::step_layers_supported(in.d_state, in.rank))
             return fail(M3_ERR_UNSUPPORTED, "m3_step_layers covers d_state a multiple of 4 with "
                         "d_state/4 a power of two up to 64 and rank 1, 2, 3, 4 or 8");
+        if (in.dtype == M3_F16)
+            return fail(M3_ERR_UNSUPPORTED, "m3_step_layers covers f32 and bf16 storage: step "
+                        "f16 layers with m3_step");
     }
     // every layer's arguments are validated before the first launch, so an
     // error leaves no layer of the cache stepped

@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(_HERE, "libmamba3_hip.so")
 M3_OK, M3_ERR_CONFIG, M3_ERR_SHAPE, M3_ERR_RANK = 0, 1, 2, 3
 M3_ERR_UNSUPPORTED, M3_ERR_HIP, M3_ERR_ARGUMENT = 4, 5, 6
 M3_ERR_STATE_DICT, M3_ERR_IO, M3_ERR_JSON = 7, 8, 9
-M3_F32, M3_BF16 = 0, 1
+M3_F32, M3_BF16, M3_F16 = 0, 1, 2
 
 _Z = C.c_size_t
 _P = C.c_void_p

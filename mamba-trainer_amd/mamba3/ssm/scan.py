@@ -17,14 +17,15 @@ import torch
 from .. import _lib
 from ..error import ArgumentError, RankError, ShapeError, UnsupportedError
 
-_DTYPES = {torch.float32: _lib.M3_F32, torch.bfloat16: _lib.M3_BF16}
+_DTYPES = {torch.float32: _lib.M3_F32, torch.bfloat16: _lib.M3_BF16, torch.float16: _lib.M3_F16}
 
 
 def _dtype_code(t: torch.Tensor) -> int:
     try:
         return _DTYPES[t.dtype]
     except KeyError:
-        raise UnsupportedError(f"unsupported: storage dtype {t.dtype}; use float32 or bfloat16")
+        raise UnsupportedError(f"unsupported: storage dtype {t.dtype}; use float32, bfloat16 or "
+                               "float16")
 
 
 def _dev(t: torch.Tensor, what: str) -> torch.Tensor:

@@ -134,6 +134,51 @@ def test_scan_argument_validation_before_device_work(kw, status, message):
     assert message in L.m3_last_error().decode()
 
 
+@pytest.mark.parametrize("kw,status,message", [
+    (dict(rank=0), 1, "MIMO rank must be positive"),
+    (dict(d_state=5, theta=1), 1, "rotational dynamics require an even d_state"),
+    (dict(head_dim=256), 4, "head_dim 256 exceeds"),
+    (dict(want_state=1), 6, "want_state needs output h and last_u"),
+    (dict(x=None, seq=8), 6, "x, b, c, dt, a_log, lambda and y are required"),
+])
+def test_f16_storage_validates_before_any_copy(kw, status, message):
+    """f16 storage (M3_F16) takes the same checks as f32 and bf16, all of them
+    before its widening copies: a rejected call allocates and launches nothing
+    (the pointers are stand-ins that are never dereferenced)."""
+    from mamba3 import _lib
+    L = _lib.lib()
+    fake = 1 << 20
+    args = dict(dtype=_lib.M3_F16, x=fake, b=fake, c=fake, dt=fake, a_log=fake, lambda_=fake)
+    args.update(kw)
+    cin = _scan_inputs(**args)
+    before = L.m3_launch_count()
+    st = L.m3_scan(C.byref(cin), C.byref(_lib.ScanOutputC()), None)
+    assert st == status, L.m3_last_error()
+    assert message in L.m3_last_error().decode()
+    assert L.m3_launch_count() == before
+
+
+def test_f16_storage_entry_points_that_do_not_take_it():
+    """m3_scan_no_alloc (which may not allocate) and m3_scan_gated refuse f16
+    storage before any device work; the workspace query sizes an f16 scan as
+    the f32 one it runs."""
+    from mamba3 import _lib
+    L = _lib.lib()
+    fake = 1 << 20
+    before = L.m3_launch_count()
+    cin = _lib.ScanInputsC(1, 64, 2, 64, 128, 1, _lib.M3_F16, fake, fake, fake, fake, fake, fake,
+                           None, None, None, 64, 0, None, 0)
+    cout = _lib.ScanOutputC(fake, _lib.SsmStateC())
+    assert L.m3_scan_no_alloc(C.byref(cin), C.byref(cout), None) == _lib.M3_ERR_UNSUPPORTED
+    assert b"f16" in L.m3_last_error()
+    assert L.m3_scan_gated(C.byref(cin), C.byref(cout), fake, 128, 0, None) == _lib.M3_ERR_UNSUPPORTED
+    assert L.m3_launch_count() == before
+    q = lambda dt: L.m3_scan_workspace_bytes(C.byref(_lib.ScanInputsC(
+        8, 2048, 12, 64, 128, 1, dt, None, None, None, None, None, None, None, None, None, 64, 1,
+        None, 0)))
+    assert q(_lib.M3_F16) == q(_lib.M3_F32) > 0
+
+
 def test_python_api_rejects_host_tensors():
     """The product path has no CPU fallback: host tensors fail loudly."""
     import torch
