@@ -39,7 +39,8 @@
  *     m3_scan_gated and m3_step_layers take f32 or bf16 only.
  *   - Calls are asynchronous on `stream` (a hipStream_t; NULL = the default
  *     stream) and never synchronise the host.  No call allocates device memory
- *     except those with f16 storage (above).
+ *     except those with f16 storage (above) and an m3_scan beyond the scan
+ *     kernels' tiles without want_state (m3_scan).
  *   - Errors return a status; m3_last_error() gives this thread's message.
  *     Validation mirrors the reference's rules and messages.
  *   - Deviations from the reference, by design:
@@ -171,7 +172,14 @@ typedef struct m3_scan_output {
 } m3_scan_output;
 
 /* mamba3_scan (scan.rs:458-618): trapezoid weights, rotating frame, MIMO
- * fold, carried state, skip path and boundary state in one launch. */
+ * fold, carried state, skip path and boundary state in one launch.  Shapes
+ * beyond the scan kernels' tiles (head_dim over 128, d_state over 256, rank
+ * over a chunk's rows: 64 for bf16, 32 for f32, halved above d_state 128)
+ * run as the recurrence, token by token, on the step kernel: one launch per
+ * token, the carried state in the output state buffers (in temporaries
+ * allocated and freed in stream order when want_state is 0).  Only shapes
+ * beyond that kernel too (2 d_state rank + head_dim rank > 16384) return
+ * M3_ERR_UNSUPPORTED, before any device work. */
 m3_status m3_scan(const m3_scan_inputs *in, const m3_scan_output *out, void *stream);
 
 /* m3_scan, then the mixer's gate on its y in place (Mamba3Mixer::finish

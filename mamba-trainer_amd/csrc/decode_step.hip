@@ -50,24 +50,26 @@ __device__ __forceinline__ float rot_hi(float x1, float x2, float cs, float sn) 
 }
 
 // Prologue shared by both bodies: angle advance, rotation of B and C into
-// LDS (rank-last [N][R] layout kept), x into LDS, and the coefficients.
+// LDS (rank-last [N][R] layout kept), x into LDS, and the coefficients.  bh
+// indexes the state, ib the inputs (bh except with in_bstride).
 template <typename T, bool FACT = false>
-__device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, float *bt,
-                                              float *ct, float *xs, float &alpha,
+__device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, size_t ib,
+                                              float *bt, float *ct, float *xs, float &alpha,
                                               float &beta, float &gamma, float *bpt = nullptr,
                                               float *xps = nullptr) {
     const int tid = threadIdx.x;
     const size_t N = a.d_state, P = a.head_dim, R = a.rank;
     const size_t half = N / 2;
     const size_t hh = bh % a.heads;
-    const float step = a.dt[bh];
-    const float lam = a.lambda[bh];
-    const size_t bc_base = bh * N * R;
+    const float step = a.dt[ib];
+    const float lam = a.lambda[ib];
+    const size_t bc_base = ib * N * R;
+    const size_t bp_base = bh * N * R;
     if (a.theta != nullptr) {
         for (size_t i = tid; i < half; i += kStepThreads) {
             // phi = wrap(prev + dt * theta)   (fused.rs:1549-1553)
             const float prev = a.angle[bh * half + i];
-            float raw = ld<T>(a.theta, bh * half + i) * step + prev;
+            float raw = ld<T>(a.theta, ib * half + i) * step + prev;
             float phi = wrap_angle(raw);
             a.angle[bh * half + i] = phi;
             float sn, cs;
@@ -78,8 +80,8 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
                 float ps, pc;
                 sincosf(prev, &ps, &pc);
                 for (size_t r = 0; r < R; ++r) {
-                    const float b1 = ld<T>(a.b_prev, bc_base + i * R + r);
-                    const float b2 = ld<T>(a.b_prev, bc_base + (i + half) * R + r);
+                    const float b1 = ld<T>(a.b_prev, bp_base + i * R + r);
+                    const float b2 = ld<T>(a.b_prev, bp_base + (i + half) * R + r);
                     bpt[i * R + r] = rot_lo(b1, b2, pc, ps);
                     bpt[(i + half) * R + r] = rot_hi(b1, b2, pc, ps);
                 }
@@ -102,11 +104,11 @@ __device__ __forceinline__ void step_prologue(const StepLaunch &a, size_t bh, fl
         for (size_t i = tid; i < N * R; i += kStepThreads) {
             bt[i] = ld<T>(a.b, bc_base + i);
             ct[i] = ld<T>(a.c, bc_base + i);
-            if constexpr (FACT) bpt[i] = ld<T>(a.b_prev, bc_base + i);
+            if constexpr (FACT) bpt[i] = ld<T>(a.b_prev, bp_base + i);
         }
     }
     for (size_t i = tid; i < P * R; i += kStepThreads) {
-        xs[i] = ld<T>(a.x, bh * P * R + i);
+        xs[i] = ld<T>(a.x, ib * P * R + i);
         if constexpr (FACT) xps[i] = ld<T>(a.x_prev, bh * P * R + i);
     }
     // alpha = exp(dt * -exp(a_log)), beta = (1 - lambda) dt alpha, gamma = lambda dt
@@ -327,7 +329,7 @@ __device__ __forceinline__ void step_body_vec(const StepLaunch &a, size_t bh,
         mix_prologue<R, FACT, CONV>(*m, bh, bt, ct, xs, alpha, beta, gamma, bpt, braw, craw, thv,
                                     scal);
     else
-        step_prologue<T, FACT>(a, bh, bt, ct, xs, alpha, beta, gamma, bpt, xps);
+        step_prologue<T, FACT>(a, bh, bh, bt, ct, xs, alpha, beta, gamma, bpt, xps);
     if constexpr (FACT && MIX) {
         for (size_t i = threadIdx.x; i < P * R; i += kStepThreads)
             xps[i] = ld<T>(a.x_prev, bh * P * R + i);
@@ -508,8 +510,9 @@ step_kernel_generic(StepLaunch a) {
     float *ct = bt + N * R;
     float *xs = ct + N * R;
     const size_t bh = blockIdx.x;
+    const size_t ib = a.in_bstride ? (bh / a.heads) * a.in_bstride * a.heads + bh % a.heads : bh;
     float alpha, beta, gamma;
-    step_prologue<T>(a, bh, bt, ct, xs, alpha, beta, gamma);
+    step_prologue<T>(a, bh, ib, bt, ct, xs, alpha, beta, gamma);
     __syncthreads();
     const float dskip = a.d_skip ? a.d_skip[bh % a.heads] : 0.0f;
     float *h = a.h + bh * P * N;
@@ -526,7 +529,7 @@ step_kernel_generic(StepLaunch a) {
         for (size_t r = 0; r < R; ++r) {
             float acc = 0.0f;
             for (size_t n = 0; n < N; ++n) acc += ct[n * R + r] * h[p * N + n];
-            y[(bh * P + p) * R + r] = from_f32<T>(acc + xs[p * R + r] * dskip);
+            y[(ib * P + p) * R + r] = from_f32<T>(acc + xs[p * R + r] * dskip);
         }
     }
 }
@@ -549,7 +552,7 @@ hipError_t dispatch(const StepLaunch &a, hipStream_t s) {
     const size_t smem = ((fact ? 3 : 2) * N * R + (fact ? 2 : 1) * a.head_dim * R) * sizeof(float);
     if (fact && !step_factored_supported(N, R)) return hipErrorNotSupported;
     const size_t G = N / 4;
-    const bool vec = (N % 4 == 0) && G >= 1 && G <= 64 && (G & (G - 1)) == 0;
+    const bool vec = (N % 4 == 0) && G >= 1 && G <= 64 && (G & (G - 1)) == 0 && a.in_bstride == 0;
     if (vec) {
         switch (R) {
             case 1: return launch_vec<T, 1>(a, smem, s);

@@ -256,6 +256,92 @@ static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
                             const void *gate_z, size_t gate_stride, void *stream,
                             int path = -1, size_t theta_stride = 0);
 
+// The step kernel's LDS holds B~, C~ (d_state x rank each) and x (head_dim x
+// rank) as f32: 64 KB.
+constexpr size_t kStepLdsFloats = 16384;
+
+// Shapes the scan kernels do not cover (head_dim, d_state or rank beyond
+// their tiles); the reference's mamba3_scan has no such limits
+// (scan.rs:458-618).
+static bool scan_by_steps_needed(const m3_scan_inputs *in) {
+    return in->head_dim > m3::kScanMaxHeadDim || in->d_state > m3::kScanMaxState ||
+           in->rank > scan_rows(in->dtype, in->d_state);
+}
+static bool step_covers(const m3_scan_inputs *in) {
+    return (2 * in->d_state + in->head_dim) * in->rank <= kStepLdsFloats;
+}
+
+// The scan of such shapes as its definition as a recurrence: one launch of
+// the step kernel's generic body per token over every (batch, head), in
+// order, carrying (h, last_u, angle) from the incoming state (zeros without
+// one).  mamba3_step on one token is the scan of that token from the state
+// (the reference checks the one against the other, tests/ssm.rs:312-380).
+// The carried state lives in the output state buffers when they are wanted,
+// else in temporaries allocated and freed in stream order.  Arguments are
+// validated by the caller; f32 or bf16 storage.
+static m3_status scan_by_steps(const m3_scan_inputs *in, const m3_scan_output *out,
+                               hipStream_t s) {
+    const size_t B = in->batch, T = in->seq, H = in->heads, P = in->head_dim, N = in->d_state;
+    const size_t R = in->rank, es = in->dtype == M3_BF16 ? 2 : 4;
+    const bool rot = in->theta != nullptr;
+    const size_t sn = B * H * P * N, an = B * H * (N / 2);
+    std::vector<void *> temps;
+    hipError_t e = hipSuccess;
+    auto temp = [&](size_t n) -> float * {
+        void *p = nullptr;
+        if (e == hipSuccess) e = hipMallocAsync(&p, n * sizeof(float), s);
+        if (e != hipSuccess) return nullptr;
+        temps.push_back(p);
+        return static_cast<float *>(p);
+    };
+    const bool want = in->want_state != 0;
+    float *h = want ? out->state.h : temp(sn);
+    float *lu = want ? out->state.last_u : temp(sn);
+    float *ang = rot ? (want ? out->state.angle : temp(an)) : nullptr;
+    const m3_ssm_state *st = in->state;
+    if (e == hipSuccess) {
+        if (st != nullptr) {
+            e = hipMemcpyAsync(h, st->h, sn * sizeof(float), hipMemcpyDeviceToDevice, s);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(lu, st->last_u, sn * sizeof(float), hipMemcpyDeviceToDevice, s);
+        } else {
+            e = zero_async(h, sn, s);
+            if (e == hipSuccess) e = zero_async(lu, sn, s);
+        }
+        if (e == hipSuccess && rot)
+            e = (st != nullptr && st->angle != nullptr)
+                    ? hipMemcpyAsync(ang, st->angle, an * sizeof(float), hipMemcpyDeviceToDevice, s)
+                    : zero_async(ang, an, s);
+    }
+    m3::StepLaunch a{};
+    a.batch = B;
+    a.heads = H;
+    a.head_dim = P;
+    a.d_state = N;
+    a.rank = R;
+    a.bf16 = in->dtype == M3_BF16;
+    a.a_log = in->a_log;
+    a.d_skip = in->d_skip;
+    a.h = h;
+    a.last_u = lu;
+    a.angle = ang;
+    a.in_bstride = T;
+    for (size_t t = 0; t < T && e == hipSuccess; ++t) {
+        a.x = static_cast<const char *>(in->x) + t * H * P * R * es;
+        a.b = static_cast<const char *>(in->b) + t * H * N * R * es;
+        a.c = static_cast<const char *>(in->c) + t * H * N * R * es;
+        a.theta = rot ? static_cast<const char *>(in->theta) + t * H * (N / 2) * es : nullptr;
+        a.dt = in->dt + t * H;
+        a.lambda = in->lambda + t * H;
+        a.y = static_cast<char *>(out->y) + t * H * P * R * es;
+        e = m3::launch_step(a, s);
+        if (e == hipSuccess) g_launches.fetch_add(1, std::memory_order_relaxed);
+    }
+    for (void *p : temps) (void)hipFreeAsync(p, s);
+    if (e != hipSuccess) return hip_fail(e, "scan by steps");
+    return ok();
+}
+
 // m3_scan with f16 storage: the f32 scan on widened copies of x, b, c and
 // theta, y narrowed back (the arguments are validated by the caller).
 static m3_status scan_f16(const m3_scan_inputs *in, const m3_scan_output *out, void *stream,
@@ -288,16 +374,14 @@ static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
         return fail(M3_ERR_CONFIG, "SSM dimensions must all be positive");
     if (in->theta != nullptr && in->d_state % 2 != 0)   // scan.rs:485-489
         return fail(M3_ERR_CONFIG, "rotational dynamics require an even d_state");
-    if (in->head_dim > m3::kScanMaxHeadDim)
-        return fail(M3_ERR_UNSUPPORTED, "head_dim %zu exceeds the scan kernel's %zu",
-                    in->head_dim, m3::kScanMaxHeadDim);
-    if (in->d_state > m3::kScanMaxState)
-        return fail(M3_ERR_UNSUPPORTED, "d_state %zu exceeds the scan kernel's %zu",
-                    in->d_state, m3::kScanMaxState);
-    const size_t rows = scan_rows(in->dtype, in->d_state);
-    if (in->rank > rows)
-        return fail(M3_ERR_UNSUPPORTED, "MIMO rank %zu exceeds %zu rows per chunk", in->rank,
-                    rows);
+    // shapes beyond the scan kernels run token by token on the step kernel
+    const bool by_steps = scan_by_steps_needed(in);
+    if (by_steps && !step_covers(in))
+        return fail(M3_ERR_UNSUPPORTED, "head_dim %zu, d_state %zu and rank %zu exceed both the "
+                    "scan kernels (head_dim <= %zu, d_state <= %zu, rank <= %zu) and the step "
+                    "kernel (2 d_state rank + head_dim rank <= %zu)", in->head_dim, in->d_state,
+                    in->rank, m3::kScanMaxHeadDim, m3::kScanMaxState,
+                    scan_rows(in->dtype, in->d_state), kStepLdsFloats);
     const m3_ssm_state *st = in->state;
     if (st != nullptr && (st->h == nullptr || st->last_u == nullptr))
         return fail(M3_ERR_ARGUMENT, "state needs both h and last_u");
@@ -345,6 +429,17 @@ static m3_status scan_entry(const m3_scan_inputs *in, const m3_scan_output *out,
         if (gate_z != nullptr || theta_stride != 0)
             return fail(M3_ERR_UNSUPPORTED, "the gate and theta in place cover bf16 storage");
         return scan_f16(in, out, stream, path);
+    }
+    if (by_steps) {
+        if (theta_stride != 0)
+            return fail(M3_ERR_UNSUPPORTED, "theta in place covers the scan kernels' shapes");
+        const m3_status st2 = scan_by_steps(in, out, s);
+        if (st2 != M3_OK || gate_z == nullptr) return st2;
+        hipError_t e = m3::launch_mixer_gate(B * in->seq, H * P * in->rank, out->y, gate_z,
+                                             gate_stride, nullptr, 0.0f, out->y, s);
+        if (e != hipSuccess) return hip_fail(e, "gate launch");
+        g_launches.fetch_add(1, std::memory_order_relaxed);
+        return ok();
     }
 
     m3::ScanLaunch a{};
@@ -523,6 +618,10 @@ m3_status m3_scan_no_alloc(const m3_scan_inputs *in, const m3_scan_output *out, 
     if (in->dtype == M3_F16)
         return fail(M3_ERR_UNSUPPORTED, "f16 storage widens into temporaries it allocates: "
                     "call m3_scan instead");
+    if (scan_by_steps_needed(in))
+        return fail(M3_ERR_UNSUPPORTED, "head_dim %zu, d_state %zu and rank %zu are beyond the "
+                    "scan kernels' tiles: call m3_scan instead", in->head_dim, in->d_state,
+                    in->rank);
     m3_scan_inputs local = *in;
     local.workspace = nullptr;
     local.workspace_bytes = 0;

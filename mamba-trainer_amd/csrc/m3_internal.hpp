@@ -22,6 +22,12 @@ struct StepLaunch {
     // Factored last_u (last_u null): the previous token's x [B,H,P,R] and
     // unrotated b [B,H,N,R] in the storage type, overwritten with this step's.
     void *x_prev, *b_prev;
+    // 0: x, b, c, theta, dt, lambda and y in the [B,H,...] layout above.
+    // Otherwise the token rows between consecutive batch entries of those
+    // (entry (b, h) at row b * in_bstride * H + h, as one token of a
+    // [B,T,H,...] window with in_bstride = T); such launches take the
+    // generic body.
+    size_t in_bstride;
 };
 hipError_t launch_step(const StepLaunch &a, hipStream_t stream);
 // Shapes the factored form (last_u null) covers: the vector body's.

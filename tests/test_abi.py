@@ -117,9 +117,11 @@ def _scan_inputs(**kw):
     (dict(rank=0), 1, "MIMO rank must be positive"),
     (dict(d_state=5, theta=1), 1, "rotational dynamics require an even d_state"),
     (dict(head_dim=0), 1, "SSM dimensions must all be positive"),
-    (dict(head_dim=256), 4, "head_dim 256 exceeds"),
-    (dict(d_state=512), 4, "d_state 512 exceeds"),
-    (dict(rank=65, dtype=1), 4, "MIMO rank 65 exceeds"),
+    # beyond the scan kernels the scan runs on the step kernel, so only shapes
+    # beyond that one's LDS are refused
+    (dict(head_dim=20000), 4, "head_dim 20000, d_state 4 and rank 1 exceed both"),
+    (dict(d_state=8192), 4, "d_state 8192 and rank 1 exceed both"),
+    (dict(rank=2000, dtype=1), 4, "and rank 2000 exceed both"),
     (dict(dtype=7), 6, "unknown dtype"),
     (dict(want_state=1), 6, "want_state needs output h and last_u"),
 ])
@@ -137,7 +139,7 @@ def test_scan_argument_validation_before_device_work(kw, status, message):
 @pytest.mark.parametrize("kw,status,message", [
     (dict(rank=0), 1, "MIMO rank must be positive"),
     (dict(d_state=5, theta=1), 1, "rotational dynamics require an even d_state"),
-    (dict(head_dim=256), 4, "head_dim 256 exceeds"),
+    (dict(head_dim=20000), 4, "exceed both the scan kernels"),
     (dict(want_state=1), 6, "want_state needs output h and last_u"),
     (dict(x=None, seq=8), 6, "x, b, c, dt, a_log, lambda and y are required"),
 ])
@@ -177,6 +179,24 @@ def test_f16_storage_entry_points_that_do_not_take_it():
         8, 2048, 12, 64, 128, 1, dt, None, None, None, None, None, None, None, None, None, 64, 1,
         None, 0)))
     assert q(_lib.M3_F16) == q(_lib.M3_F32) > 0
+
+
+def test_no_alloc_refuses_shapes_beyond_the_scan_kernels():
+    """Shapes beyond the scan kernels' tiles run token by token on the step
+    kernel, with temporaries for the carried state when it is not wanted, so
+    m3_scan_no_alloc refuses them before any device work."""
+    from mamba3 import _lib
+    L = _lib.lib()
+    fake = 1 << 20
+    before = L.m3_launch_count()
+    for P, N, R in ((192, 64, 1), (64, 320, 1), (16, 16, 80)):
+        cin = _lib.ScanInputsC(1, 64, 2, P, N, R, _lib.M3_F32, fake, fake, fake, fake, fake, fake,
+                               None, None, None, 64, 0, None, 0)
+        cout = _lib.ScanOutputC(fake, _lib.SsmStateC())
+        assert L.m3_scan_no_alloc(C.byref(cin), C.byref(cout), None) == _lib.M3_ERR_UNSUPPORTED
+        assert b"beyond the scan kernels" in L.m3_last_error()
+        assert L.m3_scan_workspace_bytes(C.byref(cin)) == 0
+    assert L.m3_launch_count() == before
 
 
 def test_python_api_rejects_host_tensors():

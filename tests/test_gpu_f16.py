@@ -30,6 +30,7 @@ def _f16(a):
     (2, 300, 3, 64, 128, 1, True, True, True, True),     # chunk-parallel (three launches)
     (1, 200, 2, 64, 64, 2, True, False, True, False),    # single pass, rank 2
     (1, 100, 2, 32, 16, 1, False, True, False, True),    # generic kernel
+    (1, 30, 2, 160, 32, 1, True, True, True, True),      # head_dim 160: token by token
 ])
 def test_f16_scan_is_the_f32_scan_rounded(B, T, H, P, N, R, theta, skip, state, chunk_parallel):
     from mamba3.ssm import ScanInputs, SsmState, mamba3_scan

@@ -146,6 +146,69 @@ def test_scan_features_against_f64(B, T, H, P, N, R, theta, skip, state, dtype, 
         assert angle_err(ang, ang64) <= (1e-4 if dtype == "f32" else 1e-3)
 
 
+# Shapes beyond the scan kernels' tiles (head_dim over 128, d_state over 256,
+# rank over the rows of a chunk): the scan runs token by token on the step
+# kernel's generic body, which the reference's mamba3_scan (no shape limits,
+# scan.rs:458-618) is held to through the f64 recurrence.
+BEYOND_CASES = [
+    # B, T, H, P, N, R, theta, skip, state, want_state, dtype
+    (2, 40, 2, 160, 64, 1, True, True, True, True, "f32"),      # head_dim 160
+    (1, 30, 2, 32, 320, 1, True, False, True, True, "bf16"),    # d_state 320
+    (2, 20, 1, 16, 16, 72, True, True, False, True, "f32"),     # rank 72 (32 rows a chunk)
+    (1, 25, 2, 16, 16, 80, False, True, True, False, "bf16"),   # rank 80 (64 rows), no state out
+]
+
+
+@pytest.mark.parametrize("B,T,H,P,N,R,theta,skip,state,want_state,dtype", BEYOND_CASES)
+def test_shapes_beyond_the_scan_kernels_against_f64(B, T, H, P, N, R, theta, skip, state,
+                                                     want_state, dtype):
+    from mamba3 import _lib
+    rng = np.random.default_rng(zlib.crc32(repr(("beyond", B, T, H, P, N, R)).encode()))
+    inp = baseline_inputs(rng, B, T, H, P, N, R, theta=theta, dtype=dtype,
+                          theta_per_head=False, state=state)
+    d_skip = rng.uniform(-1, 1, H).astype(np.float32) if skip else None
+    st = (inp["h0"], inp["last_u0"], inp.get("angle0")) if state else None
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    before = _lib.lib().m3_launch_count()
+    y, h, lu, ang = run_scan(inp, dtype=tdt, theta=theta, skip=d_skip, state=st,
+                             want_state=want_state)
+    launches = _lib.lib().m3_launch_count() - before
+    assert launches >= T, launches           # one step launch per token
+    y64, h64, lu64, ang64 = oracle_scan(inp, theta=theta, skip=d_skip, state=st)
+    tol = BF16_TOL if dtype == "bf16" else F32_TOL
+    print(f"beyond the scan kernels (P {P}, N {N}, R {R}, {dtype}): rel-L2 y {rel_l2(y, y64):.2e}",
+          flush=True)
+    assert rel_l2(y, y64) <= tol, ("y", rel_l2(y, y64))
+    if want_state:
+        assert rel_l2(h, h64) <= tol, ("h", rel_l2(h, h64))
+        assert rel_l2(lu, lu64) <= tol, ("last_u", rel_l2(lu, lu64))
+        if theta:
+            assert angle_err(ang, ang64) <= (1e-4 if dtype == "f32" else 1e-3)
+
+
+def test_gated_scan_beyond_the_scan_kernels():
+    """m3_scan_gated at a shape the scan kernels do not cover: the steps, then
+    the gate kernel, equal to m3_scan followed by m3_mixer_gate."""
+    import ctypes as C
+    from mamba3 import _lib
+    from mamba3.ssm import ScanInputs, mamba3_scan, mamba3_scan_gated
+    B, T, H, P, N, R = 2, 24, 2, 160, 32, 1
+    rng = np.random.default_rng(4242)
+    inp = baseline_inputs(rng, B, T, H, P, N, R, theta=True, dtype="bf16")
+    bf = torch.bfloat16
+    si = ScanInputs(dev(inp["x"], bf), dev(inp["b"], bf), dev(inp["c"], bf), dev(inp["dt"]),
+                    dev(inp["a_log"]), dev(inp["lam"])).with_theta(dev(inp["theta"], bf))
+    d = H * P * R
+    proj = torch.randn(B, T, d + 40, device="cuda:0").to(bf)
+    ref = mamba3_scan(si)
+    gated = torch.empty(B, T, d, dtype=bf, device="cuda:0")
+    _lib.check(_lib.lib().m3_mixer_gate(B * T, d, ref.y.data_ptr(), proj.data_ptr(), d + 40, None,
+                                        C.c_float(1e-5), gated.data_ptr(), None))
+    got = mamba3_scan_gated(si, proj)
+    torch.cuda.synchronize()
+    assert torch.equal(got.y.view(B, T, d), gated)
+
+
 # chunk_size sets the shortest segment of the chunk-parallel path (the state
 # passes between segments; inside one it advances in registers sub-chunk by
 # sub-chunk): segments of 1 to 64 sub-chunks, every rank, both storage types
@@ -222,8 +285,10 @@ def test_errors_surface_as_reference_errors():
     inp["theta"] = inp["theta"][..., :2]
     with pytest.raises(ConfigError, match="even d_state"):
         run_scan(inp)
-    inp = baseline_inputs(rng, 1, 8, 1, 16, 32, 40, theta=False)
-    with pytest.raises(UnsupportedError, match="rank"):
+    # rank 40 is past a chunk's rows but runs token by token on the step
+    # kernel; rank 300 is past that kernel's LDS as well
+    inp = baseline_inputs(rng, 1, 8, 1, 16, 32, 300, theta=False)
+    with pytest.raises(UnsupportedError, match="exceed both"):
         run_scan(inp, dtype=torch.float32, theta=False)
 
 
