@@ -72,7 +72,10 @@ __device__ __forceinline__ void conv_taps8(const float *w, const float *bias, si
 // silu (v holds the pre-silu values in, the final ones out): + bias8 (when
 // has_bias), then the RMSNorm over the state axis with gain w8 (when
 // has_norm), the sum over the row's lq lanes (lq consecutive lanes,
-// lq-aligned, a power of two; models/mamba3.rs:405-427).
+// lq-aligned, a power of two, all active; models/mamba3.rs:405-427).  Rows of
+// 8 or 16 lanes sum through DPP inside their 16-lane row (no LDS crossbar),
+// and the scale is v_rsq_f32 of mean + eps (within an ulp of 1 / sqrt): the
+// prologue kernel was bound by its instruction issue, not by its bytes.
 template <int R>
 __device__ __forceinline__ void bc_row8(float (&v)[R][8], const float (&bias8)[8], bool has_bias,
                                         const float (&w8)[8], bool has_norm, int lq, int n_state,
@@ -87,8 +90,17 @@ __device__ __forceinline__ void bc_row8(float (&v)[R][8], const float (&bias8)[8
             float ss = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) ss += v[r][j] * v[r][j];
-            ss = group_sum(ss, lq);
-            const float scale = 1.0f / sqrtf(ss / static_cast<float>(n_state) + eps);
+            if (lq == 16 || lq == 8) {
+                // within a 16-lane DPP row: xor 1, xor 2 (quad_perm), then the
+                // half-row mirror (8 lanes) and, for 16, the row mirror
+                ss += dpp_f<0xB1, 0xf, false>(ss);
+                ss += dpp_f<0x4E, 0xf, false>(ss);
+                ss += dpp_f<0x141, 0xf, false>(ss);
+                if (lq == 16) ss += dpp_f<0x140, 0xf, false>(ss);
+            } else {
+                ss = group_sum(ss, lq);
+            }
+            const float scale = __builtin_amdgcn_rsqf(ss * (1.0f / static_cast<float>(n_state)) + eps);
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[r][j] = v[r][j] * scale * w8[j];
         }

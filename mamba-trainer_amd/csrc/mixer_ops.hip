@@ -316,16 +316,18 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
     const uint16_t *plam = pdt + H;
     const uint16_t *pth = plam + (a.learned_lambda ? H : 0);
     const int nbc = 2 * H * lq;
+    const int lq_sh = __builtin_ctz(static_cast<unsigned>(lq));   // lq is a power of two
     const int nx = din / 8;
     const int thw = a.has_theta ? H * (N / 2) : 0;
     const int total = nbc + nx + thw / 8;
 
     for (int i = tid; i < total; i += 256) {
         if (i < nbc) {
-            const int u = i / lq, q = i - u * lq;
+            const int u = i >> lq_sh, q = i & (lq - 1);
             const int which = u >= H ? 1 : 0;
             const int h = u - which * H;
-            const uint16_t *s = (which ? pc : pb) + (h / per_group) * R * N + q * 8;
+            const int hg = per_group == 1 ? h : h / per_group;
+            const uint16_t *s = (which ? pc : pb) + hg * R * N + q * 8;
             const float *bias = which ? a.c_bias : a.b_bias;
             const size_t ch0 = static_cast<size_t>(s - px);
             float v[R][8];
