@@ -257,10 +257,15 @@ typedef struct m3_scan_grads {
 
 /* Backward of m3_scan on the same inputs (`in`, whose workspace must hold
  * m3_scan_backward_workspace_bytes(in) bytes, 256-byte aligned).  The forward
- * chunk states are recomputed; the forward outputs are not needed.  Covers
- * head_dim 64, d_state 64/128, rank 1/2/4 with aligned buffers (else
- * M3_ERR_UNSUPPORTED).  Partial sums inside a workgroup are accumulated with
- * LDS atomics, so repeated calls agree to f32 rounding, not bit for bit. */
+ * chunk states are recomputed; the forward outputs are not needed.  The
+ * chunk kernels take head_dim 64, d_state 64/128, rank 1/2/4 with aligned
+ * buffers; their partial sums inside a workgroup are accumulated with LDS
+ * atomics, so repeated calls agree to f32 rounding, not bit for bit.  Other
+ * shapes (and alignments) take the reverse mode of the recurrence token by
+ * token, one workgroup per sequence with states recomputed from checkpoints
+ * every 32 tokens (deterministic, and slow: a fallback), up to per-token
+ * vectors of 64 KB (2 head_dim rank + 4 d_state rank + 3 d_state/2 floats;
+ * beyond that M3_ERR_UNSUPPORTED, before any device work). */
 m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *grads, void *stream);
 
 /* Workspace bytes m3_scan_backward needs for these inputs (0 when the shape

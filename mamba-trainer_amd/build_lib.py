@@ -20,7 +20,8 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "mamba3", "libmamba3_hip.so")
 
 SOURCES = ["m3_api.cpp", "m3_mixer_api.cpp", "linear.cpp", "checkpoint.cpp", "ssd_scan.hip",
-           "ssd_scan_fast.hip", "ssd_scan_chunked.hip", "ssd_scan_backward.hip", "decode_step.hip", "mfma_selftest.hip",
+           "ssd_scan_fast.hip", "ssd_scan_chunked.hip", "ssd_scan_backward.hip",
+           "ssd_scan_backward_generic.hip", "decode_step.hip", "mfma_selftest.hip",
            "mixer_ops.hip", "skinny_gemm.hip"]
 ARCH = "gfx950"
 # Packed-FP32 instructions stay off: hipcc derives them from plain float code

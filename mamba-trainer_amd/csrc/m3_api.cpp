@@ -705,9 +705,9 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
         alignas(16) static float dummy[4] = {0, 0, 0, 0};
         chk.x = chk.b = chk.c = dummy;   // the copies are aligned: the shape decides
         chk.theta = in->theta ? dummy : nullptr;
-        if (!m3::scan_backward_supported(chk))
-            return fail(M3_ERR_UNSUPPORTED,
-                        "the scan backward covers head_dim 64, d_state 64/128, rank 1/2/4");
+        if (!m3::scan_backward_supported(chk) && !m3::scan_backward_generic_supported(chk))
+            return fail(M3_ERR_UNSUPPORTED, "the scan backward covers shapes whose per-token "
+                        "vectors fit 64 KB (2 P R + 4 N R + 3 N/2 floats)");
         const size_t rows = B * in->seq * H, R = in->rank;
         F16Copies cp(s);
         li.x = cp.add(in->x, rows * P * R, true, false);
@@ -747,11 +747,14 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
         return ok();
     }
     const m3::ScanLaunch a = scan_launch_of(in);
-    if (!m3::scan_backward_supported(a))
-        return fail(M3_ERR_UNSUPPORTED,
-                    "the scan backward covers head_dim 64, d_state 64/128, rank 1/2/4 with "
-                    "16-byte aligned buffers");
-    {
+    // shapes (or alignments) the chunk kernels do not take run the reverse
+    // mode of the recurrence token by token
+    const bool generic = !m3::scan_backward_supported(a);
+    if (generic && !m3::scan_backward_generic_supported(a))
+        return fail(M3_ERR_UNSUPPORTED, "the scan backward covers shapes whose per-token vectors "
+                    "fit 64 KB (2 P R + 4 N R + 3 N/2 floats): head_dim %zu, d_state %zu, rank %zu",
+                    P, N, in->rank);
+    if (!generic) {
         // gradient buffers are written (and dh read) in 8- and 16-byte pieces
         const void *ptrs[] = {g->dx, g->db, g->dc, g->dtheta, g->dh, g->dh0, g->dlast_u0, g->dlast_u};
         for (const void *q : ptrs)
@@ -759,7 +762,8 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
                 return fail(M3_ERR_UNSUPPORTED,
                             "the scan backward needs 16-byte aligned gradient buffers");
     }
-    const size_t need = m3::scan_backward_workspace(a);
+    const size_t need = generic ? m3::scan_backward_generic_workspace(a)
+                                : m3::scan_backward_workspace(a);
     if (in->workspace == nullptr || in->workspace_bytes < need ||
         (reinterpret_cast<uintptr_t>(in->workspace) & 255u) != 0)
         return fail(M3_ERR_ARGUMENT, "the backward needs a 256-byte aligned workspace of %zu bytes",
@@ -780,9 +784,15 @@ m3_status m3_scan_backward(const m3_scan_inputs *in, const m3_scan_grads *g, voi
     gr.dh0 = st ? g->dh0 : nullptr;
     gr.dlast_u0 = st ? g->dlast_u0 : nullptr;
     gr.dangle0 = (st && st->angle && in->theta) ? g->dangle0 : nullptr;
-    e = m3::launch_scan_backward(a, gr, in->workspace, s);
-    if (e != hipSuccess) return hip_fail(e, "scan backward launch");
-    g_launches.fetch_add((in->theta ? 5 : 4) + (g->dlast_u ? 2 : 0), std::memory_order_relaxed);
+    if (generic) {
+        e = m3::launch_scan_backward_generic(a, gr, in->workspace, s);
+        if (e != hipSuccess) return hip_fail(e, "scan backward launch");
+        g_launches.fetch_add(2, std::memory_order_relaxed);
+    } else {
+        e = m3::launch_scan_backward(a, gr, in->workspace, s);
+        if (e != hipSuccess) return hip_fail(e, "scan backward launch");
+        g_launches.fetch_add((in->theta ? 5 : 4) + (g->dlast_u ? 2 : 0), std::memory_order_relaxed);
+    }
     if (g->dd_skip != nullptr && in->d_skip == nullptr) {
         e = hipMemsetAsync(g->dd_skip, 0, H * sizeof(float), s);
         if (e != hipSuccess) return hip_fail(e, "dd_skip");
@@ -797,7 +807,8 @@ size_t m3_scan_backward_workspace_bytes(const m3_scan_inputs *in) {
     a.x = a.b = a.c = dummy;   // alignment is checked at launch
     a.theta = in->theta ? dummy : nullptr;
     a.h0 = a.last_u0 = nullptr;
-    return m3::scan_backward_workspace(a);
+    const size_t w = m3::scan_backward_workspace(a);
+    return w ? w : m3::scan_backward_generic_workspace(a);
 }
 
 m3_status m3_ssd_chunked(const m3_ssd_args *in, void *y, float *final_state, void *stream) {

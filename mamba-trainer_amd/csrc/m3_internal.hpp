@@ -159,6 +159,13 @@ bool scan_backward_supported(const ScanLaunch &a);
 size_t scan_backward_workspace(const ScanLaunch &a);
 hipError_t launch_scan_backward(const ScanLaunch &a, const ScanGrads &g, void *workspace,
                                 hipStream_t stream);
+// The same gradients for any other shape whose per-token vectors fit 64 KB
+// of LDS (2 P R + 4 N R + 3 N/2 floats): the reverse mode of the recurrence,
+// token by token, one workgroup per sequence (ssd_scan_backward_generic.hip).
+bool scan_backward_generic_supported(const ScanLaunch &a);
+size_t scan_backward_generic_workspace(const ScanLaunch &a);
+hipError_t launch_scan_backward_generic(const ScanLaunch &a, const ScanGrads &g, void *workspace,
+                                        hipStream_t stream);
 
 // Largest head_dim / d_state the scan kernels are instantiated for.
 constexpr size_t kScanMaxHeadDim = 128;

@@ -295,8 +295,8 @@ def _three_launch_sizes(need, _lib):
      "dy, dx, db, dc, ddt, dlambda and da_log are required"),
     (dict(x=16, b=16, c=16, dt=16, a_log=16, lambda_=16, theta=16, d_state=4), {}, 6,
      "dtheta is required"),
-    (dict(x=16, b=16, c=16, dt=16, a_log=16, lambda_=16), {}, 4,
-     "the scan backward covers head_dim 64"),
+    (dict(x=16, b=16, c=16, dt=16, a_log=16, lambda_=16, head_dim=20000), {}, 4,
+     "the scan backward covers shapes whose per-token vectors fit 64 KB"),
 ])
 def test_scan_backward_argument_validation_before_device_work(kw, grads, status, message):
     """m3_scan_backward rejects bad arguments with the reference's rules and
@@ -333,9 +333,12 @@ def test_scan_backward_workspace_query():
     assert w1 % 256 == 0
     assert need(8, 2048, 12, 64, 128, 1, _lib.M3_F32) == w1
     assert need(2, 100, 3, 64, 64, 2, _lib.M3_BF16) > 0
-    assert need(1, 100, 2, 48, 128, 1, _lib.M3_BF16) == 0      # head_dim 48
-    assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) == 0       # d_state 96
-    assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) == 0      # rank 3
+    # other shapes take the token walk (its own workspace), up to 64 KB of
+    # per-token vectors
+    assert need(1, 100, 2, 48, 128, 1, _lib.M3_BF16) > 0      # head_dim 48
+    assert need(1, 100, 2, 64, 96, 1, _lib.M3_BF16) > 0       # d_state 96
+    assert need(1, 100, 2, 64, 128, 3, _lib.M3_BF16) > 0      # rank 3
+    assert need(1, 100, 2, 20000, 64, 1, _lib.M3_BF16) == 0   # beyond 64 KB of LDS
 
 
 def test_no_alloc_scan_rejects_beyond_its_scratch():

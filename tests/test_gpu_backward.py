@@ -94,6 +94,37 @@ def test_backward_against_f64_reverse_mode(case):
     assert checked >= 6
 
 
+# Shapes the chunk kernels do not take (head_dim other than 64, d_state other
+# than 64 / 128, rank other than 1, 2, 4): the reverse mode of the recurrence,
+# token by token, against the same f64 reverse mode.
+GENERIC_CASES = [
+    # B, T, H, P, N, R, theta, skip, state, dtype
+    (1, 40, 2, 48, 32, 1, True, True, True, "f32"),
+    (2, 33, 1, 16, 16, 3, True, False, True, "f32"),
+    (1, 50, 1, 160, 64, 1, False, True, False, "f32"),
+    (1, 70, 2, 32, 96, 2, True, True, True, "bf16"),
+    (1, 37, 1, 24, 8, 5, True, True, False, "bf16"),
+]
+
+
+@pytest.mark.parametrize("case", GENERIC_CASES, ids=[repr(c) for c in GENERIC_CASES])
+def test_generic_backward_against_f64_reverse_mode(case):
+    from mamba3 import _lib
+    before = _lib.lib().m3_launch_count()
+    g, ref = _run(case)
+    assert _lib.lib().m3_launch_count() - before == 2   # the token walk and the head sums
+    tol = BF16_TOL if case[-1] == "bf16" else F32_TOL
+    checked = 0
+    for k in NAMES:
+        mine = getattr(g, k)
+        if mine is None or ref.get(k) is None:
+            continue
+        err = rel_l2(host(mine), ref[k])
+        assert err <= tol, (k, err)
+        checked += 1
+    assert checked >= 6
+
+
 def test_upstream_state_gradient_only():
     """dy = 0 with dL/dh and dL/dangle of the output state: the whole gradient
     flows back through the reverse state pass alone."""
@@ -238,11 +269,12 @@ def test_backward_errors_surface_as_reference_errors():
     from mamba3 import ArgumentError, UnsupportedError
     from mamba3.ssm import ScanInputs, mamba3_scan_backward
     rng = np.random.default_rng(4)
-    inp = baseline_inputs(rng, 1, 10, 1, 32, 16, 1, theta=True)
+    # head_dim 9000: its x and dy rows alone exceed the token walk's 64 KB
+    inp = baseline_inputs(rng, 1, 10, 1, 9000, 16, 1, theta=True)
     si = (ScanInputs(dev(inp["x"]), dev(inp["b"]), dev(inp["c"]), dev(inp["dt"]),
                      dev(inp["a_log"]), dev(inp["lam"])).with_theta(dev(inp["theta"])))
-    with pytest.raises(UnsupportedError):
-        mamba3_scan_backward(si, dev(np.zeros((1, 10, 1, 32, 1), np.float32)))
+    with pytest.raises(UnsupportedError, match="fit 64 KB"):
+        mamba3_scan_backward(si, dev(np.zeros((1, 10, 1, 9000, 1), np.float32)))
     # a gradient buffer off the 16-byte grid
     from mamba3 import _lib
     import ctypes as C

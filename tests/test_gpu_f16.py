@@ -140,11 +140,13 @@ def test_f16_steps_are_the_f32_steps_rounded(B, H, P, N, R, theta, skip):
     assert torch.equal(fac16.to_full().last_u, fac32.to_full().last_u)
 
 
-@pytest.mark.parametrize("theta,skip,state", [(True, True, True), (False, False, False)])
-def test_f16_backward_is_the_f32_backward_rounded(theta, skip, state):
+@pytest.mark.parametrize("theta,skip,state,P,N,R", [(True, True, True, 64, 64, 1),
+                                                   (False, False, False, 64, 64, 1),
+                                                   (True, True, True, 48, 32, 2)])   # token walk
+def test_f16_backward_is_the_f32_backward_rounded(theta, skip, state, P, N, R):
     from mamba3.ssm import ScanInputs, SsmState, mamba3_scan_backward
-    B, T, H, P, N, R = 1, 160, 2, 64, 64, 1
-    rng = np.random.default_rng(1616 + theta + 2 * state)
+    B, T, H = 1, 160, 2
+    rng = np.random.default_rng(1616 + theta + 2 * state + P)
     inp = baseline_inputs(rng, B, T, H, P, N, R, theta=theta, dtype="f32", state=state)
     x16, b16, c16 = _f16(inp["x"]), _f16(inp["b"]), _f16(inp["c"])
     th16 = _f16(inp["theta"]) if theta else None
