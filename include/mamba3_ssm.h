@@ -220,12 +220,16 @@ size_t m3_scan_workspace_bytes(const m3_scan_inputs *in);
  * the three launches' fits, the three launches run (results equal to rounding);
  * shapes whose workspace exceeds it on either form return M3_ERR_UNSUPPORTED
  * before any device work.  Otherwise results are those of m3_scan with a
- * caller workspace, bit for bit.  Every call on a GPU shares
- * that GPU's array: calls that overlap on one GPU (different streams, or
- * different host threads without ordering) race and give wrong results.  The
+ * caller workspace, bit for bit.  Every call on a GPU shares that GPU's
+ * array, so calls on one GPU must not overlap.  An eager call on a stream
+ * other than the previous eager call's, while that call may still run (its
+ * completion event, recorded after it, is pending), returns M3_ERR_ARGUMENT
+ * before any device work instead of racing; order such calls on one stream or
+ * with an event.  Calls captured into a HIP graph, and the graph's replays,
+ * are not tracked: overlapping them races and gives wrong results.  The
  * scratch needs no clearing: the chunk-parallel kernels write every byte they
  * later read within one call.  It calls no hipMalloc, hipFree or allocating
- * library routine. */
+ * library routine (the guard's event is created once per device). */
 m3_status m3_scan_no_alloc(const m3_scan_inputs *in, const m3_scan_output *out, void *stream);
 
 /* Gradients of mamba3_scan for the loss L, given dL/dy.  The reference gets

@@ -584,16 +584,18 @@ std::mutex g_scratch_mu;
 void *g_scratch[kMaxDevices] = {};
 
 // The current device's copy of `scratch` (nullptr and a message on failure).
-void *scratch_for_current_device() {
-    int dev = -1;
+// The current device's scratch address (dev receives the device), or NULL
+// with the error recorded in *st.
+void *scratch_for_current_device(int &dev, m3_status *st) {
+    dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) {
-        hip_fail(e, "hipGetDevice");
+        *st = hip_fail(e, "hipGetDevice");
         return nullptr;
     }
     if (dev < 0 || dev >= kMaxDevices) {
-        fail(M3_ERR_UNSUPPORTED, "device %d is beyond the %d devices the static scratch covers", dev,
-             kMaxDevices);
+        *st = fail(M3_ERR_UNSUPPORTED, "device %d is beyond the %d devices the static scratch covers",
+                   dev, kMaxDevices);
         return nullptr;
     }
     std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -601,13 +603,24 @@ void *scratch_for_current_device() {
         void *p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || p == nullptr) {
-            hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+            *st = hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
             return nullptr;
         }
         g_scratch[dev] = p;
     }
     return g_scratch[dev];
 }
+
+// Overlap guard of the eager (not graph-captured) calls: per device, the
+// stream of the last call and an event recorded after it.  A call on another
+// stream while that event is pending would race on the same scratch, so it is
+// refused instead.  The lock is held from the check to the record, so host
+// threads cannot slip a call in between.  Calls captured into a graph (and
+// the graph's replays) are not tracked.
+std::mutex g_guard_mu;
+hipStream_t g_guard_stream[kMaxDevices];
+hipEvent_t g_guard_event[kMaxDevices];
+bool g_guard_set[kMaxDevices];
 
 }  // namespace
 
@@ -640,13 +653,43 @@ m3_status m3_scan_no_alloc(const m3_scan_inputs *in, const m3_scan_output *out, 
                     "this scan needs %zu bytes of scratch; m3_scan_no_alloc's static scratch holds "
                     "%zu (%d MiB): call m3_scan with a caller workspace instead",
                     need, kNoAllocScratchBytes, M3_NO_ALLOC_SCRATCH_MIB);
-    if (need > 0) {
-        void *p = scratch_for_current_device();
-        if (p == nullptr) return M3_ERR_HIP;
-        local.workspace = p;
-        local.workspace_bytes = kNoAllocScratchBytes;
+    if (need == 0) return scan_entry(&local, out, nullptr, 0, stream, path);
+    int dev = -1;
+    m3_status st = M3_ERR_HIP;
+    void *p = scratch_for_current_device(dev, &st);
+    if (p == nullptr) return st;
+    local.workspace = p;
+    local.workspace_bytes = kNoAllocScratchBytes;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s, &cap);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (cap != hipStreamCaptureStatusNone) return scan_entry(&local, out, nullptr, 0, stream, path);
+    std::lock_guard<std::mutex> lock(g_guard_mu);
+    if (g_guard_set[dev] && g_guard_stream[dev] != s) {
+        e = hipEventQuery(g_guard_event[dev]);
+        if (e == hipErrorNotReady) {
+            (void)hipGetLastError();   // a pending event is not an error of the next launch
+            return fail(M3_ERR_ARGUMENT, "an m3_scan_no_alloc call on another stream may still be "
+                        "using this GPU's scratch: order the calls (one stream, or an event "
+                        "between them), or give each stream m3_scan with its own workspace");
+        }
+        if (e != hipSuccess) return hip_fail(e, "hipEventQuery");
     }
-    return scan_entry(&local, out, nullptr, 0, stream, path);
+    st = scan_entry(&local, out, nullptr, 0, stream, path);
+    if (st != M3_OK) return st;
+    if (g_guard_event[dev] == nullptr) {
+        e = hipEventCreateWithFlags(&g_guard_event[dev], hipEventDisableTiming);
+        if (e != hipSuccess) {
+            g_guard_event[dev] = nullptr;
+            return hip_fail(e, "hipEventCreateWithFlags");
+        }
+    }
+    e = hipEventRecord(g_guard_event[dev], s);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+    g_guard_stream[dev] = s;
+    g_guard_set[dev] = true;
+    return ok();
 }
 
 static m3::ScanLaunch scan_launch_of(const m3_scan_inputs *in) {

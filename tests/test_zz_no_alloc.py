@@ -109,3 +109,42 @@ def test_no_alloc_mimo_and_real_dynamics():
     assert ref[4] > 0
     for name, r, g in zip(("y", "h", "last_u"), ref[:3], got[:3]):
         assert _same(r, g), name
+
+
+@pytest.mark.gpu
+def test_no_alloc_refuses_an_overlapping_call_on_another_stream():
+    """Two eager calls on different streams would share the GPU's scratch: the
+    second is refused with M3_ERR_ARGUMENT while the first may still run (here
+    it is queued behind a long product on its stream), and accepted once the
+    first has finished; the accepted call gives the workspace scan's bytes."""
+    from mamba3 import _lib
+    L = _lib.lib()
+    inp = _inputs(31, 2, 512, 4, 128, 1, torch.bfloat16)
+    B, T, H, P, N, R = (inp[k] for k in ("B", "L", "H", "P", "N", "R"))
+    st_c = _lib.SsmStateC(inp["state"][0].data_ptr(), inp["state"][1].data_ptr(),
+                          _ptr(inp["state"][2]))
+    cin = _lib.ScanInputsC(B, T, H, P, N, R, _lib.M3_BF16, inp["x"].data_ptr(),
+                           inp["b"].data_ptr(), inp["c"].data_ptr(), inp["dt"].data_ptr(),
+                           inp["a_log"].data_ptr(), inp["lam"].data_ptr(), _ptr(inp["theta"]),
+                           _ptr(inp["d_skip"]), C.pointer(st_c), 64, 1, None, 0)
+    assert L.m3_scan_workspace_bytes(C.byref(cin)) > 0   # the scratch is used
+    y = torch.empty((B, T, H, P, R), device=DEV, dtype=torch.bfloat16)
+    h, u = torch.empty((B, H, P, N), device=DEV), torch.empty((B, H, P, N), device=DEV)
+    ang = torch.empty((B, H, N // 2), device=DEV)
+    cout = _lib.ScanOutputC(y.data_ptr(), _lib.SsmStateC(h.data_ptr(), u.data_ptr(), ang.data_ptr()))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s1):
+        m = torch.randn(4096, 4096, device=DEV)
+        for _ in range(24):
+            m = torch.mm(m, m) * 1e-3
+    assert L.m3_scan_no_alloc(C.byref(cin), C.byref(cout), C.c_void_p(s1.cuda_stream)) == _lib.M3_OK
+    assert L.m3_scan_no_alloc(C.byref(cin), C.byref(cout),
+                              C.c_void_p(s2.cuda_stream)) == _lib.M3_ERR_ARGUMENT
+    assert b"another stream" in L.m3_last_error()
+    torch.cuda.synchronize()
+    y.fill_(float("nan"))
+    assert L.m3_scan_no_alloc(C.byref(cin), C.byref(cout), C.c_void_p(s2.cuda_stream)) == _lib.M3_OK
+    torch.cuda.synchronize()
+    ref = _call(inp, False)
+    assert torch.equal(y, ref[0]) and torch.equal(h, ref[1]) and torch.equal(u, ref[2])
