@@ -171,9 +171,12 @@ def test_autograd_node_matches_the_direct_backward():
     assert rel_l2(host(d_skip.grad), host(g.d_skip)) <= 1e-6
 
 
-@pytest.mark.parametrize("dtype,R,rot", [("f32", 1, True), ("f32", 2, False), ("bf16", 1, True),
-                                         ("bf16", 4, True)])
-def test_two_windows_chained_through_the_state(dtype, R, rot):
+@pytest.mark.parametrize("dtype,R,rot,P,N", [("f32", 1, True, 64, 64), ("f32", 2, False, 64, 64),
+                                             ("bf16", 1, True, 64, 64), ("bf16", 4, True, 64, 64),
+                                             # the backward's token walk; the second
+                                             # with the forward token by token too
+                                             ("f32", 3, True, 48, 32), ("f32", 1, True, 160, 32)])
+def test_two_windows_chained_through_the_state(dtype, R, rot, P, N):
     """Two windows joined through SsmState (the second starts from the first's
     h, last_u and angle), differentiated end to end by autograd: the
     gradients equal those of the single window over the whole sequence.  The
@@ -182,7 +185,7 @@ def test_two_windows_chained_through_the_state(dtype, R, rot):
     the last_u adjoint (scan.rs:521-535, 599-618)."""
     from mamba3.ssm import ScanInputs, SsmState, mamba3_scan, mamba3_scan_backward
     rng = np.random.default_rng(11 + R)
-    B, T, H, P, N, cut = 1, 150, 2, 64, 64, 70
+    B, T, H, cut = 1, 150, 2, 70
     inp = baseline_inputs(rng, B, T, H, P, N, R, theta=rot, dtype=dtype, theta_per_head=False)
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     keys = ("x", "b", "c", "dt", "lam") + (("theta",) if rot else ())
