@@ -30,7 +30,6 @@ namespace m3 {
 namespace {
 
 constexpr int kStepThreads = 256;
-constexpr int kMaxRank = 8;        // register-resident y partials per row
 constexpr int kStepConvTaps = static_cast<int>(kMixerStepConvTaps);
 
 template <typename T>
@@ -500,7 +499,8 @@ mixer_step_kernel(MixerStepLaunch m) {
 }
 
 // Generic body for shapes the vector body does not cover (odd N, N > 256,
-// rank above kMaxRank): one thread per state row.
+// rank other than 1, 2, 3, 4 or 8, inputs at a batch stride): one thread per
+// state row.
 template <typename T>
 __global__ void __launch_bounds__(kStepThreads)
 step_kernel_generic(StepLaunch a) {

@@ -61,7 +61,7 @@ hipError_t launch_mfma_selftest(int *result_host) {
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipMemcpy(result_host, dev, sizeof(int), hipMemcpyDeviceToHost);
-    hipFree(dev);
+    (void)hipFree(dev);
     return e;
 }
 

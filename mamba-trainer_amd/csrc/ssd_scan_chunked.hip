@@ -184,8 +184,6 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int g = lane >> 4;
-    const int c = lane & 15;
 
     const size_t H = a.heads, L = a.seq;
     const size_t bhs = blockIdx.x;
@@ -195,8 +193,6 @@ chunk_state_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     const bool rot = a.theta != nullptr;
 
     const int sub = lane / G::SW;
-    const int my_t = lane % G::SW;
-    const bool tok_lane = my_t < QT;
     const int i0 = wave * G::PW + sub * PPL;
 
     const SeqBufs rs = seq_bufs<T, N, P, R>(a, bb, hh);
@@ -868,21 +864,13 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int g = lane >> 4;
-    const int c = lane & 15;
 
     const size_t H = a.heads, L = a.seq;
     const size_t bhs = blockIdx.x;
     const int seg = static_cast<int>(bhs % nseg);
     const size_t bh = bhs / nseg;
     const size_t bb = bh / H, hh = bh % H;
-    const bool rot = a.theta != nullptr;
 
-    const int sub = lane / G::SW;
-    const int my_t = lane % G::SW;
-    const bool tok_lane = my_t < QT;
-    const int i0 = wave * G::PW + sub * PPL;
-    const int pcol = 16 * wave + c;
 
     const SeqBufs rs = seq_bufs<T, N, P, R>(a, bb, hh);
     const int h_end = min(kseg, nsub - seg * kseg);
@@ -2863,7 +2851,6 @@ chunk_scan_fused_kernel(ScanLaunch a, FusedWs ws, int nsub, int kseg, int nseg, 
     constexpr int QT = G::QT, NH = G::NH, PPL = G::PPL, PW = G::PW;
     constexpr int NT = 4;             // 16-row tiles of a sub-chunk
     constexpr int NF = N / 32;        // state k-blocks (a pair's halves side by side)
-    constexpr int NTN = N / 16;
     constexpr int HV = PW / 8;
     constexpr int RB = CB * 16;       // bytes a row of the B / C tiles
     static_assert(G::SUBS == 1 && QT == 64 && PPL == PW, "lane = token, one segment a wave");
