@@ -104,6 +104,7 @@ GENERIC_CASES = [
     (1, 50, 1, 160, 64, 1, False, True, False, "f32"),
     (1, 70, 2, 32, 96, 2, True, True, True, "bf16"),
     (1, 37, 1, 24, 8, 5, True, True, False, "bf16"),
+    (3, 1, 2, 40, 16, 1, True, True, True, "f32"),        # one token
 ]
 
 

@@ -176,3 +176,20 @@ def test_f16_backward_is_the_f32_backward_rounded(theta, skip, state, P, N, R):
         assert rel_l2(host(a), host(r.to(H16))) <= 1e-5, name
     for name in ("dt", "lam", "a_log"):
         assert rel_l2(host(getattr(g16, name)), host(getattr(g32, name))) <= 1e-5, name
+
+
+def test_f16_empty_window_passes_the_state_through():
+    """seq = 0 with f16 storage: nothing is widened, the state passes through."""
+    from mamba3.ssm import ScanInputs, SsmState, mamba3_scan
+    B, H, P, N = 2, 3, 64, 64
+    g = torch.Generator(device="cuda:0").manual_seed(3)
+    x = torch.empty(B, 0, H, P, 1, dtype=H16, device="cuda:0")
+    b = torch.empty(B, 0, H, N, 1, dtype=H16, device="cuda:0")
+    st = SsmState(torch.randn(B, H, P, N, device="cuda:0", generator=g),
+                  torch.randn(B, H, P, N, device="cuda:0", generator=g), None)
+    si = ScanInputs(x, b, b.clone(), torch.empty(B, 0, H, device="cuda:0"),
+                    torch.zeros(H, device="cuda:0"), torch.empty(B, 0, H, device="cuda:0"))
+    out = mamba3_scan(si.with_state(st).with_state_output(True))
+    torch.cuda.synchronize()
+    assert out.y.shape == x.shape and out.y.dtype == H16
+    assert torch.equal(out.state.h, st.h) and torch.equal(out.state.last_u, st.last_u)

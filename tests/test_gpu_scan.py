@@ -156,6 +156,7 @@ BEYOND_CASES = [
     (1, 30, 2, 32, 320, 1, True, False, True, True, "bf16"),    # d_state 320
     (2, 20, 1, 16, 16, 72, True, True, False, True, "f32"),     # rank 72 (32 rows a chunk)
     (1, 25, 2, 16, 16, 80, False, True, True, False, "bf16"),   # rank 80 (64 rows), no state out
+    (4, 1, 3, 192, 16, 1, True, True, True, True, "f32"),       # one token, head_dim 192
 ]
 
 
