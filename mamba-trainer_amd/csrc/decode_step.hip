@@ -235,7 +235,8 @@ __device__ __forceinline__ void mix_prologue(const MixerStepLaunch &m, size_t bh
             w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
             w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
         }
-        bc_row8<R>(v, bb, bias != nullptr, w, m.bc_norm != nullptr, lq, N, m.norm_eps);
+        bc_row8<R>(v, bb, bias != nullptr, w, m.bc_norm != nullptr, lq, 1.0f / static_cast<float>(N),
+                   m.norm_eps);
         float *dst = which ? craw : braw;
 #pragma unroll
         for (int j = 0; j < 8; ++j)

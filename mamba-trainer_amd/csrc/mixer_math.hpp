@@ -32,9 +32,7 @@ __device__ __forceinline__ void unpack8(const uint4 q, float *f) {
     }
 }
 
-__device__ __forceinline__ unsigned int pack2(float a, float b) {
-    return static_cast<unsigned int>(to_bits(a)) | (static_cast<unsigned int>(to_bits(b)) << 16);
-}
+__device__ __forceinline__ unsigned int pack2(float a, float b) { return pack_bf16x2(a, b); }
 
 // Eight channels ch .. ch+7 of the depthwise causal convolution at one
 // position (nn/conv.rs:60-225, fused.rs:780-832): f = bias + sum_j w[j] x_j
@@ -72,13 +70,14 @@ __device__ __forceinline__ void conv_taps8(const float *w, const float *bias, si
 // silu (v holds the pre-silu values in, the final ones out): + bias8 (when
 // has_bias), then the RMSNorm over the state axis with gain w8 (when
 // has_norm), the sum over the row's lq lanes (lq consecutive lanes,
-// lq-aligned, a power of two, all active; models/mamba3.rs:405-427).  Rows of
+// lq-aligned, a power of two, all active; models/mamba3.rs:405-427); inv_n is
+// 1 / d_state rounded to f32, the mean a multiply.  Rows of
 // 8 or 16 lanes sum through DPP inside their 16-lane row (no LDS crossbar),
 // and the scale is v_rsq_f32 of mean + eps (within an ulp of 1 / sqrt): the
 // prologue kernel was bound by its instruction issue, not by its bytes.
 template <int R>
 __device__ __forceinline__ void bc_row8(float (&v)[R][8], const float (&bias8)[8], bool has_bias,
-                                        const float (&w8)[8], bool has_norm, int lq, int n_state,
+                                        const float (&w8)[8], bool has_norm, int lq, float inv_n,
                                         float eps) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -100,7 +99,7 @@ __device__ __forceinline__ void bc_row8(float (&v)[R][8], const float (&bias8)[8
             } else {
                 ss = group_sum(ss, lq);
             }
-            const float scale = __builtin_amdgcn_rsqf(ss * (1.0f / static_cast<float>(n_state)) + eps);
+            const float scale = __builtin_amdgcn_rsqf(ss * inv_n + eps);
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[r][j] = v[r][j] * scale * w8[j];
         }

@@ -264,7 +264,8 @@ mixer_prologue_kernel(PrologueLaunch a) {
 // ---------------------------------------------------------------- prologue, 16-byte path
 // The same prologue with every piece moved as 16-byte vectors of eight bf16.
 // Needs d_state a multiple of 8 with d_state / 8 dividing 64, d_inner and the
-// row width multiples of 8 and 16-byte aligned buffers (the host checks).
+// row width multiples of 8, a row width under 2^30 and H*N*R under 2^31 (the
+// per-item offsets are 32-bit), and 16-byte aligned buffers (the host checks).
 // Then theta's offset in the row, 2*d_inner + 2*G*R*N + H or 2H, is a multiple
 // of 8 as well: the width is that offset plus H*N/2, which is 0 or 4 mod 8
 // (4 only for odd H), and H or 2H is never 4 mod 8 for odd H.
@@ -299,7 +300,7 @@ __device__ __forceinline__ void xbc8(const PrologueLaunch &a, const uint16_t *xb
 
 template <int R, bool CONV>
 __global__ void __launch_bounds__(256)
-mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
+mixer_prologue_vec_kernel(PrologueLaunch a, int lq, int per_group, float inv_n) {
     const size_t t = blockIdx.x;
     const int tid = threadIdx.x;
     const int H = static_cast<int>(a.heads), N = static_cast<int>(a.d_state);
@@ -307,14 +308,18 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
     const int bcw = static_cast<int>(a.groups) * R * N;
     const size_t C = static_cast<size_t>(din) + 2 * static_cast<size_t>(bcw);
     const size_t pos = CONV ? t % a.seq_len : 0, seqi = CONV ? t / a.seq_len : 0;
-    const int per_group = H / static_cast<int>(a.groups);
     const uint16_t *__restrict__ row = static_cast<const uint16_t *>(a.projected) + t * a.width;
     const uint16_t *px = row + din;
-    const uint16_t *pb = px + din;
-    const uint16_t *pc = pb + bcw;
-    const uint16_t *pdt = pc + bcw;
+    const uint16_t *pdt = px + C;
     const uint16_t *plam = pdt + H;
     const uint16_t *pth = plam + (a.learned_lambda ? H : 0);
+    // This token's output rows; every per-item offset below is a 32-bit
+    // element offset from these (the row width is under 2^30, checked on the
+    // host), so the item loop does no 64-bit index arithmetic.
+    const size_t bc_row = static_cast<size_t>(H) * N * R;
+    uint16_t *ob = static_cast<uint16_t *>(a.b) + t * bc_row;
+    uint16_t *oc = static_cast<uint16_t *>(a.c) + t * bc_row;
+    uint16_t *ox = static_cast<uint16_t *>(a.x) + t * static_cast<size_t>(din);
     const int nbc = 2 * H * lq;
     const int lq_sh = __builtin_ctz(static_cast<unsigned>(lq));   // lq is a power of two
     const int nx = din / 8;
@@ -327,16 +332,17 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
             const int which = u >= H ? 1 : 0;
             const int h = u - which * H;
             const int hg = per_group == 1 ? h : h / per_group;
-            const uint16_t *s = (which ? pc : pb) + hg * R * N + q * 8;
+            // channel of state q*8, rank 0, within [x | B | C]
+            const unsigned ch0 = static_cast<unsigned>(din + which * bcw + (hg * R * N + q * 8));
             const float *bias = which ? a.c_bias : a.b_bias;
-            const size_t ch0 = static_cast<size_t>(s - px);
             float v[R][8];
 #pragma unroll
             for (int r = 0; r < R; ++r) xbc8<CONV>(a, px, pos, seqi, C, ch0 + r * N, v[r]);
             float bb[8], w[8];
+            const unsigned el = static_cast<unsigned>(h * N + q * 8);   // [H, N] element
             if (bias) {
-                const float4 b0 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8);
-                const float4 b1 = *reinterpret_cast<const float4 *>(bias + h * N + q * 8 + 4);
+                const float4 b0 = *reinterpret_cast<const float4 *>(bias + el);
+                const float4 b1 = *reinterpret_cast<const float4 *>(bias + el + 4);
                 bb[0] = b0.x; bb[1] = b0.y; bb[2] = b0.z; bb[3] = b0.w;
                 bb[4] = b1.x; bb[5] = b1.y; bb[6] = b1.z; bb[7] = b1.w;
             }
@@ -346,9 +352,8 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
                 w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
                 w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
             }
-            bc_row8<R>(v, bb, bias != nullptr, w, a.bc_norm != nullptr, lq, N, a.norm_eps);
-            uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(which ? a.c : a.b) +
-                                                   ((t * H + h) * N + q * 8) * R);
+            bc_row8<R>(v, bb, bias != nullptr, w, a.bc_norm != nullptr, lq, inv_n, a.norm_eps);
+            uint4 *dst = reinterpret_cast<uint4 *>((which ? oc : ob) + el * R);
 #pragma unroll
             for (int k = 0; k < R; ++k) {
                 unsigned int o[4];
@@ -360,14 +365,14 @@ mixer_prologue_vec_kernel(PrologueLaunch a, int lq) {
                 dst[k] = make_uint4(o[0], o[1], o[2], o[3]);
             }
         } else if (i < nbc + nx) {
-            const int k = i - nbc;
+            const unsigned k = static_cast<unsigned>(i - nbc);
             float f[8];
-            xbc8<CONV>(a, px, pos, seqi, C, static_cast<size_t>(k) * 8, f);
-            uint4 *dst = reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.x) + t * din) + k;
-            *dst = make_uint4(pack2(silu_fast(f[0]), silu_fast(f[1])), pack2(silu_fast(f[2]), silu_fast(f[3])),
-                              pack2(silu_fast(f[4]), silu_fast(f[5])), pack2(silu_fast(f[6]), silu_fast(f[7])));
+            xbc8<CONV>(a, px, pos, seqi, C, k * 8, f);
+            *reinterpret_cast<uint4 *>(ox + k * 8) =
+                make_uint4(pack2(silu_fast(f[0]), silu_fast(f[1])), pack2(silu_fast(f[2]), silu_fast(f[3])),
+                           pack2(silu_fast(f[4]), silu_fast(f[5])), pack2(silu_fast(f[6]), silu_fast(f[7])));
         } else {
-            const int k = (i - nbc - nx) * 8;
+            const unsigned k = static_cast<unsigned>(i - nbc - nx) * 8;
             uint16_t *to = static_cast<uint16_t *>(a.theta) + t * thw;
             *reinterpret_cast<uint4 *>(to + k) = *reinterpret_cast<const uint4 *>(pth + k);
         }
@@ -502,28 +507,23 @@ hipError_t launch_mixer_prologue(const PrologueLaunch &a, hipStream_t s) {
                      a.width % 8 == 0 && (a.rank == 1 || a.rank == 2 || a.rank == 4) &&
                      aligned16(a.projected) && aligned16(a.x) && aligned16(a.b) && aligned16(a.c) &&
                      aligned16(a.b_bias) && aligned16(a.c_bias) && aligned16(a.bc_norm) &&
-                     aligned16(a.theta) && a.width < (1u << 30) && aligned16(a.conv_w) &&
+                     aligned16(a.theta) && a.width < (1u << 30) && a.heads * N * a.rank < (1u << 31) &&
+                     aligned16(a.conv_w) &&
                      aligned16(a.conv_b) && aligned16(a.hist) && aligned16(a.new_hist);
     if (!vec) {
         hipLaunchKernelGGL(mixer_prologue_kernel, grid, dim3(256), 0, s, a);
         return hipGetLastError();
     }
-    const int l = static_cast<int>(lq);
+    const int l = static_cast<int>(lq), pg = static_cast<int>(a.heads / a.groups);
+    const float inv_n = 1.0f / static_cast<float>(N);   // rounded as the kernels' 1.0f / N
     const bool conv = a.conv_k != 0;
+    void (*kernel)(PrologueLaunch, int, int, float);
     switch (a.rank) {
-    case 1:
-        if (conv) hipLaunchKernelGGL((mixer_prologue_vec_kernel<1, true>), grid, dim3(256), 0, s, a, l);
-        else hipLaunchKernelGGL((mixer_prologue_vec_kernel<1, false>), grid, dim3(256), 0, s, a, l);
-        break;
-    case 2:
-        if (conv) hipLaunchKernelGGL((mixer_prologue_vec_kernel<2, true>), grid, dim3(256), 0, s, a, l);
-        else hipLaunchKernelGGL((mixer_prologue_vec_kernel<2, false>), grid, dim3(256), 0, s, a, l);
-        break;
-    default:
-        if (conv) hipLaunchKernelGGL((mixer_prologue_vec_kernel<4, true>), grid, dim3(256), 0, s, a, l);
-        else hipLaunchKernelGGL((mixer_prologue_vec_kernel<4, false>), grid, dim3(256), 0, s, a, l);
-        break;
+    case 1: kernel = conv ? mixer_prologue_vec_kernel<1, true> : mixer_prologue_vec_kernel<1, false>; break;
+    case 2: kernel = conv ? mixer_prologue_vec_kernel<2, true> : mixer_prologue_vec_kernel<2, false>; break;
+    default: kernel = conv ? mixer_prologue_vec_kernel<4, true> : mixer_prologue_vec_kernel<4, false>; break;
     }
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, a, l, pg, inv_n);
     return hipGetLastError();
 }
 
