@@ -72,7 +72,7 @@ rms_norm_kernel(size_t rows, size_t dim, const uint16_t *x, size_t xs, const flo
                     a *= wv[c][j >> 1][2 * (j & 1)];
                     b *= wv[c][j >> 1][2 * (j & 1) + 1];
                 }
-                o[j] = static_cast<unsigned int>(to_bits(a)) | (static_cast<unsigned int>(to_bits(b)) << 16);
+                o[j] = pack2(a, b);
             }
             *reinterpret_cast<uint4 *>(yr + i) = make_uint4(o[0], o[1], o[2], o[3]);
         }
@@ -109,7 +109,7 @@ rms_norm_kernel(size_t rows, size_t dim, const uint16_t *x, size_t xs, const flo
                     a *= w[i + 2 * j];
                     b *= w[i + 2 * j + 1];
                 }
-                o[j] = static_cast<unsigned int>(to_bits(a)) | (static_cast<unsigned int>(to_bits(b)) << 16);
+                o[j] = pack2(a, b);
             }
             *reinterpret_cast<uint4 *>(yr + i) = make_uint4(o[0], o[1], o[2], o[3]);
         }

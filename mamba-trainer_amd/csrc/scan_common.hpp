@@ -174,13 +174,6 @@ constexpr int vmcnt_imm() {
     return (V & 15) | ((V >> 4) << 14) | (0x7 << 4) | (0xF << 8);
 }
 
-// Two values rounded to bf16 and packed into one word (low half first).
-__device__ __forceinline__ unsigned int pk_bf16(float lo, float hi) {
-    typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-    const bf16x2v v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
-    return __builtin_bit_cast(unsigned int, v);
-}
-
 // ---- raw row tiles staged by direct-to-LDS buffer loads (gfx950)
 // A tile holds 64 rows (tokens) of CH 16-byte chunks as they lie in memory,
 // except that chunk m of row t sits at chunk m ^ rsw<CH>(t) of the row.  The

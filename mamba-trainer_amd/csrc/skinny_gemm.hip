@@ -171,8 +171,8 @@ skinny_gemm_kernel(uint32_t M, uint32_t K, uint32_t N, const void *x, const void
                 }
             }
             u32x2 pk;
-            pk[0] = pk_bf16(v[0], v[1]);
-            pk[1] = pk_bf16(v[2], v[3]);
+            pk[0] = pack_bf16x2(v[0], v[1]);
+            pk[1] = pack_bf16x2(v[2], v[3]);
             *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(y) + o) = pk;
         }
     }

@@ -519,7 +519,7 @@ chunk_state_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
                     o[1][u] = (-b1 * sn[j] + b2 * cs[j]) * wd;
                 }
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf) out[hf][e >> 1] = pk_bf16(o[hf][0], o[hf][1]);
+                for (int hf = 0; hf < 2; ++hf) out[hf][e >> 1] = pack_bf16x2(o[hf][0], o[hf][1]);
             }
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
@@ -1101,10 +1101,8 @@ chunk_scan_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
         if constexpr (R == 1) {
             if constexpr (kBf16) {
                 u32x2 pk;
-                pk[0] = static_cast<unsigned int>(from_f32<bf16_t>(acc[0]).bits) |
-                        (static_cast<unsigned int>(from_f32<bf16_t>(acc[1]).bits) << 16);
-                pk[1] = static_cast<unsigned int>(from_f32<bf16_t>(acc[2]).bits) |
-                        (static_cast<unsigned int>(from_f32<bf16_t>(acc[3]).bits) << 16);
+                pk[0] = pack_bf16x2(acc[0], acc[1]);
+                pk[1] = pack_bf16x2(acc[2], acc[3]);
                 bst8(pk, rs.y, oy);
             } else {
                 bst16(u32x4{__float_as_uint(acc[0]), __float_as_uint(acc[1]),
@@ -1329,8 +1327,8 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
                 v[r] = yv * mixm::silu_fast(zv);
             }
             u32x2 pk;
-            pk[0] = pk_bf16(v[0], v[1]);
-            pk[1] = pk_bf16(v[2], v[3]);
+            pk[0] = pack_bf16x2(v[0], v[1]);
+            pk[1] = pack_bf16x2(v[2], v[3]);
             bst8(pk, rs.y, (ytok0 + 16 * tj + cc) * rs.tok_x + (16 * wave + 4 * gg) * 2);
         }
     };
@@ -1423,8 +1421,8 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
                     }
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) {
-                        bo[hf][(q + jj) >> 1] = pk_bf16(ob[hf][0], ob[hf][1]);
-                        co[hf][(q + jj) >> 1] = pk_bf16(oc[hf][0], oc[hf][1]);
+                        bo[hf][(q + jj) >> 1] = pack_bf16x2(ob[hf][0], ob[hf][1]);
+                        co[hf][(q + jj) >> 1] = pack_bf16x2(oc[hf][0], oc[hf][1]);
                     }
                 }
             }
@@ -1618,8 +1616,8 @@ chunk_scan_dma_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
             // rows past the sequence end fall outside the buffer: dropped
             const uint32_t oy = (tok0 + t) * rs.tok_x + (16 * wave + 4 * g) * 2;
             u32x2 pk;
-            pk[0] = pk_bf16(acc[0], acc[1]);
-            pk[1] = pk_bf16(acc[2], acc[3]);
+            pk[0] = pack_bf16x2(acc[0], acc[1]);
+            pk[1] = pack_bf16x2(acc[2], acc[3]);
             if constexpr (GATE) {
                 ypend[tj] = pk;
                 zpend[tj] = bld8(rz, (tok0 + t) * zs + (16 * wave + 4 * g) * 2);
@@ -1938,7 +1936,7 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
                         o[1][u] = -v1 * sn[j] + v2 * cs[j];
                     }
 #pragma unroll
-                    for (int hf = 0; hf < 2; ++hf) out[hf][e >> 1] = pk_bf16(o[hf][0], o[hf][1]);
+                    for (int hf = 0; hf < 2; ++hf) out[hf][e >> 1] = pack_bf16x2(o[hf][0], o[hf][1]);
                 }
                 *reinterpret_cast<u32x4 *>(tile + olo) = out[0];
                 *reinterpret_cast<u32x4 *>(tile + ohi) = out[1];
@@ -2087,8 +2085,8 @@ chunk_scan_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) {
                 if (kb < nkb)
                     acc = mfma_bf16(*reinterpret_cast<const bf16x8 *>(mb + tj * 16 * LDM * 2 + kb * 64), xf[kb], acc);
             u32x2 pk;
-            pk[0] = pk_bf16(acc[0], acc[1]);
-            pk[1] = pk_bf16(acc[2], acc[3]);
+            pk[0] = pack_bf16x2(acc[0], acc[1]);
+            pk[1] = pack_bf16x2(acc[2], acc[3]);
             bst8(pk, rs.y, (tok0 + 4 * tj + g) * rs.tok_x + (16 * wave + c) * 8);
         }
     }
@@ -2265,7 +2263,7 @@ chunk_state_mimo_kernel(ScanLaunch a, ChunkWs ws, int nsub, int kseg, int nseg) 
                     o[1][u] = (-b1 * sn[j] + b2 * cs[j]) * wd;
                 }
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf) out[hf][e >> 1] = pk_bf16(o[hf][0], o[hf][1]);
+                for (int hf = 0; hf < 2; ++hf) out[hf][e >> 1] = pack_bf16x2(o[hf][0], o[hf][1]);
             }
             *reinterpret_cast<u32x4 *>(sm.b + olo) = out[0];
             *reinterpret_cast<u32x4 *>(sm.b + ohi) = out[1];
@@ -2817,8 +2815,8 @@ __device__ __forceinline__ void fused_tail(const ScanLaunch &a, const FusedWs &w
                 for (int r = 0; r < 4; ++r) yv[r] = __builtin_fmaf(yc[tj][r], dec, yl[r]);
                 const uint32_t oy = (tok0 + t) * rs.tok_x + (16 * wave + 4 * g) * 2;
                 u32x2 pk;
-                pk[0] = pk_bf16(yv[0], yv[1]);
-                pk[1] = pk_bf16(yv[2], yv[3]);
+                pk[0] = pack_bf16x2(yv[0], yv[1]);
+                pk[1] = pack_bf16x2(yv[2], yv[3]);
                 if constexpr (GATE) {
                     // the gate: bf16(y) * silu(z)   (the rounding of mixer_gate_vec_kernel)
                     const u32x2 zw = bld8(rz, (tok0 + t) * zs + (16 * wave + 4 * g) * 2);
@@ -2830,8 +2828,8 @@ __device__ __forceinline__ void fused_tail(const ScanLaunch &a, const FusedWs &w
                         const float z1 = __uint_as_float((r & 1) ? (zz & 0xFFFF0000u) : (zz << 16));
                         v[r] = y1 * mixm::silu_fast(z1);
                     }
-                    pk[0] = pk_bf16(v[0], v[1]);
-                    pk[1] = pk_bf16(v[2], v[3]);
+                    pk[0] = pack_bf16x2(v[0], v[1]);
+                    pk[1] = pack_bf16x2(v[2], v[3]);
                 }
                 bst8(pk, rs.y, oy);
             }
@@ -3023,8 +3021,8 @@ chunk_scan_fused_kernel(ScanLaunch a, FusedWs ws, int nsub, int kseg, int nseg, 
                     }
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) {
-                        bo[hf][(q + jj) >> 1] = pk_bf16(ob[hf][0], ob[hf][1]);
-                        co[hf][(q + jj) >> 1] = pk_bf16(oc[hf][0], oc[hf][1]);
+                        bo[hf][(q + jj) >> 1] = pack_bf16x2(ob[hf][0], ob[hf][1]);
+                        co[hf][(q + jj) >> 1] = pack_bf16x2(oc[hf][0], oc[hf][1]);
                     }
                 }
             }

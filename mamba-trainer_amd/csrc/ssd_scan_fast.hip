@@ -393,10 +393,8 @@ ssd_scan_fast_kernel(ScanLaunch a, int nchunks) {
             if constexpr (R == 1) {
                 if constexpr (kBf16) {
                     u32x2 pk;
-                    pk[0] = static_cast<unsigned int>(from_f32<bf16_t>(v[0]).bits) |
-                            (static_cast<unsigned int>(from_f32<bf16_t>(v[1]).bits) << 16);
-                    pk[1] = static_cast<unsigned int>(from_f32<bf16_t>(v[2]).bits) |
-                            (static_cast<unsigned int>(from_f32<bf16_t>(v[3]).bits) << 16);
+                    pk[0] = pack_bf16x2(v[0], v[1]);
+                    pk[1] = pack_bf16x2(v[2], v[3]);
                     bst8(pk, rs.y, oy);
                 } else {
                     bst16(u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]),
