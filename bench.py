@@ -57,11 +57,11 @@ MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA, TFLOP/s
 # kernel, from profiles/scan_config1_kernels.txt (rocprofv3 FETCH_SIZE /
 # WRITE_SIZE per dispatch scaled by a 256 MiB copy, SQ_VALU_MFMA_BUSY_CYCLES
 # over GRBM_GUI_ACTIVE).  At config 1 the library runs the fused single
-# launch (chunk_scan_fused_kernel): 205.5 MB read + 107.0 MB written.
+# launch (chunk_scan_fused_kernel): 205.4 MB read + 107.0 MB written.
 # Counters cannot be read inside this process; re-measured when the kernels
 # change.
-SCAN_TRAFFIC_BYTES = 312_600_000
-SCAN_MFMA_BUSY = {"chunk_scan_fused_kernel": 0.044}
+SCAN_TRAFFIC_BYTES = 312_500_000
+SCAN_MFMA_BUSY = {"chunk_scan_fused_kernel": 0.052}
 
 # BASELINE config 1 (the headline) and config 3 (decode)
 SCAN = dict(B=8, L=2048, H=12, P=64, N=128, R=1, Q=64)

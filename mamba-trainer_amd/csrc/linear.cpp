@@ -19,10 +19,13 @@
 //
 // Plan choice follows the reference's tuned plans (tensor/matmul.rs:1636-1943:
 // timing probes once per shape): the first call for a shape asks hipBLASLt's
-// heuristic for up to kCandidates algorithms, runs each a few times on the
-// caller's data into a scratch output (the caller's buffers, including an
-// in-place residual, are left untouched), keeps the fastest and blocks on the
-// stream once to read the timings.  Later calls with the shape launch the kept
+// heuristic for up to kCandidates algorithms, times each on the caller's data
+// into a scratch output (the caller's buffers, including an in-place
+// residual, are left untouched), keeps the fastest and blocks on the stream
+// to read the timings.  Each timed run follows a write of kFlushBytes, more
+// than the L2 and Infinity Cache hold, so a plan is judged on weights read
+// from HBM, as a model's layers meet them, and each candidate keeps its best
+// of kProbeRounds interleaved rounds.  Later calls with the shape launch the kept
 // plan asynchronously.  M3_LINEAR_TUNE=0 keeps the heuristic's first choice
 // (no probe, no blocking), for runs that must pick the same algorithm in
 // every process.
@@ -43,7 +46,8 @@ namespace m3 {
 namespace {
 
 constexpr int kCandidates = 8;
-constexpr int kProbeRuns = 3;
+constexpr int kProbeRounds = 3;
+constexpr size_t kFlushBytes = size_t(512) << 20;
 
 struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
@@ -105,46 +109,58 @@ bool tuning_enabled() {
     return v == nullptr || std::strcmp(v, "0") != 0;
 }
 
-// Times every candidate of `p` (kProbeRuns runs after one warm-up each) with
-// beta = 0 into a scratch [m, n] output and keeps the fastest.  Any failure
-// leaves the heuristic's first choice in place.
+// Times every candidate of `p` (one warm-up each, then kProbeRounds rounds of
+// one run per candidate, each after the cache flush) with beta = 0 into a
+// scratch [m, n] output and keeps the one with the lowest best time.  Any
+// failure leaves the heuristic's first choice in place; without the flush
+// buffer the runs are timed warm.
 void tune_plan(hipblasLtHandle_t h, size_t m, size_t n, Plan &p, const void *alpha, const void *w,
                const void *x, void *workspace, size_t ws, hipStream_t s) {
-    if (p.candidates.size() < 2) return;
-    void *scratch = nullptr;
+    const size_t nc = p.candidates.size();
+    if (nc < 2) return;
+    void *scratch = nullptr, *flush = nullptr;
     if (hipMalloc(&scratch, m * n * 2) != hipSuccess) {
         (void)hipGetLastError();
         return;
     }
+    if (hipMalloc(&flush, kFlushBytes) != hipSuccess) {
+        (void)hipGetLastError();
+        flush = nullptr;
+    }
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
         const float zero = 0.0f;
-        float best = 0.0f;
-        size_t pick = 0;
-        bool any = false;
-        for (size_t i = 0; i < p.candidates.size(); ++i) {
-            auto run = [&]() {
-                return hipblasLtMatmul(h, p.desc, alpha, w, p.a, x, p.b, &zero, scratch, p.c, scratch,
-                                       p.c, &p.candidates[i], workspace, ws, s);
-            };
-            if (run() != HIPBLAS_STATUS_SUCCESS) continue;
-            bool ok = hipEventRecord(e0, s) == hipSuccess;
-            for (int r = 0; ok && r < kProbeRuns; ++r) ok = run() == HIPBLAS_STATUS_SUCCESS;
-            ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
-            float ms = 0.0f;
-            if (!ok || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) continue;
-            if (!any || ms < best) {
-                best = ms;
-                pick = i;
-                any = true;
+        auto run = [&](size_t i) {
+            return hipblasLtMatmul(h, p.desc, alpha, w, p.a, x, p.b, &zero, scratch, p.c, scratch, p.c,
+                                   &p.candidates[i], workspace, ws, s) == HIPBLAS_STATUS_SUCCESS;
+        };
+        std::vector<float> best(nc, -1.0f);   // -1: failed or not timed
+        std::vector<char> usable(nc, 0);
+        for (size_t i = 0; i < nc; ++i) usable[i] = run(i) ? 1 : 0;
+        for (int round = 0; round < kProbeRounds; ++round) {
+            for (size_t i = 0; i < nc; ++i) {
+                if (!usable[i]) continue;
+                if (flush) (void)hipMemsetAsync(flush, round * 16 + static_cast<int>(i), kFlushBytes, s);
+                bool ok = hipEventRecord(e0, s) == hipSuccess && run(i);
+                ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+                float ms = 0.0f;
+                if (!ok || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) {
+                    usable[i] = 0;
+                    continue;
+                }
+                if (best[i] < 0.0f || ms < best[i]) best[i] = ms;
             }
         }
-        if (any) p.algo = p.candidates[pick];
+        size_t pick = nc;
+        for (size_t i = 0; i < nc; ++i)
+            if (usable[i] && best[i] >= 0.0f && (pick == nc || best[i] < best[pick])) pick = i;
+        if (pick < nc) p.algo = p.candidates[pick];
     }
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     (void)hipStreamSynchronize(s);
     (void)hipFree(scratch);
+    if (flush) (void)hipFree(flush);
     (void)hipGetLastError();
 }
 
