@@ -66,8 +66,10 @@ m3_status m3_quantize_int8_columns(size_t in_features, size_t out_features, cons
  * alias y.  The workspace (up to m3_linear_workspace_bytes(), 256-byte
  * aligned, or NULL) widens the kernels hipBLASLt may pick.  The first call
  * for a (m, k, n, scaled, workspace) shape times hipBLASLt's candidate
- * algorithms on the caller's inputs into a scratch output it allocates and
- * frees, and blocks on `stream` once; later calls are asynchronous.  The
+ * algorithms on the caller's inputs into a scratch output, each run after a
+ * 512 MB cache-evicting write (both buffers allocated and freed by the call),
+ * and blocks on `stream` while it reads the timings; later calls are
+ * asynchronous.  The
  * reference tunes its matmul plans once per shape the same way
  * (src/tensor/matmul.rs:1636-1943).  M3_LINEAR_TUNE=0 in the environment
  * keeps hipBLASLt's first choice instead. */
