@@ -72,7 +72,8 @@ m3_status m3_quantize_int8_columns(size_t in_features, size_t out_features, cons
  * asynchronous.  The
  * reference tunes its matmul plans once per shape the same way
  * (src/tensor/matmul.rs:1636-1943).  M3_LINEAR_TUNE=0 in the environment
- * keeps hipBLASLt's first choice instead. */
+ * keeps hipBLASLt's first choice instead, as does a first call made while
+ * `stream` is being captured into a graph. */
 size_t m3_linear_workspace_bytes(void);
 m3_status m3_linear(size_t m, size_t k, size_t n, const void *x, const void *w,
                     const float *col_scale, const void *residual, void *y, void *workspace,

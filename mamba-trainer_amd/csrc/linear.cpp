@@ -195,7 +195,16 @@ hipError_t launch_linear(size_t m, size_t k, size_t n, const void *x, const void
         if (it == d.plans.end()) {
             Plan p;
             if (!build_plan(handle, m, k, n, scaled, w_transposed, ws, p)) return hipErrorNotSupported;
-            if (tuning_enabled()) tune_plan(handle, m, n, p, alpha, w, x, workspace, ws, s);
+            // no probe while the stream is being captured into a graph: its
+            // allocations, fills and waits cannot be captured, so a shape
+            // first met under capture keeps hipBLASLt's first choice
+            hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(s, &cap) != hipSuccess) {
+                (void)hipGetLastError();
+                cap = hipStreamCaptureStatusActive;
+            }
+            if (tuning_enabled() && cap == hipStreamCaptureStatusNone)
+                tune_plan(handle, m, n, p, alpha, w, x, workspace, ws, s);
             it = d.plans.emplace(key, p).first;
         }
         plan = &it->second;

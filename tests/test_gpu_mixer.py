@@ -824,3 +824,47 @@ def test_fused_conv_step_with_shared_groups_writes_a_separate_history():
     assert torch.equal(fused.ssm.h, composed.ssm.h)
     assert torch.equal(fused.ssm.last_u, composed.ssm.last_u)
     assert torch.equal(fused.ssm.angle, composed.ssm.angle)
+
+
+def test_linear_first_call_under_graph_capture():
+    """m3_linear met first for its shape while the stream is captured: the
+    plan probe (allocations, cache flushes, timing waits) is skipped, the
+    captured product replays correctly five times with eager work and host
+    synchronisation between the replays, and it equals an eager call of the
+    same shape bit for bit and torch's f32 product to bf16 rounding."""
+    from mamba3 import _lib
+    from mamba3.nn import linear_workspace
+    lib = _lib.lib()
+    m, k, n = 8, 64, 344   # a decode-sized product of a shape no other test uses
+    gen = torch.Generator(device=DEV).manual_seed(71)
+    x = torch.randn(m, k, device=DEV, generator=gen).to(torch.bfloat16)
+    w = torch.randn(k, n, device=DEV, generator=gen).to(torch.bfloat16)
+    ws = linear_workspace(torch.device(DEV))
+    y_g = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    y_e = torch.empty_like(y_g)
+
+    def call(y, stream, cols=n):
+        _lib.check(lib.m3_linear(m, k, cols, x.data_ptr(), w.data_ptr(), None, None, y.data_ptr(),
+                                 ws.data_ptr(), ws.numel(), stream.cuda_stream))
+
+    # another shape first, outside the capture, so the library's hipBLASLt
+    # handle exists before it (creating one allocates)
+    call(y_e, torch.cuda.current_stream(), cols=n - 16)
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        call(y_g, side)
+    torch.cuda.synchronize()
+    ref = (x.float() @ w.float()).to(torch.bfloat16)
+    for rep in range(5):
+        y_g.zero_()
+        x.add_(0.0)   # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        call(y_e, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        assert torch.equal(y_g, y_e), rep
+        err = rel_l2(y_g.float().cpu().numpy(), ref.float().cpu().numpy())
+        assert err < 1e-2, (rep, err)
